@@ -1,0 +1,289 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X ternary linear path (one JSON line on stdout).
+
+Headline workload (value): decode ternary GEMV at LLaMA-7B FFN shapes. One
+step = one decode pass of B tokens through the three FFN projections
+(W_gate, W_up [11008,4096] and W_down [4096,11008]), bf16 activations, fp32
+accumulation, bf16 outputs. Weights, scales and activations are resident in
+HBM before timing; the weights rotate over enough distinct copies (>= 0.5 GB)
+that the 256 MB Infinity Cache cannot serve them. value = algorithmic bytes
+per step (packed weights + scales + x + y) / time per step.
+
+roofline: algorithmic bytes per GEMV launch / average GEMV launch duration
+(HIP events around every launch in the timed region, on the launch stream).
+cpu_baseline: the reference's CPU decode path (ternary_matmul_packed_parallel,
+src/model/ternary.rs:471-529, restated in C by the oracle) on the same three
+matrices at B=1, timed on this host's cores.
+
+extra: prefill GEMM (X[2048,4096] x W[N,4096], N in {4096, 11008}), 2:4
+sparse GEMM and the MoE expert layer, as TFLOP/s and fraction of the dense
+bf16 MFMA peak.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, GB/s
+BF16_PEAK_TFLOPS = 2500.0      # MI355X dense bf16 MFMA, TFLOP/s
+
+
+def gemv_bytes(n: int, k: int, b: int, xb: int = 2, yb: int = 2) -> int:
+    return n * k // 4 + 4 * n + xb * b * k + yb * b * n
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--batch", type=int, default=1, help="decode tokens per step (1, 4 or 16)")
+    ap.add_argument("--no-extra", action="store_true")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    args = ap.parse_args()
+
+    if args.gpus != 1:
+        print(f"bench.py: this build runs on exactly one GPU; --gpus {args.gpus} is not supported "
+              "(the multi-GPU sharding plan is described in DESIGN.md, not run).", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    import ferrisres_amd as frx
+    from ferrisres_amd import synth
+
+    assert torch.cuda.is_available(), "bench.py needs a gfx950 GPU"
+    dev = torch.device("cuda:0")
+    stream = torch.cuda.Stream(device=dev)
+    ctx = frx.Context(0)
+    ctx.set_stream(stream)
+    B = args.batch
+    H, I = 4096, 11008
+
+    # ---- inputs (resident before timing) -------------------------------------
+    log("bench: generating weights")
+    t_gu = synth.ternary_uniform("bench/decode", "w_gate", I, H)
+    t_dn = synth.ternary_uniform("bench/decode", "w_down", H, I)
+    w_gu = torch.from_numpy(synth.pack_rows_u32(t_gu).view(np.int32)).to(dev)
+    w_dn = torch.from_numpy(synth.pack_rows_u32(t_dn).view(np.int32)).to(dev)
+    s_gu = torch.from_numpy(synth.row_scales("bench/decode", "s_gate", I, samples=256)).to(dev)
+    s_dn = torch.from_numpy(synth.row_scales("bench/decode", "s_down", H, samples=256)).to(dev)
+    step_weight_bytes = 2 * w_gu.numel() * 4 + w_dn.numel() * 4
+    copies = max(2, int(np.ceil(512e6 / step_weight_bytes)) + 1)
+    W = [(w_gu.clone(), w_gu.clone(), w_dn.clone()) for _ in range(copies)]
+    _, xb = synth.activations("bench/decode", "x", B, H)
+    _, hb = synth.activations("bench/decode", "h", B, I)
+    x = torch.from_numpy(xb.view(np.int16)).to(dev).view(torch.bfloat16)
+    hmid = torch.from_numpy(hb.view(np.int16)).to(dev).view(torch.bfloat16)
+    g = torch.empty((B, I), dtype=torch.bfloat16, device=dev)
+    u = torch.empty((B, I), dtype=torch.bfloat16, device=dev)
+    y = torch.empty((B, H), dtype=torch.bfloat16, device=dev)
+    torch.cuda.synchronize()
+
+    b_gu = gemv_bytes(I, H, B)
+    b_dn = gemv_bytes(H, I, B)
+    step_bytes = 2 * b_gu + b_dn
+
+    def step(i, events=None):
+        wg, wu, wd = W[i % copies]
+        if events is None:
+            ctx.ternary_linear(wg, s_gu, x, g)
+            ctx.ternary_linear(wu, s_gu, x, u)
+            ctx.ternary_linear(wd, s_dn, hmid, y)
+        else:
+            for (w, s, xi, yo) in ((wg, s_gu, x, g), (wu, s_gu, x, u), (wd, s_dn, hmid, y)):
+                e0 = torch.cuda.Event(enable_timing=True)
+                e1 = torch.cuda.Event(enable_timing=True)
+                e0.record(stream)
+                ctx.ternary_linear(w, s, xi, yo)
+                e1.record(stream)
+                events.append((e0, e1, w.shape[0]))
+
+    log(f"bench: warmup {args.warmup} steps ({copies} weight copies, {copies * step_weight_bytes / 1e6:.0f} MB)")
+    with torch.cuda.stream(stream):
+        for i in range(args.warmup):
+            step(i)
+    torch.cuda.synchronize()
+
+    # timed region (value)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    with torch.cuda.stream(stream):
+        for i in range(args.steps):
+            step(i)
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    ms_per_step = elapsed / args.steps * 1e3
+    value = step_bytes / (elapsed / args.steps) / 1e9
+    log(f"bench: decode B={B}: {ms_per_step * 1e3:.1f} us/step, {value:.1f} GB/s")
+
+    # per-launch kernel durations (HIP events on the launch stream)
+    evs = []
+    with torch.cuda.stream(stream):
+        for i in range(args.steps):
+            step(i, evs)
+    torch.cuda.synchronize()
+    dur = {I: [], H: []}
+    for e0, e1, n in evs:
+        dur[n].append(e0.elapsed_time(e1) * 1e-3)
+    launch_bytes = 2 * b_gu + b_dn
+    launch_time = 2 * float(np.mean(dur[I])) + float(np.mean(dur[H]))
+    achieved = launch_bytes / launch_time / 1e9
+    roofline = {
+        "kernel": "frx::gemv_kernel<bf16,bf16>",
+        "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+        "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+        "avg_us": {"11008x4096": round(float(np.mean(dur[I])) * 1e6, 3),
+                   "4096x11008": round(float(np.mean(dur[H])) * 1e6, 3)},
+        "bytes_per_launch": {"11008x4096": b_gu, "4096x11008": b_dn},
+    }
+    traffic_file = os.path.join(ROOT, "profiles", "gemv_traffic.json")
+    if os.path.exists(traffic_file):
+        try:
+            tr = json.load(open(traffic_file))
+            if tr.get("batch") == B:
+                roofline["traffic"] = tr.get("bytes_per_launch")
+        except (OSError, ValueError):
+            pass
+
+    extra = {}
+    if not args.no_extra:
+        extra = run_extra(torch, frx, synth, ctx, stream, dev)
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        cpu = cpu_baseline(t_gu, t_dn, B, args.cpu_seconds)
+
+    out = {
+        "metric": "ternary GEMV GB/s (% HBM peak) + GEMM TFLOP/s (% MFMA peak), 1 MI355X",
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {
+            "workload": "decode_gemv_llama7b_ffn",
+            "batch_tokens": B,
+            "projections": ["gate 11008x4096", "up 11008x4096", "down 4096x11008"],
+            "x_dtype": "bf16", "y_dtype": "bf16", "accumulate": "fp32",
+            "weight_copies": copies,
+            "hbm_fraction": round(value / HBM_PEAK_GBS, 4),
+        },
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+        "extra": extra,
+    }
+    print(json.dumps(out), flush=True)
+
+
+def _time_kernel(torch, stream, fn, iters, warm=3):
+    with torch.cuda.stream(stream):
+        for _ in range(warm):
+            fn()
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    with torch.cuda.stream(stream):
+        e0.record(stream)
+        for _ in range(iters):
+            fn()
+        e1.record(stream)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) * 1e-3 / iters
+
+
+def run_extra(torch, frx, synth, ctx, stream, dev):
+    res = {}
+    M, K = 2048, 4096
+    _, xb = synth.activations("bench/prefill", "x", M, K)
+    X = torch.from_numpy(xb.view(np.int16)).to(dev).view(torch.bfloat16)
+    for N in (4096, 11008):
+        t = synth.ternary_uniform("bench/prefill", f"w{N}", N, K)
+        w = torch.from_numpy(synth.pack_rows_u32(t).view(np.int32)).to(dev)
+        s = torch.from_numpy(synth.row_scales("bench/prefill", f"s{N}", N, samples=256)).to(dev)
+        Y = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+        dt = _time_kernel(torch, stream, lambda: ctx.ternary_linear(w, s, X, Y), 20)
+        tf = 2.0 * M * N * K / dt / 1e12
+        res[f"prefill_gemm_{M}x{K}x{N}"] = {"us": round(dt * 1e6, 2), "tflops": round(tf, 1),
+                                            "frac_bf16_peak": round(tf / BF16_PEAK_TFLOPS, 4)}
+        log(f"bench: prefill N={N}: {dt * 1e6:.1f} us, {tf:.1f} TFLOP/s")
+        t24 = synth.sparse24_uniform("bench/sp24", f"w{N}", N, K)
+        meta = torch.from_numpy(frx.pack_sparse24_gpu(t24).view(np.int32)).to(dev)
+        dt = _time_kernel(torch, stream, lambda: ctx.sparse24_ternary_linear(meta, s, X, Y), 20)
+        tf = 2.0 * M * N * K / dt / 1e12
+        res[f"sparse24_gemm_{M}x{K}x{N}"] = {"us": round(dt * 1e6, 2), "tflops_dense_equiv": round(tf, 1),
+                                             "frac_bf16_peak": round(tf / BF16_PEAK_TFLOPS, 4)}
+        log(f"bench: 2:4 N={N}: {dt * 1e6:.1f} us, {tf:.1f} TFLOP/s dense-equivalent")
+        del w, Y, meta
+    # MoE expert layer
+    T, Hm, Im, E, k = 512, 2048, 5632, 16, 2
+    _, xb = synth.activations("bench/moe", "x", T, Hm)
+    _, rb = synth.activations("bench/moe", "router", E, Hm, std=0.02)
+    xm = torch.from_numpy(xb.view(np.int16)).to(dev).view(torch.bfloat16)
+    rm = torch.from_numpy(rb.view(np.int16)).to(dev).view(torch.bfloat16)
+    tg = synth.ternary_uniform("bench/moe", "w", Im, Hm)
+    td = synth.ternary_uniform("bench/moe", "wd", Hm, Im)
+    pg = torch.from_numpy(synth.pack_rows_u32(tg).view(np.int32)).to(dev)
+    pd = torch.from_numpy(synth.pack_rows_u32(td).view(np.int32)).to(dev)
+    sg = torch.from_numpy(synth.row_scales("bench/moe", "s", Im, samples=256)).to(dev)
+    sd = torch.from_numpy(synth.row_scales("bench/moe", "sd", Hm, samples=256)).to(dev)
+    wg = [pg.clone() for _ in range(E)]
+    wu = [pg.clone() for _ in range(E)]
+    wd = [pd.clone() for _ in range(E)]
+    ym = torch.empty((T, Hm), dtype=torch.bfloat16, device=dev)
+    fn = lambda: ctx.moe_ternary_ffn(xm, rm, wg, [sg] * E, wu, [sg] * E, wd, [sd] * E, ym, top_k=k)  # noqa: E731
+    dt = _time_kernel(torch, stream, fn, 20)
+    fl = T * k * 3 * 2.0 * Im * Hm
+    tf = fl / dt / 1e12
+    res["moe_512tok_h2048_i5632_e16_top2"] = {"us": round(dt * 1e6, 2), "tflops": round(tf, 1),
+                                              "frac_bf16_peak": round(tf / BF16_PEAK_TFLOPS, 4)}
+    log(f"bench: MoE: {dt * 1e6:.1f} us, {tf:.1f} TFLOP/s")
+    return res
+
+
+def cpu_baseline(t_gu, t_dn, B, seconds):
+    """Reference CPU decode path (ternary_matmul_packed_parallel) restated in
+    C, on this host's cores (capped at 16, the GPU box's CPU share)."""
+    import oracle
+    threads = max(1, min(16, os.cpu_count() or 1))
+    p_gu = oracle.pack_ternary(t_gu)
+    p_dn = oracle.pack_ternary(t_dn)
+    x = np.linspace(-1, 1, t_gu.shape[1], dtype=np.float32)
+    h = np.linspace(-1, 1, t_dn.shape[1], dtype=np.float32)
+    # one calibration call, then reps so the whole sample takes ~`seconds`
+    t1, _ = oracle.time_packed_parallel(p_gu, 0.01, x, t_gu.shape[0], t_gu.shape[1], threads, 1)
+    t2, _ = oracle.time_packed_parallel(p_dn, 0.01, h, t_dn.shape[0], t_dn.shape[1], threads, 1)
+    reps = max(3, int(seconds / max(1e-6, 2 * t1 + t2)))
+    t1, _ = oracle.time_packed_parallel(p_gu, 0.01, x, t_gu.shape[0], t_gu.shape[1], threads, reps)
+    t2, _ = oracle.time_packed_parallel(p_dn, 0.01, h, t_dn.shape[0], t_dn.shape[1], threads, reps)
+    step_t = 2 * t1 + t2
+    n_gu, k_gu = t_gu.shape
+    n_dn, k_dn = t_dn.shape
+    # same algorithmic byte count as the GPU metric at B=1 (f32 x/y on CPU)
+    byts = 2 * gemv_bytes(n_gu, k_gu, 1, 4, 4) + gemv_bytes(n_dn, k_dn, 1, 4, 4)
+    return {"value": round(byts / step_t / 1e9, 2), "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": f"ternary_matmul_packed_parallel (ternary.rs:471-529) restated in C, u8 layout, f32 x, "
+                      f"1 token through 11008x4096 x2 + 4096x11008, median of {reps} reps each "
+                      f"({step_t * 1e3:.2f} ms/step on {threads} threads)"}
+
+
+if __name__ == "__main__":
+    main()

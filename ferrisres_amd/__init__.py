@@ -1,0 +1,262 @@
+"""ferrisres_amd — MI355X (gfx950) ternary linear backend for FerrisRes.
+
+The compute lives in the C-ABI library ``libfrx_ternary.so`` (HIP kernels,
+header ``include/frx_ternary.h``). This module is a thin ctypes binding used
+by the tests and the benchmark: it loads the library (failing loudly if it is
+missing — there is no CPU fallback), maps ``frx_status`` codes to exceptions
+named after the reference's ``FerrisResError`` variants (src/error.rs:4-22),
+and passes torch device tensors as raw pointers.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libfrx_ternary.so")
+
+FRX_F32, FRX_BF16 = 0, 1
+ACT_SILU, ACT_GELU_TANH = 0, 1
+
+_STATUS = {
+    0: "Ok", 1: "Gpu", 2: "Shape", 3: "Device", 4: "Shader", 5: "OOM", 6: "Unsupported",
+}
+
+
+class FrxError(RuntimeError):
+    """A non-OK frx_status; ``kind`` is the FerrisResError variant name."""
+
+    def __init__(self, status: int, message: str):
+        self.status = status
+        self.kind = _STATUS.get(status, f"Unknown({status})")
+        super().__init__(f"{self.kind} error: {message}")
+
+
+_lib = None
+
+_u32p = ctypes.POINTER(ctypes.c_uint32)
+_f32p = ctypes.POINTER(ctypes.c_float)
+_vp = ctypes.c_void_p
+_sz = ctypes.c_size_t
+_u32 = ctypes.c_uint32
+_int = ctypes.c_int
+
+# name -> (restype, argtypes)
+_SIGS = {
+    "frx_create": (_int, [_int, ctypes.POINTER(_vp)]),
+    "frx_destroy": (None, [_vp]),
+    "frx_set_stream": (_int, [_vp, _vp]),
+    "frx_synchronize": (_int, [_vp]),
+    "frx_last_error": (ctypes.c_char_p, [_vp]),
+    "frx_status_string": (ctypes.c_char_p, [_int]),
+    "frx_version": (ctypes.c_char_p, []),
+    "frx_ternary_linear": (_int, [_vp, _vp, _vp, _vp, _int, _vp, _int, _u32, _u32, _u32]),
+    "frx_sparse24_ternary_linear": (_int, [_vp, _vp, _vp, _vp, _int, _vp, _int, _u32, _u32, _u32]),
+    "frx_moe_ternary_ffn": (_int, [_vp, _vp, _int, _vp, _int, _vp, _vp, _vp, _vp, _vp, _vp,
+                                   _u32, _u32, _u32, _u32, _u32, _int, _vp, _int, _vp, _vp]),
+    "frx_pack_ternary_u8": (_int, [_vp, _sz, _vp]),
+    "frx_unpack_ternary_u8": (_int, [_vp, _sz, _vp]),
+    "frx_repack_u8_to_u32": (_int, [_vp, _sz, _vp]),
+    "frx_gpu_packed": (_int, [_vp, _u32, _u32, ctypes.c_float, _vp, _vp]),
+    "frx_pack_sparse24_gpu": (_int, [_vp, _u32, _u32, _vp, _vp]),
+    "frx_sparse24_cpu_to_gpu": (_int, [_vp, _vp, _u32, _u32, _vp]),
+    "frx_gpu_ternary_matmul": (_int, [_vp, _vp, _vp, _vp, _sz, _sz, _sz, _vp]),
+    "frx_gpu_ternary_matmul_vram": (_int, [_vp, _vp, _vp, _vp, _sz, _sz, _sz, _vp]),
+    "frx_gpu_sparse_ternary_matmul": (_int, [_vp, _vp, _vp, _vp, _sz, _sz, _sz, _vp]),
+}
+
+
+def lib():
+    """Loads libfrx_ternary.so (raises if it has not been built)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(
+                f"{LIB_PATH} is missing: build it with __graft_entry__.build() "
+                "(there is no CPU fallback)")
+        h = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in _SIGS.items():
+            fn = getattr(h, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = h
+    return _lib
+
+
+def exported_symbols():
+    return list(_SIGS)
+
+
+def _np_ptr(a: np.ndarray):
+    return a.ctypes.data_as(_vp)
+
+
+def _check(status: int, ctx=None):
+    if status != 0:
+        msg = ""
+        if ctx is not None:
+            raw = lib().frx_last_error(ctx)
+            msg = raw.decode() if raw else ""
+        if not msg:
+            msg = lib().frx_status_string(status).decode()
+        raise FrxError(status, msg)
+
+
+# ---- host packers (no GPU) -------------------------------------------------
+
+def pack_ternary_u8(values: np.ndarray) -> np.ndarray:
+    v = np.ascontiguousarray(values, dtype=np.int8).ravel()
+    out = np.zeros((v.size + 3) // 4, dtype=np.uint8)
+    _check(lib().frx_pack_ternary_u8(_np_ptr(v), v.size, _np_ptr(out)))
+    return out
+
+
+def unpack_ternary_u8(packed: np.ndarray, n: int) -> np.ndarray:
+    p = np.ascontiguousarray(packed, dtype=np.uint8)
+    out = np.zeros(n, dtype=np.int8)
+    _check(lib().frx_unpack_ternary_u8(_np_ptr(p), n, _np_ptr(out)))
+    return out
+
+
+def repack_u8_to_u32(packed: np.ndarray, n_values: int) -> np.ndarray:
+    p = np.ascontiguousarray(packed, dtype=np.uint8)
+    if p.size < (n_values + 3) // 4:
+        raise ValueError("packed buffer shorter than ceil(n_values/4)")
+    out = np.zeros((n_values + 15) // 16, dtype=np.uint32)
+    _check(lib().frx_repack_u8_to_u32(_np_ptr(p), n_values, _np_ptr(out)))
+    return out
+
+
+def gpu_packed(values: np.ndarray, tensor_scale: float):
+    v = np.ascontiguousarray(values, dtype=np.int8)
+    n, k = v.shape
+    w = np.zeros(n * k // 16, dtype=np.uint32)
+    s = np.zeros(n, dtype=np.float32)
+    _check(lib().frx_gpu_packed(_np_ptr(v), n, k, ctypes.c_float(tensor_scale), _np_ptr(w), _np_ptr(s)))
+    return w.reshape(n, k // 16), s
+
+
+def pack_sparse24_gpu(w: np.ndarray, with_scales: bool = False):
+    v = np.ascontiguousarray(w, dtype=np.int8)
+    n, k = v.shape
+    wpr = ((k + 3) // 4 + 5) // 6
+    meta = np.zeros(n * wpr, dtype=np.uint32)
+    sc = np.zeros(n, dtype=np.float32)
+    _check(lib().frx_pack_sparse24_gpu(_np_ptr(v), n, k, _np_ptr(meta),
+                                       _np_ptr(sc) if with_scales else None))
+    meta = meta.reshape(n, wpr)
+    return (meta, sc) if with_scales else meta
+
+
+def sparse24_cpu_to_gpu(patterns: np.ndarray, signs: np.ndarray, n: int, k: int) -> np.ndarray:
+    p = np.ascontiguousarray(patterns, dtype=np.uint8)
+    s = np.ascontiguousarray(signs, dtype=np.uint8)
+    wpr = (k // 4 + 5) // 6
+    meta = np.zeros(n * wpr, dtype=np.uint32)
+    _check(lib().frx_sparse24_cpu_to_gpu(_np_ptr(p), _np_ptr(s), n, k, _np_ptr(meta)))
+    return meta.reshape(n, wpr)
+
+
+# ---- device context ----------------------------------------------------------
+
+def _dtype_code(t) -> int:
+    import torch
+    if t.dtype == torch.float32:
+        return FRX_F32
+    if t.dtype == torch.bfloat16:
+        return FRX_BF16
+    raise TypeError(f"unsupported dtype {t.dtype}")
+
+
+def _ptr(t):
+    return _vp(t.data_ptr()) if t is not None else None
+
+
+class Context:
+    """Owns an frx_ctx bound to one device and (optionally) a torch stream."""
+
+    def __init__(self, device: int = 0, stream=None):
+        h = _vp()
+        _check(lib().frx_create(device, ctypes.byref(h)))
+        self._h = h
+        if stream is not None:
+            self.set_stream(stream)
+
+    def close(self):
+        if getattr(self, "_h", None):
+            lib().frx_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def set_stream(self, stream):
+        raw = stream.cuda_stream if hasattr(stream, "cuda_stream") else int(stream or 0)
+        _check(lib().frx_set_stream(self._h, _vp(raw)), self._h)
+
+    def synchronize(self):
+        _check(lib().frx_synchronize(self._h), self._h)
+
+    # TernaryMatMulOp::dispatch analogue; all tensors on the device.
+    def ternary_linear(self, w, scale, x, y):
+        M, K = x.shape
+        N = w.shape[0]
+        _check(lib().frx_ternary_linear(self._h, _ptr(w), _ptr(scale), _ptr(x), _dtype_code(x),
+                                        _ptr(y), _dtype_code(y), M, K, N), self._h)
+        return y
+
+    def sparse24_ternary_linear(self, meta, scale, x, y):
+        M, K = x.shape
+        N = meta.shape[0]
+        _check(lib().frx_sparse24_ternary_linear(self._h, _ptr(meta), _ptr(scale), _ptr(x),
+                                                 _dtype_code(x), _ptr(y), _dtype_code(y), M, K, N),
+               self._h)
+        return y
+
+    def moe_ternary_ffn(self, x, router, w_gate, s_gate, w_up, s_up, w_down, s_down, y,
+                        top_k: int, act: int = ACT_SILU, topk_idx=None, topk_w=None):
+        T, H = x.shape
+        E = router.shape[0]
+        I = w_gate[0].shape[0]
+        arr = lambda ts: (_vp * E)(*[t.data_ptr() for t in ts])  # noqa: E731
+        _check(lib().frx_moe_ternary_ffn(
+            self._h, _ptr(x), _dtype_code(x), _ptr(router), _dtype_code(router),
+            arr(w_gate), arr(s_gate), arr(w_up), arr(s_up), arr(w_down), arr(s_down),
+            T, H, I, E, top_k, act, _ptr(y), _dtype_code(y), _ptr(topk_idx), _ptr(topk_w)),
+            self._h)
+        return y
+
+    # GpuMatmulAccelerator analogues: host numpy in, host numpy out.
+    def gpu_ternary_matmul(self, packed_weights: np.ndarray, scales: np.ndarray,
+                           inp: np.ndarray, seq_len: int, in_cols: int, out_rows: int):
+        w = np.ascontiguousarray(packed_weights, dtype=np.uint32)
+        s = np.ascontiguousarray(scales, dtype=np.float32)
+        x = np.ascontiguousarray(inp, dtype=np.float32)
+        out = np.zeros(seq_len * out_rows, dtype=np.float32)
+        _check(lib().frx_gpu_ternary_matmul(self._h, _np_ptr(w), _np_ptr(s), _np_ptr(x),
+                                            seq_len, in_cols, out_rows, _np_ptr(out)), self._h)
+        return out
+
+    def gpu_ternary_matmul_vram(self, w_dev, s_dev, inp: np.ndarray, seq_len: int, in_cols: int,
+                                out_rows: int):
+        x = np.ascontiguousarray(inp, dtype=np.float32)
+        out = np.zeros(seq_len * out_rows, dtype=np.float32)
+        _check(lib().frx_gpu_ternary_matmul_vram(self._h, _ptr(w_dev), _ptr(s_dev), _np_ptr(x),
+                                                 seq_len, in_cols, out_rows, _np_ptr(out)), self._h)
+        return out
+
+    def gpu_sparse_ternary_matmul(self, meta: np.ndarray, scales: np.ndarray, inp: np.ndarray,
+                                  seq_len: int, in_cols: int, out_rows: int):
+        m = np.ascontiguousarray(meta, dtype=np.uint32)
+        s = np.ascontiguousarray(scales, dtype=np.float32)
+        x = np.ascontiguousarray(inp, dtype=np.float32)
+        out = np.zeros(seq_len * out_rows, dtype=np.float32)
+        _check(lib().frx_gpu_sparse_ternary_matmul(self._h, _np_ptr(m), _np_ptr(s), _np_ptr(x),
+                                                   seq_len, in_cols, out_rows, _np_ptr(out)),
+               self._h)
+        return out

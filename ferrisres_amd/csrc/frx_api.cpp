@@ -1,0 +1,300 @@
+// frx_api.cpp — C ABI of libfrx_ternary.so (declared in include/frx_ternary.h).
+//
+// Host-side mirror of the reference's ternary operator surface:
+//  - frx_ternary_linear / frx_sparse24_ternary_linear = TernaryMatMulOp /
+//    SparseTernaryMatMulOp::dispatch (device buffers, stream-ordered, no sync)
+//  - frx_gpu_* = GpuMatmulAccelerator::gpu_*_matmul (host slices in, owned
+//    host result out, synchronous; src/model/gpu_forward.rs:1146-1328)
+//  - frx_moe_ternary_ffn = the model's GPU MoE glue.
+// Every failure is returned as a status (FerrisResError mapping) with a
+// message in the context; nothing aborts. There is no CPU fallback: a call
+// either runs the HIP kernels or fails.
+#include <hip/hip_runtime.h>
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <mutex>
+
+#include "../../include/frx_ternary.h"
+#include "frx_internal.hpp"
+
+struct frx_ctx {
+  int device = 0;
+  hipStream_t stream = nullptr;
+  char err[512] = {0};
+  // growable device scratch for the host-slice API and the MoE workspace
+  void *scratch = nullptr;
+  size_t scratch_bytes = 0;
+  void *moe_ws = nullptr;
+  size_t moe_ws_bytes = 0;
+};
+
+static frx_status fail(frx_ctx *ctx, frx_status st, const char *fmt, ...) {
+  if (ctx) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(ctx->err, sizeof(ctx->err), fmt, ap);
+    va_end(ap);
+  }
+  return st;
+}
+
+static frx_status hip_fail(frx_ctx *ctx, hipError_t e, const char *what) {
+  const frx_status st = (e == hipErrorOutOfMemory) ? FRX_ERR_OOM : FRX_ERR_GPU;
+  return fail(ctx, st, "%s: %s (%d)", what, hipGetErrorString(e), (int)e);
+}
+
+// Makes the context's device current for the calling thread.
+static frx_status enter(frx_ctx *ctx) {
+  if (!ctx) return FRX_ERR_DEVICE;
+  ctx->err[0] = 0;
+  hipError_t e = hipSetDevice(ctx->device);
+  if (e != hipSuccess) return fail(ctx, FRX_ERR_DEVICE, "hipSetDevice(%d): %s", ctx->device, hipGetErrorString(e));
+  return FRX_OK;
+}
+
+static bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+extern "C" {
+
+const char *frx_version(void) { return "frx_ternary 0.1.0 gfx950"; }
+
+const char *frx_status_string(frx_status s) {
+  switch (s) {
+    case FRX_OK: return "ok";
+    case FRX_ERR_GPU: return "GPU error";
+    case FRX_ERR_SHAPE: return "shape error";
+    case FRX_ERR_DEVICE: return "device error";
+    case FRX_ERR_SHADER: return "kernel error";
+    case FRX_ERR_OOM: return "out of memory";
+    case FRX_ERR_UNSUPPORTED: return "unsupported";
+  }
+  return "unknown status";
+}
+
+frx_status frx_create(int device, frx_ctx **out) {
+  if (!out) return FRX_ERR_DEVICE;
+  *out = nullptr;
+  int n = 0;
+  if (hipGetDeviceCount(&n) != hipSuccess || n <= 0) return FRX_ERR_DEVICE;
+  if (device < 0 || device >= n) return FRX_ERR_DEVICE;
+  hipDeviceProp_t prop;
+  if (hipGetDeviceProperties(&prop, device) != hipSuccess) return FRX_ERR_DEVICE;
+  if (strncmp(prop.gcnArchName, "gfx950", 6) != 0) return FRX_ERR_UNSUPPORTED;
+  frx_ctx *c = new frx_ctx();
+  c->device = device;
+  *out = c;
+  return FRX_OK;
+}
+
+void frx_destroy(frx_ctx *ctx) {
+  if (!ctx) return;
+  hipSetDevice(ctx->device);
+  if (ctx->scratch) hipFree(ctx->scratch);
+  if (ctx->moe_ws) hipFree(ctx->moe_ws);
+  delete ctx;
+}
+
+frx_status frx_set_stream(frx_ctx *ctx, void *hip_stream) {
+  if (!ctx) return FRX_ERR_DEVICE;
+  ctx->stream = reinterpret_cast<hipStream_t>(hip_stream);
+  return FRX_OK;
+}
+
+frx_status frx_synchronize(frx_ctx *ctx) {
+  frx_status st = enter(ctx);
+  if (st != FRX_OK) return st;
+  hipError_t e = hipStreamSynchronize(ctx->stream);
+  if (e != hipSuccess) return hip_fail(ctx, e, "hipStreamSynchronize");
+  return FRX_OK;
+}
+
+const char *frx_last_error(const frx_ctx *ctx) { return ctx ? ctx->err : ""; }
+
+static frx_status check_linear(frx_ctx *ctx, const void *w, const void *scale,
+                               const void *x, frx_dtype xt, const void *y,
+                               frx_dtype yt, uint32_t M, uint32_t K,
+                               uint32_t N, bool sparse) {
+  if (!w || !scale || !x || !y) return fail(ctx, FRX_ERR_SHAPE, "null buffer pointer");
+  if (M == 0 || K == 0 || N == 0) return fail(ctx, FRX_ERR_SHAPE, "empty shape M=%u K=%u N=%u", M, K, N);
+  if (!sparse && K % 16 != 0)
+    return fail(ctx, FRX_ERR_SHAPE, "in_cols=%u must be a multiple of 16 for the row-aligned u32 layout", K);
+  if (sparse && K % 4 != 0) return fail(ctx, FRX_ERR_SHAPE, "in_cols=%u must be a multiple of 4 for 2:4", K);
+  if ((xt != FRX_F32 && xt != FRX_BF16) || (yt != FRX_F32 && yt != FRX_BF16))
+    return fail(ctx, FRX_ERR_UNSUPPORTED, "dtype must be FRX_F32 or FRX_BF16");
+  if (!aligned16(x) || !aligned16(y) || !aligned16(scale))
+    return fail(ctx, FRX_ERR_UNSUPPORTED, "x, y and scale must be 16-byte aligned device pointers");
+  if ((size_t)M * K > (size_t)0x7FFFFFFF || (size_t)M * N > (size_t)0x7FFFFFFF)
+    return fail(ctx, FRX_ERR_SHAPE, "M*K or M*N exceeds 2^31 elements");
+  return FRX_OK;
+}
+
+frx_status frx_ternary_linear(frx_ctx *ctx, const uint32_t *w,
+                              const float *scale, const void *x, frx_dtype xt,
+                              void *y, frx_dtype yt, uint32_t M, uint32_t K,
+                              uint32_t N) {
+  frx_status st = enter(ctx);
+  if (st != FRX_OK) return st;
+  if ((st = check_linear(ctx, w, scale, x, xt, y, yt, M, K, N, false)) != FRX_OK) return st;
+  hipError_t e;
+  if (M <= 16)
+    e = frx::launch_gemv(w, scale, x, xt == FRX_BF16, y, yt == FRX_BF16, (int)M, (int)K, (int)N, ctx->stream);
+  else
+    e = frx::launch_gemm(w, scale, x, xt == FRX_BF16, y, yt == FRX_BF16, (int)M, (int)K, (int)N, 0, ctx->stream);
+  if (e != hipSuccess) return hip_fail(ctx, e, "ternary_linear launch");
+  return FRX_OK;
+}
+
+frx_status frx_sparse24_ternary_linear(frx_ctx *ctx, const uint32_t *meta,
+                                       const float *scale, const void *x,
+                                       frx_dtype xt, void *y, frx_dtype yt,
+                                       uint32_t M, uint32_t K, uint32_t N) {
+  frx_status st = enter(ctx);
+  if (st != FRX_OK) return st;
+  if ((st = check_linear(ctx, meta, scale, x, xt, y, yt, M, K, N, true)) != FRX_OK) return st;
+  if (K % 16 != 0 && !(xt == FRX_BF16 ? (K % 8 == 0) : (K % 4 == 0)))
+    return fail(ctx, FRX_ERR_SHAPE, "in_cols=%u: rows must stay element aligned", K);
+  hipError_t e = frx::launch_gemm(meta, scale, x, xt == FRX_BF16, y, yt == FRX_BF16, (int)M, (int)K, (int)N, 1,
+                                  ctx->stream);
+  if (e != hipSuccess) return hip_fail(ctx, e, "sparse24_ternary_linear launch");
+  return FRX_OK;
+}
+
+frx_status frx_moe_ternary_ffn(
+    frx_ctx *ctx, const void *x, frx_dtype xt, const void *router,
+    frx_dtype rt, const uint32_t *const *w_gate, const float *const *s_gate,
+    const uint32_t *const *w_up, const float *const *s_up,
+    const uint32_t *const *w_down, const float *const *s_down, uint32_t T,
+    uint32_t H, uint32_t I, uint32_t E, uint32_t top_k, frx_activation act,
+    void *y, frx_dtype yt, uint32_t *topk_idx, float *topk_w) {
+  frx_status st = enter(ctx);
+  if (st != FRX_OK) return st;
+  if (!x || !router || !w_gate || !s_gate || !w_up || !s_up || !w_down || !s_down || !y)
+    return fail(ctx, FRX_ERR_SHAPE, "null pointer argument");
+  if (T == 0 || H == 0 || I == 0 || E == 0) return fail(ctx, FRX_ERR_SHAPE, "empty shape");
+  if (E > 64) return fail(ctx, FRX_ERR_SHAPE, "num_experts=%u exceeds 64", E);
+  if (top_k == 0 || top_k > E) return fail(ctx, FRX_ERR_SHAPE, "top_k=%u must be in [1, %u]", top_k, E);
+  if (H % 16 != 0 || I % 16 != 0)
+    return fail(ctx, FRX_ERR_SHAPE, "hidden=%u and intermediate=%u must be multiples of 16", H, I);
+  if ((xt != FRX_F32 && xt != FRX_BF16) || (rt != FRX_F32 && rt != FRX_BF16) || (yt != FRX_F32 && yt != FRX_BF16))
+    return fail(ctx, FRX_ERR_UNSUPPORTED, "dtype must be FRX_F32 or FRX_BF16");
+  if (act != FRX_ACT_SILU && act != FRX_ACT_GELU_TANH) return fail(ctx, FRX_ERR_UNSUPPORTED, "activation");
+  for (uint32_t e = 0; e < E; e++)
+    if (!w_gate[e] || !s_gate[e] || !w_up[e] || !s_up[e] || !w_down[e] || !s_down[e])
+      return fail(ctx, FRX_ERR_SHAPE, "null weight pointer for expert %u", e);
+  if ((size_t)T * top_k * I > (size_t)0x7FFFFFFF) return fail(ctx, FRX_ERR_SHAPE, "T*top_k*I too large");
+  const size_t need = frx::moe_workspace_bytes((int)T, (int)H, (int)I, (int)E, (int)top_k);
+  if (need > ctx->moe_ws_bytes) {
+    if (ctx->moe_ws) {
+      hipStreamSynchronize(ctx->stream);
+      hipFree(ctx->moe_ws);
+      ctx->moe_ws = nullptr;
+      ctx->moe_ws_bytes = 0;
+    }
+    hipError_t e = hipMalloc(&ctx->moe_ws, need);
+    if (e != hipSuccess) return hip_fail(ctx, e, "MoE workspace allocation");
+    ctx->moe_ws_bytes = need;
+  }
+  frx::MoeWorkspace ws;
+  frx::moe_workspace_carve(ctx->moe_ws, (int)T, (int)H, (int)I, (int)E, (int)top_k, &ws);
+  hipError_t e = frx::launch_moe(x, xt == FRX_BF16, router, rt == FRX_BF16, w_gate, s_gate, w_up, s_up, w_down,
+                                 s_down, (int)T, (int)H, (int)I, (int)E, (int)top_k, act == FRX_ACT_GELU_TANH, y,
+                                 yt == FRX_BF16, topk_idx, topk_w, ws, ctx->stream);
+  if (e != hipSuccess) return hip_fail(ctx, e, "moe launch");
+  return FRX_OK;
+}
+
+// ---- host-slice accelerator API (GpuMatmulAccelerator) --------------------
+
+static frx_status ensure_scratch(frx_ctx *ctx, size_t bytes) {
+  if (bytes <= ctx->scratch_bytes) return FRX_OK;
+  if (ctx->scratch) {
+    hipStreamSynchronize(ctx->stream);
+    hipFree(ctx->scratch);
+    ctx->scratch = nullptr;
+    ctx->scratch_bytes = 0;
+  }
+  hipError_t e = hipMalloc(&ctx->scratch, bytes);
+  if (e != hipSuccess) return hip_fail(ctx, e, "device scratch allocation");
+  ctx->scratch_bytes = bytes;
+  return FRX_OK;
+}
+
+static size_t a256(size_t v) { return (v + 255) & ~(size_t)255; }
+
+static frx_status host_linear(frx_ctx *ctx, const uint32_t *w_host,
+                              const float *s_host, const uint32_t *w_dev,
+                              const float *s_dev, const float *input,
+                              size_t seq, size_t in_cols, size_t out_rows,
+                              float *out, bool sparse) {
+  frx_status st = enter(ctx);
+  if (st != FRX_OK) return st;
+  if (!input || !out) return fail(ctx, FRX_ERR_SHAPE, "null host buffer");
+  if (seq == 0 || in_cols == 0 || out_rows == 0) return fail(ctx, FRX_ERR_SHAPE, "empty shape");
+  if (seq > 0xFFFFFFFFu || in_cols > 0xFFFFFFFFu || out_rows > 0xFFFFFFFFu)
+    return fail(ctx, FRX_ERR_SHAPE, "dimension exceeds 32 bits");
+  size_t wwords = 0;
+  if (w_host) {
+    if (sparse) {
+      const size_t gpr = (in_cols + 3) / 4;
+      wwords = out_rows * ((gpr + 5) / 6);
+    } else {
+      wwords = out_rows * ((in_cols + 15) / 16);
+    }
+  }
+  const size_t bw = a256(wwords * 4), bs = w_host ? a256(out_rows * 4) : 0;
+  const size_t bx = a256(seq * in_cols * 4), by = a256(seq * out_rows * 4);
+  if ((st = ensure_scratch(ctx, bw + bs + bx + by)) != FRX_OK) return st;
+  char *base = reinterpret_cast<char *>(ctx->scratch);
+  uint32_t *dw = w_host ? reinterpret_cast<uint32_t *>(base) : const_cast<uint32_t *>(w_dev);
+  float *ds = w_host ? reinterpret_cast<float *>(base + bw) : const_cast<float *>(s_dev);
+  float *dx = reinterpret_cast<float *>(base + bw + bs);
+  float *dy = reinterpret_cast<float *>(base + bw + bs + bx);
+  hipError_t e;
+  if (w_host) {
+    if (!s_host) return fail(ctx, FRX_ERR_SHAPE, "null scales");
+    if ((e = hipMemcpyAsync(dw, w_host, wwords * 4, hipMemcpyHostToDevice, ctx->stream)) != hipSuccess)
+      return hip_fail(ctx, e, "weight upload");
+    if ((e = hipMemcpyAsync(ds, s_host, out_rows * 4, hipMemcpyHostToDevice, ctx->stream)) != hipSuccess)
+      return hip_fail(ctx, e, "scale upload");
+  }
+  if ((e = hipMemcpyAsync(dx, input, seq * in_cols * 4, hipMemcpyHostToDevice, ctx->stream)) != hipSuccess)
+    return hip_fail(ctx, e, "input upload");
+  st = sparse ? frx_sparse24_ternary_linear(ctx, dw, ds, dx, FRX_F32, dy, FRX_F32, (uint32_t)seq,
+                                            (uint32_t)in_cols, (uint32_t)out_rows)
+              : frx_ternary_linear(ctx, dw, ds, dx, FRX_F32, dy, FRX_F32, (uint32_t)seq, (uint32_t)in_cols,
+                                   (uint32_t)out_rows);
+  if (st != FRX_OK) return st;
+  if ((e = hipMemcpyAsync(out, dy, seq * out_rows * 4, hipMemcpyDeviceToHost, ctx->stream)) != hipSuccess)
+    return hip_fail(ctx, e, "output readback");
+  if ((e = hipStreamSynchronize(ctx->stream)) != hipSuccess) return hip_fail(ctx, e, "synchronize");
+  return FRX_OK;
+}
+
+frx_status frx_gpu_ternary_matmul(frx_ctx *ctx, const uint32_t *packed_weights,
+                                  const float *scales, const float *input,
+                                  size_t seq_len, size_t in_cols,
+                                  size_t out_rows, float *out) {
+  if (!packed_weights) return fail(ctx, FRX_ERR_SHAPE, "null packed weights");
+  return host_linear(ctx, packed_weights, scales, nullptr, nullptr, input, seq_len, in_cols, out_rows, out, false);
+}
+
+frx_status frx_gpu_ternary_matmul_vram(frx_ctx *ctx, const uint32_t *w_dev,
+                                       const float *s_dev, const float *input,
+                                       size_t seq_len, size_t in_cols,
+                                       size_t out_rows, float *out) {
+  if (!w_dev || !s_dev) return fail(ctx, FRX_ERR_SHAPE, "null device weight buffer");
+  return host_linear(ctx, nullptr, nullptr, w_dev, s_dev, input, seq_len, in_cols, out_rows, out, false);
+}
+
+frx_status frx_gpu_sparse_ternary_matmul(frx_ctx *ctx, const uint32_t *meta,
+                                         const float *scales,
+                                         const float *input, size_t seq_len,
+                                         size_t in_cols, size_t out_rows,
+                                         float *out) {
+  if (!meta) return fail(ctx, FRX_ERR_SHAPE, "null sparse metadata");
+  return host_linear(ctx, meta, scales, nullptr, nullptr, input, seq_len, in_cols, out_rows, out, true);
+}
+
+}  // extern "C"

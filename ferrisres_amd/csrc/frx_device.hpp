@@ -1,0 +1,172 @@
+// frx_device.hpp — device-side building blocks shared by the gfx950 kernels.
+//
+// Operand encoding. A 2-bit code c in {0:-1, 1:0, 2:+1, 3:0}
+// (src/model/ternary.rs:134-140) maps to the bf16 bit pattern
+// ((~c) & 3) << 14:
+//     c=0 -> 0xC000 = -2.0    c=1 -> 0x8000 = -0.0
+//     c=2 -> 0x4000 = +2.0    c=3 -> 0x0000 = +0.0
+// i.e. exactly 2*dec(c), code 3 included. Products with bf16 activations are
+// exact in the MFMA's fp32 datapath; the factor 2 is removed by scaling the
+// per-row scale by 0.5 in the epilogue (exact: a power of two).
+//
+// K-interleave. Inside a 16-code word, codes i and i+8 sit at bits 2i and
+// 2i+16, so one shift and one AND place both in the sign/exponent bits of the
+// two bf16 halves of a dword:  pair_i = (~w << (14 - 2i)) & 0xC000C000.
+// The MFMA sums over k, so any k order is valid as long as both operands use
+// the same one: activations are staged with the matching order, i.e. within
+// each 16-column block dword i holds (x[i], x[i+8]).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace frx {
+
+typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8;
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ f32x4 mfma16(const u32x4 &a, const u32x4 &b,
+                                        const f32x4 &c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+      __builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0, 0,
+      0);
+}
+
+// Pairs 4h..4h+3 of an inverted 16-code word as MFMA bf16 operand dwords.
+template <int H>
+__device__ __forceinline__ u32x4 unpack_half(uint32_t nw) {
+  u32x4 r;
+  r.x = (nw << (14 - 2 * (4 * H + 0))) & 0xC000C000u;
+  r.y = (nw << (14 - 2 * (4 * H + 1))) & 0xC000C000u;
+  r.z = (nw << (14 - 2 * (4 * H + 2))) & 0xC000C000u;
+  r.w = (nw << (14 - 2 * (4 * H + 3))) & 0xC000C000u;
+  return r;
+}
+
+// Round-to-nearest-even f32 -> bf16 (NaN stays NaN).
+__device__ __forceinline__ uint32_t bf16_rne(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7FFFFFFFu) > 0x7F800000u) return (u >> 16) | 0x40u;
+  u += 0x7FFFu + ((u >> 16) & 1u);
+  return u >> 16;
+}
+
+__device__ __forceinline__ float bf16_to_f32(uint32_t h) {
+  return __uint_as_float(h << 16);
+}
+
+// Split f32 into bf16 hi + lo with |x - hi - lo| <= 2^-17 |x| (hi carries
+// infinities, lo is then 0).
+__device__ __forceinline__ void split_bf16(float x, uint32_t &hi,
+                                           uint32_t &lo) {
+  hi = bf16_rne(x);
+  float r = x - bf16_to_f32(hi);
+  lo = ((hi & 0x7F80u) == 0x7F80u) ? 0u : bf16_rne(r);
+}
+
+// Natural bf16 dwords n[0..7] of a 16-column block (x0..x15) -> interleaved
+// dwords d[i] = x[i] | x[i+8] << 16.
+__device__ __forceinline__ void interleave16(const uint32_t n[8],
+                                             uint32_t d[8]) {
+#pragma unroll
+  for (int j = 0; j < 4; j++) {
+    d[2 * j] = (n[j] & 0xFFFFu) | (n[j + 4] << 16);
+    d[2 * j + 1] = (n[j] >> 16) | (n[j + 4] & 0xFFFF0000u);
+  }
+}
+
+// Loads one 16-column block of activations and produces the interleaved
+// bf16 dwords (hi plane; lo plane when the source is f32).
+template <typename XT>
+struct XBlock;
+
+template <>
+struct XBlock<uint16_t> {
+  static constexpr int P = 1;
+  __device__ __forceinline__ static void load(const uint16_t *src,
+                                              bool ok, uint32_t hi[8],
+                                              uint32_t lo[8]) {
+    (void)lo;
+    uint32_t n[8];
+    if (ok) {
+      const u32x4 *s = reinterpret_cast<const u32x4 *>(src);
+      u32x4 a = s[0], b = s[1];
+      n[0] = a.x; n[1] = a.y; n[2] = a.z; n[3] = a.w;
+      n[4] = b.x; n[5] = b.y; n[6] = b.z; n[7] = b.w;
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; i++) n[i] = 0;
+    }
+    interleave16(n, hi);
+  }
+};
+
+template <>
+struct XBlock<float> {
+  static constexpr int P = 2;
+  __device__ __forceinline__ static void load(const float *src, bool ok,
+                                              uint32_t hi[8], uint32_t lo[8]) {
+    uint32_t h[16], l[16];
+    if (ok) {
+      const float4 *s = reinterpret_cast<const float4 *>(src);
+#pragma unroll
+      for (int q = 0; q < 4; q++) {
+        float4 v = s[q];
+        split_bf16(v.x, h[4 * q + 0], l[4 * q + 0]);
+        split_bf16(v.y, h[4 * q + 1], l[4 * q + 1]);
+        split_bf16(v.z, h[4 * q + 2], l[4 * q + 2]);
+        split_bf16(v.w, h[4 * q + 3], l[4 * q + 3]);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 16; i++) h[i] = l[i] = 0;
+    }
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      hi[i] = h[i] | (h[i + 8] << 16);
+      lo[i] = l[i] | (l[i + 8] << 16);
+    }
+  }
+};
+
+// Output stores of 4 consecutive columns.
+template <typename YT>
+struct YStore;
+
+template <>
+struct YStore<float> {
+  __device__ __forceinline__ static void store4(float *dst, f32x4 v, int n_ok) {
+    if (n_ok >= 4 && ((reinterpret_cast<uintptr_t>(dst) & 15) == 0)) {
+      *reinterpret_cast<float4 *>(dst) = make_float4(v.x, v.y, v.z, v.w);
+    } else {
+      if (n_ok > 0) dst[0] = v.x;
+      if (n_ok > 1) dst[1] = v.y;
+      if (n_ok > 2) dst[2] = v.z;
+      if (n_ok > 3) dst[3] = v.w;
+    }
+  }
+};
+
+template <>
+struct YStore<uint16_t> {
+  __device__ __forceinline__ static void store4(uint16_t *dst, f32x4 v,
+                                                int n_ok) {
+    uint32_t a = bf16_rne(v.x), b = bf16_rne(v.y), c = bf16_rne(v.z),
+             d = bf16_rne(v.w);
+    if (n_ok >= 4 && ((reinterpret_cast<uintptr_t>(dst) & 7) == 0)) {
+      u32x2 p;
+      p.x = a | (b << 16);
+      p.y = c | (d << 16);
+      *reinterpret_cast<u32x2 *>(dst) = p;
+    } else {
+      uint16_t *o = reinterpret_cast<uint16_t *>(dst);
+      if (n_ok > 0) o[0] = (uint16_t)a;
+      if (n_ok > 1) o[1] = (uint16_t)b;
+      if (n_ok > 2) o[2] = (uint16_t)c;
+      if (n_ok > 3) o[3] = (uint16_t)d;
+    }
+  }
+};
+
+}  // namespace frx

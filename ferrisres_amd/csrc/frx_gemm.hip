@@ -1,0 +1,75 @@
+// frx_gemm.hip — prefill ternary GEMM (dense and 2:4) on gfx950 MFMA.
+//
+// Replaces ternary_matmul_main / sparse_ternary_matmul_main
+// (src/compute/kernels/ternary_matmul.rs:32-75,
+// src/compute/kernels/sparse_ternary.rs:54-112) for M > 16 tokens. The WGSL
+// kernels launch one thread per output with a 1-D grid, which cannot even be
+// dispatched at 2048 x 4096 (over 65,535 workgroups); here each workgroup
+// owns a 128 x 128 output tile (see frx_gemm_core.hpp).
+#include "frx_gemm_core.hpp"
+#include "frx_internal.hpp"
+
+namespace frx {
+
+template <int BM, int BN, int WM, int WN, int XS, int WF, typename YT>
+__global__ __launch_bounds__(WM *WN * 64) void gemm_kernel(
+    const uint32_t *__restrict__ W, const float *__restrict__ scale,
+    const void *__restrict__ X, YT *__restrict__ Y, int M, int K, int N,
+    int wvec) {
+  using Core = GemmCore<BM, BN, WM, WN, XS, 1, WF>;
+  __shared__ __align__(16) uint32_t lds[Core::LDS_DWORDS];
+  const int n0 = blockIdx.x * BN, m0 = blockIdx.y * BM;
+  XDesc xd{X, nullptr, nullptr, (long)m0, K};
+  const uint32_t *Wm[1] = {W};
+  f32x4 acc[1][Core::FN][Core::FM];
+  Core::run(lds, xd, min(BM, M - m0), Wm, n0, N, K, wvec, acc);
+  // 2*dec(c) encoding for dense codes (frx_device.hpp): halve the scale.
+  const float half = 0.5f;
+#pragma unroll
+  for (int fn = 0; fn < Core::FN; fn++) {
+    const int n = n0 + Core::rowoff(fn);
+    if (n >= N) continue;
+    const int nok = min(4, N - n);
+    const f32x4 sc = load_scale4(scale, n, nok) * half;
+#pragma unroll
+    for (int fm = 0; fm < Core::FM; fm++) {
+      const int m = m0 + Core::tok(fm);
+      if (m < M) YStore<YT>::store4(Y + (size_t)m * N + n, acc[0][fn][fm] * sc, nok);
+    }
+  }
+}
+
+template <int XS, int WF, typename YT>
+static hipError_t launch_gemm_t(const uint32_t *w, const float *scale,
+                                const void *x, void *y, int M, int K, int N,
+                                hipStream_t stream) {
+  constexpr int BM = 128, BN = 128, WM = 2, WN = 2;
+  const int wvec = ((K >> 4) % 4 == 0) && ((reinterpret_cast<uintptr_t>(w) & 15) == 0);
+  dim3 grid((N + BN - 1) / BN, (M + BM - 1) / BM);
+  hipLaunchKernelGGL((gemm_kernel<BM, BN, WM, WN, XS, WF, YT>), grid,
+                     dim3(WM * WN * 64), 0, stream, w, scale, x,
+                     reinterpret_cast<YT *>(y), M, K, N, wvec);
+  return hipGetLastError();
+}
+
+template <int WF>
+static hipError_t launch_gemm_wf(const uint32_t *w, const float *scale,
+                                 const void *x, int xt_bf16, void *y,
+                                 int yt_bf16, int M, int K, int N,
+                                 hipStream_t stream) {
+  if (xt_bf16) {
+    if (yt_bf16) return launch_gemm_t<XS_BF16, WF, uint16_t>(w, scale, x, y, M, K, N, stream);
+    return launch_gemm_t<XS_BF16, WF, float>(w, scale, x, y, M, K, N, stream);
+  }
+  if (yt_bf16) return launch_gemm_t<XS_F32, WF, uint16_t>(w, scale, x, y, M, K, N, stream);
+  return launch_gemm_t<XS_F32, WF, float>(w, scale, x, y, M, K, N, stream);
+}
+
+hipError_t launch_gemm(const uint32_t *w, const float *scale, const void *x,
+                       int xt_bf16, void *y, int yt_bf16, int M, int K, int N,
+                       int sp24, hipStream_t stream) {
+  if (sp24) return launch_gemm_wf<WF_SP24>(w, scale, x, xt_bf16, y, yt_bf16, M, K, N, stream);
+  return launch_gemm_wf<WF_DENSE>(w, scale, x, xt_bf16, y, yt_bf16, M, K, N, stream);
+}
+
+}  // namespace frx

@@ -1,0 +1,47 @@
+// frx_internal.hpp — launchers shared between the kernel files and the C ABI.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace frx {
+
+// Decode GEMV, B <= 16 tokens (frx_gemv.hip).
+hipError_t launch_gemv(const uint32_t *w, const float *scale, const void *x,
+                       int xt_bf16, void *y, int yt_bf16, int B, int K, int N,
+                       hipStream_t stream);
+// 2:4 decode GEMV, B <= 16 tokens (frx_gemv.hip).
+hipError_t launch_gemv_sp24(const uint32_t *meta, const float *scale,
+                            const void *x, int xt_bf16, void *y, int yt_bf16,
+                            int B, int K, int N, hipStream_t stream);
+// Dense / 2:4 GEMM, any M (frx_gemm.hip). sp24 selects the metadata layout.
+hipError_t launch_gemm(const uint32_t *w, const float *scale, const void *x,
+                       int xt_bf16, void *y, int yt_bf16, int M, int K, int N,
+                       int sp24, hipStream_t stream);
+
+// MoE pipeline (frx_moe.hip).
+struct MoeWorkspace {
+  uint32_t *idx;       // [T*k] selected experts (sorted order per token)
+  float *wts;          // [T*k] routing weights
+  int *counts;         // [E] tokens per expert
+  int *offsets;        // [E+1] exclusive scan of counts
+  int *perm_token;     // [T*k] token of each expert-sorted row
+  int *inv;            // [T*k] expert-sorted row of assignment t*k+j
+  int *tiles;          // [2*max_tiles] (expert, first row) per M tile
+  int *ntiles;         // [1]
+  uint16_t *h_hi;      // [T*k][I] SwiGLU output, bf16 hi plane
+  uint16_t *h_lo;      // [T*k][I] lo plane
+  float *dout;         // [T*k][H] down-projection rows
+};
+size_t moe_workspace_bytes(int T, int H, int I, int E, int top_k);
+void moe_workspace_carve(void *base, int T, int H, int I, int E, int top_k,
+                         MoeWorkspace *ws);
+hipError_t launch_moe(const void *x, int xt_bf16, const void *router,
+                      int rt_bf16, const uint32_t *const *w_gate,
+                      const float *const *s_gate, const uint32_t *const *w_up,
+                      const float *const *s_up, const uint32_t *const *w_down,
+                      const float *const *s_down, int T, int H, int I, int E,
+                      int top_k, int gelu, void *y, int yt_bf16,
+                      uint32_t *topk_idx, float *topk_w, const MoeWorkspace &ws,
+                      hipStream_t stream);
+
+}  // namespace frx

@@ -1,0 +1,167 @@
+/*
+ * frx_ternary.h — C ABI of the MI355X (gfx950) ternary linear backend for
+ * FerrisRes. Library: ferrisres_amd/libfrx_ternary.so.
+ *
+ * Weight layouts are the reference's, unchanged:
+ *  - dense: row-major [N][K/16] u32, 16 two-bit codes per word, LSB first,
+ *    codes {0b00:-1, 0b01:0, 0b10:+1, 0b11:0}
+ *    (src/compute/kernels/ternary_matmul.rs:3-11, src/model/ternary.rs:134-140);
+ *    one f32 scale per output row (ternary_matmul.rs:27,74).
+ *  - 2:4 sparse: per row ceil(ceil(K/4)/6) u32 words, six 5-bit groups per
+ *    word, group = pattern[2:0] | sign_lo[3] | sign_hi[4], sign bit 1 = -1
+ *    (src/compute/kernels/sparse_ternary.rs:7-10,71-108).
+ *
+ * Conventions:
+ *  - GPU entry points take device pointers owned by the caller, enqueue work
+ *    on the context's stream and never synchronise (the reference records
+ *    into a caller-owned CommandEncoder, kernels/ternary_matmul.rs:167-225).
+ *  - Errors are returned, never raised: the enum is 1:1 with
+ *    FerrisResError (src/error.rs:4-22). frx_last_error() gives the message.
+ *  - y[m][n] = scale[n] * sum_k dec(W[n][k]) * x[m][k] (fp32 accumulation).
+ */
+#ifndef FRX_TERNARY_H
+#define FRX_TERNARY_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct frx_ctx frx_ctx;
+
+/* 1:1 with FerrisResError::{Gpu, Shape, Device, Shader, OOM, Unsupported}
+ * (src/error.rs:4-22). */
+typedef enum frx_status {
+  FRX_OK = 0,
+  FRX_ERR_GPU = 1,
+  FRX_ERR_SHAPE = 2,
+  FRX_ERR_DEVICE = 3,
+  FRX_ERR_SHADER = 4,
+  FRX_ERR_OOM = 5,
+  FRX_ERR_UNSUPPORTED = 6
+} frx_status;
+
+typedef enum frx_dtype { FRX_F32 = 0, FRX_BF16 = 1 } frx_dtype;
+
+typedef enum frx_activation { FRX_ACT_SILU = 0, FRX_ACT_GELU_TANH = 1 } frx_activation;
+
+/* ---- context -------------------------------------------------------------
+ * Replaces the Arc<Device>/Arc<Queue> pair ops are built from
+ * (TernaryMatMulOp::new, src/compute/kernels/ternary_matmul.rs:84-155).
+ * One context per (thread, stream); contexts are independent. */
+frx_status frx_create(int device, frx_ctx **out);
+void frx_destroy(frx_ctx *ctx);
+/* Caller-owned hipStream_t (NULL = the device's null stream); the analogue of
+ * the caller-owned CommandEncoder in TernaryMatMulOp::dispatch. */
+frx_status frx_set_stream(frx_ctx *ctx, void *hip_stream);
+/* Waits for all work enqueued on the context's stream. */
+frx_status frx_synchronize(frx_ctx *ctx);
+/* Message of the last failed call on this context ("" if none). */
+const char *frx_last_error(const frx_ctx *ctx);
+const char *frx_status_string(frx_status s);
+/* Library version string ("frx_ternary <major>.<minor>.<patch> gfx950"). */
+const char *frx_version(void);
+
+/* ---- dense ternary linear --------------------------------------------------
+ * Replaces TernaryMatMulOp::dispatch(encoder, ternary, scales, input, output,
+ * seq_len, in_cols, out_rows) (src/compute/kernels/ternary_matmul.rs:167-225),
+ * WGSL entry ternary_matmul_main (:32-75).
+ *   w     [N][K/16] u32      scale [N] f32
+ *   x     [M][K]  xt         y     [M][N] yt
+ * M = seq_len, K = in_cols, N = out_rows. Requires K % 16 == 0 (the u32
+ * repack of ternary.rs:1317-1328 is row-aligned only then), M, N >= 1.
+ * M <= 16 runs the decode GEMV kernel, larger M the MFMA GEMM kernel. */
+frx_status frx_ternary_linear(frx_ctx *ctx, const uint32_t *w,
+                              const float *scale, const void *x, frx_dtype xt,
+                              void *y, frx_dtype yt, uint32_t M, uint32_t K,
+                              uint32_t N);
+
+/* ---- 2:4 sparse ternary linear ---------------------------------------------
+ * Replaces SparseTernaryMatMulOp::dispatch (src/compute/kernels/
+ * sparse_ternary.rs:194-247), WGSL entry sparse_ternary_matmul_main (:54-112).
+ *   meta [N][ceil(ceil(K/4)/6)] u32, scale [N] f32. Requires K % 4 == 0. */
+frx_status frx_sparse24_ternary_linear(frx_ctx *ctx, const uint32_t *meta,
+                                       const float *scale, const void *x,
+                                       frx_dtype xt, void *y, frx_dtype yt,
+                                       uint32_t M, uint32_t K, uint32_t N);
+
+/* ---- MoE ternary expert layer -----------------------------------------------
+ * Replaces the GPU-path MoE glue of the model (router, softmax, stable top-k,
+ * per-expert ternary SwiGLU FFN, weighted sum; src/model/
+ * cpu_block_attn_res.rs:1148-1184 and :2284-2316), whose semantics are
+ * TernaryMoELayer::forward (src/model/ternary_moe.rs:145-223) with per-row
+ * scales. Routing is done on the device (router GEMV, softmax, stable sort,
+ * per-expert histogram and scan, token permutation); the experts run as
+ * grouped ternary GEMMs.
+ *   x [T][H] xt; router [E][H] rt (row e = expert e, ternary_moe.rs:157)
+ *   w_gate[e], w_up[e]: [I][H/16] u32, s_gate[e], s_up[e]: [I] f32
+ *   w_down[e]: [H][I/16] u32, s_down[e]: [H] f32   (device pointers; the
+ *   pointer arrays themselves are host arrays of length E)
+ *   y [T][H] yt; topk_idx [T][top_k] u32 and topk_w [T][top_k] f32 (device,
+ *   may be NULL).
+ * Requires H % 16 == 0, I % 16 == 0, 1 <= top_k <= E <= 64.
+ * Workspace is allocated on the context on first use (and grown). */
+frx_status frx_moe_ternary_ffn(
+    frx_ctx *ctx, const void *x, frx_dtype xt, const void *router,
+    frx_dtype rt, const uint32_t *const *w_gate, const float *const *s_gate,
+    const uint32_t *const *w_up, const float *const *s_up,
+    const uint32_t *const *w_down, const float *const *s_down, uint32_t T,
+    uint32_t H, uint32_t I, uint32_t E, uint32_t top_k, frx_activation act,
+    void *y, frx_dtype yt, uint32_t *topk_idx, float *topk_w);
+
+/* ---- host-side packers (no GPU) --------------------------------------------*/
+/* pack_ternary (src/model/ternary.rs:146-163): out has (n+3)/4 bytes. */
+frx_status frx_pack_ternary_u8(const int8_t *values, size_t n, uint8_t *out);
+/* unpack_ternary (src/model/ternary.rs:168-179). */
+frx_status frx_unpack_ternary_u8(const uint8_t *packed, size_t n, int8_t *out);
+/* pack_ternary_u32 (src/model/ternary.rs:1317-1328): n_values codes read from
+ * ceil(n_values/4) bytes; out has ceil(n_values/16) words. */
+frx_status frx_repack_u8_to_u32(const uint8_t *packed, size_t n_values,
+                                uint32_t *out);
+/* gpu_packed() (src/model/cpu_linear.rs:164-169, cpu_moe.rs:73-78): i8 [N][K]
+ * -> u32 [N][K/16] plus per-row scales filled with the tensor scale. */
+frx_status frx_gpu_packed(const int8_t *values, uint32_t N, uint32_t K,
+                          float tensor_scale, uint32_t *w_out,
+                          float *scales_out);
+/* GPU 2:4 packer (src/compute/kernels/sparse_ternary.rs:254-318, test-only
+ * in the reference): every group of 4 must hold exactly two nonzeros
+ * (FRX_ERR_SHAPE otherwise). scales may be NULL; when given it receives the
+ * reference's per-row absmean of the nonzeros. */
+frx_status frx_pack_sparse24_gpu(const int8_t *w, uint32_t N, uint32_t K,
+                                 uint32_t *meta, float *scales);
+/* Bit-exact transcoder from the CPU SparseTernaryMatrix layout (pattern
+ * nibbles + sign pairs, bit 1 = +1; src/model/sparse_ternary.rs:52-70) to the
+ * GPU 5-bit layout (sign bit 1 = -1). Requires K % 4 == 0. */
+frx_status frx_sparse24_cpu_to_gpu(const uint8_t *patterns,
+                                   const uint8_t *signs, uint32_t N,
+                                   uint32_t K, uint32_t *meta);
+
+/* ---- host-slice accelerator API ------------------------------------------
+ * Replaces GpuMatmulAccelerator (src/model/gpu_forward.rs:1146-1328): host
+ * inputs, synchronous, host f32 output [seq][out_rows]. Device memory is
+ * owned by the context and reused across calls. */
+/* gpu_ternary_matmul (gpu_forward.rs:1154-1237): uploads weights per call. */
+frx_status frx_gpu_ternary_matmul(frx_ctx *ctx, const uint32_t *packed_weights,
+                                  const float *scales, const float *input,
+                                  size_t seq_len, size_t in_cols,
+                                  size_t out_rows, float *out);
+/* gpu_ternary_matmul_vram (gpu_forward.rs:1245-1297): weights already on the
+ * device (w_dev, s_dev device pointers); only the input is uploaded. */
+frx_status frx_gpu_ternary_matmul_vram(frx_ctx *ctx, const uint32_t *w_dev,
+                                       const float *s_dev, const float *input,
+                                       size_t seq_len, size_t in_cols,
+                                       size_t out_rows, float *out);
+/* gpu_sparse_ternary_matmul (gpu_forward.rs:1299-1327; a zero-returning stub
+ * in the reference): host 2:4 metadata in the GPU layout + per-row scales. */
+frx_status frx_gpu_sparse_ternary_matmul(frx_ctx *ctx, const uint32_t *meta,
+                                         const float *scales,
+                                         const float *input, size_t seq_len,
+                                         size_t in_cols, size_t out_rows,
+                                         float *out);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* FRX_TERNARY_H */

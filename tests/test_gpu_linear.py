@@ -1,0 +1,141 @@
+"""Dense ternary linear on the GPU (decode GEMV for M <= 16, MFMA GEMM
+above) against the CPU oracle (kernels/ternary_matmul.rs:233-265 semantics).
+
+Tolerance (fp32 accumulate vs the reference's f32): elementwise
+|y - ref| <= 1e-3 * max(|ref|, rms(ref)) and normwise 1e-3; bf16 outputs
+within 1 bf16 ulp of bf16(ref). Dyadic inputs make every partial sum exact,
+so there the GPU must equal the reference bit for bit."""
+import numpy as np
+import pytest
+import torch
+
+import ferrisres_amd as frx
+import oracle
+from ferrisres_amd import synth
+from _gpu import assert_bf16_within_1ulp, assert_close_f32, dev_bf16, dev_f32, dev_u32, host
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def ctx():
+    assert torch.cuda.is_available(), "GPU tests need a gfx950 device"
+    c = frx.Context(0)
+    yield c
+    c.close()
+
+
+def _case(name, M, K, N, seed_x="x"):
+    t = synth.ternary_uniform(name, "w", N, K)
+    w = synth.pack_rows_u32(t)
+    s = synth.row_scales(name, "s", N, samples=256)
+    xf, xb = synth.activations(name, seed_x, M, K)
+    return t, w, s, xf, xb
+
+
+def _run(ctx, w, s, xf, xb, xt, yt):
+    M, K = xf.shape
+    N = w.shape[0]
+    x = dev_bf16(xb) if xt == "bf16" else dev_f32(xf)
+    y = torch.empty((M, N), dtype=torch.bfloat16 if yt == "bf16" else torch.float32, device="cuda:0")
+    y.fill_(float("nan"))
+    ctx.ternary_linear(dev_u32(w), dev_f32(s), x, y)
+    torch.cuda.synchronize()
+    return y
+
+
+SHAPES = [(1, 256, 64), (3, 512, 100), (16, 1024, 48), (1, 2064, 33), (5, 4096, 130),
+          (17, 256, 64), (64, 1040, 200), (130, 512, 136), (257, 128, 19)]
+
+
+@pytest.mark.parametrize("M,K,N", SHAPES)
+@pytest.mark.parametrize("xt,yt", [("bf16", "f32"), ("f32", "f32"), ("bf16", "bf16"), ("f32", "bf16")])
+def test_dense_parity_random(ctx, M, K, N, xt, yt):
+    name = f"dense/{M}x{K}x{N}"
+    t, w, s, xf, xb = _case(name, M, K, N)
+    if xt == "f32":  # genuine f32 activations (exercise the hi/lo split)
+        xf = synth.normal(synth.seed_of(name, "xf32"), M * K).reshape(M, K)
+    ref = oracle.ternary_matmul_u32(w, s, xf, M, K, N)
+    y = _run(ctx, w, s, xf, xb, xt, yt)
+    if yt == "f32":
+        assert_close_f32(host(y), ref)
+    else:
+        assert_bf16_within_1ulp(y.view(torch.int16).cpu().numpy().view(np.uint16), ref)
+
+
+def _dyadic_case(M, K, N, seed):
+    rng = np.random.default_rng(seed)
+    t = rng.integers(-1, 2, size=(N, K)).astype(np.int8)
+    x = (rng.integers(-64, 65, size=(M, K)) / 8.0).astype(np.float32)
+    s = (2.0 ** rng.integers(-4, 2, size=N)).astype(np.float32)
+    return t, synth.pack_rows_u32(t), s, x, synth.f32_to_bf16_bits(x)
+
+
+@pytest.mark.parametrize("M,K,N", [(1, 4096, 11008), (16, 11008, 4096), (7, 2048, 2048), (300, 4096, 1000),
+                                   (2048, 4096, 4096)])
+def test_dense_bit_exact_on_dyadic_inputs(ctx, M, K, N):
+    t, w, s, x, xb = _dyadic_case(M, K, N, M + K + N)
+    ref = (x @ t.T.astype(np.float32)) * s[None, :]
+    for xt in ("bf16", "f32"):
+        y = host(_run(ctx, w, s, x, xb, xt, "f32"))
+        np.testing.assert_array_equal(y, ref)
+
+
+@pytest.mark.parametrize("B", [1, 4, 16])
+@pytest.mark.parametrize("K,N", [(4096, 11008), (11008, 4096)])
+def test_decode_gemv_config_shapes(ctx, B, K, N):
+    """LLaMA-7B FFN decode shapes, bf16 x, fp32 accumulate (f32 and bf16 out)."""
+    name = f"decode/{K}x{N}"
+    t, w, s, xf, xb = _case(name, B, K, N, seed_x=f"x{B}")
+    ref = oracle.ternary_matmul_u32(w, s, xf, B, K, N)
+    assert_close_f32(host(_run(ctx, w, s, xf, xb, "bf16", "f32")), ref)
+    yb = _run(ctx, w, s, xf, xb, "bf16", "bf16")
+    assert_bf16_within_1ulp(yb.view(torch.int16).cpu().numpy().view(np.uint16), ref)
+
+
+@pytest.mark.parametrize("N", [4096, 11008])
+def test_prefill_gemm_config_shapes_sampled(ctx, N):
+    """X[2048,4096] bf16 x W[N,4096]: output rows depend only on their own
+    token, so 12 sampled tokens are checked against the oracle in full."""
+    M, K = 2048, 4096
+    name = f"prefill/{N}"
+    t, w, s, xf, xb = _case(name, M, K, N)
+    y = host(_run(ctx, w, s, xf, xb, "bf16", "f32"))
+    rows = np.array([0, 1, 15, 16, 127, 128, 1000, 1023, 1024, 2000, 2046, 2047])
+    ref = oracle.ternary_matmul_u32(w, s, xf[rows], len(rows), K, N)
+    assert_close_f32(y[rows], ref)
+    assert np.isfinite(y).all()
+
+
+def test_deterministic_across_runs(ctx):
+    t, w, s, xf, xb = _case("det", 16, 4096, 1024)
+    a = host(_run(ctx, w, s, xf, xb, "bf16", "f32"))
+    b = host(_run(ctx, w, s, xf, xb, "bf16", "f32"))
+    np.testing.assert_array_equal(a, b)
+    t, w, s, xf, xb = _case("det2", 300, 1024, 256)
+    a = host(_run(ctx, w, s, xf, xb, "bf16", "f32"))
+    b = host(_run(ctx, w, s, xf, xb, "bf16", "f32"))
+    np.testing.assert_array_equal(a, b)
+
+
+def test_code3_decodes_to_zero_on_gpu(ctx):
+    K, N = 64, 16
+    rng = np.random.default_rng(0)
+    w = rng.integers(0, 2 ** 32, size=(N, K // 16), dtype=np.uint64).astype(np.uint32)  # codes 0..3
+    s = np.ones(N, np.float32)
+    x = (rng.integers(-8, 9, size=(2, K)) / 4.0).astype(np.float32)
+    ref = oracle.ternary_matmul_u32(w, s, x, 2, K, N)
+    y = host(_run(ctx, w, s, x, synth.f32_to_bf16_bits(x), "f32", "f32"))
+    np.testing.assert_array_equal(y, ref)
+    y = host(_run(ctx, w, s, np.repeat(x, 10, 0), synth.f32_to_bf16_bits(np.repeat(x, 10, 0)), "f32", "f32"))
+    np.testing.assert_array_equal(y, np.repeat(ref, 10, 0))
+
+
+def test_shape_errors_are_statuses(ctx):
+    w = dev_u32(np.zeros((4, 1), np.uint32))
+    s = dev_f32(np.ones(4, np.float32))
+    x = dev_f32(np.ones((1, 20), np.float32))
+    y = torch.empty((1, 4), dtype=torch.float32, device="cuda:0")
+    with pytest.raises(frx.FrxError) as e:
+        ctx.ternary_linear(w, s, x, y)  # K = 20 is not a multiple of 16
+    assert e.value.kind == "Shape"

@@ -1,0 +1,108 @@
+"""MoE ternary expert layer on the GPU against the oracle (GPU-path MoE glue
+semantics, cpu_block_attn_res.rs:1148-1184 = TernaryMoELayer::forward with
+per-row scales). Routing indices must be bit-exact; outputs within 1e-3."""
+import numpy as np
+import pytest
+import torch
+
+import ferrisres_amd as frx
+import oracle
+from ferrisres_amd import synth
+from _gpu import assert_close_f32, dev_bf16, dev_f32, dev_u32, host
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def ctx():
+    assert torch.cuda.is_available(), "GPU tests need a gfx950 device"
+    c = frx.Context(0)
+    yield c
+    c.close()
+
+
+def make_moe(name, T, H, I, E):
+    xf, xb = synth.activations(name, "x", T, H)
+    rf, rb = synth.activations(name, "router", E, H, std=0.02)
+    ex = {}
+    for e in range(E):
+        for mat, (n, k) in (("gate", (I, H)), ("up", (I, H)), ("down", (H, I))):
+            t = synth.ternary_uniform(name, f"{mat}{e}", n, k)
+            ex[(mat, e)] = (synth.pack_rows_u32(t), synth.row_scales(name, f"s{mat}{e}", n, samples=256))
+    return xf, xb, rf, rb, ex
+
+
+def run_gpu(ctx, xf, xb, rf, rb, ex, E, top_k, act, xt="bf16", yt="f32"):
+    T, H = xf.shape
+    dw = {k: (dev_u32(v[0]), dev_f32(v[1])) for k, v in ex.items()}
+    x = dev_bf16(xb) if xt == "bf16" else dev_f32(xf)
+    r = dev_bf16(rb) if xt == "bf16" else dev_f32(rf)
+    y = torch.empty((T, H), dtype=torch.float32 if yt == "f32" else torch.bfloat16, device="cuda:0")
+    idx = torch.zeros((T, top_k), dtype=torch.int32, device="cuda:0")
+    w = torch.zeros((T, top_k), dtype=torch.float32, device="cuda:0")
+    g = lambda m, i: [dw[(m, e)][i] for e in range(E)]  # noqa: E731
+    ctx.moe_ternary_ffn(x, r, g("gate", 0), g("gate", 1), g("up", 0), g("up", 1), g("down", 0), g("down", 1),
+                        y, top_k=top_k, act=act, topk_idx=idx, topk_w=w)
+    torch.cuda.synchronize()
+    return y, idx.cpu().numpy().astype(np.uint32), w.cpu().numpy()
+
+
+def run_oracle(xf, rf, ex, E, top_k, gelu, tokens=None):
+    x = xf if tokens is None else xf[tokens]
+    g = lambda m, i: [ex[(m, e)][i] for e in range(E)]  # noqa: E731
+    return oracle.moe_forward(x, rf, g("gate", 0), g("gate", 1), g("up", 0), g("up", 1), g("down", 0),
+                              g("down", 1), top_k, gelu)
+
+
+@pytest.mark.parametrize("T,H,I,E,k", [(40, 128, 256, 8, 2), (7, 64, 96, 4, 1), (130, 256, 160, 16, 2),
+                                       (64, 128, 128, 6, 3)])
+@pytest.mark.parametrize("act", [frx.ACT_SILU, frx.ACT_GELU_TANH])
+def test_moe_small_parity(ctx, T, H, I, E, k, act):
+    name = f"moe/{T}x{H}x{I}x{E}"
+    xf, xb, rf, rb, ex = make_moe(name, T, H, I, E)
+    y, idx, w = run_gpu(ctx, xf, xb, rf, rb, ex, E, k, act)
+    ref, ridx, rw = run_oracle(xf, rf, ex, E, k, act == frx.ACT_GELU_TANH)
+    np.testing.assert_array_equal(idx, ridx)
+    np.testing.assert_allclose(w, rw, rtol=0, atol=1e-6)
+    assert_close_f32(host(y), ref)
+
+
+def test_moe_f32_inputs(ctx):
+    xf, xb, rf, rb, ex = make_moe("moe/f32", 33, 128, 192, 5)
+    xf = synth.normal(99, 33 * 128).reshape(33, 128)
+    rf = synth.normal(98, 5 * 128, 0.05).reshape(5, 128)
+    y, idx, w = run_gpu(ctx, xf, None, rf, None, ex, 5, 2, frx.ACT_SILU, xt="f32")
+    ref, ridx, rw = run_oracle(xf, rf, ex, 5, 2, False)
+    np.testing.assert_array_equal(idx, ridx)
+    assert_close_f32(host(y), ref)
+
+
+def test_moe_config_shape(ctx):
+    """512 tokens, H=2048, I=5632, 16 experts, top-2: routing for all tokens
+    is checked bit-exactly, outputs for 24 sampled tokens in full."""
+    T, H, I, E, k = 512, 2048, 5632, 16, 2
+    xf, xb, rf, rb, ex = make_moe("moe/config", T, H, I, E)
+    y, idx, w = run_gpu(ctx, xf, xb, rf, rb, ex, E, k, frx.ACT_SILU)
+    ridx, rw, _ = oracle.moe_route(xf, rf, k)
+    np.testing.assert_array_equal(idx, ridx)
+    np.testing.assert_allclose(w, rw, rtol=0, atol=1e-6)
+    tok = np.array([0, 1, 2, 63, 64, 100, 127, 128, 200, 255, 256, 300, 333, 400, 401, 450, 480, 500, 505,
+                    508, 509, 510, 511, 17])
+    ref, _, _ = run_oracle(xf, rf, ex, E, k, False, tokens=tok)
+    assert_close_f32(host(y)[tok], ref)
+    assert np.isfinite(host(y)).all()
+
+
+def test_moe_routing_deterministic_and_repeatable(ctx):
+    xf, xb, rf, rb, ex = make_moe("moe/rep", 96, 128, 128, 8)
+    a = run_gpu(ctx, xf, xb, rf, rb, ex, 8, 2, frx.ACT_SILU)
+    b = run_gpu(ctx, xf, xb, rf, rb, ex, 8, 2, frx.ACT_SILU)
+    np.testing.assert_array_equal(host(a[0]), host(b[0]))
+    np.testing.assert_array_equal(a[1], b[1])
+
+
+def test_moe_shape_errors(ctx):
+    xf, xb, rf, rb, ex = make_moe("moe/err", 4, 64, 64, 2)
+    with pytest.raises(frx.FrxError) as e:
+        run_gpu(ctx, xf, xb, rf, rb, ex, 2, 3, frx.ACT_SILU)  # top_k > E
+    assert e.value.kind == "Shape"

@@ -1,0 +1,86 @@
+"""2:4 sparse ternary linear on the GPU against the oracle's restatement of
+the WGSL 2:4 kernel (kernels/sparse_ternary.rs:321-360), in the GPU 5-bit
+layout. Same tolerances as the dense path."""
+import json
+import os
+
+import numpy as np
+import pytest
+import torch
+
+import ferrisres_amd as frx
+import oracle
+from ferrisres_amd import synth
+from _gpu import assert_bf16_within_1ulp, assert_close_f32, dev_bf16, dev_f32, dev_u32, host
+
+pytestmark = pytest.mark.gpu
+KATS = json.load(open(os.path.join(os.path.dirname(__file__), "golden", "reference_kats.json")))
+
+
+@pytest.fixture(scope="module")
+def ctx():
+    assert torch.cuda.is_available(), "GPU tests need a gfx950 device"
+    c = frx.Context(0)
+    yield c
+    c.close()
+
+
+def _run(ctx, meta, s, xf, xb, xt, yt):
+    M, K = xf.shape
+    N = meta.shape[0]
+    x = dev_bf16(xb) if xt == "bf16" else dev_f32(xf)
+    y = torch.empty((M, N), dtype=torch.bfloat16 if yt == "bf16" else torch.float32, device="cuda:0")
+    ctx.sparse24_ternary_linear(dev_u32(meta), dev_f32(s), x, y)
+    torch.cuda.synchronize()
+    return y
+
+
+@pytest.mark.parametrize("kat", KATS["sparse24_gpu"], ids=lambda k: k["source"].split()[-1])
+def test_reference_kats_on_gpu(ctx, kat):
+    w = np.array(kat["weights"], np.int8).reshape(kat["rows"], kat["cols"])
+    meta, sc = frx.pack_sparse24_gpu(w, with_scales=True)
+    x = np.array(kat["input"], np.float32).reshape(kat["seq"], kat["cols"])
+    y = host(_run(ctx, meta, sc, x, None, "f32", "f32"))
+    np.testing.assert_allclose(y.ravel(), kat["expected"], atol=kat["tol"], rtol=0)
+
+
+@pytest.mark.parametrize("M,K,N", [(1, 96, 8), (4, 1024, 100), (16, 2048, 64), (1, 4100, 37), (33, 512, 130),
+                                   (128, 4096, 256)])
+@pytest.mark.parametrize("xt,yt", [("bf16", "f32"), ("f32", "f32"), ("bf16", "bf16")])
+def test_sparse_parity_random(ctx, M, K, N, xt, yt):
+    name = f"sp24/{M}x{K}x{N}"
+    t = synth.sparse24_uniform(name, "w", N, K)
+    meta = frx.pack_sparse24_gpu(t)
+    s = synth.row_scales(name, "s", N, samples=256)
+    xf, xb = synth.activations(name, "x", M, K)
+    if xt == "f32":
+        xf = synth.normal(7, M * K).reshape(M, K)
+    ref = oracle.sparse24_gpu_matmul(meta, s, xf, M, K, N)
+    y = _run(ctx, meta, s, xf, xb, xt, yt)
+    if yt == "f32":
+        assert_close_f32(host(y), ref)
+    else:
+        assert_bf16_within_1ulp(y.view(torch.int16).cpu().numpy().view(np.uint16), ref)
+
+
+@pytest.mark.parametrize("M,K,N", [(2048, 4096, 4096), (16, 4096, 11008), (64, 11008, 512)])
+def test_sparse_bit_exact_on_dyadic(ctx, M, K, N):
+    rng = np.random.default_rng(M + N)
+    t = synth.sparse24_uniform(f"dy/{M}", "w", N, K)
+    meta = frx.pack_sparse24_gpu(t)
+    x = (rng.integers(-64, 65, size=(M, K)) / 8.0).astype(np.float32)
+    s = (2.0 ** rng.integers(-4, 2, size=N)).astype(np.float32)
+    ref = (x @ t.T.astype(np.float32)) * s[None, :]
+    y = host(_run(ctx, meta, s, x, synth.f32_to_bf16_bits(x), "bf16", "f32"))
+    np.testing.assert_array_equal(y, ref)
+
+
+def test_cpu_layout_through_transcoder(ctx):
+    rows, cols = 64, 512
+    t = synth.sparse24_uniform("tc", "w", rows, cols)
+    p, sg = oracle.sparse24_cpu_from_ternary(t, rows, cols)
+    meta = frx.sparse24_cpu_to_gpu(p, sg, rows, cols)
+    x = synth.normal(3, 8 * cols).reshape(8, cols)
+    s = np.full(rows, 0.03, np.float32)
+    ref = oracle.sparse24_cpu_matmul(p, sg, 0.03, rows, cols, x, 8).reshape(8, rows)
+    assert_close_f32(host(_run(ctx, meta, s, x, None, "f32", "f32")), ref)

@@ -1,0 +1,273 @@
+"""Pins the oracle beyond the reference KATs: exact-arithmetic identities,
+float64 brute force, independent numpy restatements and layout round trips.
+Each check is chosen so a plausible mistake (dropped term, wrong sign or
+index, transposed operand, wrong code table) fails it."""
+import numpy as np
+import pytest
+
+import oracle
+from ferrisres_amd import synth
+
+
+def _dyadic(rng, shape):
+    # small integers / 8: every partial sum of <= 2^16 terms is exact in f32
+    return (rng.integers(-64, 65, size=shape) / 8.0).astype(np.float32)
+
+
+def _dense_f64(t, x, scales):
+    return (x.astype(np.float64) @ t.astype(np.float64).T) * scales.astype(np.float64)[None, :]
+
+
+@pytest.mark.parametrize("m,k,n", [(1, 16, 8), (3, 48, 5), (7, 256, 33), (2, 1024, 64)])
+def test_u32_matmul_exact_on_dyadic(m, k, n):
+    rng = np.random.default_rng(m * 1000 + k + n)
+    t = rng.integers(-1, 2, size=(n, k)).astype(np.int8)
+    x = _dyadic(rng, (m, k))
+    sc = (2.0 ** rng.integers(-3, 3, size=n)).astype(np.float32)  # exact scales
+    out = oracle.ternary_matmul_u32(oracle.pack_rows_u32(t), sc, x, m, k, n)
+    np.testing.assert_array_equal(out, _dense_f64(t, x, sc).astype(np.float32))
+
+
+def test_u32_matmul_code3_decodes_to_zero():
+    # word with code 3 everywhere plus a single +1 at column 5
+    w = np.full((1, 1), 0xFFFFFFFF, np.uint32)
+    w[0, 0] &= ~np.uint32(3 << 10)
+    w[0, 0] |= np.uint32(2 << 10)
+    x = np.arange(16, dtype=np.float32)[None, :] + 1
+    out = oracle.ternary_matmul_u32(w, np.ones(1, np.float32), x, 1, 16, 1)
+    assert out[0, 0] == 6.0
+
+
+@pytest.mark.parametrize("seed", [1, 2])
+def test_u32_matmul_random_vs_f64(seed):
+    rng = np.random.default_rng(seed)
+    m, k, n = 4, 2048, 96
+    t = rng.integers(-1, 2, size=(n, k)).astype(np.int8)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    sc = np.abs(rng.standard_normal(n)).astype(np.float32) * 0.02
+    out = oracle.ternary_matmul_u32(oracle.pack_rows_u32(t), sc, x, m, k, n).astype(np.float64)
+    ref = _dense_f64(t, x, sc)
+    rms = np.sqrt((ref ** 2).mean())
+    assert np.abs(out - ref).max() <= 1e-5 * rms
+
+
+def test_all_cpu_matmul_variants_agree_exactly_on_dyadic():
+    rng = np.random.default_rng(7)
+    n, k = 24, 64
+    t = rng.integers(-1, 2, size=(n, k)).astype(np.int8)
+    x = _dyadic(rng, (1, k))
+    scale = np.float32(0.5)
+    ref = _dense_f64(t, x, np.full(n, scale, np.float32)).astype(np.float32).ravel()
+    u32 = oracle.ternary_matmul_u32(oracle.pack_rows_u32(t), np.full(n, scale, np.float32), x, 1, k, n).ravel()
+    i8 = oracle.ternary_matmul_i8(t, scale, x, n, k, 1)
+    dec = oracle.ternary_matmul_decode(t, scale, x, n, k)
+    packed = oracle.pack_ternary(t)
+    pk = oracle.ternary_matmul_packed(packed, scale, x, n, k, 1)
+    pp = oracle.ternary_matmul_packed_parallel(packed, scale, x, n, k)
+    bench = oracle.bench_ternary_matmul(x, t, scale, 1, n, k)
+    for got in (u32, i8, dec, pk, pp, bench):
+        np.testing.assert_array_equal(got, ref)
+
+
+def test_blocked_matmul_vs_f64():
+    rng = np.random.default_rng(3)
+    n, k, bs = 8, 40, 16
+    t = rng.integers(-1, 2, size=(n, k)).astype(np.int8)
+    x = _dyadic(rng, (2, k))
+    sc = np.array([0.5, 0.25, 2.0], np.float32)
+    out = oracle.ternary_matmul_blocked(t, sc, bs, x, n, k, 2).reshape(2, n)
+    ref = np.zeros((2, n))
+    for b in range(3):
+        c0, c1 = b * bs, min(k, (b + 1) * bs)
+        ref += sc[b] * (x[:, c0:c1].astype(np.float64) @ t[:, c0:c1].T.astype(np.float64))
+    np.testing.assert_array_equal(out, ref.astype(np.float32))
+
+
+def test_pack_u8_bit_spec():
+    rng = np.random.default_rng(11)
+    v = rng.integers(-1, 2, size=1001).astype(np.int8)
+    p = oracle.pack_ternary(v)
+    code = np.where(v == -1, 0, np.where(v == 1, 2, 1))
+    for i in range(v.size):
+        assert (p[i // 4] >> (2 * (i % 4))) & 3 == code[i]
+    # padding bits of the last byte are zero
+    assert p[-1] >> (2 * (v.size % 4)) == 0
+
+
+def test_pack_u8_out_of_range_is_zero_code():
+    p = oracle.pack_ternary(np.array([5, -7, 1, -1], np.int8))
+    assert p[0] == (1 | (1 << 2) | (2 << 4) | (0 << 6))
+
+
+@pytest.mark.parametrize("n_values", [1, 15, 16, 17, 100, 4096])
+def test_pack_u32_closed_form(n_values):
+    rng = np.random.default_rng(n_values)
+    v = rng.integers(-1, 2, size=n_values).astype(np.int8)
+    p8 = oracle.pack_ternary(v)
+    w = oracle.pack_ternary_u32(p8, n_values)
+    assert w.size == (n_values + 15) // 16
+    for i in range(w.size):
+        for j in range(4):
+            b = p8[4 * i + j] if 4 * i + j < p8.size else 0
+            assert (int(w[i]) >> (8 * j)) & 0xFF == b
+
+
+def test_flat_u32_equals_row_aligned_when_k_mod_16():
+    rng = np.random.default_rng(5)
+    t = rng.integers(-1, 2, size=(12, 64)).astype(np.int8)
+    flat = oracle.pack_ternary_u32(oracle.pack_ternary(t), t.size).reshape(12, 4)
+    np.testing.assert_array_equal(flat, oracle.pack_rows_u32(t))
+    np.testing.assert_array_equal(flat, synth.pack_rows_u32(t))
+
+
+def _quantize_restated(w):
+    s = np.float32(0)
+    for v in w.astype(np.float32):
+        s = np.float32(s + np.float32(abs(v)))
+    alpha = np.float32(np.float32(s / np.float32(w.size)) / np.float32(0.7978845608)) if s > 0 else np.float32(1)
+    inv = np.float32(np.float32(1) / alpha)
+    q = np.trunc(np.abs(w * inv) + np.float32(0.5)) * np.sign(w * inv)  # round half away from zero
+    return np.clip(q, -1, 1).astype(np.int8), alpha
+
+
+def test_quantize_ternary_vs_restatement_and_kats():
+    rng = np.random.default_rng(9)
+    w = (rng.standard_normal(777) * 0.3).astype(np.float32)
+    q, a = oracle.quantize_ternary(w)
+    q2, a2 = _quantize_restated(w)
+    assert a == a2
+    np.testing.assert_array_equal(q, q2)
+    # ternary.rs:778-795 KATs
+    q0, _ = oracle.quantize_ternary(np.zeros(16, np.float32))
+    assert (q0 == 0).all()
+    qs, _ = oracle.quantize_ternary(np.array([-3.0, -0.5, -0.01, 0.01, 0.5, 3.0], np.float32))
+    assert qs[0] == -1 and qs[5] == 1 and qs[2] == qs[3]
+
+
+def test_sparse24_gpu_roundtrip_and_dense_equivalence():
+    t = synth.sparse24_uniform("test", "w", 37, 96)
+    meta, sc = oracle.pack_sparse24_gpu(t)
+    assert meta.shape == (37, (96 // 4 + 5) // 6)
+    np.testing.assert_array_equal(oracle.sparse24_gpu_decode(meta, 37, 96), t)
+    # the GPU test packer's scale is mean |nonzero| = 1 for +-1 weights
+    np.testing.assert_array_equal(sc, np.ones(37, np.float32))
+    rng = np.random.default_rng(2)
+    x = _dyadic(rng, (3, 96))
+    s = (2.0 ** rng.integers(-2, 2, size=37)).astype(np.float32)
+    sp = oracle.sparse24_gpu_matmul(meta, s, x, 3, 96, 37)
+    de = oracle.ternary_matmul_u32(oracle.pack_rows_u32(t), s, x, 3, 96, 37)
+    np.testing.assert_array_equal(sp, de)
+
+
+def test_sparse24_gpu_pattern_clamp():
+    # pattern id 7 decodes as pattern 5 (positions 2,3) in the WGSL kernel
+    meta = np.array([[7 | (0b01 << 3)]], np.uint32)
+    d = oracle.sparse24_gpu_decode(meta, 1, 4)
+    np.testing.assert_array_equal(d[0], [0, 0, -1, 1])
+
+
+def _from_ternary_restated(t):
+    out = np.zeros_like(t)
+    for g in range(t.size // 4):
+        v = t[4 * g:4 * g + 4]
+        order = sorted(range(4), key=lambda i: -abs(int(v[i])))  # stable
+        pos0 = order[0]
+        pos1 = order[1] if (v[order[1]] != 0 or v[order[0]] != 0) else 1
+        p0, p1 = min(pos0, pos1), max(pos0, pos1)
+        out[4 * g + p0] = 1 if v[p0] >= 0 else -1
+        out[4 * g + p1] = 1 if v[p1] >= 0 else -1
+    return out
+
+
+def test_sparse24_cpu_from_ternary_vs_restatement():
+    rng = np.random.default_rng(4)
+    t = rng.integers(-1, 2, size=(16, 32)).astype(np.int8)
+    p, s = oracle.sparse24_cpu_from_ternary(t, 16, 32)
+    d = oracle.sparse24_cpu_to_ternary(p, s, 16, 32)
+    np.testing.assert_array_equal(d, _from_ternary_restated(t.ravel()))
+    t24 = synth.sparse24_uniform("test", "cpu", 16, 32)
+    p, s = oracle.sparse24_cpu_from_ternary(t24, 16, 32)
+    np.testing.assert_array_equal(oracle.sparse24_cpu_to_ternary(p, s, 16, 32), t24.ravel())
+
+
+def test_sparse24_cpu_matmul_vs_dense():
+    t24 = synth.sparse24_uniform("test", "cpum", 8, 64)
+    p, s = oracle.sparse24_cpu_from_ternary(t24, 8, 64)
+    rng = np.random.default_rng(8)
+    x = _dyadic(rng, (2, 64))
+    out = oracle.sparse24_cpu_matmul(p, s, 0.5, 8, 64, x, 2)
+    ref = oracle.ternary_matmul_i8(t24, 0.5, x, 8, 64, 2)
+    np.testing.assert_array_equal(out, ref)
+
+
+def _softmax_route_f64(x, r, k):
+    logits = x.astype(np.float64) @ r.astype(np.float64).T
+    p = np.exp(logits - logits.max(1, keepdims=True))
+    p /= p.sum(1, keepdims=True)
+    idx = np.argsort(-p, axis=1, kind="stable")[:, :k]
+    w = np.take_along_axis(p, idx, 1)
+    return idx, w / w.sum(1, keepdims=True)
+
+
+def test_moe_route_vs_bruteforce():
+    rng = np.random.default_rng(12)
+    x = rng.standard_normal((64, 32)).astype(np.float32)
+    r = (rng.standard_normal((6, 32)) * 0.5).astype(np.float32)
+    idx, w, probs = oracle.moe_route(x, r, 2)
+    i2, w2 = _softmax_route_f64(x, r, 2)
+    np.testing.assert_array_equal(idx, i2)
+    np.testing.assert_allclose(w, w2, atol=1e-6)
+    np.testing.assert_allclose(w.sum(1), 1.0, atol=1e-6)
+    np.testing.assert_allclose(probs.sum(1), 1.0, atol=1e-6)
+
+
+def test_moe_route_ties_keep_lower_index():
+    x = np.ones((1, 4), np.float32)
+    r = np.array([[0.25] * 4, [0.5] * 4, [0.5] * 4, [0.25] * 4], np.float32)
+    idx, w, _ = oracle.moe_route(x, r, 3)
+    assert list(idx[0]) == [1, 2, 0]
+
+
+def _moe_f64(x, r, wg, sg, wu, su, wd, sd, k, gelu):
+    idx, w = _softmax_route_f64(x, r, k)
+    out = np.zeros((x.shape[0], x.shape[1]))
+    for t in range(x.shape[0]):
+        for j in range(k):
+            e = idx[t, j]
+            g = (wg[e].astype(np.float64) @ x[t]) * sg[e]
+            u = (wu[e].astype(np.float64) @ x[t]) * su[e]
+            if gelu:
+                a = 0.5 * g * (1 + np.tanh(np.sqrt(2 / np.pi) * (g + 0.044715 * g ** 3)))
+            else:
+                a = g / (1 + np.exp(-g))
+            out[t] += w[t, j] * ((wd[e].astype(np.float64) @ (a * u)) * sd[e])
+    return out, idx
+
+
+@pytest.mark.parametrize("gelu", [False, True])
+def test_moe_forward_vs_f64(gelu):
+    rng = np.random.default_rng(21 + gelu)
+    T, H, I, E, k = 9, 32, 48, 4, 2
+    x = rng.standard_normal((T, H)).astype(np.float32)
+    r = (rng.standard_normal((E, H)) * 0.3).astype(np.float32)
+    mk = lambda n, kk: rng.integers(-1, 2, size=(n, kk)).astype(np.int8)  # noqa: E731
+    wg = [mk(I, H) for _ in range(E)]
+    wu = [mk(I, H) for _ in range(E)]
+    wd = [mk(H, I) for _ in range(E)]
+    sc = lambda n: (np.abs(rng.standard_normal(n)) * 0.1 + 0.05).astype(np.float32)  # noqa: E731
+    sg = [sc(I) for _ in range(E)]
+    su = [sc(I) for _ in range(E)]
+    sd = [sc(H) for _ in range(E)]
+    pk = oracle.pack_rows_u32
+    out, idx, w = oracle.moe_forward(x, r, [pk(a) for a in wg], sg, [pk(a) for a in wu], su,
+                                     [pk(a) for a in wd], sd, k, gelu)
+    ref, idx2 = _moe_f64(x, r, wg, sg, wu, su, wd, sd, k, gelu)
+    np.testing.assert_array_equal(idx, idx2)
+    rms = np.sqrt((ref ** 2).mean())
+    assert np.abs(out - ref).max() <= 1e-5 * rms
+
+
+def test_gelu_tanh_vs_f64():
+    for v in [-3.0, -0.5, 0.0, 0.3, 2.0]:
+        ref = 0.5 * v * (1 + np.tanh(np.sqrt(2 / np.pi) * (v + 0.044715 * v ** 3)))
+        assert abs(oracle.gelu_tanh(v) - ref) <= 1e-6 * max(1.0, abs(ref))

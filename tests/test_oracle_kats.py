@@ -1,0 +1,118 @@
+"""The CPU oracle against the reference's own known-answer tests (data in
+tests/golden/reference_kats.json, transcribed from the reference's tests)."""
+import json
+import os
+
+import numpy as np
+import pytest
+
+import oracle
+
+KATS = json.load(open(os.path.join(os.path.dirname(__file__), "golden", "reference_kats.json")))
+
+
+@pytest.mark.parametrize("kat", KATS["dense_u32_matmul"], ids=lambda k: k["source"].split()[-1])
+def test_dense_u32_matmul_kats(kat):
+    v = np.array(kat["values"], np.int8).reshape(kat["rows"], kat["cols"])
+    packed = oracle.pack_rows_u32(v)
+    out = oracle.ternary_matmul_u32(packed, kat["scales"], kat["input"], kat["seq"], kat["cols"], kat["rows"])
+    np.testing.assert_allclose(out.ravel(), kat["expected"], atol=kat["tol"], rtol=0)
+
+
+def test_pack_rows_u32_codes_kat():
+    kat = KATS["pack_rows_u32_codes"][0]
+    v = np.array(kat["values"], np.int8).reshape(1, kat["cols"])
+    packed = oracle.pack_rows_u32(v).ravel()
+    assert packed.size == kat["words"]
+    for i, code in enumerate(kat["codes"]):
+        assert (int(packed[i // 16]) >> (2 * (i % 16))) & 3 == code, i
+
+
+@pytest.mark.parametrize("kat", KATS["pack_u8_roundtrip"], ids=lambda k: str(k["values"]))
+def test_pack_u8_roundtrip_kats(kat):
+    v = np.array(kat["values"], np.int8)
+    p = oracle.pack_ternary(v)
+    assert p.size == kat["packed_len"]
+    np.testing.assert_array_equal(oracle.unpack_ternary(p, v.size), v)
+
+
+def test_pack_u8_cycle_kat():
+    kat = KATS["pack_u8_cycle"]
+    v = (np.arange(kat["n"]) % 3 - 1).astype(np.int8)
+    p = oracle.pack_ternary(v)
+    assert p.size == kat["packed_len"]
+    np.testing.assert_array_equal(oracle.unpack_ternary(p, v.size), v)
+
+
+@pytest.mark.parametrize("kat", KATS["i8_matmul"], ids=lambda k: k["source"].split()[-1])
+def test_i8_matmul_kats(kat):
+    out = oracle.ternary_matmul_i8(kat["ternary"], kat["scale"], kat["input"], kat["out_rows"], kat["in_cols"], kat["seq"])
+    np.testing.assert_allclose(out, kat["expected"], atol=kat["tol"], rtol=0)
+
+
+def test_packed_matmul_kat():
+    kat = KATS["packed_matmul"][0]
+    p = oracle.pack_ternary(np.array(kat["ternary"], np.int8))
+    out = oracle.ternary_matmul_packed(p, kat["scale"], kat["input"], kat["out_rows"], kat["in_cols"], kat["seq"])
+    np.testing.assert_allclose(out, kat["expected"], atol=kat["tol"], rtol=0)
+    ref = oracle.ternary_matmul_i8(kat["ternary"], kat["scale"], kat["input"], kat["out_rows"], kat["in_cols"], kat["seq"])
+    np.testing.assert_allclose(out, ref, atol=1e-5, rtol=0)
+
+
+@pytest.mark.parametrize("kat", KATS["sparse24_gpu"], ids=lambda k: k["source"].split()[-1])
+def test_sparse24_gpu_kats(kat):
+    w = np.array(kat["weights"], np.int8).reshape(kat["rows"], kat["cols"])
+    meta, scales = oracle.pack_sparse24_gpu(w)
+    out = oracle.sparse24_gpu_matmul(meta, scales, kat["input"], kat["seq"], kat["cols"], kat["rows"])
+    np.testing.assert_allclose(out.ravel(), kat["expected"], atol=kat["tol"], rtol=0)
+
+
+def test_sparse24_gpu_packer_rejects_non_24():
+    with pytest.raises(ValueError):
+        oracle.pack_sparse24_gpu(np.array([[1, 1, 1, 0]], np.int8))
+
+
+def test_sparse24_cpu_signs_kat():
+    kat = KATS["sparse24_cpu_signs"]
+    p, s = oracle.sparse24_cpu_from_ternary(kat["ternary"], kat["rows"], kat["cols"])
+    d = oracle.sparse24_cpu_to_ternary(p, s, kat["rows"], kat["cols"])
+    for pos, val in kat["expected_positions"].items():
+        assert d[int(pos)] == val
+
+
+def test_sparse24_cpu_known_output_kat():
+    kat = KATS["sparse24_cpu_known_output"]
+    p, s = oracle.sparse24_cpu_from_ternary(kat["ternary"], kat["rows"], kat["cols"])
+    out = oracle.sparse24_cpu_matmul(p, s, kat["scale"], kat["rows"], kat["cols"], kat["input"], 1)
+    np.testing.assert_allclose(out, kat["expected"], atol=kat["tol"], rtol=0)
+    dec = oracle.sparse24_cpu_matmul_decode(p, s, kat["scale"], kat["rows"], kat["cols"], kat["input"])
+    np.testing.assert_array_equal(dec, out)
+
+
+def test_sparse24_cpu_basic_kat():
+    kat = KATS["sparse24_cpu_basic"]
+    p, s = oracle.sparse24_cpu_from_ternary(kat["ternary"], kat["rows"], kat["cols"])
+    d = oracle.sparse24_cpu_to_ternary(p, s, kat["rows"], kat["cols"]).reshape(-1, 4)
+    assert ((d != 0).sum(axis=1) <= kat["max_nonzeros_per_group"]).all()
+
+
+def test_prune_fp32_kat():
+    kat = KATS["prune_fp32"]
+    p, s, sc = oracle.prune_fp32_to_sparse24(kat["weights"], kat["rows"], kat["cols"])
+    d = oracle.sparse24_cpu_to_ternary(p, s, kat["rows"], kat["cols"])
+    np.testing.assert_array_equal(d, kat["expected_decompressed"])
+    assert sc > 0
+
+
+@pytest.mark.parametrize("kat", KATS["routing"], ids=lambda k: k["source"].split()[-1])
+def test_routing_kats(kat):
+    # Router = identity matrix, so the logits are exactly the inputs.
+    logits = np.array(kat["logits"], np.float32)[None, :]
+    e = logits.shape[1]
+    idx, w, _ = oracle.moe_route(logits, np.eye(e, dtype=np.float32), kat["top_k"])
+    assert list(idx[0]) == kat["expected_idx"]
+    sel = logits[0, kat["expected_idx"]].astype(np.float64)
+    expect = np.exp(sel) / np.exp(sel).sum()
+    np.testing.assert_allclose(w[0], expect, atol=kat["weight_tol"], rtol=0)
+    if "sum_tol" in kat:
+        assert abs(float(w[0].sum()) - 1.0) < kat["sum_tol"]
