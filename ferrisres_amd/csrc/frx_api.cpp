@@ -153,8 +153,6 @@ frx_status frx_sparse24_ternary_linear(frx_ctx *ctx, const uint32_t *meta,
   frx_status st = enter(ctx);
   if (st != FRX_OK) return st;
   if ((st = check_linear(ctx, meta, scale, x, xt, y, yt, M, K, N, true)) != FRX_OK) return st;
-  if (K % 16 != 0 && !(xt == FRX_BF16 ? (K % 8 == 0) : (K % 4 == 0)))
-    return fail(ctx, FRX_ERR_SHAPE, "in_cols=%u: rows must stay element aligned", K);
   hipError_t e = frx::launch_gemm(meta, scale, x, xt == FRX_BF16, y, yt == FRX_BF16, (int)M, (int)K, (int)N, 1,
                                   ctx->stream);
   if (e != hipSuccess) return hip_fail(ctx, e, "sparse24_ternary_linear launch");

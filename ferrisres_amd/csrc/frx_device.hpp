@@ -44,6 +44,20 @@ __device__ __forceinline__ u32x4 unpack_half(uint32_t nw) {
   return r;
 }
 
+// Same pairs from the raw (non-inverted) word: ~(w << s) & mask equals
+// (~w << s) & mask for s <= 14 because the mask keeps only bits 14-15 and
+// 30-31; mask = 0xC000C000, or 0 to zero the operand. One shift plus one
+// three-input bit op (v_bitop3) per pair.
+template <int H>
+__device__ __forceinline__ u32x4 unpack_half_m(uint32_t w, uint32_t mask) {
+  u32x4 r;
+  r.x = ~(w << (14 - 2 * (4 * H + 0))) & mask;
+  r.y = ~(w << (14 - 2 * (4 * H + 1))) & mask;
+  r.z = ~(w << (14 - 2 * (4 * H + 2))) & mask;
+  r.w = ~(w << (14 - 2 * (4 * H + 3))) & mask;
+  return r;
+}
+
 // Round-to-nearest-even f32 -> bf16 (NaN stays NaN).
 __device__ __forceinline__ uint32_t bf16_rne(float f) {
   uint32_t u = __float_as_uint(f);

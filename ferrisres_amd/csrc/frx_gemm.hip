@@ -18,8 +18,18 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_kernel(
     int wvec) {
   using Core = GemmCore<BM, BN, WM, WN, XS, 1, WF>;
   __shared__ __align__(16) uint32_t lds[Core::LDS_DWORDS];
-  const int n0 = blockIdx.x * BN, m0 = blockIdx.y * BM;
-  XDesc xd{X, nullptr, nullptr, (long)m0, K};
+  // XCD-aware tile order: hardware deals workgroup ids round-robin over the
+  // 8 XCDs (id % 8). Renumber so that each XCD receives a contiguous run of
+  // tiles in (m-tile, n-tile) row-major order, i.e. neighbouring N tiles of
+  // the same M tile (same X rows) share one XCD's L2.
+  const int gx = gridDim.x, total = gx * gridDim.y;
+  const int bid = blockIdx.y * gx + blockIdx.x;
+  // XCD x receives ids x, x+8, ...: q+1 of them for x < r, q otherwise.
+  const int q = total / 8, r = total % 8, xcd = bid % 8, kx = bid / 8;
+  const int lin = xcd < r ? xcd * (q + 1) + kx : r * (q + 1) + (xcd - r) * q + kx;
+  const int n0 = (lin % gx) * BN, m0 = (lin / gx) * BM;
+  constexpr int ES = XS == XS_F32 ? 4 : 2;
+  XDesc xd{X, nullptr, nullptr, (long)m0, K, ((K * ES) % 16) == 0};
   const uint32_t *Wm[1] = {W};
   f32x4 acc[1][Core::FN][Core::FM];
   Core::run(lds, xd, min(BM, M - m0), Wm, n0, N, K, wvec, acc);

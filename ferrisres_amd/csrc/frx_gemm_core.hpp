@@ -65,6 +65,7 @@ struct XDesc {
   const int *rowidx;  // optional: global row of tile row m = rowidx[m]
   long row0;          // used when rowidx == nullptr: global row = row0 + m
   int ldx;            // row stride in elements
+  int xvec;           // rows are 16-byte aligned (vector loads allowed)
 };
 
 template <int BM, int BN, int WM, int WN, int XS, int NW, int WF = WF_DENSE>
@@ -112,8 +113,9 @@ struct GemmCore {
       const int m = b >> 2, blk = b & 3;
       const int col = k0 + blk * 16;
       const bool ok = (b < BM * 4) && (m < m_count) && (col < K);
-      if (ok && col + 16 > K) {
-        // partial block (K % 16 != 0): element-wise, zero beyond K
+      if (ok && (col + 16 > K || !xd.xvec)) {
+        // partial block (K % 16 != 0) or unaligned rows: element-wise, zero
+        // beyond K
         const long gr = xrow(xd, m);
         const int nv = K - col;
         if constexpr (XS == XS_BF16) {
@@ -289,7 +291,7 @@ struct GemmCore {
     for (int mat = 0; mat < NW; mat++)
 #pragma unroll
       for (int fn = 0; fn < FN; fn++)
-        nw[mat][fn] = ~wb[(mat * BN + wn * TN + fn * 16 + l16) * 4 + g];
+        nw[mat][fn] = wb[(mat * BN + wn * TN + fn * 16 + l16) * 4 + g];
 #pragma unroll
     for (int h = 0; h < 2; h++) {
       u32x4 bx[P][FM];
@@ -303,8 +305,8 @@ struct GemmCore {
       for (int mat = 0; mat < NW; mat++)
 #pragma unroll
         for (int fn = 0; fn < FN; fn++) {
-          const u32x4 a = h == 0 ? unpack_half<0>(nw[mat][fn])
-                                 : unpack_half<1>(nw[mat][fn]);
+          const u32x4 a = h == 0 ? unpack_half_m<0>(nw[mat][fn], 0xC000C000u)
+                                 : unpack_half_m<1>(nw[mat][fn], 0xC000C000u);
 #pragma unroll
           for (int fm = 0; fm < FM; fm++)
 #pragma unroll

@@ -79,55 +79,181 @@ __device__ __forceinline__ float ld_f32<uint16_t>(const uint16_t *p, long i) {
 // evaluated in double and rounded to f32 (correctly rounded except in
 // vanishingly rare near-halfway cases), division is IEEE.
 #pragma clang fp contract(off)
-template <typename XT, typename RT>
-__global__ __launch_bounds__(64) void moe_router_kernel(
-    const XT *__restrict__ x, const RT *__restrict__ router, int H, int E,
-    int top_k, uint32_t *__restrict__ idx_out, float *__restrict__ w_out,
-    uint32_t *__restrict__ user_idx, float *__restrict__ user_w) {
-  __shared__ float logit[MOE_MAXE];
-  const int t = blockIdx.x, e = threadIdx.x;
-  if (e < E) {
-    const XT *xr = x + (long)t * H;
-    const RT *rr = router + (long)e * H;
-    float sum = 0.0f;
-    for (int j = 0; j < H; j++) {
-      const float prod = __fmul_rn(ld_f32(xr, j), ld_f32(rr, j));
-      sum = __fadd_rn(sum, prod);
-    }
-    logit[e] = sum;
+// 8 consecutive elements as f32 (16-byte bf16 load or two 16-byte f32 loads).
+__device__ __forceinline__ void ld8(const uint16_t *p, float v[8]) {
+  const u32x4 a = *reinterpret_cast<const u32x4 *>(p);
+  const uint32_t w[4] = {a.x, a.y, a.z, a.w};
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    v[2 * i] = __uint_as_float(w[i] << 16);
+    v[2 * i + 1] = __uint_as_float(w[i] & 0xFFFF0000u);
   }
+}
+__device__ __forceinline__ void ld8(const float *p, float v[8]) {
+  const float4 a = reinterpret_cast<const float4 *>(p)[0], b = reinterpret_cast<const float4 *>(p)[1];
+  v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+  v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+}
+
+constexpr int RT_CHMAX = 256;  // router columns staged per chunk (at most)
+
+// Chunk width so that one pass of 256 threads x 4 units of 8 columns covers
+// every staged row (tokens of the block + experts): a multiple of 8.
+static inline int router_chunk(int rows) {
+  int ch = (1024 / rows) * 8;
+  return ch > RT_CHMAX ? RT_CHMAX : ch;
+}
+
+// 256 threads = (256/EP) tokens x EP expert lanes (EP = E rounded up to a
+// power of two). Chunks of RT_CH columns of the block's token rows and of
+// all router rows are staged in LDS as f32 (double-buffered: the next
+// chunk's global loads are in flight while the current one is summed); each
+// (token, expert) lane then runs the reference's sequential dot product.
+template <typename XT, typename RT>
+__global__ __launch_bounds__(256) void moe_router_kernel(
+    const XT *__restrict__ x, const RT *__restrict__ router, int T, int H,
+    int E, int EP, int top_k, int CH, uint32_t *__restrict__ idx_out,
+    float *__restrict__ w_out, uint32_t *__restrict__ user_idx,
+    float *__restrict__ user_w) {
+  const int RS = CH + 4;  // padded row stride (floats)
+  extern __shared__ __align__(16) float rsm[];
+  const int tid = threadIdx.x, e = tid % EP, tl = tid / EP;
+  const int TPB = 256 / EP;
+  const int t = blockIdx.x * TPB + tl;
+  const int rows = TPB + E;  // staged rows: tokens then experts
+  float *buf[2] = {rsm, rsm + rows * RS};
+  float *logit = rsm + 2 * rows * RS;
+  const int nch = (H + CH - 1) / CH;
+  // each thread stages 8 consecutive columns of one row per pass
+  const int units = rows * (CH / 8);
+  float stage[4][8];
+  auto gload = [&](int c) {
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const int u = tid + i * 256;
+      const int rr = u / (CH / 8), col = c * CH + (u % (CH / 8)) * 8;
+      const bool ok = u < units && col < H;
+      if (ok && rr < TPB) {
+        const int tt = blockIdx.x * TPB + rr;
+        if (tt < T) ld8(x + (long)tt * H + col, stage[i]);
+        else for (int k = 0; k < 8; k++) stage[i][k] = 0.f;
+      } else if (ok) {
+        ld8(router + (long)(rr - TPB) * H + col, stage[i]);
+      } else {
+        for (int k = 0; k < 8; k++) stage[i][k] = 0.f;
+      }
+    }
+  };
+  auto sstore = [&](float *b) {
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const int u = tid + i * 256;
+      if (u < units) {
+        const int rr = u / (CH / 8), cc = (u % (CH / 8)) * 8;
+        float4 *d = reinterpret_cast<float4 *>(b + rr * RS + cc);
+        d[0] = make_float4(stage[i][0], stage[i][1], stage[i][2], stage[i][3]);
+        d[1] = make_float4(stage[i][4], stage[i][5], stage[i][6], stage[i][7]);
+      }
+    }
+  };
+  float sum = 0.0f;
+  gload(0);
+  sstore(buf[0]);
+  __syncthreads();
+  for (int c = 0; c < nch; c++) {
+    if (c + 1 < nch) gload(c + 1);
+    if (e < E && t < T) {
+#pragma clang fp contract(off)
+      const float *xr = buf[c & 1] + tl * RS;
+      const float *rr = buf[c & 1] + (TPB + e) * RS;
+      const int ncol = min(CH, H - c * CH);  // multiple of 8
+      int j = 0;
+      // 32 columns of LDS reads issued ahead of each run of dependent adds
+      for (; j + 32 <= ncol; j += 32) {
+        f32x4 xv[8], rv[8];
+#pragma unroll
+        for (int q = 0; q < 8; q++) {
+          xv[q] = *reinterpret_cast<const f32x4 *>(xr + j + 4 * q);
+          rv[q] = *reinterpret_cast<const f32x4 *>(rr + j + 4 * q);
+        }
+#pragma unroll
+        for (int q = 0; q < 8; q++) {
+#pragma unroll
+          for (int i = 0; i < 4; i++) {
+            const float pr = xv[q][i] * rv[q][i];
+            sum = sum + pr;
+          }
+        }
+      }
+      for (; j < ncol; j += 8) {
+        f32x4 xv[2], rv[2];
+#pragma unroll
+        for (int q = 0; q < 2; q++) {
+          xv[q] = *reinterpret_cast<const f32x4 *>(xr + j + 4 * q);
+          rv[q] = *reinterpret_cast<const f32x4 *>(rr + j + 4 * q);
+        }
+#pragma unroll
+        for (int q = 0; q < 2; q++) {
+#pragma unroll
+          for (int i = 0; i < 4; i++) {
+            const float pr = xv[q][i] * rv[q][i];
+            sum = sum + pr;
+          }
+        }
+      }
+    }
+    if (c + 1 < nch) sstore(buf[(c + 1) & 1]);
+    __syncthreads();
+  }
+  // Softmax and stable top-k in LDS, one EP-lane group per token. A lane's
+  // rank among the probabilities (greater, or equal with a lower index)
+  // reproduces the stable descending sort of the reference; the two
+  // reductions (sum of exps in expert order, sum of the top-k in sorted
+  // order) stay sequential on one lane, as in the reference.
+  float *pbuf = logit + 256;             // [256] probabilities
+  float *tsum = pbuf + 256;              // [256/EP] per-token sums
+  int *order = reinterpret_cast<int *>(tsum + 256);  // [256/EP][EP]
+  logit[tid] = sum;
+  __syncthreads();
+  const float *lg = logit + tl * EP;
+  const bool live = e < E && t < T;
+  float mx = -INFINITY;
+  for (int i = 0; i < E; i++) mx = fmaxf(mx, lg[i]);
+  const float ex = live ? (float)exp((double)__fsub_rn(lg[e], mx)) : 0.0f;
+  pbuf[tid] = ex;
   __syncthreads();
   if (e == 0) {
-    float p[MOE_MAXE];
-    int order[MOE_MAXE];
-    float mx = -INFINITY;
-    for (int i = 0; i < E; i++) mx = fmaxf(mx, logit[i]);
     float se = 0.0f;
-    for (int i = 0; i < E; i++) {
-      p[i] = (float)exp((double)__fsub_rn(logit[i], mx));
-      se = __fadd_rn(se, p[i]);
+    for (int i = 0; i < E; i++) se = __fadd_rn(se, pbuf[tl * EP + i]);
+    tsum[tl] = se;
+  }
+  __syncthreads();
+  const float pe = live ? __fdiv_rn(ex, tsum[tl]) : 0.0f;
+  __syncthreads();
+  pbuf[tid] = pe;
+  __syncthreads();
+  if (live) {
+    int rank = 0;
+    for (int j = 0; j < E; j++) {
+      const float pj = pbuf[tl * EP + j];
+      rank += (pj > pe) || (pj == pe && j < e);
     }
-    for (int i = 0; i < E; i++) p[i] = __fdiv_rn(p[i], se);
-    for (int i = 0; i < E; i++) order[i] = i;
-    for (int i = 1; i < E; i++) {  // stable insertion sort, descending
-      const int cur = order[i];
-      int j = i;
-      while (j > 0 && p[order[j - 1]] < p[cur]) {
-        order[j] = order[j - 1];
-        j--;
-      }
-      order[j] = cur;
-    }
+    if (rank < top_k) order[tl * EP + rank] = e;
+  }
+  __syncthreads();
+  if (e == 0 && t < T) {
     float ts = 0.0f;
-    for (int i = 0; i < top_k; i++) ts = __fadd_rn(ts, p[order[i]]);
-    for (int i = 0; i < top_k; i++) {
-      const uint32_t ei = (uint32_t)order[i];
-      const float wi = __fdiv_rn(p[order[i]], ts);
-      idx_out[t * top_k + i] = ei;
-      w_out[t * top_k + i] = wi;
-      if (user_idx) user_idx[t * top_k + i] = ei;
-      if (user_w) user_w[t * top_k + i] = wi;
-    }
+    for (int i = 0; i < top_k; i++) ts = __fadd_rn(ts, pbuf[tl * EP + order[tl * EP + i]]);
+    tsum[tl] = ts;
+  }
+  __syncthreads();
+  if (e < top_k && t < T) {
+    const int ei = order[tl * EP + e];
+    const float wi = __fdiv_rn(pbuf[tl * EP + ei], tsum[tl]);
+    idx_out[t * top_k + e] = (uint32_t)ei;
+    w_out[t * top_k + e] = wi;
+    if (user_idx) user_idx[t * top_k + e] = (uint32_t)ei;
+    if (user_w) user_w[t * top_k + e] = wi;
   }
 }
 
@@ -225,7 +351,7 @@ __global__ __launch_bounds__(256) void moe_gateup_kernel(
   const int mcount = min(MOE_BM, counts[e] - mstart);
   const int row0 = offsets[e] + mstart;
   const int n0 = blockIdx.x * MOE_BN;
-  XDesc xd{x, nullptr, perm_token + row0, 0, H};
+  XDesc xd{x, nullptr, perm_token + row0, 0, H, 1};
   const uint32_t *Wm[2] = {args.wg[e], args.wu[e]};
   const int wvec = ((H >> 4) % 4 == 0);
   f32x4 acc[2][Core::FN][Core::FM];
@@ -283,7 +409,7 @@ __global__ __launch_bounds__(256) void moe_down_kernel(
   const int mcount = min(MOE_BM, counts[e] - mstart);
   const int row0 = offsets[e] + mstart;
   const int n0 = blockIdx.x * MOE_BN;
-  XDesc xd{h_hi, h_lo, nullptr, (long)row0, I};
+  XDesc xd{h_hi, h_lo, nullptr, (long)row0, I, 1};
   const uint32_t *Wm[1] = {args.wd[e]};
   const int wvec = ((I >> 4) % 4 == 0);
   f32x4 acc[1][Core::FN][Core::FM];
@@ -310,18 +436,16 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(
     const float *__restrict__ dout, const float *__restrict__ wts,
     const int *__restrict__ inv, int H, int top_k, YT *__restrict__ y) {
   const int t = blockIdx.x;
-  for (int j = threadIdx.x; j < H; j += 256) {
-    float acc = 0.0f;
+  for (int j = threadIdx.x * 4; j < H; j += 1024) {  // H % 16 == 0
+    f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
     for (int k = 0; k < top_k; k++) {
+#pragma clang fp contract(off)
       const float w = wts[t * top_k + k];
-      const float d = dout[(long)inv[t * top_k + k] * H + j];
-      acc = __fadd_rn(acc, __fmul_rn(w, d));
+      const f32x4 d = *reinterpret_cast<const f32x4 *>(dout + (long)inv[t * top_k + k] * H + j);
+      const f32x4 prod = d * w;
+      acc = acc + prod;
     }
-    if constexpr (sizeof(YT) == 4) {
-      y[(long)t * H + j] = acc;
-    } else {
-      reinterpret_cast<uint16_t *>(y)[(long)t * H + j] = (uint16_t)bf16_rne(acc);
-    }
+    YStore<YT>::store4(y + (long)t * H + j, acc, 4);
   }
 }
 #pragma clang fp contract(on)
@@ -336,18 +460,37 @@ hipError_t launch_moe(const void *x, int xt_bf16, const void *router,
                       hipStream_t stream) {
   const int A = T * top_k;
   // 1. router
+  int EP = 1;
+  while (EP < E) EP *= 2;
+  const dim3 rg((T + 256 / EP - 1) / (256 / EP));
+  const int rch = router_chunk(256 / EP + E);
+  const size_t rlds = (size_t)(2 * (256 / EP + E) * (rch + 4) + 4 * 256) * 4;
+  {
+    static bool attr_set = false;  // opt in to > 64 KB of dynamic LDS once
+    if (!attr_set) {
+      (void)hipFuncSetAttribute(reinterpret_cast<const void *>(&moe_router_kernel<uint16_t, uint16_t>),
+                                hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+      (void)hipFuncSetAttribute(reinterpret_cast<const void *>(&moe_router_kernel<uint16_t, float>),
+                                hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+      (void)hipFuncSetAttribute(reinterpret_cast<const void *>(&moe_router_kernel<float, uint16_t>),
+                                hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+      (void)hipFuncSetAttribute(reinterpret_cast<const void *>(&moe_router_kernel<float, float>),
+                                hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+      attr_set = true;
+    }
+  }
   if (xt_bf16 && rt_bf16)
-    hipLaunchKernelGGL((moe_router_kernel<uint16_t, uint16_t>), dim3(T), dim3(64), 0, stream,
-                       (const uint16_t *)x, (const uint16_t *)router, H, E, top_k, ws.idx, ws.wts, topk_idx, topk_w);
+    hipLaunchKernelGGL((moe_router_kernel<uint16_t, uint16_t>), rg, dim3(256), rlds, stream,
+                       (const uint16_t *)x, (const uint16_t *)router, T, H, E, EP, top_k, rch, ws.idx, ws.wts, topk_idx, topk_w);
   else if (xt_bf16)
-    hipLaunchKernelGGL((moe_router_kernel<uint16_t, float>), dim3(T), dim3(64), 0, stream,
-                       (const uint16_t *)x, (const float *)router, H, E, top_k, ws.idx, ws.wts, topk_idx, topk_w);
+    hipLaunchKernelGGL((moe_router_kernel<uint16_t, float>), rg, dim3(256), rlds, stream,
+                       (const uint16_t *)x, (const float *)router, T, H, E, EP, top_k, rch, ws.idx, ws.wts, topk_idx, topk_w);
   else if (rt_bf16)
-    hipLaunchKernelGGL((moe_router_kernel<float, uint16_t>), dim3(T), dim3(64), 0, stream,
-                       (const float *)x, (const uint16_t *)router, H, E, top_k, ws.idx, ws.wts, topk_idx, topk_w);
+    hipLaunchKernelGGL((moe_router_kernel<float, uint16_t>), rg, dim3(256), rlds, stream,
+                       (const float *)x, (const uint16_t *)router, T, H, E, EP, top_k, rch, ws.idx, ws.wts, topk_idx, topk_w);
   else
-    hipLaunchKernelGGL((moe_router_kernel<float, float>), dim3(T), dim3(64), 0, stream,
-                       (const float *)x, (const float *)router, H, E, top_k, ws.idx, ws.wts, topk_idx, topk_w);
+    hipLaunchKernelGGL((moe_router_kernel<float, float>), rg, dim3(256), rlds, stream,
+                       (const float *)x, (const float *)router, T, H, E, EP, top_k, rch, ws.idx, ws.wts, topk_idx, topk_w);
   hipError_t err = hipGetLastError();
   if (err != hipSuccess) return err;
   // 2. group
