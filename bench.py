@@ -53,6 +53,8 @@ def main():
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--profile-target", choices=["prefill", "sparse24", "moe"], default=None,
+                    help="run only this workload's kernels (for rocprofv3 counter passes)")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -69,6 +71,10 @@ def main():
     stream = torch.cuda.Stream(device=dev)
     ctx = frx.Context(0)
     ctx.set_stream(stream)
+    if args.profile_target:
+        res = run_extra(torch, frx, synth, ctx, stream, dev, only=args.profile_target, iters=args.steps)
+        print(json.dumps({"profile_target": args.profile_target, "extra": res}), flush=True)
+        return
     B = args.batch
     H, I = 4096, 11008
 
@@ -210,7 +216,7 @@ def _time_kernel(torch, stream, fn, iters, warm=3):
     return e0.elapsed_time(e1) * 1e-3 / iters
 
 
-def run_extra(torch, frx, synth, ctx, stream, dev):
+def run_extra(torch, frx, synth, ctx, stream, dev, only=None, iters=20):
     res = {}
     M, K = 2048, 4096
     _, xb = synth.activations("bench/prefill", "x", M, K)
@@ -220,19 +226,24 @@ def run_extra(torch, frx, synth, ctx, stream, dev):
         w = torch.from_numpy(synth.pack_rows_u32(t).view(np.int32)).to(dev)
         s = torch.from_numpy(synth.row_scales("bench/prefill", f"s{N}", N, samples=256)).to(dev)
         Y = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
-        dt = _time_kernel(torch, stream, lambda: ctx.ternary_linear(w, s, X, Y), 20)
-        tf = 2.0 * M * N * K / dt / 1e12
-        res[f"prefill_gemm_{M}x{K}x{N}"] = {"us": round(dt * 1e6, 2), "tflops": round(tf, 1),
-                                            "frac_bf16_peak": round(tf / BF16_PEAK_TFLOPS, 4)}
-        log(f"bench: prefill N={N}: {dt * 1e6:.1f} us, {tf:.1f} TFLOP/s")
-        t24 = synth.sparse24_uniform("bench/sp24", f"w{N}", N, K)
-        meta = torch.from_numpy(frx.pack_sparse24_gpu(t24).view(np.int32)).to(dev)
-        dt = _time_kernel(torch, stream, lambda: ctx.sparse24_ternary_linear(meta, s, X, Y), 20)
-        tf = 2.0 * M * N * K / dt / 1e12
-        res[f"sparse24_gemm_{M}x{K}x{N}"] = {"us": round(dt * 1e6, 2), "tflops_dense_equiv": round(tf, 1),
-                                             "frac_bf16_peak": round(tf / BF16_PEAK_TFLOPS, 4)}
-        log(f"bench: 2:4 N={N}: {dt * 1e6:.1f} us, {tf:.1f} TFLOP/s dense-equivalent")
-        del w, Y, meta
+        if only in (None, "prefill"):
+            dt = _time_kernel(torch, stream, lambda: ctx.ternary_linear(w, s, X, Y), iters)
+            tf = 2.0 * M * N * K / dt / 1e12
+            res[f"prefill_gemm_{M}x{K}x{N}"] = {"us": round(dt * 1e6, 2), "tflops": round(tf, 1),
+                                                "frac_bf16_peak": round(tf / BF16_PEAK_TFLOPS, 4)}
+            log(f"bench: prefill N={N}: {dt * 1e6:.1f} us, {tf:.1f} TFLOP/s")
+        if only in (None, "sparse24"):
+            t24 = synth.sparse24_uniform("bench/sp24", f"w{N}", N, K)
+            meta = torch.from_numpy(frx.pack_sparse24_gpu(t24).view(np.int32)).to(dev)
+            dt = _time_kernel(torch, stream, lambda: ctx.sparse24_ternary_linear(meta, s, X, Y), iters)
+            tf = 2.0 * M * N * K / dt / 1e12
+            res[f"sparse24_gemm_{M}x{K}x{N}"] = {"us": round(dt * 1e6, 2), "tflops_dense_equiv": round(tf, 1),
+                                                 "frac_bf16_peak": round(tf / BF16_PEAK_TFLOPS, 4)}
+            log(f"bench: 2:4 N={N}: {dt * 1e6:.1f} us, {tf:.1f} TFLOP/s dense-equivalent")
+            del meta
+        del w, Y
+    if only not in (None, "moe"):
+        return res
     # MoE expert layer
     T, Hm, Im, E, k = 512, 2048, 5632, 16, 2
     _, xb = synth.activations("bench/moe", "x", T, Hm)
@@ -250,7 +261,7 @@ def run_extra(torch, frx, synth, ctx, stream, dev):
     wd = [pd.clone() for _ in range(E)]
     ym = torch.empty((T, Hm), dtype=torch.bfloat16, device=dev)
     fn = lambda: ctx.moe_ternary_ffn(xm, rm, wg, [sg] * E, wu, [sg] * E, wd, [sd] * E, ym, top_k=k)  # noqa: E731
-    dt = _time_kernel(torch, stream, fn, 20)
+    dt = _time_kernel(torch, stream, fn, iters)
     fl = T * k * 3 * 2.0 * Im * Hm
     tf = fl / dt / 1e12
     res["moe_512tok_h2048_i5632_e16_top2"] = {"us": round(dt * 1e6, 2), "tflops": round(tf, 1),

@@ -6,10 +6,25 @@
 // kernels launch one thread per output with a 1-D grid, which cannot even be
 // dispatched at 2048 x 4096 (over 65,535 workgroups); here each workgroup
 // owns a 128 x 128 output tile (see frx_gemm_core.hpp).
+#include "frx_gemm2.hpp"
 #include "frx_gemm_core.hpp"
 #include "frx_internal.hpp"
 
 namespace frx {
+
+// XCD-aware tile order: hardware deals workgroup ids round-robin over the 8
+// XCDs (id % 8); renumber so that each XCD receives a contiguous run of tiles
+// in (m-tile, n-tile) row-major order (neighbouring N tiles of one M tile
+// share that XCD's L2). Bijective for any tile count.
+__device__ __forceinline__ void xcd_tile(int &nt, int &mt) {
+  const int gx = gridDim.x, total = gx * gridDim.y;
+  const int bid = blockIdx.y * gx + blockIdx.x;
+  const int q = total / 8, r = total % 8, xcd = bid % 8, kx = bid / 8;
+  const int lin = xcd < r ? xcd * (q + 1) + kx : r * (q + 1) + (xcd - r) * q + kx;
+  nt = lin % gx;
+  mt = lin / gx;
+}
+
 
 template <int BM, int BN, int WM, int WN, int XS, int WF, typename YT>
 __global__ __launch_bounds__(WM *WN * 64) void gemm_kernel(
@@ -18,16 +33,9 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_kernel(
     int wvec) {
   using Core = GemmCore<BM, BN, WM, WN, XS, 1, WF>;
   __shared__ __align__(16) uint32_t lds[Core::LDS_DWORDS];
-  // XCD-aware tile order: hardware deals workgroup ids round-robin over the
-  // 8 XCDs (id % 8). Renumber so that each XCD receives a contiguous run of
-  // tiles in (m-tile, n-tile) row-major order, i.e. neighbouring N tiles of
-  // the same M tile (same X rows) share one XCD's L2.
-  const int gx = gridDim.x, total = gx * gridDim.y;
-  const int bid = blockIdx.y * gx + blockIdx.x;
-  // XCD x receives ids x, x+8, ...: q+1 of them for x < r, q otherwise.
-  const int q = total / 8, r = total % 8, xcd = bid % 8, kx = bid / 8;
-  const int lin = xcd < r ? xcd * (q + 1) + kx : r * (q + 1) + (xcd - r) * q + kx;
-  const int n0 = (lin % gx) * BN, m0 = (lin / gx) * BM;
+  int nt, mt;
+  xcd_tile(nt, mt);
+  const int n0 = nt * BN, m0 = mt * BM;
   constexpr int ES = XS == XS_F32 ? 4 : 2;
   XDesc xd{X, nullptr, nullptr, (long)m0, K, ((K * ES) % 16) == 0};
   const uint32_t *Wm[1] = {W};
@@ -47,6 +55,43 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_kernel(
       if (m < M) YStore<YT>::store4(Y + (size_t)m * N + n, acc[0][fn][fm] * sc, nok);
     }
   }
+}
+
+// bf16 activations, K % 64 == 0: the pipelined engine (frx_gemm2.hpp).
+template <int BM, int BN, int WM, int WN, int NS, typename YT>
+__global__ __launch_bounds__(WM *WN * 64) void gemm2_kernel(
+    const uint32_t *__restrict__ W, const float *__restrict__ scale,
+    const uint16_t *__restrict__ X, YT *__restrict__ Y, int M, int K, int N) {
+  using Core = Gemm2<BM, BN, WM, WN, NS, false>;
+  extern __shared__ __align__(16) uint32_t lds[];  // Core::LDS_DWORDS
+  int nt, mt;
+  xcd_tile(nt, mt);
+  const int n0 = nt * BN, m0 = mt * BM;
+  f32x4 acc[Core::FN][Core::FM];
+  const int m_count = min(BM, M - m0), n_count = min(BN, N - n0);
+  Core::run(lds, X + (size_t)m0 * K, (uint32_t)m_count * (uint32_t)K * 2u, nullptr, m_count,
+            W + (size_t)n0 * (K >> 4), n_count, K, acc);
+  Core::template store_tile<YT>(lds, acc, scale, Y, (size_t)N, m0, m_count, n0, n_count);
+}
+
+#ifndef FRX_GEMM2_NS
+#define FRX_GEMM2_NS 3
+#endif
+
+template <typename YT>
+static hipError_t launch_gemm2_t(const uint32_t *w, const float *scale, const void *x, void *y,
+                                 int M, int K, int N, hipStream_t stream) {
+  constexpr int BM = 128, BN = 256, WM = 1, WN = 4, NS = FRX_GEMM2_NS;
+  using Core = Gemm2<BM, BN, WM, WN, NS, false>;
+  constexpr int lds = Core::LDS_DWORDS * 4;
+  static std::atomic<uint64_t> done;
+  const hipError_t e =
+      opt_in_lds(reinterpret_cast<const void *>(&gemm2_kernel<BM, BN, WM, WN, NS, YT>), lds, done);
+  if (e != hipSuccess) return e;
+  dim3 grid((N + BN - 1) / BN, (M + BM - 1) / BM);
+  hipLaunchKernelGGL((gemm2_kernel<BM, BN, WM, WN, NS, YT>), grid, dim3(WM * WN * 64), lds, stream, w,
+                     scale, reinterpret_cast<const uint16_t *>(x), reinterpret_cast<YT *>(y), M, K, N);
+  return hipGetLastError();
 }
 
 template <int XS, int WF, typename YT>
@@ -78,6 +123,10 @@ static hipError_t launch_gemm_wf(const uint32_t *w, const float *scale,
 hipError_t launch_gemm(const uint32_t *w, const float *scale, const void *x,
                        int xt_bf16, void *y, int yt_bf16, int M, int K, int N,
                        int sp24, hipStream_t stream) {
+  if (!sp24 && xt_bf16 && K % 64 == 0 && M > 16 && (reinterpret_cast<uintptr_t>(w) & 15) == 0) {
+    if (yt_bf16) return launch_gemm2_t<uint16_t>(w, scale, x, y, M, K, N, stream);
+    return launch_gemm2_t<float>(w, scale, x, y, M, K, N, stream);
+  }
   if (sp24) return launch_gemm_wf<WF_SP24>(w, scale, x, xt_bf16, y, yt_bf16, M, K, N, stream);
   return launch_gemm_wf<WF_DENSE>(w, scale, x, xt_bf16, y, yt_bf16, M, K, N, stream);
 }

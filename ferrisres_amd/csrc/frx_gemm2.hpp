@@ -1,0 +1,389 @@
+// frx_gemm2.hpp — pipelined MFMA tile engine for bf16-activation ternary GEMMs.
+//
+// C[BN weight rows][BM tokens] += dec(W)[n][k] * X[m][k], one workgroup tile,
+// v_mfma_f32_16x16x32_bf16 with A = weight rows, B = tokens, fp32 acc.
+//
+// Data movement. Both tiles go global -> LDS with buffer_load_dwordx4 ... lds
+// (no VGPR staging, no VALU work per element) through an NS-stage ring, so
+// the loads of step s+NS-1 are in flight while step s is multiplied. One
+// vmcnt wait + barrier per 64-column step. Buffer (MUBUF) rather than global
+// (FLAT) LDS DMA: the compiler treats a FLAT access that may touch LDS as
+// unordered with LDS reads and would make every LDS wait of the step a full
+// lgkmcnt(0); with MUBUF the operand reads get partial waits. Each lane's
+// byte offset inside a tile is fixed for the whole K loop; the step's column
+// advance goes in the scalar soffset. The buffer's num_records is the tile's
+// valid byte range, so the hardware range check bounds every load.
+//  - X stage: BM rows x 64 bf16 (128 B per row) in natural order, 16-byte
+//    chunks XOR-swizzled by (row/2)%8 so the 16 rows of an MFMA operand read
+//    hit 16 disjoint bank groups.
+//  - W stage: BN rows x 4 words (the reference's packed u32 words).
+// Operands. Lane (i = l%16, g = l/16) of MFMA half h covers columns
+// 32h + 8g .. 32h + 8g + 7 of the step, in natural order: the X operand is
+// one 16-byte LDS read; the W operand is 8 codes of one word turned into four
+// bf16 pairs (c, c+1) with a byte permute, a packed 16-bit shift and a
+// three-input bit op per pair (about 1.25 VALU ops per weight), the same
+// 2*dec(c) encoding as frx_device.hpp. Each W operand feeds TM/16 MFMAs.
+#pragma once
+#include "frx_device.hpp"
+
+namespace frx {
+
+typedef uint16_t u16x2 __attribute__((ext_vector_type(2)));
+
+// Four natural-order operand pairs from the byte pair (b0, b0+1) of word w,
+// i.e. codes 4*b0 .. 4*b0+7. sel0 / sel1 place byte b0 / b0+1 at bytes 1
+// and 3 of a dword (v_perm_b32 selectors). Returns dwords (c0,c1) (c2,c3)
+// (c4,c5) (c6,c7) with bf16 bits ((~c)&3)<<14 in each half.
+__device__ __forceinline__ u32x4 unpack8_nat(uint32_t w, uint32_t sel0, uint32_t sel1) {
+  const uint32_t y0 = __builtin_amdgcn_perm(w, w, sel0);
+  const uint32_t y1 = __builtin_amdgcn_perm(w, w, sel1);
+  const u16x2 s_lo = {6, 4}, s_hi = {2, 0};
+  u32x4 r;
+  r.x = ~__builtin_bit_cast(uint32_t, __builtin_bit_cast(u16x2, y0) << s_lo) & 0xC000C000u;
+  r.y = ~__builtin_bit_cast(uint32_t, __builtin_bit_cast(u16x2, y0) << s_hi) & 0xC000C000u;
+  r.z = ~__builtin_bit_cast(uint32_t, __builtin_bit_cast(u16x2, y1) << s_lo) & 0xC000C000u;
+  r.w = ~__builtin_bit_cast(uint32_t, __builtin_bit_cast(u16x2, y1) << s_hi) & 0xC000C000u;
+  return r;
+}
+
+typedef __attribute__((address_space(3))) void *lds_ptr_t;
+
+// gfx950 raw buffer descriptor word 3 (32-bit data format, no swizzle, no
+// stride): byte offsets are range-checked against num_records.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void *base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, (int)bytes,
+                                           0x00020000);
+}
+
+// 16 bytes per lane from rsrc at voffset + soffset into LDS: lane l's bytes
+// land at ldst + 16 * l (M0 holds the wave's LDS base).
+// acc += A * B with the accumulator tied to one accumulation register. The
+// builtin's untied form lets the register allocator write each product to a
+// fresh register and copy it back every step (tens of copies per step in a
+// pipelined loop). Operand producers are kept at least four MFMAs ahead by
+// the schedule below, and accumulation into the same register needs no wait
+// states, so no hazard padding is needed inside the loop; readers of the
+// results after the loop get explicit padding (mfma_drain).
+__device__ __forceinline__ void mfma16_acc(f32x4 &acc, const u32x4 &a, const u32x4 &b) {
+  asm("v_mfma_f32_16x16x32_bf16 %0, %1, %2, %0" : "+a"(acc) : "v"(a), "v"(b));
+}
+
+// Wait states between the last MFMA writing an accumulator and any other
+// instruction reading it (more than the longest XDL write-to-read hazard).
+__device__ __forceinline__ void mfma_drain() {
+  asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
+}
+
+__device__ __forceinline__ void lds_load16(__amdgpu_buffer_rsrc_t r, uint32_t *ldst,
+                                           uint32_t voffset, uint32_t soffset) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_ptr_t)ldst, 16, voffset, soffset, 0, 0);
+}
+
+// s_waitcnt with only the vector-memory counter limited to n (gfx9 encoding:
+// vmcnt[3:0] in bits 3:0, vmcnt[5:4] in bits 15:14; expcnt and lgkmcnt left
+// at their maxima, i.e. not waited on).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
+
+// Requires K % 64 == 0 (whole 16-byte W chunks per row and step). GATHER:
+// tile row m reads X row rowidx[m] (the indices are read once into
+// registers, so the pipelined loop issues no other vector-memory ops and the
+// explicit vmcnt accounting below stays exact).
+// Workgroup barrier without the memory fence of __syncthreads(): the fence
+// would make the compiler drain every in-flight global->LDS load (vmcnt(0))
+// at each step. Completion of the stage about to be read is established by
+// the explicit wait_vmcnt before the barrier, and LDS reads of a stage finish
+// (their results feed MFMAs) before the barrier that precedes its reuse.
+__device__ __forceinline__ void barrier_nofence() { __builtin_amdgcn_s_barrier(); }
+
+template <int BM, int BN, int WM, int WN, int NS, bool GATHER>
+struct Gemm2 {
+  static constexpr int NT = WM * WN * 64;
+  static constexpr int WAVES = WM * WN;
+  static constexpr int TM = BM / WM, TN = BN / WN;
+  static constexpr int FM = TM / 16, FN = TN / 16;
+  static constexpr int XSTAGE = BM * 32;  // dwords (BM rows x 128 B)
+  static constexpr int WSTAGE = BN * 4;   // dwords (BN rows x 16 B)
+  static constexpr int STAGE = XSTAGE + WSTAGE;
+  static constexpr int LDS_DWORDS = NS * STAGE;
+  static constexpr int XI = BM / 8;    // 1 KB load instructions per X stage
+  static constexpr int WI = BN / 64;   // 1 KB load instructions per W stage
+  static_assert(XI % WAVES == 0 && WI % WAVES == 0, "loads must split evenly over the waves");
+  static constexpr int XPW = XI / WAVES, WPW = WI / WAVES;
+  static constexpr int LPW = XPW + WPW;  // load instructions per wave per stage
+  static_assert(TM % 16 == 0 && TN % 16 == 0, "wave tile must be 16-aligned");
+
+  // Per-lane byte offsets of the XPW X and WPW W load instructions of this
+  // wave inside their buffers, fixed for the whole K loop. X rows past
+  // m_count are clamped to the last valid row and W rows past n_count to the
+  // last valid row (their outputs are discarded by the caller). Non-gather X
+  // offsets are relative to the tile's first row; gather offsets to row 0.
+  __device__ __forceinline__ static void lane_offsets(uint32_t (&xv)[XPW], uint32_t (&wv)[WPW],
+                                                      const int *rowidx, int m_count,
+                                                      int n_count, int K) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+#pragma unroll
+    for (int i = 0; i < XPW; i++) {
+      const int r = (wave * XPW + i) * 8 + (lane >> 3);
+      const int rm = min(r, m_count - 1);
+      const uint32_t gr = GATHER ? (uint32_t)rowidx[rm] : (uint32_t)rm;
+      const uint32_t c = (lane & 7) ^ ((r >> 1) & 7);  // swizzled source chunk
+      xv[i] = gr * (uint32_t)K * 2u + 16u * c;
+    }
+#pragma unroll
+    for (int i = 0; i < WPW; i++) {
+      const int n = min((wave * WPW + i) * 64 + lane, n_count - 1);
+      wv[i] = (uint32_t)n * (uint32_t)(K >> 4) * 4u;
+    }
+  }
+
+  __device__ __forceinline__ static void issue(uint32_t *stage, __amdgpu_buffer_rsrc_t xr,
+                                               __amdgpu_buffer_rsrc_t wr, const uint32_t (&xv)[XPW],
+                                               const uint32_t (&wv)[WPW], int k0) {
+    const int wave = threadIdx.x >> 6;
+#pragma unroll
+    for (int i = 0; i < XPW; i++) lds_load16(xr, stage + (wave * XPW + i) * 256, xv[i], 2u * k0);
+#pragma unroll
+    for (int i = 0; i < WPW; i++)
+      lds_load16(wr, stage + XSTAGE + (wave * WPW + i) * 256, wv[i], (uint32_t)k0 >> 2);
+  }
+
+  __device__ __forceinline__ static u32x4 xread(const uint32_t *stage, int r, int c) {
+    return *reinterpret_cast<const u32x4 *>(stage + r * 32 + ((c ^ ((r >> 1) & 7)) * 4));
+  }
+
+  // X operand i of a step (i = h * FM + fm): tokens r0 + 16 fm, columns
+  // 32 h + 8 g .. +7.
+  __device__ __forceinline__ static u32x4 xop(const uint32_t *stage, int r0, int g, int i) {
+    return xread(stage, r0 + (i % FM) * 16, 4 * (i / FM) + g);
+  }
+
+  static constexpr int XD = 4;  // X operand reads run this many MFMA groups ahead
+
+  // Waits until at most n of this wave's stage load groups are in flight
+  // (n clamped to N; s_waitcnt takes an immediate, hence the chain).
+  template <int N>
+  __device__ __forceinline__ static void wait_stages(int n) {
+    if constexpr (N == 0) {
+      wait_vmcnt<0>();
+    } else {
+      if (n >= N) wait_vmcnt<N * LPW>();
+      else wait_stages<N - 1>(n);
+    }
+  }
+
+  // The K loop, software-pipelined so that the matrix pipe never waits on
+  // the rest of the step. With one wave per SIMD nothing else hides latency,
+  // so the instruction order is fixed with scheduling fences.
+  //
+  // Step t multiplies stage t in two halves of 32 columns (h = 0, 1), one
+  // X-operand read two tiles ahead of its MFMAs. Between the halves each wave
+  // waits for its own loads of stage t+1 and the block meets at a barrier;
+  // after it, interleaved with the second half's MFMAs, the wave issues the
+  // loads of stage t+NS-1 (into the slot of stage t-1, whose last reads fed
+  // MFMAs before the barrier), reads stage t+1's weight words and first two
+  // X operands, and unpacks stage t+1's first-half weight operands. The first
+  // half's MFMAs likewise cover the unpack of the second half's operands.
+  // Stage t+1 is issued in step t+2-NS, i.e. NS-2 steps of latency cover.
+  __device__ static void run(uint32_t *lds, const uint16_t *X, uint32_t xbytes, const int *rowidx,
+                             int m_count, const uint32_t *W, int n_count, int K,
+                             f32x4 (&acc)[FN][FM]) {
+    static_assert(NS >= 3, "the ring needs a stage being read, one landing and one free");
+    static_assert(FM >= 4 && FN <= FM && XD <= FM, "operand schedule");
+    uint32_t xv[XPW], wv[WPW];
+    lane_offsets(xv, wv, rowidx, m_count, n_count, K);
+    const __amdgpu_buffer_rsrc_t xr = buffer_rsrc(X, xbytes);
+    const __amdgpu_buffer_rsrc_t wr = buffer_rsrc(W, (uint32_t)n_count * (uint32_t)(K >> 4) * 4u);
+#pragma unroll
+    for (int fn = 0; fn < FN; fn++)
+#pragma unroll
+      for (int fm = 0; fm < FM; fm++) acc[fn][fm] = (f32x4){0.f, 0.f, 0.f, 0.f};
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int wm = wave % WM, wn = wave / WM;
+    const int l16 = lane & 15, g = lane >> 4;
+    // byte selectors: lanes with g odd take the upper half word (codes 8..15)
+    const uint32_t b0 = 2 * (g & 1);
+    const uint32_t sel0 = (b0 << 8) | (b0 << 24);
+    const uint32_t sel1 = ((b0 + 1) << 8) | ((b0 + 1) << 24);
+    const int r0 = wm * TM + l16;
+    // weight word of fragment fn, half h, in a stage
+    const int wofs = XSTAGE + (wn * TN + l16) * 4 + (g >> 1);
+    const int nks = (K + 63) >> 6;
+
+    // One stage is issued per step, always: past the last stage the last
+    // stage's columns are loaded again (valid addresses) into the slot that
+    // is free anyway and never read. The wait counts stay uniform and the
+    // step has no branch; control flow among the MFMAs makes the register
+    // allocator shuttle the accumulators between register files.
+#pragma unroll
+    for (int s = 0; s < NS - 1; s++) issue(lds + s * STAGE, xr, wr, xv, wv, min(s, nks - 1) * 64);
+    wait_vmcnt<(NS - 2) * LPW>();  // stage 0 landed
+    barrier_nofence();
+
+    // operands of step 0
+    uint32_t wq1[FN];
+    u32x4 a0[FN], bn[XD];
+    {
+      uint32_t wq0[FN];
+#pragma unroll
+      for (int fn = 0; fn < FN; fn++) {
+        wq0[fn] = lds[wofs + fn * 64];
+        wq1[fn] = lds[wofs + fn * 64 + 2];
+      }
+#pragma unroll
+      for (int d = 0; d < XD; d++) bn[d] = xop(lds, r0, g, d);
+#pragma unroll
+      for (int fn = 0; fn < FN; fn++) a0[fn] = unpack8_nat(wq0[fn], sel0, sel1);
+    }
+
+    for (int t = 0; t < nks; t++) {
+      const uint32_t *cur = lds + (t % NS) * STAGE;
+      const uint32_t *nxt = lds + ((t + 1) % NS) * STAGE;
+      u32x4 b[2 * FM];
+#pragma unroll
+      for (int d = 0; d < XD; d++) b[d] = bn[d];
+      u32x4 a1[FN];
+      __builtin_amdgcn_sched_barrier(0);
+      // first half: columns 0..31 of the stage
+#pragma unroll
+      for (int fm = 0; fm < FM; fm++) {
+        const int q = fm;
+        b[q + XD] = xop(cur, r0, g, q + XD);
+#pragma unroll
+        for (int fn = 0; fn < FN; fn++) mfma16_acc(acc[fn][fm], a0[fn], b[q]);
+        if (fm < FN) a1[fm] = unpack8_nat(wq1[fm], sel0, sel1);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      // stage t+1 landed for every wave (the NS-3 stages issued after it may
+      // stay in flight)
+      wait_vmcnt<(NS - 3) * LPW>();
+      barrier_nofence();
+      __builtin_amdgcn_sched_barrier(0);
+      // second half: columns 32..63, plus the next stage's loads and operands
+      uint32_t wq0n[FN], wq1n[FN];
+      u32x4 a0n[FN];
+#pragma unroll
+      for (int fm = 0; fm < FM; fm++) {
+        const int q = FM + fm;
+        if (q + XD < 2 * FM) b[q + XD] = xop(cur, r0, g, q + XD);
+        else bn[q + XD - 2 * FM] = xop(nxt, r0, g, q + XD - 2 * FM);
+        if (fm == 0) {
+#pragma unroll
+          for (int fn = 0; fn < FN; fn++) {
+            wq0n[fn] = nxt[wofs + fn * 64];
+            wq1n[fn] = nxt[wofs + fn * 64 + 2];
+          }
+        }
+#pragma unroll
+        for (int fn = 0; fn < FN; fn++) mfma16_acc(acc[fn][fm], a1[fn], b[q]);
+        if (fm == 0) issue(lds + ((t + NS - 1) % NS) * STAGE, xr, wr, xv, wv, min(t + NS - 1, nks - 1) * 64);
+        if (fm >= 2 && fm - 2 < FN) a0n[fm - 2] = unpack8_nat(wq0n[fm - 2], sel0, sel1);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+#pragma unroll
+      for (int fn = FM - 2; fn < FN; fn++) a0n[fn] = unpack8_nat(wq0n[fn], sel0, sel1);
+#pragma unroll
+      for (int fn = 0; fn < FN; fn++) {
+        a0[fn] = a0n[fn];
+        wq1[fn] = wq1n[fn];
+      }
+    }
+    mfma_drain();
+    // every load has landed and every read is done before the epilogue
+    // reuses the ring
+    wait_vmcnt<0>();
+    barrier_nofence();
+  }
+
+  // Epilogue: Y[m][n] = acc * 0.5 * scale[n] for the tile's m_count x n_count
+  // valid outputs (0.5 undoes the 2*dec(c) operand encoding). The raw fp32
+  // accumulators go to the LDS ring straight from the accumulation registers,
+  // in P passes of BM/P tokens (row = token, weight rows contiguous, rows
+  // padded by 16 floats so that the fragment writes of 16 tokens spread over
+  // all banks). The block then writes whole 16-byte chunks of output rows
+  // with a rolled loop in which each thread owns one column chunk (its scales
+  // load once). Stores cover full cache lines and the code stays compact: a
+  // fully unrolled per-fragment store sequence is tens of KB that each
+  // workgroup runs once, and fetching it costs more than the stores.
+  template <typename YT>
+  __device__ static void store_tile(uint32_t *lds, const f32x4 (&acc)[FN][FM],
+                                    const float *scale, YT *Y, size_t ldy, int m0, int m_count,
+                                    int n0, int n_count) {
+    constexpr int ES = sizeof(YT);
+    constexpr int PF = BN + 16;  // LDS row pitch in floats
+    constexpr int P = (BM / 2) * PF * 4 <= LDS_DWORDS * 4 ? 2 : 4;
+    static_assert(FM % P == 0 && (BM / P) * PF * 4 <= LDS_DWORDS * 4, "epilogue staging");
+    constexpr int FMP = FM / P, RP = BM / P, TMP = TM / P;
+    constexpr int CE = 16 / ES;   // output elements per 16-byte chunk
+    constexpr int CR = BN / CE;   // chunks per output row
+    static_assert(NT % CR == 0, "each thread owns one column chunk");
+    constexpr int RI = NT / CR;   // rows per iteration
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int wm = wave % WM, wn = wave / WM, l16 = lane & 15, g = lane >> 4;
+    float *st = reinterpret_cast<float *>(lds);
+    const int c = threadIdx.x % CR, r0 = threadIdx.x / CR;
+    const int nl = c * CE;
+    float sc[CE];
+#pragma unroll
+    for (int e = 0; e < CE; e++) sc[e] = 0.5f * scale[n0 + min(nl + e, n_count - 1)];
+    const bool vec = ((reinterpret_cast<uintptr_t>(Y) | (ldy * ES) | ((size_t)n0 * ES)) & 15) == 0;
+    const bool full = vec && nl + CE <= n_count;
+#pragma unroll
+    for (int p = 0; p < P; p++) {
+#pragma unroll
+      for (int fn = 0; fn < FN; fn++)
+#pragma unroll
+        for (int fmi = 0; fmi < FMP; fmi++)
+          *reinterpret_cast<f32x4 *>(st + (wm * TMP + fmi * 16 + l16) * PF + wn * TN + fn * 16 + 4 * g) =
+              acc[fn][p * FMP + fmi];
+      __syncthreads();
+      for (int lr = r0; lr < RP; lr += RI) {
+        const int m = (lr / TMP) * TM + p * TMP + lr % TMP;  // token within the tile
+        if (m >= m_count || nl >= n_count) continue;
+        const float *src = st + lr * PF + nl;
+        float v[CE];
+#pragma unroll
+        for (int e = 0; e < CE; e += 4) {
+          const f32x4 q = *reinterpret_cast<const f32x4 *>(src + e);
+          v[e] = q.x * sc[e];
+          v[e + 1] = q.y * sc[e + 1];
+          v[e + 2] = q.z * sc[e + 2];
+          v[e + 3] = q.w * sc[e + 3];
+        }
+        YT *d = Y + (size_t)(m0 + m) * ldy + n0 + nl;
+        if constexpr (ES == 4) {
+          if (full) {
+            *reinterpret_cast<f32x4 *>(d) = (f32x4){v[0], v[1], v[2], v[3]};
+          } else {
+            for (int e = 0; e < CE && nl + e < n_count; e++) d[e] = v[e];
+          }
+        } else {
+          uint32_t h[CE];
+#pragma unroll
+          for (int e = 0; e < CE; e++) h[e] = bf16_rne_nb(v[e]);
+          if (full) {
+            *reinterpret_cast<u32x4 *>(d) = (u32x4){h[0] | (h[1] << 16), h[2] | (h[3] << 16),
+                                                   h[4] | (h[5] << 16), h[6] | (h[7] << 16)};
+          } else {
+            for (int e = 0; e < CE && nl + e < n_count; e++) d[e] = (uint16_t)h[e];
+          }
+        }
+      }
+      __syncthreads();
+    }
+  }
+
+  __device__ __forceinline__ static int tok(int fm) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    return (wave % WM) * TM + fm * 16 + (lane & 15);
+  }
+  __device__ __forceinline__ static int rowoff(int fn) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    return (wave / WM) * TN + fn * 16 + 4 * (lane >> 4);
+  }
+};
+
+}  // namespace frx

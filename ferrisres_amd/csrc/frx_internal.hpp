@@ -3,7 +3,23 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <atomic>
+
 namespace frx {
+
+// Opts kernel `fn` in to `bytes` of dynamic LDS on the current device (the
+// attribute is needed above 64 KB), once per device; `done` holds one bit per
+// device id. Concurrent first calls may both set it, which is harmless.
+inline hipError_t opt_in_lds(const void *fn, int bytes, std::atomic<uint64_t> &done) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  const uint64_t bit = dev < 64 ? (uint64_t)1 << dev : 0;
+  if (bit && (done.load(std::memory_order_acquire) & bit)) return hipSuccess;
+  e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+  if (e == hipSuccess && bit) done.fetch_or(bit, std::memory_order_acq_rel);
+  return e;
+}
 
 // Decode GEMV, B <= 16 tokens (frx_gemv.hip).
 hipError_t launch_gemv(const uint32_t *w, const float *scale, const void *x,

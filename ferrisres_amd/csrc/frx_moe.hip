@@ -466,18 +466,14 @@ hipError_t launch_moe(const void *x, int xt_bf16, const void *router,
   const int rch = router_chunk(256 / EP + E);
   const size_t rlds = (size_t)(2 * (256 / EP + E) * (rch + 4) + 4 * 256) * 4;
   {
-    static bool attr_set = false;  // opt in to > 64 KB of dynamic LDS once
-    if (!attr_set) {
-      (void)hipFuncSetAttribute(reinterpret_cast<const void *>(&moe_router_kernel<uint16_t, uint16_t>),
-                                hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
-      (void)hipFuncSetAttribute(reinterpret_cast<const void *>(&moe_router_kernel<uint16_t, float>),
-                                hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
-      (void)hipFuncSetAttribute(reinterpret_cast<const void *>(&moe_router_kernel<float, uint16_t>),
-                                hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
-      (void)hipFuncSetAttribute(reinterpret_cast<const void *>(&moe_router_kernel<float, float>),
-                                hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
-      attr_set = true;
-    }
+    static std::atomic<uint64_t> done[4];
+    const void *fns[4] = {reinterpret_cast<const void *>(&moe_router_kernel<uint16_t, uint16_t>),
+                          reinterpret_cast<const void *>(&moe_router_kernel<uint16_t, float>),
+                          reinterpret_cast<const void *>(&moe_router_kernel<float, uint16_t>),
+                          reinterpret_cast<const void *>(&moe_router_kernel<float, float>)};
+    const int v = (xt_bf16 ? 0 : 2) + (rt_bf16 ? 0 : 1);
+    const hipError_t e = opt_in_lds(fns[v], 160 * 1024, done[v]);
+    if (e != hipSuccess) return e;
   }
   if (xt_bf16 && rt_bf16)
     hipLaunchKernelGGL((moe_router_kernel<uint16_t, uint16_t>), rg, dim3(256), rlds, stream,
