@@ -102,20 +102,11 @@ def main():
     b_dn = gemv_bytes(H, I, B)
     step_bytes = 2 * b_gu + b_dn
 
-    def step(i, events=None):
+    def step(i):
         wg, wu, wd = W[i % copies]
-        if events is None:
-            ctx.ternary_linear(wg, s_gu, x, g)
-            ctx.ternary_linear(wu, s_gu, x, u)
-            ctx.ternary_linear(wd, s_dn, hmid, y)
-        else:
-            for (w, s, xi, yo) in ((wg, s_gu, x, g), (wu, s_gu, x, u), (wd, s_dn, hmid, y)):
-                e0 = torch.cuda.Event(enable_timing=True)
-                e1 = torch.cuda.Event(enable_timing=True)
-                e0.record(stream)
-                ctx.ternary_linear(w, s, xi, yo)
-                e1.record(stream)
-                events.append((e0, e1, w.shape[0]))
+        ctx.ternary_linear(wg, s_gu, x, g)
+        ctx.ternary_linear(wu, s_gu, x, u)
+        ctx.ternary_linear(wd, s_dn, hmid, y)
 
     log(f"bench: warmup {args.warmup} steps ({copies} weight copies, {copies * step_weight_bytes / 1e6:.0f} MB)")
     with torch.cuda.stream(stream):
@@ -123,45 +114,92 @@ def main():
             step(i)
     torch.cuda.synchronize()
 
-    # timed region (value)
+    # The decode loop is launch-bound, so the timed K steps run as one
+    # captured HIP graph (weights rotating over the copies step by step);
+    # eager launches are the fallback where capture is unavailable.
+    def capture(fn):
+        try:
+            gr = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(gr, stream=stream):
+                fn()
+            torch.cuda.synchronize()
+            return gr
+        except Exception as e:  # noqa: BLE001 - reported in the JSON line
+            log(f"bench: graph capture unavailable ({e}); timing eager launches")
+            torch.cuda.synchronize()
+            return None
+
+    g_steps = capture(lambda: [step(i) for i in range(args.steps)])
+    timing = "hip_graph" if g_steps is not None else "eager"
     torch.cuda.synchronize()
+    # timed region (value): exactly args.steps steps
     t0 = time.perf_counter()
     with torch.cuda.stream(stream):
-        for i in range(args.steps):
-            step(i)
+        if g_steps is not None:
+            g_steps.replay()
+        else:
+            for i in range(args.steps):
+                step(i)
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
     ms_per_step = elapsed / args.steps * 1e3
     value = step_bytes / (elapsed / args.steps) / 1e9
-    log(f"bench: decode B={B}: {ms_per_step * 1e3:.1f} us/step, {value:.1f} GB/s")
+    log(f"bench: decode B={B}: {ms_per_step * 1e3:.1f} us/step, {value:.1f} GB/s ({timing})")
+    del g_steps
 
-    # per-launch kernel durations (HIP events on the launch stream)
-    evs = []
-    with torch.cuda.stream(stream):
-        for i in range(args.steps):
-            step(i, evs)
-    torch.cuda.synchronize()
-    dur = {I: [], H: []}
-    for e0, e1, n in evs:
-        dur[n].append(e0.elapsed_time(e1) * 1e-3)
+    # Per-launch GEMV time: back-to-back launches of one shape (weights
+    # rotating over the copies), HIP events on the launch stream around the
+    # whole sequence, divided by the number of launches.
+    def shape_seq(kind):
+        def fn():
+            for i in range(copies):
+                wg, wu, wd = W[i]
+                if kind == "gu":
+                    ctx.ternary_linear(wg, s_gu, x, g)
+                    ctx.ternary_linear(wu, s_gu, x, u)
+                else:
+                    ctx.ternary_linear(wd, s_dn, hmid, y)
+        return fn
+
+    per_launch = {}
+    for kind, nl in (("gu", 2 * copies), ("dn", copies)):
+        fn = shape_seq(kind)
+        gr = capture(fn) if timing == "hip_graph" else None
+        reps = max(3, args.steps // copies)
+        with torch.cuda.stream(stream):
+            (gr.replay() if gr is not None else fn())
+        torch.cuda.synchronize()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        with torch.cuda.stream(stream):
+            e0.record(stream)
+            for _ in range(reps):
+                (gr.replay() if gr is not None else fn())
+            e1.record(stream)
+        torch.cuda.synchronize()
+        per_launch[kind] = e0.elapsed_time(e1) * 1e-3 / (reps * nl)
     launch_bytes = 2 * b_gu + b_dn
-    launch_time = 2 * float(np.mean(dur[I])) + float(np.mean(dur[H]))
+    launch_time = 2 * per_launch["gu"] + per_launch["dn"]
     achieved = launch_bytes / launch_time / 1e9
     roofline = {
         "kernel": "frx::gemv_kernel<bf16,bf16>",
         "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
         "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-        "avg_us": {"11008x4096": round(float(np.mean(dur[I])) * 1e6, 3),
-                   "4096x11008": round(float(np.mean(dur[H])) * 1e6, 3)},
+        "avg_us": {"11008x4096": round(per_launch["gu"] * 1e6, 3),
+                   "4096x11008": round(per_launch["dn"] * 1e6, 3)},
         "bytes_per_launch": {"11008x4096": b_gu, "4096x11008": b_dn},
+        "timing": timing,
     }
     traffic_file = os.path.join(ROOT, "profiles", "gemv_traffic.json")
     if os.path.exists(traffic_file):
         try:
             tr = json.load(open(traffic_file))
             if tr.get("batch") == B:
-                roofline["traffic"] = tr.get("bytes_per_launch")
-        except (OSError, ValueError):
+                by = tr["bytes_per_launch"]
+                # per-launch average over the step's three launches
+                roofline["traffic"] = int(round((2 * by["11008x4096"] + by["4096x11008"]) / 3))
+                roofline["traffic_by_shape"] = by
+        except (OSError, ValueError, KeyError):
             pass
 
     extra = {}
