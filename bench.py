@@ -3,21 +3,25 @@
 
 Headline workload (value): decode ternary GEMV at LLaMA-7B FFN shapes. One
 step = one decode pass of B tokens through the three FFN projections
-(W_gate, W_up [11008,4096] and W_down [4096,11008]), bf16 activations, fp32
-accumulation, bf16 outputs. Weights, scales and activations are resident in
+(W_gate, W_up [11008,4096] on x, W_down [4096,11008] on its own [B,11008]
+input), bf16 activations, fp32 accumulation, bf16 outputs, three
+frx_ternary_linear launches. Weights, scales and activations are resident in
 HBM before timing; the weights rotate over enough distinct copies (>= 0.5 GB)
 that the 256 MB Infinity Cache cannot serve them. value = algorithmic bytes
-per step (packed weights + scales + x + y) / time per step.
+per step (packed weights + scales + x + y) / time per step, the K timed steps
+replayed from one HIP graph.
 
-roofline: algorithmic bytes per GEMV launch / average GEMV launch duration
-(HIP events around every launch in the timed region, on the launch stream).
+roofline: algorithmic bytes per GEMV launch / its average launch time over
+back-to-back launches of one shape (HIP events on the launch stream around
+the sequence), weighted over the step's three launches.
 cpu_baseline: the reference's CPU decode path (ternary_matmul_packed_parallel,
 src/model/ternary.rs:471-529, restated in C by the oracle) on the same three
 matrices at B=1, timed on this host's cores.
 
-extra: prefill GEMM (X[2048,4096] x W[N,4096], N in {4096, 11008}), 2:4
-sparse GEMM and the MoE expert layer, as TFLOP/s and fraction of the dense
-bf16 MFMA peak.
+extra: the decode FFN of the same layer through frx_ternary_ffn (fused
+gate/up/SiLU launch + fp32-input down launch), prefill GEMM (X[2048,4096] x
+W[N,4096], N in {4096, 11008}), 2:4 sparse GEMM and the MoE expert layer, as
+TFLOP/s and fraction of the dense bf16 MFMA peak.
 """
 from __future__ import annotations
 
@@ -80,22 +84,27 @@ def main():
 
     # ---- inputs (resident before timing) -------------------------------------
     log("bench: generating weights")
-    t_gu = synth.ternary_uniform("bench/decode", "w_gate", I, H)
-    t_dn = synth.ternary_uniform("bench/decode", "w_down", H, I)
-    w_gu = torch.from_numpy(synth.pack_rows_u32(t_gu).view(np.int32)).to(dev)
-    w_dn = torch.from_numpy(synth.pack_rows_u32(t_dn).view(np.int32)).to(dev)
-    s_gu = torch.from_numpy(synth.row_scales("bench/decode", "s_gate", I, samples=256)).to(dev)
-    s_dn = torch.from_numpy(synth.row_scales("bench/decode", "s_down", H, samples=256)).to(dev)
-    step_weight_bytes = 2 * w_gu.numel() * 4 + w_dn.numel() * 4
+    t_g = synth.ternary_uniform("bench/decode", "w_gate", I, H)
+    t_u = synth.ternary_uniform("bench/decode", "w_up", I, H)
+    t_d = synth.ternary_uniform("bench/decode", "w_down", H, I)
+    w_g = torch.from_numpy(synth.pack_rows_u32(t_g).view(np.int32)).to(dev)
+    w_u = torch.from_numpy(synth.pack_rows_u32(t_u).view(np.int32)).to(dev)
+    w_d = torch.from_numpy(synth.pack_rows_u32(t_d).view(np.int32)).to(dev)
+    s_g = torch.from_numpy(synth.row_scales("bench/decode", "s_gate", I, samples=256)).to(dev)
+    s_u = torch.from_numpy(synth.row_scales("bench/decode", "s_up", I, samples=256)).to(dev)
+    s_d = torch.from_numpy(synth.row_scales("bench/decode", "s_down", H, samples=256)).to(dev)
+    step_weight_bytes = (w_g.numel() + w_u.numel() + w_d.numel()) * 4
     copies = max(2, int(np.ceil(512e6 / step_weight_bytes)) + 1)
-    W = [(w_gu.clone(), w_gu.clone(), w_dn.clone()) for _ in range(copies)]
+    W = [(w_g.clone(), w_u.clone(), w_d.clone()) for _ in range(copies)]
+    del w_g, w_u, w_d
     _, xb = synth.activations("bench/decode", "x", B, H)
     _, hb = synth.activations("bench/decode", "h", B, I)
     x = torch.from_numpy(xb.view(np.int16)).to(dev).view(torch.bfloat16)
-    hmid = torch.from_numpy(hb.view(np.int16)).to(dev).view(torch.bfloat16)
+    xd = torch.from_numpy(hb.view(np.int16)).to(dev).view(torch.bfloat16)  # down-projection input
     g = torch.empty((B, I), dtype=torch.bfloat16, device=dev)
     u = torch.empty((B, I), dtype=torch.bfloat16, device=dev)
     y = torch.empty((B, H), dtype=torch.bfloat16, device=dev)
+    h = torch.empty((B, I), dtype=torch.float32, device=dev)  # fused FFN: gated product
     torch.cuda.synchronize()
 
     b_gu = gemv_bytes(I, H, B)
@@ -103,15 +112,18 @@ def main():
     step_bytes = 2 * b_gu + b_dn
 
     def step(i):
+        """One decode step: the three LLaMA-7B FFN projections as GEMVs."""
         wg, wu, wd = W[i % copies]
-        ctx.ternary_linear(wg, s_gu, x, g)
-        ctx.ternary_linear(wu, s_gu, x, u)
-        ctx.ternary_linear(wd, s_dn, hmid, y)
+        ctx.ternary_linear(wg, s_g, x, g)
+        ctx.ternary_linear(wu, s_u, x, u)
+        ctx.ternary_linear(wd, s_d, xd, y)
 
     log(f"bench: warmup {args.warmup} steps ({copies} weight copies, {copies * step_weight_bytes / 1e6:.0f} MB)")
     with torch.cuda.stream(stream):
         for i in range(args.warmup):
             step(i)
+            wg, wu, wd = W[i % copies]
+            ctx.ternary_ffn(x, wg, s_g, wu, s_u, wd, s_d, y)  # allocates the FFN workspace
     torch.cuda.synchronize()
 
     # The decode loop is launch-bound, so the timed K steps run as one
@@ -129,68 +141,61 @@ def main():
             torch.cuda.synchronize()
             return None
 
-    g_steps = capture(lambda: [step(i) for i in range(args.steps)])
-    timing = "hip_graph" if g_steps is not None else "eager"
-    torch.cuda.synchronize()
-    # timed region (value): exactly args.steps steps
-    t0 = time.perf_counter()
-    with torch.cuda.stream(stream):
-        if g_steps is not None:
-            g_steps.replay()
-        else:
-            for i in range(args.steps):
-                step(i)
-    torch.cuda.synchronize()
-    elapsed = time.perf_counter() - t0
-    ms_per_step = elapsed / args.steps * 1e3
-    value = step_bytes / (elapsed / args.steps) / 1e9
-    log(f"bench: decode B={B}: {ms_per_step * 1e3:.1f} us/step, {value:.1f} GB/s ({timing})")
-    del g_steps
-
-    # Per-launch GEMV time: back-to-back launches of one shape (weights
-    # rotating over the copies), HIP events on the launch stream around the
-    # whole sequence, divided by the number of launches.
-    def shape_seq(kind):
-        def fn():
-            for i in range(copies):
-                wg, wu, wd = W[i]
-                if kind == "gu":
-                    ctx.ternary_linear(wg, s_gu, x, g)
-                    ctx.ternary_linear(wu, s_gu, x, u)
-                else:
-                    ctx.ternary_linear(wd, s_dn, hmid, y)
-        return fn
-
-    per_launch = {}
-    for kind, nl in (("gu", 2 * copies), ("dn", copies)):
-        fn = shape_seq(kind)
-        gr = capture(fn) if timing == "hip_graph" else None
-        reps = max(3, args.steps // copies)
+    def timed(fn):
+        """Seconds for fn() run from a captured graph (or eagerly)."""
+        gr = capture(fn)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
         with torch.cuda.stream(stream):
             (gr.replay() if gr is not None else fn())
+        torch.cuda.synchronize()
+        return time.perf_counter() - t0, gr is not None
+
+    # timed region (value): exactly args.steps steps
+    elapsed, graphed = timed(lambda: [step(i) for i in range(args.steps)])
+    timing = "hip_graph" if graphed else "eager"
+    ms_per_step = elapsed / args.steps * 1e3
+    value = step_bytes / (elapsed / args.steps) / 1e9
+    log(f"bench: decode GEMV B={B}: {ms_per_step * 1e3:.1f} us/step, {value:.1f} GB/s ({timing})")
+
+    # Per-launch kernel time: back-to-back launches of one kernel (weights
+    # rotating over the copies), HIP events on the launch stream around the
+    # whole sequence, divided by the number of launches.
+    def per_launch(fn_one, per_copy, reps):
+        def seq():
+            for i in range(copies):
+                fn_one(i)
+        gr = capture(seq) if graphed else None
+        with torch.cuda.stream(stream):
+            (gr.replay() if gr is not None else seq())
         torch.cuda.synchronize()
         e0 = torch.cuda.Event(enable_timing=True)
         e1 = torch.cuda.Event(enable_timing=True)
         with torch.cuda.stream(stream):
             e0.record(stream)
             for _ in range(reps):
-                (gr.replay() if gr is not None else fn())
+                (gr.replay() if gr is not None else seq())
             e1.record(stream)
         torch.cuda.synchronize()
-        per_launch[kind] = e0.elapsed_time(e1) * 1e-3 / (reps * nl)
+        return e0.elapsed_time(e1) * 1e-3 / (reps * copies * per_copy)
+
+    reps = max(3, args.steps // copies)
+    t_gu = per_launch(lambda i: (ctx.ternary_linear(W[i][0], s_g, x, g), ctx.ternary_linear(W[i][1], s_u, x, u)),
+                      2, reps)
+    t_dn = per_launch(lambda i: ctx.ternary_linear(W[i][2], s_d, xd, y), 1, reps)
     launch_bytes = 2 * b_gu + b_dn
-    launch_time = 2 * per_launch["gu"] + per_launch["dn"]
+    launch_time = 2 * t_gu + t_dn
     achieved = launch_bytes / launch_time / 1e9
     roofline = {
-        "kernel": "frx::gemv_kernel<bf16,bf16>",
+        "kernel": "frx::gemv_kernel (linear, bf16 in, bf16 out)",
         "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
         "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-        "avg_us": {"11008x4096": round(per_launch["gu"] * 1e6, 3),
-                   "4096x11008": round(per_launch["dn"] * 1e6, 3)},
+        "avg_us": {"11008x4096": round(t_gu * 1e6, 3), "4096x11008": round(t_dn * 1e6, 3)},
         "bytes_per_launch": {"11008x4096": b_gu, "4096x11008": b_dn},
         "timing": timing,
     }
     traffic_file = os.path.join(ROOT, "profiles", "gemv_traffic.json")
+    ffn_traffic = None
     if os.path.exists(traffic_file):
         try:
             tr = json.load(open(traffic_file))
@@ -198,17 +203,41 @@ def main():
                 by = tr["bytes_per_launch"]
                 # per-launch average over the step's three launches
                 roofline["traffic"] = int(round((2 * by["11008x4096"] + by["4096x11008"]) / 3))
-                roofline["traffic_by_shape"] = by
+                roofline["traffic_by_shape"] = {k: by[k] for k in ("11008x4096", "4096x11008")}
+                ffn_traffic = {k: by[k] for k in ("glu_11008x4096", "down_f32_4096x11008") if k in by}
         except (OSError, ValueError, KeyError):
             pass
 
-    extra = {}
+    # The decode FFN of the same layer through frx_ternary_ffn: gate, up and
+    # SiLU in one launch (fp32 product), then the fp32-input down GEMV.
+    b_glu = 2 * (I * H // 4 + 4 * I) + 2 * B * H + 4 * B * I
+    b_down32 = H * I // 4 + 4 * H + 4 * B * I + 2 * B * H
+
+    def ffn_step(i):
+        wg, wu, wd = W[i % copies]
+        ctx.ternary_ffn(x, wg, s_g, wu, s_u, wd, s_d, y)
+    el_f, _ = timed(lambda: [ffn_step(i) for i in range(args.steps)])
+    t_glu = per_launch(lambda i: ctx.ternary_glu(x, W[i][0], s_g, W[i][1], s_u, h), 1, reps)
+    t_d32 = per_launch(lambda i: ctx.ternary_linear(W[i][2], s_d, h, y), 1, reps)
+    fused = {"us_per_step": round(el_f / args.steps * 1e6, 2),
+             "gb_s": round((b_glu + b_down32) / (el_f / args.steps) / 1e9, 1),
+             "launches_per_step": 2,
+             "gate_up_silu_avg_us": round(t_glu * 1e6, 3),
+             "gate_up_silu_gb_s": round(b_glu / t_glu / 1e9, 1),
+             "down_f32_in_avg_us": round(t_d32 * 1e6, 3),
+             "down_f32_in_gb_s": round(b_down32 / t_d32 / 1e9, 1),
+             "algorithmic_bytes": {"glu_11008x4096": b_glu, "down_f32_4096x11008": b_down32},
+             "traffic": ffn_traffic}
+    log(f"bench: decode FFN (fused gate/up/SiLU + down): {fused['us_per_step']} us/step; "
+        f"gate/up {fused['gate_up_silu_avg_us']} us, down {fused['down_f32_in_avg_us']} us")
+
+    extra = {"decode_ffn_fused_llama7b": fused}
     if not args.no_extra:
-        extra = run_extra(torch, frx, synth, ctx, stream, dev)
+        extra.update(run_extra(torch, frx, synth, ctx, stream, dev))
 
     cpu = None
     if not args.no_cpu_baseline:
-        cpu = cpu_baseline(t_gu, t_dn, B, args.cpu_seconds)
+        cpu = cpu_baseline(t_g, t_d, B, args.cpu_seconds)
 
     out = {
         "metric": "ternary GEMV GB/s (% HBM peak) + GEMM TFLOP/s (% MFMA peak), 1 MI355X",
@@ -224,7 +253,7 @@ def main():
         "dtype": "bf16",
         "data": "synthetic",
         "config": {
-            "workload": "decode_gemv_llama7b_ffn",
+            "workload": "decode_gemv_llama7b_ffn_shapes",
             "batch_tokens": B,
             "projections": ["gate 11008x4096", "up 11008x4096", "down 4096x11008"],
             "x_dtype": "bf16", "y_dtype": "bf16", "accumulate": "fp32",

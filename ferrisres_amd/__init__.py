@@ -56,6 +56,9 @@ _SIGS = {
     "frx_sparse24_ternary_linear": (_int, [_vp, _vp, _vp, _vp, _int, _vp, _int, _u32, _u32, _u32]),
     "frx_moe_ternary_ffn": (_int, [_vp, _vp, _int, _vp, _int, _vp, _vp, _vp, _vp, _vp, _vp,
                                    _u32, _u32, _u32, _u32, _u32, _int, _vp, _int, _vp, _vp]),
+    "frx_ternary_glu": (_int, [_vp, _vp, _int, _vp, _vp, _vp, _vp, _u32, _u32, _u32, _int, _vp]),
+    "frx_ternary_ffn": (_int, [_vp, _vp, _int, _vp, _vp, _vp, _vp, _vp, _vp, _u32, _u32, _u32,
+                               _int, _vp, _int]),
     "frx_pack_ternary_u8": (_int, [_vp, _sz, _vp]),
     "frx_unpack_ternary_u8": (_int, [_vp, _sz, _vp]),
     "frx_repack_u8_to_u32": (_int, [_vp, _sz, _vp]),
@@ -229,6 +232,23 @@ class Context:
             arr(w_gate), arr(s_gate), arr(w_up), arr(s_up), arr(w_down), arr(s_down),
             T, H, I, E, top_k, act, _ptr(y), _dtype_code(y), _ptr(topk_idx), _ptr(topk_w)),
             self._h)
+        return y
+
+    def ternary_glu(self, x, w_gate, s_gate, w_up, s_up, h, act: int = ACT_SILU):
+        """h (fp32) = act(x Wg^T s_gate) * (x Wu^T s_up)."""
+        M, H = x.shape
+        I = w_gate.shape[0]
+        _check(lib().frx_ternary_glu(self._h, _ptr(x), _dtype_code(x), _ptr(w_gate), _ptr(s_gate),
+                                     _ptr(w_up), _ptr(s_up), M, H, I, act, _ptr(h)), self._h)
+        return h
+
+    def ternary_ffn(self, x, w_gate, s_gate, w_up, s_up, w_down, s_down, y, act: int = ACT_SILU):
+        """Dense FFN: y = (act(x Wg^T s_gate) * (x Wu^T s_up)) Wd^T s_down."""
+        M, H = x.shape
+        I = w_gate.shape[0]
+        _check(lib().frx_ternary_ffn(self._h, _ptr(x), _dtype_code(x), _ptr(w_gate), _ptr(s_gate),
+                                     _ptr(w_up), _ptr(s_up), _ptr(w_down), _ptr(s_down), M, H, I,
+                                     act, _ptr(y), _dtype_code(y)), self._h)
         return y
 
     # GpuMatmulAccelerator analogues: host numpy in, host numpy out.

@@ -6,6 +6,8 @@
 //  - frx_gpu_* = GpuMatmulAccelerator::gpu_*_matmul (host slices in, owned
 //    host result out, synchronous; src/model/gpu_forward.rs:1146-1328)
 //  - frx_moe_ternary_ffn = the model's GPU MoE glue.
+//  - frx_ternary_ffn = the dense FFN branch of the model's decode step
+//    (gate/up projections, activation, product, down projection).
 // Every failure is returned as a status (FerrisResError mapping) with a
 // message in the context; nothing aborts. There is no CPU fallback: a call
 // either runs the HIP kernels or fails.
@@ -28,6 +30,10 @@ struct frx_ctx {
   size_t scratch_bytes = 0;
   void *moe_ws = nullptr;
   size_t moe_ws_bytes = 0;
+  void *ffn_ws = nullptr;  // dense FFN intermediate h (fp32)
+  size_t ffn_ws_bytes = 0;
+  void *glu_ws = nullptr;  // up projection of the GEMM-path GLU (fp32)
+  size_t glu_ws_bytes = 0;
 };
 
 static frx_status fail(frx_ctx *ctx, frx_status st, const char *fmt, ...) {
@@ -55,6 +61,8 @@ static frx_status enter(frx_ctx *ctx) {
 }
 
 static bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+static size_t a256(size_t v) { return (v + 255) & ~(size_t)255; }
 
 extern "C" {
 
@@ -93,6 +101,8 @@ void frx_destroy(frx_ctx *ctx) {
   hipSetDevice(ctx->device);
   if (ctx->scratch) hipFree(ctx->scratch);
   if (ctx->moe_ws) hipFree(ctx->moe_ws);
+  if (ctx->ffn_ws) hipFree(ctx->ffn_ws);
+  if (ctx->glu_ws) hipFree(ctx->glu_ws);
   delete ctx;
 }
 
@@ -203,6 +213,98 @@ frx_status frx_moe_ternary_ffn(
   return FRX_OK;
 }
 
+// Grows a context-owned device buffer (synchronises the stream before
+// freeing the old one; the first call at a given size allocates).
+static frx_status ensure_buffer(frx_ctx *ctx, void **buf, size_t *have, size_t need, const char *what) {
+  if (need <= *have) return FRX_OK;
+  if (*buf) {
+    hipStreamSynchronize(ctx->stream);
+    hipFree(*buf);
+    *buf = nullptr;
+    *have = 0;
+  }
+  hipError_t e = hipMalloc(buf, need);
+  if (e != hipSuccess) return hip_fail(ctx, e, what);
+  *have = need;
+  return FRX_OK;
+}
+
+static frx_status check_ffn(frx_ctx *ctx, const void *x, frx_dtype xt, const void *w_gate,
+                            const float *s_gate, const void *w_up, const float *s_up, uint32_t M,
+                            uint32_t H, uint32_t I, frx_activation act) {
+  if (!x || !w_gate || !s_gate || !w_up || !s_up) return fail(ctx, FRX_ERR_SHAPE, "null pointer argument");
+  if (M == 0 || H == 0 || I == 0) return fail(ctx, FRX_ERR_SHAPE, "empty shape M=%u H=%u I=%u", M, H, I);
+  if (H % 16 != 0 || I % 16 != 0)
+    return fail(ctx, FRX_ERR_SHAPE, "hidden=%u and intermediate=%u must be multiples of 16", H, I);
+  if (xt != FRX_F32 && xt != FRX_BF16) return fail(ctx, FRX_ERR_UNSUPPORTED, "dtype must be FRX_F32 or FRX_BF16");
+  if (act != FRX_ACT_SILU && act != FRX_ACT_GELU_TANH) return fail(ctx, FRX_ERR_UNSUPPORTED, "activation");
+  if (!aligned16(x) || !aligned16(s_gate) || !aligned16(s_up))
+    return fail(ctx, FRX_ERR_UNSUPPORTED, "x and scales must be 16-byte aligned device pointers");
+  if ((size_t)M * H > (size_t)0x7FFFFFFF || (size_t)M * I > (size_t)0x3FFFFFFF)
+    return fail(ctx, FRX_ERR_SHAPE, "M*H or M*I too large");
+  return FRX_OK;
+}
+
+// h = act(g) * u into an fp32 [M][I] buffer. M <= 16: one launch; larger M:
+// two GEMMs (g into h, u into the context's workspace) and a combine.
+static frx_status glu_into(frx_ctx *ctx, const void *x, frx_dtype xt, const uint32_t *w_gate,
+                           const float *s_gate, const uint32_t *w_up, const float *s_up, uint32_t M,
+                           uint32_t H, uint32_t I, bool gelu, float *h) {
+  hipError_t e;
+  if (M <= 16) {
+    e = frx::launch_gemv_glu(w_gate, s_gate, w_up, s_up, x, xt == FRX_BF16, h, (int)M, (int)H, (int)I, gelu,
+                             ctx->stream);
+  } else {
+    const size_t ub = a256((size_t)M * I * 4);
+    frx_status st = ensure_buffer(ctx, &ctx->glu_ws, &ctx->glu_ws_bytes, ub, "GLU workspace allocation");
+    if (st != FRX_OK) return st;
+    float *u = reinterpret_cast<float *>(ctx->glu_ws);
+    e = frx::launch_gemm(w_gate, s_gate, x, xt == FRX_BF16, h, 0, (int)M, (int)H, (int)I, 0, ctx->stream);
+    if (e == hipSuccess)
+      e = frx::launch_gemm(w_up, s_up, x, xt == FRX_BF16, u, 0, (int)M, (int)H, (int)I, 0, ctx->stream);
+    if (e == hipSuccess) e = frx::launch_glu_combine(h, u, h, (size_t)M * I, gelu, ctx->stream);
+  }
+  if (e != hipSuccess) return hip_fail(ctx, e, "gate/up launch");
+  return FRX_OK;
+}
+
+frx_status frx_ternary_glu(frx_ctx *ctx, const void *x, frx_dtype xt, const uint32_t *w_gate,
+                           const float *s_gate, const uint32_t *w_up, const float *s_up, uint32_t M,
+                           uint32_t H, uint32_t I, frx_activation act, float *h) {
+  frx_status st = enter(ctx);
+  if (st != FRX_OK) return st;
+  if ((st = check_ffn(ctx, x, xt, w_gate, s_gate, w_up, s_up, M, H, I, act)) != FRX_OK) return st;
+  if (!h) return fail(ctx, FRX_ERR_SHAPE, "null output pointer");
+  if (!aligned16(h)) return fail(ctx, FRX_ERR_UNSUPPORTED, "h must be a 16-byte aligned device pointer");
+  return glu_into(ctx, x, xt, w_gate, s_gate, w_up, s_up, M, H, I, act == FRX_ACT_GELU_TANH, h);
+}
+
+frx_status frx_ternary_ffn(frx_ctx *ctx, const void *x, frx_dtype xt, const uint32_t *w_gate,
+                           const float *s_gate, const uint32_t *w_up, const float *s_up,
+                           const uint32_t *w_down, const float *s_down, uint32_t M, uint32_t H,
+                           uint32_t I, frx_activation act, void *y, frx_dtype yt) {
+  frx_status st = enter(ctx);
+  if (st != FRX_OK) return st;
+  if ((st = check_ffn(ctx, x, xt, w_gate, s_gate, w_up, s_up, M, H, I, act)) != FRX_OK) return st;
+  if (!w_down || !s_down || !y) return fail(ctx, FRX_ERR_SHAPE, "null pointer argument");
+  if (yt != FRX_F32 && yt != FRX_BF16) return fail(ctx, FRX_ERR_UNSUPPORTED, "dtype must be FRX_F32 or FRX_BF16");
+  if (!aligned16(y) || !aligned16(s_down))
+    return fail(ctx, FRX_ERR_UNSUPPORTED, "y and scales must be 16-byte aligned device pointers");
+  if ((st = ensure_buffer(ctx, &ctx->ffn_ws, &ctx->ffn_ws_bytes, a256((size_t)M * I * 4),
+                          "FFN workspace allocation")) != FRX_OK)
+    return st;
+  float *h = reinterpret_cast<float *>(ctx->ffn_ws);
+  if ((st = glu_into(ctx, x, xt, w_gate, s_gate, w_up, s_up, M, H, I, act == FRX_ACT_GELU_TANH, h)) != FRX_OK)
+    return st;
+  hipError_t e;
+  if (M <= 16)
+    e = frx::launch_gemv(w_down, s_down, h, 0, y, yt == FRX_BF16, (int)M, (int)I, (int)H, ctx->stream);
+  else
+    e = frx::launch_gemm(w_down, s_down, h, 0, y, yt == FRX_BF16, (int)M, (int)I, (int)H, 0, ctx->stream);
+  if (e != hipSuccess) return hip_fail(ctx, e, "ffn down launch");
+  return FRX_OK;
+}
+
 // ---- host-slice accelerator API (GpuMatmulAccelerator) --------------------
 
 static frx_status ensure_scratch(frx_ctx *ctx, size_t bytes) {
@@ -218,8 +320,6 @@ static frx_status ensure_scratch(frx_ctx *ctx, size_t bytes) {
   ctx->scratch_bytes = bytes;
   return FRX_OK;
 }
-
-static size_t a256(size_t v) { return (v + 255) & ~(size_t)255; }
 
 static frx_status host_linear(frx_ctx *ctx, const uint32_t *w_host,
                               const float *s_host, const uint32_t *w_dev,

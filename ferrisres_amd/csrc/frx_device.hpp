@@ -89,12 +89,13 @@ __device__ __forceinline__ void split_bf16(float x, uint32_t &hi,
 
 // Natural bf16 dwords n[0..7] of a 16-column block (x0..x15) -> interleaved
 // dwords d[i] = x[i] | x[i+8] << 16.
+// One byte permute per output dword.
 __device__ __forceinline__ void interleave16(const uint32_t n[8],
                                              uint32_t d[8]) {
 #pragma unroll
   for (int j = 0; j < 4; j++) {
-    d[2 * j] = (n[j] & 0xFFFFu) | (n[j + 4] << 16);
-    d[2 * j + 1] = (n[j] >> 16) | (n[j + 4] & 0xFFFF0000u);
+    d[2 * j] = __builtin_amdgcn_perm(n[j + 4], n[j], 0x05040100u);
+    d[2 * j + 1] = __builtin_amdgcn_perm(n[j + 4], n[j], 0x07060302u);
   }
 }
 
@@ -151,6 +152,17 @@ struct XBlock<float> {
     }
   }
 };
+
+// FFN activations, fp32 (the reference's f32 formulas: SiLU g/(1+e^-g),
+// ternary_moe.rs:204, cpu_block_attn_res.rs:2323; GeLU-tanh,
+// gemma_mapper.rs:2073-2077).
+__device__ __forceinline__ float act_silu(float g) { return g / (1.0f + expf(-g)); }
+// gemma_mapper.rs:2073-2077
+__device__ __forceinline__ float act_gelu_tanh(float x) {
+  const float c = 0.7978845608028654f;  // sqrt(2/pi)
+  const float inner = c * (x + 0.044715f * x * x * x);
+  return 0.5f * x * (1.0f + tanhf(inner));
+}
 
 // Output stores of 4 consecutive columns.
 template <typename YT>

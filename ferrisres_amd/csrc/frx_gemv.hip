@@ -7,30 +7,29 @@
 // are the M side of v_mfma_f32_16x16x32_bf16 and the (<= 16) tokens its N
 // side. Lane (r = l%16, g = l/16) streams 16-byte chunks (64 codes) of row r
 // with dwordx4 loads; the 4 lanes of a row read 64 contiguous bytes per
-// instruction. The waves split K. Each wave issues all of its weight loads
-// (up to UMAX per lane) before anything else, so the whole matrix is in
-// flight at once; the kernel is a single HBM round trip plus the stream.
-// Codes become bf16 operands in registers (two VALU ops per weight pair,
-// frx_device.hpp); activations come from LDS in the matching K-interleaved
-// order. Lanes whose token is >= B read a zero row, and the staged rows are
-// zero-padded to a multiple of 256 columns, so operand reads never need a
-// predicate. The waves' partial tiles are summed in a fixed order through
-// LDS, so results are deterministic.
+// instruction (a "quad" of chunks). The waves split K into contiguous,
+// balanced ranges of quads, so each wave walks a contiguous stretch of every
+// row of the tile. Each wave issues all of its loads (activations first,
+// then up to UMAX weight quads per lane) before anything else, so the whole
+// matrix is in flight at once; the kernel is one HBM round trip plus the
+// stream.
 //
-// Activations are staged per K-slice into LDS as bf16 (f32 inputs as a hi/lo
-// bf16 pair: two MFMAs per operand, |error| <= 2^-17 |x|).
+// Activations. A wave reads only the x columns of its own quads, so it stages
+// exactly those (B rows x 256 columns per quad) into its own columns of the
+// LDS rows: one or two load instructions, then a wait on its own loads, and
+// no workgroup barrier before the MFMAs. Rows are K-interleaved bf16 (dword i =
+// x[i] | x[i+8] << 16, the order the weight unpack produces); f32 inputs are
+// split into a hi/lo bf16 pair (two MFMAs per operand, |error| <= 2^-17 |x|).
+// Lanes whose token is >= B read a 32-dword zero block of their wave instead.
+// Codes become bf16 operands in registers (two VALU ops per weight pair,
+// frx_device.hpp). The waves' partial tiles are summed in a fixed order
+// through LDS, so results are deterministic.
 #include "frx_device.hpp"
 #include "frx_internal.hpp"
 
 namespace frx {
 
-constexpr int GEMV_UMAX = 8;   // weight chunks per lane per batch
-constexpr int GEMV_XBMAX = 2;  // activation blocks per thread loaded up front
-
-// LDS row stride (dwords) for a slice of ks columns padded to 256: ks/2
-// dwords rounded up to 128 plus 4, so 16 tokens' 16-byte reads hit disjoint
-// banks.
-static inline int gemv_row_stride(int ks) { return ((ks + 255) / 256) * 128 + 4; }
+constexpr int GEMV_XPRE = 1;  // rounds of activation items loaded before the weights
 
 // Weight chunk c (words wb..wb+3, wb = first word of the slice + 4c) of this
 // lane's row. VEC: one dwordx4 (rows 16-byte aligned, K % 64 == 0); else four
@@ -50,110 +49,160 @@ __device__ __forceinline__ u32x4 load_chunk(const uint32_t *wrow, int wb, int kw
   }
 }
 
-template <typename XT, typename YT, int WAVES, bool VEC>
-__global__ __launch_bounds__(WAVES * 64) void gemv_kernel(
+// Epilogues. GEMV_LINEAR: Y = (W x) * scale. GEMV_SWIGLU / GEMV_GEGLU: two
+// matrices (gate W, up W2) against the same x in one pass; Y = act(gate) *
+// up, act = SiLU or GeLU-tanh (the decode FFN's first half; x is staged and
+// read once for both).
+enum { GEMV_LINEAR = 0, GEMV_SWIGLU = 1, GEMV_GEGLU = 2 };
+
+// LDS rows for slices of ks columns: token row stride in dwords (ks padded
+// to 256 columns, bf16 pairs, +4 so that 16 tokens' 16-byte reads spread
+// over the banks). Layout: P planes x B rows, then one 32-dword zero block
+// per wave.
+static inline int gemv_row_stride(int ks) { return ((ks + 255) / 256) * 128 + 4; }
+static inline size_t gemv_lds_bytes(int ks, int waves, int P, int B) {
+  return ((size_t)P * B * gemv_row_stride(ks) + (size_t)waves * 32) * 4;
+}
+
+// UMAX: weight quads per lane per load batch (registers: 4 per quad and
+// matrix).
+// Occupancy target: the 8-wave bf16 tiles of the widest decode launch (688
+// workgroups of N = 11008) need 6 waves per SIMD to be resident at once;
+// the other variants keep their registers (no spills).
+template <typename XT, typename YT, int WAVES, int UMAX, bool VEC, int EPI>
+__global__ __launch_bounds__(WAVES * 64)
+__attribute__((amdgpu_waves_per_eu(WAVES == 8 && sizeof(XT) == 2 && EPI == 0 ? 6 : 1))) void gemv_kernel(
     const uint32_t *__restrict__ W, const float *__restrict__ scale,
+    const uint32_t *__restrict__ W2, const float *__restrict__ scale2,
     const XT *__restrict__ X, YT *__restrict__ Y, int B, int K, int N, int KS,
     int rs) {
   constexpr int P = XBlock<XT>::P;
-  constexpr int NT = WAVES * 64;
+  constexpr int NW = EPI == GEMV_LINEAR ? 1 : 2;  // weight matrices
   extern __shared__ __align__(16) uint32_t lds[];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int r = lane & 15, g = lane >> 4;
   const int wpr = K >> 4;
   const int row = min((int)blockIdx.x * 16 + r, N - 1);  // clamped; stores are masked
-  const uint32_t *wrow = W + (size_t)row * wpr;
+  const uint32_t *wrow[NW];
+  wrow[0] = W + (size_t)row * wpr;
+  if constexpr (NW == 2) wrow[1] = W2 + (size_t)row * wpr;
+  uint32_t *zblk = lds + P * B * rs + wave * 32;  // this wave's zero block
   const int t = r;  // token whose activations this lane feeds (MFMA column)
-  const int zrow = P * B;  // all-zero LDS row for lanes with t >= B
-  const uint32_t *bp0 = lds + (t < B ? t : zrow) * rs;
-  const uint32_t *bq0 = lds + (t < B ? B + t : zrow) * rs;
-  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  const bool live = t < B;
+  if (lane < 8) reinterpret_cast<u32x4 *>(zblk)[lane] = (u32x4){0u, 0u, 0u, 0u};
+  f32x4 acc[NW];
+#pragma unroll
+  for (int m = 0; m < NW; m++) acc[m] = (f32x4){0.f, 0.f, 0.f, 0.f};
   // Row scales are needed only by the epilogue; fetch them now so that load
   // is not a memory round trip after the reduction.
   const int n_out = blockIdx.x * 16 + 4 * g;
-  f32x4 sc = {0.f, 0.f, 0.f, 0.f};
-  if (wave == 0 && t < B && n_out < N) {
-    const int nok = min(4, N - n_out);
-    sc.x = scale[n_out];
-    sc.y = nok > 1 ? scale[n_out + 1] : 0.f;
-    sc.z = nok > 2 ? scale[n_out + 2] : 0.f;
-    sc.w = nok > 3 ? scale[n_out + 3] : 0.f;
+  f32x4 sc[NW];
+#pragma unroll
+  for (int m = 0; m < NW; m++) {
+    const float *sp = m == 0 ? scale : scale2;
+    sc[m] = (f32x4){0.f, 0.f, 0.f, 0.f};
+    if (wave == 0 && live && n_out < N) {
+      const int nok = min(4, N - n_out);
+      sc[m].x = sp[n_out];
+      sc[m].y = nok > 1 ? sp[n_out + 1] : 0.f;
+      sc[m].z = nok > 2 ? sp[n_out + 2] : 0.f;
+      sc[m].w = nok > 3 ? sp[n_out + 3] : 0.f;
+    }
   }
 
   for (int s0 = 0; s0 < K; s0 += KS) {
     const int ks = min(KS, K - s0);
     const int nch = (ks + 63) >> 6;     // 64-column chunks in the slice
-    const int nsteps = (nch + 3) >> 2;  // a wave step covers 4 chunks
+    const int nq = (nch + 3) >> 2;      // quads: one chunk per lane group g
+    const int qa = (wave * nq) / WAVES, qb = ((wave + 1) * nq) / WAVES;  // this wave's quads
     const int kw0 = s0 >> 4;
     const int kw_end = (s0 + ks) >> 4;  // one past the slice's last word
-    const int nblk = (ks + 255) / 256 * 16;  // 16-column x blocks, padded to 256 cols
-    const int kblk = ks >> 4;
-    const int nbtot = (B + 1) * nblk;        // + the zero row
+    const int kblk = ks >> 4;           // 16-column blocks of the slice
+    const int nb = 16 * (qb - qa);      // blocks of this wave (per token)
+    const int cb0 = 16 * qa;            // first block of this wave
+    uint32_t *reg = lds + cb0 * 8;      // this wave's columns of row 0
+    // (token, block) pairs of the wave: item i -> token i / nb, block i % nb;
+    // nb = 16 * (quads of the wave), the division by the quad count is a
+    // multiply-shift (exact here: (i/16) * (quads - 1) < 2^16)
+    const int nqw = max(qb - qa, 1);
+    const uint32_t mq = (65536u + nqw - 1) / nqw;
+    auto item_tok = [&](int i) { return (int)(((uint32_t)(i >> 4) * mq) >> 16); };
+    const int nitem = B * nb;
 
-    // 1. activation loads for the first XBMAX blocks of this thread (L2-hot,
-    //    issued first so that waiting for them does not wait for the weights)
-    uint32_t xh[GEMV_XBMAX][8], xl[GEMV_XBMAX][8];
+    // 1. the first GEMV_XPRE rounds of the wave's activation items (L2-hot,
+    //    issued before the weights so that waiting for them does not wait for
+    //    the weights)
+    uint32_t xh[GEMV_XPRE][8], xl[GEMV_XPRE][8];
 #pragma unroll
-    for (int i = 0; i < GEMV_XBMAX; i++) {
-      const int bi = tid + i * NT;
-      const int tt = bi / nblk, cb = bi - tt * nblk;
-      const bool ok = bi < nbtot && tt < B && cb < kblk;
-      XBlock<XT>::load(X + (size_t)(ok ? tt : 0) * K + s0 + (ok ? cb : 0) * 16, ok, xh[i], xl[i]);
+    for (int i = 0; i < GEMV_XPRE; i++) {
+      const int it = lane + 64 * i, tt = item_tok(it), j = it - tt * nb;
+      const bool ok = it < nitem && cb0 + j < kblk;
+      XBlock<XT>::load(X + (size_t)(ok ? tt : 0) * K + s0 + (ok ? cb0 + j : 0) * 16, ok, xh[i], xl[i]);
     }
     // 2. first batch of weight loads
-    u32x4 wv[GEMV_UMAX];
+    u32x4 wv[NW][UMAX];
 #pragma unroll
-    for (int u = 0; u < GEMV_UMAX; u++) {
-      const int st = wave + WAVES * u;
-      if (st < nsteps) wv[u] = load_chunk<VEC>(wrow, kw0 + (st * 4 + g) * 4, kw_end);
+    for (int u = 0; u < UMAX; u++) {
+      const int q = qa + u;
+#pragma unroll
+      for (int m = 0; m < NW; m++)
+        if (q < qb) wv[m][u] = load_chunk<VEC>(wrow[m], kw0 + (q * 4 + g) * 4, kw_end);
     }
-    // 3. stage the slice's activations into LDS (every wave takes part)
-    if (s0 > 0) __syncthreads();  // previous slice fully consumed
-    auto put = [&](int bi, const uint32_t *hi, const uint32_t *lo) {
-      const int tt = bi / nblk, cb = bi - tt * nblk;
-      const int rh = tt < B ? tt : zrow;
-      u32x4 *d = reinterpret_cast<u32x4 *>(lds + rh * rs + cb * 8);
+    // 3. stage into the wave's columns (zero past the slice end). Quad
+    //    ownership differs between slices, so a later slice first waits until
+    //    every wave is done reading the previous one (no barrier when K fits
+    //    one slice, the decode shapes).
+    if (s0 > 0) __syncthreads();
+    auto put = [&](int tt, int j, const uint32_t *hi, const uint32_t *lo) {
+      u32x4 *d = reinterpret_cast<u32x4 *>(reg + tt * rs + j * 8);
       d[0] = (u32x4){hi[0], hi[1], hi[2], hi[3]};
       d[1] = (u32x4){hi[4], hi[5], hi[6], hi[7]};
       if constexpr (P == 2) {
-        if (tt < B) {
-          u32x4 *e = reinterpret_cast<u32x4 *>(lds + (B + tt) * rs + cb * 8);
-          e[0] = (u32x4){lo[0], lo[1], lo[2], lo[3]};
-          e[1] = (u32x4){lo[4], lo[5], lo[6], lo[7]};
-        }
+        u32x4 *e = reinterpret_cast<u32x4 *>(reg + (B + tt) * rs + j * 8);
+        e[0] = (u32x4){lo[0], lo[1], lo[2], lo[3]};
+        e[1] = (u32x4){lo[4], lo[5], lo[6], lo[7]};
       }
     };
 #pragma unroll
-    for (int i = 0; i < GEMV_XBMAX; i++) {
-      const int bi = tid + i * NT;
-      if (bi < nbtot) put(bi, xh[i], xl[i]);
+    for (int i = 0; i < GEMV_XPRE; i++) {
+      const int it = lane + 64 * i, tt = item_tok(it);
+      if (it < nitem) put(tt, it - tt * nb, xh[i], xl[i]);
     }
-    for (int bi = tid + GEMV_XBMAX * NT; bi < nbtot; bi += NT) {  // large B x K
-      const int tt = bi / nblk, cb = bi - tt * nblk;
-      const bool ok = tt < B && cb < kblk;
-      uint32_t hi[8], lo[8];
-      XBlock<XT>::load(X + (size_t)(ok ? tt : 0) * K + s0 + (ok ? cb : 0) * 16, ok, hi, lo);
-      put(bi, hi, lo);
-    }
-    __syncthreads();
-    // 3. unpack + MFMA, batch by batch
-    for (int st0 = wave; st0 < nsteps; st0 += WAVES * GEMV_UMAX) {
-      if (st0 != wave) {
+    // the remaining items, one round of 64 at a time
+    constexpr int XR = 1;
+    for (int i0 = 64 * GEMV_XPRE; i0 < nitem; i0 += 64 * XR) {
+      uint32_t hi[XR][8], lo[XR][8];
 #pragma unroll
-        for (int u = 0; u < GEMV_UMAX; u++) {
-          const int st = st0 + WAVES * u;
-          if (st < nsteps) wv[u] = load_chunk<VEC>(wrow, kw0 + (st * 4 + g) * 4, kw_end);
+      for (int i = 0; i < XR; i++) {
+        const int it = i0 + lane + 64 * i, tt = item_tok(it), j = it - tt * nb;
+        const bool ok = it < nitem && cb0 + j < kblk;
+        XBlock<XT>::load(X + (size_t)(ok ? tt : 0) * K + s0 + (ok ? cb0 + j : 0) * 16, ok, hi[i], lo[i]);
+      }
+#pragma unroll
+      for (int i = 0; i < XR; i++) {
+        const int it = i0 + lane + 64 * i, tt = item_tok(it);
+        if (it < nitem) put(tt, it - tt * nb, hi[i], lo[i]);
+      }
+    }
+    // 4. unpack + MFMA, batch by batch
+    for (int q0 = qa; q0 < qb; q0 += UMAX) {
+      if (q0 != qa) {
+#pragma unroll
+        for (int u = 0; u < UMAX; u++) {
+          const int q = q0 + u;
+#pragma unroll
+          for (int m = 0; m < NW; m++)
+            if (q < qb) wv[m][u] = load_chunk<VEC>(wrow[m], kw0 + (q * 4 + g) * 4, kw_end);
         }
       }
 #pragma unroll
-      for (int u = 0; u < GEMV_UMAX; u++) {
-        const int st = st0 + WAVES * u;
-        if (st >= nsteps) break;  // wave-uniform
-        const int c = st * 4 + g;
-        const int wb = kw0 + c * 4;
-        const uint32_t *bp = bp0 + c * 32;
-        const uint32_t *bq = bq0 + c * 32;
-        const uint32_t wq[4] = {wv[u].x, wv[u].y, wv[u].z, wv[u].w};
+      for (int u = 0; u < UMAX; u++) {
+        const int q = q0 + u;
+        if (q >= qb) break;  // wave-uniform
+        const int lc = (q - qa) * 4 + g;  // chunk within the wave's columns
+        const int wb = kw0 + (q * 4 + g) * 4;
+        const uint32_t *bp = live ? reg + t * rs + lc * 32 : zblk;
+        const uint32_t *bq = live ? reg + (B + t) * rs + lc * 32 : zblk;
         // VEC: a chunk is either entirely inside the slice or entirely past
         // its end, so one mask per chunk; otherwise one per word.
         const uint32_t mchunk = wb < kw_end ? 0xC000C000u : 0u;
@@ -161,80 +210,148 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(
         for (int q = 0; q < 4; q++) {
           // past the slice end: zero operand (the x rows there are zero too)
           const uint32_t mask = VEC ? mchunk : ((wb + q < kw_end) ? 0xC000C000u : 0u);
-          const u32x4 b0 = *reinterpret_cast<const u32x4 *>(bp + q * 8);
-          const u32x4 b1 = *reinterpret_cast<const u32x4 *>(bp + q * 8 + 4);
-          const u32x4 a0 = unpack_half_m<0>(wq[q], mask), a1 = unpack_half_m<1>(wq[q], mask);
-          acc = mfma16(a0, b0, acc);
-          acc = mfma16(a1, b1, acc);
+          const u32x4 b0 = *reinterpret_cast<const u32x4 *>(bp + (live ? q * 8 : 0));
+          const u32x4 b1 = *reinterpret_cast<const u32x4 *>(bp + (live ? q * 8 + 4 : 4));
+          u32x4 c0, c1;
           if constexpr (P == 2) {
-            const u32x4 c0 = *reinterpret_cast<const u32x4 *>(bq + q * 8);
-            const u32x4 c1 = *reinterpret_cast<const u32x4 *>(bq + q * 8 + 4);
-            acc = mfma16(a0, c0, acc);
-            acc = mfma16(a1, c1, acc);
+            c0 = *reinterpret_cast<const u32x4 *>(bq + (live ? q * 8 : 0));
+            c1 = *reinterpret_cast<const u32x4 *>(bq + (live ? q * 8 + 4 : 4));
+          }
+#pragma unroll
+          for (int m = 0; m < NW; m++) {
+            const uint32_t wq = q == 0 ? wv[m][u].x : q == 1 ? wv[m][u].y : q == 2 ? wv[m][u].z : wv[m][u].w;
+            const u32x4 a0 = unpack_half_m<0>(wq, mask), a1 = unpack_half_m<1>(wq, mask);
+            acc[m] = mfma16(a0, b0, acc[m]);
+            acc[m] = mfma16(a1, b1, acc[m]);
+            if constexpr (P == 2) {
+              acc[m] = mfma16(a0, c0, acc[m]);
+              acc[m] = mfma16(a1, c1, acc[m]);
+            }
           }
         }
       }
     }
   }
-  __syncthreads();
+  __syncthreads();  // every wave is done with its columns before the reuse
 
   // Fixed-order reduction of the waves' partial tiles.
   f32x4 *red = reinterpret_cast<f32x4 *>(lds);
-  red[wave * 64 + lane] = acc;
+#pragma unroll
+  for (int m = 0; m < NW; m++) red[(m * WAVES + wave) * 64 + lane] = acc[m];
   __syncthreads();
   if (wave == 0) {
-    f32x4 s = red[lane];
+    f32x4 s[NW];
 #pragma unroll
-    for (int w = 1; w < WAVES; w++) s += red[w * 64 + lane];
-    if (t < B && n_out < N) {  // rows 4g..4g+3 of token t
-      const f32x4 v = s * (sc * 0.5f);
+    for (int m = 0; m < NW; m++) {
+      s[m] = red[m * WAVES * 64 + lane];
+#pragma unroll
+      for (int w = 1; w < WAVES; w++) s[m] += red[(m * WAVES + w) * 64 + lane];
+      s[m] *= sc[m] * 0.5f;  // 0.5 undoes the 2*dec(c) operand encoding
+    }
+    if (live && n_out < N) {  // rows 4g..4g+3 of token t
+      f32x4 v = s[0];
+      if constexpr (NW == 2) {
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+          const float a = EPI == GEMV_GEGLU ? act_gelu_tanh(s[0][j]) : act_silu(s[0][j]);
+          v[j] = a * s[1][j];
+        }
+      }
       YStore<YT>::store4(Y + (size_t)t * N + n_out, v, min(4, N - n_out));
     }
   }
 }
 
-template <typename XT, typename YT, int WAVES, bool VEC>
-static hipError_t launch_gemv_w(const uint32_t *w, const float *scale,
-                                const void *x, void *y, int B, int K, int N,
+template <typename XT, typename YT, int WAVES, int UMAX, bool VEC, int EPI>
+static hipError_t launch_gemv_w(const uint32_t *w, const float *scale, const uint32_t *w2,
+                                const float *scale2, const void *x, void *y, int B, int K, int N,
                                 hipStream_t stream) {
   constexpr int P = XBlock<XT>::P;
-  const int budget = 56 * 1024;
-  int KS = K;
-  while (KS > 256 && (size_t)(P * B + 1) * gemv_row_stride(KS) * 4 > (size_t)budget)
-    KS = ((KS / 2) + 255) / 256 * 256;
+  constexpr int NW = EPI == GEMV_LINEAR ? 1 : 2;
+  // K slices (multiples of 256 columns) small enough that the rows fit the
+  // LDS budget; one slice at the decode shapes.
+  const size_t budget = 64 * 1024;
+  int KS = (K + 255) / 256 * 256;
+  while (KS > 256 && gemv_lds_bytes(KS, WAVES, P, B) > budget) KS = ((KS / 2) + 255) / 256 * 256;
   const int rs = gemv_row_stride(KS);
-  size_t lds = (size_t)(P * B + 1) * rs * 4;
-  if (lds < (size_t)WAVES * 64 * 16) lds = (size_t)WAVES * 64 * 16;
+  size_t lds = gemv_lds_bytes(KS, WAVES, P, B);
+  if (lds < (size_t)NW * WAVES * 64 * 16) lds = (size_t)NW * WAVES * 64 * 16;
   dim3 grid((N + 15) / 16);
-  hipLaunchKernelGGL((gemv_kernel<XT, YT, WAVES, VEC>), grid, dim3(WAVES * 64), lds, stream, w, scale,
-                     reinterpret_cast<const XT *>(x), reinterpret_cast<YT *>(y), B, K, N, KS, rs);
+  hipLaunchKernelGGL((gemv_kernel<XT, YT, WAVES, UMAX, VEC, EPI>), grid, dim3(WAVES * 64), lds, stream,
+                     w, scale, w2, scale2, reinterpret_cast<const XT *>(x), reinterpret_cast<YT *>(y),
+                     B, K, N, KS, rs);
   return hipGetLastError();
 }
 
-template <typename XT, typename YT>
-static hipError_t launch_gemv_t(const uint32_t *w, const float *scale,
-                                const void *x, void *y, int B, int K, int N,
+template <typename XT, typename YT, int EPI>
+static hipError_t launch_gemv_t(const uint32_t *w, const float *scale, const uint32_t *w2,
+                                const float *scale2, const void *x, void *y, int B, int K, int N,
                                 hipStream_t stream) {
-  // 8 waves when one batch of 4 waves could not cover K (more loads in
-  // flight); dword loads when rows are not 16-byte aligned.
-  const bool vec = ((K >> 4) & 3) == 0 && (reinterpret_cast<uintptr_t>(w) & 15) == 0;
-  if (K > 4 * GEMV_UMAX * 256) {
-    if (vec) return launch_gemv_w<XT, YT, 8, true>(w, scale, x, y, B, K, N, stream);
-    return launch_gemv_w<XT, YT, 8, false>(w, scale, x, y, B, K, N, stream);
+  // Waves per tile grow with K so that each wave holds two to three quads
+  // (short per-wave work after its loads land, many waves in flight, and few
+  // enough registers that every workgroup of the decode shapes is resident
+  // at once); UMAX covers a wave's quads in one load batch up to K = 12288.
+  // Dword loads when rows are not 16-byte aligned.
+  const bool vec = ((K >> 4) & 3) == 0 && (reinterpret_cast<uintptr_t>(w) & 15) == 0 &&
+                   (reinterpret_cast<uintptr_t>(w2) & 15) == 0;
+#define FRX_GEMV_LAUNCH(WV, UM)                                                                  \
+  return vec ? launch_gemv_w<XT, YT, WV, UM, true, EPI>(w, scale, w2, scale2, x, y, B, K, N, stream) \
+             : launch_gemv_w<XT, YT, WV, UM, false, EPI>(w, scale, w2, scale2, x, y, B, K, N, stream)
+  const int nq = (K + 255) / 256;
+  if (nq <= 8) FRX_GEMV_LAUNCH(4, 2);
+  if (nq <= 16) FRX_GEMV_LAUNCH(8, 2);
+  if constexpr (EPI != GEMV_LINEAR) {
+    // two matrices double the weight registers: 8 waves and load batches
+    FRX_GEMV_LAUNCH(8, 3);
+  } else {
+    if (nq <= 48) FRX_GEMV_LAUNCH(16, 3);
+    FRX_GEMV_LAUNCH(16, 4);
   }
-  if (vec) return launch_gemv_w<XT, YT, 4, true>(w, scale, x, y, B, K, N, stream);
-  return launch_gemv_w<XT, YT, 4, false>(w, scale, x, y, B, K, N, stream);
+#undef FRX_GEMV_LAUNCH
 }
 
 hipError_t launch_gemv(const uint32_t *w, const float *scale, const void *x,
                        int xt_bf16, void *y, int yt_bf16, int B, int K, int N,
                        hipStream_t stream) {
+  constexpr int L = GEMV_LINEAR;
   if (xt_bf16) {
-    if (yt_bf16) return launch_gemv_t<uint16_t, uint16_t>(w, scale, x, y, B, K, N, stream);
-    return launch_gemv_t<uint16_t, float>(w, scale, x, y, B, K, N, stream);
+    if (yt_bf16) return launch_gemv_t<uint16_t, uint16_t, L>(w, scale, w, scale, x, y, B, K, N, stream);
+    return launch_gemv_t<uint16_t, float, L>(w, scale, w, scale, x, y, B, K, N, stream);
   }
-  if (yt_bf16) return launch_gemv_t<float, uint16_t>(w, scale, x, y, B, K, N, stream);
-  return launch_gemv_t<float, float>(w, scale, x, y, B, K, N, stream);
+  if (yt_bf16) return launch_gemv_t<float, uint16_t, L>(w, scale, w, scale, x, y, B, K, N, stream);
+  return launch_gemv_t<float, float, L>(w, scale, w, scale, x, y, B, K, N, stream);
+}
+
+hipError_t launch_gemv_glu(const uint32_t *w_gate, const float *s_gate, const uint32_t *w_up,
+                           const float *s_up, const void *x, int xt_bf16, float *h, int B, int K,
+                           int N, int gelu, hipStream_t stream) {
+  if (xt_bf16) {
+    if (gelu)
+      return launch_gemv_t<uint16_t, float, GEMV_GEGLU>(w_gate, s_gate, w_up, s_up, x, h, B, K, N, stream);
+    return launch_gemv_t<uint16_t, float, GEMV_SWIGLU>(w_gate, s_gate, w_up, s_up, x, h, B, K, N, stream);
+  }
+  if (gelu)
+    return launch_gemv_t<float, float, GEMV_GEGLU>(w_gate, s_gate, w_up, s_up, x, h, B, K, N, stream);
+  return launch_gemv_t<float, float, GEMV_SWIGLU>(w_gate, s_gate, w_up, s_up, x, h, B, K, N, stream);
+}
+
+template <bool GELU>
+__global__ __launch_bounds__(256) void glu_combine_kernel(const float *__restrict__ g,
+                                                          const float *__restrict__ u,
+                                                          float *h, size_t n) {
+  for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t)gridDim.x * 256) {
+    const float a = GELU ? act_gelu_tanh(g[i]) : act_silu(g[i]);
+    h[i] = a * u[i];
+  }
+}
+
+hipError_t launch_glu_combine(const float *g, const float *u, float *h, size_t n, int gelu,
+                              hipStream_t stream) {
+  const size_t blocks = (n + 255) / 256;
+  const dim3 grid((unsigned)(blocks < 8192 ? blocks : 8192));
+  if (gelu) hipLaunchKernelGGL((glu_combine_kernel<true>), grid, dim3(256), 0, stream, g, u, h, n);
+  else hipLaunchKernelGGL((glu_combine_kernel<false>), grid, dim3(256), 0, stream, g, u, h, n);
+  return hipGetLastError();
 }
 
 }  // namespace frx

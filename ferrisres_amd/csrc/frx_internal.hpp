@@ -25,6 +25,14 @@ inline hipError_t opt_in_lds(const void *fn, int bytes, std::atomic<uint64_t> &d
 hipError_t launch_gemv(const uint32_t *w, const float *scale, const void *x,
                        int xt_bf16, void *y, int yt_bf16, int B, int K, int N,
                        hipStream_t stream);
+// Decode FFN first half, B <= 16 tokens (frx_gemv.hip): h[B][N] (fp32) =
+// act(gate) * up with gate/up = (W x) * scale for two [N][K] matrices.
+hipError_t launch_gemv_glu(const uint32_t *w_gate, const float *s_gate, const uint32_t *w_up,
+                           const float *s_up, const void *x, int xt_bf16, float *h, int B, int K,
+                           int N, int gelu, hipStream_t stream);
+// h[i] = act(g[i]) * u[i], n elements, fp32 (in place allowed: h == g).
+hipError_t launch_glu_combine(const float *g, const float *u, float *h, size_t n, int gelu,
+                              hipStream_t stream);
 // 2:4 decode GEMV, B <= 16 tokens (frx_gemv.hip).
 hipError_t launch_gemv_sp24(const uint32_t *meta, const float *scale,
                             const void *x, int xt_bf16, void *y, int yt_bf16,

@@ -328,13 +328,6 @@ struct GateUpArgs {
   const float *su[MOE_MAXE];
 };
 
-__device__ __forceinline__ float act_silu(float g) { return g / (1.0f + expf(-g)); }
-// gemma_mapper.rs:2073-2077
-__device__ __forceinline__ float act_gelu_tanh(float x) {
-  const float c = 0.7978845608028654f;  // sqrt(2/pi)
-  const float inner = c * (x + 0.044715f * x * x * x);
-  return 0.5f * x * (1.0f + tanhf(inner));
-}
 
 template <int XS>
 __global__ __launch_bounds__(256) void moe_gateup_kernel(

@@ -111,6 +111,41 @@ frx_status frx_moe_ternary_ffn(
     uint32_t H, uint32_t I, uint32_t E, uint32_t top_k, frx_activation act,
     void *y, frx_dtype yt, uint32_t *topk_idx, float *topk_w);
 
+/* ---- gated pair (first half of the dense FFN) -------------------------------
+ * Replaces the gate and up gpu_ternary_matmul_vram calls plus the host
+ * activation and product of the dense FFN branch
+ * (src/model/cpu_block_attn_res.rs:2319-2324):
+ *   h = act(x Wg^T * s_gate) * (x Wu^T * s_up),  h [M][I] f32 (device)
+ * Same arguments as frx_ternary_ffn below. M <= 16 is one launch that reads x
+ * once for both matrices; larger M runs two GEMMs and an element-wise
+ * combine (up projection in a context workspace, allocated on first use). */
+frx_status frx_ternary_glu(frx_ctx *ctx, const void *x, frx_dtype xt,
+                           const uint32_t *w_gate, const float *s_gate,
+                           const uint32_t *w_up, const float *s_up,
+                           uint32_t M, uint32_t H, uint32_t I,
+                           frx_activation act, float *h);
+
+/* ---- dense ternary FFN ------------------------------------------------------
+ * Replaces the dense FFN branch of the decode step
+ * (src/model/cpu_block_attn_res.rs:2317-2326; prefill forward: :1185-1194):
+ * three ternary matmul calls (gate, up, down) with the activation and the
+ * product on the host.
+ *   y = ((act(x Wg^T * s_gate)) * (x Wu^T * s_up)) Wd^T * s_down
+ *   act = SiLU g/(1+e^-g) (FRX_ACT_SILU) or GeLU-tanh (FRX_ACT_GELU_TANH).
+ *   x [M][H] xt; w_gate, w_up [I][H/16] u32, s_gate, s_up [I] f32;
+ *   w_down [H][I/16] u32, s_down [H] f32; y [M][H] yt (device pointers).
+ * The intermediate (act(g) * u, [M][I]) stays fp32 in a context workspace,
+ * as in the reference: frx_ternary_glu into the workspace, then the down
+ * projection with fp32 input (M <= 16: two launches). Requires H % 16 == 0,
+ * I % 16 == 0. The workspace is allocated on the context on first use (and
+ * grown), so a first call at a new size must not be under graph capture. */
+frx_status frx_ternary_ffn(frx_ctx *ctx, const void *x, frx_dtype xt,
+                           const uint32_t *w_gate, const float *s_gate,
+                           const uint32_t *w_up, const float *s_up,
+                           const uint32_t *w_down, const float *s_down,
+                           uint32_t M, uint32_t H, uint32_t I,
+                           frx_activation act, void *y, frx_dtype yt);
+
 /* ---- host-side packers (no GPU) --------------------------------------------*/
 /* pack_ternary (src/model/ternary.rs:146-163): out has (n+3)/4 bytes. */
 frx_status frx_pack_ternary_u8(const int8_t *values, size_t n, uint8_t *out);

@@ -59,6 +59,8 @@ def lib():
             "frxo_moe_forward": (None, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
                                         _sz, _sz, _sz, _sz, _sz, ctypes.c_int, _vp, _vp, _vp]),
             "frxo_gelu_tanh": (_f, [_f]),
+            "frxo_ffn_forward": (None, [_vp, _sz, _sz, _sz, _vp, _vp, _vp, _vp, _vp, _vp,
+                                        ctypes.c_int, _vp]),
             "frxo_time_packed_parallel": (ctypes.c_double, [_vp, _f, _vp, _sz, _sz, ctypes.c_int,
                                                             ctypes.c_int, _vp]),
         }
@@ -272,6 +274,19 @@ def moe_forward(x, router, w_gate, s_gate, w_up, s_up, w_down, s_down, top_k, ge
     lib().frxo_moe_forward(_p(xx), _p(r), arr(wg), arr(sg), arr(wu), arr(su), arr(wd), arr(sd),
                            T, H, I, E, top_k, int(gelu), _p(out), _p(idx), _p(w))
     return out, idx, w
+
+
+def ffn_forward(x, w_gate, s_gate, w_up, s_up, w_down, s_down, gelu=False):
+    """Dense FFN (gate/up u32 matmuls, activation, product, down matmul), f32."""
+    xx = _c(x, np.float32)
+    M, H = xx.shape
+    I = w_gate.shape[0]
+    arrs = [_c(a, np.uint32) for a in (w_gate, w_up, w_down)] + \
+           [_c(a, np.float32) for a in (s_gate, s_up, s_down)]
+    out = np.zeros((M, H), np.float32)
+    lib().frxo_ffn_forward(_p(xx), M, H, I, _p(arrs[0]), _p(arrs[3]), _p(arrs[1]), _p(arrs[4]),
+                           _p(arrs[2]), _p(arrs[5]), int(gelu), _p(out))
+    return out
 
 
 def gelu_tanh(x):

@@ -697,6 +697,32 @@ void frxo_moe_forward(const float *x, const float *router,
   free(d);
 }
 
+/*
+ * Dense FFN of one layer, cpu_block_attn_res.rs:2317-2326 (decode) and
+ * :1185-1194 (prefill): gated = W_gate x, upped = W_up x (the u32 matmul,
+ * per-row scales), gated = gelu_tanh(gated) or gated / (1 + exp(-gated))
+ * (:2323), combined = gated * upped, out = W_down combined, all in f32 over
+ * all seq tokens. Pinned by its decomposition into the pinned u32 matmul and
+ * the activation (checked against float64 on tiny shapes in the tests).
+ */
+void frxo_ffn_forward(const float *x, size_t seq, size_t hidden, size_t inter,
+                      const uint32_t *w_gate, const float *s_gate,
+                      const uint32_t *w_up, const float *s_up,
+                      const uint32_t *w_down, const float *s_down, int use_gelu,
+                      float *out) {
+  float *g = (float *)malloc(seq * inter * sizeof(float));
+  float *u = (float *)malloc(seq * inter * sizeof(float));
+  frxo_ternary_matmul_u32(w_gate, s_gate, x, seq, hidden, inter, g);
+  frxo_ternary_matmul_u32(w_up, s_up, x, seq, hidden, inter, u);
+  for (size_t i = 0; i < seq * inter; i++) {
+    float a = use_gelu ? frxo_gelu_tanh(g[i]) : g[i] / (1.0f + expf(-g[i]));
+    g[i] = a * u[i];
+  }
+  frxo_ternary_matmul_u32(w_down, s_down, g, seq, inter, hidden, out);
+  free(g);
+  free(u);
+}
+
 /* ---- timed multi-threaded CPU baseline ------------------------------------ */
 
 typedef struct {

@@ -96,6 +96,11 @@ void frxo_moe_forward(const float *x, const float *router,
                       size_t inter, size_t experts, size_t top_k, int use_gelu,
                       float *out, uint32_t *topk_idx, float *topk_w);
 float frxo_gelu_tanh(float x);
+void frxo_ffn_forward(const float *x, size_t seq, size_t hidden, size_t inter,
+                      const uint32_t *w_gate, const float *s_gate,
+                      const uint32_t *w_up, const float *s_up,
+                      const uint32_t *w_down, const float *s_down, int use_gelu,
+                      float *out);
 
 /* ---- multi-threaded CPU baseline (ternary.rs packed-parallel shape) ---- */
 double frxo_time_packed_parallel(const uint8_t *packed, float scale,

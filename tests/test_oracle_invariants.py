@@ -271,3 +271,30 @@ def test_gelu_tanh_vs_f64():
     for v in [-3.0, -0.5, 0.0, 0.3, 2.0]:
         ref = 0.5 * v * (1 + np.tanh(np.sqrt(2 / np.pi) * (v + 0.044715 * v ** 3)))
         assert abs(oracle.gelu_tanh(v) - ref) <= 1e-6 * max(1.0, abs(ref))
+
+
+@pytest.mark.parametrize("gelu", [False, True])
+def test_ffn_oracle_matches_float64(gelu):
+    """Dense FFN oracle (cpu_block_attn_res.rs:2317-2326) = gate/up u32
+    matmuls, activation, product, down matmul; checked against a float64
+    restatement on small shapes, and SiLU != GeLU."""
+    rng = np.random.default_rng(7)
+    M, H, I = 3, 48, 80
+    tg, tu = (rng.integers(-1, 2, (I, H)).astype(np.int8) for _ in range(2))
+    td = rng.integers(-1, 2, (H, I)).astype(np.int8)
+    sg, su = (rng.random(I).astype(np.float32) * 0.1 + 0.01 for _ in range(2))
+    sd = rng.random(H).astype(np.float32) * 0.1 + 0.01
+    x = rng.standard_normal((M, H)).astype(np.float32)
+    y = oracle.ffn_forward(x, synth.pack_rows_u32(tg), sg, synth.pack_rows_u32(tu), su,
+                           synth.pack_rows_u32(td), sd, gelu=gelu)
+    g = (x.astype(np.float64) @ tg.T.astype(np.float64)) * sg
+    u = (x.astype(np.float64) @ tu.T.astype(np.float64)) * su
+    if gelu:
+        a = 0.5 * g * (1.0 + np.tanh(np.sqrt(2.0 / np.pi) * (g + 0.044715 * g ** 3)))
+    else:
+        a = g / (1.0 + np.exp(-g))
+    ref = ((a * u) @ td.T.astype(np.float64)) * sd
+    assert np.abs(y - ref).max() <= 1e-5 * np.abs(ref).max()
+    other = oracle.ffn_forward(x, synth.pack_rows_u32(tg), sg, synth.pack_rows_u32(tu), su,
+                               synth.pack_rows_u32(td), sd, gelu=not gelu)
+    assert np.abs(other - y).max() > 1e-3 * np.abs(y).max()
