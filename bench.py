@@ -18,8 +18,9 @@ cpu_baseline: the reference's CPU decode path (ternary_matmul_packed_parallel,
 src/model/ternary.rs:471-529, restated in C by the oracle) on the same three
 matrices at B=1, timed on this host's cores.
 
-extra: the decode FFN of the same layer through frx_ternary_ffn (fused
-gate/up/SiLU launch + fp32-input down launch), prefill GEMM (X[2048,4096] x
+extra: the decode FFN of the same layer through frx_ternary_ffn (one launch
+with a grid barrier, and the two-launch execution: gate/up/SiLU launch +
+fp32-input down launch), prefill GEMM (X[2048,4096] x
 W[N,4096], N in {4096, 11008}), 2:4 sparse GEMM and the MoE expert layer, as
 TFLOP/s and fraction of the dense bf16 MFMA peak.
 """
@@ -208,28 +209,38 @@ def main():
         except (OSError, ValueError, KeyError):
             pass
 
-    # The decode FFN of the same layer through frx_ternary_ffn: gate, up and
-    # SiLU in one launch (fp32 product), then the fp32-input down GEMV.
+    # The decode FFN of the same layer through frx_ternary_ffn: one launch
+    # (gate/up/SiLU, grid barrier, down; the default at B <= 3), and the
+    # two-launch execution (gate/up/SiLU launch with fp32 product, then the
+    # fp32-input down GEMV).
     b_glu = 2 * (I * H // 4 + 4 * I) + 2 * B * H + 4 * B * I
     b_down32 = H * I // 4 + 4 * H + 4 * B * I + 2 * B * H
+    b_ffn = 2 * (I * H // 4 + 4 * I) + (H * I // 4 + 4 * H) + 2 * B * H + 2 * B * H
 
     def ffn_step(i):
         wg, wu, wd = W[i % copies]
         ctx.ternary_ffn(x, wg, s_g, wu, s_u, wd, s_d, y)
-    el_f, _ = timed(lambda: [ffn_step(i) for i in range(args.steps)])
+    fused = {"algorithmic_bytes_per_step": b_ffn}
+    for mode, key in ((frx.FFN_AUTO, "default"), (frx.FFN_TWO_LAUNCH, "two_launch")):
+        ctx.set_ffn_mode(mode)
+        el_f, _ = timed(lambda: [ffn_step(i) for i in range(args.steps)])
+        ctx.synchronize()
+        fused[key] = {"us_per_step": round(el_f / args.steps * 1e6, 2),
+                      "gb_s": round(b_ffn / (el_f / args.steps) / 1e9, 1),
+                      "hbm_fraction": round(b_ffn / (el_f / args.steps) / 1e9 / HBM_PEAK_GBS, 4)}
+    ctx.set_ffn_mode(frx.FFN_AUTO)
+    fused["default"]["launches_per_step"] = 1 if B <= 3 else 2
+    fused["two_launch"]["launches_per_step"] = 2
     t_glu = per_launch(lambda i: ctx.ternary_glu(x, W[i][0], s_g, W[i][1], s_u, h), 1, reps)
     t_d32 = per_launch(lambda i: ctx.ternary_linear(W[i][2], s_d, h, y), 1, reps)
-    fused = {"us_per_step": round(el_f / args.steps * 1e6, 2),
-             "gb_s": round((b_glu + b_down32) / (el_f / args.steps) / 1e9, 1),
-             "launches_per_step": 2,
-             "gate_up_silu_avg_us": round(t_glu * 1e6, 3),
-             "gate_up_silu_gb_s": round(b_glu / t_glu / 1e9, 1),
-             "down_f32_in_avg_us": round(t_d32 * 1e6, 3),
-             "down_f32_in_gb_s": round(b_down32 / t_d32 / 1e9, 1),
-             "algorithmic_bytes": {"glu_11008x4096": b_glu, "down_f32_4096x11008": b_down32},
-             "traffic": ffn_traffic}
-    log(f"bench: decode FFN (fused gate/up/SiLU + down): {fused['us_per_step']} us/step; "
-        f"gate/up {fused['gate_up_silu_avg_us']} us, down {fused['down_f32_in_avg_us']} us")
+    fused["two_launch"].update({
+        "gate_up_silu_avg_us": round(t_glu * 1e6, 3), "gate_up_silu_gb_s": round(b_glu / t_glu / 1e9, 1),
+        "down_f32_in_avg_us": round(t_d32 * 1e6, 3), "down_f32_in_gb_s": round(b_down32 / t_d32 / 1e9, 1),
+        "algorithmic_bytes": {"glu_11008x4096": b_glu, "down_f32_4096x11008": b_down32},
+        "traffic": ffn_traffic})
+    log(f"bench: decode FFN: {fused['default']['us_per_step']} us/step "
+        f"({fused['default']['launches_per_step']} launch), two-launch {fused['two_launch']['us_per_step']} us; "
+        f"gate/up {fused['two_launch']['gate_up_silu_avg_us']} us, down {fused['two_launch']['down_f32_in_avg_us']} us")
 
     extra = {"decode_ffn_fused_llama7b": fused}
     if not args.no_extra:

@@ -19,6 +19,7 @@ LIB_PATH = os.path.join(HERE, "libfrx_ternary.so")
 
 FRX_F32, FRX_BF16 = 0, 1
 ACT_SILU, ACT_GELU_TANH = 0, 1
+FFN_AUTO, FFN_ONE_LAUNCH, FFN_TWO_LAUNCH = 0, 1, 2
 
 _STATUS = {
     0: "Ok", 1: "Gpu", 2: "Shape", 3: "Device", 4: "Shader", 5: "OOM", 6: "Unsupported",
@@ -59,6 +60,7 @@ _SIGS = {
     "frx_ternary_glu": (_int, [_vp, _vp, _int, _vp, _vp, _vp, _vp, _u32, _u32, _u32, _int, _vp]),
     "frx_ternary_ffn": (_int, [_vp, _vp, _int, _vp, _vp, _vp, _vp, _vp, _vp, _u32, _u32, _u32,
                                _int, _vp, _int]),
+    "frx_set_ffn_mode": (_int, [_vp, _int]),
     "frx_pack_ternary_u8": (_int, [_vp, _sz, _vp]),
     "frx_unpack_ternary_u8": (_int, [_vp, _sz, _vp]),
     "frx_repack_u8_to_u32": (_int, [_vp, _sz, _vp]),
@@ -250,6 +252,10 @@ class Context:
                                      _ptr(w_up), _ptr(s_up), _ptr(w_down), _ptr(s_down), M, H, I,
                                      act, _ptr(y), _dtype_code(y)), self._h)
         return y
+
+    def set_ffn_mode(self, mode: int):
+        """frx_set_ffn_mode: FFN_AUTO, FFN_ONE_LAUNCH or FFN_TWO_LAUNCH."""
+        _check(lib().frx_set_ffn_mode(self._h, mode), self._h)
 
     # GpuMatmulAccelerator analogues: host numpy in, host numpy out.
     def gpu_ternary_matmul(self, packed_weights: np.ndarray, scales: np.ndarray,

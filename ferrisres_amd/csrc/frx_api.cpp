@@ -34,6 +34,9 @@ struct frx_ctx {
   size_t ffn_ws_bytes = 0;
   void *glu_ws = nullptr;  // up projection of the GEMM-path GLU (fp32)
   size_t glu_ws_bytes = 0;
+  unsigned *ffn_bar = nullptr;  // grid-barrier words of the one-launch FFN
+  int ffn_mode = FRX_FFN_AUTO;
+  int cus = 0;  // compute units of the device
 };
 
 static frx_status fail(frx_ctx *ctx, frx_status st, const char *fmt, ...) {
@@ -92,6 +95,7 @@ frx_status frx_create(int device, frx_ctx **out) {
   if (strncmp(prop.gcnArchName, "gfx950", 6) != 0) return FRX_ERR_UNSUPPORTED;
   frx_ctx *c = new frx_ctx();
   c->device = device;
+  c->cus = prop.multiProcessorCount;
   *out = c;
   return FRX_OK;
 }
@@ -103,6 +107,7 @@ void frx_destroy(frx_ctx *ctx) {
   if (ctx->moe_ws) hipFree(ctx->moe_ws);
   if (ctx->ffn_ws) hipFree(ctx->ffn_ws);
   if (ctx->glu_ws) hipFree(ctx->glu_ws);
+  if (ctx->ffn_bar) hipFree(ctx->ffn_bar);
   delete ctx;
 }
 
@@ -117,6 +122,30 @@ frx_status frx_synchronize(frx_ctx *ctx) {
   if (st != FRX_OK) return st;
   hipError_t e = hipStreamSynchronize(ctx->stream);
   if (e != hipSuccess) return hip_fail(ctx, e, "hipStreamSynchronize");
+  if (ctx->ffn_bar) {
+    // A one-launch FFN whose grid barrier timed out (its workgroups were not
+    // all resident at once) raised the error word: report it and reset the
+    // barrier words for the next launch.
+    unsigned err = 0;
+    e = hipMemcpy(&err, ctx->ffn_bar + frx::ffn1_error_word(), sizeof(err), hipMemcpyDeviceToHost);
+    if (e != hipSuccess) return hip_fail(ctx, e, "FFN barrier state read");
+    if (err) {
+      e = hipMemset(ctx->ffn_bar, 0, frx::ffn1_barrier_bytes());
+      if (e != hipSuccess) return hip_fail(ctx, e, "FFN barrier reset");
+      return fail(ctx, FRX_ERR_GPU,
+                  "one-launch FFN: grid barrier timed out (workgroups not co-resident); "
+                  "outputs of FFN calls since the last synchronize are invalid");
+    }
+  }
+  return FRX_OK;
+}
+
+frx_status frx_set_ffn_mode(frx_ctx *ctx, frx_ffn_mode mode) {
+  if (!ctx) return FRX_ERR_DEVICE;
+  ctx->err[0] = 0;
+  if (mode != FRX_FFN_AUTO && mode != FRX_FFN_ONE_LAUNCH && mode != FRX_FFN_TWO_LAUNCH)
+    return fail(ctx, FRX_ERR_UNSUPPORTED, "unknown FFN mode %d", (int)mode);
+  ctx->ffn_mode = mode;
   return FRX_OK;
 }
 
@@ -293,10 +322,38 @@ frx_status frx_ternary_ffn(frx_ctx *ctx, const void *x, frx_dtype xt, const uint
   if ((st = ensure_buffer(ctx, &ctx->ffn_ws, &ctx->ffn_ws_bytes, a256((size_t)M * I * 4),
                           "FFN workspace allocation")) != FRX_OK)
     return st;
+  hipError_t e;
+  int grid = 0;
+  size_t lds = 0;
+  const bool one = ctx->ffn_mode != FRX_FFN_TWO_LAUNCH && aligned16(w_gate) && aligned16(w_up) &&
+                   aligned16(w_down) &&
+                   frx::ffn1_supported((int)M, (int)H, (int)I, xt == FRX_BF16, ctx->cus, &grid, &lds);
+  if (ctx->ffn_mode == FRX_FFN_ONE_LAUNCH && !one)
+    return fail(ctx, FRX_ERR_UNSUPPORTED,
+                "one-launch FFN: unsupported shape M=%u H=%u I=%u (M <= 3, H <= 4096, I <= 11520, "
+                "multiples of 64, 16-byte aligned weights)", M, H, I);
+  if (one) {
+    if (!ctx->ffn_bar) {
+      void *p = nullptr;
+      e = hipMalloc(&p, frx::ffn1_barrier_bytes());
+      if (e != hipSuccess) return hip_fail(ctx, e, "FFN barrier allocation");
+      e = hipMemset(p, 0, frx::ffn1_barrier_bytes());
+      if (e != hipSuccess) {
+        hipFree(p);
+        return hip_fail(ctx, e, "FFN barrier initialisation");
+      }
+      ctx->ffn_bar = reinterpret_cast<unsigned *>(p);
+    }
+    static_assert(sizeof(float) == 4, "h planes");
+    e = frx::launch_ffn1(x, xt == FRX_BF16, w_gate, s_gate, w_up, s_up, w_down, s_down,
+                         reinterpret_cast<uint32_t *>(ctx->ffn_ws), y, yt == FRX_BF16, ctx->ffn_bar, (int)M,
+                         (int)H, (int)I, act == FRX_ACT_GELU_TANH, grid, lds, ctx->stream);
+    if (e != hipSuccess) return hip_fail(ctx, e, "one-launch FFN");
+    return FRX_OK;
+  }
   float *h = reinterpret_cast<float *>(ctx->ffn_ws);
   if ((st = glu_into(ctx, x, xt, w_gate, s_gate, w_up, s_up, M, H, I, act == FRX_ACT_GELU_TANH, h)) != FRX_OK)
     return st;
-  hipError_t e;
   if (M <= 16)
     e = frx::launch_gemv(w_down, s_down, h, 0, y, yt == FRX_BF16, (int)M, (int)I, (int)H, ctx->stream);
   else

@@ -107,6 +107,23 @@ struct XBlock;
 template <>
 struct XBlock<uint16_t> {
   static constexpr int P = 1;
+  static constexpr int NV = 2;  // 16-byte loads per block
+  // Unconditional raw load of a block (src must be a valid block address);
+  // finish() turns it into the staged dwords, zero when !ok. Split so that a
+  // kernel can issue further loads before it consumes these.
+  __device__ __forceinline__ static void load_raw(const uint16_t *src, u32x4 v[NV]) {
+    const u32x4 *s = reinterpret_cast<const u32x4 *>(src);
+    v[0] = s[0];
+    v[1] = s[1];
+  }
+  __device__ __forceinline__ static void finish(const u32x4 v[NV], bool ok, uint32_t hi[8],
+                                                uint32_t lo[8]) {
+    (void)lo;
+    const uint32_t m = ok ? 0xFFFFFFFFu : 0u;
+    uint32_t n[8] = {v[0].x & m, v[0].y & m, v[0].z & m, v[0].w & m,
+                     v[1].x & m, v[1].y & m, v[1].z & m, v[1].w & m};
+    interleave16(n, hi);
+  }
   __device__ __forceinline__ static void load(const uint16_t *src,
                                               bool ok, uint32_t hi[8],
                                               uint32_t lo[8]) {
@@ -128,6 +145,28 @@ struct XBlock<uint16_t> {
 template <>
 struct XBlock<float> {
   static constexpr int P = 2;
+  static constexpr int NV = 4;
+  __device__ __forceinline__ static void load_raw(const float *src, u32x4 v[NV]) {
+    const u32x4 *s = reinterpret_cast<const u32x4 *>(src);
+#pragma unroll
+    for (int q = 0; q < 4; q++) v[q] = s[q];
+  }
+  __device__ __forceinline__ static void finish(const u32x4 v[NV], bool ok, uint32_t hi[8],
+                                                uint32_t lo[8]) {
+    uint32_t h[16], l[16];
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+      const float f[4] = {__uint_as_float(v[q].x), __uint_as_float(v[q].y), __uint_as_float(v[q].z),
+                          __uint_as_float(v[q].w)};
+#pragma unroll
+      for (int e = 0; e < 4; e++) split_bf16(ok ? f[e] : 0.0f, h[4 * q + e], l[4 * q + e]);
+    }
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      hi[i] = h[i] | (h[i + 8] << 16);
+      lo[i] = l[i] | (l[i + 8] << 16);
+    }
+  }
   __device__ __forceinline__ static void load(const float *src, bool ok,
                                               uint32_t hi[8], uint32_t lo[8]) {
     uint32_t h[16], l[16];

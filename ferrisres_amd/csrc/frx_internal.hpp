@@ -42,6 +42,20 @@ hipError_t launch_gemm(const uint32_t *w, const float *scale, const void *x,
                        int xt_bf16, void *y, int yt_bf16, int M, int K, int N,
                        int sp24, hipStream_t stream);
 
+// One-launch decode FFN, M <= 3 tokens (frx_ffn.hip). ffn1_supported says
+// whether the shape fits the kernel on a device with `cus` compute units and
+// returns its grid and dynamic LDS. hs: ffn1_h_bytes(B, I) of device memory
+// for h; bar: ffn1_barrier_bytes() of zero-initialised device memory owned
+// by the caller (one per stream of launches).
+bool ffn1_supported(int B, int H, int I, int xt_bf16, int cus, int *grid, size_t *lds);
+size_t ffn1_h_bytes(int B, int I);
+size_t ffn1_barrier_bytes();
+size_t ffn1_error_word();
+hipError_t launch_ffn1(const void *x, int xt_bf16, const uint32_t *wg, const float *sg, const uint32_t *wu,
+                       const float *su, const uint32_t *wd, const float *sd, uint32_t *hs, void *y,
+                       int yt_bf16, unsigned *bar, int B, int H, int I, int gelu, int G, size_t lds,
+                       hipStream_t stream);
+
 // MoE pipeline (frx_moe.hip).
 struct MoeWorkspace {
   uint32_t *idx;       // [T*k] selected experts (sorted order per token)

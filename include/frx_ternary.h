@@ -46,6 +46,12 @@ typedef enum frx_status {
 typedef enum frx_dtype { FRX_F32 = 0, FRX_BF16 = 1 } frx_dtype;
 
 typedef enum frx_activation { FRX_ACT_SILU = 0, FRX_ACT_GELU_TANH = 1 } frx_activation;
+/* How frx_ternary_ffn runs at decode sizes (see frx_set_ffn_mode). */
+typedef enum frx_ffn_mode {
+  FRX_FFN_AUTO = 0,        /* one launch where the shape allows, else two */
+  FRX_FFN_ONE_LAUNCH = 1,  /* one launch or FRX_ERR_UNSUPPORTED */
+  FRX_FFN_TWO_LAUNCH = 2   /* gate/up/act launch + down launch */
+} frx_ffn_mode;
 
 /* ---- context -------------------------------------------------------------
  * Replaces the Arc<Device>/Arc<Queue> pair ops are built from
@@ -56,7 +62,9 @@ void frx_destroy(frx_ctx *ctx);
 /* Caller-owned hipStream_t (NULL = the device's null stream); the analogue of
  * the caller-owned CommandEncoder in TernaryMatMulOp::dispatch. */
 frx_status frx_set_stream(frx_ctx *ctx, void *hip_stream);
-/* Waits for all work enqueued on the context's stream. */
+/* Waits for all work enqueued on the context's stream. Returns FRX_ERR_GPU
+ * if a one-launch FFN since the last call timed out at its grid barrier
+ * (see frx_ternary_ffn). */
 frx_status frx_synchronize(frx_ctx *ctx);
 /* Message of the last failed call on this context ("" if none). */
 const char *frx_last_error(const frx_ctx *ctx);
@@ -138,13 +146,25 @@ frx_status frx_ternary_glu(frx_ctx *ctx, const void *x, frx_dtype xt,
  * as in the reference: frx_ternary_glu into the workspace, then the down
  * projection with fp32 input (M <= 16: two launches). Requires H % 16 == 0,
  * I % 16 == 0. The workspace is allocated on the context on first use (and
- * grown), so a first call at a new size must not be under graph capture. */
+ * grown), so a first call at a new size must not be under graph capture.
+ * Decode sizes (M <= 3, H <= 4096, I <= 11520, H and I multiples of 64,
+ * 16-byte aligned weights; LLaMA-7B's 4096/11008 included) run the whole FFN
+ * as ONE launch with a grid barrier between the halves (FRX_FFN_AUTO). That
+ * launch needs all its workgroups (one per CU) resident at once; if another
+ * kernel holds CUs so that they are not, its barrier times out, the outputs
+ * are invalid and the next frx_synchronize returns FRX_ERR_GPU. Callers that
+ * share the GPU with concurrent kernels select FRX_FFN_TWO_LAUNCH. */
 frx_status frx_ternary_ffn(frx_ctx *ctx, const void *x, frx_dtype xt,
                            const uint32_t *w_gate, const float *s_gate,
                            const uint32_t *w_up, const float *s_up,
                            const uint32_t *w_down, const float *s_down,
                            uint32_t M, uint32_t H, uint32_t I,
                            frx_activation act, void *y, frx_dtype yt);
+
+/* Selects the execution of frx_ternary_ffn on this context (default
+ * FRX_FFN_AUTO). No counterpart in the reference, whose FFN is three
+ * separate matmul calls. */
+frx_status frx_set_ffn_mode(frx_ctx *ctx, frx_ffn_mode mode);
 
 /* ---- host-side packers (no GPU) --------------------------------------------*/
 /* pack_ternary (src/model/ternary.rs:146-163): out has (n+3)/4 bytes. */

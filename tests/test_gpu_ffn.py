@@ -122,3 +122,116 @@ def test_ffn_shape_errors(ctx):
     with pytest.raises(frx.FrxError) as ei:
         ctx.ternary_ffn(x, d["gate"][0], d["gate"][1], d["up"][0], d["up"][1], d["down"][0], d["down"][1], y)
     assert ei.value.kind == "Shape"
+
+
+# ---- one-launch decode FFN (M <= 3) -------------------------------------------
+
+@pytest.fixture
+def one_launch(ctx):
+    ctx.set_ffn_mode(frx.FFN_ONE_LAUNCH)  # fails the call instead of falling back
+    yield ctx
+    ctx.set_ffn_mode(frx.FFN_AUTO)
+
+
+@pytest.mark.parametrize("M", [1, 2, 3])
+@pytest.mark.parametrize("act", [frx.ACT_SILU, frx.ACT_GELU_TANH])
+def test_ffn_one_launch_llama7b(one_launch, M, act):
+    ctx = one_launch
+    xf, xb, mats = make_ffn(f"ffn1/dec{M}", M, 4096, 11008)
+    xw = synth.bf16_bits_to_f32(xb)
+    ref = ref_ffn(xw, mats, act == frx.ACT_GELU_TANH)
+    y = run_ffn(ctx, xf, xb, mats, act)
+    ctx.synchronize()  # raises if the grid barrier timed out
+    assert_close_f32(host(y), ref)
+    yb = run_ffn(ctx, xf, xb, mats, act, yt="bf16")
+    ctx.synchronize()
+    assert_bf16_within_1ulp(yb.view(torch.int16).cpu().numpy().view(np.uint16), ref)
+
+
+@pytest.mark.parametrize("M,H,I", [(1, 64, 64), (2, 128, 192), (3, 256, 320), (1, 4096, 64),
+                                   (3, 64, 11008), (2, 1024, 2816), (1, 2048, 5632), (3, 4032, 11520)])
+def test_ffn_one_launch_shapes(one_launch, M, H, I):
+    ctx = one_launch
+    xf, xb, mats = make_ffn(f"ffn1/s{M}_{H}_{I}", M, H, I)
+    xw = synth.bf16_bits_to_f32(xb)
+    y = run_ffn(ctx, xf, xb, mats, frx.ACT_SILU)
+    ctx.synchronize()
+    assert_close_f32(host(y), ref_ffn(xw, mats, False))
+
+
+@pytest.mark.parametrize("M", [1, 3])
+def test_ffn_one_launch_f32_in(one_launch, M):
+    ctx = one_launch
+    xf, xb, mats = make_ffn(f"ffn1/f32_{M}", M, 512, 1344)
+    y = run_ffn(ctx, xf, xb, mats, frx.ACT_GELU_TANH, xt="f32", yt="f32")
+    ctx.synchronize()
+    assert_close_f32(host(y), ref_ffn(xf, mats, True))
+
+
+def test_ffn_one_launch_matches_two_launch(ctx):
+    """Both executions of the decode FFN agree (different summation orders,
+    so within fp32 rounding, not bit for bit)."""
+    xf, xb, mats = make_ffn("ffn1/both", 2, 4096, 11008)
+    ctx.set_ffn_mode(frx.FFN_TWO_LAUNCH)
+    try:
+        y2 = run_ffn(ctx, xf, xb, mats, frx.ACT_SILU)
+    finally:
+        ctx.set_ffn_mode(frx.FFN_AUTO)
+    y1 = run_ffn(ctx, xf, xb, mats, frx.ACT_SILU)  # AUTO takes the one-launch path here
+    ctx.synchronize()
+    a, b = host(y1), host(y2)
+    assert np.max(np.abs(a - b)) <= 1e-4 * max(1e-30, float(np.sqrt(np.mean(b.astype(np.float64) ** 2))))
+
+
+def test_ffn_one_launch_repeat_and_graph(one_launch):
+    """Back-to-back launches (the barrier epoch advances every launch) and
+    replays of a captured launch, each checked, with eager work between."""
+    ctx = one_launch
+    M, H, I = 1, 1024, 2816
+    cases = [make_ffn(f"ffn1/rep{i}", M, H, I) for i in range(3)]
+    refs = [ref_ffn(synth.bf16_bits_to_f32(xb), mats, False) for _, xb, mats in cases]
+    dev = [({k: (dev_u32(v[0]), dev_f32(v[1])) for k, v in mats.items()}, dev_bf16(xb)) for _, xb, mats in cases]
+    ys = [torch.empty((M, H), dtype=torch.float32, device=DEV) for _ in cases]
+
+    def call(i):
+        d, x = dev[i]
+        ctx.ternary_ffn(x, d["gate"][0], d["gate"][1], d["up"][0], d["up"][1], d["down"][0], d["down"][1], ys[i])
+
+    for rep in range(40):
+        call(rep % 3)
+    ctx.synchronize()
+    for i in range(3):
+        assert_close_f32(host(ys[i]), refs[i])
+
+    s = torch.cuda.Stream()
+    ctx.set_stream(s)
+    try:
+        with torch.cuda.stream(s):
+            call(0)  # workspace and barrier words exist before capture
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=s):
+            call(1)
+        torch.cuda.synchronize()
+        for rep in range(4):
+            ys[1].fill_(float("nan"))
+            with torch.cuda.stream(s):
+                g.replay()
+                call(2)  # an eager launch between replays
+            torch.cuda.synchronize()
+            ctx.synchronize()
+            assert_close_f32(host(ys[1]), refs[1])
+            assert_close_f32(host(ys[2]), refs[2])
+    finally:
+        ctx.set_stream(None)
+
+
+def test_ffn_one_launch_unsupported(one_launch):
+    ctx = one_launch
+    xf, xb, mats = make_ffn("ffn1/unsup", 4, 128, 192)  # M = 4 > 3
+    d = {k: (dev_u32(v[0]), dev_f32(v[1])) for k, v in mats.items()}
+    y = torch.empty((4, 128), dtype=torch.float32, device=DEV)
+    with pytest.raises(frx.FrxError) as ei:
+        ctx.ternary_ffn(dev_bf16(xb), d["gate"][0], d["gate"][1], d["up"][0], d["up"][1], d["down"][0],
+                        d["down"][1], y)
+    assert ei.value.kind == "Unsupported"
