@@ -74,6 +74,25 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm2_kernel(
   Core::template store_tile<YT>(lds, acc, scale, Y, (size_t)N, m0, m_count, n0, n_count);
 }
 
+// 2:4 weights (GPU 5-bit layout), bf16 activations, K % 64 == 0: the
+// pipelined engine on the sparse matrix pipe.
+template <int BM, int BN, int WM, int WN, int NS, typename YT>
+__global__ __launch_bounds__(WM *WN * 64) void gemm2sp_kernel(
+    const uint32_t *__restrict__ meta, const float *__restrict__ scale,
+    const uint16_t *__restrict__ X, YT *__restrict__ Y, int M, int K, int N) {
+  using Core = Gemm2<BM, BN, WM, WN, NS, false>;
+  extern __shared__ __align__(16) uint32_t lds[];
+  int nt, mt;
+  xcd_tile(nt, mt);
+  const int n0 = nt * BN, m0 = mt * BM;
+  const int wpr = ((K >> 2) + 5) / 6;
+  f32x4 acc[Core::FN][Core::FM];
+  const int m_count = min(BM, M - m0), n_count = min(BN, N - n0);
+  Core::run_sp(lds, X + (size_t)m0 * K, (uint32_t)m_count * (uint32_t)K * 2u, m_count,
+               meta + (size_t)n0 * wpr, n_count, K, wpr, acc);
+  Core::template store_tile<YT>(lds, acc, scale, Y, (size_t)N, m0, m_count, n0, n_count);
+}
+
 #ifndef FRX_GEMM2_NS
 #define FRX_GEMM2_NS 3
 #endif
@@ -90,6 +109,22 @@ static hipError_t launch_gemm2_t(const uint32_t *w, const float *scale, const vo
   if (e != hipSuccess) return e;
   dim3 grid((N + BN - 1) / BN, (M + BM - 1) / BM);
   hipLaunchKernelGGL((gemm2_kernel<BM, BN, WM, WN, NS, YT>), grid, dim3(WM * WN * 64), lds, stream, w,
+                     scale, reinterpret_cast<const uint16_t *>(x), reinterpret_cast<YT *>(y), M, K, N);
+  return hipGetLastError();
+}
+
+template <typename YT>
+static hipError_t launch_gemm2sp_t(const uint32_t *meta, const float *scale, const void *x, void *y,
+                                   int M, int K, int N, hipStream_t stream) {
+  constexpr int BM = 128, BN = 256, WM = 1, WN = 4, NS = FRX_GEMM2_NS;
+  using Core = Gemm2<BM, BN, WM, WN, NS, false>;
+  constexpr int lds = Core::LDS_DWORDS * 4;
+  static std::atomic<uint64_t> done;
+  const hipError_t e =
+      opt_in_lds(reinterpret_cast<const void *>(&gemm2sp_kernel<BM, BN, WM, WN, NS, YT>), lds, done);
+  if (e != hipSuccess) return e;
+  dim3 grid((N + BN - 1) / BN, (M + BM - 1) / BM);
+  hipLaunchKernelGGL((gemm2sp_kernel<BM, BN, WM, WN, NS, YT>), grid, dim3(WM * WN * 64), lds, stream, meta,
                      scale, reinterpret_cast<const uint16_t *>(x), reinterpret_cast<YT *>(y), M, K, N);
   return hipGetLastError();
 }
@@ -126,6 +161,10 @@ hipError_t launch_gemm(const uint32_t *w, const float *scale, const void *x,
   if (!sp24 && xt_bf16 && K % 64 == 0 && M > 16 && (reinterpret_cast<uintptr_t>(w) & 15) == 0) {
     if (yt_bf16) return launch_gemm2_t<uint16_t>(w, scale, x, y, M, K, N, stream);
     return launch_gemm2_t<float>(w, scale, x, y, M, K, N, stream);
+  }
+  if (sp24 && xt_bf16 && K % 64 == 0 && M > 16) {
+    if (yt_bf16) return launch_gemm2sp_t<uint16_t>(w, scale, x, y, M, K, N, stream);
+    return launch_gemm2sp_t<float>(w, scale, x, y, M, K, N, stream);
   }
   if (sp24) return launch_gemm_wf<WF_SP24>(w, scale, x, xt_bf16, y, yt_bf16, M, K, N, stream);
   return launch_gemm_wf<WF_DENSE>(w, scale, x, xt_bf16, y, yt_bf16, M, K, N, stream);

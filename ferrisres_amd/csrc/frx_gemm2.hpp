@@ -74,6 +74,43 @@ __device__ __forceinline__ void mfma_drain() {
   asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
 }
 
+typedef uint32_t u32x8 __attribute__((ext_vector_type(8)));
+
+// acc += A * B on the 2:4 sparse matrix pipe (twice the dense rate), tied
+// like mfma16_acc. A (16 weight rows x 64 columns, two nonzeros per group
+// of 4) arrives compressed: lane (i = l%16, kg = l/16) holds row i's values
+// for groups 4 kg .. 4 kg + 3 as 8 bf16 (two per group, lower position
+// first) and, in bits 2s+1:2s of idx, the position (0..3) inside its group
+// of compressed value s. B is 16 bf16 per lane: columns 8 kg .. 8 kg + 7 and
+// 32 + 8 kg .. 32 + 8 kg + 7 of the step for token l%16, i.e. the dense
+// engine's two X operands of the step.
+__device__ __forceinline__ void smfmac16_acc(f32x4 &acc, const u32x4 &a, const u32x8 &b, uint32_t idx) {
+  asm("v_smfmac_f32_16x16x64_bf16 %0, %1, %2, %3" : "+a"(acc) : "v"(a), "v"(b), "v"(idx));
+}
+
+// Four 2:4 groups in the GPU 5-bit layout (bits 2:0 pattern, pattern > 5
+// read as 5; bit 3 / bit 4 set: the lower / higher nonzero is -1;
+// src/compute/kernels/sparse_ternary.rs:87-107) as a compressed smfmac A
+// operand. F holds the groups at bits 5q. Values are +-2 (bf16 0x4000 /
+// 0xC000, the 2*dec encoding of the dense path); the position nibble of a
+// pattern is p0 | p1 << 2, looked up in a constant (pattern p at bits 4p:
+// (0,1) (0,2) (0,3) (1,2) (1,3) (2,3), then 5 twice).
+__device__ __forceinline__ void sp24_operand(uint32_t F, u32x4 &a, uint32_t &idx) {
+  uint32_t ix = 0;
+#pragma unroll
+  for (int q = 0; q < 4; q++) {
+    const uint32_t c = __builtin_amdgcn_ubfe(F, 5 * q, 5);
+    ix |= __builtin_amdgcn_ubfe(0xEEED9C84u, c << 2, 4) << (4 * q);
+    a[q] = (((c << 12) | (c << 27)) & 0x80008000u) | 0x40004000u;
+  }
+  idx = ix;
+}
+
+__device__ __forceinline__ void lds_load4(__amdgpu_buffer_rsrc_t r, uint32_t *ldst,
+                                          uint32_t voffset, uint32_t soffset) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_ptr_t)ldst, 4, voffset, soffset, 0, 0);
+}
+
 __device__ __forceinline__ void lds_load16(__amdgpu_buffer_rsrc_t r, uint32_t *ldst,
                                            uint32_t voffset, uint32_t soffset) {
   __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_ptr_t)ldst, 16, voffset, soffset, 0, 0);
@@ -294,6 +331,155 @@ struct Gemm2 {
     mfma_drain();
     // every load has landed and every read is done before the epilogue
     // reuses the ring
+    wait_vmcnt<0>();
+    barrier_nofence();
+  }
+
+  // ---- 2:4 sparse weights (GPU 5-bit layout, wpr words per row) ------------
+  // A step's 16 groups per row lie in the 4-word window that starts at word
+  // floor(16 s / 6) of the row (6 groups per word). Rows are only 4-byte
+  // aligned, so the window moves with 4-byte LDS DMA: lane l of a 256-byte
+  // instruction loads word l % 4 of row l / 4, which keeps the dense W-stage
+  // layout (rows of 4 words).
+  static constexpr int SWI = BN * 4 / 64;
+  static_assert(SWI % WAVES == 0, "sparse W loads must split evenly over the waves");
+  static constexpr int SWPW = SWI / WAVES;
+  static constexpr int SLPW = XPW + SWPW;
+
+  __device__ __forceinline__ static uint32_t sp_window_bytes(int s) { return 4u * (uint32_t)((16 * s) / 6); }
+
+  __device__ __forceinline__ static void issue_sp(uint32_t *stage, __amdgpu_buffer_rsrc_t xr,
+                                                  __amdgpu_buffer_rsrc_t wr, const uint32_t (&xv)[XPW],
+                                                  const uint32_t (&wv)[SWPW], int s) {
+    const int wave = threadIdx.x >> 6;
+#pragma unroll
+    for (int i = 0; i < XPW; i++) lds_load16(xr, stage + (wave * XPW + i) * 256, xv[i], 128u * (uint32_t)s);
+#pragma unroll
+    for (int i = 0; i < SWPW; i++)
+      lds_load4(wr, stage + XSTAGE + (wave * SWPW + i) * 64, wv[i], sp_window_bytes(s));
+  }
+
+  // The A operands of fragment rows wn*TN + fn*16 + l16 for step s from the
+  // W stage at ws (lane kg = g takes groups 16 s + 4 g .. + 3).
+  __device__ __forceinline__ static void sp_read(const uint32_t *ws, int s, int wrow, int g,
+                                                 uint32_t (&wa)[FN], uint32_t (&wb)[FN], int &o5) {
+    const int l0 = (4 * s) % 6 + 4 * g;  // first group, relative to the window
+    const int jw = l0 / 6;
+    o5 = 5 * (l0 - 6 * jw);
+#pragma unroll
+    for (int fn = 0; fn < FN; fn++) {
+      wa[fn] = ws[(wrow + fn * 16) * 4 + jw];
+      wb[fn] = ws[(wrow + fn * 16) * 4 + jw + 1];
+    }
+  }
+  __device__ __forceinline__ static void sp_decode(uint32_t wa, uint32_t wb, int o5, u32x4 &a, uint32_t &idx) {
+    const uint32_t F = (((wa & 0x3FFFFFFFu) >> o5) | (wb << (30 - o5))) & 0xFFFFFu;
+    sp24_operand(F, a, idx);
+  }
+
+  // B operand of token block fm in a stage: both 32-column halves.
+  __device__ __forceinline__ static u32x8 xop_sp(const uint32_t *stage, int r0, int g, int fm) {
+    const u32x4 lo = xop(stage, r0, g, fm), hi = xop(stage, r0, g, FM + fm);
+    return (u32x8){lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+  }
+
+  static constexpr int XDS = 2;  // sparse: B operands read this many token blocks ahead
+
+  // The 2:4 K loop: the schedule of run() with one sparse MFMA per
+  // (row block, token block) and step; the first half of a step covers token
+  // blocks 0 .. FM/2-1, the second half the rest plus the next stage's loads,
+  // window reads and operand decode. Requires K % 64 == 0.
+  __device__ static void run_sp(uint32_t *lds, const uint16_t *X, uint32_t xbytes, int m_count,
+                                const uint32_t *W, int n_count, int K, int wpr, f32x4 (&acc)[FN][FM]) {
+    static_assert(NS >= 3 && FM % 2 == 0 && FM / 2 >= XDS && FN <= FM / 2 + 1, "sparse schedule");
+    uint32_t xv[XPW], wv[SWPW];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+#pragma unroll
+    for (int i = 0; i < XPW; i++) {
+      const int r = (wave * XPW + i) * 8 + (lane >> 3);
+      const int rm = min(r, m_count - 1);
+      const uint32_t c = (lane & 7) ^ ((r >> 1) & 7);
+      xv[i] = (uint32_t)rm * (uint32_t)K * 2u + 16u * c;
+    }
+#pragma unroll
+    for (int i = 0; i < SWPW; i++) {
+      const int n = min((wave * SWPW + i) * 16 + (lane >> 2), n_count - 1);
+      wv[i] = ((uint32_t)n * (uint32_t)wpr + (uint32_t)(lane & 3)) * 4u;
+    }
+    const __amdgpu_buffer_rsrc_t xr = buffer_rsrc(X, xbytes);
+    const __amdgpu_buffer_rsrc_t wr = buffer_rsrc(W, (uint32_t)n_count * (uint32_t)wpr * 4u);
+#pragma unroll
+    for (int fn = 0; fn < FN; fn++)
+#pragma unroll
+      for (int fm = 0; fm < FM; fm++) acc[fn][fm] = (f32x4){0.f, 0.f, 0.f, 0.f};
+    const int wm = wave % WM, wn = wave / WM;
+    const int l16 = lane & 15, g = lane >> 4;
+    const int r0 = wm * TM + l16;
+    const int wrow = wn * TN + l16;
+    const int nks = (K + 63) >> 6;
+
+#pragma unroll
+    for (int s = 0; s < NS - 1; s++) issue_sp(lds + s * STAGE, xr, wr, xv, wv, min(s, nks - 1));
+    wait_vmcnt<(NS - 2) * SLPW>();
+    barrier_nofence();
+
+    u32x4 a[FN];
+    uint32_t ix[FN];
+    u32x8 bn[XDS];
+    {
+      uint32_t wa[FN], wb[FN];
+      int o5;
+      sp_read(lds + XSTAGE, 0, wrow, g, wa, wb, o5);
+#pragma unroll
+      for (int d = 0; d < XDS; d++) bn[d] = xop_sp(lds, r0, g, d);
+#pragma unroll
+      for (int fn = 0; fn < FN; fn++) sp_decode(wa[fn], wb[fn], o5, a[fn], ix[fn]);
+    }
+
+    for (int t = 0; t < nks; t++) {
+      const uint32_t *cur = lds + (t % NS) * STAGE;
+      const uint32_t *nxt = lds + ((t + 1) % NS) * STAGE;
+      u32x8 b[FM];
+#pragma unroll
+      for (int d = 0; d < XDS; d++) b[d] = bn[d];
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int fm = 0; fm < FM / 2; fm++) {
+        b[fm + XDS] = xop_sp(cur, r0, g, fm + XDS);
+#pragma unroll
+        for (int fn = 0; fn < FN; fn++) smfmac16_acc(acc[fn][fm], a[fn], b[fm], ix[fn]);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      wait_vmcnt<(NS - 3) * SLPW>();
+      barrier_nofence();
+      __builtin_amdgcn_sched_barrier(0);
+      uint32_t wa[FN], wb[FN];
+      int o5 = 0;
+      u32x4 an[FN];
+      uint32_t ixn[FN];
+#pragma unroll
+      for (int fm = FM / 2; fm < FM; fm++) {
+        if (fm + XDS < FM) b[fm + XDS] = xop_sp(cur, r0, g, fm + XDS);
+        else bn[fm + XDS - FM] = xop_sp(nxt, r0, g, fm + XDS - FM);
+        if (fm == FM / 2) sp_read(nxt + XSTAGE, t + 1, wrow, g, wa, wb, o5);
+#pragma unroll
+        for (int fn = 0; fn < FN; fn++) smfmac16_acc(acc[fn][fm], a[fn], b[fm], ix[fn]);
+        if (fm == FM / 2) issue_sp(lds + ((t + NS - 1) % NS) * STAGE, xr, wr, xv, wv, min(t + NS - 1, nks - 1));
+        if (fm > FM / 2 && fm - FM / 2 - 1 < FN) {
+          const int fn = fm - FM / 2 - 1;
+          sp_decode(wa[fn], wb[fn], o5, an[fn], ixn[fn]);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
+#pragma unroll
+      for (int fn = FM / 2 - 1; fn < FN; fn++) sp_decode(wa[fn], wb[fn], o5, an[fn], ixn[fn]);
+#pragma unroll
+      for (int fn = 0; fn < FN; fn++) {
+        a[fn] = an[fn];
+        ix[fn] = ixn[fn];
+      }
+    }
+    mfma_drain();
     wait_vmcnt<0>();
     barrier_nofence();
   }

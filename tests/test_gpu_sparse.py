@@ -84,3 +84,36 @@ def test_cpu_layout_through_transcoder(ctx):
     s = np.full(rows, 0.03, np.float32)
     ref = oracle.sparse24_cpu_matmul(p, sg, 0.03, rows, cols, x, 8).reshape(8, rows)
     assert_close_f32(host(_run(ctx, meta, s, x, None, "f32", "f32")), ref)
+
+
+def test_sparse_raw_metadata_patterns_6_7(ctx):
+    """Raw metadata words: every 5-bit code including patterns 6 and 7
+    (read as 5 by the reference) and set bits 30-31 (not part of any
+    group). The prefill path (bf16, K % 64 == 0) against the oracle."""
+    M, K, N = 64, 512, 256
+    rng = np.random.default_rng(67)
+    wpr = (K // 4 + 5) // 6
+    meta = rng.integers(0, 2**32, size=(N, wpr), dtype=np.uint64).astype(np.uint32)
+    s = (rng.random(N) * 0.05 + 0.01).astype(np.float32)
+    xf, xb = synth.activations("sp24/raw", "x", M, K)
+    xw = synth.bf16_bits_to_f32(xb)
+    ref = oracle.sparse24_gpu_matmul(meta, s, xw, M, K, N)
+    y = _run(ctx, meta, s, xf, xb, "bf16", "f32")
+    assert_close_f32(host(y), ref)
+
+
+def test_sparse_prefill_11008_sampled(ctx):
+    """2:4 prefill at X[2048, 4096] x W[11008, 4096]: every output row of
+    eight sampled tokens against the oracle (each row depends only on its
+    token)."""
+    M, K, N = 2048, 4096, 11008
+    name = "sp24/prefill11008"
+    t = synth.sparse24_uniform(name, "w", N, K)
+    meta = frx.pack_sparse24_gpu(t)
+    s = synth.row_scales(name, "s", N, samples=256)
+    xf, xb = synth.activations(name, "x", M, K)
+    y = host(_run(ctx, meta, s, xf, xb, "bf16", "f32"))
+    rows = np.array([0, 1, 127, 128, 1000, 1919, 2046, 2047])
+    xw = synth.bf16_bits_to_f32(xb)[rows]
+    ref = oracle.sparse24_gpu_matmul(meta, s, np.ascontiguousarray(xw), len(rows), K, N)
+    assert_close_f32(y[rows], ref.reshape(len(rows), N))
