@@ -158,9 +158,12 @@ struct Gemm2 {
   // m_count are clamped to the last valid row and W rows past n_count to the
   // last valid row (their outputs are discarded by the caller). Non-gather X
   // offsets are relative to the tile's first row; gather offsets to row 0.
+  // ldx: X row stride (elements); wk: columns of W (its row length; the K
+  // loop may run past it, see run). Dual weights: W-stage rows [BN/2, BN)
+  // come from a second matrix (rows n - BN/2), each of n_count valid rows.
   __device__ __forceinline__ static void lane_offsets(uint32_t (&xv)[XPW], uint32_t (&wv)[WPW],
                                                       const int *rowidx, int m_count,
-                                                      int n_count, int K) {
+                                                      int n_count, int ldx, int wk, bool dual) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
 #pragma unroll
     for (int i = 0; i < XPW; i++) {
@@ -168,24 +171,27 @@ struct Gemm2 {
       const int rm = min(r, m_count - 1);
       const uint32_t gr = GATHER ? (uint32_t)rowidx[rm] : (uint32_t)rm;
       const uint32_t c = (lane & 7) ^ ((r >> 1) & 7);  // swizzled source chunk
-      xv[i] = gr * (uint32_t)K * 2u + 16u * c;
+      xv[i] = gr * (uint32_t)ldx * 2u + 16u * c;
     }
 #pragma unroll
     for (int i = 0; i < WPW; i++) {
-      const int n = min((wave * WPW + i) * 64 + lane, n_count - 1);
-      wv[i] = (uint32_t)n * (uint32_t)(K >> 4) * 4u;
+      int n = (wave * WPW + i) * 64 + lane;
+      if (dual && n >= BN / 2) n -= BN / 2;
+      n = min(n, n_count - 1);
+      wv[i] = (uint32_t)n * (uint32_t)(wk >> 4) * 4u;
     }
   }
 
+  // k0: X column of the stage; kw0: its W column.
   __device__ __forceinline__ static void issue(uint32_t *stage, __amdgpu_buffer_rsrc_t xr,
-                                               __amdgpu_buffer_rsrc_t wr, const uint32_t (&xv)[XPW],
-                                               const uint32_t (&wv)[WPW], int k0) {
+                                               const __amdgpu_buffer_rsrc_t (&wr)[WPW], const uint32_t (&xv)[XPW],
+                                               const uint32_t (&wv)[WPW], int k0, int kw0) {
     const int wave = threadIdx.x >> 6;
 #pragma unroll
     for (int i = 0; i < XPW; i++) lds_load16(xr, stage + (wave * XPW + i) * 256, xv[i], 2u * k0);
 #pragma unroll
     for (int i = 0; i < WPW; i++)
-      lds_load16(wr, stage + XSTAGE + (wave * WPW + i) * 256, wv[i], (uint32_t)k0 >> 2);
+      lds_load16(wr[i], stage + XSTAGE + (wave * WPW + i) * 256, wv[i], (uint32_t)kw0 >> 2);
   }
 
   __device__ __forceinline__ static u32x4 xread(const uint32_t *stage, int r, int c) {
@@ -225,15 +231,32 @@ struct Gemm2 {
   // X operands, and unpacks stage t+1's first-half weight operands. The first
   // half's MFMAs likewise cover the unpack of the second half's operands.
   // Stage t+1 is issued in step t+2-NS, i.e. NS-2 steps of latency cover.
+  //
+  // W2 != nullptr: dual weights (W-stage rows BN/2.. from W2). wk: W's
+  // columns, K <= 2 wk; past wk the loop multiplies X's columns by W again
+  // (W column k - wk), which runs an fp32 activation stored as bf16 hi | lo
+  // halves of one row in a single pass (K = 2 wk). ldx: X row stride in
+  // elements (default K).
   __device__ static void run(uint32_t *lds, const uint16_t *X, uint32_t xbytes, const int *rowidx,
                              int m_count, const uint32_t *W, int n_count, int K,
-                             f32x4 (&acc)[FN][FM]) {
+                             f32x4 (&acc)[FN][FM], const uint32_t *W2 = nullptr, int wk = 0, int ldx = 0) {
     static_assert(NS >= 3, "the ring needs a stage being read, one landing and one free");
     static_assert(FM >= 4 && FN <= FM && XD <= FM, "operand schedule");
+    if (wk == 0) wk = K;
+    if (ldx == 0) ldx = K;
+    const bool dual = W2 != nullptr;
     uint32_t xv[XPW], wv[WPW];
-    lane_offsets(xv, wv, rowidx, m_count, n_count, K);
+    lane_offsets(xv, wv, rowidx, m_count, n_count, ldx, wk, dual);
     const __amdgpu_buffer_rsrc_t xr = buffer_rsrc(X, xbytes);
-    const __amdgpu_buffer_rsrc_t wr = buffer_rsrc(W, (uint32_t)n_count * (uint32_t)(K >> 4) * 4u);
+    __amdgpu_buffer_rsrc_t wr[WPW];
+    {
+      const int wave = threadIdx.x >> 6;
+#pragma unroll
+      for (int i = 0; i < WPW; i++) {
+        const bool second = dual && (wave * WPW + i) * 64 >= BN / 2;
+        wr[i] = buffer_rsrc(second ? W2 : W, (uint32_t)n_count * (uint32_t)(wk >> 4) * 4u);
+      }
+    }
 #pragma unroll
     for (int fn = 0; fn < FN; fn++)
 #pragma unroll
@@ -256,7 +279,10 @@ struct Gemm2 {
     // step has no branch; control flow among the MFMAs makes the register
     // allocator shuttle the accumulators between register files.
 #pragma unroll
-    for (int s = 0; s < NS - 1; s++) issue(lds + s * STAGE, xr, wr, xv, wv, min(s, nks - 1) * 64);
+    for (int s = 0; s < NS - 1; s++) {
+      const int k0 = min(s, nks - 1) * 64;
+      issue(lds + s * STAGE, xr, wr, xv, wv, k0, k0 >= wk ? k0 - wk : k0);
+    }
     wait_vmcnt<(NS - 2) * LPW>();  // stage 0 landed
     barrier_nofence();
 
@@ -316,7 +342,10 @@ struct Gemm2 {
         }
 #pragma unroll
         for (int fn = 0; fn < FN; fn++) mfma16_acc(acc[fn][fm], a1[fn], b[q]);
-        if (fm == 0) issue(lds + ((t + NS - 1) % NS) * STAGE, xr, wr, xv, wv, min(t + NS - 1, nks - 1) * 64);
+        if (fm == 0) {
+          const int k0 = min(t + NS - 1, nks - 1) * 64;
+          issue(lds + ((t + NS - 1) % NS) * STAGE, xr, wr, xv, wv, k0, k0 >= wk ? k0 - wk : k0);
+        }
         if (fm >= 2 && fm - 2 < FN) a0n[fm - 2] = unpack8_nat(wq0n[fm - 2], sel0, sel1);
         __builtin_amdgcn_sched_barrier(0);
       }

@@ -18,6 +18,7 @@
 //                    per operand), fp32 rows.
 //   5. combine       out[t] = sum_k w[t,k] * d[row(t,k)] in k order from 0.0,
 //                    exactly the reference's accumulation (deterministic).
+#include "frx_gemm2.hpp"
 #include "frx_gemm_core.hpp"
 #include "frx_internal.hpp"
 
@@ -40,7 +41,7 @@ size_t moe_workspace_bytes(int T, int H, int I, int E, int top_k) {
   b += align256(max_tiles * 8);         // tiles
   b += align256(4);                     // ntiles
   b += align256(A * I * 2) * 2;         // h planes
-  b += align256(A * H * 4);             // dout
+  b += align256(A * H * 4) * 2;         // dout, dout_lo
   return b;
 }
 
@@ -61,6 +62,7 @@ void moe_workspace_carve(void *base, int T, int H, int I, int E, int top_k,
   ws->h_hi = reinterpret_cast<uint16_t *>(take(A * I * 2));
   ws->h_lo = reinterpret_cast<uint16_t *>(take(A * I * 2));
   ws->dout = reinterpret_cast<float *>(take(A * H * 4));
+  ws->dout_lo = reinterpret_cast<float *>(take(A * H * 4));
 }
 
 template <typename T>
@@ -97,20 +99,27 @@ __device__ __forceinline__ void ld8(const float *p, float v[8]) {
 
 constexpr int RT_CHMAX = 256;  // router columns staged per chunk (at most)
 
-// Chunk width so that one pass of 256 threads x 4 units of 8 columns covers
-// every staged row (tokens of the block + experts): a multiple of 8.
+// One wave per workgroup (RT_NT threads); each thread stages RT_SP units of
+// 8 columns per chunk.
+constexpr int RT_NT = 64, RT_SP = 8;
+
+// Chunk width so that one pass of RT_NT threads x RT_SP units of 8 columns
+// covers every staged row (tokens of the block + experts): a multiple of 8.
 static inline int router_chunk(int rows) {
-  int ch = (1024 / rows) * 8;
+  int ch = (RT_NT * RT_SP / rows) * 8;
   return ch > RT_CHMAX ? RT_CHMAX : ch;
 }
 
-// 256 threads = (256/EP) tokens x EP expert lanes (EP = E rounded up to a
-// power of two). Chunks of RT_CH columns of the block's token rows and of
-// all router rows are staged in LDS as f32 (double-buffered: the next
-// chunk's global loads are in flight while the current one is summed); each
-// (token, expert) lane then runs the reference's sequential dot product.
+// RT_NT threads = (RT_NT/EP) tokens x EP expert lanes (EP = E rounded up to
+// a power of two). A (token, expert) lane's logit is a chain of H dependent
+// adds, so the kernel time is one chain's latency: one wave per workgroup
+// spreads the chains over as many SIMDs as possible. Chunks of CH columns of
+// the block's token rows and of all router rows are staged in LDS as f32
+// (double-buffered: the next chunk's global loads are in flight while the
+// current one is summed); each lane runs the reference's sequential dot
+// product.
 template <typename XT, typename RT>
-__global__ __launch_bounds__(256) void moe_router_kernel(
+__global__ __launch_bounds__(RT_NT) void moe_router_kernel(
     const XT *__restrict__ x, const RT *__restrict__ router, int T, int H,
     int E, int EP, int top_k, int CH, uint32_t *__restrict__ idx_out,
     float *__restrict__ w_out, uint32_t *__restrict__ user_idx,
@@ -118,54 +127,109 @@ __global__ __launch_bounds__(256) void moe_router_kernel(
   const int RS = CH + 4;  // padded row stride (floats)
   extern __shared__ __align__(16) float rsm[];
   const int tid = threadIdx.x, e = tid % EP, tl = tid / EP;
-  const int TPB = 256 / EP;
+  const int TPB = RT_NT / EP;
   const int t = blockIdx.x * TPB + tl;
   const int rows = TPB + E;  // staged rows: tokens then experts
-  float *buf[2] = {rsm, rsm + rows * RS};
+  // the two chunk buffers, indexed off the __shared__ base so that reads
+  // stay LDS instructions (a pointer picked from an array would turn them
+  // into generic FLAT loads)
+  auto buf = [&](int i) { return rsm + i * rows * RS; };
   float *logit = rsm + 2 * rows * RS;
   const int nch = (H + CH - 1) / CH;
-  // each thread stages 8 consecutive columns of one row per pass
+  // each thread stages 8 consecutive columns of one row per pass. The loads
+  // are unconditional (out-of-range units read a valid clamped address and
+  // are zeroed when stored): a load under a divergent branch makes the
+  // compiler wait for it on the spot, which serialises the chunk's loads.
   const int units = rows * (CH / 8);
-  float stage[4][8];
-  auto gload = [&](int c) {
+  constexpr int NVX = sizeof(XT) == 2 ? 1 : 2, NVR = sizeof(RT) == 2 ? 1 : 2;  // 16-byte loads per unit
+  constexpr bool SAME = sizeof(XT) == sizeof(RT);
+  // same element size: one load from the selected row; otherwise both
+  // candidates are loaded and the store picks one
+  struct Raw {
+    u32x4 a[RT_SP][NVX], b[RT_SP][SAME ? 1 : NVR];
+    bool ok[RT_SP], tok[RT_SP];
+  };
+  auto gload = [&](int c, Raw &raw) {
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-      const int u = tid + i * 256;
+    for (int i = 0; i < RT_SP; i++) {
+      const int u = tid + i * RT_NT;
       const int rr = u / (CH / 8), col = c * CH + (u % (CH / 8)) * 8;
-      const bool ok = u < units && col < H;
-      if (ok && rr < TPB) {
-        const int tt = blockIdx.x * TPB + rr;
-        if (tt < T) ld8(x + (long)tt * H + col, stage[i]);
-        else for (int k = 0; k < 8; k++) stage[i][k] = 0.f;
-      } else if (ok) {
-        ld8(router + (long)(rr - TPB) * H + col, stage[i]);
+      const int tt = blockIdx.x * TPB + rr;
+      const bool tok = rr < TPB;
+      raw.ok[i] = u < units && col < H && (!tok || tt < T);
+      raw.tok[i] = tok;
+      const int cc = raw.ok[i] ? col : 0;
+      const u32x4 *xs = reinterpret_cast<const u32x4 *>(x + (long)min(tt, T - 1) * H + cc);
+      const u32x4 *rs = reinterpret_cast<const u32x4 *>(router + (long)min(max(rr - TPB, 0), E - 1) * H + cc);
+      if constexpr (SAME) {
+        const u32x4 *src = tok ? xs : rs;
+#pragma unroll
+        for (int v = 0; v < NVX; v++) raw.a[i][v] = src[v];
       } else {
-        for (int k = 0; k < 8; k++) stage[i][k] = 0.f;
+#pragma unroll
+        for (int v = 0; v < NVX; v++) raw.a[i][v] = xs[v];
+#pragma unroll
+        for (int v = 0; v < NVR; v++) raw.b[i][v] = rs[v];
       }
     }
   };
-  auto sstore = [&](float *b) {
+  // 8 elements (one 16-byte bf16 load or two 16-byte f32 loads) as f32,
+  // zero when m == 0
+  auto cvt8 = [](const u32x4 *r, int nv, uint32_t m, float v8[8]) {
+    if (nv == 1) {
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-      const int u = tid + i * 256;
+      for (int q = 0; q < 4; q++) {
+        const uint32_t w = r[0][q] & m;
+        v8[2 * q] = __uint_as_float(w << 16);
+        v8[2 * q + 1] = __uint_as_float(w & 0xFFFF0000u);
+      }
+    } else {
+#pragma unroll
+      for (int q = 0; q < 4; q++) {
+        v8[q] = __uint_as_float(r[0][q] & m);
+        v8[4 + q] = __uint_as_float(r[1][q] & m);
+      }
+    }
+  };
+  auto sstore = [&](float *b, const Raw &raw) {
+#pragma unroll
+    for (int i = 0; i < RT_SP; i++) {
+      const int u = tid + i * RT_NT;
       if (u < units) {
         const int rr = u / (CH / 8), cc = (u % (CH / 8)) * 8;
+        const uint32_t m = raw.ok[i] ? 0xFFFFFFFFu : 0u;
+        float v8[8];
+        if constexpr (SAME) {
+          cvt8(raw.a[i], NVX, m, v8);
+        } else {
+          float va[8], vb[8];
+          cvt8(raw.a[i], NVX, m, va);
+          cvt8(raw.b[i], NVR, m, vb);
+#pragma unroll
+          for (int q = 0; q < 8; q++) v8[q] = raw.tok[i] ? va[q] : vb[q];
+        }
         float4 *d = reinterpret_cast<float4 *>(b + rr * RS + cc);
-        d[0] = make_float4(stage[i][0], stage[i][1], stage[i][2], stage[i][3]);
-        d[1] = make_float4(stage[i][4], stage[i][5], stage[i][6], stage[i][7]);
+        d[0] = make_float4(v8[0], v8[1], v8[2], v8[3]);
+        d[1] = make_float4(v8[4], v8[5], v8[6], v8[7]);
       }
     }
   };
   float sum = 0.0f;
-  gload(0);
-  sstore(buf[0]);
+  // Staged data of two chunks sits in registers: chunk c + 2 is loaded while
+  // chunk c is summed and chunk c + 1 (loaded during chunk c - 1) is stored.
+  Raw r0, r1;
+  gload(0, r0);
+  gload(min(1, nch - 1), r1);
+  sstore(buf(0), r0);
   __syncthreads();
-  for (int c = 0; c < nch; c++) {
-    if (c + 1 < nch) gload(c + 1);
+  // (loads and calls are unconditional inside the loop: a conditionally
+  // loaded register set makes the compiler wait for every load at the merge)
+  auto chunk = [&](int c, const Raw &rnext, Raw &rfree) {
+    gload(min(c + 2, nch - 1), rfree);
     if (e < E && t < T) {
 #pragma clang fp contract(off)
-      const float *xr = buf[c & 1] + tl * RS;
-      const float *rr = buf[c & 1] + (TPB + e) * RS;
+      const float *xr = buf(c & 1) + tl * RS;
+      const float *rr = buf(c & 1) + (TPB + e) * RS;
       const int ncol = min(CH, H - c * CH);  // multiple of 8
       int j = 0;
       // 32 columns of LDS reads issued ahead of each run of dependent adds
@@ -202,17 +266,23 @@ __global__ __launch_bounds__(256) void moe_router_kernel(
         }
       }
     }
-    if (c + 1 < nch) sstore(buf[(c + 1) & 1]);
+    if (c + 1 < nch) sstore(buf((c + 1) & 1), rnext);
     __syncthreads();
+  };
+  int c = 0;
+  for (; c + 1 < nch; c += 2) {
+    chunk(c, r1, r0);
+    chunk(c + 1, r0, r1);
   }
+  if (c < nch) chunk(c, r1, r0);
   // Softmax and stable top-k in LDS, one EP-lane group per token. A lane's
   // rank among the probabilities (greater, or equal with a lower index)
   // reproduces the stable descending sort of the reference; the two
   // reductions (sum of exps in expert order, sum of the top-k in sorted
   // order) stay sequential on one lane, as in the reference.
-  float *pbuf = logit + 256;             // [256] probabilities
-  float *tsum = pbuf + 256;              // [256/EP] per-token sums
-  int *order = reinterpret_cast<int *>(tsum + 256);  // [256/EP][EP]
+  float *pbuf = logit + RT_NT;             // [RT_NT] probabilities
+  float *tsum = pbuf + RT_NT;              // [RT_NT/EP] per-token sums
+  int *order = reinterpret_cast<int *>(tsum + RT_NT);  // [RT_NT/EP][EP]
   logit[tid] = sum;
   __syncthreads();
   const float *lg = logit + tl * EP;
@@ -422,11 +492,111 @@ __global__ __launch_bounds__(256) void moe_down_kernel(
   }
 }
 
+// ---- 3b/4b. the grouped GEMMs on the pipelined engine -------------------------
+// bf16 activations, H % 64 == 0, I % 64 == 0, 16-byte aligned weights. Tiles
+// of MOE_BM expert-sorted rows. gate/up: one 256-row weight tile holds 128
+// gate rows and the same 128 up rows (frx_gemm2.hpp dual weights), token
+// rows gathered through perm_token; the epilogue writes h = act(g) * u as
+// bf16 hi | lo halves of one row of h2 [A][2 I]. down: the hi halves and the
+// lo halves of h2's rows times W_down in separate workgroups (blockIdx.z),
+// each into its own fp32 partial [A][H]; the combine adds the two.
+constexpr int MOE2_BN = 256;
+using MoeGateUpCore = Gemm2<MOE_BM, MOE2_BN, 1, 4, 4, true>;
+using MoeDownCore = Gemm2<MOE_BM, MOE2_BN, 1, 4, 4, false>;
+
+__global__ __launch_bounds__(256) void moe_gateup2_kernel(
+    const GateUpArgs args, const uint16_t *__restrict__ x, int T, int H, int I,
+    const int *__restrict__ tiles, const int *__restrict__ ntiles,
+    const int *__restrict__ counts, const int *__restrict__ offsets,
+    const int *__restrict__ perm_token, uint16_t *__restrict__ h2, int gelu) {
+  using Core = MoeGateUpCore;
+  extern __shared__ __align__(16) uint32_t lds[];
+  const int tile = blockIdx.y;
+  if (tile >= *ntiles) return;  // whole workgroup
+  const int e = tiles[2 * tile], mstart = tiles[2 * tile + 1];
+  const int mcount = min(MOE_BM, counts[e] - mstart);
+  const int row0 = offsets[e] + mstart;
+  const int n0 = blockIdx.x * (MOE2_BN / 2), nc = min(MOE2_BN / 2, I - n0);
+  f32x4 acc[Core::FN][Core::FM];
+  Core::run(lds, x, (uint32_t)T * (uint32_t)H * 2u, perm_token + row0, mcount,
+            args.wg[e] + (size_t)n0 * (H >> 4), nc, H, acc, args.wu[e] + (size_t)n0 * (H >> 4), H);
+  // Epilogue: fragments to LDS in two passes of 32 tokens (row pitch
+  // MOE2_BN + 16 floats); each thread then owns 4 gate columns (and the
+  // same 4 up columns 128 further) of 4 tokens per pass.
+  constexpr int PF = MOE2_BN + 16, P = 2, TMP = MOE_BM / P, FMP = Core::FM / P;
+  static_assert(TMP * PF <= Core::LDS_DWORDS, "epilogue staging");
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, l16 = lane & 15, g = lane >> 4;
+  float *st = reinterpret_cast<float *>(lds);
+  const int c = threadIdx.x % 32, rr = threadIdx.x / 32;
+  f32x4 sgv, suv;
+#pragma unroll
+  for (int j = 0; j < 4; j++) {
+    const int n = n0 + min(4 * c + j, nc - 1);
+    sgv[j] = 0.5f * args.sg[e][n];  // 0.5 undoes the 2*dec(c) operand encoding
+    suv[j] = 0.5f * args.su[e][n];
+  }
+#pragma unroll
+  for (int p = 0; p < P; p++) {
+#pragma unroll
+    for (int fn = 0; fn < Core::FN; fn++)
+#pragma unroll
+      for (int fmi = 0; fmi < FMP; fmi++)
+        *reinterpret_cast<f32x4 *>(st + (fmi * 16 + l16) * PF + wave * Core::TN + fn * 16 + 4 * g) =
+            acc[fn][p * FMP + fmi];
+    __syncthreads();
+    for (int lr = rr; lr < TMP; lr += 8) {
+      const int m = p * TMP + lr;
+      if (m >= mcount || 4 * c >= nc) continue;
+      const f32x4 gv = *reinterpret_cast<const f32x4 *>(st + lr * PF + 4 * c) * sgv;
+      const f32x4 uv = *reinterpret_cast<const f32x4 *>(st + lr * PF + MOE2_BN / 2 + 4 * c) * suv;
+      uint32_t hh[4], hl[4];
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        const float a = gelu ? act_gelu_tanh(gv[j]) : act_silu(gv[j]);
+        split_bf16(a * uv[j], hh[j], hl[j]);
+      }
+      uint16_t *d = h2 + (size_t)(row0 + m) * (2 * (size_t)I) + n0 + 4 * c;
+      if (4 * c + 4 <= nc) {
+        *reinterpret_cast<u32x2 *>(d) = (u32x2){hh[0] | (hh[1] << 16), hh[2] | (hh[3] << 16)};
+        *reinterpret_cast<u32x2 *>(d + I) = (u32x2){hl[0] | (hl[1] << 16), hl[2] | (hl[3] << 16)};
+      } else {
+        for (int j = 0; j < nc - 4 * c; j++) {
+          d[j] = (uint16_t)hh[j];
+          d[I + j] = (uint16_t)hl[j];
+        }
+      }
+    }
+    __syncthreads();
+  }
+}
+
+__global__ __launch_bounds__(256) void moe_down2_kernel(
+    const DownArgs args, const uint16_t *__restrict__ h2, int H, int I,
+    const int *__restrict__ tiles, const int *__restrict__ ntiles,
+    const int *__restrict__ counts, const int *__restrict__ offsets,
+    float *__restrict__ dout, float *__restrict__ dout_lo) {
+  using Core = MoeDownCore;
+  extern __shared__ __align__(16) uint32_t lds[];
+  const int tile = blockIdx.y;
+  if (tile >= *ntiles) return;  // whole workgroup
+  const int e = tiles[2 * tile], mstart = tiles[2 * tile + 1];
+  const int mcount = min(MOE_BM, counts[e] - mstart);
+  const int row0 = offsets[e] + mstart;
+  const int n0 = blockIdx.x * MOE2_BN, nc = min(MOE2_BN, H - n0);
+  const int half = blockIdx.z;  // 0: hi, 1: lo
+  f32x4 acc[Core::FN][Core::FM];
+  Core::run(lds, h2 + (size_t)row0 * (2 * (size_t)I) + half * I, (uint32_t)mcount * (uint32_t)I * 4u - half * I * 2u,
+            nullptr, mcount, args.wd[e] + (size_t)n0 * (I >> 4), nc, I, acc, nullptr, I, 2 * I);
+  Core::template store_tile<float>(lds, acc, args.sd[e], half ? dout_lo : dout, (size_t)H, row0, mcount, n0, nc);
+}
+
 // ---- 5. combine ---------------------------------------------------------------
 // cpu_block_attn_res.rs:1179 `expert_outputs[t*hd+d] += w * down[d]`, k order.
+// dout_lo != nullptr: the down rows arrive as two partials (hi and lo halves
+// of the activation), d = dout + dout_lo.
 template <typename YT>
 __global__ __launch_bounds__(256) void moe_combine_kernel(
-    const float *__restrict__ dout, const float *__restrict__ wts,
+    const float *__restrict__ dout, const float *__restrict__ dout_lo, const float *__restrict__ wts,
     const int *__restrict__ inv, int H, int top_k, YT *__restrict__ y) {
   const int t = blockIdx.x;
   for (int j = threadIdx.x * 4; j < H; j += 1024) {  // H % 16 == 0
@@ -434,7 +604,9 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(
     for (int k = 0; k < top_k; k++) {
 #pragma clang fp contract(off)
       const float w = wts[t * top_k + k];
-      const f32x4 d = *reinterpret_cast<const f32x4 *>(dout + (long)inv[t * top_k + k] * H + j);
+      const long o = (long)inv[t * top_k + k] * H + j;
+      f32x4 d = *reinterpret_cast<const f32x4 *>(dout + o);
+      if (dout_lo) d = d + *reinterpret_cast<const f32x4 *>(dout_lo + o);
       const f32x4 prod = d * w;
       acc = acc + prod;
     }
@@ -455,9 +627,10 @@ hipError_t launch_moe(const void *x, int xt_bf16, const void *router,
   // 1. router
   int EP = 1;
   while (EP < E) EP *= 2;
-  const dim3 rg((T + 256 / EP - 1) / (256 / EP));
-  const int rch = router_chunk(256 / EP + E);
-  const size_t rlds = (size_t)(2 * (256 / EP + E) * (rch + 4) + 4 * 256) * 4;
+  const int tpb = RT_NT / EP;
+  const dim3 rg((T + tpb - 1) / tpb);
+  const int rch = router_chunk(tpb + E);
+  const size_t rlds = (size_t)(2 * (tpb + E) * (rch + 4) + 4 * RT_NT) * 4;
   {
     static std::atomic<uint64_t> done[4];
     const void *fns[4] = {reinterpret_cast<const void *>(&moe_router_kernel<uint16_t, uint16_t>),
@@ -469,16 +642,16 @@ hipError_t launch_moe(const void *x, int xt_bf16, const void *router,
     if (e != hipSuccess) return e;
   }
   if (xt_bf16 && rt_bf16)
-    hipLaunchKernelGGL((moe_router_kernel<uint16_t, uint16_t>), rg, dim3(256), rlds, stream,
+    hipLaunchKernelGGL((moe_router_kernel<uint16_t, uint16_t>), rg, dim3(RT_NT), rlds, stream,
                        (const uint16_t *)x, (const uint16_t *)router, T, H, E, EP, top_k, rch, ws.idx, ws.wts, topk_idx, topk_w);
   else if (xt_bf16)
-    hipLaunchKernelGGL((moe_router_kernel<uint16_t, float>), rg, dim3(256), rlds, stream,
+    hipLaunchKernelGGL((moe_router_kernel<uint16_t, float>), rg, dim3(RT_NT), rlds, stream,
                        (const uint16_t *)x, (const float *)router, T, H, E, EP, top_k, rch, ws.idx, ws.wts, topk_idx, topk_w);
   else if (rt_bf16)
-    hipLaunchKernelGGL((moe_router_kernel<float, uint16_t>), rg, dim3(256), rlds, stream,
+    hipLaunchKernelGGL((moe_router_kernel<float, uint16_t>), rg, dim3(RT_NT), rlds, stream,
                        (const float *)x, (const uint16_t *)router, T, H, E, EP, top_k, rch, ws.idx, ws.wts, topk_idx, topk_w);
   else
-    hipLaunchKernelGGL((moe_router_kernel<float, float>), rg, dim3(256), rlds, stream,
+    hipLaunchKernelGGL((moe_router_kernel<float, float>), rg, dim3(RT_NT), rlds, stream,
                        (const float *)x, (const float *)router, T, H, E, EP, top_k, rch, ws.idx, ws.wts, topk_idx, topk_w);
   hipError_t err = hipGetLastError();
   if (err != hipSuccess) return err;
@@ -496,6 +669,26 @@ hipError_t launch_moe(const void *x, int xt_bf16, const void *router,
     ga.sg[i] = v ? s_gate[i] : nullptr;
     ga.su[i] = v ? s_up[i] : nullptr;
   }
+  bool engine2 = xt_bf16 && H % 64 == 0 && I % 64 == 0;
+  for (int i = 0; i < E && engine2; i++)
+    engine2 = ((reinterpret_cast<uintptr_t>(w_gate[i]) | reinterpret_cast<uintptr_t>(w_up[i]) |
+                reinterpret_cast<uintptr_t>(w_down[i])) & 15) == 0;
+  DownArgs da;
+  for (int i = 0; i < MOE_MAXE; i++) {
+    da.wd[i] = i < E ? w_down[i] : nullptr;
+    da.sd[i] = i < E ? s_down[i] : nullptr;
+  }
+  if (engine2) {
+    const dim3 g1((I + MOE2_BN / 2 - 1) / (MOE2_BN / 2), max_tiles);
+    hipLaunchKernelGGL(moe_gateup2_kernel, g1, dim3(256), MoeGateUpCore::LDS_DWORDS * 4, stream, ga,
+                       (const uint16_t *)x, T, H, I, ws.tiles, ws.ntiles, ws.counts, ws.offsets,
+                       ws.perm_token, ws.h_hi, gelu);
+    if ((err = hipGetLastError()) != hipSuccess) return err;
+    const dim3 g2((H + MOE2_BN - 1) / MOE2_BN, max_tiles, 2);
+    hipLaunchKernelGGL(moe_down2_kernel, g2, dim3(256), MoeDownCore::LDS_DWORDS * 4, stream, da, ws.h_hi,
+                       H, I, ws.tiles, ws.ntiles, ws.counts, ws.offsets, ws.dout, ws.dout_lo);
+    if ((err = hipGetLastError()) != hipSuccess) return err;
+  } else {
   dim3 g1((I + MOE_BN - 1) / MOE_BN, max_tiles);
   if (xt_bf16)
     hipLaunchKernelGGL((moe_gateup_kernel<XS_BF16>), g1, dim3(256), 0, stream, ga, x, H, I,
@@ -505,22 +698,18 @@ hipError_t launch_moe(const void *x, int xt_bf16, const void *router,
                        ws.tiles, ws.ntiles, ws.counts, ws.offsets, ws.perm_token, ws.h_hi, ws.h_lo, gelu);
   if ((err = hipGetLastError()) != hipSuccess) return err;
   // 4. down
-  DownArgs da;
-  for (int i = 0; i < MOE_MAXE; i++) {
-    da.wd[i] = i < E ? w_down[i] : nullptr;
-    da.sd[i] = i < E ? s_down[i] : nullptr;
-  }
   dim3 g2((H + MOE_BN - 1) / MOE_BN, max_tiles);
   hipLaunchKernelGGL(moe_down_kernel, g2, dim3(256), 0, stream, da, ws.h_hi, ws.h_lo, H, I,
                      ws.tiles, ws.ntiles, ws.counts, ws.offsets, ws.dout);
   if ((err = hipGetLastError()) != hipSuccess) return err;
+  }
   // 5. combine
   if (yt_bf16)
     hipLaunchKernelGGL((moe_combine_kernel<uint16_t>), dim3(T), dim3(256), 0, stream, ws.dout,
-                       ws.wts, ws.inv, H, top_k, (uint16_t *)y);
+                       engine2 ? ws.dout_lo : nullptr, ws.wts, ws.inv, H, top_k, (uint16_t *)y);
   else
     hipLaunchKernelGGL((moe_combine_kernel<float>), dim3(T), dim3(256), 0, stream, ws.dout,
-                       ws.wts, ws.inv, H, top_k, (float *)y);
+                       engine2 ? ws.dout_lo : nullptr, ws.wts, ws.inv, H, top_k, (float *)y);
   return hipGetLastError();
 }
 
