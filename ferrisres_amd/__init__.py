@@ -61,6 +61,12 @@ _SIGS = {
     "frx_ternary_ffn": (_int, [_vp, _vp, _int, _vp, _vp, _vp, _vp, _vp, _vp, _u32, _u32, _u32,
                                _int, _vp, _int]),
     "frx_set_ffn_mode": (_int, [_vp, _int]),
+    "frx_upload_ternary": (_int, [_vp, _vp, _u32, _u32, _vp, ctypes.c_float, ctypes.POINTER(_vp),
+                                  ctypes.POINTER(_vp)]),
+    "frx_upload_stm": (_int, [_vp, _vp, _sz, ctypes.POINTER(_vp), ctypes.POINTER(_vp), ctypes.POINTER(_u32),
+                              ctypes.POINTER(_u32)]),
+    "frx_sparse24_cpu_to_gpu_device": (_int, [_vp, _vp, _vp, _u32, _u32, _vp]),
+    "frx_free": (_int, [_vp, _vp]),
     "frx_pack_ternary_u8": (_int, [_vp, _sz, _vp]),
     "frx_unpack_ternary_u8": (_int, [_vp, _sz, _vp]),
     "frx_repack_u8_to_u32": (_int, [_vp, _sz, _vp]),
@@ -176,7 +182,29 @@ def _dtype_code(t) -> int:
 
 
 def _ptr(t):
-    return _vp(t.data_ptr()) if t is not None else None
+    """Device address of a tensor, a DeviceBuffer or a raw integer address."""
+    if t is None:
+        return None
+    if isinstance(t, int):
+        return _vp(t)
+    return _vp(t.data_ptr())
+
+
+class DeviceBuffer:
+    """Device memory allocated by the library (frx_upload_*); released with
+    frx_free on close() or when the owning context closes it. data_ptr()
+    gives the address, so it can be passed wherever a tensor is."""
+
+    def __init__(self, ctx, addr: int, nbytes: int, shape):
+        self._ctx, self.addr, self.nbytes, self.shape = ctx, addr, nbytes, tuple(shape)
+
+    def data_ptr(self) -> int:
+        return self.addr
+
+    def close(self):
+        if self.addr:
+            _check(lib().frx_free(self._ctx._h, _vp(self.addr)), self._ctx._h)
+            self.addr = 0
 
 
 class Context:
@@ -252,6 +280,35 @@ class Context:
                                      _ptr(w_up), _ptr(s_up), _ptr(w_down), _ptr(s_down), M, H, I,
                                      act, _ptr(y), _dtype_code(y)), self._h)
         return y
+
+    # Weight ingest: resident device copies in the GPU layout.
+    def upload_ternary(self, packed_u8: np.ndarray, N: int, K: int, row_scales=None, tensor_scale: float = 1.0):
+        """frx_upload_ternary: pack_ternary bytes [N*K/4] -> (w [N][K/16] u32,
+        scales [N] f32) on the device, as DeviceBuffers."""
+        p = np.ascontiguousarray(packed_u8, dtype=np.uint8)
+        rs = None if row_scales is None else np.ascontiguousarray(row_scales, dtype=np.float32)
+        w, sc = _vp(), _vp()
+        _check(lib().frx_upload_ternary(self._h, p.ctypes.data_as(_vp), N, K,
+                                        None if rs is None else rs.ctypes.data_as(_vp),
+                                        ctypes.c_float(tensor_scale), ctypes.byref(w), ctypes.byref(sc)), self._h)
+        return DeviceBuffer(self, w.value, N * K // 4, (N, K // 16)), DeviceBuffer(self, sc.value, 4 * N, (N,))
+
+    def upload_stm(self, image: bytes):
+        """frx_upload_stm: an .stm file image -> (meta [N][ceil(K/24)] u32,
+        scales [N] f32) on the device, plus (N, K)."""
+        buf = np.frombuffer(bytes(image), dtype=np.uint8)
+        m, sc, n, k = _vp(), _vp(), _u32(), _u32()
+        _check(lib().frx_upload_stm(self._h, buf.ctypes.data_as(_vp), buf.size, ctypes.byref(m),
+                                    ctypes.byref(sc), ctypes.byref(n), ctypes.byref(k)), self._h)
+        N, K = n.value, k.value
+        wpr = (K // 4 + 5) // 6
+        return (DeviceBuffer(self, m.value, 4 * N * wpr, (N, wpr)), DeviceBuffer(self, sc.value, 4 * N, (N,)), N, K)
+
+    def sparse24_cpu_to_gpu_device(self, patterns, signs, N: int, K: int, meta):
+        """frx_sparse24_cpu_to_gpu_device on device tensors (stream-ordered)."""
+        _check(lib().frx_sparse24_cpu_to_gpu_device(self._h, _ptr(patterns), _ptr(signs), N, K, _ptr(meta)),
+               self._h)
+        return meta
 
     def set_ffn_mode(self, mode: int):
         """frx_set_ffn_mode: FFN_AUTO, FFN_ONE_LAUNCH or FFN_TWO_LAUNCH."""

@@ -17,6 +17,7 @@
 #include <string.h>
 
 #include <mutex>
+#include <vector>
 
 #include "../../include/frx_ternary.h"
 #include "frx_internal.hpp"
@@ -450,6 +451,138 @@ frx_status frx_gpu_sparse_ternary_matmul(frx_ctx *ctx, const uint32_t *meta,
                                          float *out) {
   if (!meta) return fail(ctx, FRX_ERR_SHAPE, "null sparse metadata");
   return host_linear(ctx, meta, scales, nullptr, nullptr, input, seq_len, in_cols, out_rows, out, true);
+}
+
+// ---- weight ingest (resident upload, done once) ----------------------------
+
+// Device allocation that frx_free releases; on failure nothing is left
+// allocated.
+static frx_status dev_alloc(frx_ctx *ctx, void **p, size_t bytes, const char *what) {
+  *p = nullptr;
+  const hipError_t e = hipMalloc(p, bytes ? bytes : 4);
+  if (e != hipSuccess) {
+    *p = nullptr;
+    return hip_fail(ctx, e, what);
+  }
+  return FRX_OK;
+}
+
+static frx_status upload_scales(frx_ctx *ctx, const float *row_scales, float tensor_scale, uint32_t N,
+                                float **s_dev) {
+  frx_status st = dev_alloc(ctx, reinterpret_cast<void **>(s_dev), (size_t)N * 4, "scale allocation");
+  if (st != FRX_OK) return st;
+  std::vector<float> bc;
+  const float *src = row_scales;
+  if (!src) {  // gpu_packed(): the tensor scale on every row
+    bc.assign(N, tensor_scale);
+    src = bc.data();
+  }
+  const hipError_t e = hipMemcpy(*s_dev, src, (size_t)N * 4, hipMemcpyHostToDevice);
+  if (e != hipSuccess) {
+    hipFree(*s_dev);
+    *s_dev = nullptr;
+    return hip_fail(ctx, e, "scale upload");
+  }
+  return FRX_OK;
+}
+
+frx_status frx_upload_ternary(frx_ctx *ctx, const uint8_t *packed, uint32_t N, uint32_t K,
+                              const float *row_scales, float tensor_scale, uint32_t **w_dev, float **s_dev) {
+  frx_status st = enter(ctx);
+  if (st != FRX_OK) return st;
+  if (!packed || !w_dev || !s_dev) return fail(ctx, FRX_ERR_SHAPE, "null pointer argument");
+  *w_dev = nullptr;
+  *s_dev = nullptr;
+  if (N == 0 || K == 0) return fail(ctx, FRX_ERR_SHAPE, "empty shape N=%u K=%u", N, K);
+  if (K % 16 != 0) return fail(ctx, FRX_ERR_SHAPE, "K=%u must be a multiple of 16 for row-aligned u32 words", K);
+  const size_t bytes = (size_t)N * K / 4;
+  if ((st = dev_alloc(ctx, reinterpret_cast<void **>(w_dev), bytes, "weight allocation")) != FRX_OK) return st;
+  // pack_ternary_u32 regroups 4 bytes little-endian into a word: on this
+  // little-endian device the u32 layout is the u8 stream itself.
+  hipError_t e = hipMemcpy(*w_dev, packed, bytes, hipMemcpyHostToDevice);
+  if (e != hipSuccess) {
+    hipFree(*w_dev);
+    *w_dev = nullptr;
+    return hip_fail(ctx, e, "weight upload");
+  }
+  if ((st = upload_scales(ctx, row_scales, tensor_scale, N, s_dev)) != FRX_OK) {
+    hipFree(*w_dev);
+    *w_dev = nullptr;
+  }
+  return st;
+}
+
+frx_status frx_sparse24_cpu_to_gpu_device(frx_ctx *ctx, const uint8_t *patterns, const uint8_t *signs,
+                                          uint32_t N, uint32_t K, uint32_t *meta) {
+  frx_status st = enter(ctx);
+  if (st != FRX_OK) return st;
+  if (!patterns || !signs || !meta) return fail(ctx, FRX_ERR_SHAPE, "null pointer argument");
+  if (K % 4 != 0) return fail(ctx, FRX_ERR_SHAPE, "K=%u must be a multiple of 4", K);
+  if ((size_t)N * K > (size_t)0x7FFFFFFF * 4) return fail(ctx, FRX_ERR_SHAPE, "matrix too large");
+  const hipError_t e = frx::launch_sp24_cpu_to_gpu(patterns, signs, (int)N, (int)K, meta, ctx->stream);
+  if (e != hipSuccess) return hip_fail(ctx, e, "2:4 transcode launch");
+  return FRX_OK;
+}
+
+// .stm image: magic "STM1", rows, cols, scale (f32), pattern bytes, sign
+// bytes, then the two arrays; little-endian (expert_loader.rs:6-16,63-106).
+frx_status frx_upload_stm(frx_ctx *ctx, const void *image, size_t len, uint32_t **meta_dev, float **s_dev,
+                          uint32_t *N_out, uint32_t *K_out) {
+  frx_status st = enter(ctx);
+  if (st != FRX_OK) return st;
+  if (!image || !meta_dev || !s_dev) return fail(ctx, FRX_ERR_SHAPE, "null pointer argument");
+  *meta_dev = nullptr;
+  *s_dev = nullptr;
+  constexpr size_t HDR = 24;
+  if (len < HDR) return fail(ctx, FRX_ERR_SHAPE, "STM image too small: %zu bytes", len);
+  const uint8_t *b = reinterpret_cast<const uint8_t *>(image);
+  auto u32 = [&](size_t o) { uint32_t v; memcpy(&v, b + o, 4); return v; };
+  if (u32(0) != 0x53544D31u) return fail(ctx, FRX_ERR_SHAPE, "invalid STM magic 0x%08X", u32(0));
+  const uint32_t rows = u32(4), cols = u32(8);
+  float scale;
+  memcpy(&scale, b + 12, 4);
+  const size_t pb = u32(16), sb = u32(20);
+  if (len < HDR + pb + sb) return fail(ctx, FRX_ERR_SHAPE, "STM data truncated: expected %zu bytes, got %zu", HDR + pb + sb, len);
+  if (rows == 0 || cols == 0 || cols % 4 != 0)
+    return fail(ctx, FRX_ERR_SHAPE, "STM shape rows=%u cols=%u (cols must be a multiple of 4)", rows, cols);
+  const size_t ng = (size_t)rows * cols / 4;
+  if (pb < (ng + 1) / 2 || sb < (ng + 3) / 4)
+    return fail(ctx, FRX_ERR_SHAPE, "STM arrays too short for %u x %u (%zu pattern, %zu sign bytes)", rows, cols, pb, sb);
+  const size_t wpr = ((size_t)cols / 4 + 5) / 6;
+  void *tmp = nullptr;
+  if ((st = dev_alloc(ctx, &tmp, pb + sb, "STM staging allocation")) != FRX_OK) return st;
+  if ((st = dev_alloc(ctx, reinterpret_cast<void **>(meta_dev), (size_t)rows * wpr * 4, "2:4 metadata allocation")) !=
+      FRX_OK) {
+    hipFree(tmp);
+    return st;
+  }
+  hipError_t e = hipMemcpy(tmp, b + HDR, pb + sb, hipMemcpyHostToDevice);
+  const uint8_t *dp = reinterpret_cast<const uint8_t *>(tmp);
+  if (e == hipSuccess) e = frx::launch_sp24_cpu_to_gpu(dp, dp + pb, (int)rows, (int)cols, *meta_dev, ctx->stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+  hipFree(tmp);
+  if (e != hipSuccess) {
+    hipFree(*meta_dev);
+    *meta_dev = nullptr;
+    return hip_fail(ctx, e, "STM upload / transcode");
+  }
+  if ((st = upload_scales(ctx, nullptr, scale, rows, s_dev)) != FRX_OK) {
+    hipFree(*meta_dev);
+    *meta_dev = nullptr;
+    return st;
+  }
+  if (N_out) *N_out = rows;
+  if (K_out) *K_out = cols;
+  return FRX_OK;
+}
+
+frx_status frx_free(frx_ctx *ctx, void *dev_ptr) {
+  frx_status st = enter(ctx);
+  if (st != FRX_OK) return st;
+  if (!dev_ptr) return FRX_OK;
+  const hipError_t e = hipFree(dev_ptr);
+  if (e != hipSuccess) return hip_fail(ctx, e, "hipFree");
+  return FRX_OK;
 }
 
 }  // extern "C"

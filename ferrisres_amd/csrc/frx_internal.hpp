@@ -56,6 +56,10 @@ hipError_t launch_ffn1(const void *x, int xt_bf16, const uint32_t *wg, const flo
                        int yt_bf16, unsigned *bar, int B, int H, int I, int gelu, int G, size_t lds,
                        hipStream_t stream);
 
+// CPU 2:4 layout -> GPU 5-bit layout on the device (frx_ingest.hip); K % 4 == 0.
+hipError_t launch_sp24_cpu_to_gpu(const uint8_t *patterns, const uint8_t *signs, int N, int K, uint32_t *meta,
+                                  hipStream_t stream);
+
 // MoE pipeline (frx_moe.hip).
 struct MoeWorkspace {
   uint32_t *idx;       // [T*k] selected experts (sorted order per token)

@@ -116,7 +116,8 @@ frx_status frx_sparse24_cpu_to_gpu(const uint8_t *patterns, const uint8_t *signs
   for (size_t r = 0; r < N; r++) {
     for (size_t g = 0; g < gpr; g++) {
       const size_t gi = r * gpr + g;
-      const uint32_t pat = (gi % 2 == 0) ? (patterns[gi / 2] & 7u) : ((patterns[gi / 2] >> 4) & 7u);
+      uint32_t pat = (gi % 2 == 0) ? (patterns[gi / 2] & 7u) : ((patterns[gi / 2] >> 4) & 7u);
+      if (pat > 5u) pat = 0u;  // to_ternary's fallback (sparse_ternary.rs:172-176)
       const uint32_t sb = (signs[gi / 4] >> ((gi % 4) * 2)) & 3u;
       const uint32_t neg = (~sb) & 3u;  // polarity flip: CPU 1 = +1, GPU 1 = -1
       meta[r * wpr + g / 6] |= (pat | (neg << 3)) << ((g % 6) * 5);

@@ -166,6 +166,42 @@ frx_status frx_ternary_ffn(frx_ctx *ctx, const void *x, frx_dtype xt,
  * separate matmul calls. */
 frx_status frx_set_ffn_mode(frx_ctx *ctx, frx_ffn_mode mode);
 
+/* ---- weight ingest (resident upload, done once) ----------------------------
+ * Replaces GpuVramCache::upload / GpuWeightCache::build
+ * (src/model/cpu_block_attn_res.rs:3005-3171) and the .stm expert files of
+ * expert_loader.rs:6-152: weights reach the device once, in the GPU layout,
+ * and are then passed to the entry points above as device pointers.
+ * Buffers returned through w_dev / meta_dev / s_dev are allocated by the
+ * library and released with frx_free. Synchronous (load time). */
+
+/* Dense [N][K] ternary matrix from pack_ternary bytes (4 codes per byte,
+ * src/model/ternary.rs:146-163), K % 16 == 0: *w_dev receives the u32 words
+ * [N][K/16] of pack_ternary_u32 (ternary.rs:1317-1328; on a little-endian
+ * device the same bytes), *s_dev the per-row scales (row_scales[N], or
+ * tensor_scale on every row when row_scales is NULL, as gpu_packed() does,
+ * src/model/cpu_linear.rs:164-169). */
+frx_status frx_upload_ternary(frx_ctx *ctx, const uint8_t *packed, uint32_t N, uint32_t K,
+                              const float *row_scales, float tensor_scale, uint32_t **w_dev,
+                              float **s_dev);
+/* 2:4 matrix from an .stm file image (expert_loader.rs:6-16,63-106: magic
+ * 0x53544D31 "STM1", rows, cols, scale f32, pattern bytes, sign bytes, then
+ * the CPU-layout patterns and signs; little-endian). The arrays go to the
+ * device and are transcoded there into the GPU 5-bit layout (*meta_dev
+ * [N][ceil(K/24)]); *s_dev holds the tensor scale on every row; *N, *K
+ * receive rows and cols (may be NULL). FRX_ERR_SHAPE for an image shorter
+ * than the header, a wrong magic or truncated arrays (the reference's
+ * InvalidData cases), cols % 4 != 0, or arrays too short for rows x cols. */
+frx_status frx_upload_stm(frx_ctx *ctx, const void *image, size_t len, uint32_t **meta_dev,
+                          float **s_dev, uint32_t *N, uint32_t *K);
+/* CPU 2:4 layout (patterns, signs; device pointers) -> GPU layout (meta,
+ * device) on the context's stream; bit-exact with frx_sparse24_cpu_to_gpu.
+ * Requires K % 4 == 0. No synchronisation, no allocation. */
+frx_status frx_sparse24_cpu_to_gpu_device(frx_ctx *ctx, const uint8_t *patterns,
+                                          const uint8_t *signs, uint32_t N, uint32_t K,
+                                          uint32_t *meta);
+/* Releases a buffer returned by frx_upload_ternary / frx_upload_stm. */
+frx_status frx_free(frx_ctx *ctx, void *dev_ptr);
+
 /* ---- host-side packers (no GPU) --------------------------------------------*/
 /* pack_ternary (src/model/ternary.rs:146-163): out has (n+3)/4 bytes. */
 frx_status frx_pack_ternary_u8(const int8_t *values, size_t n, uint8_t *out);
@@ -188,7 +224,10 @@ frx_status frx_pack_sparse24_gpu(const int8_t *w, uint32_t N, uint32_t K,
                                  uint32_t *meta, float *scales);
 /* Bit-exact transcoder from the CPU SparseTernaryMatrix layout (pattern
  * nibbles + sign pairs, bit 1 = +1; src/model/sparse_ternary.rs:52-70) to the
- * GPU 5-bit layout (sign bit 1 = -1). Requires K % 4 == 0. */
+ * GPU 5-bit layout (sign bit 1 = -1). Requires K % 4 == 0. Patterns 6 and 7
+ * (never written by a packer) become pattern 0, as in to_ternary
+ * (sparse_ternary.rs:172-176), so decoding either layout gives the same
+ * matrix. */
 frx_status frx_sparse24_cpu_to_gpu(const uint8_t *patterns,
                                    const uint8_t *signs, uint32_t N,
                                    uint32_t K, uint32_t *meta);

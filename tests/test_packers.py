@@ -67,3 +67,19 @@ def test_sparse24_cpu_to_gpu_transcoder(seed):
     p, s = oracle.sparse24_cpu_from_ternary(t24, rows, cols)
     m2, _ = oracle.pack_sparse24_gpu(t24)
     np.testing.assert_array_equal(frx.sparse24_cpu_to_gpu(p, s, rows, cols), m2)
+
+
+def test_sparse24_transcoder_patterns_6_7_follow_to_ternary():
+    """Raw CPU-layout bytes (every pattern nibble 0..7, any sign bits): the
+    transcoded GPU metadata decodes to the matrix to_ternary reads from the
+    CPU layout (patterns 6 and 7 fall back to pattern 0 there,
+    sparse_ternary.rs:172-176)."""
+    rng = np.random.default_rng(67)
+    rows, cols = 13, 96
+    ng = rows * cols // 4
+    p = rng.integers(0, 256, size=(ng + 1) // 2, dtype=np.uint8)
+    s = rng.integers(0, 256, size=(ng + 3) // 4, dtype=np.uint8)
+    assert ((p & 7) >= 6).any() and ((p >> 4) >= 6).any()
+    meta = frx.sparse24_cpu_to_gpu(p, s, rows, cols)
+    np.testing.assert_array_equal(oracle.sparse24_gpu_decode(meta, rows, cols).ravel(),
+                                  oracle.sparse24_cpu_to_ternary(p, s, rows, cols))
