@@ -205,7 +205,7 @@ def main():
                 # per-launch average over the step's three launches
                 roofline["traffic"] = int(round((2 * by["11008x4096"] + by["4096x11008"]) / 3))
                 roofline["traffic_by_shape"] = {k: by[k] for k in ("11008x4096", "4096x11008")}
-                ffn_traffic = {k: by[k] for k in ("glu_11008x4096", "down_f32_4096x11008") if k in by}
+                ffn_traffic = {k: by[k] for k in ("glu_11008x4096", "down_f32_4096x11008", "ffn1_llama7b") if k in by}
         except (OSError, ValueError, KeyError):
             pass
 
@@ -230,6 +230,8 @@ def main():
                       "hbm_fraction": round(b_ffn / (el_f / args.steps) / 1e9 / HBM_PEAK_GBS, 4)}
     ctx.set_ffn_mode(frx.FFN_AUTO)
     fused["default"]["launches_per_step"] = 1 if B <= 3 else 2
+    if ffn_traffic and "ffn1_llama7b" in ffn_traffic and B <= 3:
+        fused["default"]["traffic"] = ffn_traffic["ffn1_llama7b"]
     fused["two_launch"]["launches_per_step"] = 2
     t_glu = per_launch(lambda i: ctx.ternary_glu(x, W[i][0], s_g, W[i][1], s_u, h), 1, reps)
     t_d32 = per_launch(lambda i: ctx.ternary_linear(W[i][2], s_d, h, y), 1, reps)
