@@ -94,13 +94,20 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm2sp_kernel(
 }
 
 #ifndef FRX_GEMM2_NS
-#define FRX_GEMM2_NS 3
+#define FRX_GEMM2_NS 4
+#endif
+// Waves across the token dimension of a 128 x 256 tile: 1 gives 4 waves of
+// 128 x 64 (one per SIMD); 2 gives 8 waves of 64 x 64 (two per SIMD, half
+// the operand reuse per wave), measured slower (2:4: 81 / 220 us against
+// 72 / 173 us at N = 4096 / 11008).
+#ifndef FRX_GEMM2_WM
+#define FRX_GEMM2_WM 1
 #endif
 
 template <typename YT>
 static hipError_t launch_gemm2_t(const uint32_t *w, const float *scale, const void *x, void *y,
                                  int M, int K, int N, hipStream_t stream) {
-  constexpr int BM = 128, BN = 256, WM = 1, WN = 4, NS = FRX_GEMM2_NS;
+  constexpr int BM = 128, BN = 256, WM = FRX_GEMM2_WM, WN = 4, NS = FRX_GEMM2_NS;
   using Core = Gemm2<BM, BN, WM, WN, NS, false>;
   constexpr int lds = Core::LDS_DWORDS * 4;
   static std::atomic<uint64_t> done;
@@ -116,7 +123,7 @@ static hipError_t launch_gemm2_t(const uint32_t *w, const float *scale, const vo
 template <typename YT>
 static hipError_t launch_gemm2sp_t(const uint32_t *meta, const float *scale, const void *x, void *y,
                                    int M, int K, int N, hipStream_t stream) {
-  constexpr int BM = 128, BN = 256, WM = 1, WN = 4, NS = FRX_GEMM2_NS;
+  constexpr int BM = 128, BN = 256, WM = FRX_GEMM2_WM, WN = 4, NS = FRX_GEMM2_NS;
   using Core = Gemm2<BM, BN, WM, WN, NS, false>;
   constexpr int lds = Core::LDS_DWORDS * 4;
   static std::atomic<uint64_t> done;

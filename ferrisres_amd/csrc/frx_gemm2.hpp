@@ -147,8 +147,14 @@ struct Gemm2 {
   static constexpr int STAGE = XSTAGE + WSTAGE;
   static constexpr int LDS_DWORDS = NS * STAGE;
   static constexpr int XI = BM / 8;    // 1 KB load instructions per X stage
-  static constexpr int WI = BN / 64;   // 1 KB load instructions per W stage
-  static_assert(XI % WAVES == 0 && WI % WAVES == 0, "loads must split evenly over the waves");
+  static_assert(XI % WAVES == 0, "X loads must split evenly over the waves");
+  // W stage: 1 KB (16-byte DMA, 64 rows) instructions when they split evenly
+  // over the waves, else 256-byte (4-byte DMA: lane l loads word l % 4 of row
+  // l / 4) instructions; both fill rows of 4 words.
+  static constexpr bool W4 = (BN / 64) % WAVES != 0;
+  static constexpr int WROWS = W4 ? 16 : 64;  // rows per W load instruction
+  static constexpr int WI = BN / WROWS;
+  static_assert(WI % WAVES == 0, "W loads must split evenly over the waves");
   static constexpr int XPW = XI / WAVES, WPW = WI / WAVES;
   static constexpr int LPW = XPW + WPW;  // load instructions per wave per stage
   static_assert(TM % 16 == 0 && TN % 16 == 0, "wave tile must be 16-aligned");
@@ -175,10 +181,10 @@ struct Gemm2 {
     }
 #pragma unroll
     for (int i = 0; i < WPW; i++) {
-      int n = (wave * WPW + i) * 64 + lane;
+      int n = (wave * WPW + i) * WROWS + (W4 ? lane >> 2 : lane);
       if (dual && n >= BN / 2) n -= BN / 2;
       n = min(n, n_count - 1);
-      wv[i] = (uint32_t)n * (uint32_t)(wk >> 4) * 4u;
+      wv[i] = ((uint32_t)n * (uint32_t)(wk >> 4) + (W4 ? (uint32_t)(lane & 3) : 0u)) * 4u;
     }
   }
 
@@ -190,8 +196,10 @@ struct Gemm2 {
 #pragma unroll
     for (int i = 0; i < XPW; i++) lds_load16(xr, stage + (wave * XPW + i) * 256, xv[i], 2u * k0);
 #pragma unroll
-    for (int i = 0; i < WPW; i++)
-      lds_load16(wr[i], stage + XSTAGE + (wave * WPW + i) * 256, wv[i], (uint32_t)kw0 >> 2);
+    for (int i = 0; i < WPW; i++) {
+      if constexpr (W4) lds_load4(wr[i], stage + XSTAGE + (wave * WPW + i) * 64, wv[i], (uint32_t)kw0 >> 2);
+      else lds_load16(wr[i], stage + XSTAGE + (wave * WPW + i) * 256, wv[i], (uint32_t)kw0 >> 2);
+    }
   }
 
   __device__ __forceinline__ static u32x4 xread(const uint32_t *stage, int r, int c) {
@@ -253,7 +261,7 @@ struct Gemm2 {
       const int wave = threadIdx.x >> 6;
 #pragma unroll
       for (int i = 0; i < WPW; i++) {
-        const bool second = dual && (wave * WPW + i) * 64 >= BN / 2;
+        const bool second = dual && (wave * WPW + i) * WROWS >= BN / 2;
         wr[i] = buffer_rsrc(second ? W2 : W, (uint32_t)n_count * (uint32_t)(wk >> 4) * 4u);
       }
     }
@@ -420,7 +428,7 @@ struct Gemm2 {
   // window reads and operand decode. Requires K % 64 == 0.
   __device__ static void run_sp(uint32_t *lds, const uint16_t *X, uint32_t xbytes, int m_count,
                                 const uint32_t *W, int n_count, int K, int wpr, f32x4 (&acc)[FN][FM]) {
-    static_assert(NS >= 3 && FM % 2 == 0 && FM / 2 >= XDS && FN <= FM / 2 + 1, "sparse schedule");
+    static_assert(NS >= 3 && FM % 2 == 0 && FM / 2 >= XDS, "sparse schedule");
     uint32_t xv[XPW], wv[SWPW];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
 #pragma unroll
