@@ -18,11 +18,12 @@
 //    hit 16 disjoint bank groups.
 //  - W stage: BN rows x 4 words (the reference's packed u32 words).
 // Operands. Lane (i = l%16, g = l/16) of MFMA half h covers columns
-// 32h + 8g .. 32h + 8g + 7 of the step, in natural order: the X operand is
-// one 16-byte LDS read; the W operand is 8 codes of one word turned into four
-// bf16 pairs (c, c+1) with a byte permute, a packed 16-bit shift and a
-// three-input bit op per pair (about 1.25 VALU ops per weight), the same
-// 2*dec(c) encoding as frx_device.hpp. Each W operand feeds TM/16 MFMAs.
+// 16g + 8h .. 16g + 8h + 7 of the step, in natural order: the X operand is
+// one 16-byte LDS read; the two W operands of a lane are the 16 codes of
+// weight word g of its row, turned into bf16 pairs (c, c+1) by four masked
+// shifted copies and one byte permute per pair (unpack16_nat, about 0.94
+// VALU ops per weight), the same 2*dec(c) encoding as frx_device.hpp. Each
+// W operand feeds TM/16 MFMAs.
 #pragma once
 #include "frx_device.hpp"
 
@@ -44,6 +45,26 @@ __device__ __forceinline__ u32x4 unpack8_nat(uint32_t w, uint32_t sel0, uint32_t
   r.z = ~__builtin_bit_cast(uint32_t, __builtin_bit_cast(u16x2, y1) << s_lo) & 0xC000C000u;
   r.w = ~__builtin_bit_cast(uint32_t, __builtin_bit_cast(u16x2, y1) << s_hi) & 0xC000C000u;
   return r;
+}
+
+// A whole 16-code word as two natural-order operands: lo = codes 0..7 as
+// pairs (0,1) (2,3) (4,5) (6,7), hi = codes 8..15. m_r = ~(w << (6 - 2r)) &
+// 0xC0C0C0C0 holds code 4b + r (inverted) in the top two bits of byte b;
+// dword j (codes 2j, 2j+1) is one byte permute: byte j/2 of m_{2(j%2)} as
+// its byte 1, of m_{2(j%2)+1} as its byte 3, zeros elsewhere (selector
+// 0x0C). 15 VALU ops per 16 weights, the same 2*dec(c) bf16 encoding.
+__device__ __forceinline__ void unpack16_nat(uint32_t w, u32x4 &lo, u32x4 &hi) {
+  const uint32_t m0 = ~(w << 6) & 0xC0C0C0C0u, m1 = ~(w << 4) & 0xC0C0C0C0u;
+  const uint32_t m2 = ~(w << 2) & 0xC0C0C0C0u, m3 = ~w & 0xC0C0C0C0u;
+  uint32_t d[8];
+#pragma unroll
+  for (int j = 0; j < 8; j++) {
+    const uint32_t b = (uint32_t)(j >> 1);
+    const uint32_t sel = 0x0Cu | (b << 8) | (0x0Cu << 16) | ((4u + b) << 24);
+    d[j] = (j & 1) ? __builtin_amdgcn_perm(m3, m2, sel) : __builtin_amdgcn_perm(m1, m0, sel);
+  }
+  lo = (u32x4){d[0], d[1], d[2], d[3]};
+  hi = (u32x4){d[4], d[5], d[6], d[7]};
 }
 
 typedef __attribute__((address_space(3))) void *lds_ptr_t;
@@ -207,9 +228,9 @@ struct Gemm2 {
   }
 
   // X operand i of a step (i = h * FM + fm): tokens r0 + 16 fm, columns
-  // 32 h + 8 g .. +7.
+  // 16 g + 8 h .. +7 (the codes of weight word g of the step, half h).
   __device__ __forceinline__ static u32x4 xop(const uint32_t *stage, int r0, int g, int i) {
-    return xread(stage, r0 + (i % FM) * 16, 4 * (i / FM) + g);
+    return xread(stage, r0 + (i % FM) * 16, 2 * g + i / FM);
   }
 
   static constexpr int XD = 4;  // X operand reads run this many MFMA groups ahead
@@ -272,13 +293,9 @@ struct Gemm2 {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int wm = wave % WM, wn = wave / WM;
     const int l16 = lane & 15, g = lane >> 4;
-    // byte selectors: lanes with g odd take the upper half word (codes 8..15)
-    const uint32_t b0 = 2 * (g & 1);
-    const uint32_t sel0 = (b0 << 8) | (b0 << 24);
-    const uint32_t sel1 = ((b0 + 1) << 8) | ((b0 + 1) << 24);
     const int r0 = wm * TM + l16;
-    // weight word of fragment fn, half h, in a stage
-    const int wofs = XSTAGE + (wn * TN + l16) * 4 + (g >> 1);
+    // weight word g of fragment fn's row in a stage (both halves of the step)
+    const int wofs = XSTAGE + (wn * TN + l16) * 4 + g;
     const int nks = (K + 63) >> 6;
 
     // One stage is issued per step, always: past the last stage the last
@@ -295,19 +312,15 @@ struct Gemm2 {
     barrier_nofence();
 
     // operands of step 0
-    uint32_t wq1[FN];
-    u32x4 a0[FN], bn[XD];
+    u32x4 a0[FN], a1[FN], bn[XD];
     {
-      uint32_t wq0[FN];
+      uint32_t wq[FN];
 #pragma unroll
-      for (int fn = 0; fn < FN; fn++) {
-        wq0[fn] = lds[wofs + fn * 64];
-        wq1[fn] = lds[wofs + fn * 64 + 2];
-      }
+      for (int fn = 0; fn < FN; fn++) wq[fn] = lds[wofs + fn * 64];
 #pragma unroll
       for (int d = 0; d < XD; d++) bn[d] = xop(lds, r0, g, d);
 #pragma unroll
-      for (int fn = 0; fn < FN; fn++) a0[fn] = unpack8_nat(wq0[fn], sel0, sel1);
+      for (int fn = 0; fn < FN; fn++) unpack16_nat(wq[fn], a0[fn], a1[fn]);
     }
 
     for (int t = 0; t < nks; t++) {
@@ -316,16 +329,14 @@ struct Gemm2 {
       u32x4 b[2 * FM];
 #pragma unroll
       for (int d = 0; d < XD; d++) b[d] = bn[d];
-      u32x4 a1[FN];
       __builtin_amdgcn_sched_barrier(0);
-      // first half: columns 0..31 of the stage
+      // first half: the low 8 codes of each weight word
 #pragma unroll
       for (int fm = 0; fm < FM; fm++) {
         const int q = fm;
         b[q + XD] = xop(cur, r0, g, q + XD);
 #pragma unroll
         for (int fn = 0; fn < FN; fn++) mfma16_acc(acc[fn][fm], a0[fn], b[q]);
-        if (fm < FN) a1[fm] = unpack8_nat(wq1[fm], sel0, sel1);
         __builtin_amdgcn_sched_barrier(0);
       }
       // stage t+1 landed for every wave (the NS-3 stages issued after it may
@@ -333,9 +344,9 @@ struct Gemm2 {
       wait_vmcnt<(NS - 3) * LPW>();
       barrier_nofence();
       __builtin_amdgcn_sched_barrier(0);
-      // second half: columns 32..63, plus the next stage's loads and operands
-      uint32_t wq0n[FN], wq1n[FN];
-      u32x4 a0n[FN];
+      // second half: the high 8 codes, plus the next stage's loads and operands
+      uint32_t wqn[FN];
+      u32x4 a0n[FN], a1n[FN];
 #pragma unroll
       for (int fm = 0; fm < FM; fm++) {
         const int q = FM + fm;
@@ -343,10 +354,7 @@ struct Gemm2 {
         else bn[q + XD - 2 * FM] = xop(nxt, r0, g, q + XD - 2 * FM);
         if (fm == 0) {
 #pragma unroll
-          for (int fn = 0; fn < FN; fn++) {
-            wq0n[fn] = nxt[wofs + fn * 64];
-            wq1n[fn] = nxt[wofs + fn * 64 + 2];
-          }
+          for (int fn = 0; fn < FN; fn++) wqn[fn] = nxt[wofs + fn * 64];
         }
 #pragma unroll
         for (int fn = 0; fn < FN; fn++) mfma16_acc(acc[fn][fm], a1[fn], b[q]);
@@ -354,15 +362,15 @@ struct Gemm2 {
           const int k0 = min(t + NS - 1, nks - 1) * 64;
           issue(lds + ((t + NS - 1) % NS) * STAGE, xr, wr, xv, wv, k0, k0 >= wk ? k0 - wk : k0);
         }
-        if (fm >= 2 && fm - 2 < FN) a0n[fm - 2] = unpack8_nat(wq0n[fm - 2], sel0, sel1);
+        if (fm >= 2 && fm - 2 < FN) unpack16_nat(wqn[fm - 2], a0n[fm - 2], a1n[fm - 2]);
         __builtin_amdgcn_sched_barrier(0);
       }
 #pragma unroll
-      for (int fn = FM - 2; fn < FN; fn++) a0n[fn] = unpack8_nat(wq0n[fn], sel0, sel1);
+      for (int fn = FM - 2; fn < FN; fn++) unpack16_nat(wqn[fn], a0n[fn], a1n[fn]);
 #pragma unroll
       for (int fn = 0; fn < FN; fn++) {
         a0[fn] = a0n[fn];
-        wq1[fn] = wq1n[fn];
+        a1[fn] = a1n[fn];
       }
     }
     mfma_drain();
@@ -414,9 +422,10 @@ struct Gemm2 {
     sp24_operand(F, a, idx);
   }
 
-  // B operand of token block fm in a stage: both 32-column halves.
+  // B operand of token block fm in a stage: columns 8 g .. 8 g + 7 and
+  // 32 + 8 g .. 32 + 8 g + 7 (the sparse operand layout).
   __device__ __forceinline__ static u32x8 xop_sp(const uint32_t *stage, int r0, int g, int fm) {
-    const u32x4 lo = xop(stage, r0, g, fm), hi = xop(stage, r0, g, FM + fm);
+    const u32x4 lo = xread(stage, r0 + fm * 16, g), hi = xread(stage, r0 + fm * 16, 4 + g);
     return (u32x8){lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
   }
 
