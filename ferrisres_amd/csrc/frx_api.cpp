@@ -352,6 +352,17 @@ frx_status frx_ternary_ffn(frx_ctx *ctx, const void *x, frx_dtype xt, const uint
     if (e != hipSuccess) return hip_fail(ctx, e, "one-launch FFN");
     return FRX_OK;
   }
+  if (xt == FRX_BF16 && (int)M >= frx::GEMV_DIRECT_MIN_B && M <= 16) {
+    // h as bf16 hi/lo planes (the same M*I*4 bytes), consumed by the down
+    // GEMV without staging: at these M the fp32 rows of h do not fit LDS.
+    uint16_t *hp = reinterpret_cast<uint16_t *>(ctx->ffn_ws);
+    e = frx::launch_gemv_glu_planes(w_gate, s_gate, w_up, s_up, x, hp, (int)M, (int)H, (int)I,
+                                    act == FRX_ACT_GELU_TANH, ctx->stream);
+    if (e != hipSuccess) return hip_fail(ctx, e, "ffn gate/up launch");
+    e = frx::launch_gemv_planes(w_down, s_down, hp, y, yt == FRX_BF16, (int)M, (int)I, (int)H, ctx->stream);
+    if (e != hipSuccess) return hip_fail(ctx, e, "ffn down launch");
+    return FRX_OK;
+  }
   float *h = reinterpret_cast<float *>(ctx->ffn_ws);
   if ((st = glu_into(ctx, x, xt, w_gate, s_gate, w_up, s_up, M, H, I, act == FRX_ACT_GELU_TANH, h)) != FRX_OK)
     return st;

@@ -103,11 +103,30 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm2sp_kernel(
 #ifndef FRX_GEMM2_WM
 #define FRX_GEMM2_WM 1
 #endif
+// Tokens per tile of the 2:4 launches (64 was measured slower there: 83 /
+// 203 us against 71 / 158 us at 2048 x 4096 x 4096 / 11008).
+#ifndef FRX_GEMM2_BM
+#define FRX_GEMM2_BM 128
+#endif
 
-template <typename YT>
-static hipError_t launch_gemm2_t(const uint32_t *w, const float *scale, const void *x, void *y,
-                                 int M, int K, int N, hipStream_t stream) {
-  constexpr int BM = 128, BN = 256, WM = FRX_GEMM2_WM, WN = 4, NS = FRX_GEMM2_NS;
+// Compute units of the current device (queried once).
+static int device_cus() {
+  static std::atomic<int> cus{0};
+  int c = cus.load(std::memory_order_relaxed);
+  if (c == 0) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&c, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || c <= 0)
+      c = 256;
+    cus.store(c, std::memory_order_relaxed);
+  }
+  return c;
+}
+
+template <int BM, typename YT>
+static hipError_t launch_gemm2_bm(const uint32_t *w, const float *scale, const void *x, void *y,
+                                  int M, int K, int N, hipStream_t stream) {
+  constexpr int BN = 256, WM = FRX_GEMM2_WM, WN = 4, NS = FRX_GEMM2_NS;
   using Core = Gemm2<BM, BN, WM, WN, NS, false>;
   constexpr int lds = Core::LDS_DWORDS * 4;
   static std::atomic<uint64_t> done;
@@ -120,10 +139,23 @@ static hipError_t launch_gemm2_t(const uint32_t *w, const float *scale, const vo
   return hipGetLastError();
 }
 
+// Dense tiles: 128 tokens x 256 rows, or 64 x 256 when the 128-token grid
+// would give each CU at most one workgroup: the 64-token tile (48 KB of LDS,
+// 64 accumulation registers per lane) runs two workgroups per CU, so each
+// SIMD interleaves two waves (2048 x 4096 x 4096: 64 us against 70 us; at
+// N = 11008 the 128-token tile stays ahead, 175 against 198 us).
+template <typename YT>
+static hipError_t launch_gemm2_t(const uint32_t *w, const float *scale, const void *x, void *y,
+                                 int M, int K, int N, hipStream_t stream) {
+  const long tiles128 = (long)((M + 127) / 128) * ((N + 255) / 256);
+  if (tiles128 <= device_cus()) return launch_gemm2_bm<64, YT>(w, scale, x, y, M, K, N, stream);
+  return launch_gemm2_bm<128, YT>(w, scale, x, y, M, K, N, stream);
+}
+
 template <typename YT>
 static hipError_t launch_gemm2sp_t(const uint32_t *meta, const float *scale, const void *x, void *y,
                                    int M, int K, int N, hipStream_t stream) {
-  constexpr int BM = 128, BN = 256, WM = FRX_GEMM2_WM, WN = 4, NS = FRX_GEMM2_NS;
+  constexpr int BM = FRX_GEMM2_BM, BN = 256, WM = FRX_GEMM2_WM, WN = 4, NS = FRX_GEMM2_NS;
   using Core = Gemm2<BM, BN, WM, WN, NS, false>;
   constexpr int lds = Core::LDS_DWORDS * 4;
   static std::atomic<uint64_t> done;

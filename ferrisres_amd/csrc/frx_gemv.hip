@@ -25,6 +25,7 @@
 // frx_device.hpp). The waves' partial tiles are summed in a fixed order
 // through LDS, so results are deterministic.
 #include "frx_device.hpp"
+#include "frx_gemm2.hpp"
 #include "frx_internal.hpp"
 
 namespace frx {
@@ -310,10 +311,229 @@ static hipError_t launch_gemv_t(const uint32_t *w, const float *scale, const uin
 #undef FRX_GEMV_LAUNCH
 }
 
+// ---- bf16 activations, 8 <= B <= 16: operands straight from L2 ------------
+//
+// Staging every token's activation row in LDS needs B*K*2 bytes per
+// workgroup (352 KB at B = 16, K = 11008), more than a CU holds; the slices
+// that would take serialise the launch. Here no lane stages anything: lane
+// (r = l%16, g = l/16), which feeds token r as the MFMA's B operand, loads
+// its own 32 bytes of x[r] for each weight word it decodes (two 16-byte
+// buffer loads, the B operands of the word's two MFMAs), and the word's
+// codes become natural-order bf16 pairs (unpack16_nat), so the loaded bytes
+// are the operands as they are.
+// Word order. The four lanes of a row load 16 consecutive words (64 bytes,
+// 16 bytes each) and transpose them across the four 16-lane rows of the
+// wave (two v_permlane32_swap + two v_permlane16_swap per quad), so that
+// lane g decodes words g, g+4, g+8, g+12. The four lanes of a token then
+// read adjacent 32-byte pieces of x for the same instruction: one 128-byte
+// line per token, 16 lines per load instead of 64.
+// Planes. With XPL = 2 the activations arrive as two bf16 planes (hi, lo)
+// whose sum is an fp32 vector to 2^-17 (the decode FFN's gated product):
+// every word then loads both planes and runs four MFMAs. YSPLIT writes the
+// output the same way, as bf16 hi and lo planes of [B][N] each. The loads go through a buffer descriptor
+// whose range is the B x K activation matrix: lanes of tokens >= B and words
+// past K (or past the wave's quads) read zeros without touching memory, and
+// a zero operand cancels whatever its weight word holds, so no lane needs a
+// mask, a predicate or a clamp on the activation side. A wave issues the
+// activations of its first D words, then every weight quad of its batch
+// (whole matrix in flight), then keeps D words of activations in flight
+// ahead of the word it multiplies. The waves' tiles are reduced in a fixed
+// order through LDS, as in gemv_kernel.
+template <typename YT, int WAVES, int UMAX, int D, bool VEC, int EPI, int XPL, bool YSPLIT>
+__global__ __launch_bounds__(WAVES * 64) void gemv_direct_kernel(
+    const uint32_t *__restrict__ W, const float *__restrict__ scale,
+    const uint32_t *__restrict__ W2, const float *__restrict__ scale2,
+    const uint16_t *__restrict__ X, const uint16_t *__restrict__ X2, YT *__restrict__ Y, int B,
+    int K, int N) {
+  static_assert(XPL == 1 || XPL == 2, "activation planes");
+  static_assert(!YSPLIT || sizeof(YT) == 2, "split output is two bf16 planes");
+  constexpr int NW = EPI == GEMV_LINEAR ? 1 : 2;
+  constexpr int NWD = 4 * UMAX;  // weight words per lane in one batch
+  static_assert(D >= 1 && D <= NWD, "prefetch distance");
+  __shared__ f32x4 red[NW * WAVES * 64];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int r = lane & 15, g = lane >> 4;
+  const int wpr = K >> 4;
+  const int row = min((int)blockIdx.x * 16 + r, N - 1);  // clamped; stores are masked
+  const uint32_t *wrow[NW];
+  wrow[0] = W + (size_t)row * wpr;
+  if constexpr (NW == 2) wrow[1] = W2 + (size_t)row * wpr;
+  const int nch = (K + 63) >> 6, nq = (nch + 3) >> 2;
+  const int qa = (wave * nq) / WAVES, qb = ((wave + 1) * nq) / WAVES;  // this wave's quads
+  const __amdgpu_buffer_rsrc_t xr = buffer_rsrc(X, (uint32_t)B * (uint32_t)K * 2u);
+  const __amdgpu_buffer_rsrc_t xr2 = buffer_rsrc(XPL == 2 ? X2 : X, (uint32_t)B * (uint32_t)K * 2u);
+  const uint32_t xrow = (uint32_t)r * (uint32_t)K * 2u;  // past the range when r >= B
+  constexpr uint32_t XOOB = 0x80000000u;                   // an offset past any range
+  const bool live = r < B;
+  const int n_out = blockIdx.x * 16 + 4 * g;
+  f32x4 sc[NW];
+#pragma unroll
+  for (int m = 0; m < NW; m++) {
+    const float *sp = m == 0 ? scale : scale2;
+    sc[m] = (f32x4){0.f, 0.f, 0.f, 0.f};
+    if (wave == 0 && live && n_out < N) {
+      const int nok = min(4, N - n_out);
+      sc[m].x = sp[n_out];
+      sc[m].y = nok > 1 ? sp[n_out + 1] : 0.f;
+      sc[m].z = nok > 2 ? sp[n_out + 2] : 0.f;
+      sc[m].w = nok > 3 ? sp[n_out + 3] : 0.f;
+    }
+  }
+  f32x4 acc[NW];
+#pragma unroll
+  for (int m = 0; m < NW; m++) acc[m] = (f32x4){0.f, 0.f, 0.f, 0.f};
+
+  for (int q0 = qa; q0 < qb; q0 += UMAX) {
+    const int nwd = 4 * min(UMAX, qb - q0);  // words of this batch (per lane)
+    // word j of the batch: word 16(q0 + j/4) + 4(j%4) + g of the row
+    auto xoff = [&](int j) -> uint32_t {
+      const int col = 256 * (q0 + (j >> 2)) + 64 * (j & 3) + 16 * g;
+      return (j < nwd && col < K) ? xrow + 2u * (uint32_t)col : XOOB;
+    };
+    u32x4 xv[NWD][2 * XPL];  // [hi0, hi1, lo0, lo1]
+    auto xload = [&](int j) {
+      const uint32_t o = xoff(j);
+      xv[j][0] = __builtin_amdgcn_raw_buffer_load_b128(xr, o, 0, 0);
+      xv[j][1] = __builtin_amdgcn_raw_buffer_load_b128(xr, o + 16u, 0, 0);
+      if constexpr (XPL == 2) {
+        xv[j][2] = __builtin_amdgcn_raw_buffer_load_b128(xr2, o, 0, 0);
+        xv[j][3] = __builtin_amdgcn_raw_buffer_load_b128(xr2, o + 16u, 0, 0);
+      }
+    };
+#pragma unroll
+    for (int j = 0; j < D; j++) xload(j);
+    // every weight quad of the batch (addresses clamped to the row; words
+    // past the wave's quads or past K meet zero activations)
+    u32x4 wv[NW][UMAX];
+#pragma unroll
+    for (int u = 0; u < UMAX; u++) {
+      const int wb = 4 * (4 * (q0 + u) + g);
+#pragma unroll
+      for (int m = 0; m < NW; m++) wv[m][u] = load_chunk<VEC>(wrow[m], wb, wpr);
+    }
+#pragma unroll
+    for (int j = 0; j < NWD; j++) {
+      if (j + D < NWD) xload(j + D);
+      if (j >= nwd) continue;  // wave-uniform: past the batch's words
+      const int u = j >> 2, wi = j & 3;
+      if (wi == 0) {
+        // 4x4 transpose of quad u across the lane rows g (every lane takes
+        // part): lane g held words 4g..4g+3 of the quad and now holds words
+        // g, g+4, g+8, g+12. The off-diagonal 2x2 blocks swap between lane
+        // halves, then the off-diagonal elements of each block between
+        // adjacent rows.
+#pragma unroll
+        for (int m = 0; m < NW; m++) {
+          u32x4 &v = wv[m][u];
+          const auto p02 = __builtin_amdgcn_permlane32_swap(v.x, v.z, false, false);
+          const auto p13 = __builtin_amdgcn_permlane32_swap(v.y, v.w, false, false);
+          const auto p01 = __builtin_amdgcn_permlane16_swap(p02[0], p13[0], false, false);
+          const auto p23 = __builtin_amdgcn_permlane16_swap(p02[1], p13[1], false, false);
+          v = (u32x4){p01[0], p01[1], p23[0], p23[1]};
+        }
+      }
+#pragma unroll
+      for (int m = 0; m < NW; m++) {
+        const uint32_t wq = wi == 0 ? wv[m][u].x : wi == 1 ? wv[m][u].y : wi == 2 ? wv[m][u].z : wv[m][u].w;
+        u32x4 a0, a1;
+        unpack16_nat(wq, a0, a1);
+        acc[m] = mfma16(a0, xv[j][0], acc[m]);
+        acc[m] = mfma16(a1, xv[j][1], acc[m]);
+        if constexpr (XPL == 2) {
+          acc[m] = mfma16(a0, xv[j][2], acc[m]);
+          acc[m] = mfma16(a1, xv[j][3], acc[m]);
+        }
+      }
+    }
+  }
+
+  // Fixed-order reduction of the waves' partial tiles.
+#pragma unroll
+  for (int m = 0; m < NW; m++) red[(m * WAVES + wave) * 64 + lane] = acc[m];
+  __syncthreads();
+  if (wave == 0) {
+    f32x4 s[NW];
+#pragma unroll
+    for (int m = 0; m < NW; m++) {
+      s[m] = red[m * WAVES * 64 + lane];
+#pragma unroll
+      for (int w = 1; w < WAVES; w++) s[m] += red[(m * WAVES + w) * 64 + lane];
+      s[m] *= sc[m] * 0.5f;  // 0.5 undoes the 2*dec(c) operand encoding
+    }
+    if (live && n_out < N) {  // rows 4g..4g+3 of token r
+      f32x4 v = s[0];
+      if constexpr (NW == 2) {
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+          const float a = EPI == GEMV_GEGLU ? act_gelu_tanh(s[0][j]) : act_silu(s[0][j]);
+          v[j] = a * s[1][j];
+        }
+      }
+      if constexpr (YSPLIT) {
+        // hi = bf16(v), lo = bf16(v - hi) (lo = 0 where hi is not finite)
+        f32x4 hi, lo;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+          hi[j] = bf16_to_f32(bf16_rne(v[j]));
+          lo[j] = (__float_as_uint(hi[j]) & 0x7F800000u) == 0x7F800000u ? 0.0f : v[j] - hi[j];
+        }
+        YStore<uint16_t>::store4(reinterpret_cast<uint16_t *>(Y) + (size_t)r * N + n_out, hi,
+                                 min(4, N - n_out));
+        YStore<uint16_t>::store4(reinterpret_cast<uint16_t *>(Y) + (size_t)B * N + (size_t)r * N + n_out,
+                                 lo, min(4, N - n_out));
+      } else {
+        YStore<YT>::store4(Y + (size_t)r * N + n_out, v, min(4, N - n_out));
+      }
+    }
+  }
+}
+
+template <typename YT, int WAVES, int UMAX, int D, bool VEC, int EPI, int XPL, bool YSPLIT>
+static hipError_t launch_gemv_d(const uint32_t *w, const float *scale, const uint32_t *w2,
+                                const float *scale2, const void *x, const void *x2, void *y, int B,
+                                int K, int N, hipStream_t stream) {
+  hipLaunchKernelGGL((gemv_direct_kernel<YT, WAVES, UMAX, D, VEC, EPI, XPL, YSPLIT>),
+                     dim3((N + 15) / 16), dim3(WAVES * 64), 0, stream, w, scale, w2, scale2,
+                     reinterpret_cast<const uint16_t *>(x), reinterpret_cast<const uint16_t *>(x2),
+                     reinterpret_cast<YT *>(y), B, K, N);
+  return hipGetLastError();
+}
+
+template <typename YT, int EPI, int XPL = 1, bool YSPLIT = false>
+static hipError_t launch_gemv_direct(const uint32_t *w, const float *scale, const uint32_t *w2,
+                                     const float *scale2, const void *x, const void *x2, void *y,
+                                     int B, int K, int N, hipStream_t stream) {
+  // Waves per tile as in gemv_kernel (two to three quads per wave). D words
+  // of activations in flight per lane (8 registers per plane): 8 for the
+  // 16-wave tiles (one workgroup per CU), 4 where several workgroups of a
+  // wide matrix must be resident at once or two planes double the registers.
+  const bool vec = ((K >> 4) & 3) == 0 && (reinterpret_cast<uintptr_t>(w) & 15) == 0 &&
+                   (reinterpret_cast<uintptr_t>(w2) & 15) == 0;
+#define FRX_GEMV_D(WV, UM, DD)                                                                          \
+  return vec ? launch_gemv_d<YT, WV, UM, DD, true, EPI, XPL, YSPLIT>(w, scale, w2, scale2, x, x2, y, B, K, \
+                                                                      N, stream)                        \
+             : launch_gemv_d<YT, WV, UM, DD, false, EPI, XPL, YSPLIT>(w, scale, w2, scale2, x, x2, y, B,  \
+                                                                       K, N, stream)
+  const int nq = (K + 255) / 256;
+  if (nq <= 8) FRX_GEMV_D(4, 2, 4);
+  if (nq <= 16) FRX_GEMV_D(8, 2, 4);
+  if constexpr (EPI != GEMV_LINEAR) {
+    FRX_GEMV_D(8, 3, 4);
+  } else {
+    if (nq <= 48) FRX_GEMV_D(16, 3, XPL == 2 ? 4 : 8);
+    FRX_GEMV_D(16, 4, XPL == 2 ? 2 : 8);
+  }
+#undef FRX_GEMV_D
+}
+
 hipError_t launch_gemv(const uint32_t *w, const float *scale, const void *x,
                        int xt_bf16, void *y, int yt_bf16, int B, int K, int N,
                        hipStream_t stream) {
   constexpr int L = GEMV_LINEAR;
+  if (xt_bf16 && B >= GEMV_DIRECT_MIN_B) {
+    if (yt_bf16) return launch_gemv_direct<uint16_t, L>(w, scale, w, scale, x, x, y, B, K, N, stream);
+    return launch_gemv_direct<float, L>(w, scale, w, scale, x, x, y, B, K, N, stream);
+  }
   if (xt_bf16) {
     if (yt_bf16) return launch_gemv_t<uint16_t, uint16_t, L>(w, scale, w, scale, x, y, B, K, N, stream);
     return launch_gemv_t<uint16_t, float, L>(w, scale, w, scale, x, y, B, K, N, stream);
@@ -325,6 +545,10 @@ hipError_t launch_gemv(const uint32_t *w, const float *scale, const void *x,
 hipError_t launch_gemv_glu(const uint32_t *w_gate, const float *s_gate, const uint32_t *w_up,
                            const float *s_up, const void *x, int xt_bf16, float *h, int B, int K,
                            int N, int gelu, hipStream_t stream) {
+  if (xt_bf16 && B >= GEMV_DIRECT_MIN_B) {
+    if (gelu) return launch_gemv_direct<float, GEMV_GEGLU>(w_gate, s_gate, w_up, s_up, x, x, h, B, K, N, stream);
+    return launch_gemv_direct<float, GEMV_SWIGLU>(w_gate, s_gate, w_up, s_up, x, x, h, B, K, N, stream);
+  }
   if (xt_bf16) {
     if (gelu)
       return launch_gemv_t<uint16_t, float, GEMV_GEGLU>(w_gate, s_gate, w_up, s_up, x, h, B, K, N, stream);
@@ -352,6 +576,24 @@ hipError_t launch_glu_combine(const float *g, const float *u, float *h, size_t n
   if (gelu) hipLaunchKernelGGL((glu_combine_kernel<true>), grid, dim3(256), 0, stream, g, u, h, n);
   else hipLaunchKernelGGL((glu_combine_kernel<false>), grid, dim3(256), 0, stream, g, u, h, n);
   return hipGetLastError();
+}
+
+hipError_t launch_gemv_glu_planes(const uint32_t *w_gate, const float *s_gate, const uint32_t *w_up,
+                                  const float *s_up, const void *x, uint16_t *h_planes, int B, int K,
+                                  int N, int gelu, hipStream_t stream) {
+  if (gelu)
+    return launch_gemv_direct<uint16_t, GEMV_GEGLU, 1, true>(w_gate, s_gate, w_up, s_up, x, x, h_planes, B,
+                                                             K, N, stream);
+  return launch_gemv_direct<uint16_t, GEMV_SWIGLU, 1, true>(w_gate, s_gate, w_up, s_up, x, x, h_planes, B,
+                                                            K, N, stream);
+}
+
+hipError_t launch_gemv_planes(const uint32_t *w, const float *scale, const uint16_t *x_planes, void *y,
+                              int yt_bf16, int B, int K, int N, hipStream_t stream) {
+  const uint16_t *lo = x_planes + (size_t)B * K;
+  if (yt_bf16)
+    return launch_gemv_direct<uint16_t, GEMV_LINEAR, 2>(w, scale, w, scale, x_planes, lo, y, B, K, N, stream);
+  return launch_gemv_direct<float, GEMV_LINEAR, 2>(w, scale, w, scale, x_planes, lo, y, B, K, N, stream);
 }
 
 }  // namespace frx

@@ -21,6 +21,16 @@ inline hipError_t opt_in_lds(const void *fn, int bytes, std::atomic<uint64_t> &d
   return e;
 }
 
+// Smallest B that takes the direct-operand decode kernel (bf16 activations).
+// Below it the staged kernel is faster: its activation loads are fully
+// coalesced and at small B its rows fit LDS in one or two slices (measured at
+// the LLaMA-7B decode shapes: B = 4 staged 7.3 / 7.8 us per launch against
+// 9.3 / 8.7 us direct; B = 16 staged 14.5 / 21.3 us against 14.3 / 13.2 us).
+#ifndef FRX_GEMV_DIRECT_MIN_B
+#define FRX_GEMV_DIRECT_MIN_B 8
+#endif
+constexpr int GEMV_DIRECT_MIN_B = FRX_GEMV_DIRECT_MIN_B;
+
 // Decode GEMV, B <= 16 tokens (frx_gemv.hip).
 hipError_t launch_gemv(const uint32_t *w, const float *scale, const void *x,
                        int xt_bf16, void *y, int yt_bf16, int B, int K, int N,
@@ -30,6 +40,15 @@ hipError_t launch_gemv(const uint32_t *w, const float *scale, const void *x,
 hipError_t launch_gemv_glu(const uint32_t *w_gate, const float *s_gate, const uint32_t *w_up,
                            const float *s_up, const void *x, int xt_bf16, float *h, int B, int K,
                            int N, int gelu, hipStream_t stream);
+// The same with bf16 activations, h written as two bf16 planes (hi [B][N]
+// then lo [B][N], hi + lo = h to 2^-17), B <= 16 (frx_gemv.hip).
+hipError_t launch_gemv_glu_planes(const uint32_t *w_gate, const float *s_gate, const uint32_t *w_up,
+                                  const float *s_up, const void *x, uint16_t *h_planes, int B, int K,
+                                  int N, int gelu, hipStream_t stream);
+// Decode GEMV over activations given as bf16 hi/lo planes (hi [B][K] then
+// lo [B][K]), B <= 16 (frx_gemv.hip).
+hipError_t launch_gemv_planes(const uint32_t *w, const float *scale, const uint16_t *x_planes, void *y,
+                              int yt_bf16, int B, int K, int N, hipStream_t stream);
 // h[i] = act(g[i]) * u[i], n elements, fp32 (in place allowed: h == g).
 hipError_t launch_glu_combine(const float *g, const float *u, float *h, size_t n, int gelu,
                               hipStream_t stream);

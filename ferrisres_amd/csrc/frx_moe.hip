@@ -5,8 +5,8 @@
 // with per-row scales). The reference runs it as host loops over tokens and
 // experts with 3 GEMV dispatches per (token, expert); here it is five
 // launches:
-//   1. router_topk   one wave per token: logits (sequential f32 sums, no
-//                    FMA, bit-identical to the reference), softmax, stable
+//   1. router_topk   one lane per (token, expert): logits (sequential f32
+//                    sums, bit-identical to the reference), softmax, stable
 //                    descending sort of the probabilities, top-k, weights.
 //   2. group         one workgroup: per-expert histogram, exclusive scan and
 //                    a stable scatter of the (token, k) assignments into
@@ -76,8 +76,10 @@ __device__ __forceinline__ float ld_f32<uint16_t>(const uint16_t *p, long i) {
 
 // ---- 1. router + softmax + stable top-k -----------------------------------
 // ternary_moe.rs:152-183 / cpu_block_attn_res.rs:1150-1166. The logit of
-// expert e is a left-to-right f32 sum of x[j]*r[e][j] with no contraction,
-// so it is bit-identical to the reference for the same inputs; exp is
+// expert e is a left-to-right f32 sum of x[j]*r[e][j], each product rounded
+// to f32 before its add, so it is bit-identical to the reference for the
+// same inputs (bf16 x and r: the product is exact, and a fused multiply-add
+// rounds once to that same sum; otherwise a separate multiply and add); exp is
 // evaluated in double and rounded to f32 (correctly rounded except in
 // vanishingly rare near-halfway cases), division is IEEE.
 #pragma clang fp contract(off)
@@ -143,6 +145,7 @@ __global__ __launch_bounds__(RT_NT) void moe_router_kernel(
   const int units = rows * (CH / 8);
   constexpr int NVX = sizeof(XT) == 2 ? 1 : 2, NVR = sizeof(RT) == 2 ? 1 : 2;  // 16-byte loads per unit
   constexpr bool SAME = sizeof(XT) == sizeof(RT);
+  constexpr bool EXACT_PRODUCT = sizeof(XT) == 2 && sizeof(RT) == 2;
   // same element size: one load from the selected row; otherwise both
   // candidates are loaded and the store picks one
   struct Raw {
@@ -231,24 +234,54 @@ __global__ __launch_bounds__(RT_NT) void moe_router_kernel(
       const float *xr = buf(c & 1) + tl * RS;
       const float *rr = buf(c & 1) + (TPB + e) * RS;
       const int ncol = min(CH, H - c * CH);  // multiple of 8
-      int j = 0;
-      // 32 columns of LDS reads issued ahead of each run of dependent adds
-      for (; j + 32 <= ncol; j += 32) {
-        f32x4 xv[8], rv[8];
+      // One step of the chain: sum = fl(sum + fl(x * r)). With bf16 x and r
+      // the product is exact in f32 (8-bit significands), so a fused
+      // multiply-add rounds once to the same value and halves the issue.
+      auto step = [&](float xe, float re) {
+        if constexpr (EXACT_PRODUCT) sum = __fmaf_rn(xe, re, sum);
+        else sum = sum + xe * re;
+      };
+      // 24-column blocks, the LDS reads of block b + 1 issued before the
+      // dependent steps of block b (two register sets, unrolled by two so
+      // they alternate without copies; the read-ahead past the last block
+      // re-reads that block). 24 columns are 12 reads, so a block's reads can
+      // all be outstanding within the 4-bit LDS wait counter while the
+      // previous block is consumed.
+      constexpr int BQ = 6;  // 16-byte reads per row and block
+      const int nblk = ncol / (4 * BQ);
+      auto rd = [&](int b, f32x4 *xv, f32x4 *rv) {
+        const int j = min(b, max(nblk - 1, 0)) * (4 * BQ);
 #pragma unroll
-        for (int q = 0; q < 8; q++) {
+        for (int q = 0; q < BQ; q++) {
           xv[q] = *reinterpret_cast<const f32x4 *>(xr + j + 4 * q);
           rv[q] = *reinterpret_cast<const f32x4 *>(rr + j + 4 * q);
         }
+      };
+      auto run = [&](const f32x4 *xv, const f32x4 *rv) {
 #pragma unroll
-        for (int q = 0; q < 8; q++) {
+        for (int q = 0; q < BQ; q++) {
 #pragma unroll
-          for (int i = 0; i < 4; i++) {
-            const float pr = xv[q][i] * rv[q][i];
-            sum = sum + pr;
-          }
+          for (int i = 0; i < 4; i++) step(xv[q][i], rv[q][i]);
         }
+      };
+      // (the scheduling barriers keep each read-ahead in front of the chain
+      // it overlaps; left alone, the scheduler sinks the reads below the
+      // chain and every block starts with an LDS round trip)
+      f32x4 xa[BQ], ra[BQ], xb[BQ], rb[BQ];
+      rd(0, xa, ra);
+      int b = 0;
+      for (; b + 2 <= nblk; b += 2) {
+        rd(b + 1, xb, rb);
+        __builtin_amdgcn_sched_barrier(0);
+        run(xa, ra);
+        __builtin_amdgcn_sched_barrier(0);
+        rd(b + 2, xa, ra);
+        __builtin_amdgcn_sched_barrier(0);
+        run(xb, rb);
+        __builtin_amdgcn_sched_barrier(0);
       }
+      if (b < nblk) run(xa, ra);
+      int j = nblk * (4 * BQ);
       for (; j < ncol; j += 8) {
         f32x4 xv[2], rv[2];
 #pragma unroll
@@ -259,10 +292,7 @@ __global__ __launch_bounds__(RT_NT) void moe_router_kernel(
 #pragma unroll
         for (int q = 0; q < 2; q++) {
 #pragma unroll
-          for (int i = 0; i < 4; i++) {
-            const float pr = xv[q][i] * rv[q][i];
-            sum = sum + pr;
-          }
+          for (int i = 0; i < 4; i++) step(xv[q][i], rv[q][i]);
         }
       }
     }

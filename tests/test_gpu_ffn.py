@@ -67,8 +67,8 @@ def test_ffn_decode_llama7b_shape(ctx, M):
     assert_close_f32(host(y), ref_ffn(xw, mats, False))
 
 
-@pytest.mark.parametrize("M,H,I", [(1, 64, 96), (3, 128, 48), (7, 96, 272), (16, 256, 160),
-                                   (17, 64, 96), (40, 128, 256)])
+@pytest.mark.parametrize("M,H,I", [(1, 64, 96), (3, 128, 48), (7, 96, 272), (9, 272, 208),
+                                   (16, 256, 160), (17, 64, 96), (40, 128, 256)])
 @pytest.mark.parametrize("act", [frx.ACT_SILU, frx.ACT_GELU_TANH])
 def test_ffn_small_parity(ctx, M, H, I, act):
     xf, xb, mats = make_ffn(f"ffn/s{M}_{H}_{I}", M, H, I)
@@ -85,7 +85,7 @@ def test_ffn_f32_in_bf16_out(ctx, M):
     assert_bf16_within_1ulp(y.view(torch.int16).cpu().numpy().view(np.uint16), ref)
 
 
-@pytest.mark.parametrize("M,H,I", [(1, 4096, 11008), (4, 256, 96), (33, 128, 160)])
+@pytest.mark.parametrize("M,H,I", [(1, 4096, 11008), (4, 256, 96), (12, 272, 208), (33, 128, 160)])
 @pytest.mark.parametrize("act", [frx.ACT_SILU, frx.ACT_GELU_TANH])
 def test_glu_parity(ctx, M, H, I, act):
     xf, xb, mats = make_ffn(f"glu/{M}_{H}_{I}", M, H, I)
