@@ -112,6 +112,63 @@ static inline int router_chunk(int rows) {
   return ch > RT_CHMAX ? RT_CHMAX : ch;
 }
 
+// Softmax and stable top-k in LDS, one EP-lane group per token (lane
+// (tl, e) holds the logit of expert e for token t). A lane's rank among the
+// probabilities (greater, or equal with a lower index) reproduces the stable
+// descending sort of the reference; the two reductions (sum of exps in
+// expert order, sum of the top-k in sorted order) stay sequential on one
+// lane, as in the reference. logit: 4 * RT_NT floats of LDS.
+__device__ __forceinline__ void router_softmax_topk(float sum, float *logit, int tid, int e, int tl, int t,
+                                                    int T, int E, int EP, int top_k,
+                                                    uint32_t *__restrict__ idx_out, float *__restrict__ w_out,
+                                                    uint32_t *__restrict__ user_idx, float *__restrict__ user_w) {
+  float *pbuf = logit + RT_NT;             // [RT_NT] probabilities
+  float *tsum = pbuf + RT_NT;              // [RT_NT/EP] per-token sums
+  int *order = reinterpret_cast<int *>(tsum + RT_NT);  // [RT_NT/EP][EP]
+  logit[tid] = sum;
+  __syncthreads();
+  const float *lg = logit + tl * EP;
+  const bool live = e < E && t < T;
+  float mx = -INFINITY;
+  for (int i = 0; i < E; i++) mx = fmaxf(mx, lg[i]);
+  const float ex = live ? (float)exp((double)__fsub_rn(lg[e], mx)) : 0.0f;
+  pbuf[tid] = ex;
+  __syncthreads();
+  if (e == 0) {
+    float se = 0.0f;
+    for (int i = 0; i < E; i++) se = __fadd_rn(se, pbuf[tl * EP + i]);
+    tsum[tl] = se;
+  }
+  __syncthreads();
+  const float pe = live ? __fdiv_rn(ex, tsum[tl]) : 0.0f;
+  __syncthreads();
+  pbuf[tid] = pe;
+  __syncthreads();
+  if (live) {
+    int rank = 0;
+    for (int j = 0; j < E; j++) {
+      const float pj = pbuf[tl * EP + j];
+      rank += (pj > pe) || (pj == pe && j < e);
+    }
+    if (rank < top_k) order[tl * EP + rank] = e;
+  }
+  __syncthreads();
+  if (e == 0 && t < T) {
+    float ts = 0.0f;
+    for (int i = 0; i < top_k; i++) ts = __fadd_rn(ts, pbuf[tl * EP + order[tl * EP + i]]);
+    tsum[tl] = ts;
+  }
+  __syncthreads();
+  if (e < top_k && t < T) {
+    const int ei = order[tl * EP + e];
+    const float wi = __fdiv_rn(pbuf[tl * EP + ei], tsum[tl]);
+    idx_out[t * top_k + e] = (uint32_t)ei;
+    w_out[t * top_k + e] = wi;
+    if (user_idx) user_idx[t * top_k + e] = (uint32_t)ei;
+    if (user_w) user_w[t * top_k + e] = wi;
+  }
+}
+
 // RT_NT threads = (RT_NT/EP) tokens x EP expert lanes (EP = E rounded up to
 // a power of two). A (token, expert) lane's logit is a chain of H dependent
 // adds, so the kernel time is one chain's latency: one wave per workgroup
@@ -305,56 +362,153 @@ __global__ __launch_bounds__(RT_NT) void moe_router_kernel(
     chunk(c + 1, r0, r1);
   }
   if (c < nch) chunk(c, r1, r0);
-  // Softmax and stable top-k in LDS, one EP-lane group per token. A lane's
-  // rank among the probabilities (greater, or equal with a lower index)
-  // reproduces the stable descending sort of the reference; the two
-  // reductions (sum of exps in expert order, sum of the top-k in sorted
-  // order) stay sequential on one lane, as in the reference.
-  float *pbuf = logit + RT_NT;             // [RT_NT] probabilities
-  float *tsum = pbuf + RT_NT;              // [RT_NT/EP] per-token sums
-  int *order = reinterpret_cast<int *>(tsum + RT_NT);  // [RT_NT/EP][EP]
-  logit[tid] = sum;
-  __syncthreads();
-  const float *lg = logit + tl * EP;
-  const bool live = e < E && t < T;
-  float mx = -INFINITY;
-  for (int i = 0; i < E; i++) mx = fmaxf(mx, lg[i]);
-  const float ex = live ? (float)exp((double)__fsub_rn(lg[e], mx)) : 0.0f;
-  pbuf[tid] = ex;
-  __syncthreads();
-  if (e == 0) {
-    float se = 0.0f;
-    for (int i = 0; i < E; i++) se = __fadd_rn(se, pbuf[tl * EP + i]);
-    tsum[tl] = se;
-  }
-  __syncthreads();
-  const float pe = live ? __fdiv_rn(ex, tsum[tl]) : 0.0f;
-  __syncthreads();
-  pbuf[tid] = pe;
-  __syncthreads();
-  if (live) {
-    int rank = 0;
-    for (int j = 0; j < E; j++) {
-      const float pj = pbuf[tl * EP + j];
-      rank += (pj > pe) || (pj == pe && j < e);
+  router_softmax_topk(sum, logit, tid, e, tl, t, T, E, EP, top_k, idx_out, w_out, user_idx, user_w);
+}
+
+// Resident variant for bf16 router weights when the block's data fits LDS
+// (E = 16, H = 2048: 100 KB). Measured on the chunked kernel above, staging
+// (per-chunk global loads, conversion, LDS writes) cost as much as the
+// dependent chains and did not overlap them: one wave does both. Here the
+// router rows arrive once by LDS DMA as bf16 (no registers, no VALU), the
+// block's token rows once as f32, and the chains then read LDS only; a
+// router value is widened from its bf16 pair with one shift or mask, which
+// fits the latency of the dependent add. Row strides are padded by 16 bytes
+// so the 16 experts' (and the tokens') 16-byte reads hit disjoint banks.
+static inline int router_res_row_bytes(int H) { return (H * 2 + 1023) / 1024 * 1024 + 16; }
+static inline size_t router_res_lds(int H, int E, int tpb) {
+  return (size_t)tpb * (H + 4) * 4 + (size_t)E * router_res_row_bytes(H) + 4 * RT_NT * 4;
+}
+
+template <typename XT>
+__global__ __launch_bounds__(RT_NT) void moe_router_res_kernel(
+    const XT *__restrict__ x, const uint16_t *__restrict__ router, int T, int H, int E, int EP,
+    int top_k, int RSB, uint32_t *__restrict__ idx_out, float *__restrict__ w_out,
+    uint32_t *__restrict__ user_idx, float *__restrict__ user_w) {
+  extern __shared__ __align__(16) uint32_t smr[];
+  const int tid = threadIdx.x, e = tid % EP, tl = tid / EP;
+  const int TPB = RT_NT / EP;
+  const int t = blockIdx.x * TPB + tl;
+  const int XS = H + 4;                                   // token row stride (floats)
+  float *xs = reinterpret_cast<float *>(smr);             // [TPB][XS] f32
+  uint32_t *rs = smr + TPB * XS;                           // [E][RSB / 4] bf16 pairs
+  float *logit = reinterpret_cast<float *>(rs + E * (RSB >> 2));
+  // 1. router rows, 1 KB DMA instructions (lanes past a row's end fill that
+  //    row's padding; past the matrix the descriptor returns zeros)
+  {
+    const __amdgpu_buffer_rsrc_t rr = buffer_rsrc(router, (uint32_t)E * (uint32_t)H * 2u);
+    const int ipr = (H * 2 + 1023) >> 10;
+    for (int i = 0; i < E * ipr; i++) {
+      const int row = i / ipr, j = i - row * ipr;
+      lds_load16(rr, rs + row * (RSB >> 2) + j * 256, (uint32_t)row * (uint32_t)H * 2u + (uint32_t)j * 1024u + 16u * tid,
+                 0u);
     }
-    if (rank < top_k) order[tl * EP + rank] = e;
   }
+  // 2. the block's token rows as f32 (zeros for tokens past T): UB 8-column
+  //    units per lane in flight per batch (one batch at H = 2048, E = 16);
+  //    loads are unconditional from clamped addresses
+  {
+    constexpr int NV = sizeof(XT) == 2 ? 1 : 2;  // 16-byte loads per unit
+    constexpr int UB = sizeof(XT) == 2 ? 16 : 8;
+    const int upr = H >> 3, units = TPB * upr;
+    for (int u0 = 0; u0 < units; u0 += UB * RT_NT) {
+      u32x4 raw[UB][NV];
+#pragma unroll
+      for (int q = 0; q < UB; q++) {
+        const int u = min(u0 + q * RT_NT + tid, units - 1), rrow = u / upr, c = (u - rrow * upr) * 8;
+        const int tt = min(blockIdx.x * TPB + rrow, T - 1);
+        const u32x4 *src = reinterpret_cast<const u32x4 *>(x + (size_t)tt * H + c);
+#pragma unroll
+        for (int v = 0; v < NV; v++) raw[q][v] = src[v];
+      }
+#pragma unroll
+      for (int q = 0; q < UB; q++) {
+        const int u = u0 + q * RT_NT + tid;
+        if (u < units) {
+          const int rrow = u / upr, c = (u - rrow * upr) * 8;
+          const uint32_t m = blockIdx.x * TPB + rrow < T ? 0xFFFFFFFFu : 0u;
+          float v8[8];
+          if constexpr (NV == 1) {
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+              const uint32_t w = raw[q][0][k] & m;
+              v8[2 * k] = __uint_as_float(w << 16);
+              v8[2 * k + 1] = __uint_as_float(w & 0xFFFF0000u);
+            }
+          } else {
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+              v8[k] = __uint_as_float(raw[q][0][k] & m);
+              v8[4 + k] = __uint_as_float(raw[q][1][k] & m);
+            }
+          }
+          float4 *d = reinterpret_cast<float4 *>(xs + rrow * XS + c);
+          d[0] = make_float4(v8[0], v8[1], v8[2], v8[3]);
+          d[1] = make_float4(v8[4], v8[5], v8[6], v8[7]);
+        }
+      }
+    }
+  }
+  wait_vmcnt<0>();  // the router rows landed
   __syncthreads();
-  if (e == 0 && t < T) {
-    float ts = 0.0f;
-    for (int i = 0; i < top_k; i++) ts = __fadd_rn(ts, pbuf[tl * EP + order[tl * EP + i]]);
-    tsum[tl] = ts;
+  // 3. one dependent chain per lane (left to right, as the reference)
+  float sum = 0.0f;
+  if (e < E && t < T) {
+#pragma clang fp contract(off)
+    const float *xr = xs + tl * XS;
+    const uint32_t *rw = rs + e * (RSB >> 2);
+    constexpr bool EXACT_PRODUCT = sizeof(XT) == 2;  // bf16 x bf16: exact in f32
+    auto step = [&](float xe, float re) {
+      if constexpr (EXACT_PRODUCT) sum = __fmaf_rn(xe, re, sum);
+      else sum = sum + xe * re;
+    };
+    // 32-column blocks: 8 token reads + 4 router reads (12, within the LDS
+    // wait counter), read one block ahead of the chain
+    const int nblk = H >> 5;
+    auto rd = [&](int b, f32x4 *xv, u32x4 *rv) {
+      const int j = min(b, max(nblk - 1, 0)) * 32;
+#pragma unroll
+      for (int q = 0; q < 8; q++) xv[q] = *reinterpret_cast<const f32x4 *>(xr + j + 4 * q);
+#pragma unroll
+      for (int q = 0; q < 4; q++) rv[q] = *reinterpret_cast<const u32x4 *>(rw + (j >> 1) + 4 * q);
+    };
+    auto run = [&](const f32x4 *xv, const u32x4 *rv) {
+#pragma unroll
+      for (int q = 0; q < 4; q++) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {  // router columns 8q + 2i, 8q + 2i + 1
+          const uint32_t d = rv[q][i];
+          step(xv[2 * q + (i >> 1)][(2 * i) & 3], __uint_as_float(d << 16));
+          step(xv[2 * q + (i >> 1)][(2 * i + 1) & 3], __uint_as_float(d & 0xFFFF0000u));
+        }
+      }
+    };
+    f32x4 xa[8], xb[8];
+    u32x4 ra[4], rb[4];
+    rd(0, xa, ra);
+    int b = 0;
+    for (; b + 2 <= nblk; b += 2) {
+      rd(b + 1, xb, rb);
+      __builtin_amdgcn_sched_barrier(0);
+      run(xa, ra);
+      __builtin_amdgcn_sched_barrier(0);
+      rd(b + 2, xa, ra);
+      __builtin_amdgcn_sched_barrier(0);
+      run(xb, rb);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    if (b < nblk) run(xa, ra);
+    for (int j = nblk * 32; j < H; j += 8) {  // H % 32 columns, 8 at a time
+      const f32x4 x0 = *reinterpret_cast<const f32x4 *>(xr + j), x1 = *reinterpret_cast<const f32x4 *>(xr + j + 4);
+      const u32x4 r = *reinterpret_cast<const u32x4 *>(rw + (j >> 1));
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const f32x4 &xv = i < 2 ? x0 : x1;
+        step(xv[(2 * i) & 3], __uint_as_float(r[i] << 16));
+        step(xv[(2 * i + 1) & 3], __uint_as_float(r[i] & 0xFFFF0000u));
+      }
+    }
   }
-  __syncthreads();
-  if (e < top_k && t < T) {
-    const int ei = order[tl * EP + e];
-    const float wi = __fdiv_rn(pbuf[tl * EP + ei], tsum[tl]);
-    idx_out[t * top_k + e] = (uint32_t)ei;
-    w_out[t * top_k + e] = wi;
-    if (user_idx) user_idx[t * top_k + e] = (uint32_t)ei;
-    if (user_w) user_w[t * top_k + e] = wi;
-  }
+  router_softmax_topk(sum, logit, tid, e, tl, t, T, E, EP, top_k, idx_out, w_out, user_idx, user_w);
 }
 
 // ---- 2. histogram / scan / stable scatter / tile schedule -----------------
@@ -531,8 +685,11 @@ __global__ __launch_bounds__(256) void moe_down_kernel(
 // lo halves of h2's rows times W_down in separate workgroups (blockIdx.z),
 // each into its own fp32 partial [A][H]; the combine adds the two.
 constexpr int MOE2_BN = 256;
-using MoeGateUpCore = Gemm2<MOE_BM, MOE2_BN, 1, 4, 4, true>;
-using MoeDownCore = Gemm2<MOE_BM, MOE2_BN, 1, 4, 4, false>;
+#ifndef FRX_MOE_NS
+#define FRX_MOE_NS 4
+#endif
+using MoeGateUpCore = Gemm2<MOE_BM, MOE2_BN, 1, 4, FRX_MOE_NS, true>;
+using MoeDownCore = Gemm2<MOE_BM, MOE2_BN, 1, 4, FRX_MOE_NS, false>;
 
 __global__ __launch_bounds__(256) void moe_gateup2_kernel(
     const GateUpArgs args, const uint16_t *__restrict__ x, int T, int H, int I,
@@ -671,7 +828,21 @@ hipError_t launch_moe(const void *x, int xt_bf16, const void *router,
     const hipError_t e = opt_in_lds(fns[v], 160 * 1024, done[v]);
     if (e != hipSuccess) return e;
   }
-  if (xt_bf16 && rt_bf16)
+  const size_t res_lds = router_res_lds(H, E, tpb);
+  if (rt_bf16 && res_lds <= 160 * 1024) {
+    static std::atomic<uint64_t> done_res[2];
+    const void *fn = xt_bf16 ? reinterpret_cast<const void *>(&moe_router_res_kernel<uint16_t>)
+                             : reinterpret_cast<const void *>(&moe_router_res_kernel<float>);
+    const hipError_t e = opt_in_lds(fn, 160 * 1024, done_res[xt_bf16 ? 0 : 1]);
+    if (e != hipSuccess) return e;
+    const int rsb = router_res_row_bytes(H);
+    if (xt_bf16)
+      hipLaunchKernelGGL((moe_router_res_kernel<uint16_t>), rg, dim3(RT_NT), res_lds, stream, (const uint16_t *)x,
+                         (const uint16_t *)router, T, H, E, EP, top_k, rsb, ws.idx, ws.wts, topk_idx, topk_w);
+    else
+      hipLaunchKernelGGL((moe_router_res_kernel<float>), rg, dim3(RT_NT), res_lds, stream, (const float *)x,
+                         (const uint16_t *)router, T, H, E, EP, top_k, rsb, ws.idx, ws.wts, topk_idx, topk_w);
+  } else if (xt_bf16 && rt_bf16)
     hipLaunchKernelGGL((moe_router_kernel<uint16_t, uint16_t>), rg, dim3(RT_NT), rlds, stream,
                        (const uint16_t *)x, (const uint16_t *)router, T, H, E, EP, top_k, rch, ws.idx, ws.wts, topk_idx, topk_w);
   else if (xt_bf16)

@@ -13,7 +13,7 @@
  * transcribed as data into tests/golden/reference_kats.json), closed-form
  * invariants, and brute force in float64 on small inputs. The reference is
  * Rust and no Rust toolchain exists here, so the reference itself cannot be
- * built or run ("Oracle"); the bit-level f32 rounding sequence
+ * built or run; the bit-level f32 rounding sequence
  * of the Rust build is therefore matched by construction (same loop order,
  * same libm) and pinned only by the KATs, which the reference checks at 1e-5.
  */
