@@ -97,9 +97,10 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm2sp_kernel(
 #define FRX_GEMM2_NS 4
 #endif
 // Waves across the token dimension of a 128 x 256 tile: 1 gives 4 waves of
-// 128 x 64 (one per SIMD); 2 gives 8 waves of 64 x 64 (two per SIMD, half
-// the operand reuse per wave), measured slower (2:4: 81 / 220 us against
-// 72 / 173 us at N = 4096 / 11008).
+// 128 tokens x 64 rows (one per SIMD); 2 gives 2 x 2 waves of 64 tokens x
+// 128 rows, which halves the activation reads from LDS but doubles each
+// wave's weight decode, measured slower (2048 x 4096 x 4096 / 11008: dense
+// 76 / 184 us against 65 / 175 us, 2:4 87 / 195 us against 71 / 157 us).
 #ifndef FRX_GEMM2_WM
 #define FRX_GEMM2_WM 1
 #endif
@@ -126,7 +127,7 @@ static int device_cus() {
 template <int BM, typename YT>
 static hipError_t launch_gemm2_bm(const uint32_t *w, const float *scale, const void *x, void *y,
                                   int M, int K, int N, hipStream_t stream) {
-  constexpr int BN = 256, WM = FRX_GEMM2_WM, WN = 4, NS = FRX_GEMM2_NS;
+  constexpr int BN = 256, WM = FRX_GEMM2_WM, WN = 4 / FRX_GEMM2_WM, NS = FRX_GEMM2_NS;
   using Core = Gemm2<BM, BN, WM, WN, NS, false>;
   constexpr int lds = Core::LDS_DWORDS * 4;
   static std::atomic<uint64_t> done;
@@ -147,15 +148,17 @@ static hipError_t launch_gemm2_bm(const uint32_t *w, const float *scale, const v
 template <typename YT>
 static hipError_t launch_gemm2_t(const uint32_t *w, const float *scale, const void *x, void *y,
                                  int M, int K, int N, hipStream_t stream) {
+#if FRX_GEMM2_WM == 1
   const long tiles128 = (long)((M + 127) / 128) * ((N + 255) / 256);
   if (tiles128 <= device_cus()) return launch_gemm2_bm<64, YT>(w, scale, x, y, M, K, N, stream);
+#endif
   return launch_gemm2_bm<128, YT>(w, scale, x, y, M, K, N, stream);
 }
 
 template <typename YT>
 static hipError_t launch_gemm2sp_t(const uint32_t *meta, const float *scale, const void *x, void *y,
                                    int M, int K, int N, hipStream_t stream) {
-  constexpr int BM = FRX_GEMM2_BM, BN = 256, WM = FRX_GEMM2_WM, WN = 4, NS = FRX_GEMM2_NS;
+  constexpr int BM = FRX_GEMM2_BM, BN = 256, WM = FRX_GEMM2_WM, WN = 4 / FRX_GEMM2_WM, NS = FRX_GEMM2_NS;
   using Core = Gemm2<BM, BN, WM, WN, NS, false>;
   constexpr int lds = Core::LDS_DWORDS * 4;
   static std::atomic<uint64_t> done;

@@ -270,7 +270,7 @@ struct Gemm2 {
                              int m_count, const uint32_t *W, int n_count, int K,
                              f32x4 (&acc)[FN][FM], const uint32_t *W2 = nullptr, int wk = 0, int ldx = 0) {
     static_assert(NS >= 3, "the ring needs a stage being read, one landing and one free");
-    static_assert(FM >= 4 && FN <= FM && XD <= FM, "operand schedule");
+    static_assert(FM >= 4 && XD <= FM, "operand schedule");
     if (wk == 0) wk = K;
     if (ldx == 0) ldx = K;
     const bool dual = W2 != nullptr;

@@ -95,6 +95,8 @@ struct MoeWorkspace {
   uint16_t *h_lo;      // [T*k][I] lo plane
   float *dout;         // [T*k][H] down-projection rows
   float *dout_lo;      // [T*k][H] second partial (engine-2 path: lo halves)
+  float *dout2;        // [2][T*k][H] engine-2 path with split K: the second
+                       // K half's hi and lo partials
 };
 size_t moe_workspace_bytes(int T, int H, int I, int E, int top_k);
 void moe_workspace_carve(void *base, int T, int H, int I, int E, int top_k,

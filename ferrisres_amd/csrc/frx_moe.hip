@@ -42,6 +42,7 @@ size_t moe_workspace_bytes(int T, int H, int I, int E, int top_k) {
   b += align256(4);                     // ntiles
   b += align256(A * I * 2) * 2;         // h planes
   b += align256(A * H * 4) * 2;         // dout, dout_lo
+  b += align256(A * H * 4 * 2);         // dout2 (second K half)
   return b;
 }
 
@@ -63,6 +64,7 @@ void moe_workspace_carve(void *base, int T, int H, int I, int E, int top_k,
   ws->h_lo = reinterpret_cast<uint16_t *>(take(A * I * 2));
   ws->dout = reinterpret_cast<float *>(take(A * H * 4));
   ws->dout_lo = reinterpret_cast<float *>(take(A * H * 4));
+  ws->dout2 = reinterpret_cast<float *>(take(A * H * 4 * 2));
 }
 
 template <typename T>
@@ -685,10 +687,17 @@ __global__ __launch_bounds__(256) void moe_down_kernel(
 // lo halves of h2's rows times W_down in separate workgroups (blockIdx.z),
 // each into its own fp32 partial [A][H]; the combine adds the two.
 constexpr int MOE2_BN = 256;
+// gate/up tile: MOE_GU_BN / 2 gate rows and the same up rows (128 measured
+// slower at the 512-token, 16-expert layer: 92 us against 89 us, although
+// its 2112 workgroups fill the CUs more evenly than 1056)
+#ifndef FRX_MOE_GU_BN
+#define FRX_MOE_GU_BN 256
+#endif
+constexpr int MOE_GU_BN = FRX_MOE_GU_BN;
 #ifndef FRX_MOE_NS
 #define FRX_MOE_NS 4
 #endif
-using MoeGateUpCore = Gemm2<MOE_BM, MOE2_BN, 1, 4, FRX_MOE_NS, true>;
+using MoeGateUpCore = Gemm2<MOE_BM, MOE_GU_BN, 1, 4, FRX_MOE_NS, true>;
 using MoeDownCore = Gemm2<MOE_BM, MOE2_BN, 1, 4, FRX_MOE_NS, false>;
 
 __global__ __launch_bounds__(256) void moe_gateup2_kernel(
@@ -703,18 +712,19 @@ __global__ __launch_bounds__(256) void moe_gateup2_kernel(
   const int e = tiles[2 * tile], mstart = tiles[2 * tile + 1];
   const int mcount = min(MOE_BM, counts[e] - mstart);
   const int row0 = offsets[e] + mstart;
-  const int n0 = blockIdx.x * (MOE2_BN / 2), nc = min(MOE2_BN / 2, I - n0);
+  const int n0 = blockIdx.x * (MOE_GU_BN / 2), nc = min(MOE_GU_BN / 2, I - n0);
   f32x4 acc[Core::FN][Core::FM];
   Core::run(lds, x, (uint32_t)T * (uint32_t)H * 2u, perm_token + row0, mcount,
             args.wg[e] + (size_t)n0 * (H >> 4), nc, H, acc, args.wu[e] + (size_t)n0 * (H >> 4), H);
   // Epilogue: fragments to LDS in two passes of 32 tokens (row pitch
-  // MOE2_BN + 16 floats); each thread then owns 4 gate columns (and the
-  // same 4 up columns 128 further) of 4 tokens per pass.
-  constexpr int PF = MOE2_BN + 16, P = 2, TMP = MOE_BM / P, FMP = Core::FM / P;
+  // MOE_GU_BN + 16 floats); each thread then owns 4 gate columns (and the
+  // same 4 up columns MOE_GU_BN / 2 further) of a run of tokens per pass.
+  constexpr int PF = MOE_GU_BN + 16, P = 2, TMP = MOE_BM / P, FMP = Core::FM / P;
   static_assert(TMP * PF <= Core::LDS_DWORDS, "epilogue staging");
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, l16 = lane & 15, g = lane >> 4;
   float *st = reinterpret_cast<float *>(lds);
-  const int c = threadIdx.x % 32, rr = threadIdx.x / 32;
+  constexpr int CT = MOE_GU_BN / 8, RT = 256 / CT;  // column threads, rows per iteration
+  const int c = threadIdx.x % CT, rr = threadIdx.x / CT;
   f32x4 sgv, suv;
 #pragma unroll
   for (int j = 0; j < 4; j++) {
@@ -731,11 +741,11 @@ __global__ __launch_bounds__(256) void moe_gateup2_kernel(
         *reinterpret_cast<f32x4 *>(st + (fmi * 16 + l16) * PF + wave * Core::TN + fn * 16 + 4 * g) =
             acc[fn][p * FMP + fmi];
     __syncthreads();
-    for (int lr = rr; lr < TMP; lr += 8) {
+    for (int lr = rr; lr < TMP; lr += RT) {
       const int m = p * TMP + lr;
       if (m >= mcount || 4 * c >= nc) continue;
       const f32x4 gv = *reinterpret_cast<const f32x4 *>(st + lr * PF + 4 * c) * sgv;
-      const f32x4 uv = *reinterpret_cast<const f32x4 *>(st + lr * PF + MOE2_BN / 2 + 4 * c) * suv;
+      const f32x4 uv = *reinterpret_cast<const f32x4 *>(st + lr * PF + MOE_GU_BN / 2 + 4 * c) * suv;
       uint32_t hh[4], hl[4];
 #pragma unroll
       for (int j = 0; j < 4; j++) {
@@ -757,11 +767,17 @@ __global__ __launch_bounds__(256) void moe_gateup2_kernel(
   }
 }
 
+// blockIdx.z = half + 2 * part: the hi or lo half of h (two fp32 partials,
+// as in the reference's single f32 sum to 2^-17) times columns
+// [part * ks, part * ks + ks) of the down rows. ks = I / 2 when I % 128 == 0:
+// the split gives three workgroups per CU at the 512-token, 16-expert layer
+// instead of a 2 / 1 mix (384 workgroups); the partials are summed by the
+// combine in a fixed order.
 __global__ __launch_bounds__(256) void moe_down2_kernel(
-    const DownArgs args, const uint16_t *__restrict__ h2, int H, int I,
+    const DownArgs args, const uint16_t *__restrict__ h2, int H, int I, int ks,
     const int *__restrict__ tiles, const int *__restrict__ ntiles,
     const int *__restrict__ counts, const int *__restrict__ offsets,
-    float *__restrict__ dout, float *__restrict__ dout_lo) {
+    float *__restrict__ dout, float *__restrict__ dout_lo, float *__restrict__ dout2, int A) {
   using Core = MoeDownCore;
   extern __shared__ __align__(16) uint32_t lds[];
   const int tile = blockIdx.y;
@@ -770,21 +786,26 @@ __global__ __launch_bounds__(256) void moe_down2_kernel(
   const int mcount = min(MOE_BM, counts[e] - mstart);
   const int row0 = offsets[e] + mstart;
   const int n0 = blockIdx.x * MOE2_BN, nc = min(MOE2_BN, H - n0);
-  const int half = blockIdx.z;  // 0: hi, 1: lo
+  const int half = blockIdx.z & 1, part = blockIdx.z >> 1;  // half 0: hi, 1: lo
+  const int k0 = part * ks;
   f32x4 acc[Core::FN][Core::FM];
-  Core::run(lds, h2 + (size_t)row0 * (2 * (size_t)I) + half * I, (uint32_t)mcount * (uint32_t)I * 4u - half * I * 2u,
-            nullptr, mcount, args.wd[e] + (size_t)n0 * (I >> 4), nc, I, acc, nullptr, I, 2 * I);
-  Core::template store_tile<float>(lds, acc, args.sd[e], half ? dout_lo : dout, (size_t)H, row0, mcount, n0, nc);
+  Core::run(lds, h2 + (size_t)row0 * (2 * (size_t)I) + half * I + k0,
+            (uint32_t)mcount * (uint32_t)I * 4u - (uint32_t)(half * I + k0) * 2u, nullptr, mcount,
+            args.wd[e] + (size_t)n0 * (I >> 4) + (k0 >> 4), nc, ks, acc, nullptr, I, 2 * I);
+  float *out = part == 0 ? (half ? dout_lo : dout) : dout2 + (size_t)half * A * H;
+  Core::template store_tile<float>(lds, acc, args.sd[e], out, (size_t)H, row0, mcount, n0, nc);
 }
 
 // ---- 5. combine ---------------------------------------------------------------
 // cpu_block_attn_res.rs:1179 `expert_outputs[t*hd+d] += w * down[d]`, k order.
 // dout_lo != nullptr: the down rows arrive as two partials (hi and lo halves
-// of the activation), d = dout + dout_lo.
+// of the activation), d = dout + dout_lo; dout2 != nullptr: two more (the
+// second K half's hi and lo, A rows apart), d = (dout + dout_lo) + (hi2 + lo2).
 template <typename YT>
 __global__ __launch_bounds__(256) void moe_combine_kernel(
-    const float *__restrict__ dout, const float *__restrict__ dout_lo, const float *__restrict__ wts,
-    const int *__restrict__ inv, int H, int top_k, YT *__restrict__ y) {
+    const float *__restrict__ dout, const float *__restrict__ dout_lo, const float *__restrict__ dout2,
+    int A, const float *__restrict__ wts, const int *__restrict__ inv, int H, int top_k,
+    YT *__restrict__ y) {
   const int t = blockIdx.x;
   for (int j = threadIdx.x * 4; j < H; j += 1024) {  // H % 16 == 0
     f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -794,6 +815,9 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(
       const long o = (long)inv[t * top_k + k] * H + j;
       f32x4 d = *reinterpret_cast<const f32x4 *>(dout + o);
       if (dout_lo) d = d + *reinterpret_cast<const f32x4 *>(dout_lo + o);
+      if (dout2)
+        d = d + (*reinterpret_cast<const f32x4 *>(dout2 + o) +
+                 *reinterpret_cast<const f32x4 *>(dout2 + (long)A * H + o));
       const f32x4 prod = d * w;
       acc = acc + prod;
     }
@@ -871,6 +895,7 @@ hipError_t launch_moe(const void *x, int xt_bf16, const void *router,
     ga.su[i] = v ? s_up[i] : nullptr;
   }
   bool engine2 = xt_bf16 && H % 64 == 0 && I % 64 == 0;
+  bool down_split = false;  // engine-2 down GEMM in two K halves (four partials)
   for (int i = 0; i < E && engine2; i++)
     engine2 = ((reinterpret_cast<uintptr_t>(w_gate[i]) | reinterpret_cast<uintptr_t>(w_up[i]) |
                 reinterpret_cast<uintptr_t>(w_down[i])) & 15) == 0;
@@ -880,14 +905,16 @@ hipError_t launch_moe(const void *x, int xt_bf16, const void *router,
     da.sd[i] = i < E ? s_down[i] : nullptr;
   }
   if (engine2) {
-    const dim3 g1((I + MOE2_BN / 2 - 1) / (MOE2_BN / 2), max_tiles);
+    const dim3 g1((I + MOE_GU_BN / 2 - 1) / (MOE_GU_BN / 2), max_tiles);
     hipLaunchKernelGGL(moe_gateup2_kernel, g1, dim3(256), MoeGateUpCore::LDS_DWORDS * 4, stream, ga,
                        (const uint16_t *)x, T, H, I, ws.tiles, ws.ntiles, ws.counts, ws.offsets,
                        ws.perm_token, ws.h_hi, gelu);
     if ((err = hipGetLastError()) != hipSuccess) return err;
-    const dim3 g2((H + MOE2_BN - 1) / MOE2_BN, max_tiles, 2);
+    const int ks = I % 128 == 0 ? I / 2 : I;
+    const dim3 g2((H + MOE2_BN - 1) / MOE2_BN, max_tiles, ks < I ? 4 : 2);
     hipLaunchKernelGGL(moe_down2_kernel, g2, dim3(256), MoeDownCore::LDS_DWORDS * 4, stream, da, ws.h_hi,
-                       H, I, ws.tiles, ws.ntiles, ws.counts, ws.offsets, ws.dout, ws.dout_lo);
+                       H, I, ks, ws.tiles, ws.ntiles, ws.counts, ws.offsets, ws.dout, ws.dout_lo, ws.dout2, A);
+    down_split = ks < I;
     if ((err = hipGetLastError()) != hipSuccess) return err;
   } else {
   dim3 g1((I + MOE_BN - 1) / MOE_BN, max_tiles);
@@ -907,10 +934,12 @@ hipError_t launch_moe(const void *x, int xt_bf16, const void *router,
   // 5. combine
   if (yt_bf16)
     hipLaunchKernelGGL((moe_combine_kernel<uint16_t>), dim3(T), dim3(256), 0, stream, ws.dout,
-                       engine2 ? ws.dout_lo : nullptr, ws.wts, ws.inv, H, top_k, (uint16_t *)y);
+                       engine2 ? ws.dout_lo : nullptr, down_split ? ws.dout2 : nullptr, A, ws.wts, ws.inv,
+                       H, top_k, (uint16_t *)y);
   else
     hipLaunchKernelGGL((moe_combine_kernel<float>), dim3(T), dim3(256), 0, stream, ws.dout,
-                       engine2 ? ws.dout_lo : nullptr, ws.wts, ws.inv, H, top_k, (float *)y);
+                       engine2 ? ws.dout_lo : nullptr, down_split ? ws.dout2 : nullptr, A, ws.wts, ws.inv,
+                       H, top_k, (float *)y);
   return hipGetLastError();
 }
 
