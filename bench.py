@@ -20,7 +20,8 @@ matrices at B=1, timed on this host's cores.
 
 extra: the decode FFN of the same layer through frx_ternary_ffn (one launch
 with a grid barrier, and the two-launch execution: gate/up/SiLU launch +
-fp32-input down launch), prefill GEMM (X[2048,4096] x
+fp32-input down launch), the same decode step at B = 4 and 16 (default
+run), prefill GEMM (X[2048,4096] x
 W[N,4096], N in {4096, 11008}), 2:4 sparse GEMM and the MoE expert layer, as
 TFLOP/s and fraction of the dense bf16 MFMA peak.
 """
@@ -245,6 +246,44 @@ def main():
         f"gate/up {fused['two_launch']['gate_up_silu_avg_us']} us, down {fused['two_launch']['down_f32_in_avg_us']} us")
 
     extra = {"decode_ffn_fused_llama7b": fused}
+    if B == 1 and not args.no_extra:
+        # The decode configuration's other batch sizes: the same three
+        # projections, weights rotating, timed the same way (B < 8: staged
+        # gemv_kernel; B >= 8: gemv_direct_kernel).
+        batches = {}
+        for bx in (4, 16):
+            _, xbx = synth.activations("bench/decode", "x", bx, H)
+            _, hbx = synth.activations("bench/decode", "h", bx, I)
+            xx = torch.from_numpy(xbx.view(np.int16)).to(dev).view(torch.bfloat16)
+            xdx = torch.from_numpy(hbx.view(np.int16)).to(dev).view(torch.bfloat16)
+            gx = torch.empty((bx, I), dtype=torch.bfloat16, device=dev)
+            ux = torch.empty((bx, I), dtype=torch.bfloat16, device=dev)
+            yx = torch.empty((bx, H), dtype=torch.bfloat16, device=dev)
+
+            def stepx(i, xx=xx, xdx=xdx, gx=gx, ux=ux, yx=yx):
+                wg, wu, wd = W[i % copies]
+                ctx.ternary_linear(wg, s_g, xx, gx)
+                ctx.ternary_linear(wu, s_u, xx, ux)
+                ctx.ternary_linear(wd, s_d, xdx, yx)
+            with torch.cuda.stream(stream):
+                for i in range(2):
+                    stepx(i)
+            torch.cuda.synchronize()
+            el_x, _ = timed(lambda: [stepx(i) for i in range(args.steps)])
+            bytes_x = 2 * gemv_bytes(I, H, bx) + gemv_bytes(H, I, bx)
+            tgu_x = per_launch(lambda i: (ctx.ternary_linear(W[i][0], s_g, xx, gx),
+                                          ctx.ternary_linear(W[i][1], s_u, xx, ux)), 2, reps)
+            tdn_x = per_launch(lambda i: ctx.ternary_linear(W[i][2], s_d, xdx, yx), 1, reps)
+            batches[f"B{bx}"] = {
+                "us_per_step": round(el_x / args.steps * 1e6, 2),
+                "gb_s": round(bytes_x / (el_x / args.steps) / 1e9, 1),
+                "hbm_fraction": round(bytes_x / (el_x / args.steps) / 1e9 / HBM_PEAK_GBS, 4),
+                "avg_us": {"11008x4096": round(tgu_x * 1e6, 3), "4096x11008": round(tdn_x * 1e6, 3)},
+                "kernel": "frx::gemv_kernel (staged)" if bx < 8 else "frx::gemv_direct_kernel",
+            }
+            log(f"bench: decode GEMV B={bx}: {batches[f'B{bx}']['us_per_step']} us/step, "
+                f"{batches[f'B{bx}']['gb_s']} GB/s")
+        extra["decode_gemv_llama7b_batches"] = batches
     if not args.no_extra:
         extra.update(run_extra(torch, frx, synth, ctx, stream, dev))
 
