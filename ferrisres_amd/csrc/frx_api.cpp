@@ -339,6 +339,9 @@ frx_status frx_ternary_ffn(frx_ctx *ctx, const void *x, frx_dtype xt, const uint
       e = hipMalloc(&p, frx::ffn1_barrier_bytes());
       if (e != hipSuccess) return hip_fail(ctx, e, "FFN barrier allocation");
       e = hipMemset(p, 0, frx::ffn1_barrier_bytes());
+      // the legacy stream of hipMemset does not order against a non-blocking
+      // caller stream: wait for it here (first use only)
+      if (e == hipSuccess) e = hipDeviceSynchronize();
       if (e != hipSuccess) {
         hipFree(p);
         return hip_fail(ctx, e, "FFN barrier initialisation");

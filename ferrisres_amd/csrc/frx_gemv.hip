@@ -499,6 +499,149 @@ static hipError_t launch_gemv_d(const uint32_t *w, const float *scale, const uin
   return hipGetLastError();
 }
 
+// ---- bf16 activations, B >= 8, wide matrices: taller tiles ---------------
+//
+// At B = 16 the direct kernel's time is its activation loads (ablation at
+// 11008x4096 / 4096x11008: 14.1 / 12.4 us per launch, 5.3 / 5.2 us with the
+// activation loads removed, decode and reduction under 0.7 us): every
+// 16-row tile reads all of x, 90 MB per launch from L2. Here a tile is
+// 16 * RS rows and each activation load feeds RS row blocks (RS unpacks and
+// 2 * RS MFMAs per word), which divides that traffic by RS. Used where the
+// taller tiles still give every CU a workgroup (11008x4096: 14.3 -> 12.2 us
+// at RS = 2). Where they would not, the direct kernel stays: splitting K
+// over workgroups with an in-kernel combine (device-coherent partials and a
+// per-tile counter) was measured: the combine's chain of memory round trips
+// cost what the halved traffic saved (4096x11008: 12.9 us against 12.8 us),
+// and 32-row tiles without a split leave half the CUs idle there (15.6 us).
+template <typename YT, int WAVES, int UMAX, int D, bool VEC, int RS>
+__global__ __launch_bounds__(WAVES * 64) void gemv_tall_kernel(
+    const uint32_t *__restrict__ W, const float *__restrict__ scale, const uint16_t *__restrict__ X,
+    YT *__restrict__ Y, int B, int K, int N) {
+  constexpr int NWD = 4 * UMAX;  // weight words per lane and row block in one batch
+  static_assert(D >= 1 && D <= NWD, "prefetch distance");
+  __shared__ f32x4 red[RS * WAVES * 64];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int r = lane & 15, g = lane >> 4;
+  const int wpr = K >> 4;
+  const int n_base = blockIdx.x * 16 * RS;
+  const uint32_t *wrow[RS];
+#pragma unroll
+  for (int rs = 0; rs < RS; rs++) wrow[rs] = W + (size_t)min(n_base + 16 * rs + r, N - 1) * wpr;
+  const int nch = (K + 63) >> 6, nq = (nch + 3) >> 2;
+  const int qa = (wave * nq) / WAVES, qb = ((wave + 1) * nq) / WAVES;  // this wave's quads
+  const __amdgpu_buffer_rsrc_t xr = buffer_rsrc(X, (uint32_t)B * (uint32_t)K * 2u);
+  const uint32_t xrow = (uint32_t)r * (uint32_t)K * 2u;  // past the range when r >= B
+  constexpr uint32_t XOOB = 0x80000000u;
+  const bool live = r < B;
+  f32x4 sc[RS];
+#pragma unroll
+  for (int rs = 0; rs < RS; rs++) {
+    const int n_out = n_base + 16 * rs + 4 * g;
+    sc[rs] = (f32x4){0.f, 0.f, 0.f, 0.f};
+    if (wave == 0 && live && n_out < N) {
+      const int nok = min(4, N - n_out);
+      sc[rs].x = scale[n_out];
+      sc[rs].y = nok > 1 ? scale[n_out + 1] : 0.f;
+      sc[rs].z = nok > 2 ? scale[n_out + 2] : 0.f;
+      sc[rs].w = nok > 3 ? scale[n_out + 3] : 0.f;
+    }
+  }
+  f32x4 acc[RS];
+#pragma unroll
+  for (int rs = 0; rs < RS; rs++) acc[rs] = (f32x4){0.f, 0.f, 0.f, 0.f};
+
+  for (int q0 = qa; q0 < qb; q0 += UMAX) {
+    const int nwd = 4 * min(UMAX, qb - q0);
+    auto xoff = [&](int j) -> uint32_t {
+      const int col = 256 * (q0 + (j >> 2)) + 64 * (j & 3) + 16 * g;
+      return (j < nwd && col < K) ? xrow + 2u * (uint32_t)col : XOOB;
+    };
+    u32x4 xv[NWD][2];
+    auto xload = [&](int j) {
+      const uint32_t o = xoff(j);
+      xv[j][0] = __builtin_amdgcn_raw_buffer_load_b128(xr, o, 0, 0);
+      xv[j][1] = __builtin_amdgcn_raw_buffer_load_b128(xr, o + 16u, 0, 0);
+    };
+#pragma unroll
+    for (int j = 0; j < D; j++) xload(j);
+    u32x4 wv[RS][UMAX];
+#pragma unroll
+    for (int u = 0; u < UMAX; u++) {
+      const int wb = 4 * (4 * (q0 + u) + g);
+#pragma unroll
+      for (int rs = 0; rs < RS; rs++) wv[rs][u] = load_chunk<VEC>(wrow[rs], wb, wpr);
+    }
+#pragma unroll
+    for (int j = 0; j < NWD; j++) {
+      if (j + D < NWD) xload(j + D);
+      if (j >= nwd) continue;  // wave-uniform
+      const int u = j >> 2, wi = j & 3;
+      if (wi == 0) {
+        // the 4x4 word transpose of gemv_direct_kernel, per row block
+#pragma unroll
+        for (int rs = 0; rs < RS; rs++) {
+          u32x4 &v = wv[rs][u];
+          const auto p02 = __builtin_amdgcn_permlane32_swap(v.x, v.z, false, false);
+          const auto p13 = __builtin_amdgcn_permlane32_swap(v.y, v.w, false, false);
+          const auto p01 = __builtin_amdgcn_permlane16_swap(p02[0], p13[0], false, false);
+          const auto p23 = __builtin_amdgcn_permlane16_swap(p02[1], p13[1], false, false);
+          v = (u32x4){p01[0], p01[1], p23[0], p23[1]};
+        }
+      }
+#pragma unroll
+      for (int rs = 0; rs < RS; rs++) {
+        const uint32_t wq = wi == 0 ? wv[rs][u].x : wi == 1 ? wv[rs][u].y : wi == 2 ? wv[rs][u].z : wv[rs][u].w;
+        u32x4 a0, a1;
+        unpack16_nat(wq, a0, a1);
+        acc[rs] = mfma16(a0, xv[j][0], acc[rs]);
+        acc[rs] = mfma16(a1, xv[j][1], acc[rs]);
+      }
+    }
+  }
+
+  // Fixed-order reduction of the waves' partial tiles.
+#pragma unroll
+  for (int rs = 0; rs < RS; rs++) red[(rs * WAVES + wave) * 64 + lane] = acc[rs];
+  __syncthreads();
+  if (wave != 0) return;
+#pragma unroll
+  for (int rs = 0; rs < RS; rs++) {
+    f32x4 v = red[rs * WAVES * 64 + lane];
+#pragma unroll
+    for (int w = 1; w < WAVES; w++) v += red[(rs * WAVES + w) * 64 + lane];
+    const int n_out = n_base + 16 * rs + 4 * g;
+    if (live && n_out < N) YStore<YT>::store4(Y + (size_t)r * N + n_out, v * sc[rs] * 0.5f, min(4, N - n_out));
+  }
+}
+
+template <typename YT, int WAVES, int UMAX, int D, bool VEC, int RS>
+static hipError_t launch_gemv_tall_w(const uint32_t *w, const float *scale, const void *x, void *y, int B, int K,
+                                     int N, hipStream_t stream) {
+  hipLaunchKernelGGL((gemv_tall_kernel<YT, WAVES, UMAX, D, VEC, RS>), dim3((N + 16 * RS - 1) / (16 * RS)),
+                     dim3(WAVES * 64), 0, stream, w, scale, reinterpret_cast<const uint16_t *>(x),
+                     reinterpret_cast<YT *>(y), B, K, N);
+  return hipGetLastError();
+}
+
+// Rows per tile of the tall kernel: 16 * GEMV_TALL_RS.
+constexpr int GEMV_TALL_RS = 2;
+
+template <typename YT>
+static hipError_t launch_gemv_tall(const uint32_t *w, const float *scale, const void *x, void *y, int B, int K,
+                                   int N, hipStream_t stream) {
+  constexpr int RS = GEMV_TALL_RS;
+  const bool vec = ((K >> 4) & 3) == 0 && (reinterpret_cast<uintptr_t>(w) & 15) == 0;
+  const int nq = (K + 255) / 256;
+#define FRX_GEMV_T(WV, UM)                                                                       \
+  return vec ? launch_gemv_tall_w<YT, WV, UM, 4, true, RS>(w, scale, x, y, B, K, N, stream) \
+             : launch_gemv_tall_w<YT, WV, UM, 4, false, RS>(w, scale, x, y, B, K, N, stream)
+  if (nq <= 8) FRX_GEMV_T(4, 2);
+  if (nq <= 16) FRX_GEMV_T(8, 2);
+  if (nq <= 48) FRX_GEMV_T(16, 3);
+  FRX_GEMV_T(16, 4);
+#undef FRX_GEMV_T
+}
+
 template <typename YT, int EPI, int XPL = 1, bool YSPLIT = false>
 static hipError_t launch_gemv_direct(const uint32_t *w, const float *scale, const uint32_t *w2,
                                      const float *scale2, const void *x, const void *x2, void *y,
@@ -531,6 +674,20 @@ hipError_t launch_gemv(const uint32_t *w, const float *scale, const void *x,
                        hipStream_t stream) {
   constexpr int L = GEMV_LINEAR;
   if (xt_bf16 && B >= GEMV_DIRECT_MIN_B) {
+    // taller tiles where their grid still covers every CU
+    static std::atomic<int> cus{0};
+    int c = cus.load(std::memory_order_relaxed);
+    if (c == 0) {
+      int dev = 0;
+      if (hipGetDevice(&dev) != hipSuccess ||
+          hipDeviceGetAttribute(&c, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || c <= 0)
+        c = 256;
+      cus.store(c, std::memory_order_relaxed);
+    }
+    if ((N + 16 * GEMV_TALL_RS - 1) / (16 * GEMV_TALL_RS) >= c) {
+      if (yt_bf16) return launch_gemv_tall<uint16_t>(w, scale, x, y, B, K, N, stream);
+      return launch_gemv_tall<float>(w, scale, x, y, B, K, N, stream);
+    }
     if (yt_bf16) return launch_gemv_direct<uint16_t, L>(w, scale, w, scale, x, x, y, B, K, N, stream);
     return launch_gemv_direct<float, L>(w, scale, w, scale, x, x, y, B, K, N, stream);
   }

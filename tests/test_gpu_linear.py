@@ -45,7 +45,7 @@ def _run(ctx, w, s, xf, xb, xt, yt):
 
 
 SHAPES = [(1, 256, 64), (3, 512, 100), (16, 1024, 48), (1, 2064, 33), (5, 4096, 130),
-          (9, 2064, 33), (12, 4096, 130),
+          (9, 2064, 33), (12, 4096, 130), (10, 1040, 8200),
           (17, 256, 64), (64, 1040, 200), (130, 512, 136), (257, 128, 19)]
 
 
