@@ -32,11 +32,12 @@ def make_moe(name, T, H, I, E):
     return xf, xb, rf, rb, ex
 
 
-def run_gpu(ctx, xf, xb, rf, rb, ex, E, top_k, act, xt="bf16", yt="f32"):
+def run_gpu(ctx, xf, xb, rf, rb, ex, E, top_k, act, xt="bf16", yt="f32", rt=None):
     T, H = xf.shape
+    rt = xt if rt is None else rt
     dw = {k: (dev_u32(v[0]), dev_f32(v[1])) for k, v in ex.items()}
     x = dev_bf16(xb) if xt == "bf16" else dev_f32(xf)
-    r = dev_bf16(rb) if xt == "bf16" else dev_f32(rf)
+    r = dev_bf16(rb) if rt == "bf16" else dev_f32(rf)
     y = torch.empty((T, H), dtype=torch.float32 if yt == "f32" else torch.bfloat16, device="cuda:0")
     idx = torch.zeros((T, top_k), dtype=torch.int32, device="cuda:0")
     w = torch.zeros((T, top_k), dtype=torch.float32, device="cuda:0")
@@ -74,6 +75,24 @@ def test_moe_f32_inputs(ctx):
     y, idx, w = run_gpu(ctx, xf, None, rf, None, ex, 5, 2, frx.ACT_SILU, xt="f32")
     ref, ridx, rw = run_oracle(xf, rf, ex, 5, 2, False)
     np.testing.assert_array_equal(idx, ridx)
+    assert_close_f32(host(y), ref)
+
+
+@pytest.mark.parametrize("xt,rt", [("f32", "bf16"), ("bf16", "f32")])
+def test_moe_mixed_input_dtypes(ctx, xt, rt):
+    """f32 tokens with bf16 router weights (the resident router, separate
+    multiply and add) and bf16 tokens with f32 router weights (the chunked
+    router); routing indices bit-exact."""
+    T, H, I, E, k = 40, 256, 192, 6, 2
+    xf, xb, rf, rb, ex = make_moe(f"moe/mix_{xt}_{rt}", T, H, I, E)
+    if xt == "f32":
+        xf, xb = synth.normal(97, T * H).reshape(T, H), None
+    if rt == "f32":
+        rf, rb = synth.normal(96, E * H, 0.05).reshape(E, H), None
+    y, idx, w = run_gpu(ctx, xf, xb, rf, rb, ex, E, k, frx.ACT_SILU, xt=xt, rt=rt)
+    ref, ridx, rw = run_oracle(xf, rf, ex, E, k, False)
+    np.testing.assert_array_equal(idx, ridx)
+    np.testing.assert_allclose(w, rw, rtol=0, atol=1e-6)
     assert_close_f32(host(y), ref)
 
 
