@@ -16,7 +16,12 @@ back-to-back launches of one shape (HIP events on the launch stream around
 the sequence), weighted over the step's three launches.
 cpu_baseline: the reference's CPU decode path (ternary_matmul_packed_parallel,
 src/model/ternary.rs:471-529, restated in C by the oracle) on the same three
-matrices at B=1, timed on this host's cores.
+matrices at B=1, timed on this host's cores; its breakdown adds the branchy
+i8 loop and the CPU 2:4 matmul (one thread each) and the single 2048x2048
+linear, each with median, p10 and p90.
+
+Per-launch GPU times carry the median, p10 and p90 over the individual
+replays (decode) or launches (prefill, 2:4, MoE; 200 back-to-back).
 
 extra: the decode FFN of the same layer through frx_ternary_ffn (one launch
 with a grid barrier, and the two-launch execution: gate/up/SiLU launch +
@@ -163,7 +168,9 @@ def main():
     # Per-launch kernel time: back-to-back launches of one kernel (weights
     # rotating over the copies), HIP events on the launch stream around the
     # whole sequence, divided by the number of launches.
-    def per_launch(fn_one, per_copy, reps):
+    def per_launch(fn_one, per_copy, reps, stats=None):
+        """Average seconds per launch; with `stats` (a dict) also the median,
+        p10 and p90 of the per-launch time over the individual replays."""
         def seq():
             for i in range(copies):
                 fn_one(i)
@@ -171,20 +178,28 @@ def main():
         with torch.cuda.stream(stream):
             (gr.replay() if gr is not None else seq())
         torch.cuda.synchronize()
-        e0 = torch.cuda.Event(enable_timing=True)
-        e1 = torch.cuda.Event(enable_timing=True)
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(reps + 1)]
         with torch.cuda.stream(stream):
-            e0.record(stream)
-            for _ in range(reps):
+            ev[0].record(stream)
+            for r in range(reps):
                 (gr.replay() if gr is not None else seq())
-            e1.record(stream)
+                ev[r + 1].record(stream)
         torch.cuda.synchronize()
-        return e0.elapsed_time(e1) * 1e-3 / (reps * copies * per_copy)
+        per = copies * per_copy
+        if stats is not None:
+            samples = np.array([ev[r].elapsed_time(ev[r + 1]) * 1e3 / per for r in range(reps)])
+            stats.update({"median_us": round(float(np.median(samples)), 3),
+                          "p10_us": round(float(np.percentile(samples, 10)), 3),
+                          "p90_us": round(float(np.percentile(samples, 90)), 3),
+                          "samples": reps, "launches_per_sample": per})
+        return ev[0].elapsed_time(ev[reps]) * 1e-3 / (reps * per)
 
     reps = max(3, args.steps // copies)
+    dist_reps = max(reps, 30)  # enough replays for the percentiles (>= 200 launches per shape)
+    dist = {"11008x4096": {}, "4096x11008": {}}
     t_gu = per_launch(lambda i: (ctx.ternary_linear(W[i][0], s_g, x, g), ctx.ternary_linear(W[i][1], s_u, x, u)),
-                      2, reps)
-    t_dn = per_launch(lambda i: ctx.ternary_linear(W[i][2], s_d, xd, y), 1, reps)
+                      2, dist_reps, dist["11008x4096"])
+    t_dn = per_launch(lambda i: ctx.ternary_linear(W[i][2], s_d, xd, y), 1, dist_reps, dist["4096x11008"])
     launch_bytes = 2 * b_gu + b_dn
     launch_time = 2 * t_gu + t_dn
     achieved = launch_bytes / launch_time / 1e9
@@ -193,6 +208,7 @@ def main():
         "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
         "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
         "avg_us": {"11008x4096": round(t_gu * 1e6, 3), "4096x11008": round(t_dn * 1e6, 3)},
+        "launch_time_distribution": dist,
         "bytes_per_launch": {"11008x4096": b_gu, "4096x11008": b_dn},
         "timing": timing,
     }
@@ -271,14 +287,18 @@ def main():
             torch.cuda.synchronize()
             el_x, _ = timed(lambda: [stepx(i) for i in range(args.steps)])
             bytes_x = 2 * gemv_bytes(I, H, bx) + gemv_bytes(H, I, bx)
+            dist_x = {"11008x4096": {}, "4096x11008": {}}
             tgu_x = per_launch(lambda i: (ctx.ternary_linear(W[i][0], s_g, xx, gx),
-                                          ctx.ternary_linear(W[i][1], s_u, xx, ux)), 2, reps)
-            tdn_x = per_launch(lambda i: ctx.ternary_linear(W[i][2], s_d, xdx, yx), 1, reps)
+                                          ctx.ternary_linear(W[i][1], s_u, xx, ux)), 2, dist_reps,
+                               dist_x["11008x4096"])
+            tdn_x = per_launch(lambda i: ctx.ternary_linear(W[i][2], s_d, xdx, yx), 1, dist_reps,
+                               dist_x["4096x11008"])
             batches[f"B{bx}"] = {
                 "us_per_step": round(el_x / args.steps * 1e6, 2),
                 "gb_s": round(bytes_x / (el_x / args.steps) / 1e9, 1),
                 "hbm_fraction": round(bytes_x / (el_x / args.steps) / 1e9 / HBM_PEAK_GBS, 4),
                 "avg_us": {"11008x4096": round(tgu_x * 1e6, 3), "4096x11008": round(tdn_x * 1e6, 3)},
+                "launch_time_distribution": dist_x,
                 "kernel": "frx::gemv_kernel (staged)" if bx < 8 else "frx::gemv_direct_kernel",
             }
             log(f"bench: decode GEMV B={bx}: {batches[f'B{bx}']['us_per_step']} us/step, "
@@ -319,23 +339,30 @@ def main():
     print(json.dumps(out), flush=True)
 
 
-def _time_kernel(torch, stream, fn, iters, warm=3):
+def _time_kernel(torch, stream, fn, iters, warm=3, stats=None):
+    """Average seconds per launch over `iters` back-to-back launches (HIP
+    events on the launch stream); with `stats` also the median, p10 and p90
+    of the individual launch times."""
     with torch.cuda.stream(stream):
         for _ in range(warm):
             fn()
     torch.cuda.synchronize()
-    e0 = torch.cuda.Event(enable_timing=True)
-    e1 = torch.cuda.Event(enable_timing=True)
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(iters + 1)]
     with torch.cuda.stream(stream):
-        e0.record(stream)
-        for _ in range(iters):
+        ev[0].record(stream)
+        for i in range(iters):
             fn()
-        e1.record(stream)
+            ev[i + 1].record(stream)
     torch.cuda.synchronize()
-    return e0.elapsed_time(e1) * 1e-3 / iters
+    if stats is not None:
+        samples = np.array([ev[i].elapsed_time(ev[i + 1]) * 1e3 for i in range(iters)])
+        stats.update({"median_us": round(float(np.median(samples)), 2),
+                      "p10_us": round(float(np.percentile(samples, 10)), 2),
+                      "p90_us": round(float(np.percentile(samples, 90)), 2), "launches": iters})
+    return ev[0].elapsed_time(ev[iters]) * 1e-3 / iters
 
 
-def run_extra(torch, frx, synth, ctx, stream, dev, only=None, iters=20):
+def run_extra(torch, frx, synth, ctx, stream, dev, only=None, iters=200):
     res = {}
     M, K = 2048, 4096
     _, xb = synth.activations("bench/prefill", "x", M, K)
@@ -346,18 +373,20 @@ def run_extra(torch, frx, synth, ctx, stream, dev, only=None, iters=20):
         s = torch.from_numpy(synth.row_scales("bench/prefill", f"s{N}", N, samples=256)).to(dev)
         Y = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
         if only in (None, "prefill"):
-            dt = _time_kernel(torch, stream, lambda: ctx.ternary_linear(w, s, X, Y), iters)
+            st = {}
+            dt = _time_kernel(torch, stream, lambda: ctx.ternary_linear(w, s, X, Y), iters, stats=st)
             tf = 2.0 * M * N * K / dt / 1e12
             res[f"prefill_gemm_{M}x{K}x{N}"] = {"us": round(dt * 1e6, 2), "tflops": round(tf, 1),
-                                                "frac_bf16_peak": round(tf / BF16_PEAK_TFLOPS, 4)}
+                                                "frac_bf16_peak": round(tf / BF16_PEAK_TFLOPS, 4), **st}
             log(f"bench: prefill N={N}: {dt * 1e6:.1f} us, {tf:.1f} TFLOP/s")
         if only in (None, "sparse24"):
             t24 = synth.sparse24_uniform("bench/sp24", f"w{N}", N, K)
             meta = torch.from_numpy(frx.pack_sparse24_gpu(t24).view(np.int32)).to(dev)
-            dt = _time_kernel(torch, stream, lambda: ctx.sparse24_ternary_linear(meta, s, X, Y), iters)
+            st = {}
+            dt = _time_kernel(torch, stream, lambda: ctx.sparse24_ternary_linear(meta, s, X, Y), iters, stats=st)
             tf = 2.0 * M * N * K / dt / 1e12
             res[f"sparse24_gemm_{M}x{K}x{N}"] = {"us": round(dt * 1e6, 2), "tflops_dense_equiv": round(tf, 1),
-                                                 "frac_bf16_peak": round(tf / BF16_PEAK_TFLOPS, 4)}
+                                                 "frac_bf16_peak": round(tf / BF16_PEAK_TFLOPS, 4), **st}
             log(f"bench: 2:4 N={N}: {dt * 1e6:.1f} us, {tf:.1f} TFLOP/s dense-equivalent")
             del meta
         del w, Y
@@ -380,39 +409,129 @@ def run_extra(torch, frx, synth, ctx, stream, dev, only=None, iters=20):
     wd = [pd.clone() for _ in range(E)]
     ym = torch.empty((T, Hm), dtype=torch.bfloat16, device=dev)
     fn = lambda: ctx.moe_ternary_ffn(xm, rm, wg, [sg] * E, wu, [sg] * E, wd, [sd] * E, ym, top_k=k)  # noqa: E731
-    dt = _time_kernel(torch, stream, fn, iters)
+    st = {}
+    dt = _time_kernel(torch, stream, fn, iters, stats=st)
     fl = T * k * 3 * 2.0 * Im * Hm
     tf = fl / dt / 1e12
     res["moe_512tok_h2048_i5632_e16_top2"] = {"us": round(dt * 1e6, 2), "tflops": round(tf, 1),
-                                              "frac_bf16_peak": round(tf / BF16_PEAK_TFLOPS, 4)}
+                                              "frac_bf16_peak": round(tf / BF16_PEAK_TFLOPS, 4), **st}
     log(f"bench: MoE: {dt * 1e6:.1f} us, {tf:.1f} TFLOP/s")
     return res
 
 
+def _cpu_time(fn, seconds, max_reps=200):
+    """Median, p10 and p90 wall seconds of fn() over enough calls to fill
+    about `seconds` (at least 3)."""
+    t0 = time.perf_counter()
+    fn()  # warm-up call, also the calibration
+    t1 = time.perf_counter() - t0
+    reps = max(3, min(max_reps, int(seconds / max(t1, 1e-6))))
+    ts = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t0)
+    ts = np.array(ts)
+    return float(np.median(ts)), float(np.percentile(ts, 10)), float(np.percentile(ts, 90)), reps
+
+
+def _cpu_entry(kernel, shapes, t, byts, flops, threads):
+    med, p10, p90, reps = t
+    return {"kernel": kernel, "shapes": shapes, "threads": threads, "reps": reps,
+            "ms": round(med * 1e3, 3), "p10_ms": round(p10 * 1e3, 3), "p90_ms": round(p90 * 1e3, 3),
+            "gb_s": round(byts / med / 1e9, 2), "gflop_s": round(flops / med / 1e9, 2)}
+
+
 def cpu_baseline(t_gu, t_dn, B, seconds):
-    """Reference CPU decode path (ternary_matmul_packed_parallel) restated in
-    C, on this host's cores (capped at 16, the GPU box's CPU share)."""
+    """The reference's CPU linear paths restated in C by the oracle, on this
+    host's cores (capped at 16, the CPU share of one GPU):
+
+    value: ternary_matmul_packed_parallel (src/model/ternary.rs:471-529, u8
+    packed, row batches over a thread pool) on the decode step's three
+    matrices at B=1, in GB/s over the same algorithmic bytes as the GPU
+    metric (f32 x and y on the CPU).
+
+    breakdown: at the single-linear configuration (x[1,2048] f32,
+    W[2048,2048]) and at the decode shapes, (i) the branchy i8 loop of
+    benches/ternary_bench.rs:87-106 on one thread, (ii) the packed parallel
+    path, (iii) the CPU 2:4 matmul SparseTernaryMatrix::matmul_decode
+    (src/model/sparse_ternary.rs:255-320) on one thread; ms are medians over
+    the reps, GB/s over the bytes each kernel reads (i8, u8 packed or
+    pattern+sign bytes, plus f32 x and y), GFLOP/s as 2*N*K."""
     import oracle
     threads = max(1, min(16, os.cpu_count() or 1))
-    p_gu = oracle.pack_ternary(t_gu)
-    p_dn = oracle.pack_ternary(t_dn)
-    x = np.linspace(-1, 1, t_gu.shape[1], dtype=np.float32)
-    h = np.linspace(-1, 1, t_dn.shape[1], dtype=np.float32)
-    # one calibration call, then reps so the whole sample takes ~`seconds`
-    t1, _ = oracle.time_packed_parallel(p_gu, 0.01, x, t_gu.shape[0], t_gu.shape[1], threads, 1)
-    t2, _ = oracle.time_packed_parallel(p_dn, 0.01, h, t_dn.shape[0], t_dn.shape[1], threads, 1)
-    reps = max(3, int(seconds / max(1e-6, 2 * t1 + t2)))
-    t1, _ = oracle.time_packed_parallel(p_gu, 0.01, x, t_gu.shape[0], t_gu.shape[1], threads, reps)
-    t2, _ = oracle.time_packed_parallel(p_dn, 0.01, h, t_dn.shape[0], t_dn.shape[1], threads, reps)
-    step_t = 2 * t1 + t2
     n_gu, k_gu = t_gu.shape
     n_dn, k_dn = t_dn.shape
+    p_gu = oracle.pack_ternary(t_gu)
+    p_dn = oracle.pack_ternary(t_dn)
+    x = np.linspace(-1, 1, k_gu, dtype=np.float32)
+    h = np.linspace(-1, 1, k_dn, dtype=np.float32)
+    # one calibration call, then reps so the sample takes ~half of `seconds`
+    t1, _ = oracle.time_packed_parallel(p_gu, 0.01, x, n_gu, k_gu, threads, 1)
+    t2, _ = oracle.time_packed_parallel(p_dn, 0.01, h, n_dn, k_dn, threads, 1)
+    reps = max(3, int(0.5 * seconds / max(1e-6, 2 * t1 + t2)))
+    q1 = np.zeros(2)
+    q2 = np.zeros(2)
+    t1, _ = oracle.time_packed_parallel(p_gu, 0.01, x, n_gu, k_gu, threads, reps, q1)
+    t2, _ = oracle.time_packed_parallel(p_dn, 0.01, h, n_dn, k_dn, threads, reps, q2)
+    step_t = 2 * t1 + t2
     # same algorithmic byte count as the GPU metric at B=1 (f32 x/y on CPU)
     byts = 2 * gemv_bytes(n_gu, k_gu, 1, 4, 4) + gemv_bytes(n_dn, k_dn, 1, 4, 4)
+
+    from ferrisres_amd import synth
+    budget = 0.5 * seconds / 4  # the rest of the sample over the four single-thread entries
+    breakdown = []
+    # single linear x[1,2048] f32 ~N(0,1), W[2048,2048] U{-1,0,+1}
+    n1 = k1 = 2048
+    w1 = synth.ternary_uniform("cpu/linear", "w", n1, k1)
+    x1, _ = synth.activations("cpu/linear", "x", 1, k1, bf16=False)
+    x1 = np.ascontiguousarray(x1.reshape(-1), dtype=np.float32)
+    sc1 = float(synth.row_scales("cpu/linear", "s", 1)[0])
+    fl1 = 2.0 * n1 * k1
+    breakdown.append(_cpu_entry(
+        "ternary_bench i8 (benches/ternary_bench.rs:87-106)", "1x2048x2048",
+        _cpu_time(lambda: oracle.bench_ternary_matmul(x1, w1, sc1, 1, n1, k1), budget),
+        n1 * k1 + 4 * k1 + 4 * n1, fl1, 1))
+    p1 = oracle.pack_ternary(w1)
+    q = np.zeros(2)
+    t_p1, _ = oracle.time_packed_parallel(p1, sc1, x1, n1, k1, threads, 200, q)
+    breakdown.append(_cpu_entry(
+        "ternary_matmul_packed_parallel (ternary.rs:471-529)", "1x2048x2048",
+        (t_p1, q[0], q[1], 200), gemv_bytes(n1, k1, 1, 4, 4) - 4 * n1, fl1, threads))
+    s1 = synth.sparse24_uniform("cpu/linear", "w24", n1, k1)
+    pt1, sg1 = oracle.sparse24_cpu_from_ternary(s1, n1, k1)
+    breakdown.append(_cpu_entry(
+        "SparseTernaryMatrix::matmul_decode (sparse_ternary.rs:255-320)", "1x2048x2048",
+        _cpu_time(lambda: oracle.sparse24_cpu_matmul_decode(pt1, sg1, sc1, n1, k1, x1), budget),
+        pt1.nbytes + sg1.nbytes + 4 * k1 + 4 * n1, fl1, 1))
+    # decode shapes: one token through gate/up [11008,4096] and down [4096,11008]
+    fl_step = 2.0 * (2 * n_gu * k_gu + n_dn * k_dn)
+    breakdown.append(_cpu_entry(
+        "ternary_bench i8 (benches/ternary_bench.rs:87-106)", "decode step 2x(11008x4096)+4096x11008",
+        _cpu_time(lambda: (oracle.bench_ternary_matmul(x, t_gu, 0.01, 1, n_gu, k_gu),
+                           oracle.bench_ternary_matmul(x, t_gu, 0.01, 1, n_gu, k_gu),
+                           oracle.bench_ternary_matmul(h, t_dn, 0.01, 1, n_dn, k_dn)), budget, max_reps=20),
+        2 * (n_gu * k_gu + 4 * k_gu + 4 * n_gu) + n_dn * k_dn + 4 * k_dn + 4 * n_dn, fl_step, 1))
+    # p10/p90 of the step: the per-matrix percentiles added up (2 x gate/up + down)
+    breakdown.append(_cpu_entry(
+        "ternary_matmul_packed_parallel (ternary.rs:471-529)", "decode step 2x(11008x4096)+4096x11008",
+        (step_t, 2 * q1[0] + q2[0], 2 * q1[1] + q2[1], reps), byts - 4 * (2 * n_gu + n_dn), fl_step, threads))
+    s_gu = synth.sparse24_uniform("cpu/decode", "w24_gu", n_gu, k_gu)
+    s_dn = synth.sparse24_uniform("cpu/decode", "w24_dn", n_dn, k_dn)
+    pg, sgg = oracle.sparse24_cpu_from_ternary(s_gu, n_gu, k_gu)
+    pd, sgd = oracle.sparse24_cpu_from_ternary(s_dn, n_dn, k_dn)
+    breakdown.append(_cpu_entry(
+        "SparseTernaryMatrix::matmul_decode (sparse_ternary.rs:255-320)", "decode step 2x(11008x4096)+4096x11008",
+        _cpu_time(lambda: (oracle.sparse24_cpu_matmul_decode(pg, sgg, 0.01, n_gu, k_gu, x),
+                           oracle.sparse24_cpu_matmul_decode(pg, sgg, 0.01, n_gu, k_gu, x),
+                           oracle.sparse24_cpu_matmul_decode(pd, sgd, 0.01, n_dn, k_dn, h)), budget, max_reps=20),
+        2 * (pg.nbytes + sgg.nbytes + 4 * k_gu + 4 * n_gu) + pd.nbytes + sgd.nbytes + 4 * k_dn + 4 * n_dn,
+        fl_step, 1))
     return {"value": round(byts / step_t / 1e9, 2), "unit": "GB/s", "cores": threads, "kind": "port",
             "sample": f"ternary_matmul_packed_parallel (ternary.rs:471-529) restated in C, u8 layout, f32 x, "
                       f"1 token through 11008x4096 x2 + 4096x11008, median of {reps} reps each "
-                      f"({step_t * 1e3:.2f} ms/step on {threads} threads)"}
+                      f"({step_t * 1e3:.2f} ms/step on {threads} threads)",
+            "breakdown": breakdown}
 
 
 if __name__ == "__main__":

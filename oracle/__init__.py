@@ -62,7 +62,7 @@ def lib():
             "frxo_ffn_forward": (None, [_vp, _sz, _sz, _sz, _vp, _vp, _vp, _vp, _vp, _vp,
                                         ctypes.c_int, _vp]),
             "frxo_time_packed_parallel": (ctypes.c_double, [_vp, _f, _vp, _sz, _sz, ctypes.c_int,
-                                                            ctypes.c_int, _vp]),
+                                                            ctypes.c_int, _vp, _vp]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(h, name)
@@ -293,9 +293,12 @@ def gelu_tanh(x):
     return lib().frxo_gelu_tanh(float(x))
 
 
-def time_packed_parallel(packed, scale, inp, out_rows, in_cols, threads, reps):
+def time_packed_parallel(packed, scale, inp, out_rows, in_cols, threads, reps, pct=None):
+    """Median seconds per call over `reps` calls (and the output); a
+    2-element float64 `pct` receives the 10th and 90th percentiles."""
     p = _c(packed, np.uint8)
     x = _c(inp, np.float32)
     out = np.zeros(out_rows, np.float32)
-    t = lib().frxo_time_packed_parallel(_p(p), scale, _p(x), out_rows, in_cols, threads, reps, _p(out))
+    q = None if pct is None else _p(pct)
+    t = lib().frxo_time_packed_parallel(_p(p), scale, _p(x), out_rows, in_cols, threads, reps, _p(out), q)
     return t, out

@@ -769,12 +769,13 @@ static int cmp_double(const void *x, const void *y) {
  * Times ternary_matmul_packed_parallel (ternary.rs:471-529): rows split into
  * ceil(N / max(N/32,1)) row batches spread over `threads` workers (rayon's
  * par_chunks_mut split, statically round-robined). Returns the median wall
- * time in seconds over `reps` calls.
+ * time in seconds over `reps` calls; when `pct` is not NULL it receives the
+ * 10th and 90th percentile (nearest rank) in pct[0], pct[1].
  */
 double frxo_time_packed_parallel(const uint8_t *packed, float scale,
                                  const float *input, size_t out_rows,
                                  size_t in_cols, int threads, int reps,
-                                 float *out) {
+                                 float *out, double *pct) {
   if (threads < 1) threads = 1;
   if (reps < 1) reps = 1;
   pthread_t *th = (pthread_t *)malloc(sizeof(pthread_t) * (size_t)threads);
@@ -794,6 +795,10 @@ double frxo_time_packed_parallel(const uint8_t *packed, float scale,
   pthread_barrier_destroy(&bar);
   qsort(times, (size_t)reps, sizeof(double), cmp_double);
   double med = times[reps / 2];
+  if (pct) {
+    pct[0] = times[(reps - 1) / 10];
+    pct[1] = times[(9 * (reps - 1) + 9) / 10];
+  }
   free(th);
   free(args);
   free(times);

@@ -106,7 +106,7 @@ void frxo_ffn_forward(const float *x, size_t seq, size_t hidden, size_t inter,
 double frxo_time_packed_parallel(const uint8_t *packed, float scale,
                                  const float *input, size_t out_rows,
                                  size_t in_cols, int threads, int reps,
-                                 float *out);
+                                 float *out, double *pct);
 
 #ifdef __cplusplus
 }
