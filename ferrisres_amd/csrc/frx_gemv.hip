@@ -669,10 +669,165 @@ static hipError_t launch_gemv_direct(const uint32_t *w, const float *scale, cons
 #undef FRX_GEMV_D
 }
 
+// ---- one bf16 token (B = 1): whole rows per wave --------------------------
+//
+// Each wave owns RW complete rows, so no partial sums cross waves. A wave
+// instruction reads a 1 KB window of one row (lane l: bytes 16l..16l+15 of
+// the window, full 128-byte lines); the 16 MFMA rows are the 16 lane
+// segments of that window (row r = l%16, k-group g = l/16 as the MFMA
+// lays out A) and the 16 MFMA columns the activations of the same
+// segments, so column c of B holds x at the positions of A's row c and the
+// dot product is the diagonal of the 16x16 accumulator. A lane's 64
+// activations per window (natural order, the order unpack16_nat gives the
+// codes) come from LDS, staged once per workgroup with a 16-byte pad per
+// 64 values so that the lanes' 128-byte reads spread over the banks; one
+// read feeds the wave's RW rows. Activations past K are zero, and the
+// weight loads of a partial last window are clamped inside the row (the
+// zero activations cancel whatever those words hold). The diagonal lives
+// in lanes (c, c/4) register c%4: two quad DPP adds and four lane reads
+// sum it, in a fixed order, so results are deterministic.
+// Against the 16-row tiles with K split over waves (gemv_kernel at B = 1),
+// measured over rotating weights: 5.38 -> 4.83 us (11008x4096) and 5.33 ->
+// 4.97 us (4096x11008) per launch. A per-wave timeline shows the weights of
+// a launch landing within ~1 us, ~2.3 us after the start; the decode (15
+// VALU ops per word) then runs on every SIMD at once, which is what
+// remains above the bare read.
+constexpr int ROWS_XCH = 36;  // LDS dwords per 64-activation chunk (128 B + 16 B pad)
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float v) {
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+
+template <typename YT, int WAVES, int RW, int NI>
+__global__ __launch_bounds__(WAVES * 64) void gemv_rows_kernel(const uint32_t *__restrict__ W,
+                                                               const float *__restrict__ scale,
+                                                               const uint16_t *__restrict__ X,
+                                                               YT *__restrict__ Y, int K, int N) {
+  extern __shared__ __align__(16) uint32_t lds[];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int row0 = ((int)blockIdx.x * WAVES + wave) * RW;
+  const int kw = K >> 4;   // words per row
+  const int nxp = K >> 3;  // 16-byte pieces of x
+  constexpr int NT = WAVES * 64;
+  constexpr int XR = (NI * 512 + NT - 1) / NT;  // staging rounds over NI * 4096 activations
+  // 1. activations (zero past K), issued before the weights so that waiting
+  //    for them does not wait for the weights
+  u32x4 xs[XR];
+  const u32x4 *X4 = reinterpret_cast<const u32x4 *>(X);
+#pragma unroll
+  for (int r = 0; r < XR; r++) {
+    const int j = tid + r * NT;
+    xs[r] = (u32x4){0u, 0u, 0u, 0u};
+    if (j < nxp) xs[r] = X4[j];
+  }
+  // 2. the wave's weights: RW rows x NI windows
+  u32x4 wv[RW][NI];
+#pragma unroll
+  for (int rr = 0; rr < RW; rr++) {
+    const uint32_t *wr = W + (size_t)min(row0 + rr, N - 1) * kw;
+#pragma unroll
+    for (int i = 0; i < NI; i++)
+      wv[rr][i] = *reinterpret_cast<const u32x4 *>(wr + min(i * 256 + 4 * lane, kw - 4));
+  }
+  float sc[RW];
+#pragma unroll
+  for (int rr = 0; rr < RW; rr++) sc[rr] = scale[min(row0 + rr, N - 1)];
+  // 3. stage: 16-byte piece j -> chunk j/8, slot j%8
+#pragma unroll
+  for (int r = 0; r < XR; r++) {
+    const int j = tid + r * NT;
+    if (j < NI * 512) *reinterpret_cast<u32x4 *>(lds + (j >> 3) * ROWS_XCH + (j & 7) * 4) = xs[r];
+  }
+  __syncthreads();
+  // 4. per window: the lane's 64 activations, then each row's 4 words
+  f32x4 acc[RW];
+#pragma unroll
+  for (int rr = 0; rr < RW; rr++) acc[rr] = (f32x4){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int i = 0; i < NI; i++) {
+    u32x4 xb[8];
+    const uint32_t *xp = lds + (i * 64 + lane) * ROWS_XCH;
+#pragma unroll
+    for (int q = 0; q < 8; q++) xb[q] = *reinterpret_cast<const u32x4 *>(xp + 4 * q);
+#pragma unroll
+    for (int rr = 0; rr < RW; rr++) {
+      const uint32_t wq[4] = {wv[rr][i].x, wv[rr][i].y, wv[rr][i].z, wv[rr][i].w};
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        u32x4 lo, hi;
+        unpack16_nat(wq[j], lo, hi);
+        acc[rr] = mfma16(lo, xb[2 * j], acc[rr]);
+        acc[rr] = mfma16(hi, xb[2 * j + 1], acc[rr]);
+      }
+    }
+  }
+  // 5. diagonal: lane (c = l%16, rg = l/16) holds C[4rg + e][c]
+  const int c = lane & 15, rg = lane >> 4, e = c & 3;
+  const bool diag = (c >> 2) == rg;
+  float tot[RW];
+#pragma unroll
+  for (int rr = 0; rr < RW; rr++) {
+    float v = e == 0 ? acc[rr][0] : e == 1 ? acc[rr][1] : e == 2 ? acc[rr][2] : acc[rr][3];
+    v = diag ? v : 0.f;
+    v += dpp_f32<0xB1>(v);  // quad_perm [1,0,3,2]
+    v += dpp_f32<0x4E>(v);  // quad_perm [2,3,0,1]
+    const float a = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+    const float b = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 20));
+    const float d = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 40));
+    const float f = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 60));
+    tot[rr] = ((a + b) + (d + f)) * sc[rr] * 0.5f;  // 0.5 undoes the 2*dec(c) encoding
+  }
+  if (lane < RW) {
+    float t = tot[0];
+#pragma unroll
+    for (int rr = 1; rr < RW; rr++)
+      if (lane == rr) t = tot[rr];
+    const int row = row0 + lane;
+    if (row < N) {
+      if constexpr (sizeof(YT) == 2) Y[row] = (uint16_t)bf16_rne(t);
+      else Y[row] = t;
+    }
+  }
+}
+
+template <typename YT, int RW, int NI>
+static hipError_t launch_gemv_rows_w(const uint32_t *w, const float *scale, const void *x, void *y, int K,
+                                     int N, hipStream_t stream) {
+  constexpr int WAVES = 8;
+  const dim3 grid((N + WAVES * RW - 1) / (WAVES * RW));
+  const size_t lds = (size_t)NI * 64 * ROWS_XCH * 4;
+  hipLaunchKernelGGL((gemv_rows_kernel<YT, WAVES, RW, NI>), grid, dim3(WAVES * 64), lds, stream, w, scale,
+                     reinterpret_cast<const uint16_t *>(x), reinterpret_cast<YT *>(y), K, N);
+  return hipGetLastError();
+}
+
+// One bf16 token, K % 64 == 0, K <= 16384, 16-byte aligned weights and
+// activations; two rows per wave where a row is one window (x read once per
+// two rows), one row per wave above (registers).
+static bool gemv_rows_ok(const uint32_t *w, const void *x, int B, int K) {
+  return B == 1 && K % 64 == 0 && K <= 4 * 4096 && (reinterpret_cast<uintptr_t>(w) & 15) == 0 &&
+         (reinterpret_cast<uintptr_t>(x) & 15) == 0;
+}
+
+template <typename YT>
+static hipError_t launch_gemv_rows(const uint32_t *w, const float *scale, const void *x, void *y, int K, int N,
+                                   hipStream_t stream) {
+  const int ni = (K + 4095) / 4096;
+  if (ni == 1) return launch_gemv_rows_w<YT, 2, 1>(w, scale, x, y, K, N, stream);
+  if (ni == 2) return launch_gemv_rows_w<YT, 1, 2>(w, scale, x, y, K, N, stream);
+  if (ni == 3) return launch_gemv_rows_w<YT, 1, 3>(w, scale, x, y, K, N, stream);
+  return launch_gemv_rows_w<YT, 1, 4>(w, scale, x, y, K, N, stream);
+}
+
 hipError_t launch_gemv(const uint32_t *w, const float *scale, const void *x,
                        int xt_bf16, void *y, int yt_bf16, int B, int K, int N,
                        hipStream_t stream) {
   constexpr int L = GEMV_LINEAR;
+  if (xt_bf16 && gemv_rows_ok(w, x, B, K)) {
+    if (yt_bf16) return launch_gemv_rows<uint16_t>(w, scale, x, y, K, N, stream);
+    return launch_gemv_rows<float>(w, scale, x, y, K, N, stream);
+  }
   if (xt_bf16 && B >= GEMV_DIRECT_MIN_B) {
     // taller tiles where their grid still covers every CU
     static std::atomic<int> cus{0};

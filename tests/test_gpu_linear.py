@@ -82,6 +82,48 @@ def test_dense_bit_exact_on_dyadic_inputs(ctx, M, K, N):
         np.testing.assert_array_equal(y, ref)
 
 
+@pytest.mark.parametrize("K,N", [(64, 1), (64, 17), (4160, 35), (8192, 20), (12352, 9), (16384, 50),
+                                 (16448, 5)])
+@pytest.mark.parametrize("yt", ["f32", "bf16"])
+def test_single_token_rows(ctx, K, N, yt):
+    """One bf16 token: whole rows per wave for K % 64 == 0 up to 16384 (one
+    to four 1 KB windows per row, the last one partial at 4160 and 12352;
+    rows past N in the last workgroup), the 16-row tiles at 16448."""
+    name = f"rows/{K}x{N}"
+    t, w, s, xf, xb = _case(name, 1, K, N)
+    ref = oracle.ternary_matmul_u32(w, s, xf, 1, K, N)
+    y = _run(ctx, w, s, xf, xb, "bf16", yt)
+    if yt == "f32":
+        assert_close_f32(host(y), ref)
+    else:
+        assert_bf16_within_1ulp(y.view(torch.int16).cpu().numpy().view(np.uint16), ref)
+
+
+@pytest.mark.parametrize("K,N", [(4160, 300), (12352, 40), (4096, 64)])
+def test_single_token_rows_bit_exact_on_dyadic_inputs(ctx, K, N):
+    t, w, s, x, xb = _dyadic_case(1, K, N, K + N)
+    ref = (x @ t.T.astype(np.float32)) * s[None, :]
+    y = host(_run(ctx, w, s, x, xb, "bf16", "f32"))
+    np.testing.assert_array_equal(y, ref)
+
+
+def test_single_token_unaligned_weights(ctx):
+    """Packed weights 4 bytes past a 16-byte boundary take the 16-row tiles
+    (dword loads); both placements match the oracle."""
+    K, N = 4096, 300
+    t, w, s, xf, xb = _case("rows/unaligned", 1, K, N)
+    ref = oracle.ternary_matmul_u32(w, s, xf, 1, K, N)
+    buf = torch.zeros(w.size + 4, dtype=torch.int32, device="cuda:0")
+    buf[1:1 + w.size] = torch.from_numpy(w.reshape(-1).view(np.int32)).to("cuda:0")
+    w_un = buf[1:1 + w.size].view(N, K // 16)
+    assert w_un.data_ptr() % 16 == 4
+    y = torch.empty((1, N), dtype=torch.float32, device="cuda:0")
+    ctx.ternary_linear(w_un, dev_f32(s), dev_bf16(xb), y)
+    torch.cuda.synchronize()
+    assert_close_f32(host(y), ref)
+    assert_close_f32(host(_run(ctx, w, s, xf, xb, "bf16", "f32")), ref)
+
+
 @pytest.mark.parametrize("B", [1, 4, 16])
 @pytest.mark.parametrize("K,N", [(4096, 11008), (11008, 4096)])
 def test_decode_gemv_config_shapes(ctx, B, K, N):
