@@ -107,6 +107,33 @@ def test_single_token_rows_bit_exact_on_dyadic_inputs(ctx, K, N):
     np.testing.assert_array_equal(y, ref)
 
 
+@pytest.mark.parametrize("M,K,N", [(2, 64, 9), (3, 1024, 70), (4, 2048, 33), (2, 4096, 300), (3, 4160, 20),
+                                   (4, 8192, 17), (4, 11008, 100), (2, 12352, 40), (4, 14336, 8),
+                                   (3, 14400, 8)])
+@pytest.mark.parametrize("yt", ["f32", "bf16"])
+def test_two_to_four_tokens_rows(ctx, M, K, N, yt):
+    """2 <= B <= 4 bf16 tokens: 4 rows x 4 segments per MFMA for K % 64 == 0
+    up to 14336 (1 to 14 windows of 1024 codes, rounded up to the
+    instantiated counts; rows past N in the last workgroup), the 16-row
+    tiles at 14400."""
+    name = f"rows4/{M}x{K}x{N}"
+    t, w, s, xf, xb = _case(name, M, K, N)
+    ref = oracle.ternary_matmul_u32(w, s, xf, M, K, N)
+    y = _run(ctx, w, s, xf, xb, "bf16", yt)
+    if yt == "f32":
+        assert_close_f32(host(y), ref)
+    else:
+        assert_bf16_within_1ulp(y.view(torch.int16).cpu().numpy().view(np.uint16), ref)
+
+
+@pytest.mark.parametrize("M,K,N", [(4, 4160, 64), (2, 11008, 48), (3, 4096, 130)])
+def test_two_to_four_tokens_bit_exact_on_dyadic_inputs(ctx, M, K, N):
+    t, w, s, x, xb = _dyadic_case(M, K, N, M * K + N)
+    ref = (x @ t.T.astype(np.float32)) * s[None, :]
+    y = host(_run(ctx, w, s, x, xb, "bf16", "f32"))
+    np.testing.assert_array_equal(y, ref)
+
+
 def test_single_token_unaligned_weights(ctx):
     """Packed weights 4 bytes past a 16-byte boundary take the 16-row tiles
     (dword loads); both placements match the oracle."""
