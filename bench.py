@@ -204,7 +204,9 @@ def main():
     launch_time = 2 * t_gu + t_dn
     achieved = launch_bytes / launch_time / 1e9
     roofline = {
-        "kernel": "frx::gemv_kernel (linear, bf16 in, bf16 out)",
+        "kernel": "frx::gemv_rows_kernel (B=1, linear, bf16 in, bf16 out)" if B == 1 else
+                  "frx::gemv_rows4_kernel" if 2 <= B <= 4 else "frx::gemv_kernel (staged)" if B < 8 else
+                  "frx::gemv_direct_kernel / gemv_tall_kernel",
         "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
         "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
         "avg_us": {"11008x4096": round(t_gu * 1e6, 3), "4096x11008": round(t_dn * 1e6, 3)},
@@ -264,8 +266,8 @@ def main():
     extra = {"decode_ffn_fused_llama7b": fused}
     if B == 1 and not args.no_extra:
         # The decode configuration's other batch sizes: the same three
-        # projections, weights rotating, timed the same way (B < 8: staged
-        # gemv_kernel; B >= 8: gemv_direct_kernel).
+        # projections, weights rotating, timed the same way (B = 4: the
+        # four-segment rows kernel; B = 16: the tall and direct kernels).
         batches = {}
         for bx in (4, 16):
             _, xbx = synth.activations("bench/decode", "x", bx, H)
@@ -299,7 +301,8 @@ def main():
                 "hbm_fraction": round(bytes_x / (el_x / args.steps) / 1e9 / HBM_PEAK_GBS, 4),
                 "avg_us": {"11008x4096": round(tgu_x * 1e6, 3), "4096x11008": round(tdn_x * 1e6, 3)},
                 "launch_time_distribution": dist_x,
-                "kernel": "frx::gemv_kernel (staged)" if bx < 8 else "frx::gemv_direct_kernel",
+                "kernel": "frx::gemv_rows4_kernel" if bx <= 4 else "frx::gemv_kernel (staged)" if bx < 8
+                else "frx::gemv_tall_kernel (11008x4096) / gemv_direct_kernel (4096x11008)",
             }
             log(f"bench: decode GEMV B={bx}: {batches[f'B{bx}']['us_per_step']} us/step, "
                 f"{batches[f'B{bx}']['gb_s']} GB/s")
