@@ -686,7 +686,14 @@ __global__ __launch_bounds__(256) void moe_down_kernel(
 // bf16 hi | lo halves of one row of h2 [A][2 I]. down: the hi halves and the
 // lo halves of h2's rows times W_down in separate workgroups (blockIdx.z),
 // each into its own fp32 partial [A][H]; the combine adds the two.
-constexpr int MOE2_BN = 256;
+// (512-row tiles measured slower for both GEMMs at the 512-token, 16-expert
+// layer: gate/up 85.6 -> 98.5 us, down 73.5 -> 83.8 us; half the
+// workgroups at two waves per SIMD cost more than the halved activation
+// re-reads save)
+#ifndef FRX_MOE_DOWN_BN
+#define FRX_MOE_DOWN_BN 256
+#endif
+constexpr int MOE2_BN = FRX_MOE_DOWN_BN;
 // gate/up tile: MOE_GU_BN / 2 gate rows and the same up rows (128 measured
 // slower at the 512-token, 16-expert layer: 92 us against 89 us, although
 // its 2112 workgroups fill the CUs more evenly than 1056)
@@ -719,7 +726,8 @@ __global__ __launch_bounds__(256) void moe_gateup2_kernel(
   // Epilogue: fragments to LDS in two passes of 32 tokens (row pitch
   // MOE_GU_BN + 16 floats); each thread then owns 4 gate columns (and the
   // same 4 up columns MOE_GU_BN / 2 further) of a run of tokens per pass.
-  constexpr int PF = MOE_GU_BN + 16, P = 2, TMP = MOE_BM / P, FMP = Core::FM / P;
+  constexpr int PF = MOE_GU_BN + 16, P = (MOE_BM / 2) * PF <= Core::LDS_DWORDS ? 2 : 4;
+  constexpr int TMP = MOE_BM / P, FMP = Core::FM / P;
   static_assert(TMP * PF <= Core::LDS_DWORDS, "epilogue staging");
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, l16 = lane & 15, g = lane >> 4;
   float *st = reinterpret_cast<float *>(lds);
