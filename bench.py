@@ -23,10 +23,9 @@ linear, each with median, p10 and p90.
 Per-launch GPU times carry the median, p10 and p90 over the individual
 replays (decode) or launches (prefill, 2:4, MoE; 200 back-to-back).
 
-extra: the decode FFN of the same layer through frx_ternary_ffn (one launch
-with a grid barrier, and the two-launch execution: gate/up/SiLU launch +
-fp32-input down launch), the same decode step at B = 4 and 16 (default
-run), prefill GEMM (X[2048,4096] x
+extra: the decode FFN of the same layer through frx_ternary_ffn (the
+default, one-launch and two-launch executions), the same decode step at
+B = 4 and 16 (default run), prefill GEMM (X[2048,4096] x
 W[N,4096], N in {4096, 11008}), 2:4 sparse GEMM and the MoE expert layer, as
 TFLOP/s and fraction of the dense bf16 MFMA peak.
 """
@@ -228,10 +227,12 @@ def main():
         except (OSError, ValueError, KeyError):
             pass
 
-    # The decode FFN of the same layer through frx_ternary_ffn: one launch
-    # (gate/up/SiLU, grid barrier, down; the default at B <= 3), and the
-    # two-launch execution (gate/up/SiLU launch with fp32 product, then the
-    # fp32-input down GEMV).
+    # The decode FFN of the same layer through frx_ternary_ffn, in each of
+    # its modes: the default (B = 1: gate/up/SiLU rows into bf16 hi/lo planes
+    # of h, then the down rows over both planes; B = 2..3: one launch with a
+    # grid barrier; B >= 4: two launches), the one-launch kernel (B <= 3) and
+    # the two-launch execution. The frx_ternary_glu entry (fp32 h) and the
+    # fp32-input down GEMV are timed on their own as well.
     b_glu = 2 * (I * H // 4 + 4 * I) + 2 * B * H + 4 * B * I
     b_down32 = H * I // 4 + 4 * H + 4 * B * I + 2 * B * H
     b_ffn = 2 * (I * H // 4 + 4 * I) + (H * I // 4 + 4 * H) + 2 * B * H + 2 * B * H
@@ -240,7 +241,10 @@ def main():
         wg, wu, wd = W[i % copies]
         ctx.ternary_ffn(x, wg, s_g, wu, s_u, wd, s_d, y)
     fused = {"algorithmic_bytes_per_step": b_ffn}
-    for mode, key in ((frx.FFN_AUTO, "default"), (frx.FFN_TWO_LAUNCH, "two_launch")):
+    modes = [(frx.FFN_AUTO, "default"), (frx.FFN_TWO_LAUNCH, "two_launch")]
+    if B <= 3:
+        modes.append((frx.FFN_ONE_LAUNCH, "one_launch"))
+    for mode, key in modes:
         ctx.set_ffn_mode(mode)
         el_f, _ = timed(lambda: [ffn_step(i) for i in range(args.steps)])
         ctx.synchronize()
@@ -248,20 +252,26 @@ def main():
                       "gb_s": round(b_ffn / (el_f / args.steps) / 1e9, 1),
                       "hbm_fraction": round(b_ffn / (el_f / args.steps) / 1e9 / HBM_PEAK_GBS, 4)}
     ctx.set_ffn_mode(frx.FFN_AUTO)
-    fused["default"]["launches_per_step"] = 1 if B <= 3 else 2
-    if ffn_traffic and "ffn1_llama7b" in ffn_traffic and B <= 3:
-        fused["default"]["traffic"] = ffn_traffic["ffn1_llama7b"]
+    fused["default"]["launches_per_step"] = 1 if 2 <= B <= 3 else 2
+    fused["default"]["kernels"] = (
+        "gemv_rows_kernel gate/up/SiLU -> h planes, gemv_rows_kernel down over both planes" if B == 1 else
+        "ffn1_kernel" if B <= 3 else "GLU + down GEMV (planes at B >= 8)")
     fused["two_launch"]["launches_per_step"] = 2
+    if "one_launch" in fused:
+        fused["one_launch"].update({"launches_per_step": 1, "kernels": "ffn1_kernel"})
+        if ffn_traffic and "ffn1_llama7b" in ffn_traffic:
+            fused["one_launch"]["traffic"] = ffn_traffic["ffn1_llama7b"]
     t_glu = per_launch(lambda i: ctx.ternary_glu(x, W[i][0], s_g, W[i][1], s_u, h), 1, reps)
     t_d32 = per_launch(lambda i: ctx.ternary_linear(W[i][2], s_d, h, y), 1, reps)
-    fused["two_launch"].update({
+    fused["glu_entry_and_f32_down"] = {
         "gate_up_silu_avg_us": round(t_glu * 1e6, 3), "gate_up_silu_gb_s": round(b_glu / t_glu / 1e9, 1),
         "down_f32_in_avg_us": round(t_d32 * 1e6, 3), "down_f32_in_gb_s": round(b_down32 / t_d32 / 1e9, 1),
         "algorithmic_bytes": {"glu_11008x4096": b_glu, "down_f32_4096x11008": b_down32},
-        "traffic": ffn_traffic})
-    log(f"bench: decode FFN: {fused['default']['us_per_step']} us/step "
-        f"({fused['default']['launches_per_step']} launch), two-launch {fused['two_launch']['us_per_step']} us; "
-        f"gate/up {fused['two_launch']['gate_up_silu_avg_us']} us, down {fused['two_launch']['down_f32_in_avg_us']} us")
+        "traffic": ffn_traffic}
+    log(f"bench: decode FFN: default {fused['default']['us_per_step']} us/step "
+        f"({fused['default']['launches_per_step']} launches), two-launch {fused['two_launch']['us_per_step']} us"
+        + (f", one-launch {fused['one_launch']['us_per_step']} us" if "one_launch" in fused else "")
+        + f"; frx_ternary_glu {t_glu * 1e6:.2f} us, fp32-input down {t_d32 * 1e6:.2f} us")
 
     extra = {"decode_ffn_fused_llama7b": fused}
     if B == 1 and not args.no_extra:

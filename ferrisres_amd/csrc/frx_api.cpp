@@ -324,6 +324,18 @@ frx_status frx_ternary_ffn(frx_ctx *ctx, const void *x, frx_dtype xt, const uint
                           "FFN workspace allocation")) != FRX_OK)
     return st;
   hipError_t e;
+  if (ctx->ffn_mode != FRX_FFN_ONE_LAUNCH && xt == FRX_BF16 && aligned16(w_gate) && aligned16(w_up) &&
+      aligned16(w_down) && frx::gemv_rows_ffn_ok((int)M, (int)H, (int)I)) {
+    // one token: gate/up/act into bf16 hi/lo planes of h (the first 4*I
+    // bytes of the workspace), then the down rows over both planes
+    uint16_t *hp = reinterpret_cast<uint16_t *>(ctx->ffn_ws);
+    e = frx::launch_gemv_rows_glu_planes(w_gate, s_gate, w_up, s_up, x, hp, (int)H, (int)I,
+                                         act == FRX_ACT_GELU_TANH, ctx->stream);
+    if (e != hipSuccess) return hip_fail(ctx, e, "ffn gate/up launch");
+    e = frx::launch_gemv_rows_planes(w_down, s_down, hp, y, yt == FRX_BF16, (int)I, (int)H, ctx->stream);
+    if (e != hipSuccess) return hip_fail(ctx, e, "ffn down launch");
+    return FRX_OK;
+  }
   int grid = 0;
   size_t lds = 0;
   const bool one = ctx->ffn_mode != FRX_FFN_TWO_LAUNCH && aligned16(w_gate) && aligned16(w_up) &&

@@ -699,106 +699,150 @@ __device__ __forceinline__ float dpp_f32(float v) {
   return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xF, 0xF, false));
 }
 
-template <typename YT, int WAVES, int RW, int NI>
-__global__ __launch_bounds__(WAVES * 64) void gemv_rows_kernel(const uint32_t *__restrict__ W,
-                                                               const float *__restrict__ scale,
-                                                               const uint16_t *__restrict__ X,
-                                                               YT *__restrict__ Y, int K, int N) {
+// NW = 2 (EPI = GEMV_SWIGLU / GEMV_GEGLU): rows of the gate (W) and up (W2)
+// matrices with the same index against the same x; h = act(g) * u is
+// written as bf16 hi and lo planes (Y = [2][N], |h - hi - lo| <= 2^-17 |h|).
+// XPL = 2: the activations arrive as two bf16 planes (X hi, X2 lo) whose sum
+// is an fp32 vector to 2^-17; both are staged and each word runs four MFMAs
+// into the same accumulator.
+template <typename YT, int WAVES, int RW, int NI, int NW = 1, int XPL = 1, int EPI = GEMV_LINEAR>
+__global__ __launch_bounds__(WAVES * 64) void gemv_rows_kernel(
+    const uint32_t *__restrict__ W, const float *__restrict__ scale, const uint32_t *__restrict__ W2,
+    const float *__restrict__ scale2, const uint16_t *__restrict__ X, const uint16_t *__restrict__ X2,
+    YT *__restrict__ Y, int K, int N) {
+  static_assert((NW == 2) == (EPI != GEMV_LINEAR), "two matrices exactly for the GLU epilogues");
   extern __shared__ __align__(16) uint32_t lds[];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int row0 = ((int)blockIdx.x * WAVES + wave) * RW;
   const int kw = K >> 4;   // words per row
   const int nxp = K >> 3;  // 16-byte pieces of x
   constexpr int NT = WAVES * 64;
-  constexpr int XR = (NI * 512 + NT - 1) / NT;  // staging rounds over NI * 4096 activations
+  constexpr int PP = NI * 512;                  // staged pieces per plane (NI * 4096 activations)
+  constexpr int PD = NI * 64 * ROWS_XCH;        // LDS dwords per plane
+  constexpr int XR = (XPL * PP + NT - 1) / NT;  // staging rounds
   // 1. activations (zero past K), issued before the weights so that waiting
   //    for them does not wait for the weights
   u32x4 xs[XR];
-  const u32x4 *X4 = reinterpret_cast<const u32x4 *>(X);
 #pragma unroll
   for (int r = 0; r < XR; r++) {
-    const int j = tid + r * NT;
+    const int j = tid + r * NT, pl = j >= PP ? 1 : 0, jp = j - pl * PP;
+    const u32x4 *X4 = reinterpret_cast<const u32x4 *>(pl ? X2 : X);
     xs[r] = (u32x4){0u, 0u, 0u, 0u};
-    if (j < nxp) xs[r] = X4[j];
+    if (pl < XPL && jp < nxp) xs[r] = X4[jp];
   }
-  // 2. the wave's weights: RW rows x NI windows
-  u32x4 wv[RW][NI];
+  // 2. the wave's weights: NW matrices x RW rows x NI windows
+  u32x4 wv[NW][RW][NI];
+  float sc[NW][RW];
 #pragma unroll
-  for (int rr = 0; rr < RW; rr++) {
-    const uint32_t *wr = W + (size_t)min(row0 + rr, N - 1) * kw;
-#pragma unroll
-    for (int i = 0; i < NI; i++)
-      wv[rr][i] = *reinterpret_cast<const u32x4 *>(wr + min(i * 256 + 4 * lane, kw - 4));
-  }
-  float sc[RW];
-#pragma unroll
-  for (int rr = 0; rr < RW; rr++) sc[rr] = scale[min(row0 + rr, N - 1)];
-  // 3. stage: 16-byte piece j -> chunk j/8, slot j%8
-#pragma unroll
-  for (int r = 0; r < XR; r++) {
-    const int j = tid + r * NT;
-    if (j < NI * 512) *reinterpret_cast<u32x4 *>(lds + (j >> 3) * ROWS_XCH + (j & 7) * 4) = xs[r];
-  }
-  __syncthreads();
-  // 4. per window: the lane's 64 activations, then each row's 4 words
-  f32x4 acc[RW];
-#pragma unroll
-  for (int rr = 0; rr < RW; rr++) acc[rr] = (f32x4){0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-  for (int i = 0; i < NI; i++) {
-    u32x4 xb[8];
-    const uint32_t *xp = lds + (i * 64 + lane) * ROWS_XCH;
-#pragma unroll
-    for (int q = 0; q < 8; q++) xb[q] = *reinterpret_cast<const u32x4 *>(xp + 4 * q);
+  for (int m = 0; m < NW; m++)
 #pragma unroll
     for (int rr = 0; rr < RW; rr++) {
-      const uint32_t wq[4] = {wv[rr][i].x, wv[rr][i].y, wv[rr][i].z, wv[rr][i].w};
+      const int row = min(row0 + rr, N - 1);
+      const uint32_t *wr = (m ? W2 : W) + (size_t)row * kw;
 #pragma unroll
-      for (int j = 0; j < 4; j++) {
-        u32x4 lo, hi;
-        unpack16_nat(wq[j], lo, hi);
-        acc[rr] = mfma16(lo, xb[2 * j], acc[rr]);
-        acc[rr] = mfma16(hi, xb[2 * j + 1], acc[rr]);
-      }
+      for (int i = 0; i < NI; i++)
+        wv[m][rr][i] = *reinterpret_cast<const u32x4 *>(wr + min(i * 256 + 4 * lane, kw - 4));
+      sc[m][rr] = (m ? scale2 : scale)[row];
     }
+  // 3. stage: plane p, 16-byte piece j -> chunk j/8, slot j%8
+#pragma unroll
+  for (int r = 0; r < XR; r++) {
+    const int j = tid + r * NT, pl = j >= PP ? 1 : 0, jp = j - pl * PP;
+    if (pl < XPL) *reinterpret_cast<u32x4 *>(lds + pl * PD + (jp >> 3) * ROWS_XCH + (jp & 7) * 4) = xs[r];
+  }
+  __syncthreads();
+  // 4. per window: the lane's 64 activations (per plane), then each row's 4 words
+  f32x4 acc[NW][RW];
+#pragma unroll
+  for (int m = 0; m < NW; m++)
+#pragma unroll
+    for (int rr = 0; rr < RW; rr++) acc[m][rr] = (f32x4){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int i = 0; i < NI; i++) {
+    u32x4 xb[XPL][8];
+#pragma unroll
+    for (int p = 0; p < XPL; p++) {
+      const uint32_t *xp = lds + p * PD + (i * 64 + lane) * ROWS_XCH;
+#pragma unroll
+      for (int q = 0; q < 8; q++) xb[p][q] = *reinterpret_cast<const u32x4 *>(xp + 4 * q);
+    }
+#pragma unroll
+    for (int m = 0; m < NW; m++)
+#pragma unroll
+      for (int rr = 0; rr < RW; rr++) {
+        const uint32_t wq[4] = {wv[m][rr][i].x, wv[m][rr][i].y, wv[m][rr][i].z, wv[m][rr][i].w};
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+          u32x4 lo, hi;
+          unpack16_nat(wq[j], lo, hi);
+#pragma unroll
+          for (int p = 0; p < XPL; p++) {
+            acc[m][rr] = mfma16(lo, xb[p][2 * j], acc[m][rr]);
+            acc[m][rr] = mfma16(hi, xb[p][2 * j + 1], acc[m][rr]);
+          }
+        }
+      }
   }
   // 5. diagonal: lane (c = l%16, rg = l/16) holds C[4rg + e][c]
   const int c = lane & 15, rg = lane >> 4, e = c & 3;
   const bool diag = (c >> 2) == rg;
-  float tot[RW];
+  float tot[NW][RW];
 #pragma unroll
-  for (int rr = 0; rr < RW; rr++) {
-    float v = e == 0 ? acc[rr][0] : e == 1 ? acc[rr][1] : e == 2 ? acc[rr][2] : acc[rr][3];
-    v = diag ? v : 0.f;
-    v += dpp_f32<0xB1>(v);  // quad_perm [1,0,3,2]
-    v += dpp_f32<0x4E>(v);  // quad_perm [2,3,0,1]
-    const float a = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
-    const float b = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 20));
-    const float d = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 40));
-    const float f = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 60));
-    tot[rr] = ((a + b) + (d + f)) * sc[rr] * 0.5f;  // 0.5 undoes the 2*dec(c) encoding
-  }
+  for (int m = 0; m < NW; m++)
+#pragma unroll
+    for (int rr = 0; rr < RW; rr++) {
+      const f32x4 A = acc[m][rr];
+      float v = e == 0 ? A[0] : e == 1 ? A[1] : e == 2 ? A[2] : A[3];
+      v = diag ? v : 0.f;
+      v += dpp_f32<0xB1>(v);  // quad_perm [1,0,3,2]
+      v += dpp_f32<0x4E>(v);  // quad_perm [2,3,0,1]
+      const float a = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+      const float b = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 20));
+      const float d = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 40));
+      const float f = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 60));
+      tot[m][rr] = ((a + b) + (d + f)) * sc[m][rr] * 0.5f;  // 0.5 undoes the 2*dec(c) encoding
+    }
   if (lane < RW) {
-    float t = tot[0];
+    float t[NW];
 #pragma unroll
-    for (int rr = 1; rr < RW; rr++)
-      if (lane == rr) t = tot[rr];
+    for (int m = 0; m < NW; m++) {
+      t[m] = tot[m][0];
+#pragma unroll
+      for (int rr = 1; rr < RW; rr++)
+        if (lane == rr) t[m] = tot[m][rr];
+    }
     const int row = row0 + lane;
     if (row < N) {
-      if constexpr (sizeof(YT) == 2) Y[row] = (uint16_t)bf16_rne(t);
-      else Y[row] = t;
+      if constexpr (EPI != GEMV_LINEAR) {
+        const float h = (EPI == GEMV_GEGLU ? act_gelu_tanh(t[0]) : act_silu(t[0])) * t[1];
+        uint32_t hh, hl;
+        split_bf16(h, hh, hl);
+        Y[row] = (uint16_t)hh;
+        Y[N + row] = (uint16_t)hl;
+      } else if constexpr (sizeof(YT) == 2) {
+        Y[row] = (uint16_t)bf16_rne(t[0]);
+      } else {
+        Y[row] = t[0];
+      }
     }
   }
 }
 
-template <typename YT, int RW, int NI>
-static hipError_t launch_gemv_rows_w(const uint32_t *w, const float *scale, const void *x, void *y, int K,
-                                     int N, hipStream_t stream) {
+template <typename YT, int RW, int NI, int NW = 1, int XPL = 1, int EPI = GEMV_LINEAR>
+static hipError_t launch_gemv_rows_w(const uint32_t *w, const float *scale, const uint32_t *w2, const float *scale2,
+                                     const void *x, const void *x2, void *y, int K, int N, hipStream_t stream) {
   constexpr int WAVES = 8;
   const dim3 grid((N + WAVES * RW - 1) / (WAVES * RW));
-  const size_t lds = (size_t)NI * 64 * ROWS_XCH * 4;
-  hipLaunchKernelGGL((gemv_rows_kernel<YT, WAVES, RW, NI>), grid, dim3(WAVES * 64), lds, stream, w, scale,
-                     reinterpret_cast<const uint16_t *>(x), reinterpret_cast<YT *>(y), K, N);
+  const size_t lds = (size_t)XPL * NI * 64 * ROWS_XCH * 4;
+  if (lds > 64 * 1024) {
+    static std::atomic<uint64_t> done;
+    const hipError_t e = opt_in_lds(reinterpret_cast<const void *>(&gemv_rows_kernel<YT, WAVES, RW, NI, NW, XPL, EPI>),
+                                    (int)lds, done);
+    if (e != hipSuccess) return e;
+  }
+  hipLaunchKernelGGL((gemv_rows_kernel<YT, WAVES, RW, NI, NW, XPL, EPI>), grid, dim3(WAVES * 64), lds, stream, w,
+                     scale, w2, scale2, reinterpret_cast<const uint16_t *>(x),
+                     reinterpret_cast<const uint16_t *>(x2), reinterpret_cast<YT *>(y), K, N);
   return hipGetLastError();
 }
 
@@ -952,10 +996,46 @@ template <typename YT>
 static hipError_t launch_gemv_rows(const uint32_t *w, const float *scale, const void *x, void *y, int K, int N,
                                    hipStream_t stream) {
   const int ni = (K + 4095) / 4096;
-  if (ni == 1) return launch_gemv_rows_w<YT, 2, 1>(w, scale, x, y, K, N, stream);
-  if (ni == 2) return launch_gemv_rows_w<YT, 1, 2>(w, scale, x, y, K, N, stream);
-  if (ni == 3) return launch_gemv_rows_w<YT, 1, 3>(w, scale, x, y, K, N, stream);
-  return launch_gemv_rows_w<YT, 1, 4>(w, scale, x, y, K, N, stream);
+  if (ni == 1) return launch_gemv_rows_w<YT, 2, 1>(w, scale, w, scale, x, x, y, K, N, stream);
+  if (ni == 2) return launch_gemv_rows_w<YT, 1, 2>(w, scale, w, scale, x, x, y, K, N, stream);
+  if (ni == 3) return launch_gemv_rows_w<YT, 1, 3>(w, scale, w, scale, x, x, y, K, N, stream);
+  return launch_gemv_rows_w<YT, 1, 4>(w, scale, w, scale, x, x, y, K, N, stream);
+}
+
+// Decode FFN of one bf16 token through the rows kernels: gate/up/act into
+// hi/lo planes of h, then the down rows over both planes.
+bool gemv_rows_ffn_ok(int M, int H, int I) {
+  return M == 1 && H % 64 == 0 && I % 64 == 0 && H <= 4 * 4096 && I <= 4 * 4096;
+}
+
+hipError_t launch_gemv_rows_glu_planes(const uint32_t *w_gate, const float *s_gate, const uint32_t *w_up,
+                                       const float *s_up, const void *x, uint16_t *h_planes, int K, int N,
+                                       int gelu, hipStream_t stream) {
+  const int ni = (K + 4095) / 4096;
+#define FRX_ROWS_GLU(NI)                                                                                        \
+  return gelu ? launch_gemv_rows_w<uint16_t, 1, NI, 2, 1, GEMV_GEGLU>(w_gate, s_gate, w_up, s_up, x, x, h_planes, \
+                                                                      K, N, stream)                           \
+              : launch_gemv_rows_w<uint16_t, 1, NI, 2, 1, GEMV_SWIGLU>(w_gate, s_gate, w_up, s_up, x, x,      \
+                                                                       h_planes, K, N, stream)
+  if (ni == 1) FRX_ROWS_GLU(1);
+  if (ni == 2) FRX_ROWS_GLU(2);
+  if (ni == 3) FRX_ROWS_GLU(3);
+  FRX_ROWS_GLU(4);
+#undef FRX_ROWS_GLU
+}
+
+hipError_t launch_gemv_rows_planes(const uint32_t *w, const float *scale, const uint16_t *x_planes, void *y,
+                                   int yt_bf16, int K, int N, hipStream_t stream) {
+  const int ni = (K + 4095) / 4096;
+  const uint16_t *lo = x_planes + K;
+#define FRX_ROWS_PL(RW, NI)                                                                                   \
+  return yt_bf16 ? launch_gemv_rows_w<uint16_t, RW, NI, 1, 2>(w, scale, w, scale, x_planes, lo, y, K, N, stream) \
+                 : launch_gemv_rows_w<float, RW, NI, 1, 2>(w, scale, w, scale, x_planes, lo, y, K, N, stream)
+  if (ni == 1) FRX_ROWS_PL(2, 1);
+  if (ni == 2) FRX_ROWS_PL(1, 2);
+  if (ni == 3) FRX_ROWS_PL(1, 3);
+  FRX_ROWS_PL(1, 4);
+#undef FRX_ROWS_PL
 }
 
 hipError_t launch_gemv(const uint32_t *w, const float *scale, const void *x,

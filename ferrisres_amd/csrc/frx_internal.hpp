@@ -32,6 +32,15 @@ inline hipError_t opt_in_lds(const void *fn, int bytes, std::atomic<uint64_t> &d
 constexpr int GEMV_DIRECT_MIN_B = FRX_GEMV_DIRECT_MIN_B;
 
 // Decode GEMV, B <= 16 tokens (frx_gemv.hip).
+// One bf16 token through the whole-rows kernels (M == 1, H and I multiples
+// of 64 up to 16384): gate/up/act into bf16 hi/lo planes h_planes [2][N],
+// then the linear rows over both planes (x_planes [2][K]).
+bool gemv_rows_ffn_ok(int M, int H, int I);
+hipError_t launch_gemv_rows_glu_planes(const uint32_t *w_gate, const float *s_gate, const uint32_t *w_up,
+                                       const float *s_up, const void *x, uint16_t *h_planes, int K, int N,
+                                       int gelu, hipStream_t stream);
+hipError_t launch_gemv_rows_planes(const uint32_t *w, const float *scale, const uint16_t *x_planes, void *y,
+                                   int yt_bf16, int K, int N, hipStream_t stream);
 hipError_t launch_gemv(const uint32_t *w, const float *scale, const void *x,
                        int xt_bf16, void *y, int yt_bf16, int B, int K, int N,
                        hipStream_t stream);

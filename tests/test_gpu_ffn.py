@@ -77,6 +77,37 @@ def test_ffn_small_parity(ctx, M, H, I, act):
     assert_close_f32(host(y), ref_ffn(xw, mats, act == frx.ACT_GELU_TANH))
 
 
+@pytest.mark.parametrize("H,I", [(64, 64), (1024, 2816), (2048, 5632), (128, 16384), (16384, 128),
+                                 (4160, 8256)])
+@pytest.mark.parametrize("act", [frx.ACT_SILU, frx.ACT_GELU_TANH])
+def test_ffn_single_token_rows(ctx, H, I, act):
+    """One bf16 token in the default mode: gate/up/act by whole rows into bf16
+    hi/lo planes of h, then the down rows over both planes (H and I multiples
+    of 64 up to 16384: one to four 4096-column windows on either side; the
+    down launch at I = 16384 holds 74 KB of LDS)."""
+    xf, xb, mats = make_ffn(f"ffn/rows{H}_{I}", 1, H, I)
+    xw = synth.bf16_bits_to_f32(xb)
+    ref = ref_ffn(xw, mats, act == frx.ACT_GELU_TANH)
+    assert_close_f32(host(run_ffn(ctx, xf, xb, mats, act)), ref)
+    yb = run_ffn(ctx, xf, xb, mats, act, yt="bf16")
+    assert_bf16_within_1ulp(yb.view(torch.int16).cpu().numpy().view(np.uint16), ref)
+
+
+def test_ffn_single_token_rows_matches_one_launch(ctx):
+    """The rows path (default at M = 1) and the one-launch kernel agree to
+    fp32 rounding (different summation orders)."""
+    xf, xb, mats = make_ffn("ffn/rows_vs_one", 1, 4096, 11008)
+    y_rows = host(run_ffn(ctx, xf, xb, mats, frx.ACT_SILU))
+    ctx.set_ffn_mode(frx.FFN_ONE_LAUNCH)
+    try:
+        y_one = host(run_ffn(ctx, xf, xb, mats, frx.ACT_SILU))
+        ctx.synchronize()
+    finally:
+        ctx.set_ffn_mode(frx.FFN_AUTO)
+    rms = float(np.sqrt(np.mean(y_one.astype(np.float64) ** 2)))
+    assert np.max(np.abs(y_rows - y_one)) <= 1e-4 * rms
+
+
 @pytest.mark.parametrize("M", [2, 24])
 def test_ffn_f32_in_bf16_out(ctx, M):
     xf, xb, mats = make_ffn(f"ffn/f32_{M}", M, 128, 208)
