@@ -20,6 +20,7 @@ LIB_PATH = os.path.join(HERE, "libfrx_ternary.so")
 FRX_F32, FRX_BF16 = 0, 1
 ACT_SILU, ACT_GELU_TANH = 0, 1
 FFN_AUTO, FFN_ONE_LAUNCH, FFN_TWO_LAUNCH = 0, 1, 2
+QUANT_ABSMEAN, QUANT_STE = 0, 1
 
 _STATUS = {
     0: "Ok", 1: "Gpu", 2: "Shape", 3: "Device", 4: "Shader", 5: "OOM", 6: "Unsupported",
@@ -66,6 +67,7 @@ _SIGS = {
     "frx_upload_stm": (_int, [_vp, _vp, _sz, ctypes.POINTER(_vp), ctypes.POINTER(_vp), ctypes.POINTER(_u32),
                               ctypes.POINTER(_u32)]),
     "frx_sparse24_cpu_to_gpu_device": (_int, [_vp, _vp, _vp, _u32, _u32, _vp]),
+    "frx_quantize_ternary": (_int, [_vp, _vp, _int, _u32, _u32, _int, _vp, _vp]),
     "frx_free": (_int, [_vp, _vp]),
     "frx_pack_ternary_u8": (_int, [_vp, _sz, _vp]),
     "frx_unpack_ternary_u8": (_int, [_vp, _sz, _vp]),
@@ -309,6 +311,17 @@ class Context:
         _check(lib().frx_sparse24_cpu_to_gpu_device(self._h, _ptr(patterns), _ptr(signs), N, K, _ptr(meta)),
                self._h)
         return meta
+
+    def quantize_ternary(self, w, rule: int, packed, scale):
+        """frx_quantize_ternary: each row of w [N][K] (f32 or bf16 device
+        tensor) quantised on its own (QUANT_ABSMEAN: quantize_ternary,
+        ternary.rs:31-57; QUANT_STE: BitLinear::forward_ste,
+        shadow_weights.rs:203-231) into packed [N][K/16] u32 codes and
+        scale [N] f32. Stream-ordered."""
+        N, K = w.shape
+        _check(lib().frx_quantize_ternary(self._h, _ptr(w), _dtype_code(w), N, K, rule, _ptr(packed),
+                                          _ptr(scale)), self._h)
+        return packed, scale
 
     def set_ffn_mode(self, mode: int):
         """frx_set_ffn_mode: FFN_AUTO, FFN_ONE_LAUNCH or FFN_TWO_LAUNCH."""

@@ -538,6 +538,21 @@ frx_status frx_upload_ternary(frx_ctx *ctx, const uint8_t *packed, uint32_t N, u
   return st;
 }
 
+frx_status frx_quantize_ternary(frx_ctx *ctx, const void *w, frx_dtype wt, uint32_t N, uint32_t K,
+                                frx_quant_rule rule, uint32_t *packed, float *scale) {
+  frx_status st = enter(ctx);
+  if (st != FRX_OK) return st;
+  if (!w || !packed || !scale) return fail(ctx, FRX_ERR_SHAPE, "null pointer argument");
+  if (K == 0 || K % 16 != 0) return fail(ctx, FRX_ERR_SHAPE, "K=%u must be a positive multiple of 16", K);
+  if (wt != FRX_F32 && wt != FRX_BF16) return fail(ctx, FRX_ERR_UNSUPPORTED, "dtype must be FRX_F32 or FRX_BF16");
+  if (rule != FRX_QUANT_ABSMEAN && rule != FRX_QUANT_STE) return fail(ctx, FRX_ERR_UNSUPPORTED, "quantisation rule");
+  if (N > 0x7FFFFFFFu || K > 0x7FFFFFF0u) return fail(ctx, FRX_ERR_SHAPE, "N=%u K=%u too large", N, K);
+  const hipError_t e =
+      frx::launch_quantize(w, wt == FRX_BF16, (int)N, (int)K, (int)rule, packed, scale, ctx->stream);
+  if (e != hipSuccess) return hip_fail(ctx, e, "quantise launch");
+  return FRX_OK;
+}
+
 frx_status frx_sparse24_cpu_to_gpu_device(frx_ctx *ctx, const uint8_t *patterns, const uint8_t *signs,
                                           uint32_t N, uint32_t K, uint32_t *meta) {
   frx_status st = enter(ctx);

@@ -85,6 +85,11 @@ hipError_t launch_ffn1(const void *x, int xt_bf16, const uint32_t *wg, const flo
                        hipStream_t stream);
 
 // CPU 2:4 layout -> GPU 5-bit layout on the device (frx_ingest.hip); K % 4 == 0.
+// Per-row ternary quantisation (rule 0: quantize_ternary, 1: the STE rule of
+// BitLinear::forward_ste) of W [N][K] (f32, or bf16 when wt_bf16), K % 16 ==
+// 0: scale [N], packed [N][K/16].
+hipError_t launch_quantize(const void *w, int wt_bf16, int N, int K, int rule, uint32_t *packed, float *scale,
+                           hipStream_t stream);
 hipError_t launch_sp24_cpu_to_gpu(const uint8_t *patterns, const uint8_t *signs, int N, int K, uint32_t *meta,
                                   hipStream_t stream);
 

@@ -206,6 +206,28 @@ frx_status frx_upload_stm(frx_ctx *ctx, const void *image, size_t len, uint32_t 
 frx_status frx_sparse24_cpu_to_gpu_device(frx_ctx *ctx, const uint8_t *patterns,
                                           const uint8_t *signs, uint32_t N, uint32_t K,
                                           uint32_t *meta);
+/* ---- on-device quantisation (training-side producer of the layout) ----------
+ * Replaces quantize_ternary (src/model/ternary.rs:31-57, used by
+ * quantize_ste / TernarySteResult::requantize :237-258 and
+ * BitLinear::requantize, src/training/shadow_weights.rs:152-160) and the
+ * on-the-fly quantisation of BitLinear::forward_ste (shadow_weights.rs:
+ * 203-231), applied to every row of W [N][K] on its own (N = 1 with K = n
+ * is the reference's call on a whole n-value tensor):
+ *   FRX_QUANT_ABSMEAN: alpha = mean|w| / sqrt(2/pi) (1 when sum|w| is not
+ *     > 0), q = clamp(round_half_away(w * (1 / alpha)), -1, 1);
+ *   FRX_QUANT_STE: alpha = mean|w|, q = +1 where w / alpha > 0.5, -1 where
+ *     < -0.5, else 0; every q = 0 when alpha < 1e-10.
+ * sum|w| is accumulated left to right in f32, as in the reference, so alpha
+ * and every code are bit-identical to the reference applied to that row.
+ * w: [N][K] f32, or bf16 (bf16 shadow weights, widened exactly); packed:
+ * [N][K/16] u32 codes (q + 1, 16 per word LSB first: pack_ternary then
+ * pack_ternary_u32); scale: [N] f32 alpha (the dequantised row is
+ * alpha * q). Device pointers, stream-ordered, no allocation. Requires
+ * K % 16 == 0 and K > 0. */
+typedef enum frx_quant_rule { FRX_QUANT_ABSMEAN = 0, FRX_QUANT_STE = 1 } frx_quant_rule;
+frx_status frx_quantize_ternary(frx_ctx *ctx, const void *w, frx_dtype wt, uint32_t N, uint32_t K,
+                                frx_quant_rule rule, uint32_t *packed, float *scale);
+
 /* Releases a buffer returned by frx_upload_ternary / frx_upload_stm. */
 frx_status frx_free(frx_ctx *ctx, void *dev_ptr);
 

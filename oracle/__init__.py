@@ -47,6 +47,7 @@ def lib():
             "frxo_ternary_matmul_blocked": (None, [_vp, _vp, _sz, _vp, _sz, _sz, _sz, _vp]),
             "frxo_bench_ternary_matmul": (None, [_vp, _vp, _f, _sz, _sz, _sz, _vp]),
             "frxo_quantize_ternary": (_f, [_vp, _sz, _vp]),
+            "frxo_quantize_ste": (_f, [_vp, _sz, _vp]),
             "frxo_pack_sparse24_gpu": (ctypes.c_int, [_vp, _sz, _sz, _vp, _vp]),
             "frxo_sparse24_gpu_matmul": (None, [_vp, _vp, _vp, _sz, _sz, _sz, _vp]),
             "frxo_sparse24_gpu_decode": (None, [_vp, _sz, _sz, _vp]),
@@ -172,6 +173,15 @@ def quantize_ternary(weights):
     out = np.zeros(w.size, np.int8)
     alpha = lib().frxo_quantize_ternary(_p(w), w.size, _p(out))
     return out, np.float32(alpha)
+
+
+def quantize_ste(weights):
+    """BitLinear::forward_ste's quantisation (shadow_weights.rs:203-231):
+    (codes i8, alpha)."""
+    w = _c(weights, np.float32).reshape(-1)
+    out = np.zeros(w.size, np.int8)
+    a = lib().frxo_quantize_ste(_p(w), w.size, _p(out))
+    return out, np.float32(a)
 
 
 def pack_sparse24_gpu(weights):

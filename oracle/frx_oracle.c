@@ -336,6 +336,30 @@ float frxo_quantize_ternary(const float *weights, size_t n, int8_t *out) {
   return alpha;
 }
 
+/*
+ * shadow_weights.rs:203-231 BitLinear::forward_ste, the on-the-fly
+ * quantisation: alpha = sum|w| / n (left-to-right f32 sum), then per value
+ * normalized = w / alpha; +1 if > 0.5, -1 if < -0.5, else 0; all 0 when
+ * alpha < 1e-10. Returns alpha. Pinned by closed cases in the tests: the
+ * +-0.5 boundaries map to 0 (strict comparisons, unlike round()), a constant
+ * row maps to its sign, tiny and zero rows to 0.
+ */
+float frxo_quantize_ste(const float *weights, size_t n, int8_t *out) {
+  if (n == 0) return 0.0f;
+  float sum = 0.0f;
+  for (size_t i = 0; i < n; i++) sum += fabsf(weights[i]);
+  const float alpha = sum / (float)n;
+  for (size_t i = 0; i < n; i++) {
+    if (alpha < 1e-10f) {
+      out[i] = 0;
+    } else {
+      const float t = weights[i] / alpha;
+      out[i] = t > 0.5f ? 1 : t < -0.5f ? -1 : 0;
+    }
+  }
+  return alpha;
+}
+
 /* ---- 2:4 sparse ---------------------------------------------------------- */
 
 /* kernels/sparse_ternary.rs:45-52 and sparse_ternary.rs:27-34 (same LUT). */

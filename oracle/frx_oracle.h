@@ -55,6 +55,7 @@ void frxo_bench_ternary_matmul(const float *a, const int8_t *weights,
                                float scale, size_t m, size_t n, size_t k,
                                float *out);
 float frxo_quantize_ternary(const float *weights, size_t n, int8_t *out);
+float frxo_quantize_ste(const float *weights, size_t n, int8_t *out);
 
 /* ---- 2:4 sparse, GPU (WGSL) layout ------------------------------------- */
 int frxo_pack_sparse24_gpu(const int8_t *weights, size_t rows, size_t cols,

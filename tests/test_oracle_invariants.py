@@ -298,3 +298,26 @@ def test_ffn_oracle_matches_float64(gelu):
     other = oracle.ffn_forward(x, synth.pack_rows_u32(tg), sg, synth.pack_rows_u32(tu), su,
                                synth.pack_rows_u32(td), sd, gelu=not gelu)
     assert np.abs(other - y).max() > 1e-3 * np.abs(y).max()
+
+
+def test_quantize_ste_closed_cases():
+    """BitLinear::forward_ste (shadow_weights.rs:203-231): alpha = mean|w|,
+    strict +-0.5 thresholds on w / alpha (unlike round(), which takes +-0.5
+    away from zero), all zero below alpha = 1e-10."""
+    q, a = oracle.quantize_ste(np.array([0.5, -0.5, 1.5, -1.5], np.float32))  # alpha = 1
+    assert a == 1.0 and q.tolist() == [0, 0, 1, -1]
+    q, a = oracle.quantize_ste(np.array([0.6, -0.4], np.float32))  # alpha = 0.5: t = 1.2, -0.8
+    assert a == np.float32(0.5) and q.tolist() == [1, -1]
+    q, a = oracle.quantize_ste(np.full(16, -0.25, np.float32))  # constant row: its sign
+    assert a == np.float32(0.25) and (q == -1).all()
+    for row in (np.zeros(8, np.float32), np.full(8, 1e-11, np.float32)):
+        q, a = oracle.quantize_ste(row)
+        assert a < 1e-10 and (q == 0).all()
+    q, a = oracle.quantize_ste(np.array([1.0, np.nan, -3.0], np.float32))  # NaN mean: every t is NaN
+    assert np.isnan(a) and (q == 0).all()
+    # quantize_ternary rounds +-0.5 away from zero: with |w| summing to
+    # 4 * ABSMEAN_NORM exactly, alpha = 1 and w * (1 / alpha) = w
+    norm = np.float32(0.7978845608)
+    w = np.array([0.5, -0.5, 1.5, np.float32(4) * norm - np.float32(2.5)], np.float32)
+    qt, at = oracle.quantize_ternary(w)
+    assert at == 1.0 and qt.tolist() == [1, -1, 1, 1]
