@@ -1,9 +1,14 @@
 // frx_gemv.hip — decode ternary GEMV for M <= 16 tokens on gfx950.
 //
 // Replaces the WGSL entry ternary_matmul_main
-// (src/compute/kernels/ternary_matmul.rs:32-75) for decode shapes.
+// (src/compute/kernels/ternary_matmul.rs:32-75) for decode shapes. Four
+// kernels: gemv_rows_kernel (one bf16 token: whole rows per wave, 16 row
+// segments per MFMA), gemv_rows4_kernel (2-4 bf16 tokens: 4 rows x 4
+// segments), gemv_direct_kernel / gemv_tall_kernel (8-16 bf16 tokens,
+// operands from L2) and gemv_kernel below (f32 activations, other token
+// counts and unaligned shapes); launch_gemv picks one.
 //
-// Mapping. One workgroup (WAVES waves) owns a 16-row tile of W. The 16 rows
+// gemv_kernel mapping. One workgroup (WAVES waves) owns a 16-row tile of W. The 16 rows
 // are the M side of v_mfma_f32_16x16x32_bf16 and the (<= 16) tokens its N
 // side. Lane (r = l%16, g = l/16) streams 16-byte chunks (64 codes) of row r
 // with dwordx4 loads; the 4 lanes of a row read 64 contiguous bytes per
