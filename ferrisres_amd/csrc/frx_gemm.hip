@@ -124,10 +124,19 @@ static int device_cus() {
   return c;
 }
 
-template <int BM, typename YT>
+// Tile of the launches whose 128 x 256 grid gives each CU at most one
+// workgroup: 0 = 64 tokens x 256 rows (default); 1 = 128 x 128, which halves
+// the decode VALU per MFMA (a wave's 64 codes per lane then feed 32 MFMAs
+// instead of 16) but doubles the activation reads from LDS: measured slower
+// (2048x4096x4096: 66.1 against 63.8 us).
+#ifndef FRX_GEMM2_SMALL_TILE
+#define FRX_GEMM2_SMALL_TILE 0
+#endif
+
+template <int BM, typename YT, int BN = 256>
 static hipError_t launch_gemm2_bm(const uint32_t *w, const float *scale, const void *x, void *y,
                                   int M, int K, int N, hipStream_t stream) {
-  constexpr int BN = 256, WM = FRX_GEMM2_WM, WN = 4 / FRX_GEMM2_WM, NS = FRX_GEMM2_NS;
+  constexpr int WM = FRX_GEMM2_WM, WN = 4 / FRX_GEMM2_WM, NS = FRX_GEMM2_NS;
   using Core = Gemm2<BM, BN, WM, WN, NS, false>;
   constexpr int lds = Core::LDS_DWORDS * 4;
   static std::atomic<uint64_t> done;
@@ -150,7 +159,11 @@ static hipError_t launch_gemm2_t(const uint32_t *w, const float *scale, const vo
                                  int M, int K, int N, hipStream_t stream) {
 #if FRX_GEMM2_WM == 1
   const long tiles128 = (long)((M + 127) / 128) * ((N + 255) / 256);
+#if FRX_GEMM2_SMALL_TILE == 1
+  if (tiles128 <= device_cus()) return launch_gemm2_bm<128, YT, 128>(w, scale, x, y, M, K, N, stream);
+#else
   if (tiles128 <= device_cus()) return launch_gemm2_bm<64, YT>(w, scale, x, y, M, K, N, stream);
+#endif
 #endif
   return launch_gemm2_bm<128, YT>(w, scale, x, y, M, K, N, stream);
 }
