@@ -126,9 +126,9 @@ static int device_cus() {
 
 // Tile of the launches whose 128 x 256 grid gives each CU at most one
 // workgroup: 0 = 64 tokens x 256 rows (default); 1 = 128 x 128, which halves
-// the decode VALU per MFMA (a wave's 64 codes per lane then feed 32 MFMAs
-// instead of 16) but doubles the activation reads from LDS: measured slower
-// (2048x4096x4096: 66.1 against 63.8 us).
+// the decode VALU per MFMA (per K step a wave decodes 32 codes per lane
+// instead of 64 for the same 32 MFMAs) but doubles the activation reads
+// from LDS: measured slower (2048x4096x4096: 66.1 against 63.8 us).
 #ifndef FRX_GEMM2_SMALL_TILE
 #define FRX_GEMM2_SMALL_TILE 0
 #endif
