@@ -68,8 +68,8 @@ def main():
     args = ap.parse_args()
 
     if args.gpus != 1:
-        print(f"bench.py: this build runs on exactly one GPU; --gpus {args.gpus} is not supported "
-              "(the multi-GPU sharding plan is described in DESIGN.md, not run).", file=sys.stderr)
+        print(f"bench.py: the ternary linear path runs on exactly one GPU here; --gpus {args.gpus} "
+              "is not supported (sharding across GPUs is a design, not run).", file=sys.stderr)
         sys.exit(2)
 
     import torch
