@@ -866,7 +866,11 @@ static hipError_t launch_gemv_rows_w(const uint32_t *w, const float *scale, cons
 // read a zero block). Measured over rotating weights at B = 4: 6.41 ->
 // 5.78 us (11008x4096) and 6.76 -> 5.93 us (4096x11008) per launch against
 // the 16-row tiles.
-template <typename YT, int WAVES, int RW, int NI>
+// KS = 2: the windows of each row group are split between two waves (the
+// first and second halves of K), so a workgroup whose LDS holds long token
+// rows still has two waves per SIMD; the second wave's partial tile goes
+// through LDS and is added to the first's in that order.
+template <typename YT, int WAVES, int RW, int NI, int KS = 1>
 __global__ __launch_bounds__(WAVES * 64) void gemv_rows4_kernel(const uint32_t *__restrict__ W,
                                                                 const float *__restrict__ scale,
                                                                 const uint16_t *__restrict__ X,
@@ -877,8 +881,12 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_rows4_kernel(const uint32_t *
   constexpr int NT = WAVES * 64;
   constexpr int PPT = NI * 128;            // staged 16-byte pieces per token
   constexpr int XR = (4 * PPT + NT - 1) / NT;
+  constexpr int GW = WAVES / KS;            // waves per K part
+  constexpr int NIP = (NI + KS - 1) / KS;   // windows per K part
+  static_assert(WAVES % KS == 0, "K parts split the waves evenly");
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int grp0 = ((int)blockIdx.x * WAVES + wave) * RW;  // first 4-row group of the wave
+  const int part = wave / GW, wg = wave - part * GW;
+  const int grp0 = ((int)blockIdx.x * GW + wg) * RW;  // first 4-row group of the wave
   const int kw = K >> 4;
   const int nxp = K >> 3;  // 16-byte pieces per activation row
   // 1. activations of the B tokens (zero past K and for tokens >= B)
@@ -893,14 +901,16 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_rows4_kernel(const uint32_t *
   // 2. weights: lane (a, s, g) of group G reads row 4G + a at (4g + s) * 16
   //    bytes into each 256-byte window (clamped inside the row)
   const int a = (lane & 15) >> 2, s = lane & 3, g = lane >> 4;
-  u32x4 wv[RW][NI];
+  u32x4 wv[RW][NIP];
   float sc[RW];
 #pragma unroll
   for (int rr = 0; rr < RW; rr++) {
     const uint32_t *wr = W + (size_t)min((grp0 + rr) * 4 + a, N - 1) * kw;
 #pragma unroll
-    for (int i = 0; i < NI; i++)
-      wv[rr][i] = *reinterpret_cast<const u32x4 *>(wr + min(i * 64 + (g * 4 + s) * 4, kw - 4));
+    for (int i = 0; i < NIP; i++) {
+      const int win = min(part * NIP + i, NI - 1);  // a window past NI is loaded, never used
+      wv[rr][i] = *reinterpret_cast<const u32x4 *>(wr + min(win * 64 + (g * 4 + s) * 4, kw - 4));
+    }
     sc[rr] = scale[min((grp0 + rr) * 4 + g, N - 1)];  // the row this lane's sum lands on
   }
   // 3. stage: token t, piece p -> chunk p/8 slot p%8; zero block after the tokens
@@ -918,9 +928,11 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_rows4_kernel(const uint32_t *
 #pragma unroll
   for (int rr = 0; rr < RW; rr++) acc[rr] = (f32x4){0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-  for (int i = 0; i < NI; i++) {
+  for (int i = 0; i < NIP; i++) {
+    const int win = part * NIP + i;
+    if (win >= NI) continue;  // wave-uniform: the last part's missing windows
     u32x4 xb[8];
-    const uint32_t *xp = live ? lds + tcol * TS + (i * 16 + g * 4 + scol) * ROWS_XCH : lds + 4 * TS;
+    const uint32_t *xp = live ? lds + tcol * TS + (win * 16 + g * 4 + scol) * ROWS_XCH : lds + 4 * TS;
 #pragma unroll
     for (int q = 0; q < 8; q++) xb[q] = *reinterpret_cast<const u32x4 *>(xp + (live ? 4 * q : 4 * (q & 1)));
 #pragma unroll
@@ -934,6 +946,18 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_rows4_kernel(const uint32_t *
         acc[rr] = mfma16(hi, xb[2 * j + 1], acc[rr]);
       }
     }
+  }
+  if constexpr (KS > 1) {
+    // second-half partials through LDS (after the zero block), added in order
+    f32x4 *cb = reinterpret_cast<f32x4 *>(lds + 4 * TS + 32);
+    if (part == 1) {
+#pragma unroll
+      for (int rr = 0; rr < RW; rr++) cb[(wg * RW + rr) * 64 + lane] = acc[rr];
+    }
+    __syncthreads();
+    if (part != 0) return;
+#pragma unroll
+    for (int rr = 0; rr < RW; rr++) acc[rr] = acc[rr] + cb[(wg * RW + rr) * 64 + lane];
   }
   // 5. lane (col, rg) register e holds C[(a=rg, s=e)][(t=col/4, s'=col%4)]
   const int e = lane & 3;
@@ -951,31 +975,39 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_rows4_kernel(const uint32_t *
   }
 }
 
-template <typename YT, int WAVES, int RW, int NI>
+template <typename YT, int WAVES, int RW, int NI, int KS = 1>
 static hipError_t launch_gemv_rows4_w(const uint32_t *w, const float *scale, const void *x, void *y, int B,
                                       int K, int N, hipStream_t stream) {
-  const dim3 grid((N + WAVES * RW * 4 - 1) / (WAVES * RW * 4));
-  const size_t lds = ((size_t)4 * (NI * 16 * ROWS_XCH + 16) + 32) * 4;
+  constexpr int GW = WAVES / KS;
+  const dim3 grid((N + GW * RW * 4 - 1) / (GW * RW * 4));
+  const size_t lds = ((size_t)4 * (NI * 16 * ROWS_XCH + 16) + 32) * 4 + (KS > 1 ? (size_t)GW * RW * 64 * 16 : 0);
   if (lds > 64 * 1024) {
     static std::atomic<uint64_t> done;
     const hipError_t e =
-        opt_in_lds(reinterpret_cast<const void *>(&gemv_rows4_kernel<YT, WAVES, RW, NI>), (int)lds, done);
+        opt_in_lds(reinterpret_cast<const void *>(&gemv_rows4_kernel<YT, WAVES, RW, NI, KS>), (int)lds, done);
     if (e != hipSuccess) return e;
   }
-  hipLaunchKernelGGL((gemv_rows4_kernel<YT, WAVES, RW, NI>), grid, dim3(WAVES * 64), lds, stream, w, scale,
+  hipLaunchKernelGGL((gemv_rows4_kernel<YT, WAVES, RW, NI, KS>), grid, dim3(WAVES * 64), lds, stream, w, scale,
                      reinterpret_cast<const uint16_t *>(x), reinterpret_cast<YT *>(y), B, K, N);
   return hipGetLastError();
 }
 
 // 2 <= B <= 4 bf16 tokens, K % 64 == 0 and K <= 14336 (four token rows in
 // LDS), 16-byte aligned weights and activations. Up to K = 4096: 8 waves of
-// 2 groups (64 rows per workgroup); above: 4 waves of 1 group (16 rows per
-// workgroup, one workgroup per CU by its LDS). Window counts round up to
-// the instantiated ones (extra windows hold zero activations).
+// 2 groups (64 rows per workgroup); above: 8 waves, each group's windows
+// split between two of them (16 rows per workgroup, one workgroup per CU by
+// its LDS). Window counts round up to the instantiated ones (extra windows
+// hold zero activations).
 static bool gemv_rows4_ok(const uint32_t *w, const void *x, int B, int K) {
   return B >= 2 && B <= 4 && K % 64 == 0 && K <= 14336 && (reinterpret_cast<uintptr_t>(w) & 15) == 0 &&
          (reinterpret_cast<uintptr_t>(x) & 15) == 0;
 }
+
+// K parts of the long-row (K > 4096) launches: 2 measured 7.04 -> 6.48 us
+// per 4096x11008 launch at B = 4 against 1 (4 waves, one per SIMD).
+#ifndef FRX_ROWS4_KS
+#define FRX_ROWS4_KS 2
+#endif
 
 template <typename YT>
 static hipError_t launch_gemv_rows4(const uint32_t *w, const float *scale, const void *x, void *y, int B, int K,
@@ -984,9 +1016,15 @@ static hipError_t launch_gemv_rows4(const uint32_t *w, const float *scale, const
   if (ni <= 1) return launch_gemv_rows4_w<YT, 8, 2, 1>(w, scale, x, y, B, K, N, stream);
   if (ni <= 2) return launch_gemv_rows4_w<YT, 8, 2, 2>(w, scale, x, y, B, K, N, stream);
   if (ni <= 4) return launch_gemv_rows4_w<YT, 8, 2, 4>(w, scale, x, y, B, K, N, stream);
+#if FRX_ROWS4_KS == 2
+  if (ni <= 8) return launch_gemv_rows4_w<YT, 8, 1, 8, 2>(w, scale, x, y, B, K, N, stream);
+  if (ni <= 11) return launch_gemv_rows4_w<YT, 8, 1, 11, 2>(w, scale, x, y, B, K, N, stream);
+  return launch_gemv_rows4_w<YT, 8, 1, 14, 2>(w, scale, x, y, B, K, N, stream);
+#else
   if (ni <= 8) return launch_gemv_rows4_w<YT, 4, 1, 8>(w, scale, x, y, B, K, N, stream);
   if (ni <= 11) return launch_gemv_rows4_w<YT, 4, 1, 11>(w, scale, x, y, B, K, N, stream);
   return launch_gemv_rows4_w<YT, 4, 1, 14>(w, scale, x, y, B, K, N, stream);
+#endif
 }
 
 // One bf16 token, K % 64 == 0, K <= 16384, 16-byte aligned weights and
