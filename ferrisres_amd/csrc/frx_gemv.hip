@@ -993,38 +993,28 @@ static hipError_t launch_gemv_rows4_w(const uint32_t *w, const float *scale, con
 }
 
 // 2 <= B <= 4 bf16 tokens, K % 64 == 0 and K <= 14336 (four token rows in
-// LDS), 16-byte aligned weights and activations. Up to K = 4096: 8 waves of
-// 2 groups (64 rows per workgroup); above: 8 waves, each group's windows
-// split between two of them (16 rows per workgroup, one workgroup per CU by
-// its LDS). Window counts round up to the instantiated ones (extra windows
-// hold zero activations).
+// LDS), 16-byte aligned weights and activations. Window counts round up to
+// the instantiated ones (extra windows hold zero activations).
 static bool gemv_rows4_ok(const uint32_t *w, const void *x, int B, int K) {
   return B >= 2 && B <= 4 && K % 64 == 0 && K <= 14336 && (reinterpret_cast<uintptr_t>(w) & 15) == 0 &&
          (reinterpret_cast<uintptr_t>(x) & 15) == 0;
 }
 
-// K parts of the long-row (K > 4096) launches: 2 measured 7.04 -> 6.48 us
-// per 4096x11008 launch at B = 4 against 1 (4 waves, one per SIMD).
-#ifndef FRX_ROWS4_KS
-#define FRX_ROWS4_KS 2
-#endif
 
 template <typename YT>
 static hipError_t launch_gemv_rows4(const uint32_t *w, const float *scale, const void *x, void *y, int B, int K,
                                     int N, hipStream_t stream) {
   const int ni = (K + 1023) / 1024;
-  if (ni <= 1) return launch_gemv_rows4_w<YT, 8, 2, 1>(w, scale, x, y, B, K, N, stream);
-  if (ni <= 2) return launch_gemv_rows4_w<YT, 8, 2, 2>(w, scale, x, y, B, K, N, stream);
-  if (ni <= 4) return launch_gemv_rows4_w<YT, 8, 2, 4>(w, scale, x, y, B, K, N, stream);
-#if FRX_ROWS4_KS == 2
+  // one 4-row group per wave and (above one window) each group's windows
+  // split over two waves: 8 waves, 16 or 32 rows per workgroup, so N = 11008
+  // gives 688 workgroups instead of 172 (11008x4096 at B = 4: 6.8 -> 6.0 us
+  // per launch; 4096x11008: 7.04 -> 6.48 us against 4 waves of one group)
+  if (ni <= 1) return launch_gemv_rows4_w<YT, 8, 1, 1>(w, scale, x, y, B, K, N, stream);
+  if (ni <= 2) return launch_gemv_rows4_w<YT, 8, 1, 2, 2>(w, scale, x, y, B, K, N, stream);
+  if (ni <= 4) return launch_gemv_rows4_w<YT, 8, 1, 4, 2>(w, scale, x, y, B, K, N, stream);
   if (ni <= 8) return launch_gemv_rows4_w<YT, 8, 1, 8, 2>(w, scale, x, y, B, K, N, stream);
   if (ni <= 11) return launch_gemv_rows4_w<YT, 8, 1, 11, 2>(w, scale, x, y, B, K, N, stream);
   return launch_gemv_rows4_w<YT, 8, 1, 14, 2>(w, scale, x, y, B, K, N, stream);
-#else
-  if (ni <= 8) return launch_gemv_rows4_w<YT, 4, 1, 8>(w, scale, x, y, B, K, N, stream);
-  if (ni <= 11) return launch_gemv_rows4_w<YT, 4, 1, 11>(w, scale, x, y, B, K, N, stream);
-  return launch_gemv_rows4_w<YT, 4, 1, 14>(w, scale, x, y, B, K, N, stream);
-#endif
 }
 
 // One bf16 token, K % 64 == 0, K <= 16384, 16-byte aligned weights and
