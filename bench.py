@@ -228,8 +228,8 @@ def main():
             pass
 
     # The decode FFN of the same layer through frx_ternary_ffn, in each of
-    # its modes: the default (B = 1: gate/up/SiLU rows into bf16 hi/lo planes
-    # of h, then the down rows over both planes; B = 2..3: one launch with a
+    # its modes: the default (B <= 2: gate/up/SiLU rows into bf16 hi/lo planes
+    # of h, then the down rows over both planes; B = 3: one launch with a
     # grid barrier; B >= 4: two launches), the one-launch kernel (B <= 3) and
     # the two-launch execution. The frx_ternary_glu entry (fp32 h) and the
     # fp32-input down GEMV are timed on their own as well.
@@ -255,10 +255,11 @@ def main():
                       "gb_s": round(b_ffn / (el_f / args.steps) / 1e9, 1),
                       "hbm_fraction": round(b_ffn / (el_f / args.steps) / 1e9 / HBM_PEAK_GBS, 4)}
     ctx.set_ffn_mode(frx.FFN_AUTO)
-    fused["default"]["launches_per_step"] = 1 if 2 <= B <= 3 else 2
+    fused["default"]["launches_per_step"] = 1 if B == 3 else 2
     fused["default"]["kernels"] = (
         "gemv_rows_kernel gate/up/SiLU -> h planes, gemv_rows_kernel down over both planes" if B == 1 else
-        "ffn1_kernel" if B <= 3 else "GLU + down GEMV (planes at B >= 8)")
+        "gemv_rows4_kernel gate/up/SiLU -> h planes, gemv_rows4_kernel down over both planes" if B == 2 else
+        "ffn1_kernel" if B == 3 else "GLU + down GEMV (planes at B >= 8)")
     fused["two_launch"]["launches_per_step"] = 2
     if "one_launch" in fused:
         fused["one_launch"].update({"launches_per_step": 1, "kernels": "ffn1_kernel"})

@@ -336,6 +336,18 @@ frx_status frx_ternary_ffn(frx_ctx *ctx, const void *x, frx_dtype xt, const uint
     if (e != hipSuccess) return hip_fail(ctx, e, "ffn down launch");
     return FRX_OK;
   }
+  if (ctx->ffn_mode != FRX_FFN_ONE_LAUNCH && xt == FRX_BF16 && aligned16(w_gate) && aligned16(w_up) &&
+      aligned16(w_down) && frx::gemv_rows4_ffn_ok((int)M, (int)H, (int)I)) {
+    // two tokens: the same in the 4-segment kernels, the down launch taking
+    // h's hi and lo planes of both tokens as its four token columns
+    uint16_t *hp = reinterpret_cast<uint16_t *>(ctx->ffn_ws);
+    e = frx::launch_gemv_rows4_glu_planes(w_gate, s_gate, w_up, s_up, x, hp, (int)M, (int)H, (int)I,
+                                          act == FRX_ACT_GELU_TANH, ctx->stream);
+    if (e != hipSuccess) return hip_fail(ctx, e, "ffn gate/up launch");
+    e = frx::launch_gemv_rows4_planes(w_down, s_down, hp, y, yt == FRX_BF16, (int)I, (int)H, ctx->stream);
+    if (e != hipSuccess) return hip_fail(ctx, e, "ffn down launch");
+    return FRX_OK;
+  }
   int grid = 0;
   size_t lds = 0;
   const bool one = ctx->ffn_mode != FRX_FFN_TWO_LAUNCH && aligned16(w_gate) && aligned16(w_up) &&

@@ -870,11 +870,18 @@ static hipError_t launch_gemv_rows_w(const uint32_t *w, const float *scale, cons
 // first and second halves of K), so a workgroup whose LDS holds long token
 // rows still has two waves per SIMD; the second wave's partial tile goes
 // through LDS and is added to the first's in that order.
-template <typename YT, int WAVES, int RW, int NI, int KS = 1>
-__global__ __launch_bounds__(WAVES * 64) void gemv_rows4_kernel(const uint32_t *__restrict__ W,
-                                                                const float *__restrict__ scale,
-                                                                const uint16_t *__restrict__ X,
-                                                                YT *__restrict__ Y, int B, int K, int N) {
+// NW = 2 (EPI = GEMV_SWIGLU / GEMV_GEGLU): gate (W) and up (W2) groups of
+// the same rows against the same tokens; h = act(g) * u is written as bf16
+// hi and lo planes (Y = [2][B][N]). VPL (B = 2): X holds the hi and lo
+// planes of two tokens ([2][2][K]), staged as four token rows; the hi and
+// lo results of a token (quads t and t + 2 of a lane row) are added by one
+// DPP rotation.
+template <typename YT, int WAVES, int RW, int NI, int KS = 1, int NW = 1, int EPI = GEMV_LINEAR, bool VPL = false>
+__global__ __launch_bounds__(WAVES * 64) void gemv_rows4_kernel(
+    const uint32_t *__restrict__ W, const float *__restrict__ scale, const uint32_t *__restrict__ W2,
+    const float *__restrict__ scale2, const uint16_t *__restrict__ X, YT *__restrict__ Y, int B, int K, int N) {
+  static_assert((NW == 2) == (EPI != GEMV_LINEAR), "two matrices exactly for the GLU epilogues");
+  static_assert(!(VPL && NW == 2), "planes feed the linear epilogue");
   extern __shared__ __align__(16) uint32_t lds[];
   constexpr int NCH = NI * 16;             // 64-value chunks per token
   constexpr int TS = NCH * ROWS_XCH + 16;  // token stride (dwords)
@@ -889,6 +896,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_rows4_kernel(const uint32_t *
   const int grp0 = ((int)blockIdx.x * GW + wg) * RW;  // first 4-row group of the wave
   const int kw = K >> 4;
   const int nxp = K >> 3;  // 16-byte pieces per activation row
+  const int BS = VPL ? 2 * B : B;  // staged token rows
   // 1. activations of the B tokens (zero past K and for tokens >= B)
   u32x4 xs[XR];
   const u32x4 *X4 = reinterpret_cast<const u32x4 *>(X);
@@ -896,23 +904,25 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_rows4_kernel(const uint32_t *
   for (int r = 0; r < XR; r++) {
     const int j = tid + r * NT, t = j / PPT, p = j - t * PPT;
     xs[r] = (u32x4){0u, 0u, 0u, 0u};
-    if (t < B && p < nxp) xs[r] = X4[(size_t)t * nxp + p];
+    if (t < BS && p < nxp) xs[r] = X4[(size_t)t * nxp + p];
   }
   // 2. weights: lane (a, s, g) of group G reads row 4G + a at (4g + s) * 16
   //    bytes into each 256-byte window (clamped inside the row)
   const int a = (lane & 15) >> 2, s = lane & 3, g = lane >> 4;
-  u32x4 wv[RW][NIP];
-  float sc[RW];
+  u32x4 wv[NW][RW][NIP];
+  float sc[NW][RW];
 #pragma unroll
-  for (int rr = 0; rr < RW; rr++) {
-    const uint32_t *wr = W + (size_t)min((grp0 + rr) * 4 + a, N - 1) * kw;
+  for (int m = 0; m < NW; m++)
 #pragma unroll
-    for (int i = 0; i < NIP; i++) {
-      const int win = min(part * NIP + i, NI - 1);  // a window past NI is loaded, never used
-      wv[rr][i] = *reinterpret_cast<const u32x4 *>(wr + min(win * 64 + (g * 4 + s) * 4, kw - 4));
+    for (int rr = 0; rr < RW; rr++) {
+      const uint32_t *wr = (m ? W2 : W) + (size_t)min((grp0 + rr) * 4 + a, N - 1) * kw;
+#pragma unroll
+      for (int i = 0; i < NIP; i++) {
+        const int win = min(part * NIP + i, NI - 1);  // a window past NI is loaded, never used
+        wv[m][rr][i] = *reinterpret_cast<const u32x4 *>(wr + min(win * 64 + (g * 4 + s) * 4, kw - 4));
+      }
+      sc[m][rr] = (m ? scale2 : scale)[min((grp0 + rr) * 4 + g, N - 1)];  // the row this lane's sum lands on
     }
-    sc[rr] = scale[min((grp0 + rr) * 4 + g, N - 1)];  // the row this lane's sum lands on
-  }
   // 3. stage: token t, piece p -> chunk p/8 slot p%8; zero block after the tokens
 #pragma unroll
   for (int r = 0; r < XR; r++) {
@@ -923,10 +933,12 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_rows4_kernel(const uint32_t *
   __syncthreads();
   // 4. per window: this lane's 64 activations of token col/4, then the words
   const int tcol = (lane & 15) >> 2, scol = lane & 3;
-  const bool live = tcol < B;
-  f32x4 acc[RW];
+  const bool live = tcol < BS;
+  f32x4 acc[NW][RW];
 #pragma unroll
-  for (int rr = 0; rr < RW; rr++) acc[rr] = (f32x4){0.f, 0.f, 0.f, 0.f};
+  for (int m = 0; m < NW; m++)
+#pragma unroll
+    for (int rr = 0; rr < RW; rr++) acc[m][rr] = (f32x4){0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int i = 0; i < NIP; i++) {
     const int win = part * NIP + i;
@@ -936,59 +948,83 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_rows4_kernel(const uint32_t *
 #pragma unroll
     for (int q = 0; q < 8; q++) xb[q] = *reinterpret_cast<const u32x4 *>(xp + (live ? 4 * q : 4 * (q & 1)));
 #pragma unroll
-    for (int rr = 0; rr < RW; rr++) {
-      const uint32_t wq[4] = {wv[rr][i].x, wv[rr][i].y, wv[rr][i].z, wv[rr][i].w};
+    for (int m = 0; m < NW; m++)
 #pragma unroll
-      for (int j = 0; j < 4; j++) {
-        u32x4 lo, hi;
-        unpack16_nat(wq[j], lo, hi);
-        acc[rr] = mfma16(lo, xb[2 * j], acc[rr]);
-        acc[rr] = mfma16(hi, xb[2 * j + 1], acc[rr]);
+      for (int rr = 0; rr < RW; rr++) {
+        const uint32_t wq[4] = {wv[m][rr][i].x, wv[m][rr][i].y, wv[m][rr][i].z, wv[m][rr][i].w};
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+          u32x4 lo, hi;
+          unpack16_nat(wq[j], lo, hi);
+          acc[m][rr] = mfma16(lo, xb[2 * j], acc[m][rr]);
+          acc[m][rr] = mfma16(hi, xb[2 * j + 1], acc[m][rr]);
+        }
       }
-    }
   }
   if constexpr (KS > 1) {
     // second-half partials through LDS (after the zero block), added in order
     f32x4 *cb = reinterpret_cast<f32x4 *>(lds + 4 * TS + 32);
     if (part == 1) {
 #pragma unroll
-      for (int rr = 0; rr < RW; rr++) cb[(wg * RW + rr) * 64 + lane] = acc[rr];
+      for (int m = 0; m < NW; m++)
+#pragma unroll
+        for (int rr = 0; rr < RW; rr++) cb[((wg * NW + m) * RW + rr) * 64 + lane] = acc[m][rr];
     }
     __syncthreads();
     if (part != 0) return;
 #pragma unroll
-    for (int rr = 0; rr < RW; rr++) acc[rr] = acc[rr] + cb[(wg * RW + rr) * 64 + lane];
+    for (int m = 0; m < NW; m++)
+#pragma unroll
+      for (int rr = 0; rr < RW; rr++) acc[m][rr] = acc[m][rr] + cb[((wg * NW + m) * RW + rr) * 64 + lane];
   }
   // 5. lane (col, rg) register e holds C[(a=rg, s=e)][(t=col/4, s'=col%4)]
   const int e = lane & 3;
 #pragma unroll
   for (int rr = 0; rr < RW; rr++) {
-    float v = e == 0 ? acc[rr][0] : e == 1 ? acc[rr][1] : e == 2 ? acc[rr][2] : acc[rr][3];
-    v += dpp_f32<0xB1>(v);  // quad_perm [1,0,3,2]
-    v += dpp_f32<0x4E>(v);  // quad_perm [2,3,0,1]
+    float v[NW];
+#pragma unroll
+    for (int m = 0; m < NW; m++) {
+      const f32x4 A = acc[m][rr];
+      v[m] = e == 0 ? A[0] : e == 1 ? A[1] : e == 2 ? A[2] : A[3];
+      v[m] += dpp_f32<0xB1>(v[m]);  // quad_perm [1,0,3,2]
+      v[m] += dpp_f32<0x4E>(v[m]);  // quad_perm [2,3,0,1]
+      if constexpr (VPL) v[m] += dpp_f32<0x128>(v[m]);  // row_ror:8: token t's hi + lo
+    }
     const int row = (grp0 + rr) * 4 + g;
-    if (e == 0 && live && row < N) {
-      const float yv = v * sc[rr] * 0.5f;
-      if constexpr (sizeof(YT) == 2) Y[(size_t)tcol * N + row] = (uint16_t)bf16_rne(yv);
-      else Y[(size_t)tcol * N + row] = yv;
+    if (e == 0 && tcol < B && row < N) {
+      if constexpr (EPI != GEMV_LINEAR) {
+        const float gv = v[0] * sc[0][rr] * 0.5f, uv = v[1] * sc[1][rr] * 0.5f;
+        const float h = (EPI == GEMV_GEGLU ? act_gelu_tanh(gv) : act_silu(gv)) * uv;
+        uint32_t hh, hl;
+        split_bf16(h, hh, hl);
+        Y[(size_t)tcol * N + row] = (uint16_t)hh;
+        Y[(size_t)(B + tcol) * N + row] = (uint16_t)hl;
+      } else {
+        const float yv = v[0] * sc[0][rr] * 0.5f;
+        if constexpr (sizeof(YT) == 2) Y[(size_t)tcol * N + row] = (uint16_t)bf16_rne(yv);
+        else Y[(size_t)tcol * N + row] = yv;
+      }
     }
   }
 }
 
-template <typename YT, int WAVES, int RW, int NI, int KS = 1>
-static hipError_t launch_gemv_rows4_w(const uint32_t *w, const float *scale, const void *x, void *y, int B,
-                                      int K, int N, hipStream_t stream) {
+template <typename YT, int WAVES, int RW, int NI, int KS = 1, int NW = 1, int EPI = GEMV_LINEAR, bool VPL = false>
+static hipError_t launch_gemv_rows4_w(const uint32_t *w, const float *scale, const uint32_t *w2,
+                                      const float *scale2, const void *x, void *y, int B, int K, int N,
+                                      hipStream_t stream) {
   constexpr int GW = WAVES / KS;
   const dim3 grid((N + GW * RW * 4 - 1) / (GW * RW * 4));
-  const size_t lds = ((size_t)4 * (NI * 16 * ROWS_XCH + 16) + 32) * 4 + (KS > 1 ? (size_t)GW * RW * 64 * 16 : 0);
+  const size_t lds =
+      ((size_t)4 * (NI * 16 * ROWS_XCH + 16) + 32) * 4 + (KS > 1 ? (size_t)GW * NW * RW * 64 * 16 : 0);
   if (lds > 64 * 1024) {
     static std::atomic<uint64_t> done;
-    const hipError_t e =
-        opt_in_lds(reinterpret_cast<const void *>(&gemv_rows4_kernel<YT, WAVES, RW, NI, KS>), (int)lds, done);
+    const hipError_t e = opt_in_lds(
+        reinterpret_cast<const void *>(&gemv_rows4_kernel<YT, WAVES, RW, NI, KS, NW, EPI, VPL>), (int)lds, done);
     if (e != hipSuccess) return e;
   }
-  hipLaunchKernelGGL((gemv_rows4_kernel<YT, WAVES, RW, NI, KS>), grid, dim3(WAVES * 64), lds, stream, w, scale,
-                     reinterpret_cast<const uint16_t *>(x), reinterpret_cast<YT *>(y), B, K, N);
+  hipLaunchKernelGGL((gemv_rows4_kernel<YT, WAVES, RW, NI, KS, NW, EPI, VPL>), grid, dim3(WAVES * 64), lds, stream,
+                     w, scale, w2, scale2, reinterpret_cast<const uint16_t *>(x), reinterpret_cast<YT *>(y), B, K,
+                     N);
   return hipGetLastError();
 }
 
@@ -1009,12 +1045,55 @@ static hipError_t launch_gemv_rows4(const uint32_t *w, const float *scale, const
   // split over two waves: 8 waves, 16 or 32 rows per workgroup, so N = 11008
   // gives 688 workgroups instead of 172 (11008x4096 at B = 4: 6.8 -> 6.0 us
   // per launch; 4096x11008: 7.04 -> 6.48 us against 4 waves of one group)
-  if (ni <= 1) return launch_gemv_rows4_w<YT, 8, 1, 1>(w, scale, x, y, B, K, N, stream);
-  if (ni <= 2) return launch_gemv_rows4_w<YT, 8, 1, 2, 2>(w, scale, x, y, B, K, N, stream);
-  if (ni <= 4) return launch_gemv_rows4_w<YT, 8, 1, 4, 2>(w, scale, x, y, B, K, N, stream);
-  if (ni <= 8) return launch_gemv_rows4_w<YT, 8, 1, 8, 2>(w, scale, x, y, B, K, N, stream);
-  if (ni <= 11) return launch_gemv_rows4_w<YT, 8, 1, 11, 2>(w, scale, x, y, B, K, N, stream);
-  return launch_gemv_rows4_w<YT, 8, 1, 14, 2>(w, scale, x, y, B, K, N, stream);
+  if (ni <= 1) return launch_gemv_rows4_w<YT, 8, 1, 1>(w, scale, w, scale, x, y, B, K, N, stream);
+  if (ni <= 2) return launch_gemv_rows4_w<YT, 8, 1, 2, 2>(w, scale, w, scale, x, y, B, K, N, stream);
+  if (ni <= 4) return launch_gemv_rows4_w<YT, 8, 1, 4, 2>(w, scale, w, scale, x, y, B, K, N, stream);
+  if (ni <= 8) return launch_gemv_rows4_w<YT, 8, 1, 8, 2>(w, scale, w, scale, x, y, B, K, N, stream);
+  if (ni <= 11) return launch_gemv_rows4_w<YT, 8, 1, 11, 2>(w, scale, w, scale, x, y, B, K, N, stream);
+  return launch_gemv_rows4_w<YT, 8, 1, 14, 2>(w, scale, w, scale, x, y, B, K, N, stream);
+}
+
+// Decode FFN of two bf16 tokens through the 4-segment kernels: gate/up/act
+// into hi/lo planes of h ([2][2][N]), then the down rows with the planes as
+// four token columns (H and I multiples of 64 up to 14336).
+bool gemv_rows4_ffn_ok(int M, int H, int I) {
+  return M == 2 && H % 64 == 0 && I % 64 == 0 && H <= 14336 && I <= 14336;
+}
+
+hipError_t launch_gemv_rows4_glu_planes(const uint32_t *w_gate, const float *s_gate, const uint32_t *w_up,
+                                        const float *s_up, const void *x, uint16_t *h_planes, int B, int K, int N,
+                                        int gelu, hipStream_t stream) {
+  const int ni = (K + 1023) / 1024;
+#define FRX_R4_GLU(NI, KS)                                                                                      \
+  return gelu ? launch_gemv_rows4_w<uint16_t, 8, 1, NI, KS, 2, GEMV_GEGLU>(w_gate, s_gate, w_up, s_up, x,      \
+                                                                           h_planes, B, K, N, stream)         \
+              : launch_gemv_rows4_w<uint16_t, 8, 1, NI, KS, 2, GEMV_SWIGLU>(w_gate, s_gate, w_up, s_up, x,     \
+                                                                            h_planes, B, K, N, stream)
+  if (ni <= 1) FRX_R4_GLU(1, 1);
+  if (ni <= 2) FRX_R4_GLU(2, 2);
+  if (ni <= 4) FRX_R4_GLU(4, 2);
+  if (ni <= 8) FRX_R4_GLU(8, 2);
+  if (ni <= 11) FRX_R4_GLU(11, 2);
+  FRX_R4_GLU(14, 2);
+#undef FRX_R4_GLU
+}
+
+hipError_t launch_gemv_rows4_planes(const uint32_t *w, const float *scale, const uint16_t *x_planes, void *y,
+                                    int yt_bf16, int K, int N, hipStream_t stream) {
+  const int ni = (K + 1023) / 1024;
+#define FRX_R4_PL(NI, KS)                                                                                         \
+  return yt_bf16                                                                                                  \
+             ? launch_gemv_rows4_w<uint16_t, 8, 1, NI, KS, 1, GEMV_LINEAR, true>(w, scale, w, scale, x_planes, y, \
+                                                                                 2, K, N, stream)                 \
+             : launch_gemv_rows4_w<float, 8, 1, NI, KS, 1, GEMV_LINEAR, true>(w, scale, w, scale, x_planes, y, 2, \
+                                                                              K, N, stream)
+  if (ni <= 1) FRX_R4_PL(1, 1);
+  if (ni <= 2) FRX_R4_PL(2, 2);
+  if (ni <= 4) FRX_R4_PL(4, 2);
+  if (ni <= 8) FRX_R4_PL(8, 2);
+  if (ni <= 11) FRX_R4_PL(11, 2);
+  FRX_R4_PL(14, 2);
+#undef FRX_R4_PL
 }
 
 // One bf16 token, K % 64 == 0, K <= 16384, 16-byte aligned weights and

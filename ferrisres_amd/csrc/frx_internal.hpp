@@ -41,6 +41,15 @@ hipError_t launch_gemv_rows_glu_planes(const uint32_t *w_gate, const float *s_ga
                                        int gelu, hipStream_t stream);
 hipError_t launch_gemv_rows_planes(const uint32_t *w, const float *scale, const uint16_t *x_planes, void *y,
                                    int yt_bf16, int K, int N, hipStream_t stream);
+// Two bf16 tokens through the 4-segment kernels (M == 2, H and I multiples of
+// 64 up to 14336): gate/up/act into bf16 hi/lo planes h_planes [2][2][N],
+// then the linear rows over both planes of both tokens (x_planes [2][2][K]).
+bool gemv_rows4_ffn_ok(int M, int H, int I);
+hipError_t launch_gemv_rows4_glu_planes(const uint32_t *w_gate, const float *s_gate, const uint32_t *w_up,
+                                        const float *s_up, const void *x, uint16_t *h_planes, int B, int K, int N,
+                                        int gelu, hipStream_t stream);
+hipError_t launch_gemv_rows4_planes(const uint32_t *w, const float *scale, const uint16_t *x_planes, void *y,
+                                    int yt_bf16, int K, int N, hipStream_t stream);
 hipError_t launch_gemv(const uint32_t *w, const float *scale, const void *x,
                        int xt_bf16, void *y, int yt_bf16, int B, int K, int N,
                        hipStream_t stream);

@@ -48,7 +48,7 @@ typedef enum frx_dtype { FRX_F32 = 0, FRX_BF16 = 1 } frx_dtype;
 typedef enum frx_activation { FRX_ACT_SILU = 0, FRX_ACT_GELU_TANH = 1 } frx_activation;
 /* How frx_ternary_ffn runs at decode sizes (see frx_set_ffn_mode). */
 typedef enum frx_ffn_mode {
-  FRX_FFN_AUTO = 0,        /* M = 1: two whole-row launches; M <= 3: one
+  FRX_FFN_AUTO = 0,        /* M <= 2: two whole-row launches; M = 3: one
                               launch where the shape allows; else two */
   FRX_FFN_ONE_LAUNCH = 1,  /* one launch or FRX_ERR_UNSUPPORTED */
   FRX_FFN_TWO_LAUNCH = 2   /* gate/up/act launch + down launch */
@@ -148,15 +148,15 @@ frx_status frx_ternary_glu(frx_ctx *ctx, const void *x, frx_dtype xt,
  * projection with fp32 input (M <= 16: two launches). Requires H % 16 == 0,
  * I % 16 == 0. The workspace is allocated on the context on first use (and
  * grown), so a first call at a new size must not be under graph capture.
- * One bf16 token (M = 1, H and I multiples of 64 up to 16384, 16-byte
- * aligned weights) runs as two launches that each read whole weight rows
- * per wave, with the intermediate as bf16 hi and lo planes
- * (|h - hi - lo| <= 2^-17 |h|) in the same workspace (FRX_FFN_AUTO and
- * FRX_FFN_TWO_LAUNCH).
+ * One or two bf16 tokens (M = 1: H and I multiples of 64 up to 16384; M = 2:
+ * up to 14336; 16-byte aligned weights) run as two launches that each read
+ * whole weight rows per wave, with the intermediate as bf16 hi and lo
+ * planes (|h - hi - lo| <= 2^-17 |h|) in the same workspace (FRX_FFN_AUTO
+ * and FRX_FFN_TWO_LAUNCH).
  * Other decode sizes (M <= 3, H <= 4096, I <= 11520, H and I multiples of
  * 64, 16-byte aligned weights; LLaMA-7B's 4096/11008 included) run the whole
  * FFN as ONE launch with a grid barrier between the halves (FRX_FFN_AUTO;
- * FRX_FFN_ONE_LAUNCH also at M = 1). That
+ * FRX_FFN_ONE_LAUNCH also at M = 1 and 2). That
  * launch needs all its workgroups (one per CU) resident at once; if another
  * kernel holds CUs so that they are not, its barrier times out, the outputs
  * are invalid and the next frx_synchronize returns FRX_ERR_GPU. Callers that

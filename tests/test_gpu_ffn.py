@@ -93,6 +93,23 @@ def test_ffn_single_token_rows(ctx, H, I, act):
     assert_bf16_within_1ulp(yb.view(torch.int16).cpu().numpy().view(np.uint16), ref)
 
 
+@pytest.mark.parametrize("H,I", [(64, 64), (1024, 2816), (4096, 11008), (128, 14336), (14336, 128),
+                                 (2112, 4160)])
+@pytest.mark.parametrize("act", [frx.ACT_SILU, frx.ACT_GELU_TANH])
+def test_ffn_two_tokens_rows(ctx, H, I, act):
+    """Two bf16 tokens in the default mode: gate/up/act in the 4-segment
+    kernel into bf16 hi/lo planes of h, then the down launch with the two
+    tokens' hi and lo planes as its four token columns (H and I multiples of
+    64 up to 14336: one to fourteen 1024-column windows, split over two
+    waves above one)."""
+    xf, xb, mats = make_ffn(f"ffn/rows2_{H}_{I}", 2, H, I)
+    xw = synth.bf16_bits_to_f32(xb)
+    ref = ref_ffn(xw, mats, act == frx.ACT_GELU_TANH)
+    assert_close_f32(host(run_ffn(ctx, xf, xb, mats, act)), ref)
+    yb = run_ffn(ctx, xf, xb, mats, act, yt="bf16")
+    assert_bf16_within_1ulp(yb.view(torch.int16).cpu().numpy().view(np.uint16), ref)
+
+
 def test_ffn_single_token_rows_matches_one_launch(ctx):
     """The rows path (default at M = 1) and the one-launch kernel agree to
     fp32 rounding (different summation orders)."""
@@ -208,7 +225,11 @@ def test_ffn_one_launch_matches_two_launch(ctx):
         y2 = run_ffn(ctx, xf, xb, mats, frx.ACT_SILU)
     finally:
         ctx.set_ffn_mode(frx.FFN_AUTO)
-    y1 = run_ffn(ctx, xf, xb, mats, frx.ACT_SILU)  # AUTO takes the one-launch path here
+    ctx.set_ffn_mode(frx.FFN_ONE_LAUNCH)
+    try:
+        y1 = run_ffn(ctx, xf, xb, mats, frx.ACT_SILU)
+    finally:
+        ctx.set_ffn_mode(frx.FFN_AUTO)
     ctx.synchronize()
     a, b = host(y1), host(y2)
     assert np.max(np.abs(a - b)) <= 1e-4 * max(1e-30, float(np.sqrt(np.mean(b.astype(np.float64) ** 2))))
