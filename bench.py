@@ -25,7 +25,8 @@ replays (decode) or launches (prefill, 2:4, MoE; 200 back-to-back).
 
 extra: the decode FFN of the same layer through frx_ternary_ffn (the
 default, one-launch and two-launch executions), the same decode step at
-B = 4 and 16 (default run), prefill GEMM (X[2048,4096] x
+B = 4 and 16 (default run), the B=1 GEMV at growing weight sizes (up to
+the stacked LLaMA-70B gate/up, 117 MB), prefill GEMM (X[2048,4096] x
 W[N,4096], N in {4096, 11008}), 2:4 sparse GEMM and the MoE expert layer, as
 TFLOP/s and fraction of the dense bf16 MFMA peak.
 """
@@ -321,6 +322,8 @@ def main():
             log(f"bench: decode GEMV B={bx}: {batches[f'B{bx}']['us_per_step']} us/step, "
                 f"{batches[f'B{bx}']['gb_s']} GB/s")
         extra["decode_gemv_llama7b_batches"] = batches
+    if B == 1 and not args.no_extra:
+        extra["decode_gemv_b1_by_weight_size"] = gemv_size_sweep(torch, ctx, stream, dev)
     if not args.no_extra:
         extra.update(run_extra(torch, frx, synth, ctx, stream, dev))
 
@@ -433,6 +436,60 @@ def run_extra(torch, frx, synth, ctx, stream, dev, only=None, iters=200):
     res["moe_512tok_h2048_i5632_e16_top2"] = {"us": round(dt * 1e6, 2), "tflops": round(tf, 1),
                                               "frac_bf16_peak": round(tf / BF16_PEAK_TFLOPS, 4), **st}
     log(f"bench: MoE: {dt * 1e6:.1f} us, {tf:.1f} TFLOP/s")
+    return res
+
+
+def gemv_size_sweep(torch, ctx, stream, dev, reps=40):
+    """The B=1 decode GEMV (bf16 x, bf16 y) at growing weight sizes: the
+    LLaMA-7B projection, the LLaMA-70B gate/up projection [28672, 8192] and
+    both of them stacked [57344, 8192]. Each launch pays a fixed start-up
+    (dispatch and the first HBM round trip); larger matrices spread it over
+    more bytes, so the rate approaches what the kernel streams at. Weights
+    are uniform ternary codes made on the device, rotating over copies that
+    total >= 0.5 GB; times are HIP events around back-to-back launches. A
+    device copy of the same words (torch, read + write) is timed beside it
+    as the rate a stock streaming kernel gets at that size."""
+    res = {}
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(20240607)
+    shifts = (2 * torch.arange(16, device=dev, dtype=torch.int64))
+    for n, k in ((11008, 4096), (28672, 8192), (57344, 8192)):
+        codes = torch.randint(0, 3, (n, k // 16, 16), generator=gen, device=dev, dtype=torch.int64)
+        w0 = (codes << shifts).sum(dim=2).to(torch.int64)
+        w0 = torch.where(w0 >= 2 ** 31, w0 - 2 ** 32, w0).to(torch.int32)
+        del codes
+        s = torch.full((n,), 0.0159, dtype=torch.float32, device=dev)
+        x = torch.randn((1, k), generator=gen, device=dev).to(torch.bfloat16)
+        y = torch.empty((1, n), dtype=torch.bfloat16, device=dev)
+        nbytes = gemv_bytes(n, k, 1)
+        copies = max(3, int(np.ceil(512e6 / (n * k // 4))) + 1)
+        ws = [w0] + [w0.clone() for _ in range(copies - 1)]
+        it = [0]
+
+        def one():
+            ctx.ternary_linear(ws[it[0] % copies], s, x, y)
+            it[0] += 1
+        st = {}
+        dt = _time_kernel(torch, stream, one, reps * copies, warm=copies, stats=st)
+        # calibration: torch's device copy of the same packed words (read +
+        # write), rotating over the same copies
+        dst = torch.empty_like(w0)
+
+        def copy_only():
+            dst.copy_(ws[it[0] % copies])
+            it[0] += 1
+        dc = _time_kernel(torch, stream, copy_only, reps * copies, warm=copies)
+        wbytes = n * k // 4
+        res[f"{n}x{k}"] = {"us": round(dt * 1e6, 3), "gb_s": round(nbytes / dt / 1e9, 1),
+                           "hbm_fraction": round(nbytes / dt / 1e9 / HBM_PEAK_GBS, 4),
+                           "algorithmic_bytes": nbytes, "weight_copies": copies, **st,
+                           "stock_copy_us": round(dc * 1e6, 3),
+                           "stock_copy_gb_s_read_plus_write": round(2 * wbytes / dc / 1e9, 1)}
+        log(f"bench: GEMV B=1 {n}x{k}: {dt * 1e6:.2f} us, {nbytes / dt / 1e9:.1f} GB/s; "
+            f"torch copy of the weights {dc * 1e6:.2f} us, {2 * wbytes / dc / 1e9:.1f} GB/s read+write")
+        del dst
+        del ws, w0
+        torch.cuda.synchronize()
     return res
 
 

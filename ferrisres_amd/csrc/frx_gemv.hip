@@ -1104,11 +1104,21 @@ static bool gemv_rows_ok(const uint32_t *w, const void *x, int B, int K) {
          (reinterpret_cast<uintptr_t>(x) & 15) == 0;
 }
 
+constexpr int GEMV_ROWS_TALL_N = 16384;  // rows from which a wave owns two rows above 4096 codes
+
 template <typename YT>
 static hipError_t launch_gemv_rows(const uint32_t *w, const float *scale, const void *x, void *y, int K, int N,
                                    hipStream_t stream) {
   const int ni = (K + 4095) / 4096;
   if (ni == 1) return launch_gemv_rows_w<YT, 2, 1>(w, scale, w, scale, x, x, y, K, N, stream);
+  // Tall matrices (more rows than one residency pass holds at one row per
+  // wave: 4 workgroups x 8 waves per CU): two rows per wave, twice the
+  // weight bytes in flight per wave.
+  if (N >= GEMV_ROWS_TALL_N) {
+    if (ni == 2) return launch_gemv_rows_w<YT, 2, 2>(w, scale, w, scale, x, x, y, K, N, stream);
+    if (ni == 3) return launch_gemv_rows_w<YT, 2, 3>(w, scale, w, scale, x, x, y, K, N, stream);
+    return launch_gemv_rows_w<YT, 2, 4>(w, scale, w, scale, x, x, y, K, N, stream);
+  }
   if (ni == 2) return launch_gemv_rows_w<YT, 1, 2>(w, scale, w, scale, x, x, y, K, N, stream);
   if (ni == 3) return launch_gemv_rows_w<YT, 1, 3>(w, scale, w, scale, x, x, y, K, N, stream);
   return launch_gemv_rows_w<YT, 1, 4>(w, scale, w, scale, x, x, y, K, N, stream);

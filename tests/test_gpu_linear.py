@@ -99,7 +99,18 @@ def test_single_token_rows(ctx, K, N, yt):
         assert_bf16_within_1ulp(y.view(torch.int16).cpu().numpy().view(np.uint16), ref)
 
 
-@pytest.mark.parametrize("K,N", [(4160, 300), (12352, 40), (4096, 64)])
+@pytest.mark.parametrize("K,N", [(2048, 16385), (4160, 16400), (8256, 16384), (12352, 16390)])
+def test_single_token_rows_tall(ctx, K, N):
+    """From N = 16384 rows a wave owns two rows at every window count (one
+    to four windows, the last one partial); f32 and bf16 outputs."""
+    t, w, s, xf, xb = _case(f"rows/tall/{K}x{N}", 1, K, N)
+    ref = oracle.ternary_matmul_u32(w, s, xf, 1, K, N)
+    assert_close_f32(host(_run(ctx, w, s, xf, xb, "bf16", "f32")), ref)
+    yb = _run(ctx, w, s, xf, xb, "bf16", "bf16")
+    assert_bf16_within_1ulp(yb.view(torch.int16).cpu().numpy().view(np.uint16), ref)
+
+
+@pytest.mark.parametrize("K,N", [(4160, 300), (12352, 40), (4096, 64), (4160, 16390)])
 def test_single_token_rows_bit_exact_on_dyadic_inputs(ctx, K, N):
     t, w, s, x, xb = _dyadic_case(1, K, N, K + N)
     ref = (x @ t.T.astype(np.float32)) * s[None, :]
