@@ -3,7 +3,8 @@
 // Replaces the WGSL entry ternary_matmul_main
 // (src/compute/kernels/ternary_matmul.rs:32-75) for decode shapes. Four
 // kernels: gemv_rows_kernel (one bf16 token: whole rows per wave, 16 row
-// segments per MFMA), gemv_rows4_kernel (2-4 bf16 tokens: 4 rows x 4
+// segments per MFMA; gemv_rows_stream_kernel is its persistent form for
+// tall matrices), gemv_rows4_kernel (2-4 bf16 tokens: 4 rows x 4
 // segments), gemv_direct_kernel / gemv_tall_kernel (8-16 bf16 tokens,
 // operands from L2) and gemv_kernel below (f32 activations, other token
 // counts and unaligned shapes); launch_gemv picks one.
@@ -851,6 +852,156 @@ static hipError_t launch_gemv_rows_w(const uint32_t *w, const float *scale, cons
   return hipGetLastError();
 }
 
+// ---- tall single-token GEMV: persistent waves, next group in flight ------
+//
+// Above one residency pass the one-shot rows kernel runs in lockstep passes:
+// the resident workgroups load, wait, then decode together, so a pass's
+// loads do not overlap its decode. Here the grid is two workgroups per CU
+// and each wave walks row groups g, g + G, g + 2G, ... (G = waves in the
+// grid), two register sets alternating: the next group's words are loaded
+// before the current group is decoded. The loads are buffer loads issued
+// unconditionally: a group past the end gets an offset beyond the buffer's
+// range and reads zeros without touching memory, so no load sits in a branch
+// (a conditional load makes the compiler copy its registers at the join and
+// wait for it there). Per group the work is the rows kernel's: the same LDS
+// activations, windows, MFMA diagonal and reduction order.
+constexpr uint32_t ROWS_STREAM_OOB = 0x80000000u;  // past every weight buffer this path takes
+
+template <int RW, int NI>
+__device__ __forceinline__ void rows_stream_load(__amdgpu_buffer_rsrc_t wr, const float *__restrict__ scale, int g,
+                                                 int ng, int kw, int N, int lane, u32x4 (&wv)[RW][NI],
+                                                 float (&sc)[RW]) {
+  const bool live = g < ng;
+#pragma unroll
+  for (int rr = 0; rr < RW; rr++) {
+    const int row = min(g * RW + rr, N - 1);
+    const uint32_t base = (uint32_t)row * (uint32_t)kw * 4u;
+#pragma unroll
+    for (int i = 0; i < NI; i++) {
+      const uint32_t off = live ? base + 4u * (uint32_t)min(i * 256 + 4 * lane, kw - 4) : ROWS_STREAM_OOB;
+      wv[rr][i] = __builtin_amdgcn_raw_buffer_load_b128(wr, off, 0, 0);
+    }
+    sc[rr] = scale[row];
+  }
+}
+
+template <typename YT, int RW, int NI>
+__device__ __forceinline__ void rows_stream_group(const uint32_t *lds, const u32x4 (&wv)[RW][NI],
+                                                  const float (&sc)[RW], int g, int N, int lane,
+                                                  YT *__restrict__ Y) {
+  f32x4 acc[RW];
+#pragma unroll
+  for (int rr = 0; rr < RW; rr++) acc[rr] = (f32x4){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int i = 0; i < NI; i++) {
+    u32x4 xb[8];
+    const uint32_t *xp = lds + (i * 64 + lane) * ROWS_XCH;
+#pragma unroll
+    for (int q = 0; q < 8; q++) xb[q] = *reinterpret_cast<const u32x4 *>(xp + 4 * q);
+#pragma unroll
+    for (int rr = 0; rr < RW; rr++) {
+      const uint32_t wq[4] = {wv[rr][i].x, wv[rr][i].y, wv[rr][i].z, wv[rr][i].w};
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        u32x4 lo, hi;
+        unpack16_nat(wq[j], lo, hi);
+        acc[rr] = mfma16(lo, xb[2 * j], acc[rr]);
+        acc[rr] = mfma16(hi, xb[2 * j + 1], acc[rr]);
+      }
+    }
+  }
+  const int c = lane & 15, rg = lane >> 4, e = c & 3;
+  const bool diag = (c >> 2) == rg;
+  float t = 0.f;
+#pragma unroll
+  for (int rr = 0; rr < RW; rr++) {
+    const f32x4 A = acc[rr];
+    float v = e == 0 ? A[0] : e == 1 ? A[1] : e == 2 ? A[2] : A[3];
+    v = diag ? v : 0.f;
+    v += dpp_f32<0xB1>(v);
+    v += dpp_f32<0x4E>(v);
+    const float a = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+    const float b = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 20));
+    const float d = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 40));
+    const float f = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 60));
+    const float tr = ((a + b) + (d + f)) * sc[rr] * 0.5f;  // 0.5 undoes the 2*dec(c) encoding
+    if (lane == rr) t = tr;
+  }
+  const int row = g * RW + lane;
+  if (lane < RW && row < N) {
+    if constexpr (sizeof(YT) == 2) Y[row] = (uint16_t)bf16_rne(t);
+    else Y[row] = t;
+  }
+}
+
+template <typename YT, int WAVES, int RW, int NI>
+__global__ __launch_bounds__(WAVES * 64) void gemv_rows_stream_kernel(const uint32_t *__restrict__ W,
+                                                                      const float *__restrict__ scale,
+                                                                      const uint16_t *__restrict__ X,
+                                                                      YT *__restrict__ Y, int K, int N) {
+  extern __shared__ __align__(16) uint32_t lds[];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int kw = K >> 4, nxp = K >> 3;
+  const int ng = (N + RW - 1) / RW;
+  const int stride = (int)gridDim.x * WAVES;
+  int g = (int)blockIdx.x * WAVES + wave;
+  const __amdgpu_buffer_rsrc_t wr = buffer_rsrc(W, (uint32_t)N * (uint32_t)kw * 4u);
+  constexpr int NT = WAVES * 64;
+  constexpr int PP = NI * 512;
+  constexpr int XR = (PP + NT - 1) / NT;
+  // activations first (zero past K), then the first group's weights
+  u32x4 xs[XR];
+  const u32x4 *X4 = reinterpret_cast<const u32x4 *>(X);
+#pragma unroll
+  for (int r = 0; r < XR; r++) {
+    const int j = tid + r * NT;
+    xs[r] = (u32x4){0u, 0u, 0u, 0u};
+    if (j < PP && j < nxp) xs[r] = X4[j];
+  }
+  u32x4 wa[RW][NI], wb[RW][NI];
+  float sa[RW], sb[RW];
+  rows_stream_load<RW, NI>(wr, scale, g, ng, kw, N, lane, wa, sa);
+#pragma unroll
+  for (int r = 0; r < XR; r++) {
+    const int j = tid + r * NT;
+    if (j < PP) *reinterpret_cast<u32x4 *>(lds + (j >> 3) * ROWS_XCH + (j & 7) * 4) = xs[r];
+  }
+  __syncthreads();
+  for (; g < ng; g += 2 * stride) {  // wave-uniform; no barrier below
+    const int g1 = g + stride, g2 = g1 + stride;
+    rows_stream_load<RW, NI>(wr, scale, g1, ng, kw, N, lane, wb, sb);
+    __builtin_amdgcn_sched_barrier(0);  // keep the prefetch ahead of the decode
+    rows_stream_group<YT, RW, NI>(lds, wa, sa, g, N, lane, Y);
+    rows_stream_load<RW, NI>(wr, scale, g2, ng, kw, N, lane, wa, sa);
+    __builtin_amdgcn_sched_barrier(0);
+    if (g1 < ng) rows_stream_group<YT, RW, NI>(lds, wb, sb, g1, N, lane, Y);
+  }
+}
+
+static int device_cu_count() {
+  static std::atomic<int> cus[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  int n = cus[dev].load(std::memory_order_relaxed);
+  if (n <= 0) {
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cus[dev].store(n, std::memory_order_relaxed);
+  }
+  return n;
+}
+
+template <typename YT, int RW, int NI>
+static hipError_t launch_gemv_rows_stream(const uint32_t *w, const float *scale, const void *x, void *y, int K,
+                                          int N, hipStream_t stream) {
+  constexpr int WAVES = 8;
+  const int ng = (N + RW - 1) / RW;
+  const int grid = std::min((ng + WAVES - 1) / WAVES, 2 * device_cu_count());
+  const size_t lds = (size_t)NI * 64 * ROWS_XCH * 4;  // at most 36 KB (NI <= 4)
+  hipLaunchKernelGGL((gemv_rows_stream_kernel<YT, WAVES, RW, NI>), dim3(grid), dim3(WAVES * 64), lds, stream, w,
+                     scale, reinterpret_cast<const uint16_t *>(x), reinterpret_cast<YT *>(y), K, N);
+  return hipGetLastError();
+}
+
 // ---- two to four bf16 tokens: four rows x four segments per MFMA ----------
 //
 // The same diagonal idea with the 16 MFMA rows as 4 rows x 4 segments and
@@ -1104,7 +1255,7 @@ static bool gemv_rows_ok(const uint32_t *w, const void *x, int B, int K) {
          (reinterpret_cast<uintptr_t>(x) & 15) == 0;
 }
 
-constexpr int GEMV_ROWS_TALL_N = 16384;  // rows from which a wave owns two rows above 4096 codes
+constexpr int GEMV_ROWS_TALL_N = 16384;  // rows from which waves persist over row groups above 4096 codes
 
 template <typename YT>
 static hipError_t launch_gemv_rows(const uint32_t *w, const float *scale, const void *x, void *y, int K, int N,
@@ -1112,9 +1263,15 @@ static hipError_t launch_gemv_rows(const uint32_t *w, const float *scale, const 
   const int ni = (K + 4095) / 4096;
   if (ni == 1) return launch_gemv_rows_w<YT, 2, 1>(w, scale, w, scale, x, x, y, K, N, stream);
   // Tall matrices (more rows than one residency pass holds at one row per
-  // wave: 4 workgroups x 8 waves per CU): two rows per wave, twice the
-  // weight bytes in flight per wave.
+  // wave: 4 workgroups x 8 waves per CU), above one window per row.
   if (N >= GEMV_ROWS_TALL_N) {
+    // persistent waves; buffer offsets are 32-bit with the out-of-range
+    // marker above every weight byte
+    if ((size_t)N * (size_t)K / 4 < (size_t)ROWS_STREAM_OOB) {
+      if (ni == 2) return launch_gemv_rows_stream<YT, 2, 2>(w, scale, x, y, K, N, stream);
+      if (ni == 3) return launch_gemv_rows_stream<YT, 1, 3>(w, scale, x, y, K, N, stream);
+      return launch_gemv_rows_stream<YT, 1, 4>(w, scale, x, y, K, N, stream);
+    }
     if (ni == 2) return launch_gemv_rows_w<YT, 2, 2>(w, scale, w, scale, x, x, y, K, N, stream);
     if (ni == 3) return launch_gemv_rows_w<YT, 2, 3>(w, scale, w, scale, x, x, y, K, N, stream);
     return launch_gemv_rows_w<YT, 2, 4>(w, scale, w, scale, x, x, y, K, N, stream);

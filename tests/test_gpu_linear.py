@@ -101,8 +101,10 @@ def test_single_token_rows(ctx, K, N, yt):
 
 @pytest.mark.parametrize("K,N", [(2048, 16385), (4160, 16400), (8256, 16384), (12352, 16390)])
 def test_single_token_rows_tall(ctx, K, N):
-    """From N = 16384 rows a wave owns two rows at every window count (one
-    to four windows, the last one partial); f32 and bf16 outputs."""
+    """From N = 16384 rows, above one window, persistent waves walk row
+    groups with the next group's words in flight (two, three and four
+    windows, the last one partial; ragged last group); the one-window case
+    stays on the one-shot kernel. f32 and bf16 outputs."""
     t, w, s, xf, xb = _case(f"rows/tall/{K}x{N}", 1, K, N)
     ref = oracle.ternary_matmul_u32(w, s, xf, 1, K, N)
     assert_close_f32(host(_run(ctx, w, s, xf, xb, "bf16", "f32")), ref)
