@@ -99,7 +99,7 @@ def test_single_token_rows(ctx, K, N, yt):
         assert_bf16_within_1ulp(y.view(torch.int16).cpu().numpy().view(np.uint16), ref)
 
 
-@pytest.mark.parametrize("K,N", [(2048, 16385), (4160, 16400), (8256, 16384), (12352, 16390)])
+@pytest.mark.parametrize("K,N", [(2048, 16385), (4160, 16401), (8256, 16384), (12352, 16390)])
 def test_single_token_rows_tall(ctx, K, N):
     """From N = 16384 rows, above one window, persistent waves walk row
     groups with the next group's words in flight (two, three and four
