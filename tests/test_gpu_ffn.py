@@ -78,7 +78,7 @@ def test_ffn_small_parity(ctx, M, H, I, act):
 
 
 @pytest.mark.parametrize("H,I", [(64, 64), (1024, 2816), (2048, 5632), (128, 16384), (16384, 128),
-                                 (4160, 8256)])
+                                 (4160, 8256), (4096, 11008), (12352, 8256)])
 @pytest.mark.parametrize("act", [frx.ACT_SILU, frx.ACT_GELU_TANH])
 def test_ffn_single_token_rows(ctx, H, I, act):
     """One bf16 token in the default mode: gate/up/act by whole rows into bf16
