@@ -309,6 +309,10 @@ frx_status frx_ternary_glu(frx_ctx *ctx, const void *x, frx_dtype xt, const uint
   return glu_into(ctx, x, xt, w_gate, s_gate, w_up, s_up, M, H, I, act == FRX_ACT_GELU_TANH, h);
 }
 
+// Token counts from which the unfused FFN writes h as bf16 hi/lo planes for
+// the unstaged down GEMV (below: fp32 h, staged down).
+static constexpr int FFN_PLANES_MIN_M = 4;
+
 frx_status frx_ternary_ffn(frx_ctx *ctx, const void *x, frx_dtype xt, const uint32_t *w_gate,
                            const float *s_gate, const uint32_t *w_up, const float *s_up,
                            const uint32_t *w_down, const float *s_down, uint32_t M, uint32_t H,
@@ -379,7 +383,7 @@ frx_status frx_ternary_ffn(frx_ctx *ctx, const void *x, frx_dtype xt, const uint
     if (e != hipSuccess) return hip_fail(ctx, e, "one-launch FFN");
     return FRX_OK;
   }
-  if (xt == FRX_BF16 && (int)M >= frx::GEMV_DIRECT_MIN_B && M <= 16) {
+  if (xt == FRX_BF16 && (int)M >= FFN_PLANES_MIN_M && M <= 16) {
     // h as bf16 hi/lo planes (the same M*I*4 bytes), consumed by the down
     // GEMV without staging: at these M the fp32 rows of h do not fit LDS.
     uint16_t *hp = reinterpret_cast<uint16_t *>(ctx->ffn_ws);

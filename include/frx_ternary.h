@@ -152,7 +152,8 @@ frx_status frx_ternary_glu(frx_ctx *ctx, const void *x, frx_dtype xt,
  * up to 14336; 16-byte aligned weights) run as two launches that each read
  * whole weight rows per wave, with the intermediate as bf16 hi and lo
  * planes (|h - hi - lo| <= 2^-17 |h|) in the same workspace (FRX_FFN_AUTO
- * and FRX_FFN_TWO_LAUNCH).
+ * and FRX_FFN_TWO_LAUNCH). With bf16 x at 4 <= M <= 16 the intermediate is
+ * the same pair of bf16 planes, read by the down GEMV without staging.
  * Other decode sizes (M <= 3, H <= 4096, I <= 11520, H and I multiples of
  * 64, 16-byte aligned weights; LLaMA-7B's 4096/11008 included) run the whole
  * FFN as ONE launch with a grid barrier between the halves (FRX_FFN_AUTO;

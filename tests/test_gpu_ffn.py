@@ -146,13 +146,18 @@ def test_glu_parity(ctx, M, H, I, act):
 
 
 def test_ffn_equals_composition(ctx):
-    """The fused path equals glu followed by the fp32-input linear."""
-    M, H, I = 4, 256, 320
+    """Where h stays fp32 (three tokens, two-launch mode) the fused path
+    equals glu followed by the fp32-input linear bit for bit."""
+    M, H, I = 3, 256, 320
     xf, xb, mats = make_ffn("ffn/comp", M, H, I)
     d = {k: (dev_u32(v[0]), dev_f32(v[1])) for k, v in mats.items()}
     x = dev_bf16(xb)
     y = torch.empty((M, H), dtype=torch.float32, device=DEV)
-    ctx.ternary_ffn(x, d["gate"][0], d["gate"][1], d["up"][0], d["up"][1], d["down"][0], d["down"][1], y)
+    ctx.set_ffn_mode(frx.FFN_TWO_LAUNCH)
+    try:
+        ctx.ternary_ffn(x, d["gate"][0], d["gate"][1], d["up"][0], d["up"][1], d["down"][0], d["down"][1], y)
+    finally:
+        ctx.set_ffn_mode(frx.FFN_AUTO)
     h = torch.empty((M, I), dtype=torch.float32, device=DEV)
     ctx.ternary_glu(x, d["gate"][0], d["gate"][1], d["up"][0], d["up"][1], h)
     y2 = torch.empty((M, H), dtype=torch.float32, device=DEV)
