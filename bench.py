@@ -24,8 +24,8 @@ Per-launch GPU times carry the median, p10 and p90 over the individual
 replays (decode) or launches (prefill, 2:4, MoE; 200 back-to-back).
 
 extra: the decode FFN of the same layer through frx_ternary_ffn (the
-default, one-launch and two-launch executions), the same decode step at
-B = 4 and 16 (default run), the B=1 GEMV at growing weight sizes (up to
+default, one-launch and two-launch executions), the same decode step and
+decode FFN at B = 4 and 16 (default run), the B=1 GEMV at growing weight sizes (up to
 the stacked LLaMA-70B gate/up, 117 MB), prefill GEMM (X[2048,4096] x
 W[N,4096], N in {4096, 11008}), 2:4 sparse GEMM and the MoE expert layer, as
 TFLOP/s and fraction of the dense bf16 MFMA peak.
@@ -310,7 +310,19 @@ def main():
                                dist_x["11008x4096"])
             tdn_x = per_launch(lambda i: ctx.ternary_linear(W[i][2], s_d, xdx, yx), 1, dist_reps,
                                dist_x["4096x11008"])
+            yfx = torch.empty((bx, H), dtype=torch.bfloat16, device=dev)
+
+            def ffnx(i, xx=xx, yfx=yfx):
+                wg, wu, wd = W[i % copies]
+                ctx.ternary_ffn(xx, wg, s_g, wu, s_u, wd, s_d, yfx)
+            with torch.cuda.stream(stream):  # first call outside capture (workspace)
+                ffnx(0)
+            torch.cuda.synchronize()
+            el_fx, _ = timed(lambda: [ffnx(i) for i in range(args.steps)])
+            b_ffn_x = 2 * (I * H // 4 + 4 * I) + (H * I // 4 + 4 * H) + 2 * bx * H + 2 * bx * H
             batches[f"B{bx}"] = {
+                "decode_ffn_us_per_step": round(el_fx / args.steps * 1e6, 2),
+                "decode_ffn_gb_s": round(b_ffn_x / (el_fx / args.steps) / 1e9, 1),
                 "us_per_step": round(el_x / args.steps * 1e6, 2),
                 "gb_s": round(bytes_x / (el_x / args.steps) / 1e9, 1),
                 "hbm_fraction": round(bytes_x / (el_x / args.steps) / 1e9 / HBM_PEAK_GBS, 4),
@@ -320,7 +332,7 @@ def main():
                 else "frx::gemv_tall_kernel (11008x4096) / gemv_direct_kernel (4096x11008)",
             }
             log(f"bench: decode GEMV B={bx}: {batches[f'B{bx}']['us_per_step']} us/step, "
-                f"{batches[f'B{bx}']['gb_s']} GB/s")
+                f"{batches[f'B{bx}']['gb_s']} GB/s; frx_ternary_ffn {batches[f'B{bx}']['decode_ffn_us_per_step']} us")
         extra["decode_gemv_llama7b_batches"] = batches
     if B == 1 and not args.no_extra:
         extra["decode_gemv_b1_by_weight_size"] = gemv_size_sweep(torch, ctx, stream, dev)
