@@ -26,6 +26,9 @@ struct frx_ctx {
   int device = 0;
   hipStream_t stream = nullptr;
   char err[512] = {0};
+  // Workspaces replaced by larger ones stay allocated until frx_destroy: a
+  // graph captured at a smaller size still holds their addresses.
+  std::vector<void *> retired;
   // growable device scratch for the host-slice API and the MoE workspace
   void *scratch = nullptr;
   size_t scratch_bytes = 0;
@@ -109,6 +112,7 @@ void frx_destroy(frx_ctx *ctx) {
   if (ctx->ffn_ws) hipFree(ctx->ffn_ws);
   if (ctx->glu_ws) hipFree(ctx->glu_ws);
   if (ctx->ffn_bar) hipFree(ctx->ffn_bar);
+  for (void *p : ctx->retired) hipFree(p);
   delete ctx;
 }
 
@@ -131,7 +135,10 @@ frx_status frx_synchronize(frx_ctx *ctx) {
     e = hipMemcpy(&err, ctx->ffn_bar + frx::ffn1_error_word(), sizeof(err), hipMemcpyDeviceToHost);
     if (e != hipSuccess) return hip_fail(ctx, e, "FFN barrier state read");
     if (err) {
-      e = hipMemset(ctx->ffn_bar, 0, frx::ffn1_barrier_bytes());
+      // reset on the context's stream and wait for it, so that the next
+      // one-launch FFN on this stream sees the cleared words
+      e = hipMemsetAsync(ctx->ffn_bar, 0, frx::ffn1_barrier_bytes(), ctx->stream);
+      if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
       if (e != hipSuccess) return hip_fail(ctx, e, "FFN barrier reset");
       return fail(ctx, FRX_ERR_GPU,
                   "one-launch FFN: grid barrier timed out (workgroups not co-resident); "
@@ -199,6 +206,21 @@ frx_status frx_sparse24_ternary_linear(frx_ctx *ctx, const uint32_t *meta,
   return FRX_OK;
 }
 
+// Grows a context-owned device buffer. The buffer it replaces is retired,
+// not freed: a graph captured at a smaller size still writes to it, so it
+// stays allocated until frx_destroy. The first call at a larger size
+// allocates and must not be under graph capture.
+static frx_status ensure_buffer(frx_ctx *ctx, void **buf, size_t *have, size_t need, const char *what) {
+  if (need <= *have) return FRX_OK;
+  void *p = nullptr;
+  hipError_t e = hipMalloc(&p, need);
+  if (e != hipSuccess) return hip_fail(ctx, e, what);
+  if (*buf) ctx->retired.push_back(*buf);
+  *buf = p;
+  *have = need;
+  return FRX_OK;
+}
+
 frx_status frx_moe_ternary_ffn(
     frx_ctx *ctx, const void *x, frx_dtype xt, const void *router,
     frx_dtype rt, const uint32_t *const *w_gate, const float *const *s_gate,
@@ -223,17 +245,8 @@ frx_status frx_moe_ternary_ffn(
       return fail(ctx, FRX_ERR_SHAPE, "null weight pointer for expert %u", e);
   if ((size_t)T * top_k * I > (size_t)0x7FFFFFFF) return fail(ctx, FRX_ERR_SHAPE, "T*top_k*I too large");
   const size_t need = frx::moe_workspace_bytes((int)T, (int)H, (int)I, (int)E, (int)top_k);
-  if (need > ctx->moe_ws_bytes) {
-    if (ctx->moe_ws) {
-      hipStreamSynchronize(ctx->stream);
-      hipFree(ctx->moe_ws);
-      ctx->moe_ws = nullptr;
-      ctx->moe_ws_bytes = 0;
-    }
-    hipError_t e = hipMalloc(&ctx->moe_ws, need);
-    if (e != hipSuccess) return hip_fail(ctx, e, "MoE workspace allocation");
-    ctx->moe_ws_bytes = need;
-  }
+  if ((st = ensure_buffer(ctx, &ctx->moe_ws, &ctx->moe_ws_bytes, need, "MoE workspace allocation")) != FRX_OK)
+    return st;
   frx::MoeWorkspace ws;
   frx::moe_workspace_carve(ctx->moe_ws, (int)T, (int)H, (int)I, (int)E, (int)top_k, &ws);
   hipError_t e = frx::launch_moe(x, xt == FRX_BF16, router, rt == FRX_BF16, w_gate, s_gate, w_up, s_up, w_down,
@@ -243,21 +256,6 @@ frx_status frx_moe_ternary_ffn(
   return FRX_OK;
 }
 
-// Grows a context-owned device buffer (synchronises the stream before
-// freeing the old one; the first call at a given size allocates).
-static frx_status ensure_buffer(frx_ctx *ctx, void **buf, size_t *have, size_t need, const char *what) {
-  if (need <= *have) return FRX_OK;
-  if (*buf) {
-    hipStreamSynchronize(ctx->stream);
-    hipFree(*buf);
-    *buf = nullptr;
-    *have = 0;
-  }
-  hipError_t e = hipMalloc(buf, need);
-  if (e != hipSuccess) return hip_fail(ctx, e, what);
-  *have = need;
-  return FRX_OK;
-}
 
 static frx_status check_ffn(frx_ctx *ctx, const void *x, frx_dtype xt, const void *w_gate,
                             const float *s_gate, const void *w_up, const float *s_up, uint32_t M,
@@ -276,19 +274,23 @@ static frx_status check_ffn(frx_ctx *ctx, const void *x, frx_dtype xt, const voi
 }
 
 // h = act(g) * u into an fp32 [M][I] buffer. M <= 16: one launch; larger M:
-// two GEMMs (g into h, u into the context's workspace) and a combine.
+// two GEMMs (g into h, u into u_ws, or into the context's workspace when
+// u_ws is null) and a combine.
 static frx_status glu_into(frx_ctx *ctx, const void *x, frx_dtype xt, const uint32_t *w_gate,
                            const float *s_gate, const uint32_t *w_up, const float *s_up, uint32_t M,
-                           uint32_t H, uint32_t I, bool gelu, float *h) {
+                           uint32_t H, uint32_t I, bool gelu, float *h, float *u_ws) {
   hipError_t e;
   if (M <= 16) {
     e = frx::launch_gemv_glu(w_gate, s_gate, w_up, s_up, x, xt == FRX_BF16, h, (int)M, (int)H, (int)I, gelu,
                              ctx->stream);
   } else {
-    const size_t ub = a256((size_t)M * I * 4);
-    frx_status st = ensure_buffer(ctx, &ctx->glu_ws, &ctx->glu_ws_bytes, ub, "GLU workspace allocation");
-    if (st != FRX_OK) return st;
-    float *u = reinterpret_cast<float *>(ctx->glu_ws);
+    float *u = u_ws;
+    if (!u) {
+      const size_t ub = a256((size_t)M * I * 4);
+      frx_status st = ensure_buffer(ctx, &ctx->glu_ws, &ctx->glu_ws_bytes, ub, "GLU workspace allocation");
+      if (st != FRX_OK) return st;
+      u = reinterpret_cast<float *>(ctx->glu_ws);
+    }
     e = frx::launch_gemm(w_gate, s_gate, x, xt == FRX_BF16, h, 0, (int)M, (int)H, (int)I, 0, ctx->stream);
     if (e == hipSuccess)
       e = frx::launch_gemm(w_up, s_up, x, xt == FRX_BF16, u, 0, (int)M, (int)H, (int)I, 0, ctx->stream);
@@ -306,33 +308,37 @@ frx_status frx_ternary_glu(frx_ctx *ctx, const void *x, frx_dtype xt, const uint
   if ((st = check_ffn(ctx, x, xt, w_gate, s_gate, w_up, s_up, M, H, I, act)) != FRX_OK) return st;
   if (!h) return fail(ctx, FRX_ERR_SHAPE, "null output pointer");
   if (!aligned16(h)) return fail(ctx, FRX_ERR_UNSUPPORTED, "h must be a 16-byte aligned device pointer");
-  return glu_into(ctx, x, xt, w_gate, s_gate, w_up, s_up, M, H, I, act == FRX_ACT_GELU_TANH, h);
+  return glu_into(ctx, x, xt, w_gate, s_gate, w_up, s_up, M, H, I, act == FRX_ACT_GELU_TANH, h, nullptr);
 }
 
 // Token counts from which the unfused FFN writes h as bf16 hi/lo planes for
 // the unstaged down GEMV (below: fp32 h, staged down).
 static constexpr int FFN_PLANES_MIN_M = 4;
 
-frx_status frx_ternary_ffn(frx_ctx *ctx, const void *x, frx_dtype xt, const uint32_t *w_gate,
-                           const float *s_gate, const uint32_t *w_up, const float *s_up,
-                           const uint32_t *w_down, const float *s_down, uint32_t M, uint32_t H,
-                           uint32_t I, frx_activation act, void *y, frx_dtype yt) {
-  frx_status st = enter(ctx);
-  if (st != FRX_OK) return st;
-  if ((st = check_ffn(ctx, x, xt, w_gate, s_gate, w_up, s_up, M, H, I, act)) != FRX_OK) return st;
+static frx_status check_ffn_down(frx_ctx *ctx, const uint32_t *w_down, const float *s_down, void *y,
+                                 frx_dtype yt) {
   if (!w_down || !s_down || !y) return fail(ctx, FRX_ERR_SHAPE, "null pointer argument");
   if (yt != FRX_F32 && yt != FRX_BF16) return fail(ctx, FRX_ERR_UNSUPPORTED, "dtype must be FRX_F32 or FRX_BF16");
   if (!aligned16(y) || !aligned16(s_down))
     return fail(ctx, FRX_ERR_UNSUPPORTED, "y and scales must be 16-byte aligned device pointers");
-  if ((st = ensure_buffer(ctx, &ctx->ffn_ws, &ctx->ffn_ws_bytes, a256((size_t)M * I * 4),
-                          "FFN workspace allocation")) != FRX_OK)
-    return st;
+  return FRX_OK;
+}
+
+// The dense FFN with its intermediate in `ws` (at least M*I*4 bytes, 256-byte
+// aligned). u_ws: the GEMM path's up projection (M > 16; null = the
+// context's workspace). allow_one: the one-launch kernel may run (it needs
+// the context's barrier words).
+static frx_status ffn_run(frx_ctx *ctx, const void *x, frx_dtype xt, const uint32_t *w_gate, const float *s_gate,
+                          const uint32_t *w_up, const float *s_up, const uint32_t *w_down, const float *s_down,
+                          uint32_t M, uint32_t H, uint32_t I, frx_activation act, void *y, frx_dtype yt, void *ws,
+                          float *u_ws, bool allow_one) {
   hipError_t e;
-  if (ctx->ffn_mode != FRX_FFN_ONE_LAUNCH && xt == FRX_BF16 && aligned16(w_gate) && aligned16(w_up) &&
-      aligned16(w_down) && frx::gemv_rows_ffn_ok((int)M, (int)H, (int)I)) {
+  const bool two_only = ctx->ffn_mode == FRX_FFN_TWO_LAUNCH || !allow_one;
+  if ((!allow_one || ctx->ffn_mode != FRX_FFN_ONE_LAUNCH) && xt == FRX_BF16 && aligned16(w_gate) &&
+      aligned16(w_up) && aligned16(w_down) && frx::gemv_rows_ffn_ok((int)M, (int)H, (int)I)) {
     // one token: gate/up/act into bf16 hi/lo planes of h (the first 4*I
     // bytes of the workspace), then the down rows over both planes
-    uint16_t *hp = reinterpret_cast<uint16_t *>(ctx->ffn_ws);
+    uint16_t *hp = reinterpret_cast<uint16_t *>(ws);
     e = frx::launch_gemv_rows_glu_planes(w_gate, s_gate, w_up, s_up, x, hp, (int)H, (int)I,
                                          act == FRX_ACT_GELU_TANH, ctx->stream);
     if (e != hipSuccess) return hip_fail(ctx, e, "ffn gate/up launch");
@@ -340,11 +346,11 @@ frx_status frx_ternary_ffn(frx_ctx *ctx, const void *x, frx_dtype xt, const uint
     if (e != hipSuccess) return hip_fail(ctx, e, "ffn down launch");
     return FRX_OK;
   }
-  if (ctx->ffn_mode != FRX_FFN_ONE_LAUNCH && xt == FRX_BF16 && aligned16(w_gate) && aligned16(w_up) &&
-      aligned16(w_down) && frx::gemv_rows4_ffn_ok((int)M, (int)H, (int)I)) {
+  if ((!allow_one || ctx->ffn_mode != FRX_FFN_ONE_LAUNCH) && xt == FRX_BF16 && aligned16(w_gate) &&
+      aligned16(w_up) && aligned16(w_down) && frx::gemv_rows4_ffn_ok((int)M, (int)H, (int)I)) {
     // two tokens: the same in the 4-segment kernels, the down launch taking
     // h's hi and lo planes of both tokens as its four token columns
-    uint16_t *hp = reinterpret_cast<uint16_t *>(ctx->ffn_ws);
+    uint16_t *hp = reinterpret_cast<uint16_t *>(ws);
     e = frx::launch_gemv_rows4_glu_planes(w_gate, s_gate, w_up, s_up, x, hp, (int)M, (int)H, (int)I,
                                           act == FRX_ACT_GELU_TANH, ctx->stream);
     if (e != hipSuccess) return hip_fail(ctx, e, "ffn gate/up launch");
@@ -354,10 +360,9 @@ frx_status frx_ternary_ffn(frx_ctx *ctx, const void *x, frx_dtype xt, const uint
   }
   int grid = 0;
   size_t lds = 0;
-  const bool one = ctx->ffn_mode != FRX_FFN_TWO_LAUNCH && aligned16(w_gate) && aligned16(w_up) &&
-                   aligned16(w_down) &&
+  const bool one = !two_only && aligned16(w_gate) && aligned16(w_up) && aligned16(w_down) &&
                    frx::ffn1_supported((int)M, (int)H, (int)I, xt == FRX_BF16, ctx->cus, &grid, &lds);
-  if (ctx->ffn_mode == FRX_FFN_ONE_LAUNCH && !one)
+  if (allow_one && ctx->ffn_mode == FRX_FFN_ONE_LAUNCH && !one)
     return fail(ctx, FRX_ERR_UNSUPPORTED,
                 "one-launch FFN: unsupported shape M=%u H=%u I=%u (M <= 3, H <= 4096, I <= 11520, "
                 "multiples of 64, 16-byte aligned weights)", M, H, I);
@@ -376,17 +381,16 @@ frx_status frx_ternary_ffn(frx_ctx *ctx, const void *x, frx_dtype xt, const uint
       }
       ctx->ffn_bar = reinterpret_cast<unsigned *>(p);
     }
-    static_assert(sizeof(float) == 4, "h planes");
     e = frx::launch_ffn1(x, xt == FRX_BF16, w_gate, s_gate, w_up, s_up, w_down, s_down,
-                         reinterpret_cast<uint32_t *>(ctx->ffn_ws), y, yt == FRX_BF16, ctx->ffn_bar, (int)M,
-                         (int)H, (int)I, act == FRX_ACT_GELU_TANH, grid, lds, ctx->stream);
+                         reinterpret_cast<uint32_t *>(ws), y, yt == FRX_BF16, ctx->ffn_bar, (int)M, (int)H, (int)I,
+                         act == FRX_ACT_GELU_TANH, grid, lds, ctx->stream);
     if (e != hipSuccess) return hip_fail(ctx, e, "one-launch FFN");
     return FRX_OK;
   }
   if (xt == FRX_BF16 && (int)M >= FFN_PLANES_MIN_M && M <= 16) {
     // h as bf16 hi/lo planes (the same M*I*4 bytes), consumed by the down
     // GEMV without staging: at these M the fp32 rows of h do not fit LDS.
-    uint16_t *hp = reinterpret_cast<uint16_t *>(ctx->ffn_ws);
+    uint16_t *hp = reinterpret_cast<uint16_t *>(ws);
     e = frx::launch_gemv_glu_planes(w_gate, s_gate, w_up, s_up, x, hp, (int)M, (int)H, (int)I,
                                     act == FRX_ACT_GELU_TANH, ctx->stream);
     if (e != hipSuccess) return hip_fail(ctx, e, "ffn gate/up launch");
@@ -394,9 +398,9 @@ frx_status frx_ternary_ffn(frx_ctx *ctx, const void *x, frx_dtype xt, const uint
     if (e != hipSuccess) return hip_fail(ctx, e, "ffn down launch");
     return FRX_OK;
   }
-  float *h = reinterpret_cast<float *>(ctx->ffn_ws);
-  if ((st = glu_into(ctx, x, xt, w_gate, s_gate, w_up, s_up, M, H, I, act == FRX_ACT_GELU_TANH, h)) != FRX_OK)
-    return st;
+  float *h = reinterpret_cast<float *>(ws);
+  frx_status st = glu_into(ctx, x, xt, w_gate, s_gate, w_up, s_up, M, H, I, act == FRX_ACT_GELU_TANH, h, u_ws);
+  if (st != FRX_OK) return st;
   if (M <= 16)
     e = frx::launch_gemv(w_down, s_down, h, 0, y, yt == FRX_BF16, (int)M, (int)I, (int)H, ctx->stream);
   else
@@ -405,12 +409,28 @@ frx_status frx_ternary_ffn(frx_ctx *ctx, const void *x, frx_dtype xt, const uint
   return FRX_OK;
 }
 
+frx_status frx_ternary_ffn(frx_ctx *ctx, const void *x, frx_dtype xt, const uint32_t *w_gate,
+                           const float *s_gate, const uint32_t *w_up, const float *s_up,
+                           const uint32_t *w_down, const float *s_down, uint32_t M, uint32_t H,
+                           uint32_t I, frx_activation act, void *y, frx_dtype yt) {
+  frx_status st = enter(ctx);
+  if (st != FRX_OK) return st;
+  if ((st = check_ffn(ctx, x, xt, w_gate, s_gate, w_up, s_up, M, H, I, act)) != FRX_OK) return st;
+  if ((st = check_ffn_down(ctx, w_down, s_down, y, yt)) != FRX_OK) return st;
+  if ((st = ensure_buffer(ctx, &ctx->ffn_ws, &ctx->ffn_ws_bytes, a256((size_t)M * I * 4),
+                          "FFN workspace allocation")) != FRX_OK)
+    return st;
+  return ffn_run(ctx, x, xt, w_gate, s_gate, w_up, s_up, w_down, s_down, M, H, I, act, y, yt, ctx->ffn_ws, nullptr,
+                 true);
+}
+
 // ---- host-slice accelerator API (GpuMatmulAccelerator) --------------------
 
+// The host-slice calls synchronise before they return, so nothing in flight
+// uses the old scratch when it grows: it is freed at once.
 static frx_status ensure_scratch(frx_ctx *ctx, size_t bytes) {
   if (bytes <= ctx->scratch_bytes) return FRX_OK;
   if (ctx->scratch) {
-    hipStreamSynchronize(ctx->stream);
     hipFree(ctx->scratch);
     ctx->scratch = nullptr;
     ctx->scratch_bytes = 0;

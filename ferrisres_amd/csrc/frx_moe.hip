@@ -147,10 +147,16 @@ __device__ __forceinline__ void router_softmax_topk(float sum, float *logit, int
   pbuf[tid] = pe;
   __syncthreads();
   if (live) {
+    // Unordered pairs (NaN) count as ties, broken by index, as the
+    // reference's sort_by(partial_cmp().unwrap_or(Equal)) keeps them. Within
+    // a token the probabilities are either all NaN (a NaN or +inf logit
+    // makes the exp sum NaN) or all ordered, so the ranks are a permutation
+    // of 0..E-1 in both cases and every slot below top_k is written.
     int rank = 0;
     for (int j = 0; j < E; j++) {
       const float pj = pbuf[tl * EP + j];
-      rank += (pj > pe) || (pj == pe && j < e);
+      const bool tie = !(pj < pe) && !(pj > pe);
+      rank += (pj > pe) || (tie && j < e);
     }
     if (rank < top_k) order[tl * EP + rank] = e;
   }
@@ -162,7 +168,8 @@ __device__ __forceinline__ void router_softmax_topk(float sum, float *logit, int
   }
   __syncthreads();
   if (e < top_k && t < T) {
-    const int ei = order[tl * EP + e];
+    const int oi = order[tl * EP + e];
+    const int ei = (unsigned)oi < (unsigned)E ? oi : 0;  // the ranks above fill every slot; kept in range regardless
     const float wi = __fdiv_rn(pbuf[tl * EP + ei], tsum[tl]);
     idx_out[t * top_k + e] = (uint32_t)ei;
     w_out[t * top_k + e] = wi;

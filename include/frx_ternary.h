@@ -111,7 +111,9 @@ frx_status frx_sparse24_ternary_linear(frx_ctx *ctx, const uint32_t *meta,
  *   y [T][H] yt; topk_idx [T][top_k] u32 and topk_w [T][top_k] f32 (device,
  *   may be NULL).
  * Requires H % 16 == 0, I % 16 == 0, 1 <= top_k <= E <= 64.
- * Workspace is allocated on the context on first use (and grown). */
+ * Workspace is allocated on the context on first use and grown on the first
+ * call at a larger size (not under graph capture); a replaced workspace is
+ * kept until frx_destroy, so graphs captured at smaller sizes stay valid. */
 frx_status frx_moe_ternary_ffn(
     frx_ctx *ctx, const void *x, frx_dtype xt, const void *router,
     frx_dtype rt, const uint32_t *const *w_gate, const float *const *s_gate,
@@ -143,25 +145,29 @@ frx_status frx_ternary_glu(frx_ctx *ctx, const void *x, frx_dtype xt,
  *   act = SiLU g/(1+e^-g) (FRX_ACT_SILU) or GeLU-tanh (FRX_ACT_GELU_TANH).
  *   x [M][H] xt; w_gate, w_up [I][H/16] u32, s_gate, s_up [I] f32;
  *   w_down [H][I/16] u32, s_down [H] f32; y [M][H] yt (device pointers).
- * The intermediate (act(g) * u, [M][I]) stays fp32 in a context workspace,
- * as in the reference: frx_ternary_glu into the workspace, then the down
- * projection with fp32 input (M <= 16: two launches). Requires H % 16 == 0,
- * I % 16 == 0. The workspace is allocated on the context on first use (and
- * grown), so a first call at a new size must not be under graph capture.
- * One or two bf16 tokens (M = 1: H and I multiples of 64 up to 16384; M = 2:
- * up to 14336; 16-byte aligned weights) run as two launches that each read
- * whole weight rows per wave, with the intermediate as bf16 hi and lo
- * planes (|h - hi - lo| <= 2^-17 |h|) in the same workspace (FRX_FFN_AUTO
- * and FRX_FFN_TWO_LAUNCH). With bf16 x at 4 <= M <= 16 the intermediate is
- * the same pair of bf16 planes, read by the down GEMV without staging.
- * Other decode sizes (M <= 3, H <= 4096, I <= 11520, H and I multiples of
- * 64, 16-byte aligned weights; LLaMA-7B's 4096/11008 included) run the whole
- * FFN as ONE launch with a grid barrier between the halves (FRX_FFN_AUTO;
- * FRX_FFN_ONE_LAUNCH also at M = 1 and 2). That
- * launch needs all its workgroups (one per CU) resident at once; if another
- * kernel holds CUs so that they are not, its barrier times out, the outputs
- * are invalid and the next frx_synchronize returns FRX_ERR_GPU. Callers that
- * share the GPU with concurrent kernels select FRX_FFN_TWO_LAUNCH. */
+ * Requires H % 16 == 0, I % 16 == 0. The intermediate h = act(g) * u
+ * ([M][I]) lives in a context workspace of M*I*4 bytes. Paths, by M and the
+ * dtype of x (FRX_FFN_AUTO):
+ *  - bf16 x, M = 1 (H, I multiples of 64 up to 16384) or M = 2 (up to
+ *    14336), 16-byte aligned weights: two launches that read whole weight
+ *    rows per wave; h as bf16 hi + lo planes, |h - hi - lo| <= 2^-17 |h|.
+ *  - M = 3 (H <= 4096, I <= 11520, multiples of 64, 16-byte aligned
+ *    weights; LLaMA-7B's 4096/11008 included): one launch with a grid
+ *    barrier between the halves; h as bf16 hi + lo planes (2^-17).
+ *  - bf16 x, 4 <= M <= 16: gate/up/act launch writing h as bf16 hi + lo
+ *    planes (2^-17), then the down GEMV over both planes.
+ *  - f32 x at M <= 16, and every other shape at M <= 16: h in fp32, then the
+ *    down GEMV with fp32 input, as the reference keeps it.
+ *  - M > 16: gate and up GEMMs (the up projection in a second context
+ *    workspace), an element-wise fp32 combine, then the down GEMM.
+ * Workspaces grow on the first call at a larger size, and that first call
+ * must not be under graph capture. A workspace replaced by a larger one is
+ * kept until frx_destroy, so graphs captured at smaller sizes stay valid.
+ * The one-launch kernel needs all its workgroups (one per CU) resident at
+ * once; if another kernel holds CUs so that they are not, its barrier times
+ * out, the outputs are invalid and the next frx_synchronize returns
+ * FRX_ERR_GPU. Callers that share the GPU with concurrent kernels select
+ * FRX_FFN_TWO_LAUNCH (M = 3 then takes the fp32-h path). */
 frx_status frx_ternary_ffn(frx_ctx *ctx, const void *x, frx_dtype xt,
                            const uint32_t *w_gate, const float *s_gate,
                            const uint32_t *w_up, const float *s_up,

@@ -45,6 +45,9 @@ def lib():
             "frxo_ternary_matmul_packed": (None, [_vp, _f, _vp, _sz, _sz, _sz, _vp]),
             "frxo_ternary_matmul_packed_rows": (None, [_vp, _f, _vp, _sz, _sz, _sz, _sz, _vp]),
             "frxo_ternary_matmul_blocked": (None, [_vp, _vp, _sz, _vp, _sz, _sz, _sz, _vp]),
+            "frxo_ternary_sparse_indices": (None, [_vp, _sz, _sz, _vp, _vp, _vp, _vp]),
+            "frxo_ternary_matmul_sparse_decode": (None, [_vp, _vp, _vp, _vp, _f, _vp, _sz, _vp]),
+            "frxo_ternary_stats": (_f, [_vp, _sz, _vp, _vp]),
             "frxo_bench_ternary_matmul": (None, [_vp, _vp, _f, _sz, _sz, _sz, _vp]),
             "frxo_quantize_ternary": (_f, [_vp, _sz, _vp]),
             "frxo_quantize_ste": (_f, [_vp, _sz, _vp]),
@@ -55,7 +58,6 @@ def lib():
             "frxo_sparse24_cpu_to_ternary": (None, [_vp, _vp, _sz, _sz, _vp]),
             "frxo_sparse24_cpu_matmul": (None, [_vp, _vp, _f, _sz, _sz, _vp, _sz, _vp]),
             "frxo_sparse24_cpu_matmul_decode": (None, [_vp, _vp, _f, _sz, _sz, _vp, _vp]),
-            "frxo_prune_fp32_to_sparse24": (_f, [_vp, _sz, _sz, _vp, _vp]),
             "frxo_moe_route": (None, [_vp, _vp, _sz, _sz, _sz, _sz, _vp, _vp, _vp]),
             "frxo_moe_forward": (None, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
                                         _sz, _sz, _sz, _sz, _sz, ctypes.c_int, _vp, _vp, _vp]),
@@ -243,13 +245,36 @@ def sparse24_cpu_matmul_decode(pats, signs, scale, rows, cols, inp):
     return out
 
 
-def prune_fp32_to_sparse24(weights, rows, cols):
-    w = _c(weights, np.float32)
-    ng = rows * cols // 4
-    pats = np.zeros((ng + 1) // 2, np.uint8)
-    signs = np.zeros((ng + 3) // 4, np.uint8)
-    sc = lib().frxo_prune_fp32_to_sparse24(_p(w), rows, cols, _p(pats), _p(signs))
-    return pats, signs, np.float32(sc)
+def ternary_sparse_indices(ternary, out_rows, in_cols):
+    """ternary.rs:681-707 as CSR arrays (pos_off, pos_idx, neg_off, neg_idx)."""
+    t = _c(ternary, np.int8)
+    po = np.zeros(out_rows + 1, np.uint32)
+    no = np.zeros(out_rows + 1, np.uint32)
+    lib().frxo_ternary_sparse_indices(_p(t), out_rows, in_cols, _p(po), None, _p(no), None)
+    pi = np.zeros(max(int(po[-1]), 1), np.uint32)
+    ni = np.zeros(max(int(no[-1]), 1), np.uint32)
+    lib().frxo_ternary_sparse_indices(_p(t), out_rows, in_cols, _p(po), _p(pi), _p(no), _p(ni))
+    return po, pi[:int(po[-1])], no, ni[:int(no[-1])]
+
+
+def ternary_matmul_sparse_decode(pos_off, pos_idx, neg_off, neg_idx, scale, x, out_rows):
+    """ternary.rs:647-673."""
+    po, no = _c(pos_off, np.uint32), _c(neg_off, np.uint32)
+    pi = _c(pos_idx if len(pos_idx) else np.zeros(1), np.uint32)
+    ni = _c(neg_idx if len(neg_idx) else np.zeros(1), np.uint32)
+    xx = _c(x, np.float32)
+    out = np.zeros(out_rows, np.float32)
+    lib().frxo_ternary_matmul_sparse_decode(_p(po), _p(pi), _p(no), _p(ni), scale, _p(xx), out_rows, _p(out))
+    return out
+
+
+def ternary_stats(ternary):
+    """ternary.rs:725-746: (counts [neg1, zero, pos1], ratios, compression)."""
+    t = _c(ternary, np.int8).ravel()
+    counts = np.zeros(3, np.uint64)
+    ratios = np.zeros(3, np.float32)
+    comp = lib().frxo_ternary_stats(_p(t), t.size, _p(counts), _p(ratios))
+    return counts, ratios, float(comp)
 
 
 def moe_route(x, router, top_k):

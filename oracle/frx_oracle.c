@@ -285,6 +285,76 @@ void frxo_ternary_matmul_blocked(const int8_t *ternary, const float *scales,
 }
 
 /*
+ * ternary.rs:681-707 ternary_sparse_indices: per row, the column indices of
+ * +1 entries (pos) and of -1 entries (neg), in column order; other values
+ * are in neither list. Returned as CSR arrays: pos_off[r]..pos_off[r+1] index
+ * pos_idx (same for neg). With pos_idx/neg_idx NULL only the offsets (the
+ * list sizes) are filled. Pinned by KAT ternary.rs:1238-1254.
+ */
+void frxo_ternary_sparse_indices(const int8_t *ternary, size_t out_rows,
+                                 size_t in_cols, uint32_t *pos_off,
+                                 uint32_t *pos_idx, uint32_t *neg_off,
+                                 uint32_t *neg_idx) {
+  uint32_t np = 0, nn = 0;
+  for (size_t r = 0; r < out_rows; r++) {
+    pos_off[r] = np;
+    neg_off[r] = nn;
+    const int8_t *row = ternary + r * in_cols;
+    for (size_t j = 0; j < in_cols; j++) {
+      if (row[j] == 1) {
+        if (pos_idx) pos_idx[np] = (uint32_t)j;
+        np++;
+      } else if (row[j] == -1) {
+        if (neg_idx) neg_idx[nn] = (uint32_t)j;
+        nn++;
+      }
+    }
+  }
+  pos_off[out_rows] = np;
+  neg_off[out_rows] = nn;
+}
+
+/*
+ * ternary.rs:647-673 ternary_matmul_sparse_decode: per row, sum += x[j] over
+ * the pos list in order, then sum -= x[j] over the neg list in order; out =
+ * scale * sum. Pinned by KAT ternary.rs:1208-1236 (equals the decode matmul)
+ * and exactness on dyadic inputs.
+ */
+void frxo_ternary_matmul_sparse_decode(const uint32_t *pos_off,
+                                       const uint32_t *pos_idx,
+                                       const uint32_t *neg_off,
+                                       const uint32_t *neg_idx, float scale,
+                                       const float *input, size_t out_rows,
+                                       float *out) {
+  for (size_t r = 0; r < out_rows; r++) {
+    float sum = 0.0f;
+    for (uint32_t i = pos_off[r]; i < pos_off[r + 1]; i++) sum += input[pos_idx[i]];
+    for (uint32_t i = neg_off[r]; i < neg_off[r + 1]; i++) sum -= input[neg_idx[i]];
+    out[r] = scale * sum;
+  }
+}
+
+/*
+ * ternary.rs:725-746 ternary_stats: counts of -1 and +1, zeros = n - both,
+ * ratios count as f32 / n as f32, compression 32 / 2. out: [num_neg1,
+ * num_zero, num_pos1] and ratios[3] in the same order; returns the
+ * compression ratio. Pinned by KAT ternary.rs:894-904.
+ */
+float frxo_ternary_stats(const int8_t *ternary, size_t n, uint64_t counts[3],
+                         float ratios[3]) {
+  uint64_t neg = 0, pos = 0;
+  for (size_t i = 0; i < n; i++) {
+    if (ternary[i] == -1) neg++;
+    if (ternary[i] == 1) pos++;
+  }
+  counts[0] = neg;
+  counts[1] = n - neg - pos;
+  counts[2] = pos;
+  for (int i = 0; i < 3; i++) ratios[i] = (float)counts[i] / (float)n;
+  return 32.0f / 2.0f;
+}
+
+/*
  * benches/ternary_bench.rs:87-106 (the criterion bench's inline i8 loop):
  * weights indexed [col*k + ki] (i.e. W is [n x k] row-major), branchy
  * add/sub, c = sum * scale. Pinned by equality with frxo_ternary_matmul_u32
@@ -560,52 +630,6 @@ void frxo_sparse24_cpu_matmul_decode(const uint8_t *patterns,
                                      size_t rows, size_t cols,
                                      const float *input, float *out) {
   frxo_sparse24_cpu_matmul(patterns, signs, scale, rows, cols, input, 1, out);
-}
-
-/*
- * sparse_ternary.rs:598-663 prune_fp32_to_sparse_ternary: stable sort of
- * the 4 values by |v| descending (partial_cmp, NaN compares Equal), keep
- * the first two, sign = v >= 0; scale = (sum|W| / n) / ABSMEAN_NORM over the
- * whole tensor (1.0 if zero). Returns the scale. Pinned by KAT
- * sparse_ternary.rs:523-544.
- */
-float frxo_prune_fp32_to_sparse24(const float *weights, size_t rows,
-                                  size_t cols, uint8_t *patterns,
-                                  uint8_t *signs) {
-  size_t ng = rows * cols / 4;
-  memset(patterns, 0, (ng + 1) / 2);
-  memset(signs, 0, (ng + 3) / 4);
-  for (size_t g = 0; g < ng; g++) {
-    const float *v = weights + g * 4;
-    int idx[4] = {0, 1, 2, 3};
-    for (int i = 1; i < 4; i++) {
-      int cur = idx[i], j = i - 1;
-      float ca = fabsf(v[cur]);
-      /* move while the earlier element is strictly smaller (stable); NaN
-       * compares as Equal in the reference, i.e. never moves */
-      while (j >= 0 && fabsf(v[idx[j]]) < ca) {
-        idx[j + 1] = idx[j];
-        j--;
-      }
-      idx[j + 1] = cur;
-    }
-    int pos0 = idx[0], pos1 = idx[1];
-    float val0 = v[pos0], val1 = v[pos1];
-    int p0 = pos0 < pos1 ? pos0 : pos1, p1 = pos0 < pos1 ? pos1 : pos0;
-    int pat = find_pattern(p0, p1);
-    if (g % 2 == 0)
-      patterns[g / 2] |= (uint8_t)(pat & 7);
-    else
-      patterns[g / 2] |= (uint8_t)((pat & 7) << 4);
-    /* the reference keys the sign bits on the sort order (val0 -> bit 0),
-     * not on the position order (sparse_ternary.rs:640-642) */
-    uint8_t s0 = val0 >= 0.0f ? 1 : 0, s1 = val1 >= 0.0f ? 1 : 0;
-    signs[g / 4] |= (uint8_t)((s0 | (s1 << 1)) << ((g % 4) * 2));
-  }
-  float sum_abs = 0.0f;
-  for (size_t i = 0; i < rows * cols; i++) sum_abs += fabsf(weights[i]);
-  return sum_abs > 0.0f ? (sum_abs / (float)(rows * cols)) / ABSMEAN_NORM
-                        : 1.0f;
 }
 
 /* ---- MoE ------------------------------------------------------------------ */

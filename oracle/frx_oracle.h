@@ -51,6 +51,18 @@ void frxo_ternary_matmul_blocked(const int8_t *ternary, const float *scales,
                                  size_t block_size, const float *input,
                                  size_t out_rows, size_t in_cols, size_t seq,
                                  float *out);
+void frxo_ternary_sparse_indices(const int8_t *ternary, size_t out_rows,
+                                 size_t in_cols, uint32_t *pos_off,
+                                 uint32_t *pos_idx, uint32_t *neg_off,
+                                 uint32_t *neg_idx);
+void frxo_ternary_matmul_sparse_decode(const uint32_t *pos_off,
+                                       const uint32_t *pos_idx,
+                                       const uint32_t *neg_off,
+                                       const uint32_t *neg_idx, float scale,
+                                       const float *input, size_t out_rows,
+                                       float *out);
+float frxo_ternary_stats(const int8_t *ternary, size_t n, uint64_t counts[3],
+                         float ratios[3]);
 void frxo_bench_ternary_matmul(const float *a, const int8_t *weights,
                                float scale, size_t m, size_t n, size_t k,
                                float *out);
@@ -78,9 +90,6 @@ void frxo_sparse24_cpu_matmul_decode(const uint8_t *patterns,
                                      const uint8_t *signs, float scale,
                                      size_t rows, size_t cols,
                                      const float *input, float *out);
-float frxo_prune_fp32_to_sparse24(const float *weights, size_t rows,
-                                  size_t cols, uint8_t *patterns,
-                                  uint8_t *signs);
 void frxo_sparse24_gpu_decode(const uint32_t *packed, size_t rows, size_t cols,
                               int8_t *out);
 

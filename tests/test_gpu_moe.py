@@ -125,3 +125,26 @@ def test_moe_shape_errors(ctx):
     with pytest.raises(frx.FrxError) as e:
         run_gpu(ctx, xf, xb, rf, rb, ex, 2, 3, frx.ACT_SILU)  # top_k > E
     assert e.value.kind == "Shape"
+
+
+def test_moe_nonfinite_tokens_route_like_the_reference(ctx):
+    """A token whose activations hold NaN or +-inf makes every routing
+    probability of that token NaN (or leaves them finite for -inf logits);
+    the reference's stable sort then keeps expert order 0..k-1
+    (ternary_moe.rs:175, partial_cmp().unwrap_or(Equal)). Indices must be in
+    range and equal to the oracle's for every token, finite or not."""
+    T, H, I, E, k = 24, 128, 128, 8, 2
+    xf, xb, rf, rb, ex = make_moe("moe/nonfinite", T, H, I, E)
+    xf = xf.copy()
+    xf[3, 5] = np.nan
+    xf[7, :] = np.inf
+    xf[11, 0] = -np.inf
+    xf[12, 17] = np.inf
+    y, idx, w = run_gpu(ctx, xf, None, rf, None, ex, E, k, frx.ACT_SILU, xt="f32")
+    ridx, rw, _ = oracle.moe_route(xf, rf, k)
+    assert (idx < E).all()
+    np.testing.assert_array_equal(idx, ridx)
+    finite = [t for t in range(T) if np.isfinite(xf[t]).all()]
+    np.testing.assert_allclose(w[finite], rw[finite], rtol=0, atol=1e-6)
+    ref, _, _ = run_oracle(xf, rf, ex, E, k, False, tokens=np.array(finite))
+    assert_close_f32(host(y)[finite], ref)

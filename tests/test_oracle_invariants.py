@@ -228,6 +228,53 @@ def test_moe_route_ties_keep_lower_index():
     assert list(idx[0]) == [1, 2, 0]
 
 
+def _gpu_rank_rule(probs, k):
+    """The device router's ranking: a lane's rank is the number of experts
+    with a greater probability plus the lower-indexed experts it ties with,
+    where an unordered pair (NaN) counts as a tie. Returns [T][k] indices, or
+    None for a token whose ranks are not a permutation."""
+    T, E = probs.shape
+    out = np.zeros((T, k), np.uint32)
+    for t in range(T):
+        slots = [None] * E
+        for e in range(E):
+            pe = probs[t, e]
+            rank = 0
+            for j in range(E):
+                pj = probs[t, j]
+                tie = not (pj < pe) and not (pj > pe)
+                rank += (pj > pe) or (tie and j < e)
+            if slots[rank] is not None:
+                return None
+            slots[rank] = e
+        out[t] = slots[:k]
+    return out
+
+
+def test_moe_route_nonfinite_tokens_and_gpu_rank_rule():
+    """NaN and +inf in a token's activations make all of its probabilities
+    NaN (the exp sum is NaN); the oracle's stable sort then keeps experts in
+    index order, as the reference's sort_by(partial_cmp().unwrap_or(Equal))
+    does. The device router's rank rule must give the same indices and a
+    permutation for every token, finite ones included."""
+    rng = np.random.default_rng(31)
+    T, H, E, k = 12, 16, 6, 3
+    x = rng.standard_normal((T, H)).astype(np.float32)
+    r = (rng.standard_normal((E, H)) * 0.5).astype(np.float32)
+    x[2, 3] = np.nan
+    x[4, :] = np.inf
+    x[5, 0] = -np.inf
+    x[6, 1] = np.inf
+    idx, w, probs = oracle.moe_route(x, r, k)
+    for t in (2, 4, 6):
+        assert np.isnan(probs[t]).all(), t
+        assert list(idx[t]) == list(range(k)), t
+    np.testing.assert_array_equal(_gpu_rank_rule(probs, k), idx)
+    # the rule without the tie clause for NaN leaves slots unwritten
+    nan_row = np.full((1, E), np.nan, np.float32)
+    assert _gpu_rank_rule(nan_row, k) is not None
+
+
 def _moe_f64(x, r, wg, sg, wu, su, wd, sd, k, gelu):
     idx, w = _softmax_route_f64(x, r, k)
     out = np.zeros((x.shape[0], x.shape[1]))
@@ -321,3 +368,29 @@ def test_quantize_ste_closed_cases():
     w = np.array([0.5, -0.5, 1.5, np.float32(4) * norm - np.float32(2.5)], np.float32)
     qt, at = oracle.quantize_ternary(w)
     assert at == 1.0 and qt.tolist() == [1, -1, 1, 1]
+
+
+def test_sparse_index_decode_exact_on_dyadic_and_vs_f64():
+    rng = np.random.default_rng(41)
+    rows, cols = 37, 200
+    t = rng.integers(-1, 2, size=rows * cols).astype(np.int8)
+    xd = (rng.integers(-64, 65, size=cols) / 8).astype(np.float32)
+    idx = oracle.ternary_sparse_indices(t, rows, cols)
+    # every +1 and -1 is listed once, in column order
+    po, pi, no, ni = idx
+    assert po[-1] == (t == 1).sum() and no[-1] == (t == -1).sum()
+    for r in range(rows):
+        assert (np.diff(pi[po[r]:po[r + 1]].astype(np.int64)) > 0).all()
+    exact = t.reshape(rows, cols).astype(np.float64) @ xd.astype(np.float64) * 0.25
+    np.testing.assert_array_equal(oracle.ternary_matmul_sparse_decode(*idx, 0.25, xd, rows), exact.astype(np.float32))
+    x = rng.standard_normal(cols).astype(np.float32)
+    ref = t.reshape(rows, cols).astype(np.float64) @ x.astype(np.float64) * 0.7
+    np.testing.assert_allclose(oracle.ternary_matmul_sparse_decode(*idx, 0.7, x, rows), ref, rtol=1e-5, atol=1e-5)
+
+
+def test_ternary_stats_counts_every_value_once():
+    rng = np.random.default_rng(42)
+    t = rng.integers(-1, 2, size=10007).astype(np.int8)
+    counts, ratios, _ = oracle.ternary_stats(t)
+    assert list(counts) == [(t == -1).sum(), (t == 0).sum(), (t == 1).sum()]
+    np.testing.assert_allclose(ratios.sum(), 1.0, atol=1e-6)

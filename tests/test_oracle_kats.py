@@ -96,14 +96,6 @@ def test_sparse24_cpu_basic_kat():
     assert ((d != 0).sum(axis=1) <= kat["max_nonzeros_per_group"]).all()
 
 
-def test_prune_fp32_kat():
-    kat = KATS["prune_fp32"]
-    p, s, sc = oracle.prune_fp32_to_sparse24(kat["weights"], kat["rows"], kat["cols"])
-    d = oracle.sparse24_cpu_to_ternary(p, s, kat["rows"], kat["cols"])
-    np.testing.assert_array_equal(d, kat["expected_decompressed"])
-    assert sc > 0
-
-
 @pytest.mark.parametrize("kat", KATS["routing"], ids=lambda k: k["source"].split()[-1])
 def test_routing_kats(kat):
     # Router = identity matrix, so the logits are exactly the inputs.
@@ -116,3 +108,59 @@ def test_routing_kats(kat):
     np.testing.assert_allclose(w[0], expect, atol=kat["weight_tol"], rtol=0)
     if "sum_tol" in kat:
         assert abs(float(w[0].sum()) - 1.0) < kat["sum_tol"]
+
+
+def test_ternary_stats_kat():
+    kat = KATS["ternary_stats"]
+    counts, ratios, comp = oracle.ternary_stats(np.array(kat["values"], np.int8))
+    assert list(counts) == [kat["num_neg1"], kat["num_zero"], kat["num_pos1"]]
+    assert abs(float(ratios[1]) - kat["ratio_zero"]) < kat["ratio_tol"]
+    assert abs(comp - kat["compression_ratio_vs_f32"]) < 0.01
+
+
+def test_sparse_indices_kat():
+    kat = KATS["sparse_indices_counts"]
+    po, pi, no, ni = oracle.ternary_sparse_indices(np.array(kat["ternary"], np.int8), kat["rows"], kat["cols"])
+    for r in range(kat["rows"]):
+        assert list(pi[po[r]:po[r + 1]]) == kat["pos"][r]
+        assert list(ni[no[r]:no[r + 1]]) == kat["neg"][r]
+
+
+def test_sparse_decode_vs_general_kat():
+    kat = KATS["sparse_decode_vs_general"]
+    rows, cols = kat["rows"], kat["cols"]
+    t = np.array([{0: 1, 1: -1, 2: 0}[i % 3] for i in range(rows * cols)], np.int8)
+    x = (np.arange(cols, dtype=np.float32) * np.float32(0.1)).astype(np.float32)
+    idx = oracle.ternary_sparse_indices(t, rows, cols)
+    out = oracle.ternary_matmul_sparse_decode(*idx, kat["scale"], x, rows)
+    ref = oracle.ternary_matmul_decode(t, kat["scale"], x, rows, cols)
+    np.testing.assert_allclose(out, ref, rtol=0, atol=kat["tol"])
+
+
+def test_blocked_vs_scalar_kat():
+    kat = KATS["blocked_vs_scalar"]
+    rows, cols, bs = kat["rows"], kat["cols"], kat["block_size"]
+    w = (np.sin(np.arange(rows * cols, dtype=np.float32) * np.float32(1.618)) * np.float32(0.5)).astype(np.float32)
+    nb = (cols + bs - 1) // bs
+    scales = np.zeros(nb, np.float32)
+    for b in range(nb):
+        blk = w.reshape(rows, cols)[:, b * bs:(b + 1) * bs]
+        s = np.float32(0)
+        for v in blk.ravel():
+            s = np.float32(s + np.float32(abs(v)))
+        scales[b] = (s / np.float32(blk.size)) / np.float32(0.7978845608) if s > 0 else np.float32(1.0)
+    t = np.zeros(rows * cols, np.int8)
+    for r in range(rows):
+        for b in range(nb):
+            inv = np.float32(1.0) / scales[b]
+            for j in range(b * bs, min((b + 1) * bs, cols)):
+                v = np.float32(w[r * cols + j] * inv)
+                t[r * cols + j] = int(np.clip(np.sign(v) * np.floor(abs(v) + 0.5), -1, 1))
+    x = np.cos(np.arange(cols, dtype=np.float32) * np.float32(0.1)).astype(np.float32)
+    out = oracle.ternary_matmul_blocked(t, scales, bs, x, rows, cols, 1)
+    ref = np.zeros(rows, np.float32)
+    for r in range(rows):
+        for b in range(nb):
+            for j in range(b * bs, min((b + 1) * bs, cols)):
+                ref[r] = np.float32(ref[r] + np.float32(scales[b] * np.float32(t[r * cols + j])) * x[j])
+    np.testing.assert_allclose(out, ref, rtol=0, atol=kat["tol"])
