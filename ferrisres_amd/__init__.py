@@ -61,6 +61,8 @@ _SIGS = {
     "frx_ternary_glu": (_int, [_vp, _vp, _int, _vp, _vp, _vp, _vp, _u32, _u32, _u32, _int, _vp]),
     "frx_ternary_ffn": (_int, [_vp, _vp, _int, _vp, _vp, _vp, _vp, _vp, _vp, _u32, _u32, _u32,
                                _int, _vp, _int]),
+    "frx_ternary_ffn_noalloc": (_int, [_vp, _vp, _int, _vp, _vp, _vp, _vp, _vp, _vp, _u32, _u32, _u32,
+                                       _int, _vp, _int]),
     "frx_set_ffn_mode": (_int, [_vp, _int]),
     "frx_upload_ternary": (_int, [_vp, _vp, _u32, _u32, _vp, ctypes.c_float, ctypes.POINTER(_vp),
                                   ctypes.POINTER(_vp)]),
@@ -281,6 +283,16 @@ class Context:
         _check(lib().frx_ternary_ffn(self._h, _ptr(x), _dtype_code(x), _ptr(w_gate), _ptr(s_gate),
                                      _ptr(w_up), _ptr(s_up), _ptr(w_down), _ptr(s_down), M, H, I,
                                      act, _ptr(y), _dtype_code(y)), self._h)
+        return y
+
+    def ternary_ffn_noalloc(self, x, w_gate, s_gate, w_up, s_up, w_down, s_down, y, act: int = ACT_SILU):
+        """frx_ternary_ffn_noalloc: the dense FFN with its intermediate in the
+        library's fixed per-GPU scratch array (no device allocation)."""
+        M, H = x.shape
+        I = w_gate.shape[0]
+        _check(lib().frx_ternary_ffn_noalloc(self._h, _ptr(x), _dtype_code(x), _ptr(w_gate), _ptr(s_gate),
+                                             _ptr(w_up), _ptr(s_up), _ptr(w_down), _ptr(s_down), M, H, I,
+                                             act, _ptr(y), _dtype_code(y)), self._h)
         return y
 
     # Weight ingest: resident device copies in the GPU layout.

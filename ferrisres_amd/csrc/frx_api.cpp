@@ -22,6 +22,43 @@
 #include "../../include/frx_ternary.h"
 #include "frx_internal.hpp"
 
+// Device scratch of frx_ternary_ffn_noalloc: one array per GPU, held until
+// the process ends. Its host-side name is only a handle: kernels and copies
+// get the device address from hipGetSymbolAddress (noalloc_scratch_ptr).
+// Every call on a GPU shares that GPU's array; calls that overlap on one GPU
+// race on it.
+static __device__ __align__(256) unsigned char
+    frx_noalloc_scratch[FRX_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_noalloc_mu;
+void *g_noalloc_ptr[kMaxDevices];  // device address of frx_noalloc_scratch per device
+hipError_t g_noalloc_err[kMaxDevices];
+bool g_noalloc_done[kMaxDevices];
+
+// Resolves the scratch array's device address on `device` once (that device
+// current while it runs) and returns the cached result after that.
+hipError_t noalloc_scratch_ptr(int device, void **out) {
+  *out = nullptr;
+  if (device < 0 || device >= kMaxDevices) return hipErrorInvalidDevice;
+  std::lock_guard<std::mutex> lk(g_noalloc_mu);
+  if (!g_noalloc_done[device]) {
+    int prev = 0;
+    hipError_t e = hipGetDevice(&prev);
+    if (e == hipSuccess) e = hipSetDevice(device);
+    void *p = nullptr;
+    if (e == hipSuccess) e = hipGetSymbolAddress(&p, HIP_SYMBOL(frx_noalloc_scratch));
+    if (prev != device) hipSetDevice(prev);
+    g_noalloc_ptr[device] = e == hipSuccess ? p : nullptr;
+    g_noalloc_err[device] = e;
+    g_noalloc_done[device] = true;
+  }
+  *out = g_noalloc_ptr[device];
+  return g_noalloc_err[device];
+}
+}  // namespace
+
 struct frx_ctx {
   int device = 0;
   hipStream_t stream = nullptr;
@@ -29,6 +66,8 @@ struct frx_ctx {
   // Workspaces replaced by larger ones stay allocated until frx_destroy: a
   // graph captured at a smaller size still holds their addresses.
   std::vector<void *> retired;
+  void *noalloc = nullptr;  // device address of frx_noalloc_scratch on this device
+  hipError_t noalloc_err = hipSuccess;
   // growable device scratch for the host-slice API and the MoE workspace
   void *scratch = nullptr;
   size_t scratch_bytes = 0;
@@ -100,6 +139,7 @@ frx_status frx_create(int device, frx_ctx **out) {
   frx_ctx *c = new frx_ctx();
   c->device = device;
   c->cus = prop.multiProcessorCount;
+  c->noalloc_err = noalloc_scratch_ptr(device, &c->noalloc);
   *out = c;
   return FRX_OK;
 }
@@ -422,6 +462,29 @@ frx_status frx_ternary_ffn(frx_ctx *ctx, const void *x, frx_dtype xt, const uint
     return st;
   return ffn_run(ctx, x, xt, w_gate, s_gate, w_up, s_up, w_down, s_down, M, H, I, act, y, yt, ctx->ffn_ws, nullptr,
                  true);
+}
+
+frx_status frx_ternary_ffn_noalloc(frx_ctx *ctx, const void *x, frx_dtype xt, const uint32_t *w_gate,
+                                   const float *s_gate, const uint32_t *w_up, const float *s_up,
+                                   const uint32_t *w_down, const float *s_down, uint32_t M, uint32_t H,
+                                   uint32_t I, frx_activation act, void *y, frx_dtype yt) {
+  frx_status st = enter(ctx);
+  if (st != FRX_OK) return st;
+  if ((st = check_ffn(ctx, x, xt, w_gate, s_gate, w_up, s_up, M, H, I, act)) != FRX_OK) return st;
+  if ((st = check_ffn_down(ctx, w_down, s_down, y, yt)) != FRX_OK) return st;
+  if (ctx->noalloc_err != hipSuccess || !ctx->noalloc)
+    return fail(ctx, FRX_ERR_GPU, "no-allocation FFN: scratch address unavailable: %s",
+                hipGetErrorString(ctx->noalloc_err));
+  const size_t hb = a256((size_t)M * I * 4);
+  const size_t need = M > 16 ? 2 * hb : hb;  // h, and the GEMM path's up projection
+  if (need > FRX_NOALLOC_SCRATCH_BYTES)
+    return fail(ctx, FRX_ERR_UNSUPPORTED,
+                "no-allocation FFN: M=%u I=%u needs %zu bytes of scratch, the maximum is %u "
+                "(M*I*4 bytes for M <= 16, twice that above)",
+                M, I, need, (unsigned)FRX_NOALLOC_SCRATCH_BYTES);
+  char *base = reinterpret_cast<char *>(ctx->noalloc);
+  return ffn_run(ctx, x, xt, w_gate, s_gate, w_up, s_up, w_down, s_down, M, H, I, act, y, yt, base,
+                 M > 16 ? reinterpret_cast<float *>(base + hb) : nullptr, false);
 }
 
 // ---- host-slice accelerator API (GpuMatmulAccelerator) --------------------

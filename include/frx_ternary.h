@@ -175,6 +175,26 @@ frx_status frx_ternary_ffn(frx_ctx *ctx, const void *x, frx_dtype xt,
                            uint32_t M, uint32_t H, uint32_t I,
                            frx_activation act, void *y, frx_dtype yt);
 
+/* ---- dense ternary FFN without allocation ------------------------------------
+ * No counterpart in the reference. For callers that cannot allocate device
+ * memory: code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc. Same arguments, semantics and kernels as frx_ternary_ffn
+ * in FRX_FFN_TWO_LAUNCH execution (whatever frx_set_ffn_mode selected), but
+ * the intermediate lives in a fixed device array of the library
+ * (FRX_NOALLOC_SCRATCH_BYTES per GPU, held until the process ends) and the
+ * call allocates nothing. It needs M*I*4 bytes of that array (rounded up to
+ * 256) for M <= 16 and twice that above; larger shapes return
+ * FRX_ERR_UNSUPPORTED. Every call on a GPU shares that GPU's array: calls
+ * that overlap on one GPU (other streams, other contexts, other threads)
+ * race on it, and must be serialised by the caller. */
+#define FRX_NOALLOC_SCRATCH_BYTES (4u << 20)
+frx_status frx_ternary_ffn_noalloc(frx_ctx *ctx, const void *x, frx_dtype xt,
+                                   const uint32_t *w_gate, const float *s_gate,
+                                   const uint32_t *w_up, const float *s_up,
+                                   const uint32_t *w_down, const float *s_down,
+                                   uint32_t M, uint32_t H, uint32_t I,
+                                   frx_activation act, void *y, frx_dtype yt);
+
 /* Selects the execution of frx_ternary_ffn on this context (default
  * FRX_FFN_AUTO). No counterpart in the reference, whose FFN is three
  * separate matmul calls. */

@@ -28,9 +28,11 @@ int main(void) {
   linear_fn lin = frx_ternary_linear;
   linear_fn sp = frx_sparse24_ternary_linear;
   ffn_fn ffn = frx_ternary_ffn;
+  ffn_fn ffn_na = frx_ternary_ffn_noalloc;
   (void)lin;
   (void)sp;
   (void)ffn;
+  (void)ffn_na;
 
   /* pack_ternary: values -1,0,+1,0,+1 -> codes 00,01,10,01 | 10 */
   const int8_t vals[5] = {-1, 0, 1, 0, 1};
