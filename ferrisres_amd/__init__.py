@@ -20,6 +20,7 @@ LIB_PATH = os.path.join(HERE, "libfrx_ternary.so")
 FRX_F32, FRX_BF16 = 0, 1
 ACT_SILU, ACT_GELU_TANH = 0, 1
 FFN_AUTO, FFN_ONE_LAUNCH, FFN_TWO_LAUNCH = 0, 1, 2
+MOE_TERNARY_MOE_LAYER, MOE_CPU_MOE_LAYER = 0, 1
 QUANT_ABSMEAN, QUANT_STE = 0, 1
 
 _STATUS = {
@@ -56,6 +57,11 @@ _SIGS = {
     "frx_version": (ctypes.c_char_p, []),
     "frx_ternary_linear": (_int, [_vp, _vp, _vp, _vp, _int, _vp, _int, _u32, _u32, _u32]),
     "frx_sparse24_ternary_linear": (_int, [_vp, _vp, _vp, _vp, _int, _vp, _int, _u32, _u32, _u32]),
+    "frx_ternary_linear_blocked": (_int, [_vp, _vp, _vp, _u32, _vp, _int, _vp, _int, _u32, _u32, _u32]),
+    "frx_ternary_sparse_decode": (_int, [_vp, _vp, _vp, _vp, _vp, ctypes.c_float, _vp, _int, _vp, _int,
+                                         _u32, _u32, _u32]),
+    "frx_ternary_stats": (_int, [_vp, _vp, _u32, _u32, _vp]),
+    "frx_ternary_sparse_indices": (_int, [_vp, _u32, _u32, _vp, _vp, _vp, _vp]),
     "frx_moe_ternary_ffn": (_int, [_vp, _vp, _int, _vp, _int, _vp, _vp, _vp, _vp, _vp, _vp,
                                    _u32, _u32, _u32, _u32, _u32, _int, _vp, _int, _vp, _vp]),
     "frx_ternary_glu": (_int, [_vp, _vp, _int, _vp, _vp, _vp, _vp, _u32, _u32, _u32, _int, _vp]),
@@ -64,6 +70,7 @@ _SIGS = {
     "frx_ternary_ffn_noalloc": (_int, [_vp, _vp, _int, _vp, _vp, _vp, _vp, _vp, _vp, _u32, _u32, _u32,
                                        _int, _vp, _int]),
     "frx_set_ffn_mode": (_int, [_vp, _int]),
+    "frx_set_moe_routing": (_int, [_vp, _int]),
     "frx_upload_ternary": (_int, [_vp, _vp, _u32, _u32, _vp, ctypes.c_float, ctypes.POINTER(_vp),
                                   ctypes.POINTER(_vp)]),
     "frx_upload_stm": (_int, [_vp, _vp, _sz, ctypes.POINTER(_vp), ctypes.POINTER(_vp), ctypes.POINTER(_u32),
@@ -153,6 +160,20 @@ def gpu_packed(values: np.ndarray, tensor_scale: float):
     return w.reshape(n, k // 16), s
 
 
+def ternary_sparse_indices(values: np.ndarray):
+    """frx_ternary_sparse_indices (ternary_sparse_indices, ternary.rs:681-707)
+    as CSR arrays (pos_off, pos_idx, neg_off, neg_idx) for an i8 [N][K]."""
+    v = np.ascontiguousarray(values, dtype=np.int8)
+    n, k = v.shape
+    po = np.zeros(n + 1, np.uint32)
+    no = np.zeros(n + 1, np.uint32)
+    _check(lib().frx_ternary_sparse_indices(_np_ptr(v), n, k, _np_ptr(po), None, _np_ptr(no), None))
+    pi = np.zeros(max(int(po[-1]), 1), np.uint32)
+    ni = np.zeros(max(int(no[-1]), 1), np.uint32)
+    _check(lib().frx_ternary_sparse_indices(_np_ptr(v), n, k, _np_ptr(po), _np_ptr(pi), _np_ptr(no), _np_ptr(ni)))
+    return po, pi, no, ni
+
+
 def pack_sparse24_gpu(w: np.ndarray, with_scales: bool = False):
     v = np.ascontiguousarray(w, dtype=np.int8)
     n, k = v.shape
@@ -183,6 +204,40 @@ def _dtype_code(t) -> int:
     if t.dtype == torch.bfloat16:
         return FRX_BF16
     raise TypeError(f"unsupported dtype {t.dtype}")
+
+
+def _numel(t):
+    if hasattr(t, "numel"):
+        return int(t.numel())
+    return int(np.prod(t.shape))
+
+
+def _shape_err(msg):
+    return FrxError(2, msg)
+
+
+def _shape2(t, name):
+    if len(t.shape) != 2:
+        raise _shape_err(f"{name} must be 2-D, got shape {tuple(t.shape)}")
+    return int(t.shape[0]), int(t.shape[1])
+
+
+def _rows(t, words_per_row, name):
+    """Rows of a packed matrix whose rows hold words_per_row u32 words."""
+    n = _numel(t)
+    if words_per_row <= 0 or n % words_per_row:
+        raise _shape_err(f"{name} holds {n} words, not a multiple of {words_per_row} per row")
+    return n // words_per_row
+
+
+def _expect_numel(t, n, name):
+    if t is not None and _numel(t) < n:
+        raise _shape_err(f"{name} holds {_numel(t)} elements, needs {n}")
+
+
+def _expect_shape(t, shape, name):
+    if tuple(int(d) for d in t.shape) != tuple(shape):
+        raise _shape_err(f"{name} has shape {tuple(t.shape)}, expected {tuple(shape)}")
 
 
 def _ptr(t):
@@ -241,25 +296,61 @@ class Context:
 
     # TernaryMatMulOp::dispatch analogue; all tensors on the device.
     def ternary_linear(self, w, scale, x, y):
-        M, K = x.shape
-        N = w.shape[0]
+        M, K = _shape2(x, "x")
+        N = _rows(w, K // 16, "w") if K % 16 == 0 else int(w.shape[0])
+        _expect_numel(scale, N, "scale")
+        _expect_shape(y, (M, N), "y")
         _check(lib().frx_ternary_linear(self._h, _ptr(w), _ptr(scale), _ptr(x), _dtype_code(x),
                                         _ptr(y), _dtype_code(y), M, K, N), self._h)
         return y
 
     def sparse24_ternary_linear(self, meta, scale, x, y):
-        M, K = x.shape
-        N = meta.shape[0]
+        M, K = _shape2(x, "x")
+        N = _rows(meta, ((K + 3) // 4 + 5) // 6, "meta")
+        _expect_numel(scale, N, "scale")
+        _expect_shape(y, (M, N), "y")
         _check(lib().frx_sparse24_ternary_linear(self._h, _ptr(meta), _ptr(scale), _ptr(x),
                                                  _dtype_code(x), _ptr(y), _dtype_code(y), M, K, N),
                self._h)
         return y
 
+    def ternary_linear_blocked(self, w, block_scales, block_size: int, x, y):
+        """frx_ternary_linear_blocked (ternary_matmul_blocked, ternary.rs:541-579)."""
+        M, K = _shape2(x, "x")
+        N = _rows(w, K // 16, "w")
+        if block_size > 0:
+            _expect_numel(block_scales, (K + block_size - 1) // block_size, "block_scales")
+        _expect_shape(y, (M, N), "y")
+        _check(lib().frx_ternary_linear_blocked(self._h, _ptr(w), _ptr(block_scales), block_size, _ptr(x),
+                                                _dtype_code(x), _ptr(y), _dtype_code(y), M, K, N), self._h)
+        return y
+
+    def ternary_sparse_decode(self, pos_off, pos_idx, neg_off, neg_idx, scale: float, x, y):
+        """frx_ternary_sparse_decode (ternary_matmul_sparse_decode, ternary.rs:647-673)."""
+        M, K = _shape2(x, "x")
+        N = y.shape[-1]
+        _expect_shape(y, (M, N), "y")
+        _expect_numel(pos_off, N + 1, "pos_off")
+        _expect_numel(neg_off, N + 1, "neg_off")
+        _check(lib().frx_ternary_sparse_decode(self._h, _ptr(pos_off), _ptr(pos_idx), _ptr(neg_off), _ptr(neg_idx),
+                                               ctypes.c_float(scale), _ptr(x), _dtype_code(x), _ptr(y),
+                                               _dtype_code(y), M, K, N), self._h)
+        return y
+
+    def ternary_stats(self, w, K: int, counts):
+        """frx_ternary_stats: counts (3 x u64 on the device) of -1, 0, +1 codes."""
+        N = _rows(w, K // 16, "w")
+        _expect_numel(counts, 3, "counts")
+        _check(lib().frx_ternary_stats(self._h, _ptr(w), N, K, _ptr(counts)), self._h)
+        return counts
+
     def moe_ternary_ffn(self, x, router, w_gate, s_gate, w_up, s_up, w_down, s_down, y,
                         top_k: int, act: int = ACT_SILU, topk_idx=None, topk_w=None):
-        T, H = x.shape
-        E = router.shape[0]
-        I = w_gate[0].shape[0]
+        T, H = _shape2(x, "x")
+        E = len(w_gate)
+        _expect_numel(router, E * H, "router")
+        I = _rows(w_gate[0], H // 16, "w_gate[0]") if H % 16 == 0 else int(w_gate[0].shape[0])
+        _expect_shape(y, (T, H), "y")
         arr = lambda ts: (_vp * E)(*[t.data_ptr() for t in ts])  # noqa: E731
         _check(lib().frx_moe_ternary_ffn(
             self._h, _ptr(x), _dtype_code(x), _ptr(router), _dtype_code(router),
@@ -334,6 +425,11 @@ class Context:
         _check(lib().frx_quantize_ternary(self._h, _ptr(w), _dtype_code(w), N, K, rule, _ptr(packed),
                                           _ptr(scale)), self._h)
         return packed, scale
+
+    def set_moe_routing(self, routing: int):
+        """frx_set_moe_routing: MOE_TERNARY_MOE_LAYER (router [E,H], default)
+        or MOE_CPU_MOE_LAYER (CpuMoELayer: router [H,E], top-k by logit)."""
+        _check(lib().frx_set_moe_routing(self._h, routing), self._h)
 
     def set_ffn_mode(self, mode: int):
         """frx_set_ffn_mode: FFN_AUTO, FFN_ONE_LAUNCH or FFN_TWO_LAUNCH."""

@@ -77,8 +77,15 @@ struct frx_ctx {
   size_t ffn_ws_bytes = 0;
   void *glu_ws = nullptr;  // up projection of the GEMM-path GLU (fp32)
   size_t glu_ws_bytes = 0;
+  void *blk_ws = nullptr;  // prescaled activations of the column-block linear (fp32)
+  size_t blk_ws_bytes = 0;
+  void *unit_ws = nullptr;  // unit row scales of the column-block linear
+  size_t unit_ws_bytes = 0;
   unsigned *ffn_bar = nullptr;  // grid-barrier words of the one-launch FFN
   int ffn_mode = FRX_FFN_AUTO;
+  int moe_routing = FRX_MOE_TERNARY_MOE_LAYER;
+  void *router_ws = nullptr;  // [E][H] copy of a [H][E] router (CpuMoELayer routing)
+  size_t router_ws_bytes = 0;
   int cus = 0;  // compute units of the device
 };
 
@@ -151,6 +158,9 @@ void frx_destroy(frx_ctx *ctx) {
   if (ctx->moe_ws) hipFree(ctx->moe_ws);
   if (ctx->ffn_ws) hipFree(ctx->ffn_ws);
   if (ctx->glu_ws) hipFree(ctx->glu_ws);
+  if (ctx->blk_ws) hipFree(ctx->blk_ws);
+  if (ctx->router_ws) hipFree(ctx->router_ws);
+  if (ctx->unit_ws) hipFree(ctx->unit_ws);
   if (ctx->ffn_bar) hipFree(ctx->ffn_bar);
   for (void *p : ctx->retired) hipFree(p);
   delete ctx;
@@ -194,6 +204,15 @@ frx_status frx_set_ffn_mode(frx_ctx *ctx, frx_ffn_mode mode) {
   if (mode != FRX_FFN_AUTO && mode != FRX_FFN_ONE_LAUNCH && mode != FRX_FFN_TWO_LAUNCH)
     return fail(ctx, FRX_ERR_UNSUPPORTED, "unknown FFN mode %d", (int)mode);
   ctx->ffn_mode = mode;
+  return FRX_OK;
+}
+
+frx_status frx_set_moe_routing(frx_ctx *ctx, frx_moe_routing routing) {
+  if (!ctx) return FRX_ERR_DEVICE;
+  ctx->err[0] = 0;
+  if (routing != FRX_MOE_TERNARY_MOE_LAYER && routing != FRX_MOE_CPU_MOE_LAYER)
+    return fail(ctx, FRX_ERR_UNSUPPORTED, "unknown MoE routing %d", (int)routing);
+  ctx->moe_routing = routing;
   return FRX_OK;
 }
 
@@ -289,9 +308,20 @@ frx_status frx_moe_ternary_ffn(
     return st;
   frx::MoeWorkspace ws;
   frx::moe_workspace_carve(ctx->moe_ws, (int)T, (int)H, (int)I, (int)E, (int)top_k, &ws);
-  hipError_t e = frx::launch_moe(x, xt == FRX_BF16, router, rt == FRX_BF16, w_gate, s_gate, w_up, s_up, w_down,
+  const void *router_eh = router;
+  if (ctx->moe_routing == FRX_MOE_CPU_MOE_LAYER) {
+    // CpuMoELayer reads its router as [H][E]; the kernels read [E][H]
+    const size_t rb = (size_t)H * E * (rt == FRX_BF16 ? 2 : 4);
+    if ((st = ensure_buffer(ctx, &ctx->router_ws, &ctx->router_ws_bytes, a256(rb), "router workspace allocation")) !=
+        FRX_OK)
+      return st;
+    hipError_t e = frx::launch_router_transpose(router, rt == FRX_BF16, ctx->router_ws, (int)H, (int)E, ctx->stream);
+    if (e != hipSuccess) return hip_fail(ctx, e, "router transpose launch");
+    router_eh = ctx->router_ws;
+  }
+  hipError_t e = frx::launch_moe(x, xt == FRX_BF16, router_eh, rt == FRX_BF16, w_gate, s_gate, w_up, s_up, w_down,
                                  s_down, (int)T, (int)H, (int)I, (int)E, (int)top_k, act == FRX_ACT_GELU_TANH, y,
-                                 yt == FRX_BF16, topk_idx, topk_w, ws, ctx->stream);
+                                 yt == FRX_BF16, topk_idx, topk_w, ws, ctx->moe_routing, ctx->stream);
   if (e != hipSuccess) return hip_fail(ctx, e, "moe launch");
   return FRX_OK;
 }
@@ -485,6 +515,69 @@ frx_status frx_ternary_ffn_noalloc(frx_ctx *ctx, const void *x, frx_dtype xt, co
   char *base = reinterpret_cast<char *>(ctx->noalloc);
   return ffn_run(ctx, x, xt, w_gate, s_gate, w_up, s_up, w_down, s_down, M, H, I, act, y, yt, base,
                  M > 16 ? reinterpret_cast<float *>(base + hb) : nullptr, false);
+}
+
+// ---- the reference's other matmul forms --------------------------------------
+
+frx_status frx_ternary_linear_blocked(frx_ctx *ctx, const uint32_t *w, const float *block_scales,
+                                      uint32_t block_size, const void *x, frx_dtype xt, void *y, frx_dtype yt,
+                                      uint32_t M, uint32_t K, uint32_t N) {
+  frx_status st = enter(ctx);
+  if (st != FRX_OK) return st;
+  if (!block_scales) return fail(ctx, FRX_ERR_SHAPE, "null block scales");
+  if (block_size == 0) return fail(ctx, FRX_ERR_SHAPE, "block_size must be positive");
+  if ((st = check_linear(ctx, w, block_scales, x, xt, y, yt, M, K, N, false)) != FRX_OK) return st;
+  if ((st = ensure_buffer(ctx, &ctx->blk_ws, &ctx->blk_ws_bytes, a256((size_t)M * K * 4),
+                          "block-scale workspace allocation")) != FRX_OK)
+    return st;
+  if (ctx->unit_ws_bytes < (size_t)N * 4) {
+    if ((st = ensure_buffer(ctx, &ctx->unit_ws, &ctx->unit_ws_bytes, a256((size_t)N * 4),
+                            "unit scale allocation")) != FRX_OK)
+      return st;
+    hipError_t e = frx::launch_fill(reinterpret_cast<float *>(ctx->unit_ws), 1.0f, ctx->unit_ws_bytes / 4,
+                                    ctx->stream);
+    if (e != hipSuccess) return hip_fail(ctx, e, "unit scale fill");
+  }
+  float *xs = reinterpret_cast<float *>(ctx->blk_ws);
+  const float *ones = reinterpret_cast<const float *>(ctx->unit_ws);
+  hipError_t e = frx::launch_block_prescale(x, xt == FRX_BF16, block_scales, (int)block_size, xs, (int)M, (int)K,
+                                            ctx->stream);
+  if (e == hipSuccess) {
+    if (M <= 16)
+      e = frx::launch_gemv(w, ones, xs, 0, y, yt == FRX_BF16, (int)M, (int)K, (int)N, ctx->stream);
+    else
+      e = frx::launch_gemm(w, ones, xs, 0, y, yt == FRX_BF16, (int)M, (int)K, (int)N, 0, ctx->stream);
+  }
+  if (e != hipSuccess) return hip_fail(ctx, e, "column-block linear launch");
+  return FRX_OK;
+}
+
+frx_status frx_ternary_sparse_decode(frx_ctx *ctx, const uint32_t *pos_off, const uint32_t *pos_idx,
+                                     const uint32_t *neg_off, const uint32_t *neg_idx, float scale, const void *x,
+                                     frx_dtype xt, void *y, frx_dtype yt, uint32_t M, uint32_t K, uint32_t N) {
+  frx_status st = enter(ctx);
+  if (st != FRX_OK) return st;
+  if (!pos_off || !pos_idx || !neg_off || !neg_idx || !x || !y)
+    return fail(ctx, FRX_ERR_SHAPE, "null buffer pointer");
+  if (M == 0 || K == 0 || N == 0) return fail(ctx, FRX_ERR_SHAPE, "empty shape M=%u K=%u N=%u", M, K, N);
+  if ((xt != FRX_F32 && xt != FRX_BF16) || (yt != FRX_F32 && yt != FRX_BF16))
+    return fail(ctx, FRX_ERR_UNSUPPORTED, "dtype must be FRX_F32 or FRX_BF16");
+  if (M > 65535) return fail(ctx, FRX_ERR_SHAPE, "M=%u exceeds 65535 tokens", M);
+  hipError_t e = frx::launch_index_decode(pos_off, pos_idx, neg_off, neg_idx, scale, x, xt == FRX_BF16, y,
+                                          yt == FRX_BF16, (int)M, (int)K, (int)N, ctx->stream);
+  if (e != hipSuccess) return hip_fail(ctx, e, "index-list decode launch");
+  return FRX_OK;
+}
+
+frx_status frx_ternary_stats(frx_ctx *ctx, const uint32_t *w, uint32_t N, uint32_t K, unsigned long long *counts) {
+  frx_status st = enter(ctx);
+  if (st != FRX_OK) return st;
+  if (!w || !counts) return fail(ctx, FRX_ERR_SHAPE, "null buffer pointer");
+  if (N == 0 || K == 0) return fail(ctx, FRX_ERR_SHAPE, "empty shape N=%u K=%u", N, K);
+  if (K % 16 != 0) return fail(ctx, FRX_ERR_SHAPE, "K=%u must be a multiple of 16", K);
+  hipError_t e = frx::launch_stats(w, (size_t)N * (K / 16), counts, ctx->stream);
+  if (e != hipSuccess) return hip_fail(ctx, e, "statistics launch");
+  return FRX_OK;
 }
 
 // ---- host-slice accelerator API (GpuMatmulAccelerator) --------------------

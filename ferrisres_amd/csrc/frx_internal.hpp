@@ -102,6 +102,21 @@ hipError_t launch_quantize(const void *w, int wt_bf16, int N, int K, int rule, u
 hipError_t launch_sp24_cpu_to_gpu(const uint8_t *patterns, const uint8_t *signs, int N, int K, uint32_t *meta,
                                   hipStream_t stream);
 
+// The reference's other matmul forms (frx_variants.hip).
+// Index-list decode: y[m][r] = scale * (sum of x[m][pos] - sum of x[m][neg])
+// over the CSR lists of row r.
+hipError_t launch_index_decode(const uint32_t *pos_off, const uint32_t *pos_idx, const uint32_t *neg_off,
+                               const uint32_t *neg_idx, float scale, const void *x, int xt_bf16, void *y,
+                               int yt_bf16, int M, int K, int N, hipStream_t stream);
+// counts[0..2] (device) = number of -1, 0, +1 codes in nwords packed words.
+hipError_t launch_stats(const uint32_t *w, size_t nwords, unsigned long long *counts, hipStream_t stream);
+// xs[m][k] = x[m][k] * scales[k / block_size] (fp32).
+hipError_t launch_block_prescale(const void *x, int xt_bf16, const float *scales, int block_size, float *xs, int M,
+                                 int K, hipStream_t stream);
+hipError_t launch_fill(float *p, float v, size_t n, hipStream_t stream);
+// [H][E] router -> [E][H].
+hipError_t launch_router_transpose(const void *src, int rt_bf16, void *dst, int H, int E, hipStream_t stream);
+
 // MoE pipeline (frx_moe.hip).
 struct MoeWorkspace {
   uint32_t *idx;       // [T*k] selected experts (sorted order per token)
@@ -131,6 +146,6 @@ hipError_t launch_moe(const void *x, int xt_bf16, const void *router,
                       const float *const *s_down, int T, int H, int I, int E,
                       int top_k, int gelu, void *y, int yt_bf16,
                       uint32_t *topk_idx, float *topk_w, const MoeWorkspace &ws,
-                      hipStream_t stream);
+                      int routing, hipStream_t stream);
 
 }  // namespace frx

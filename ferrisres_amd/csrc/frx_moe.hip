@@ -120,10 +120,15 @@ static inline int router_chunk(int rows) {
 // descending sort of the reference; the two reductions (sum of exps in
 // expert order, sum of the top-k in sorted order) stay sequential on one
 // lane, as in the reference. logit: 4 * RT_NT floats of LDS.
+// by_logit (CpuMoELayer::top_k_select_with_probs, src/model/cpu_moe.rs:
+// 365-400): the experts are ranked by logit instead of probability and the
+// weights are exp(l_k - l_max) over the selected logits, divided by their
+// sum in rank order when it is positive.
 __device__ __forceinline__ void router_softmax_topk(float sum, float *logit, int tid, int e, int tl, int t,
                                                     int T, int E, int EP, int top_k,
                                                     uint32_t *__restrict__ idx_out, float *__restrict__ w_out,
-                                                    uint32_t *__restrict__ user_idx, float *__restrict__ user_w) {
+                                                    uint32_t *__restrict__ user_idx, float *__restrict__ user_w,
+                                                    int by_logit) {
   float *pbuf = logit + RT_NT;             // [RT_NT] probabilities
   float *tsum = pbuf + RT_NT;              // [RT_NT/EP] per-token sums
   int *order = reinterpret_cast<int *>(tsum + RT_NT);  // [RT_NT/EP][EP]
@@ -151,16 +156,34 @@ __device__ __forceinline__ void router_softmax_topk(float sum, float *logit, int
     // reference's sort_by(partial_cmp().unwrap_or(Equal)) keeps them. Within
     // a token the probabilities are either all NaN (a NaN or +inf logit
     // makes the exp sum NaN) or all ordered, so the ranks are a permutation
-    // of 0..E-1 in both cases and every slot below top_k is written.
+    // of 0..E-1 in both cases and every slot below top_k is written. Ranked
+    // by logit, a NaN logit ties with every expert; ties break by index.
     int rank = 0;
+    const float ve = by_logit ? lg[e] : pe;
     for (int j = 0; j < E; j++) {
-      const float pj = pbuf[tl * EP + j];
-      const bool tie = !(pj < pe) && !(pj > pe);
-      rank += (pj > pe) || (tie && j < e);
+      const float vj = by_logit ? lg[j] : pbuf[tl * EP + j];
+      const bool tie = !(vj < ve) && !(vj > ve);
+      rank += (vj > ve) || (tie && j < e);
+    }
+    if (by_logit) {
+      // a NaN among the logits makes the rank relation intransitive: fall
+      // back to index order for the whole token
+      bool any_nan = false;
+      for (int j = 0; j < E; j++) any_nan |= lg[j] != lg[j];
+      if (any_nan) rank = e;
     }
     if (rank < top_k) order[tl * EP + rank] = e;
   }
   __syncthreads();
+  if (by_logit) {
+    // weights: exp(l_k - l_max) over the top-k logits (rank order), as pbuf
+    if (live) {
+      int r = -1;
+      for (int i = 0; i < top_k; i++) r = order[tl * EP + i] == e ? i : r;
+      if (r >= 0) pbuf[tid] = (float)exp((double)__fsub_rn(lg[e], lg[order[tl * EP]]));
+    }
+    __syncthreads();
+  }
   if (e == 0 && t < T) {
     float ts = 0.0f;
     for (int i = 0; i < top_k; i++) ts = __fadd_rn(ts, pbuf[tl * EP + order[tl * EP + i]]);
@@ -170,7 +193,8 @@ __device__ __forceinline__ void router_softmax_topk(float sum, float *logit, int
   if (e < top_k && t < T) {
     const int oi = order[tl * EP + e];
     const int ei = (unsigned)oi < (unsigned)E ? oi : 0;  // the ranks above fill every slot; kept in range regardless
-    const float wi = __fdiv_rn(pbuf[tl * EP + ei], tsum[tl]);
+    const float ts = tsum[tl];
+    const float wi = (by_logit && !(ts > 0.0f)) ? pbuf[tl * EP + ei] : __fdiv_rn(pbuf[tl * EP + ei], ts);
     idx_out[t * top_k + e] = (uint32_t)ei;
     w_out[t * top_k + e] = wi;
     if (user_idx) user_idx[t * top_k + e] = (uint32_t)ei;
@@ -191,7 +215,7 @@ __global__ __launch_bounds__(RT_NT) void moe_router_kernel(
     const XT *__restrict__ x, const RT *__restrict__ router, int T, int H,
     int E, int EP, int top_k, int CH, uint32_t *__restrict__ idx_out,
     float *__restrict__ w_out, uint32_t *__restrict__ user_idx,
-    float *__restrict__ user_w) {
+    float *__restrict__ user_w, int by_logit) {
   const int RS = CH + 4;  // padded row stride (floats)
   extern __shared__ __align__(16) float rsm[];
   const int tid = threadIdx.x, e = tid % EP, tl = tid / EP;
@@ -371,7 +395,7 @@ __global__ __launch_bounds__(RT_NT) void moe_router_kernel(
     chunk(c + 1, r0, r1);
   }
   if (c < nch) chunk(c, r1, r0);
-  router_softmax_topk(sum, logit, tid, e, tl, t, T, E, EP, top_k, idx_out, w_out, user_idx, user_w);
+  router_softmax_topk(sum, logit, tid, e, tl, t, T, E, EP, top_k, idx_out, w_out, user_idx, user_w, by_logit);
 }
 
 // Resident variant for bf16 router weights when the block's data fits LDS
@@ -392,7 +416,7 @@ template <typename XT>
 __global__ __launch_bounds__(RT_NT) void moe_router_res_kernel(
     const XT *__restrict__ x, const uint16_t *__restrict__ router, int T, int H, int E, int EP,
     int top_k, int RSB, uint32_t *__restrict__ idx_out, float *__restrict__ w_out,
-    uint32_t *__restrict__ user_idx, float *__restrict__ user_w) {
+    uint32_t *__restrict__ user_idx, float *__restrict__ user_w, int by_logit) {
   extern __shared__ __align__(16) uint32_t smr[];
   const int tid = threadIdx.x, e = tid % EP, tl = tid / EP;
   const int TPB = RT_NT / EP;
@@ -517,7 +541,7 @@ __global__ __launch_bounds__(RT_NT) void moe_router_res_kernel(
       }
     }
   }
-  router_softmax_topk(sum, logit, tid, e, tl, t, T, E, EP, top_k, idx_out, w_out, user_idx, user_w);
+  router_softmax_topk(sum, logit, tid, e, tl, t, T, E, EP, top_k, idx_out, w_out, user_idx, user_w, by_logit);
 }
 
 // ---- 2. histogram / scan / stable scatter / tile schedule -----------------
@@ -820,13 +844,16 @@ template <typename YT>
 __global__ __launch_bounds__(256) void moe_combine_kernel(
     const float *__restrict__ dout, const float *__restrict__ dout_lo, const float *__restrict__ dout2,
     int A, const float *__restrict__ wts, const int *__restrict__ inv, int H, int top_k,
-    YT *__restrict__ y) {
+    YT *__restrict__ y, int skip_small) {
   const int t = blockIdx.x;
   for (int j = threadIdx.x * 4; j < H; j += 1024) {  // H % 16 == 0
     f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
     for (int k = 0; k < top_k; k++) {
 #pragma clang fp contract(off)
       const float w = wts[t * top_k + k];
+      // CpuMoELayer skips experts whose weight is below 1e-8 in magnitude
+      // (src/model/cpu_moe.rs:172)
+      if (skip_small && fabsf(w) < 1e-8f) continue;
       const long o = (long)inv[t * top_k + k] * H + j;
       f32x4 d = *reinterpret_cast<const f32x4 *>(dout + o);
       if (dout_lo) d = d + *reinterpret_cast<const f32x4 *>(dout_lo + o);
@@ -848,7 +875,7 @@ hipError_t launch_moe(const void *x, int xt_bf16, const void *router,
                       const float *const *s_down, int T, int H, int I, int E,
                       int top_k, int gelu, void *y, int yt_bf16,
                       uint32_t *topk_idx, float *topk_w, const MoeWorkspace &ws,
-                      hipStream_t stream) {
+                      int routing, hipStream_t stream) {
   const int A = T * top_k;
   // 1. router
   int EP = 1;
@@ -877,22 +904,22 @@ hipError_t launch_moe(const void *x, int xt_bf16, const void *router,
     const int rsb = router_res_row_bytes(H);
     if (xt_bf16)
       hipLaunchKernelGGL((moe_router_res_kernel<uint16_t>), rg, dim3(RT_NT), res_lds, stream, (const uint16_t *)x,
-                         (const uint16_t *)router, T, H, E, EP, top_k, rsb, ws.idx, ws.wts, topk_idx, topk_w);
+                         (const uint16_t *)router, T, H, E, EP, top_k, rsb, ws.idx, ws.wts, topk_idx, topk_w, routing);
     else
       hipLaunchKernelGGL((moe_router_res_kernel<float>), rg, dim3(RT_NT), res_lds, stream, (const float *)x,
-                         (const uint16_t *)router, T, H, E, EP, top_k, rsb, ws.idx, ws.wts, topk_idx, topk_w);
+                         (const uint16_t *)router, T, H, E, EP, top_k, rsb, ws.idx, ws.wts, topk_idx, topk_w, routing);
   } else if (xt_bf16 && rt_bf16)
     hipLaunchKernelGGL((moe_router_kernel<uint16_t, uint16_t>), rg, dim3(RT_NT), rlds, stream,
-                       (const uint16_t *)x, (const uint16_t *)router, T, H, E, EP, top_k, rch, ws.idx, ws.wts, topk_idx, topk_w);
+                       (const uint16_t *)x, (const uint16_t *)router, T, H, E, EP, top_k, rch, ws.idx, ws.wts, topk_idx, topk_w, routing);
   else if (xt_bf16)
     hipLaunchKernelGGL((moe_router_kernel<uint16_t, float>), rg, dim3(RT_NT), rlds, stream,
-                       (const uint16_t *)x, (const float *)router, T, H, E, EP, top_k, rch, ws.idx, ws.wts, topk_idx, topk_w);
+                       (const uint16_t *)x, (const float *)router, T, H, E, EP, top_k, rch, ws.idx, ws.wts, topk_idx, topk_w, routing);
   else if (rt_bf16)
     hipLaunchKernelGGL((moe_router_kernel<float, uint16_t>), rg, dim3(RT_NT), rlds, stream,
-                       (const float *)x, (const uint16_t *)router, T, H, E, EP, top_k, rch, ws.idx, ws.wts, topk_idx, topk_w);
+                       (const float *)x, (const uint16_t *)router, T, H, E, EP, top_k, rch, ws.idx, ws.wts, topk_idx, topk_w, routing);
   else
     hipLaunchKernelGGL((moe_router_kernel<float, float>), rg, dim3(RT_NT), rlds, stream,
-                       (const float *)x, (const float *)router, T, H, E, EP, top_k, rch, ws.idx, ws.wts, topk_idx, topk_w);
+                       (const float *)x, (const float *)router, T, H, E, EP, top_k, rch, ws.idx, ws.wts, topk_idx, topk_w, routing);
   hipError_t err = hipGetLastError();
   if (err != hipSuccess) return err;
   // 2. group
@@ -950,11 +977,11 @@ hipError_t launch_moe(const void *x, int xt_bf16, const void *router,
   if (yt_bf16)
     hipLaunchKernelGGL((moe_combine_kernel<uint16_t>), dim3(T), dim3(256), 0, stream, ws.dout,
                        engine2 ? ws.dout_lo : nullptr, down_split ? ws.dout2 : nullptr, A, ws.wts, ws.inv,
-                       H, top_k, (uint16_t *)y);
+                       H, top_k, (uint16_t *)y, routing);
   else
     hipLaunchKernelGGL((moe_combine_kernel<float>), dim3(T), dim3(256), 0, stream, ws.dout,
                        engine2 ? ws.dout_lo : nullptr, down_split ? ws.dout2 : nullptr, A, ws.wts, ws.inv,
-                       H, top_k, (float *)y);
+                       H, top_k, (float *)y, routing);
   return hipGetLastError();
 }
 

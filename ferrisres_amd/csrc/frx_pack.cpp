@@ -126,4 +126,31 @@ frx_status frx_sparse24_cpu_to_gpu(const uint8_t *patterns, const uint8_t *signs
   return FRX_OK;
 }
 
+// ternary_sparse_indices (src/model/ternary.rs:681-707) as CSR arrays: the
+// +1 and -1 columns of each row in column order; offsets only when the index
+// arrays are NULL.
+frx_status frx_ternary_sparse_indices(const int8_t *values, uint32_t N, uint32_t K, uint32_t *pos_off,
+                                      uint32_t *pos_idx, uint32_t *neg_off, uint32_t *neg_idx) {
+  if (!values || !pos_off || !neg_off) return FRX_ERR_SHAPE;
+  if ((size_t)N * K > 0xFFFFFFFFull) return FRX_ERR_SHAPE;
+  uint32_t np = 0, nn = 0;
+  for (size_t r = 0; r < N; r++) {
+    pos_off[r] = np;
+    neg_off[r] = nn;
+    const int8_t *row = values + r * K;
+    for (uint32_t j = 0; j < K; j++) {
+      if (row[j] == 1) {
+        if (pos_idx) pos_idx[np] = j;
+        np++;
+      } else if (row[j] == -1) {
+        if (neg_idx) neg_idx[nn] = j;
+        nn++;
+      }
+    }
+  }
+  pos_off[N] = np;
+  neg_off[N] = nn;
+  return FRX_OK;
+}
+
 }  // extern "C"

@@ -54,6 +54,12 @@ typedef enum frx_ffn_mode {
   FRX_FFN_TWO_LAUNCH = 2   /* gate/up/act launch + down launch */
 } frx_ffn_mode;
 
+/* Routing semantics of frx_moe_ternary_ffn (see frx_set_moe_routing). */
+typedef enum frx_moe_routing {
+  FRX_MOE_TERNARY_MOE_LAYER = 0, /* TernaryMoELayer and the GPU-path glue */
+  FRX_MOE_CPU_MOE_LAYER = 1      /* CpuMoELayer */
+} frx_moe_routing;
+
 /* ---- context -------------------------------------------------------------
  * Replaces the Arc<Device>/Arc<Queue> pair ops are built from
  * (TernaryMatMulOp::new, src/compute/kernels/ternary_matmul.rs:84-155).
@@ -86,6 +92,45 @@ frx_status frx_ternary_linear(frx_ctx *ctx, const uint32_t *w,
                               const float *scale, const void *x, frx_dtype xt,
                               void *y, frx_dtype yt, uint32_t M, uint32_t K,
                               uint32_t N);
+
+/* ---- dense ternary linear with column-block scales --------------------------
+ * Replaces ternary_matmul_blocked (src/model/ternary.rs:541-579): each block
+ * of block_size input columns has its own scale, shared by all rows, and
+ * there is no per-row scale:
+ *   y[m][n] = sum_b block_scales[b] * sum_{k in block b} dec(W[n][k]) x[m][k]
+ *   block_scales [ceil(K / block_size)] f32 (device). Same layouts and
+ * requirements as frx_ternary_linear. The activations are prescaled per
+ * element in fp32 (a context workspace of M*K*4 bytes, allocated on the
+ * first call at a larger size) and run through the dense kernels. */
+frx_status frx_ternary_linear_blocked(frx_ctx *ctx, const uint32_t *w,
+                                      const float *block_scales,
+                                      uint32_t block_size, const void *x,
+                                      frx_dtype xt, void *y, frx_dtype yt,
+                                      uint32_t M, uint32_t K, uint32_t N);
+
+/* ---- index-list decode -------------------------------------------------------
+ * Replaces ternary_matmul_sparse_decode (src/model/ternary.rs:647-673) with
+ * the lists of ternary_sparse_indices (:681-707) as CSR arrays (device):
+ * row r's +1 columns are pos_idx[pos_off[r] .. pos_off[r+1]), its -1 columns
+ * neg_idx[neg_off[r] .. neg_off[r+1]).
+ *   y[m][r] = scale * (sum_pos x[m][j] - sum_neg x[m][j])
+ * x [M][K] xt, y [M][N] yt; every index must be < K. */
+frx_status frx_ternary_sparse_decode(frx_ctx *ctx, const uint32_t *pos_off,
+                                     const uint32_t *pos_idx,
+                                     const uint32_t *neg_off,
+                                     const uint32_t *neg_idx, float scale,
+                                     const void *x, frx_dtype xt, void *y,
+                                     frx_dtype yt, uint32_t M, uint32_t K,
+                                     uint32_t N);
+
+/* ---- statistics of a packed matrix -------------------------------------------
+ * Replaces the counts of ternary_stats (src/model/ternary.rs:725-746) for a
+ * matrix already on the device in the dense layout [N][K/16] u32:
+ * counts[0] = number of -1 codes, counts[1] = zeros (codes 0b01 and 0b11),
+ * counts[2] = +1 codes (device array of 3 u64, stream-ordered). The ratios
+ * are counts / (N*K) and the compression ratio is 16, as in the reference. */
+frx_status frx_ternary_stats(frx_ctx *ctx, const uint32_t *w, uint32_t N,
+                             uint32_t K, unsigned long long *counts);
 
 /* ---- 2:4 sparse ternary linear ---------------------------------------------
  * Replaces SparseTernaryMatMulOp::dispatch (src/compute/kernels/
@@ -195,6 +240,22 @@ frx_status frx_ternary_ffn_noalloc(frx_ctx *ctx, const void *x, frx_dtype xt,
                                    uint32_t M, uint32_t H, uint32_t I,
                                    frx_activation act, void *y, frx_dtype yt);
 
+/* Selects the routing semantics of frx_moe_ternary_ffn on this context
+ * (default FRX_MOE_TERNARY_MOE_LAYER: router [E][H], softmax over all
+ * experts, stable top-k by probability, weights renormalised over the top-k;
+ * src/model/ternary_moe.rs:145-223). FRX_MOE_CPU_MOE_LAYER follows
+ * CpuMoELayer (src/model/cpu_moe.rs:146-201,365-400): the router is read as
+ * [H][E] (transposed into a context workspace of H*E elements on the device,
+ * allocated on the first call at a larger size), the top-k is ranked by
+ * logit (ties by index; a NaN logit puts the token's experts in index
+ * order), the weights are exp(l - l_max) over the selected logits divided by
+ * their sum, and experts whose weight is below 1e-8 in magnitude are
+ * skipped. The logits are sequential f32 dot products over H; the
+ * reference's matrixmultiply::sgemm sums in an order this library does not
+ * reproduce. CpuMoELayer's LoRA adapters (training-time) are not part of the
+ * call. */
+frx_status frx_set_moe_routing(frx_ctx *ctx, frx_moe_routing routing);
+
 /* Selects the execution of frx_ternary_ffn on this context (default
  * FRX_FFN_AUTO). No counterpart in the reference, whose FFN is three
  * separate matmul calls. */
@@ -261,6 +322,15 @@ frx_status frx_free(frx_ctx *ctx, void *dev_ptr);
 /* ---- host-side packers (no GPU) --------------------------------------------*/
 /* pack_ternary (src/model/ternary.rs:146-163): out has (n+3)/4 bytes. */
 frx_status frx_pack_ternary_u8(const int8_t *values, size_t n, uint8_t *out);
+/* ternary_sparse_indices (src/model/ternary.rs:681-707) as CSR arrays:
+ * values [N][K] i8; pos_off, neg_off [N + 1]; pos_idx, neg_idx receive the
+ * column indices of +1 and -1 entries in column order. With pos_idx and
+ * neg_idx NULL only the offsets are written (pos_off[N], neg_off[N] give
+ * the list lengths to allocate). */
+frx_status frx_ternary_sparse_indices(const int8_t *values, uint32_t N,
+                                      uint32_t K, uint32_t *pos_off,
+                                      uint32_t *pos_idx, uint32_t *neg_off,
+                                      uint32_t *neg_idx);
 /* unpack_ternary (src/model/ternary.rs:168-179). */
 frx_status frx_unpack_ternary_u8(const uint8_t *packed, size_t n, int8_t *out);
 /* pack_ternary_u32 (src/model/ternary.rs:1317-1328): n_values codes read from

@@ -48,6 +48,9 @@ def lib():
             "frxo_ternary_sparse_indices": (None, [_vp, _sz, _sz, _vp, _vp, _vp, _vp]),
             "frxo_ternary_matmul_sparse_decode": (None, [_vp, _vp, _vp, _vp, _f, _vp, _sz, _vp]),
             "frxo_ternary_stats": (_f, [_vp, _sz, _vp, _vp]),
+            "frxo_moe_route_cpu_layer": (None, [_vp, _vp, _sz, _sz, _sz, _sz, _vp, _vp]),
+            "frxo_moe_forward_routed": (None, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _sz, _sz, _sz, _sz,
+                                               ctypes.c_int, ctypes.c_int, _vp, _vp, _vp]),
             "frxo_bench_ternary_matmul": (None, [_vp, _vp, _f, _sz, _sz, _sz, _vp]),
             "frxo_quantize_ternary": (_f, [_vp, _sz, _vp]),
             "frxo_quantize_ste": (_f, [_vp, _sz, _vp]),
@@ -289,12 +292,26 @@ def moe_route(x, router, top_k):
     return idx, w, probs
 
 
-def moe_forward(x, router, w_gate, s_gate, w_up, s_up, w_down, s_down, top_k, gelu=False):
+def moe_route_cpu_layer(x, router_he, top_k):
+    """CpuMoELayer routing (cpu_moe.rs:146,365-400) with the router [H][E]."""
+    xx = _c(x, np.float32)
+    r = _c(router_he, np.float32)
+    T, H = xx.shape
+    E = r.shape[1]
+    idx = np.zeros((T, top_k), np.uint32)
+    w = np.zeros((T, top_k), np.float32)
+    lib().frxo_moe_route_cpu_layer(_p(xx), _p(r), T, H, E, top_k, _p(idx), _p(w))
+    return idx, w
+
+
+def moe_forward(x, router, w_gate, s_gate, w_up, s_up, w_down, s_down, top_k, gelu=False, routing=0):
     """Expert weights: lists of u32 [rows][cols/16] arrays and f32 scale arrays."""
     xx = _c(x, np.float32)
     r = _c(router, np.float32)
     T, H = xx.shape
-    E = r.shape[0]
+    E = len(w_gate)
+    if r.shape != ((H, E) if routing == 1 else (E, H)):
+        raise ValueError(f"router shape {r.shape} does not match H={H}, E={E}, routing={routing}")
     I = w_gate[0].shape[0]
     keep = [_c(a, np.uint32) for a in (*w_gate, *w_up, *w_down)] + \
            [_c(a, np.float32) for a in (*s_gate, *s_up, *s_down)]
@@ -306,8 +323,8 @@ def moe_forward(x, router, w_gate, s_gate, w_up, s_up, w_down, s_down, top_k, ge
     out = np.zeros((T, H), np.float32)
     idx = np.zeros((T, top_k), np.uint32)
     w = np.zeros((T, top_k), np.float32)
-    lib().frxo_moe_forward(_p(xx), _p(r), arr(wg), arr(sg), arr(wu), arr(su), arr(wd), arr(sd),
-                           T, H, I, E, top_k, int(gelu), _p(out), _p(idx), _p(w))
+    lib().frxo_moe_forward_routed(_p(xx), _p(r), arr(wg), arr(sg), arr(wu), arr(su), arr(wd), arr(sd),
+                                  T, H, I, E, top_k, int(gelu), int(routing), _p(out), _p(idx), _p(w))
     return out, idx, w
 
 

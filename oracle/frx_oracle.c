@@ -699,6 +699,57 @@ void frxo_moe_route(const float *x, const float *router, size_t tokens,
 }
 
 /*
+ * cpu_moe.rs:365-400 top_k_select_with_probs on logits computed as
+ * cpu_moe.rs:146 does, with the router read as [H][E]: l_e = sum_h x_h *
+ * R[h*E+e] (sequential in h; the reference's matrixmultiply::sgemm adds in
+ * its own blocked order, which is not restated), experts sorted by logit
+ * descending (stable, so ties keep index order), w_k = expf(l_k - l_max) for
+ * the top-k in rank order, divided by their sum when the sum is > 0. A NaN
+ * logit (a panic in the reference's unwrap) puts the token's experts in
+ * index order.
+ */
+void frxo_moe_route_cpu_layer(const float *x, const float *router_he, size_t tokens, size_t hidden,
+                              size_t experts, size_t top_k, uint32_t *topk_idx, float *topk_w) {
+  float *l = (float *)malloc(experts * sizeof(float));
+  size_t *order = (size_t *)malloc(experts * sizeof(size_t));
+  for (size_t t = 0; t < tokens; t++) {
+    const float *xr = x + t * hidden;
+    int any_nan = 0;
+    for (size_t e = 0; e < experts; e++) {
+      float dot = 0.0f;
+      for (size_t h = 0; h < hidden; h++) dot += xr[h] * router_he[h * experts + e];
+      l[e] = dot;
+      any_nan |= dot != dot;
+    }
+    for (size_t e = 0; e < experts; e++) order[e] = e;
+    if (!any_nan) {
+      for (size_t i = 1; i < experts; i++) {
+        size_t cur = order[i];
+        size_t j = i;
+        while (j > 0 && l[order[j - 1]] < l[cur]) {
+          order[j] = order[j - 1];
+          j--;
+        }
+        order[j] = cur;
+      }
+    }
+    const size_t k = top_k < experts ? top_k : experts;
+    const float max_l = l[order[0]];
+    float top_sum = 0.0f;
+    for (size_t i = 0; i < k; i++) {
+      const float ev = expf(l[order[i]] - max_l);
+      top_sum += ev;
+      topk_idx[t * top_k + i] = (uint32_t)order[i];
+      topk_w[t * top_k + i] = ev;
+    }
+    if (top_sum > 0.0f)
+      for (size_t i = 0; i < k; i++) topk_w[t * top_k + i] /= top_sum;
+  }
+  free(l);
+  free(order);
+}
+
+/*
  * MoE forward of the GPU-path glue, cpu_block_attn_res.rs:1148-1184, which is
  * TernaryMoELayer::forward (ternary_moe.rs:145-223) with per-row scales:
  * per token, route (above), then for each selected expert in sorted order:
@@ -709,6 +760,18 @@ void frxo_moe_route(const float *x, const float *router, size_t tokens,
  * and the reference's shape / non-zero / GeLU != SwiGLU tests
  * (ternary_moe.rs:311-443).
  */
+/* routing 0: TernaryMoELayer / GPU glue; 1: CpuMoELayer (router [H][E],
+ * frxo_moe_route_cpu_layer, experts with |w| < 1e-8 skipped as
+ * cpu_moe.rs:172 does). */
+void frxo_moe_forward_routed(const float *x, const float *router,
+                             const uint32_t *const *w_gate,
+                             const float *const *s_gate,
+                             const uint32_t *const *w_up, const float *const *s_up,
+                             const uint32_t *const *w_down,
+                             const float *const *s_down, size_t tokens, size_t hidden,
+                             size_t inter, size_t experts, size_t top_k, int use_gelu,
+                             int routing, float *out, uint32_t *topk_idx, float *topk_w);
+
 void frxo_moe_forward(const float *x, const float *router,
                       const uint32_t *const *w_gate,
                       const float *const *s_gate,
@@ -717,8 +780,22 @@ void frxo_moe_forward(const float *x, const float *router,
                       const float *const *s_down, size_t tokens, size_t hidden,
                       size_t inter, size_t experts, size_t top_k, int use_gelu,
                       float *out, uint32_t *topk_idx, float *topk_w) {
-  frxo_moe_route(x, router, tokens, hidden, experts, top_k, topk_idx, topk_w,
-                 NULL);
+  frxo_moe_forward_routed(x, router, w_gate, s_gate, w_up, s_up, w_down, s_down, tokens, hidden, inter, experts,
+                          top_k, use_gelu, 0, out, topk_idx, topk_w);
+}
+
+void frxo_moe_forward_routed(const float *x, const float *router,
+                             const uint32_t *const *w_gate,
+                             const float *const *s_gate,
+                             const uint32_t *const *w_up, const float *const *s_up,
+                             const uint32_t *const *w_down,
+                             const float *const *s_down, size_t tokens, size_t hidden,
+                             size_t inter, size_t experts, size_t top_k, int use_gelu,
+                             int routing, float *out, uint32_t *topk_idx, float *topk_w) {
+  if (routing == 1)
+    frxo_moe_route_cpu_layer(x, router, tokens, hidden, experts, top_k, topk_idx, topk_w);
+  else
+    frxo_moe_route(x, router, tokens, hidden, experts, top_k, topk_idx, topk_w, NULL);
   float *g = (float *)malloc(inter * sizeof(float));
   float *u = (float *)malloc(inter * sizeof(float));
   float *d = (float *)malloc(hidden * sizeof(float));
@@ -730,6 +807,7 @@ void frxo_moe_forward(const float *x, const float *router,
     for (size_t i = 0; i < k; i++) {
       uint32_t e = topk_idx[t * top_k + i];
       float w = topk_w[t * top_k + i];
+      if (routing == 1 && fabsf(w) < 1e-8f) continue;
       frxo_ternary_matmul_u32(w_gate[e], s_gate[e], xr, 1, hidden, inter, g);
       frxo_ternary_matmul_u32(w_up[e], s_up[e], xr, 1, hidden, inter, u);
       for (size_t j = 0; j < inter; j++) {

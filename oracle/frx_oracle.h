@@ -97,6 +97,16 @@ void frxo_sparse24_gpu_decode(const uint32_t *packed, size_t rows, size_t cols,
 void frxo_moe_route(const float *x, const float *router, size_t tokens,
                     size_t hidden, size_t experts, size_t top_k,
                     uint32_t *topk_idx, float *topk_w, float *probs_out);
+void frxo_moe_route_cpu_layer(const float *x, const float *router_he, size_t tokens, size_t hidden,
+                              size_t experts, size_t top_k, uint32_t *topk_idx, float *topk_w);
+void frxo_moe_forward_routed(const float *x, const float *router,
+                             const uint32_t *const *w_gate,
+                             const float *const *s_gate,
+                             const uint32_t *const *w_up, const float *const *s_up,
+                             const uint32_t *const *w_down,
+                             const float *const *s_down, size_t tokens, size_t hidden,
+                             size_t inter, size_t experts, size_t top_k, int use_gelu,
+                             int routing, float *out, uint32_t *topk_idx, float *topk_w);
 void frxo_moe_forward(const float *x, const float *router,
                       const uint32_t *const *w_gate,
                       const float *const *s_gate,

@@ -48,11 +48,11 @@ def run_gpu(ctx, xf, xb, rf, rb, ex, E, top_k, act, xt="bf16", yt="f32", rt=None
     return y, idx.cpu().numpy().astype(np.uint32), w.cpu().numpy()
 
 
-def run_oracle(xf, rf, ex, E, top_k, gelu, tokens=None):
+def run_oracle(xf, rf, ex, E, top_k, gelu, tokens=None, routing=0):
     x = xf if tokens is None else xf[tokens]
     g = lambda m, i: [ex[(m, e)][i] for e in range(E)]  # noqa: E731
     return oracle.moe_forward(x, rf, g("gate", 0), g("gate", 1), g("up", 0), g("up", 1), g("down", 0),
-                              g("down", 1), top_k, gelu)
+                              g("down", 1), top_k, gelu, routing=routing)
 
 
 @pytest.mark.parametrize("T,H,I,E,k", [(40, 128, 256, 8, 2), (7, 64, 96, 4, 1), (130, 256, 160, 16, 2),
@@ -148,3 +148,62 @@ def test_moe_nonfinite_tokens_route_like_the_reference(ctx):
     np.testing.assert_allclose(w[finite], rw[finite], rtol=0, atol=1e-6)
     ref, _, _ = run_oracle(xf, rf, ex, E, k, False, tokens=np.array(finite))
     assert_close_f32(host(y)[finite], ref)
+
+
+@pytest.mark.parametrize("T,H,I,E,k,xt", [(40, 128, 256, 8, 2, "bf16"), (33, 192, 128, 5, 3, "f32"),
+                                          (7, 64, 96, 4, 4, "bf16")])
+def test_moe_cpu_moe_layer_routing(ctx, T, H, I, E, k, xt):
+    """CpuMoELayer semantics (cpu_moe.rs:146-201, 365-400): router read as
+    [H, E], experts ranked by logit, weights exp(l - l_max) over the top k.
+    The router's values are the same as the [E, H] layer's, transposed."""
+    name = f"moe/cpu/{T}x{H}x{I}x{E}"
+    xf, xb, rf, rb, ex = make_moe(name, T, H, I, E)
+    rf_he = np.ascontiguousarray(rf.T)
+    rb_he = np.ascontiguousarray(rb.T) if rb is not None else None
+    if xt == "f32":
+        xf = synth.normal(77, T * H).reshape(T, H)
+    ctx.set_moe_routing(frx.MOE_CPU_MOE_LAYER)
+    try:
+        y, idx, w = run_gpu(ctx, xf, xb, rf_he, rb_he, ex, E, k, frx.ACT_SILU, xt=xt)
+    finally:
+        ctx.set_moe_routing(frx.MOE_TERNARY_MOE_LAYER)
+    ref, ridx, rw = run_oracle(xf, rf_he, ex, E, k, False, routing=1)
+    np.testing.assert_array_equal(idx, ridx)
+    np.testing.assert_allclose(w, rw, rtol=0, atol=1e-6)
+    assert_close_f32(host(y), ref)
+
+
+def test_moe_cpu_moe_layer_underflow_ranking_and_skip(ctx):
+    """Logits far apart: the runner-up weight underflows below 1e-8 and is
+    skipped, so the second expert's NaN down scale never reaches the output;
+    the experts whose probabilities underflow to 0 are still ranked by
+    logit. The [E, H] routing, by contrast, adds the NaN expert."""
+    T, H, I, E, k = 4, 64, 64, 3, 3
+    xf, xb, rf, rb, ex = make_moe("moe/cpu/skip", T, H, I, E)
+    xf = np.zeros((T, H), np.float32)
+    xf[:, 0] = 1.0
+    r_he = np.zeros((H, E), np.float32)
+    r_he[0] = [0.0, -150.0, -120.0]
+    ex = dict(ex)
+    ex[("down", 1)] = (ex[("down", 1)][0], np.full(H, np.nan, np.float32))
+    ctx.set_moe_routing(frx.MOE_CPU_MOE_LAYER)
+    try:
+        y, idx, w = run_gpu(ctx, xf, None, r_he, None, ex, E, k, frx.ACT_SILU, xt="f32", rt="f32")
+    finally:
+        ctx.set_moe_routing(frx.MOE_TERNARY_MOE_LAYER)
+    ref, ridx, rw = run_oracle(xf, r_he, ex, E, k, False, routing=1)
+    assert (ridx == np.array([0, 2, 1], np.uint32)).all()
+    np.testing.assert_array_equal(idx, ridx)
+    np.testing.assert_array_equal(w, rw)
+    assert np.isfinite(host(y)).all()
+    assert_close_f32(host(y), ref)
+    y0, idx0, _ = run_gpu(ctx, xf, None, np.ascontiguousarray(r_he.T), None, ex, E, k, frx.ACT_SILU, xt="f32",
+                          rt="f32")
+    assert list(idx0[0]) == [0, 1, 2]
+    assert not np.isfinite(host(y0)).all()
+
+
+def test_moe_routing_mode_rejects_unknown(ctx):
+    with pytest.raises(frx.FrxError) as e:
+        ctx.set_moe_routing(7)
+    assert e.value.kind == "Unsupported"

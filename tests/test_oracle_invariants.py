@@ -275,6 +275,87 @@ def test_moe_route_nonfinite_tokens_and_gpu_rank_rule():
     assert _gpu_rank_rule(nan_row, k) is not None
 
 
+def _cpu_layer_route_f64(x, r_he, k):
+    """CpuMoELayer ranking (cpu_moe.rs:365-400) in float64: experts sorted
+    by logit (stable), weights exp(l - l_max) over the top k, normalised."""
+    logits = x.astype(np.float64) @ r_he.astype(np.float64)
+    idx = np.argsort(-logits, axis=1, kind="stable")[:, :k]
+    top = np.take_along_axis(logits, idx, 1)
+    w = np.exp(top - top[:, :1])
+    return idx, w / w.sum(1, keepdims=True)
+
+
+def test_moe_route_cpu_layer_vs_bruteforce():
+    rng = np.random.default_rng(41)
+    x = rng.standard_normal((64, 32)).astype(np.float32)
+    r = (rng.standard_normal((32, 7)) * 0.5).astype(np.float32)  # [H][E]
+    idx, w = oracle.moe_route_cpu_layer(x, r, 3)
+    i2, w2 = _cpu_layer_route_f64(x, r, 3)
+    np.testing.assert_array_equal(idx, i2)
+    np.testing.assert_allclose(w, w2, atol=1e-6)
+    # on distinct probabilities the softmax router over the transposed matrix
+    # ranks the same way and its renormalised top-k probabilities are the
+    # same weights, up to rounding
+    i3, w3, _ = oracle.moe_route(x, np.ascontiguousarray(r.T), 3)
+    np.testing.assert_array_equal(idx, i3)
+    np.testing.assert_allclose(w, w3, atol=1e-6)
+
+
+def test_moe_route_cpu_layer_ranks_underflowed_probabilities_by_logit():
+    # logits 0, -150, -120: both small probabilities underflow to 0, so the
+    # softmax router ties them (index order) while CpuMoELayer ranks by logit
+    x = np.ones((1, 1), np.float32)
+    r = np.array([[0.0, -150.0, -120.0]], np.float32)  # [H=1][E=3]
+    idx, w = oracle.moe_route_cpu_layer(x, r, 3)
+    i3, _, _ = oracle.moe_route(x, np.ascontiguousarray(r.T), 3)
+    assert list(idx[0]) == [0, 2, 1]
+    assert list(i3[0]) == [0, 1, 2]
+    assert list(w[0]) == [1.0, 0.0, 0.0]
+
+
+def test_moe_route_cpu_layer_ties_and_nan():
+    # ties keep the lower index (a stable sort); a NaN logit puts the token's
+    # experts in index order
+    x = np.ones((2, 4), np.float32)
+    x[1, 2] = np.nan
+    r = np.array([[0.25, 0.5, 0.5, 0.25]] * 4, np.float32)  # [H][E]: logits 1, 2, 2, 1
+    idx, w = oracle.moe_route_cpu_layer(x, r, 3)
+    assert list(idx[0]) == [1, 2, 0]
+    np.testing.assert_allclose(w[0], np.array([1, 1, np.exp(-1)]) / (2 + np.exp(-1)), rtol=1e-6)
+    assert list(idx[1]) == [0, 1, 2]
+
+
+def test_moe_forward_cpu_layer_skips_negligible_experts():
+    """cpu_moe.rs:172: an expert whose weight is below 1e-8 is skipped, so a
+    NaN produced by that expert alone does not reach the output."""
+    rng = np.random.default_rng(43)
+    T, H, I, E, k = 3, 16, 32, 3, 2
+    x = rng.standard_normal((T, H)).astype(np.float32)
+    r = np.zeros((H, E), np.float32)
+    r[0, 0] = 40.0 / x[:, 0].max()  # expert 0 dominates by more than ln(1e8) for token argmax
+    t_dom = int(np.argmax(x[:, 0]))
+    mk = lambda n, kk: rng.integers(-1, 2, size=(n, kk)).astype(np.int8)  # noqa: E731
+    wg = [mk(I, H) for _ in range(E)]
+    wu = [mk(I, H) for _ in range(E)]
+    wd = [mk(H, I) for _ in range(E)]
+    pk = lambda m: oracle.pack_rows_u32(m)  # noqa: E731
+    sg = [np.full(I, 0.5, np.float32) for _ in range(E)]
+    su = [np.full(I, 0.25, np.float32) for _ in range(E)]
+    sd = [np.full(H, 0.125, np.float32) for _ in range(E)]
+    # a NaN down scale on experts 1 and 2: their output is NaN everywhere
+    sd[1][:] = np.nan
+    sd[2][:] = np.nan
+    out, idx, w = oracle.moe_forward(x, r, [pk(m) for m in wg], sg, [pk(m) for m in wu], su,
+                                     [pk(m) for m in wd], sd, k, routing=1)
+    assert idx[t_dom, 0] == 0 and w[t_dom, 1] < 1e-8
+    assert np.isfinite(out[t_dom]).all()
+    assert not np.isfinite(out).all()  # the other tokens use the NaN experts
+    # the default (GPU-path glue) routing adds every selected expert
+    out0, _, _ = oracle.moe_forward(x, np.ascontiguousarray(r.T), [pk(m) for m in wg], sg,
+                                    [pk(m) for m in wu], su, [pk(m) for m in wd], sd, k)
+    assert not np.isfinite(out0[t_dom]).all()
+
+
 def _moe_f64(x, r, wg, sg, wu, su, wd, sd, k, gelu):
     idx, w = _softmax_route_f64(x, r, k)
     out = np.zeros((x.shape[0], x.shape[1]))

@@ -1,4 +1,6 @@
 """Host packers of libfrx_ternary.so (no GPU) — bit-exact with the oracle."""
+import os
+
 import numpy as np
 import pytest
 
@@ -83,3 +85,20 @@ def test_sparse24_transcoder_patterns_6_7_follow_to_ternary():
     meta = frx.sparse24_cpu_to_gpu(p, s, rows, cols)
     np.testing.assert_array_equal(oracle.sparse24_gpu_decode(meta, rows, cols).ravel(),
                                   oracle.sparse24_cpu_to_ternary(p, s, rows, cols))
+
+
+def test_sparse_indices_host_equals_oracle():
+    """frx_ternary_sparse_indices (ternary_sparse_indices, ternary.rs:681-707)
+    equals the oracle's CSR lists, the reference KAT included."""
+    import json
+    kats = json.load(open(os.path.join(os.path.dirname(__file__), "golden", "reference_kats.json")))
+    kat = kats["sparse_indices_counts"]
+    po, pi, no, ni = frx.ternary_sparse_indices(np.array(kat["ternary"], np.int8).reshape(kat["rows"], kat["cols"]))
+    for r in range(kat["rows"]):
+        assert list(pi[po[r]:po[r + 1]]) == kat["pos"][r]
+        assert list(ni[no[r]:no[r + 1]]) == kat["neg"][r]
+    t = np.random.default_rng(3).integers(-1, 2, size=(57, 130)).astype(np.int8)
+    a = frx.ternary_sparse_indices(t)
+    b = oracle.ternary_sparse_indices(t, 57, 130)
+    for x, y in zip(a, b):
+        np.testing.assert_array_equal(x[:len(y)], y)
