@@ -206,7 +206,7 @@ def main():
     roofline = {
         "kernel": "frx::gemv_rows_kernel (B=1, linear, bf16 in, bf16 out)" if B == 1 else
                   "frx::gemv_rows4_kernel" if 2 <= B <= 4 else "frx::gemv_kernel (staged)" if B < 8 else
-                  "frx::gemv_direct_kernel / gemv_tall_kernel",
+                  "frx::gemv_xs_kernel",
         "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
         "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
         "avg_us": {"11008x4096": round(t_gu * 1e6, 3), "4096x11008": round(t_dn * 1e6, 3)},
@@ -260,7 +260,7 @@ def main():
     fused["default"]["kernels"] = (
         "gemv_rows_kernel gate/up/SiLU -> h planes, gemv_rows_kernel down over both planes" if B == 1 else
         "gemv_rows4_kernel gate/up/SiLU -> h planes, gemv_rows4_kernel down over both planes" if B == 2 else
-        "ffn1_kernel" if B == 3 else "GLU + down GEMV (planes at B >= 8)")
+        "ffn1_kernel" if B == 3 else "GLU + down GEMV (planes at B >= 4)")
     fused["two_launch"]["launches_per_step"] = 2
     if "one_launch" in fused:
         fused["one_launch"].update({"launches_per_step": 1, "kernels": "ffn1_kernel"})

@@ -1002,6 +1002,184 @@ static hipError_t launch_gemv_rows_stream(const uint32_t *w, const float *scale,
   return hipGetLastError();
 }
 
+// ---- 8 to 16 bf16 tokens: activations staged per wave ---------------------
+//
+// One workgroup per CU owns a contiguous range of rows (T tiles of 16 rows x
+// 16 tokens, the M and N sides of v_mfma_f32_16x16x32_bf16) and its waves
+// split K into ranges of whole quads (256 columns). A wave stages the x of
+// its current quad, all 16 tokens, in its own 8 KB of LDS and computes every
+// tile of the workgroup from it, so each CU reads x once and each weight
+// word is decoded once. Measured against the per-lane operand loads of
+// gemv_direct_kernel / gemv_tall_kernel at B = 16: 12.3 -> 7.5 us
+// (11008x4096) and 13.3 -> 9.5 us (4096x11008) per launch.
+//  - Staging: load instruction ii of a quad reads tokens 2ii and 2ii+1, 512
+//    contiguous bytes each (whole 128-byte lines; the per-lane 32-byte
+//    operand loads touched 16 half-used lines per instruction and ran the
+//    L2 -> L1 path at half its line rate).
+//  - LDS layout: 16-byte slot ((m*2 + h)*64 + g*16 + (t ^ (2g + h))) holds
+//    x[t][256Q + 64m + 16g + 8h .. +7]. The XOR spreads both the staging
+//    writes (eight consecutive pieces of one token) and the operand reads
+//    (eight consecutive tokens of one piece) over distinct bank groups.
+//  - Weights: lane (r, g) loads 16 bytes (words 4g..4g+3 of the quad) of row
+//    r of each tile, and the 4x4 word transpose of gemv_direct_kernel gives
+//    it words g, g+4, g+8, g+12; step m multiplies word 4m + g against the
+//    slots (m, h = 0 / 1) of token t = lane % 16.
+//  - Tokens >= B and columns >= K are staged as zeros (buffer loads past the
+//    range), rows past the workgroup's range read zero words; the waves'
+//    partial tiles are added in wave order through LDS (deterministic).
+constexpr int XS_QUAD_BYTES = 8192;
+
+template <typename YT, int WAVES, int T, int UMAX>
+__global__ __launch_bounds__(WAVES * 64) void gemv_xs_kernel(const uint32_t *__restrict__ W,
+                                                             const float *__restrict__ scale,
+                                                             const uint16_t *__restrict__ X, YT *__restrict__ Y,
+                                                             int B, int K, int N) {
+  extern __shared__ __align__(16) uint32_t lds[];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int r = lane & 15, g = lane >> 4;
+  const int b0 = (int)((long long)blockIdx.x * N / gridDim.x);
+  const int b1 = (int)((long long)(blockIdx.x + 1) * N / gridDim.x);
+  const int wpr = K >> 4;
+  const int nq = (K + 255) >> 8;
+  const int qa = (wave * nq) / WAVES, qb = ((wave + 1) * nq) / WAVES;
+  uint8_t *xl = reinterpret_cast<uint8_t *>(lds) + wave * XS_QUAD_BYTES;
+  const __amdgpu_buffer_rsrc_t xr = buffer_rsrc(X, (uint32_t)B * (uint32_t)K * 2u);
+  const __amdgpu_buffer_rsrc_t wr = buffer_rsrc(W, (uint32_t)N * (uint32_t)wpr * 4u);
+  constexpr uint32_t OOB = 0x80000000u;  // a buffer offset past any range this path takes
+  const int st = lane >> 5, sp = lane & 31;  // staging: token of the pair, 16-byte piece
+  const int sm = sp >> 3, sg = (sp >> 1) & 3, sh = sp & 1;
+  auto xload = [&](int q, u32x4(&xs)[8]) {
+#pragma unroll
+    for (int ii = 0; ii < 8; ii++) {
+      const int t = 2 * ii + st, col = 256 * q + 8 * sp;
+      const uint32_t off =
+          (q < qb && t < B && col < K) ? ((uint32_t)t * (uint32_t)K + (uint32_t)col) * 2u : OOB;
+      xs[ii] = __builtin_amdgcn_raw_buffer_load_b128(xr, off, 0, 0);
+    }
+  };
+  u32x4 xs[8];
+  xload(qa, xs);  // first, so that it does not wait behind the weights
+  u32x4 wv[T][UMAX];
+#pragma unroll
+  for (int tt = 0; tt < T; tt++)
+#pragma unroll
+    for (int u = 0; u < UMAX; u++) {
+      const int row = b0 + 16 * tt + r, q = qa + u, wi = 16 * q + 4 * g;
+      const uint32_t off =
+          (row < b1 && q < qb && wi < wpr) ? ((uint32_t)row * (uint32_t)wpr + (uint32_t)wi) * 4u : OOB;
+      wv[tt][u] = __builtin_amdgcn_raw_buffer_load_b128(wr, off, 0, 0);
+    }
+  f32x4 acc[T];
+#pragma unroll
+  for (int tt = 0; tt < T; tt++) acc[tt] = (f32x4){0.f, 0.f, 0.f, 0.f};
+  const int t = lane & 15;
+#pragma unroll
+  for (int u = 0; u < UMAX; u++) {
+    if (qa + u >= qb) break;  // wave-uniform
+    // the wave's own LDS area: its reads of the previous quad precede these
+    // writes in the wave's LDS order
+#pragma unroll
+    for (int ii = 0; ii < 8; ii++) {
+      const int ts = 2 * ii + st;
+      *reinterpret_cast<u32x4 *>(xl + ((sm * 2 + sh) * 64 + sg * 16 + (ts ^ (2 * sg + sh))) * 16) = xs[ii];
+    }
+    if (u + 1 < UMAX) xload(qa + u + 1, xs);
+#pragma unroll
+    for (int tt = 0; tt < T; tt++) {
+      u32x4 &v = wv[tt][u];
+      const auto p02 = __builtin_amdgcn_permlane32_swap(v.x, v.z, false, false);
+      const auto p13 = __builtin_amdgcn_permlane32_swap(v.y, v.w, false, false);
+      const auto p01 = __builtin_amdgcn_permlane16_swap(p02[0], p13[0], false, false);
+      const auto p23 = __builtin_amdgcn_permlane16_swap(p02[1], p13[1], false, false);
+      v = (u32x4){p01[0], p01[1], p23[0], p23[1]};
+    }
+#pragma unroll
+    for (int m = 0; m < 4; m++) {
+      const u32x4 x0 = *reinterpret_cast<const u32x4 *>(xl + ((m * 2) * 64 + g * 16 + (t ^ (2 * g))) * 16);
+      const u32x4 x1 = *reinterpret_cast<const u32x4 *>(xl + ((m * 2 + 1) * 64 + g * 16 + (t ^ (2 * g + 1))) * 16);
+#pragma unroll
+      for (int tt = 0; tt < T; tt++) {
+        const uint32_t wq = m == 0 ? wv[tt][u].x : m == 1 ? wv[tt][u].y : m == 2 ? wv[tt][u].z : wv[tt][u].w;
+        u32x4 a0, a1;
+        unpack16_nat(wq, a0, a1);
+        acc[tt] = mfma16(a0, x0, acc[tt]);
+        acc[tt] = mfma16(a1, x1, acc[tt]);
+      }
+    }
+  }
+  // Partial tiles, added in wave order; wave tt finishes tile tt.
+  __syncthreads();
+  f32x4 *red = reinterpret_cast<f32x4 *>(lds);
+#pragma unroll
+  for (int tt = 0; tt < T; tt++) red[(tt * WAVES + wave) * 64 + lane] = acc[tt];
+  __syncthreads();
+  if (wave < T) {
+    const int tt = wave;
+    f32x4 s = red[tt * WAVES * 64 + lane];
+    for (int w = 1; w < WAVES; w++) s += red[(tt * WAVES + w) * 64 + lane];
+    const int n_out = b0 + 16 * tt + 4 * g;  // rows 4g..4g+3 of token t
+    if (t < B && n_out < b1) {
+      const int nok = min(4, b1 - n_out);
+      const f32x4 sc = {scale[n_out], nok > 1 ? scale[n_out + 1] : 0.f, nok > 2 ? scale[n_out + 2] : 0.f,
+                        nok > 3 ? scale[n_out + 3] : 0.f};
+      YStore<YT>::store4(Y + (size_t)t * N + n_out, s * sc * 0.5f, nok);  // 0.5: the 2*dec(c) encoding
+    }
+  }
+}
+
+template <typename YT, int WAVES, int T, int UMAX>
+static hipError_t launch_gemv_xs_w(const uint32_t *w, const float *scale, const void *x, void *y, int B, int K,
+                                   int N, int G, hipStream_t stream) {
+  static_assert(T * 1024 <= XS_QUAD_BYTES, "the partial tiles reuse the staging area");
+  const size_t lds = (size_t)WAVES * XS_QUAD_BYTES;
+  if (lds > 64 * 1024) {
+    static std::atomic<uint64_t> done;
+    const hipError_t e =
+        opt_in_lds(reinterpret_cast<const void *>(&gemv_xs_kernel<YT, WAVES, T, UMAX>), (int)lds, done);
+    if (e != hipSuccess) return e;
+  }
+  hipLaunchKernelGGL((gemv_xs_kernel<YT, WAVES, T, UMAX>), dim3(G), dim3(WAVES * 64), lds, stream, w, scale,
+                     reinterpret_cast<const uint16_t *>(x), reinterpret_cast<YT *>(y), B, K, N);
+  return hipGetLastError();
+}
+
+// Shapes gemv_xs_kernel takes: K up to 64 quads (16384), 16-byte aligned x.
+static bool gemv_xs_ok(const void *x, int B, int K) {
+  return B >= 1 && B <= 16 && K <= 64 * 256 && (reinterpret_cast<uintptr_t>(x) & 15) == 0;
+}
+
+// Grid: one workgroup per CU, fewer where that would leave tiles of fewer
+// than 16 rows, more where a workgroup would hold more than TMAX tiles.
+// Waves: 16 (one quad each up to K = 4096, two up to 8192), 12 with up to
+// four quads (K <= 12288; measured 9.5 us against 10.0 us with 16 waves of
+// three quads at 4096x11008, B = 16), else 16 waves of four.
+template <typename YT>
+static hipError_t launch_gemv_xs(const uint32_t *w, const float *scale, const void *x, void *y, int B, int K, int N,
+                                 hipStream_t stream) {
+  const int nq = (K + 255) / 256;
+  const int tmax = nq <= 32 ? 4 : 2;  // tiles per workgroup (weight registers: tiles x quads per wave)
+  int G = std::min(device_cu_count(), (N + 15) / 16);
+  if ((N + G - 1) / G > 16 * tmax) G = (N + 16 * tmax - 1) / (16 * tmax);
+  const int tiles = ((N + G - 1) / G + 15) / 16;
+#define FRX_XS(WV, TT, UM) return launch_gemv_xs_w<YT, WV, TT, UM>(w, scale, x, y, B, K, N, G, stream)
+#define FRX_XS_T(WV, UM)   \
+  if (tiles <= 1) FRX_XS(WV, 1, UM); \
+  if (tiles <= 2) FRX_XS(WV, 2, UM); \
+  if (tiles <= 3) FRX_XS(WV, 3, UM); \
+  FRX_XS(WV, 4, UM)
+  if (nq <= 16) { FRX_XS_T(16, 1); }
+  if (nq <= 32) { FRX_XS_T(16, 2); }
+  if (nq <= 48) {
+    if (tiles <= 1) FRX_XS(12, 1, 4);
+    FRX_XS(12, 2, 4);
+  }
+  if (tiles <= 1) FRX_XS(16, 1, 4);
+  FRX_XS(16, 2, 4);
+#undef FRX_XS_T
+#undef FRX_XS
+}
+
 // ---- two to four bf16 tokens: four rows x four segments per MFMA ----------
 //
 // The same diagonal idea with the 16 MFMA rows as 4 rows x 4 segments and
@@ -1328,6 +1506,10 @@ hipError_t launch_gemv(const uint32_t *w, const float *scale, const void *x,
   if (xt_bf16 && gemv_rows4_ok(w, x, B, K)) {
     if (yt_bf16) return launch_gemv_rows4<uint16_t>(w, scale, x, y, B, K, N, stream);
     return launch_gemv_rows4<float>(w, scale, x, y, B, K, N, stream);
+  }
+  if (xt_bf16 && B >= GEMV_DIRECT_MIN_B && gemv_xs_ok(x, B, K)) {
+    if (yt_bf16) return launch_gemv_xs<uint16_t>(w, scale, x, y, B, K, N, stream);
+    return launch_gemv_xs<float>(w, scale, x, y, B, K, N, stream);
   }
   if (xt_bf16 && B >= GEMV_DIRECT_MIN_B) {
     // taller tiles where their grid still covers every CU

@@ -147,6 +147,32 @@ def test_two_to_four_tokens_bit_exact_on_dyadic_inputs(ctx, M, K, N):
     np.testing.assert_array_equal(y, ref)
 
 
+@pytest.mark.parametrize("M,K,N", [(8, 16, 5), (11, 272, 17), (16, 4112, 700), (13, 8208, 33), (16, 12288, 1100),
+                                   (9, 16384, 40), (16, 4096, 16400), (16, 11008, 9000)])
+@pytest.mark.parametrize("yt", ["f32", "bf16"])
+def test_eight_to_sixteen_tokens_staged(ctx, M, K, N, yt):
+    """8 <= B <= 16 bf16 tokens through the per-wave staged activations: K
+    from one word to 64 quads (partial last quads), N below one tile, ragged
+    last tiles, more than 64 rows per CU (extra workgroups), and the
+    two-tile limit above 32 quads."""
+    name = f"xs/{M}x{K}x{N}"
+    t, w, s, xf, xb = _case(name, M, K, N)
+    ref = oracle.ternary_matmul_u32(w, s, xf, M, K, N)
+    y = _run(ctx, w, s, xf, xb, "bf16", yt)
+    if yt == "f32":
+        assert_close_f32(host(y), ref)
+    else:
+        assert_bf16_within_1ulp(y.view(torch.int16).cpu().numpy().view(np.uint16), ref)
+
+
+@pytest.mark.parametrize("M,K,N", [(16, 4096, 11008), (12, 12352, 300), (8, 2048, 64)])
+def test_eight_to_sixteen_tokens_bit_exact_on_dyadic_inputs(ctx, M, K, N):
+    t, w, s, x, xb = _dyadic_case(M, K, N, M * K + N + 1)
+    ref = (x @ t.T.astype(np.float32)) * s[None, :]
+    y = host(_run(ctx, w, s, x, xb, "bf16", "f32"))
+    np.testing.assert_array_equal(y, ref)
+
+
 def test_single_token_unaligned_weights(ctx):
     """Packed weights 4 bytes past a 16-byte boundary take the 16-row tiles
     (dword loads); both placements match the oracle."""
