@@ -149,8 +149,13 @@ def main():
             return None
 
     def timed(fn):
-        """Seconds for fn() run from a captured graph (or eagerly)."""
+        """Seconds for fn() run from a captured graph (or eagerly). The graph
+        is replayed once untimed first, so the timed replay does not include
+        its one-time upload."""
         gr = capture(fn)
+        torch.cuda.synchronize()
+        with torch.cuda.stream(stream):
+            (gr.replay() if gr is not None else fn())
         torch.cuda.synchronize()
         t0 = time.perf_counter()
         with torch.cuda.stream(stream):
@@ -329,11 +334,32 @@ def main():
                 "avg_us": {"11008x4096": round(tgu_x * 1e6, 3), "4096x11008": round(tdn_x * 1e6, 3)},
                 "launch_time_distribution": dist_x,
                 "kernel": "frx::gemv_rows4_kernel" if bx <= 4 else "frx::gemv_kernel (staged)" if bx < 8
-                else "frx::gemv_tall_kernel (11008x4096) / gemv_direct_kernel (4096x11008)",
+                else "frx::gemv_xs_kernel",
             }
             log(f"bench: decode GEMV B={bx}: {batches[f'B{bx}']['us_per_step']} us/step, "
                 f"{batches[f'B{bx}']['gb_s']} GB/s; frx_ternary_ffn {batches[f'B{bx}']['decode_ffn_us_per_step']} us")
         extra["decode_gemv_llama7b_batches"] = batches
+        # The literal drop-in: TernaryMatMulOp::dispatch and
+        # gpu_ternary_matmul_vram hand over f32 activations and take f32
+        # outputs. Per-launch times at the decode shapes, f32 in / f32 out.
+        f32res = {}
+        for bx in (1, 4, 16):
+            xf32 = torch.randn((bx, H), dtype=torch.float32, device=dev)
+            hf32 = torch.randn((bx, I), dtype=torch.float32, device=dev)
+            yg = torch.empty((bx, I), dtype=torch.float32, device=dev)
+            yd = torch.empty((bx, H), dtype=torch.float32, device=dev)
+            with torch.cuda.stream(stream):
+                ctx.ternary_linear(W[0][0], s_g, xf32, yg)
+                ctx.ternary_linear(W[0][2], s_d, hf32, yd)
+            torch.cuda.synchronize()
+            t1 = per_launch(lambda i, xf32=xf32, yg=yg: ctx.ternary_linear(W[i][0], s_g, xf32, yg), 1, reps)
+            t2 = per_launch(lambda i, hf32=hf32, yd=yd: ctx.ternary_linear(W[i][2], s_d, hf32, yd), 1, reps)
+            f32res[f"B{bx}"] = {
+                "avg_us": {"11008x4096": round(t1 * 1e6, 3), "4096x11008": round(t2 * 1e6, 3)},
+                "gb_s": {"11008x4096": round(gemv_bytes(I, H, bx, 4, 4) / t1 / 1e9, 1),
+                         "4096x11008": round(gemv_bytes(H, I, bx, 4, 4) / t2 / 1e9, 1)}}
+            log(f"bench: f32 in/out B={bx}: {t1 * 1e6:.2f} / {t2 * 1e6:.2f} us per launch")
+        extra["decode_gemv_f32_in_out"] = f32res
     if B == 1 and not args.no_extra:
         extra["decode_gemv_b1_by_weight_size"] = gemv_size_sweep(torch, ctx, stream, dev)
     if not args.no_extra:

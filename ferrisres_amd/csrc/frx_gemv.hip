@@ -1027,13 +1027,26 @@ static hipError_t launch_gemv_rows_stream(const uint32_t *w, const float *scale,
 //  - Tokens >= B and columns >= K are staged as zeros (buffer loads past the
 //    range), rows past the workgroup's range read zero words; the waves'
 //    partial tiles are added in wave order through LDS (deterministic).
-constexpr int XS_QUAD_BYTES = 8192;
+//  - Activation sources (XS): one bf16 plane, or two bf16 planes whose sum
+//    is the fp32 activation (hi, lo: the decode FFN's intermediate). Two
+//    planes take 16 KB per wave and quad and two MFMAs per operand. (fp32
+//    activations split into such planes at staging were measured slower
+//    than gemv_kernel<float>: every CU splits all of x, 8 VALU ops a value.)
+//  - NW = 2 (EPI = GEMV_SWIGLU / GEMV_GEGLU): the gate (W) and up (W2)
+//    tiles of the same rows against the same staged x; h = act(g) * u, as
+//    fp32 or (YSPLIT) as bf16 hi/lo planes Y = [2][B][N].
+constexpr int XS_QUAD_BYTES = 8192;  // one plane of a quad: 16 tokens x 256 bf16
+enum { XS_BF16 = 0, XS_PLANES = 1 };
 
-template <typename YT, int WAVES, int T, int UMAX>
-__global__ __launch_bounds__(WAVES * 64) void gemv_xs_kernel(const uint32_t *__restrict__ W,
-                                                             const float *__restrict__ scale,
-                                                             const uint16_t *__restrict__ X, YT *__restrict__ Y,
-                                                             int B, int K, int N) {
+template <typename YT, int WAVES, int T, int UMAX, int NW, int EPI, int XS, bool YSPLIT>
+__global__ __launch_bounds__(WAVES * 64) void gemv_xs_kernel(
+    const uint32_t *__restrict__ W, const float *__restrict__ scale, const uint32_t *__restrict__ W2,
+    const float *__restrict__ scale2, const void *__restrict__ Xv, const uint16_t *__restrict__ X2,
+    YT *__restrict__ Y, int B, int K, int N) {
+  static_assert((NW == 2) == (EPI != GEMV_LINEAR), "two matrices exactly for the GLU epilogues");
+  static_assert(!YSPLIT || (NW == 2 && sizeof(YT) == 2), "split output is the GLU's bf16 planes");
+  constexpr int XP = XS == XS_BF16 ? 1 : 2;  // planes staged per quad
+  constexpr int NL = 8 * XP;  // 16-byte loads per lane and quad
   extern __shared__ __align__(16) uint32_t lds[];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -1043,139 +1056,212 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_xs_kernel(const uint32_t *__r
   const int wpr = K >> 4;
   const int nq = (K + 255) >> 8;
   const int qa = (wave * nq) / WAVES, qb = ((wave + 1) * nq) / WAVES;
-  uint8_t *xl = reinterpret_cast<uint8_t *>(lds) + wave * XS_QUAD_BYTES;
-  const __amdgpu_buffer_rsrc_t xr = buffer_rsrc(X, (uint32_t)B * (uint32_t)K * 2u);
+  uint8_t *xl = reinterpret_cast<uint8_t *>(lds) + wave * XP * XS_QUAD_BYTES;
+  const uint32_t xbytes = (uint32_t)B * (uint32_t)K * 2u;
+  const __amdgpu_buffer_rsrc_t xr = buffer_rsrc(Xv, xbytes);
+  const __amdgpu_buffer_rsrc_t xr2 = buffer_rsrc(XS == XS_PLANES ? (const void *)X2 : Xv, xbytes);
   const __amdgpu_buffer_rsrc_t wr = buffer_rsrc(W, (uint32_t)N * (uint32_t)wpr * 4u);
+  const __amdgpu_buffer_rsrc_t wr2 = buffer_rsrc(NW == 2 ? W2 : W, (uint32_t)N * (uint32_t)wpr * 4u);
   constexpr uint32_t OOB = 0x80000000u;  // a buffer offset past any range this path takes
-  const int st = lane >> 5, sp = lane & 31;  // staging: token of the pair, 16-byte piece
+  const int st = lane >> 5, sp = lane & 31;  // staging: token of the pair, 16-byte bf16 piece
   const int sm = sp >> 3, sg = (sp >> 1) & 3, sh = sp & 1;
-  auto xload = [&](int q, u32x4(&xs)[8]) {
+  auto xload = [&](int q, u32x4(&xs)[NL]) {
 #pragma unroll
     for (int ii = 0; ii < 8; ii++) {
       const int t = 2 * ii + st, col = 256 * q + 8 * sp;
-      const uint32_t off =
-          (q < qb && t < B && col < K) ? ((uint32_t)t * (uint32_t)K + (uint32_t)col) * 2u : OOB;
-      xs[ii] = __builtin_amdgcn_raw_buffer_load_b128(xr, off, 0, 0);
+      const bool ok = q < qb && t < B && col < K;
+      const uint32_t e = (uint32_t)t * (uint32_t)K + (uint32_t)col;  // element index
+      xs[ii] = __builtin_amdgcn_raw_buffer_load_b128(xr, ok ? e * 2u : OOB, 0, 0);
+      if constexpr (XS == XS_PLANES) xs[8 + ii] = __builtin_amdgcn_raw_buffer_load_b128(xr2, ok ? e * 2u : OOB, 0, 0);
     }
   };
-  u32x4 xs[8];
-  xload(qa, xs);  // first, so that it does not wait behind the weights
-  u32x4 wv[T][UMAX];
+  auto xstore = [&](const u32x4(&xs)[NL]) {
 #pragma unroll
-  for (int tt = 0; tt < T; tt++)
-#pragma unroll
-    for (int u = 0; u < UMAX; u++) {
-      const int row = b0 + 16 * tt + r, q = qa + u, wi = 16 * q + 4 * g;
-      const uint32_t off =
-          (row < b1 && q < qb && wi < wpr) ? ((uint32_t)row * (uint32_t)wpr + (uint32_t)wi) * 4u : OOB;
-      wv[tt][u] = __builtin_amdgcn_raw_buffer_load_b128(wr, off, 0, 0);
+    for (int ii = 0; ii < 8; ii++) {
+      const int ts = 2 * ii + st;
+      uint8_t *dst = xl + ((sm * 2 + sh) * 64 + sg * 16 + (ts ^ (2 * sg + sh))) * 16;
+      *reinterpret_cast<u32x4 *>(dst) = xs[ii];
+      if constexpr (XS == XS_PLANES) *reinterpret_cast<u32x4 *>(dst + XS_QUAD_BYTES) = xs[8 + ii];
     }
-  f32x4 acc[T];
+  };
+  u32x4 xs[NL];
+  xload(qa, xs);  // first, so that it does not wait behind the weights
+  u32x4 wv[NW][T][UMAX];
 #pragma unroll
-  for (int tt = 0; tt < T; tt++) acc[tt] = (f32x4){0.f, 0.f, 0.f, 0.f};
+  for (int mw = 0; mw < NW; mw++)
+#pragma unroll
+    for (int tt = 0; tt < T; tt++)
+#pragma unroll
+      for (int u = 0; u < UMAX; u++) {
+        const int row = b0 + 16 * tt + r, q = qa + u, wi = 16 * q + 4 * g;
+        const uint32_t off =
+            (row < b1 && q < qb && wi < wpr) ? ((uint32_t)row * (uint32_t)wpr + (uint32_t)wi) * 4u : OOB;
+        wv[mw][tt][u] = __builtin_amdgcn_raw_buffer_load_b128(mw ? wr2 : wr, off, 0, 0);
+      }
+  f32x4 acc[NW][T];
+#pragma unroll
+  for (int mw = 0; mw < NW; mw++)
+#pragma unroll
+    for (int tt = 0; tt < T; tt++) acc[mw][tt] = (f32x4){0.f, 0.f, 0.f, 0.f};
   const int t = lane & 15;
 #pragma unroll
   for (int u = 0; u < UMAX; u++) {
     if (qa + u >= qb) break;  // wave-uniform
     // the wave's own LDS area: its reads of the previous quad precede these
     // writes in the wave's LDS order
-#pragma unroll
-    for (int ii = 0; ii < 8; ii++) {
-      const int ts = 2 * ii + st;
-      *reinterpret_cast<u32x4 *>(xl + ((sm * 2 + sh) * 64 + sg * 16 + (ts ^ (2 * sg + sh))) * 16) = xs[ii];
-    }
+    xstore(xs);
     if (u + 1 < UMAX) xload(qa + u + 1, xs);
 #pragma unroll
-    for (int tt = 0; tt < T; tt++) {
-      u32x4 &v = wv[tt][u];
-      const auto p02 = __builtin_amdgcn_permlane32_swap(v.x, v.z, false, false);
-      const auto p13 = __builtin_amdgcn_permlane32_swap(v.y, v.w, false, false);
-      const auto p01 = __builtin_amdgcn_permlane16_swap(p02[0], p13[0], false, false);
-      const auto p23 = __builtin_amdgcn_permlane16_swap(p02[1], p13[1], false, false);
-      v = (u32x4){p01[0], p01[1], p23[0], p23[1]};
-    }
-#pragma unroll
-    for (int m = 0; m < 4; m++) {
-      const u32x4 x0 = *reinterpret_cast<const u32x4 *>(xl + ((m * 2) * 64 + g * 16 + (t ^ (2 * g))) * 16);
-      const u32x4 x1 = *reinterpret_cast<const u32x4 *>(xl + ((m * 2 + 1) * 64 + g * 16 + (t ^ (2 * g + 1))) * 16);
+    for (int mw = 0; mw < NW; mw++)
 #pragma unroll
       for (int tt = 0; tt < T; tt++) {
-        const uint32_t wq = m == 0 ? wv[tt][u].x : m == 1 ? wv[tt][u].y : m == 2 ? wv[tt][u].z : wv[tt][u].w;
-        u32x4 a0, a1;
-        unpack16_nat(wq, a0, a1);
-        acc[tt] = mfma16(a0, x0, acc[tt]);
-        acc[tt] = mfma16(a1, x1, acc[tt]);
+        u32x4 &v = wv[mw][tt][u];
+        const auto p02 = __builtin_amdgcn_permlane32_swap(v.x, v.z, false, false);
+        const auto p13 = __builtin_amdgcn_permlane32_swap(v.y, v.w, false, false);
+        const auto p01 = __builtin_amdgcn_permlane16_swap(p02[0], p13[0], false, false);
+        const auto p23 = __builtin_amdgcn_permlane16_swap(p02[1], p13[1], false, false);
+        v = (u32x4){p01[0], p01[1], p23[0], p23[1]};
       }
+#pragma unroll
+    for (int m = 0; m < 4; m++) {
+      u32x4 x0[XP], x1[XP];
+#pragma unroll
+      for (int p = 0; p < XP; p++) {
+        x0[p] = *reinterpret_cast<const u32x4 *>(xl + p * XS_QUAD_BYTES + ((m * 2) * 64 + g * 16 + (t ^ (2 * g))) * 16);
+        x1[p] = *reinterpret_cast<const u32x4 *>(xl + p * XS_QUAD_BYTES +
+                                                 ((m * 2 + 1) * 64 + g * 16 + (t ^ (2 * g + 1))) * 16);
+      }
+#pragma unroll
+      for (int mw = 0; mw < NW; mw++)
+#pragma unroll
+        for (int tt = 0; tt < T; tt++) {
+          const u32x4 &v = wv[mw][tt][u];
+          const uint32_t wq = m == 0 ? v.x : m == 1 ? v.y : m == 2 ? v.z : v.w;
+          u32x4 a0, a1;
+          unpack16_nat(wq, a0, a1);
+#pragma unroll
+          for (int p = 0; p < XP; p++) {
+            acc[mw][tt] = mfma16(a0, x0[p], acc[mw][tt]);
+            acc[mw][tt] = mfma16(a1, x1[p], acc[mw][tt]);
+          }
+        }
     }
   }
   // Partial tiles, added in wave order; wave tt finishes tile tt.
   __syncthreads();
   f32x4 *red = reinterpret_cast<f32x4 *>(lds);
 #pragma unroll
-  for (int tt = 0; tt < T; tt++) red[(tt * WAVES + wave) * 64 + lane] = acc[tt];
+  for (int mw = 0; mw < NW; mw++)
+#pragma unroll
+    for (int tt = 0; tt < T; tt++) red[((mw * T + tt) * WAVES + wave) * 64 + lane] = acc[mw][tt];
   __syncthreads();
   if (wave < T) {
     const int tt = wave;
-    f32x4 s = red[tt * WAVES * 64 + lane];
-    for (int w = 1; w < WAVES; w++) s += red[(tt * WAVES + w) * 64 + lane];
     const int n_out = b0 + 16 * tt + 4 * g;  // rows 4g..4g+3 of token t
     if (t < B && n_out < b1) {
       const int nok = min(4, b1 - n_out);
-      const f32x4 sc = {scale[n_out], nok > 1 ? scale[n_out + 1] : 0.f, nok > 2 ? scale[n_out + 2] : 0.f,
-                        nok > 3 ? scale[n_out + 3] : 0.f};
-      YStore<YT>::store4(Y + (size_t)t * N + n_out, s * sc * 0.5f, nok);  // 0.5: the 2*dec(c) encoding
+      f32x4 v[NW];
+#pragma unroll
+      for (int mw = 0; mw < NW; mw++) {
+        const f32x4 *rp = red + (mw * T + tt) * WAVES * 64 + lane;
+        f32x4 s = rp[0];
+        for (int w = 1; w < WAVES; w++) s += rp[w * 64];
+        const float *sp2 = mw ? scale2 : scale;
+        const f32x4 sc = {sp2[n_out], nok > 1 ? sp2[n_out + 1] : 0.f, nok > 2 ? sp2[n_out + 2] : 0.f,
+                          nok > 3 ? sp2[n_out + 3] : 0.f};
+        v[mw] = s * sc * 0.5f;  // 0.5: the 2*dec(c) operand encoding
+      }
+      f32x4 o = v[0];
+      if constexpr (NW == 2) {
+#pragma unroll
+        for (int j = 0; j < 4; j++) o[j] = (EPI == GEMV_GEGLU ? act_gelu_tanh(v[0][j]) : act_silu(v[0][j])) * v[1][j];
+      }
+      if constexpr (YSPLIT) {
+        f32x4 hi, lo;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+          hi[j] = bf16_to_f32(bf16_rne(o[j]));
+          lo[j] = (__float_as_uint(hi[j]) & 0x7F800000u) == 0x7F800000u ? 0.0f : o[j] - hi[j];
+        }
+        YStore<uint16_t>::store4(reinterpret_cast<uint16_t *>(Y) + (size_t)t * N + n_out, hi, nok);
+        YStore<uint16_t>::store4(reinterpret_cast<uint16_t *>(Y) + (size_t)B * N + (size_t)t * N + n_out, lo, nok);
+      } else {
+        YStore<YT>::store4(Y + (size_t)t * N + n_out, o, nok);
+      }
     }
   }
 }
 
-template <typename YT, int WAVES, int T, int UMAX>
-static hipError_t launch_gemv_xs_w(const uint32_t *w, const float *scale, const void *x, void *y, int B, int K,
-                                   int N, int G, hipStream_t stream) {
-  static_assert(T * 1024 <= XS_QUAD_BYTES, "the partial tiles reuse the staging area");
-  const size_t lds = (size_t)WAVES * XS_QUAD_BYTES;
+template <typename YT, int WAVES, int T, int UMAX, int NW, int EPI, int XS, bool YSPLIT>
+static hipError_t launch_gemv_xs_w(const uint32_t *w, const float *scale, const uint32_t *w2, const float *scale2,
+                                   const void *x, const void *x2, void *y, int B, int K, int N, int G,
+                                   hipStream_t stream) {
+  constexpr int XP = XS == XS_BF16 ? 1 : 2;
+  static_assert(NW * T * 1024 <= XP * XS_QUAD_BYTES, "the partial tiles reuse the staging area");
+  const size_t lds = (size_t)WAVES * XP * XS_QUAD_BYTES;
   if (lds > 64 * 1024) {
     static std::atomic<uint64_t> done;
-    const hipError_t e =
-        opt_in_lds(reinterpret_cast<const void *>(&gemv_xs_kernel<YT, WAVES, T, UMAX>), (int)lds, done);
+    const hipError_t e = opt_in_lds(
+        reinterpret_cast<const void *>(&gemv_xs_kernel<YT, WAVES, T, UMAX, NW, EPI, XS, YSPLIT>), (int)lds, done);
     if (e != hipSuccess) return e;
   }
-  hipLaunchKernelGGL((gemv_xs_kernel<YT, WAVES, T, UMAX>), dim3(G), dim3(WAVES * 64), lds, stream, w, scale,
-                     reinterpret_cast<const uint16_t *>(x), reinterpret_cast<YT *>(y), B, K, N);
+  hipLaunchKernelGGL((gemv_xs_kernel<YT, WAVES, T, UMAX, NW, EPI, XS, YSPLIT>), dim3(G), dim3(WAVES * 64), lds,
+                     stream, w, scale, w2, scale2, x, reinterpret_cast<const uint16_t *>(x2),
+                     reinterpret_cast<YT *>(y), B, K, N);
   return hipGetLastError();
 }
 
-// Shapes gemv_xs_kernel takes: K up to 64 quads (16384), 16-byte aligned x.
-static bool gemv_xs_ok(const void *x, int B, int K) {
-  return B >= 1 && B <= 16 && K <= 64 * 256 && (reinterpret_cast<uintptr_t>(x) & 15) == 0;
+// Shapes gemv_xs_kernel takes: up to 16 tokens, K up to 64 quads (16384; 48
+// with two planes or two matrices), 16-byte aligned activations.
+static bool gemv_xs_ok(const void *x, int B, int K, int XP, int NW) {
+  const int nq = (K + 255) / 256;
+  return B >= 1 && B <= 16 && nq <= (XP == 1 && NW == 1 ? 64 : 48) && (reinterpret_cast<uintptr_t>(x) & 15) == 0;
 }
 
 // Grid: one workgroup per CU, fewer where that would leave tiles of fewer
-// than 16 rows, more where a workgroup would hold more than TMAX tiles.
-// Waves: 16 (one quad each up to K = 4096, two up to 8192), 12 with up to
-// four quads (K <= 12288; measured 9.5 us against 10.0 us with 16 waves of
-// three quads at 4096x11008, B = 16), else 16 waves of four.
-template <typename YT>
-static hipError_t launch_gemv_xs(const uint32_t *w, const float *scale, const void *x, void *y, int B, int K, int N,
-                                 hipStream_t stream) {
-  const int nq = (K + 255) / 256;
-  const int tmax = nq <= 32 ? 4 : 2;  // tiles per workgroup (weight registers: tiles x quads per wave)
+// than 16 rows, more where a workgroup would hold more tiles than its
+// weight registers allow (tiles x quads per wave x matrices <= 8).
+static int gemv_xs_grid(int N, int tmax) {
   int G = std::min(device_cu_count(), (N + 15) / 16);
   if ((N + G - 1) / G > 16 * tmax) G = (N + 16 * tmax - 1) / (16 * tmax);
-  const int tiles = ((N + G - 1) / G + 15) / 16;
-#define FRX_XS(WV, TT, UM) return launch_gemv_xs_w<YT, WV, TT, UM>(w, scale, x, y, B, K, N, G, stream)
-#define FRX_XS_T(WV, UM)   \
-  if (tiles <= 1) FRX_XS(WV, 1, UM); \
-  if (tiles <= 2) FRX_XS(WV, 2, UM); \
-  if (tiles <= 3) FRX_XS(WV, 3, UM); \
-  FRX_XS(WV, 4, UM)
-  if (nq <= 16) { FRX_XS_T(16, 1); }
-  if (nq <= 32) { FRX_XS_T(16, 2); }
-  if (nq <= 48) {
-    if (tiles <= 1) FRX_XS(12, 1, 4);
-    FRX_XS(12, 2, 4);
+  return G;
+}
+
+// Waves and quads per wave. One plane and one matrix: 16 waves of one quad
+// (K <= 4096) or two (8192); 12 waves of up to four quads (K <= 12288;
+// measured 9.5 us against 10.0 us with 16 waves of three quads at
+// 4096x11008, B = 16); 16 waves of four above. Two planes (16 KB per wave)
+// or two matrices (twice the weight registers): 8 waves of up to 2, 4 or 6
+// quads, so that a wave has 256 registers.
+template <typename YT, int NW, int EPI, int XS, bool YSPLIT>
+static hipError_t launch_gemv_xs(const uint32_t *w, const float *scale, const uint32_t *w2, const float *scale2,
+                                 const void *x, const void *x2, void *y, int B, int K, int N, hipStream_t stream) {
+  const int nq = (K + 255) / 256;
+#define FRX_XS(WV, TT, UM)                                                                                    \
+  return launch_gemv_xs_w<YT, WV, TT, UM, NW, EPI, XS, YSPLIT>(w, scale, w2, scale2, x, x2, y, B, K, N, \
+                                                                gemv_xs_grid(N, TT), stream)
+#define FRX_XS_T(WV, UM, TMAX)                                                               \
+  {                                                                                          \
+    const int tiles = ((N + gemv_xs_grid(N, TMAX) - 1) / gemv_xs_grid(N, TMAX) + 15) / 16; \
+    if (tiles <= 1 || TMAX == 1) FRX_XS(WV, 1, UM);                                          \
+    if (tiles <= 2 || TMAX == 2) FRX_XS(WV, (TMAX >= 2 ? 2 : 1), UM);                        \
+    if (tiles <= 3 || TMAX == 3) FRX_XS(WV, (TMAX >= 3 ? 3 : 1), UM);                        \
+    FRX_XS(WV, (TMAX >= 4 ? 4 : 1), UM);                                                     \
   }
-  if (tiles <= 1) FRX_XS(16, 1, 4);
-  FRX_XS(16, 2, 4);
+  if constexpr (XS == XS_BF16 && NW == 1) {
+    if (nq <= 16) FRX_XS_T(16, 1, 4);
+    if (nq <= 32) FRX_XS_T(16, 2, 4);
+    if (nq <= 48) FRX_XS_T(12, 4, 2);
+    FRX_XS_T(16, 4, 2);
+  } else if constexpr (NW == 1) {
+    if (nq <= 16) FRX_XS_T(8, 2, 4);
+    if (nq <= 32) FRX_XS_T(8, 4, 2);
+    FRX_XS_T(8, 6, 1);
+  } else {
+    if (nq <= 16) FRX_XS_T(8, 2, 2);
+    if (nq <= 32) FRX_XS_T(8, 4, 1);
+    FRX_XS_T(8, 6, 1);
+  }
 #undef FRX_XS_T
 #undef FRX_XS
 }
@@ -1507,9 +1593,9 @@ hipError_t launch_gemv(const uint32_t *w, const float *scale, const void *x,
     if (yt_bf16) return launch_gemv_rows4<uint16_t>(w, scale, x, y, B, K, N, stream);
     return launch_gemv_rows4<float>(w, scale, x, y, B, K, N, stream);
   }
-  if (xt_bf16 && B >= GEMV_DIRECT_MIN_B && gemv_xs_ok(x, B, K)) {
-    if (yt_bf16) return launch_gemv_xs<uint16_t>(w, scale, x, y, B, K, N, stream);
-    return launch_gemv_xs<float>(w, scale, x, y, B, K, N, stream);
+  if (xt_bf16 && B >= GEMV_DIRECT_MIN_B && gemv_xs_ok(x, B, K, 1, 1)) {
+    if (yt_bf16) return launch_gemv_xs<uint16_t, 1, L, XS_BF16, false>(w, scale, w, scale, x, x, y, B, K, N, stream);
+    return launch_gemv_xs<float, 1, L, XS_BF16, false>(w, scale, w, scale, x, x, y, B, K, N, stream);
   }
   if (xt_bf16 && B >= GEMV_DIRECT_MIN_B) {
     // taller tiles where their grid still covers every CU
@@ -1540,6 +1626,13 @@ hipError_t launch_gemv(const uint32_t *w, const float *scale, const void *x,
 hipError_t launch_gemv_glu(const uint32_t *w_gate, const float *s_gate, const uint32_t *w_up,
                            const float *s_up, const void *x, int xt_bf16, float *h, int B, int K,
                            int N, int gelu, hipStream_t stream) {
+  if (xt_bf16 && B >= GEMV_DIRECT_MIN_B && gemv_xs_ok(x, B, K, 1, 2)) {
+    if (gelu)
+      return launch_gemv_xs<float, 2, GEMV_GEGLU, XS_BF16, false>(w_gate, s_gate, w_up, s_up, x, x, h, B, K, N,
+                                                                   stream);
+    return launch_gemv_xs<float, 2, GEMV_SWIGLU, XS_BF16, false>(w_gate, s_gate, w_up, s_up, x, x, h, B, K, N,
+                                                                  stream);
+  }
   if (xt_bf16 && B >= GEMV_DIRECT_MIN_B) {
     if (gelu) return launch_gemv_direct<float, GEMV_GEGLU>(w_gate, s_gate, w_up, s_up, x, x, h, B, K, N, stream);
     return launch_gemv_direct<float, GEMV_SWIGLU>(w_gate, s_gate, w_up, s_up, x, x, h, B, K, N, stream);
@@ -1576,6 +1669,13 @@ hipError_t launch_glu_combine(const float *g, const float *u, float *h, size_t n
 hipError_t launch_gemv_glu_planes(const uint32_t *w_gate, const float *s_gate, const uint32_t *w_up,
                                   const float *s_up, const void *x, uint16_t *h_planes, int B, int K,
                                   int N, int gelu, hipStream_t stream) {
+  if (B >= GEMV_DIRECT_MIN_B && gemv_xs_ok(x, B, K, 1, 2)) {
+    if (gelu)
+      return launch_gemv_xs<uint16_t, 2, GEMV_GEGLU, XS_BF16, true>(w_gate, s_gate, w_up, s_up, x, x, h_planes, B,
+                                                                     K, N, stream);
+    return launch_gemv_xs<uint16_t, 2, GEMV_SWIGLU, XS_BF16, true>(w_gate, s_gate, w_up, s_up, x, x, h_planes, B,
+                                                                    K, N, stream);
+  }
   if (gelu)
     return launch_gemv_direct<uint16_t, GEMV_GEGLU, 1, true>(w_gate, s_gate, w_up, s_up, x, x, h_planes, B,
                                                              K, N, stream);
@@ -1586,6 +1686,13 @@ hipError_t launch_gemv_glu_planes(const uint32_t *w_gate, const float *s_gate, c
 hipError_t launch_gemv_planes(const uint32_t *w, const float *scale, const uint16_t *x_planes, void *y,
                               int yt_bf16, int B, int K, int N, hipStream_t stream) {
   const uint16_t *lo = x_planes + (size_t)B * K;
+  if (B >= GEMV_DIRECT_MIN_B && gemv_xs_ok(x_planes, B, K, 2, 1) && (reinterpret_cast<uintptr_t>(lo) & 15) == 0) {
+    if (yt_bf16)
+      return launch_gemv_xs<uint16_t, 1, GEMV_LINEAR, XS_PLANES, false>(w, scale, w, scale, x_planes, lo, y, B, K,
+                                                                        N, stream);
+    return launch_gemv_xs<float, 1, GEMV_LINEAR, XS_PLANES, false>(w, scale, w, scale, x_planes, lo, y, B, K, N,
+                                                                   stream);
+  }
   if (yt_bf16)
     return launch_gemv_direct<uint16_t, GEMV_LINEAR, 2>(w, scale, w, scale, x_planes, lo, y, B, K, N, stream);
   return launch_gemv_direct<float, GEMV_LINEAR, 2>(w, scale, w, scale, x_planes, lo, y, B, K, N, stream);
