@@ -852,6 +852,201 @@ static hipError_t launch_gemv_rows_w(const uint32_t *w, const float *scale, cons
   return hipGetLastError();
 }
 
+// ---- one token, balanced: one or two workgroups per CU --------------------
+//
+// The rows kernel's decode (whole 1 KB windows per wave instruction, the MFMA
+// diagonal, the same reduction order) with the rows of the matrix split
+// evenly over G = 1 or 2 workgroups per CU, and within a workgroup over its
+// 8 waves, so that every CU decodes the same number of rows. Every wave
+// issues its share of x first and a workgroup barrier separates those loads
+// from the weight loads: in the CU's in-order memory pipeline the staging of
+// x then does not wait behind weights. Row scales are scalar loads (uniform
+// rows). Measured per launch against gemv_rows_kernel: 5.66 -> 5.50 us
+// (11008x4096, G = 2 per CU) and 5.67 -> 5.28 us (4096x11008, G = 1).
+// XF32: fp32 activations, split once per workgroup at staging into bf16 hi
+// and lo planes (hi = bf16(x), lo = bf16(x - hi), |x - hi - lo| <= 2^-17 |x|,
+// lo = 0 where hi is not finite); each word then runs four MFMAs.
+template <typename YT, int NI, int RMAX, bool XF32>
+__global__ __launch_bounds__(512) void gemv_bal_kernel(const uint32_t *__restrict__ W, const float *__restrict__ scale,
+                                                       const void *__restrict__ Xv, YT *__restrict__ Y, int K, int N) {
+  constexpr int WAVES = 8, NT = 512;
+  constexpr int XPL = XF32 ? 2 : 1;
+  constexpr int PP = NI * 512;                   // 8-value pieces of x staged (NI * 4096 values)
+  constexpr int PD = NI * 64 * ROWS_XCH;         // LDS dwords per plane
+  constexpr int XR = (PP + NT - 1) / NT;         // pieces per thread
+  constexpr int XL = XF32 ? 2 : 1;               // 16-byte loads per piece
+  extern __shared__ __align__(16) uint32_t lds[];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int b0 = (int)((long long)blockIdx.x * N / gridDim.x);
+  const int cb = (int)((long long)(blockIdx.x + 1) * N / gridDim.x) - b0;
+  const int row0 = b0 + wave * cb / WAVES, cnt = b0 + (wave + 1) * cb / WAVES - row0;
+  const int kw = K >> 4;
+  constexpr uint32_t OOB = 0x80000000u;  // a buffer offset past any range this path takes
+  const __amdgpu_buffer_rsrc_t xr = buffer_rsrc(Xv, (uint32_t)K * (XF32 ? 4u : 2u));
+  const __amdgpu_buffer_rsrc_t wr = buffer_rsrc(W, (uint32_t)N * (uint32_t)kw * 4u);
+  // 1. x pieces (zero past K), then a barrier: all of the CU's x loads are
+  //    ahead of its weight loads
+  u32x4 xs[XR][XL];
+#pragma unroll
+  for (int r = 0; r < XR; r++) {
+    const int j = tid + r * NT;
+    const uint32_t off = j < PP ? (uint32_t)j * (XF32 ? 32u : 16u) : OOB;
+#pragma unroll
+    for (int l = 0; l < XL; l++) xs[r][l] = __builtin_amdgcn_raw_buffer_load_b128(xr, off + 16u * l, 0, 0);
+  }
+  __syncthreads();
+  // 2. the wave's rows (rows past cnt read zeros without touching memory)
+  u32x4 wv[RMAX][NI];
+#pragma unroll
+  for (int rr = 0; rr < RMAX; rr++)
+#pragma unroll
+    for (int i = 0; i < NI; i++) {
+      const int wi = i * 256 + 4 * lane;
+      const uint32_t off = (rr < cnt && wi < kw) ? ((uint32_t)(row0 + rr) * (uint32_t)kw + (uint32_t)wi) * 4u : OOB;
+      wv[rr][i] = __builtin_amdgcn_raw_buffer_load_b128(wr, off, 0, 0);
+    }
+  float sc[RMAX];
+#pragma unroll
+  for (int rr = 0; rr < RMAX; rr++) sc[rr] = scale[min(row0 + rr, N - 1)];
+  // 3. stage: piece j -> chunk j/8, slot j%8 (per plane)
+#pragma unroll
+  for (int r = 0; r < XR; r++) {
+    const int j = tid + r * NT;
+    if (j < PP) {
+      uint32_t *dst = lds + (j >> 3) * ROWS_XCH + (j & 7) * 4;
+      if constexpr (XF32) {
+        const float f[8] = {__uint_as_float(xs[r][0].x), __uint_as_float(xs[r][0].y), __uint_as_float(xs[r][0].z),
+                            __uint_as_float(xs[r][0].w), __uint_as_float(xs[r][1].x), __uint_as_float(xs[r][1].y),
+                            __uint_as_float(xs[r][1].z), __uint_as_float(xs[r][1].w)};
+        uint32_t hi[8], lo[8];
+#pragma unroll
+        for (int e = 0; e < 8; e++) split_bf16(f[e], hi[e], lo[e]);
+        *reinterpret_cast<u32x4 *>(dst) =
+            (u32x4){hi[0] | (hi[1] << 16), hi[2] | (hi[3] << 16), hi[4] | (hi[5] << 16), hi[6] | (hi[7] << 16)};
+        *reinterpret_cast<u32x4 *>(dst + PD) =
+            (u32x4){lo[0] | (lo[1] << 16), lo[2] | (lo[3] << 16), lo[4] | (lo[5] << 16), lo[6] | (lo[7] << 16)};
+      } else {
+        *reinterpret_cast<u32x4 *>(dst) = xs[r][0];
+      }
+    }
+  }
+  __syncthreads();
+  // 4. the lane's activations of every window once (registers; re-read per
+  //    row where two planes of more than two windows would not fit), then
+  //    rows in order as their weights land, each reduced right away
+  constexpr bool XREG = NI * XPL <= 4;
+  u32x4 xb[XREG ? NI : 1][XPL][8];
+  auto xread = [&](int i, u32x4(&dst)[XPL][8]) {
+#pragma unroll
+    for (int p = 0; p < XPL; p++) {
+      const uint32_t *xp = lds + p * PD + (i * 64 + lane) * ROWS_XCH;
+#pragma unroll
+      for (int q = 0; q < 8; q++) dst[p][q] = *reinterpret_cast<const u32x4 *>(xp + 4 * q);
+    }
+  };
+  if constexpr (XREG) {
+#pragma unroll
+    for (int i = 0; i < NI; i++) xread(i, xb[i]);
+  }
+  float res = 0.f;
+  const int c = lane & 15, rg = lane >> 4, e = c & 3;
+#pragma unroll
+  for (int rr = 0; rr < RMAX; rr++) {
+    if (rr < cnt) {  // wave-uniform
+      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int i = 0; i < NI; i++) {
+        u32x4 xw[XPL][8];
+        if constexpr (!XREG) xread(i, xw);
+        const u32x4(&xv)[XPL][8] = XREG ? xb[XREG ? i : 0] : xw;
+        const uint32_t wq[4] = {wv[rr][i].x, wv[rr][i].y, wv[rr][i].z, wv[rr][i].w};
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+          u32x4 lo, hi;
+          unpack16_nat(wq[j], lo, hi);
+#pragma unroll
+          for (int p = 0; p < XPL; p++) {
+            acc = mfma16(lo, xv[p][2 * j], acc);
+            acc = mfma16(hi, xv[p][2 * j + 1], acc);
+          }
+        }
+      }
+      // diagonal: lane (c = l%16, rg = l/16) holds C[4rg + e][c]
+      float v = e == 0 ? acc[0] : e == 1 ? acc[1] : e == 2 ? acc[2] : acc[3];
+      v = (c >> 2) == rg ? v : 0.f;
+      v += dpp_f32<0xB1>(v);  // quad_perm [1,0,3,2]
+      v += dpp_f32<0x4E>(v);  // quad_perm [2,3,0,1]
+      const float a = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+      const float b = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 20));
+      const float d = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 40));
+      const float f = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 60));
+      const float tot = ((a + b) + (d + f)) * sc[rr] * 0.5f;  // 0.5 undoes the 2*dec(c) encoding
+      if (lane == rr) res = tot;
+    }
+  }
+  if (lane < cnt) {
+    if constexpr (sizeof(YT) == 2) Y[row0 + lane] = (uint16_t)bf16_rne(res);
+    else Y[row0 + lane] = res;
+  }
+}
+
+// Most rows per wave of the balanced kernel. The row slots are sized to the
+// launch (a slot past the wave's rows still costs its loads: at 4096x11008,
+// four slots for two rows measured 6.30 against 5.31 us).
+constexpr int GEMV_BAL_RMAX = 4;
+
+template <typename YT, int NI, int RMAX, bool XF32>
+static hipError_t launch_gemv_bal_w(const uint32_t *w, const float *scale, const void *x, void *y, int K, int N,
+                                    int G, hipStream_t stream) {
+  const size_t lds = (size_t)(XF32 ? 2 : 1) * NI * 64 * ROWS_XCH * 4;
+  if (lds > 64 * 1024) {
+    static std::atomic<uint64_t> done;
+    const hipError_t e =
+        opt_in_lds(reinterpret_cast<const void *>(&gemv_bal_kernel<YT, NI, RMAX, XF32>), (int)lds, done);
+    if (e != hipSuccess) return e;
+  }
+  hipLaunchKernelGGL((gemv_bal_kernel<YT, NI, RMAX, XF32>), dim3(G), dim3(512), lds, stream, w, scale, x,
+                     reinterpret_cast<YT *>(y), K, N);
+  return hipGetLastError();
+}
+
+static int device_cu_count();
+
+// One token, K % 64 == 0 up to 16384, 16-byte aligned weights and x, and at
+// most GEMV_BAL_RMAX rows per wave at G workgroups (two per CU for one
+// window per row, one above).
+static bool gemv_bal_grid(const uint32_t *w, const void *x, int B, int K, int N, int *G) {
+  if (B != 1 || K % 64 != 0 || K > 4 * 4096 || (reinterpret_cast<uintptr_t>(w) & 15) != 0 ||
+      (reinterpret_cast<uintptr_t>(x) & 15) != 0)
+    return false;
+  const int ni = (K + 4095) / 4096;
+  const int g = std::min((ni == 1 ? 2 : 1) * device_cu_count(), (N + 7) / 8);
+  if ((N + g - 1) / g > 8 * GEMV_BAL_RMAX) return false;
+  *G = g;
+  return true;
+}
+
+template <typename YT, int NI, bool XF32>
+static hipError_t launch_gemv_bal_r(const uint32_t *w, const float *scale, const void *x, void *y, int K, int N, int G,
+                                    hipStream_t stream) {
+  const int rmax = ((N + G - 1) / G + 7) / 8;
+  if (rmax <= 1) return launch_gemv_bal_w<YT, NI, 1, XF32>(w, scale, x, y, K, N, G, stream);
+  if (rmax <= 2) return launch_gemv_bal_w<YT, NI, 2, XF32>(w, scale, x, y, K, N, G, stream);
+  if (rmax <= 3) return launch_gemv_bal_w<YT, NI, 3, XF32>(w, scale, x, y, K, N, G, stream);
+  return launch_gemv_bal_w<YT, NI, 4, XF32>(w, scale, x, y, K, N, G, stream);
+}
+
+template <typename YT, bool XF32>
+static hipError_t launch_gemv_bal(const uint32_t *w, const float *scale, const void *x, void *y, int K, int N, int G,
+                                  hipStream_t stream) {
+  const int ni = (K + 4095) / 4096;
+  if (ni == 1) return launch_gemv_bal_r<YT, 1, XF32>(w, scale, x, y, K, N, G, stream);
+  if (ni == 2) return launch_gemv_bal_r<YT, 2, XF32>(w, scale, x, y, K, N, G, stream);
+  if (ni == 3) return launch_gemv_bal_r<YT, 3, XF32>(w, scale, x, y, K, N, G, stream);
+  return launch_gemv_bal_r<YT, 4, XF32>(w, scale, x, y, K, N, G, stream);
+}
+
 // ---- tall single-token GEMV: persistent waves, next group in flight ------
 //
 // Above one residency pass the one-shot rows kernel runs in lockstep passes:
@@ -1585,6 +1780,15 @@ hipError_t launch_gemv(const uint32_t *w, const float *scale, const void *x,
                        int xt_bf16, void *y, int yt_bf16, int B, int K, int N,
                        hipStream_t stream) {
   constexpr int L = GEMV_LINEAR;
+  int G = 0;
+  if (gemv_bal_grid(w, x, B, K, N, &G)) {
+    if (xt_bf16) {
+      if (yt_bf16) return launch_gemv_bal<uint16_t, false>(w, scale, x, y, K, N, G, stream);
+      return launch_gemv_bal<float, false>(w, scale, x, y, K, N, G, stream);
+    }
+    if (yt_bf16) return launch_gemv_bal<uint16_t, true>(w, scale, x, y, K, N, G, stream);
+    return launch_gemv_bal<float, true>(w, scale, x, y, K, N, G, stream);
+  }
   if (xt_bf16 && gemv_rows_ok(w, x, B, K)) {
     if (yt_bf16) return launch_gemv_rows<uint16_t>(w, scale, x, y, K, N, stream);
     return launch_gemv_rows<float>(w, scale, x, y, K, N, stream);
