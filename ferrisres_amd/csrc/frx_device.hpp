@@ -87,6 +87,20 @@ __device__ __forceinline__ void split_bf16(float x, uint32_t &hi,
   lo = ((hi & 0x7F80u) == 0x7F80u) ? 0u : bf16_rne(r);
 }
 
+// split_bf16 of two values at once, packed: hi = (bf16(a), bf16(b)), lo =
+// (bf16(a - hi_a), bf16(b - hi_b)), a lo half zero where its hi half is not
+// finite. The rounding is the hardware's packed f32 -> bf16 conversion
+// (round to nearest even, as bf16_rne), about five VALU ops a value.
+__device__ __forceinline__ void split2_bf16(float a, float b, uint32_t &hi, uint32_t &lo) {
+  typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+  typedef float f32x2 __attribute__((ext_vector_type(2)));
+  hi = __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){a, b}, bf16x2));
+  const float ha = __uint_as_float(hi << 16), hb = __uint_as_float(hi & 0xFFFF0000u);
+  const float ra = __builtin_isfinite(ha) ? a - ha : 0.0f;
+  const float rb = __builtin_isfinite(hb) ? b - hb : 0.0f;
+  lo = __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){ra, rb}, bf16x2));
+}
+
 // Natural bf16 dwords n[0..7] of a 16-column block (x0..x15) -> interleaved
 // dwords d[i] = x[i] | x[i+8] << 16.
 // One byte permute per output dword.

@@ -864,8 +864,9 @@ static hipError_t launch_gemv_rows_w(const uint32_t *w, const float *scale, cons
 // rows). Measured per launch against gemv_rows_kernel: 5.66 -> 5.50 us
 // (11008x4096, G = 2 per CU) and 5.67 -> 5.28 us (4096x11008, G = 1).
 // XF32: fp32 activations, split once per workgroup at staging into bf16 hi
-// and lo planes (hi = bf16(x), lo = bf16(x - hi), |x - hi - lo| <= 2^-17 |x|,
-// lo = 0 where hi is not finite); each word then runs four MFMAs.
+// and lo planes (split2_bf16: hi = bf16(x), lo = bf16(x - hi), |x - hi - lo|
+// <= 2^-17 |x|, lo = 0 where hi is not finite); each word then runs four
+// MFMAs.
 template <typename YT, int NI, int RMAX, bool XF32>
 __global__ __launch_bounds__(512) void gemv_bal_kernel(const uint32_t *__restrict__ W, const float *__restrict__ scale,
                                                        const void *__restrict__ Xv, YT *__restrict__ Y, int K, int N) {
@@ -919,13 +920,11 @@ __global__ __launch_bounds__(512) void gemv_bal_kernel(const uint32_t *__restric
         const float f[8] = {__uint_as_float(xs[r][0].x), __uint_as_float(xs[r][0].y), __uint_as_float(xs[r][0].z),
                             __uint_as_float(xs[r][0].w), __uint_as_float(xs[r][1].x), __uint_as_float(xs[r][1].y),
                             __uint_as_float(xs[r][1].z), __uint_as_float(xs[r][1].w)};
-        uint32_t hi[8], lo[8];
+        uint32_t hi[4], lo[4];
 #pragma unroll
-        for (int e = 0; e < 8; e++) split_bf16(f[e], hi[e], lo[e]);
-        *reinterpret_cast<u32x4 *>(dst) =
-            (u32x4){hi[0] | (hi[1] << 16), hi[2] | (hi[3] << 16), hi[4] | (hi[5] << 16), hi[6] | (hi[7] << 16)};
-        *reinterpret_cast<u32x4 *>(dst + PD) =
-            (u32x4){lo[0] | (lo[1] << 16), lo[2] | (lo[3] << 16), lo[4] | (lo[5] << 16), lo[6] | (lo[7] << 16)};
+        for (int e = 0; e < 4; e++) split2_bf16(f[2 * e], f[2 * e + 1], hi[e], lo[e]);
+        *reinterpret_cast<u32x4 *>(dst) = (u32x4){hi[0], hi[1], hi[2], hi[3]};
+        *reinterpret_cast<u32x4 *>(dst + PD) = (u32x4){lo[0], lo[1], lo[2], lo[3]};
       } else {
         *reinterpret_cast<u32x4 *>(dst) = xs[r][0];
       }
@@ -1222,16 +1221,17 @@ static hipError_t launch_gemv_rows_stream(const uint32_t *w, const float *scale,
 //  - Tokens >= B and columns >= K are staged as zeros (buffer loads past the
 //    range), rows past the workgroup's range read zero words; the waves'
 //    partial tiles are added in wave order through LDS (deterministic).
-//  - Activation sources (XS): one bf16 plane, or two bf16 planes whose sum
-//    is the fp32 activation (hi, lo: the decode FFN's intermediate). Two
-//    planes take 16 KB per wave and quad and two MFMAs per operand. (fp32
-//    activations split into such planes at staging were measured slower
-//    than gemv_kernel<float>: every CU splits all of x, 8 VALU ops a value.)
+//  - Activation sources (XS): one bf16 plane; two bf16 planes whose sum is
+//    the fp32 activation (hi, lo: the decode FFN's intermediate); or fp32,
+//    split at staging into such a pair (split2_bf16). Two planes take 16 KB
+//    per wave and quad and two MFMAs per operand. Token pairs at or past B
+//    are not staged: their LDS slots feed only MFMA columns of tokens that
+//    are never stored.
 //  - NW = 2 (EPI = GEMV_SWIGLU / GEMV_GEGLU): the gate (W) and up (W2)
 //    tiles of the same rows against the same staged x; h = act(g) * u, as
 //    fp32 or (YSPLIT) as bf16 hi/lo planes Y = [2][B][N].
 constexpr int XS_QUAD_BYTES = 8192;  // one plane of a quad: 16 tokens x 256 bf16
-enum { XS_BF16 = 0, XS_PLANES = 1 };
+enum { XS_BF16 = 0, XS_PLANES = 1, XS_F32 = 2 };
 
 template <typename YT, int WAVES, int T, int UMAX, int NW, int EPI, int XS, bool YSPLIT>
 __global__ __launch_bounds__(WAVES * 64) void gemv_xs_kernel(
@@ -1241,7 +1241,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_xs_kernel(
   static_assert((NW == 2) == (EPI != GEMV_LINEAR), "two matrices exactly for the GLU epilogues");
   static_assert(!YSPLIT || (NW == 2 && sizeof(YT) == 2), "split output is the GLU's bf16 planes");
   constexpr int XP = XS == XS_BF16 ? 1 : 2;  // planes staged per quad
-  constexpr int NL = 8 * XP;  // 16-byte loads per lane and quad
+  constexpr int NL = 8 * XP;  // 16-byte loads per lane and quad (fp32: two per piece)
   extern __shared__ __align__(16) uint32_t lds[];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -1252,7 +1252,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_xs_kernel(
   const int nq = (K + 255) >> 8;
   const int qa = (wave * nq) / WAVES, qb = ((wave + 1) * nq) / WAVES;
   uint8_t *xl = reinterpret_cast<uint8_t *>(lds) + wave * XP * XS_QUAD_BYTES;
-  const uint32_t xbytes = (uint32_t)B * (uint32_t)K * 2u;
+  const uint32_t xbytes = (uint32_t)B * (uint32_t)K * (XS == XS_F32 ? 4u : 2u);
   const __amdgpu_buffer_rsrc_t xr = buffer_rsrc(Xv, xbytes);
   const __amdgpu_buffer_rsrc_t xr2 = buffer_rsrc(XS == XS_PLANES ? (const void *)X2 : Xv, xbytes);
   const __amdgpu_buffer_rsrc_t wr = buffer_rsrc(W, (uint32_t)N * (uint32_t)wpr * 4u);
@@ -1266,8 +1266,14 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_xs_kernel(
       const int t = 2 * ii + st, col = 256 * q + 8 * sp;
       const bool ok = q < qb && t < B && col < K;
       const uint32_t e = (uint32_t)t * (uint32_t)K + (uint32_t)col;  // element index
-      xs[ii] = __builtin_amdgcn_raw_buffer_load_b128(xr, ok ? e * 2u : OOB, 0, 0);
-      if constexpr (XS == XS_PLANES) xs[8 + ii] = __builtin_amdgcn_raw_buffer_load_b128(xr2, ok ? e * 2u : OOB, 0, 0);
+      if constexpr (XS == XS_F32) {
+        xs[2 * ii] = __builtin_amdgcn_raw_buffer_load_b128(xr, ok ? e * 4u : OOB, 0, 0);
+        xs[2 * ii + 1] = __builtin_amdgcn_raw_buffer_load_b128(xr, ok ? e * 4u + 16u : OOB, 0, 0);
+      } else {
+        xs[ii] = __builtin_amdgcn_raw_buffer_load_b128(xr, ok ? e * 2u : OOB, 0, 0);
+        if constexpr (XS == XS_PLANES)
+          xs[8 + ii] = __builtin_amdgcn_raw_buffer_load_b128(xr2, ok ? e * 2u : OOB, 0, 0);
+      }
     }
   };
   auto xstore = [&](const u32x4(&xs)[NL]) {
@@ -1275,8 +1281,20 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_xs_kernel(
     for (int ii = 0; ii < 8; ii++) {
       const int ts = 2 * ii + st;
       uint8_t *dst = xl + ((sm * 2 + sh) * 64 + sg * 16 + (ts ^ (2 * sg + sh))) * 16;
-      *reinterpret_cast<u32x4 *>(dst) = xs[ii];
-      if constexpr (XS == XS_PLANES) *reinterpret_cast<u32x4 *>(dst + XS_QUAD_BYTES) = xs[8 + ii];
+      if constexpr (XS == XS_F32) {
+        if (2 * ii >= B) continue;  // wave-uniform
+        const u32x4 a = xs[2 * ii], b = xs[2 * ii + 1];
+        uint32_t hi[4], lo[4];
+        split2_bf16(__uint_as_float(a.x), __uint_as_float(a.y), hi[0], lo[0]);
+        split2_bf16(__uint_as_float(a.z), __uint_as_float(a.w), hi[1], lo[1]);
+        split2_bf16(__uint_as_float(b.x), __uint_as_float(b.y), hi[2], lo[2]);
+        split2_bf16(__uint_as_float(b.z), __uint_as_float(b.w), hi[3], lo[3]);
+        *reinterpret_cast<u32x4 *>(dst) = (u32x4){hi[0], hi[1], hi[2], hi[3]};
+        *reinterpret_cast<u32x4 *>(dst + XS_QUAD_BYTES) = (u32x4){lo[0], lo[1], lo[2], lo[3]};
+      } else {
+        *reinterpret_cast<u32x4 *>(dst) = xs[ii];
+        if constexpr (XS == XS_PLANES) *reinterpret_cast<u32x4 *>(dst + XS_QUAD_BYTES) = xs[8 + ii];
+      }
     }
   };
   u32x4 xs[NL];
@@ -1823,6 +1841,10 @@ hipError_t launch_gemv(const uint32_t *w, const float *scale, const void *x,
     if (yt_bf16) return launch_gemv_t<uint16_t, uint16_t, L>(w, scale, w, scale, x, y, B, K, N, stream);
     return launch_gemv_t<uint16_t, float, L>(w, scale, w, scale, x, y, B, K, N, stream);
   }
+  if (gemv_xs_ok(x, B, K, 2, 1)) {  // fp32 x, 2 to 16 tokens: staged as bf16 hi/lo planes
+    if (yt_bf16) return launch_gemv_xs<uint16_t, 1, L, XS_F32, false>(w, scale, w, scale, x, x, y, B, K, N, stream);
+    return launch_gemv_xs<float, 1, L, XS_F32, false>(w, scale, w, scale, x, x, y, B, K, N, stream);
+  }
   if (yt_bf16) return launch_gemv_t<float, uint16_t, L>(w, scale, w, scale, x, y, B, K, N, stream);
   return launch_gemv_t<float, float, L>(w, scale, w, scale, x, y, B, K, N, stream);
 }
@@ -1836,6 +1858,13 @@ hipError_t launch_gemv_glu(const uint32_t *w_gate, const float *s_gate, const ui
                                                                    stream);
     return launch_gemv_xs<float, 2, GEMV_SWIGLU, XS_BF16, false>(w_gate, s_gate, w_up, s_up, x, x, h, B, K, N,
                                                                   stream);
+  }
+  if (!xt_bf16 && B >= 2 && gemv_xs_ok(x, B, K, 2, 2)) {
+    if (gelu)
+      return launch_gemv_xs<float, 2, GEMV_GEGLU, XS_F32, false>(w_gate, s_gate, w_up, s_up, x, x, h, B, K, N,
+                                                                  stream);
+    return launch_gemv_xs<float, 2, GEMV_SWIGLU, XS_F32, false>(w_gate, s_gate, w_up, s_up, x, x, h, B, K, N,
+                                                                 stream);
   }
   if (xt_bf16 && B >= GEMV_DIRECT_MIN_B) {
     if (gelu) return launch_gemv_direct<float, GEMV_GEGLU>(w_gate, s_gate, w_up, s_up, x, x, h, B, K, N, stream);

@@ -72,9 +72,12 @@ def _dyadic_case(M, K, N, seed):
     return t, synth.pack_rows_u32(t), s, x, synth.f32_to_bf16_bits(x)
 
 
-@pytest.mark.parametrize("M,K,N", [(1, 4096, 11008), (16, 11008, 4096), (7, 2048, 2048), (300, 4096, 1000),
+@pytest.mark.parametrize("M,K,N", [(1, 4096, 11008), (1, 11008, 4096), (4, 4096, 11008), (4, 11008, 4096),
+                                   (16, 4096, 11008), (16, 11008, 4096), (7, 2048, 2048), (300, 4096, 1000),
                                    (2048, 4096, 4096)])
 def test_dense_bit_exact_on_dyadic_inputs(ctx, M, K, N):
+    """bf16 and f32 activations (the f32 drop-in path of TernaryMatMulOp,
+    split into bf16 hi/lo planes) at the decode shapes and token counts."""
     t, w, s, x, xb = _dyadic_case(M, K, N, M + K + N)
     ref = (x @ t.T.astype(np.float32)) * s[None, :]
     for xt in ("bf16", "f32"):
