@@ -56,6 +56,7 @@ _SIGS = {
     "frx_status_string": (ctypes.c_char_p, [_int]),
     "frx_version": (ctypes.c_char_p, []),
     "frx_ternary_linear": (_int, [_vp, _vp, _vp, _vp, _int, _vp, _int, _u32, _u32, _u32]),
+    "frx_ternary_linear_bias": (_int, [_vp, _vp, _vp, _vp, _vp, _int, _vp, _int, _u32, _u32, _u32]),
     "frx_sparse24_ternary_linear": (_int, [_vp, _vp, _vp, _vp, _int, _vp, _int, _u32, _u32, _u32]),
     "frx_ternary_linear_blocked": (_int, [_vp, _vp, _vp, _u32, _vp, _int, _vp, _int, _u32, _u32, _u32]),
     "frx_ternary_sparse_decode": (_int, [_vp, _vp, _vp, _vp, _vp, ctypes.c_float, _vp, _int, _vp, _int,
@@ -295,11 +296,20 @@ class Context:
         _check(lib().frx_synchronize(self._h), self._h)
 
     # TernaryMatMulOp::dispatch analogue; all tensors on the device.
-    def ternary_linear(self, w, scale, x, y):
+    def ternary_linear(self, w, scale, x, y, bias=None):
+        """frx_ternary_linear; with bias ([N] f32) frx_ternary_linear_bias
+        (TernaryLinear::forward with a bias, ternary_linear.rs:94-115)."""
         M, K = _shape2(x, "x")
         N = _rows(w, K // 16, "w") if K % 16 == 0 else int(w.shape[0])
         _expect_numel(scale, N, "scale")
         _expect_shape(y, (M, N), "y")
+        if bias is not None:
+            _expect_numel(bias, N, "bias")
+            if _dtype_code(bias) != FRX_F32:
+                raise TypeError("bias must be float32")
+            _check(lib().frx_ternary_linear_bias(self._h, _ptr(w), _ptr(scale), _ptr(bias), _ptr(x),
+                                                 _dtype_code(x), _ptr(y), _dtype_code(y), M, K, N), self._h)
+            return y
         _check(lib().frx_ternary_linear(self._h, _ptr(w), _ptr(scale), _ptr(x), _dtype_code(x),
                                         _ptr(y), _dtype_code(y), M, K, N), self._h)
         return y

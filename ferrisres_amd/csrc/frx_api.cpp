@@ -236,20 +236,33 @@ static frx_status check_linear(frx_ctx *ctx, const void *w, const void *scale,
   return FRX_OK;
 }
 
-frx_status frx_ternary_linear(frx_ctx *ctx, const uint32_t *w,
-                              const float *scale, const void *x, frx_dtype xt,
-                              void *y, frx_dtype yt, uint32_t M, uint32_t K,
-                              uint32_t N) {
+static frx_status ternary_linear_run(frx_ctx *ctx, const uint32_t *w, const float *scale, const float *bias,
+                                     const void *x, frx_dtype xt, void *y, frx_dtype yt, uint32_t M, uint32_t K,
+                                     uint32_t N) {
   frx_status st = enter(ctx);
   if (st != FRX_OK) return st;
   if ((st = check_linear(ctx, w, scale, x, xt, y, yt, M, K, N, false)) != FRX_OK) return st;
   hipError_t e;
   if (M <= 16)
-    e = frx::launch_gemv(w, scale, x, xt == FRX_BF16, y, yt == FRX_BF16, (int)M, (int)K, (int)N, ctx->stream);
+    e = frx::launch_gemv(w, scale, x, xt == FRX_BF16, y, yt == FRX_BF16, (int)M, (int)K, (int)N, ctx->stream, bias);
   else
-    e = frx::launch_gemm(w, scale, x, xt == FRX_BF16, y, yt == FRX_BF16, (int)M, (int)K, (int)N, 0, ctx->stream);
+    e = frx::launch_gemm(w, scale, x, xt == FRX_BF16, y, yt == FRX_BF16, (int)M, (int)K, (int)N, 0, ctx->stream,
+                         bias);
   if (e != hipSuccess) return hip_fail(ctx, e, "ternary_linear launch");
   return FRX_OK;
+}
+
+frx_status frx_ternary_linear(frx_ctx *ctx, const uint32_t *w,
+                              const float *scale, const void *x, frx_dtype xt,
+                              void *y, frx_dtype yt, uint32_t M, uint32_t K,
+                              uint32_t N) {
+  return ternary_linear_run(ctx, w, scale, nullptr, x, xt, y, yt, M, K, N);
+}
+
+frx_status frx_ternary_linear_bias(frx_ctx *ctx, const uint32_t *w, const float *scale, const float *bias,
+                                   const void *x, frx_dtype xt, void *y, frx_dtype yt, uint32_t M, uint32_t K,
+                                   uint32_t N) {
+  return ternary_linear_run(ctx, w, scale, bias, x, xt, y, yt, M, K, N);
 }
 
 frx_status frx_sparse24_ternary_linear(frx_ctx *ctx, const uint32_t *meta,

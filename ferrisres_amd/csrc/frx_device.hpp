@@ -217,6 +217,22 @@ __device__ __forceinline__ float act_gelu_tanh(float x) {
   return 0.5f * x * (1.0f + tanhf(inner));
 }
 
+// Output bias, added to the scaled f32 result as a separate rounding step:
+// the layer computes y = (alpha * sum) + bias in two f32 operations, so the
+// product must not fuse with the addition into one multiply-add.
+__device__ __forceinline__ float add_bias(float v, float b) {
+#pragma clang fp contract(off)
+  return v + b;
+}
+
+// Bias of output rows n..n+3 (rows past N read row N-1; their stores are
+// masked).
+__device__ __forceinline__ f32x4 add_bias4(f32x4 v, const float *bias, int n, int N) {
+#pragma unroll
+  for (int j = 0; j < 4; j++) v[j] = add_bias(v[j], bias[min(n + j, N - 1)]);
+  return v;
+}
+
 // Output stores of 4 consecutive columns.
 template <typename YT>
 struct YStore;

@@ -30,7 +30,7 @@ template <int BM, int BN, int WM, int WN, int XS, int WF, typename YT>
 __global__ __launch_bounds__(WM *WN * 64) void gemm_kernel(
     const uint32_t *__restrict__ W, const float *__restrict__ scale,
     const void *__restrict__ X, YT *__restrict__ Y, int M, int K, int N,
-    int wvec) {
+    int wvec, const float *__restrict__ bias) {
   using Core = GemmCore<BM, BN, WM, WN, XS, 1, WF>;
   __shared__ __align__(16) uint32_t lds[Core::LDS_DWORDS];
   int nt, mt;
@@ -52,7 +52,11 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_kernel(
 #pragma unroll
     for (int fm = 0; fm < Core::FM; fm++) {
       const int m = m0 + Core::tok(fm);
-      if (m < M) YStore<YT>::store4(Y + (size_t)m * N + n, acc[0][fn][fm] * sc, nok);
+      if (m < M) {
+        f32x4 v = acc[0][fn][fm] * sc;
+        if (bias) v = add_bias4(v, bias, n, N);
+        YStore<YT>::store4(Y + (size_t)m * N + n, v, nok);
+      }
     }
   }
 }
@@ -61,7 +65,8 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm_kernel(
 template <int BM, int BN, int WM, int WN, int NS, typename YT>
 __global__ __launch_bounds__(WM *WN * 64) void gemm2_kernel(
     const uint32_t *__restrict__ W, const float *__restrict__ scale,
-    const uint16_t *__restrict__ X, YT *__restrict__ Y, int M, int K, int N) {
+    const uint16_t *__restrict__ X, YT *__restrict__ Y, int M, int K, int N,
+    const float *__restrict__ bias) {
   using Core = Gemm2<BM, BN, WM, WN, NS, false>;
   extern __shared__ __align__(16) uint32_t lds[];  // Core::LDS_DWORDS
   int nt, mt;
@@ -71,7 +76,7 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm2_kernel(
   const int m_count = min(BM, M - m0), n_count = min(BN, N - n0);
   Core::run(lds, X + (size_t)m0 * K, (uint32_t)m_count * (uint32_t)K * 2u, nullptr, m_count,
             W + (size_t)n0 * (K >> 4), n_count, K, acc);
-  Core::template store_tile<YT>(lds, acc, scale, Y, (size_t)N, m0, m_count, n0, n_count);
+  Core::template store_tile<YT>(lds, acc, scale, Y, (size_t)N, m0, m_count, n0, n_count, bias);
 }
 
 // 2:4 weights (GPU 5-bit layout), bf16 activations, K % 64 == 0: the
@@ -79,7 +84,8 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm2_kernel(
 template <int BM, int BN, int WM, int WN, int NS, typename YT>
 __global__ __launch_bounds__(WM *WN * 64) void gemm2sp_kernel(
     const uint32_t *__restrict__ meta, const float *__restrict__ scale,
-    const uint16_t *__restrict__ X, YT *__restrict__ Y, int M, int K, int N) {
+    const uint16_t *__restrict__ X, YT *__restrict__ Y, int M, int K, int N,
+    const float *__restrict__ bias) {
   using Core = Gemm2<BM, BN, WM, WN, NS, false>;
   extern __shared__ __align__(16) uint32_t lds[];
   int nt, mt;
@@ -90,7 +96,7 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm2sp_kernel(
   const int m_count = min(BM, M - m0), n_count = min(BN, N - n0);
   Core::run_sp(lds, X + (size_t)m0 * K, (uint32_t)m_count * (uint32_t)K * 2u, m_count,
                meta + (size_t)n0 * wpr, n_count, K, wpr, acc);
-  Core::template store_tile<YT>(lds, acc, scale, Y, (size_t)N, m0, m_count, n0, n_count);
+  Core::template store_tile<YT>(lds, acc, scale, Y, (size_t)N, m0, m_count, n0, n_count, bias);
 }
 
 #ifndef FRX_GEMM2_NS
@@ -135,7 +141,7 @@ static int device_cus() {
 
 template <int BM, typename YT, int BN = 256>
 static hipError_t launch_gemm2_bm(const uint32_t *w, const float *scale, const void *x, void *y,
-                                  int M, int K, int N, hipStream_t stream) {
+                                  int M, int K, int N, hipStream_t stream, const float *bias) {
   constexpr int WM = FRX_GEMM2_WM, WN = 4 / FRX_GEMM2_WM, NS = FRX_GEMM2_NS;
   using Core = Gemm2<BM, BN, WM, WN, NS, false>;
   constexpr int lds = Core::LDS_DWORDS * 4;
@@ -145,7 +151,7 @@ static hipError_t launch_gemm2_bm(const uint32_t *w, const float *scale, const v
   if (e != hipSuccess) return e;
   dim3 grid((N + BN - 1) / BN, (M + BM - 1) / BM);
   hipLaunchKernelGGL((gemm2_kernel<BM, BN, WM, WN, NS, YT>), grid, dim3(WM * WN * 64), lds, stream, w,
-                     scale, reinterpret_cast<const uint16_t *>(x), reinterpret_cast<YT *>(y), M, K, N);
+                     scale, reinterpret_cast<const uint16_t *>(x), reinterpret_cast<YT *>(y), M, K, N, bias);
   return hipGetLastError();
 }
 
@@ -156,21 +162,21 @@ static hipError_t launch_gemm2_bm(const uint32_t *w, const float *scale, const v
 // N = 11008 the 128-token tile stays ahead, 175 against 198 us).
 template <typename YT>
 static hipError_t launch_gemm2_t(const uint32_t *w, const float *scale, const void *x, void *y,
-                                 int M, int K, int N, hipStream_t stream) {
+                                 int M, int K, int N, hipStream_t stream, const float *bias) {
 #if FRX_GEMM2_WM == 1
   const long tiles128 = (long)((M + 127) / 128) * ((N + 255) / 256);
 #if FRX_GEMM2_SMALL_TILE == 1
-  if (tiles128 <= device_cus()) return launch_gemm2_bm<128, YT, 128>(w, scale, x, y, M, K, N, stream);
+  if (tiles128 <= device_cus()) return launch_gemm2_bm<128, YT, 128>(w, scale, x, y, M, K, N, stream, bias);
 #else
-  if (tiles128 <= device_cus()) return launch_gemm2_bm<64, YT>(w, scale, x, y, M, K, N, stream);
+  if (tiles128 <= device_cus()) return launch_gemm2_bm<64, YT>(w, scale, x, y, M, K, N, stream, bias);
 #endif
 #endif
-  return launch_gemm2_bm<128, YT>(w, scale, x, y, M, K, N, stream);
+  return launch_gemm2_bm<128, YT>(w, scale, x, y, M, K, N, stream, bias);
 }
 
 template <typename YT>
 static hipError_t launch_gemm2sp_t(const uint32_t *meta, const float *scale, const void *x, void *y,
-                                   int M, int K, int N, hipStream_t stream) {
+                                   int M, int K, int N, hipStream_t stream, const float *bias) {
   constexpr int BM = FRX_GEMM2_BM, BN = 256, WM = FRX_GEMM2_WM, WN = 4 / FRX_GEMM2_WM, NS = FRX_GEMM2_NS;
   using Core = Gemm2<BM, BN, WM, WN, NS, false>;
   constexpr int lds = Core::LDS_DWORDS * 4;
@@ -180,20 +186,20 @@ static hipError_t launch_gemm2sp_t(const uint32_t *meta, const float *scale, con
   if (e != hipSuccess) return e;
   dim3 grid((N + BN - 1) / BN, (M + BM - 1) / BM);
   hipLaunchKernelGGL((gemm2sp_kernel<BM, BN, WM, WN, NS, YT>), grid, dim3(WM * WN * 64), lds, stream, meta,
-                     scale, reinterpret_cast<const uint16_t *>(x), reinterpret_cast<YT *>(y), M, K, N);
+                     scale, reinterpret_cast<const uint16_t *>(x), reinterpret_cast<YT *>(y), M, K, N, bias);
   return hipGetLastError();
 }
 
 template <int XS, int WF, typename YT>
 static hipError_t launch_gemm_t(const uint32_t *w, const float *scale,
                                 const void *x, void *y, int M, int K, int N,
-                                hipStream_t stream) {
+                                hipStream_t stream, const float *bias) {
   constexpr int BM = 128, BN = 128, WM = 2, WN = 2;
   const int wvec = ((K >> 4) % 4 == 0) && ((reinterpret_cast<uintptr_t>(w) & 15) == 0);
   dim3 grid((N + BN - 1) / BN, (M + BM - 1) / BM);
   hipLaunchKernelGGL((gemm_kernel<BM, BN, WM, WN, XS, WF, YT>), grid,
                      dim3(WM * WN * 64), 0, stream, w, scale, x,
-                     reinterpret_cast<YT *>(y), M, K, N, wvec);
+                     reinterpret_cast<YT *>(y), M, K, N, wvec, bias);
   return hipGetLastError();
 }
 
@@ -201,28 +207,28 @@ template <int WF>
 static hipError_t launch_gemm_wf(const uint32_t *w, const float *scale,
                                  const void *x, int xt_bf16, void *y,
                                  int yt_bf16, int M, int K, int N,
-                                 hipStream_t stream) {
+                                 hipStream_t stream, const float *bias) {
   if (xt_bf16) {
-    if (yt_bf16) return launch_gemm_t<XS_BF16, WF, uint16_t>(w, scale, x, y, M, K, N, stream);
-    return launch_gemm_t<XS_BF16, WF, float>(w, scale, x, y, M, K, N, stream);
+    if (yt_bf16) return launch_gemm_t<XS_BF16, WF, uint16_t>(w, scale, x, y, M, K, N, stream, bias);
+    return launch_gemm_t<XS_BF16, WF, float>(w, scale, x, y, M, K, N, stream, bias);
   }
-  if (yt_bf16) return launch_gemm_t<XS_F32, WF, uint16_t>(w, scale, x, y, M, K, N, stream);
-  return launch_gemm_t<XS_F32, WF, float>(w, scale, x, y, M, K, N, stream);
+  if (yt_bf16) return launch_gemm_t<XS_F32, WF, uint16_t>(w, scale, x, y, M, K, N, stream, bias);
+  return launch_gemm_t<XS_F32, WF, float>(w, scale, x, y, M, K, N, stream, bias);
 }
 
 hipError_t launch_gemm(const uint32_t *w, const float *scale, const void *x,
                        int xt_bf16, void *y, int yt_bf16, int M, int K, int N,
-                       int sp24, hipStream_t stream) {
+                       int sp24, hipStream_t stream, const float *bias) {
   if (!sp24 && xt_bf16 && K % 64 == 0 && M > 16 && (reinterpret_cast<uintptr_t>(w) & 15) == 0) {
-    if (yt_bf16) return launch_gemm2_t<uint16_t>(w, scale, x, y, M, K, N, stream);
-    return launch_gemm2_t<float>(w, scale, x, y, M, K, N, stream);
+    if (yt_bf16) return launch_gemm2_t<uint16_t>(w, scale, x, y, M, K, N, stream, bias);
+    return launch_gemm2_t<float>(w, scale, x, y, M, K, N, stream, bias);
   }
   if (sp24 && xt_bf16 && K % 64 == 0 && M > 16) {
-    if (yt_bf16) return launch_gemm2sp_t<uint16_t>(w, scale, x, y, M, K, N, stream);
-    return launch_gemm2sp_t<float>(w, scale, x, y, M, K, N, stream);
+    if (yt_bf16) return launch_gemm2sp_t<uint16_t>(w, scale, x, y, M, K, N, stream, bias);
+    return launch_gemm2sp_t<float>(w, scale, x, y, M, K, N, stream, bias);
   }
-  if (sp24) return launch_gemm_wf<WF_SP24>(w, scale, x, xt_bf16, y, yt_bf16, M, K, N, stream);
-  return launch_gemm_wf<WF_DENSE>(w, scale, x, xt_bf16, y, yt_bf16, M, K, N, stream);
+  if (sp24) return launch_gemm_wf<WF_SP24>(w, scale, x, xt_bf16, y, yt_bf16, M, K, N, stream, bias);
+  return launch_gemm_wf<WF_DENSE>(w, scale, x, xt_bf16, y, yt_bf16, M, K, N, stream, bias);
 }
 
 }  // namespace frx

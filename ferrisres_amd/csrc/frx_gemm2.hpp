@@ -543,7 +543,7 @@ struct Gemm2 {
   template <typename YT>
   __device__ static void store_tile(uint32_t *lds, const f32x4 (&acc)[FN][FM],
                                     const float *scale, YT *Y, size_t ldy, int m0, int m_count,
-                                    int n0, int n_count) {
+                                    int n0, int n_count, const float *bias = nullptr) {
     constexpr int ES = sizeof(YT);
     constexpr int PF = BN + 16;  // LDS row pitch in floats
     constexpr int P = (BM / 2) * PF * 4 <= LDS_DWORDS * 4 ? 2 : 4;
@@ -561,6 +561,9 @@ struct Gemm2 {
     float sc[CE];
 #pragma unroll
     for (int e = 0; e < CE; e++) sc[e] = 0.5f * scale[n0 + min(nl + e, n_count - 1)];
+    float bv[CE];  // row bias (added after the scale, its own rounding)
+#pragma unroll
+    for (int e = 0; e < CE; e++) bv[e] = bias ? bias[n0 + min(nl + e, n_count - 1)] : 0.f;
     const bool vec = ((reinterpret_cast<uintptr_t>(Y) | (ldy * ES) | ((size_t)n0 * ES)) & 15) == 0;
     const bool full = vec && nl + CE <= n_count;
 #pragma unroll
@@ -584,6 +587,10 @@ struct Gemm2 {
           v[e + 1] = q.y * sc[e + 1];
           v[e + 2] = q.z * sc[e + 2];
           v[e + 3] = q.w * sc[e + 3];
+        }
+        if (bias) {
+#pragma unroll
+          for (int e = 0; e < CE; e++) v[e] = add_bias(v[e], bv[e]);
         }
         YT *d = Y + (size_t)(m0 + m) * ldy + n0 + nl;
         if constexpr (ES == 4) {

@@ -82,7 +82,7 @@ __attribute__((amdgpu_waves_per_eu(WAVES == 8 && sizeof(XT) == 2 && EPI == 0 ? 6
     const uint32_t *__restrict__ W, const float *__restrict__ scale,
     const uint32_t *__restrict__ W2, const float *__restrict__ scale2,
     const XT *__restrict__ X, YT *__restrict__ Y, int B, int K, int N, int KS,
-    int rs) {
+    int rs, const float *__restrict__ bias) {
   constexpr int P = XBlock<XT>::P;
   constexpr int NW = EPI == GEMV_LINEAR ? 1 : 2;  // weight matrices
   extern __shared__ __align__(16) uint32_t lds[];
@@ -264,6 +264,8 @@ __attribute__((amdgpu_waves_per_eu(WAVES == 8 && sizeof(XT) == 2 && EPI == 0 ? 6
           v[j] = a * s[1][j];
         }
       }
+      if constexpr (NW == 1)
+        if (bias) v = add_bias4(v, bias, n_out, N);
       YStore<YT>::store4(Y + (size_t)t * N + n_out, v, min(4, N - n_out));
     }
   }
@@ -272,7 +274,7 @@ __attribute__((amdgpu_waves_per_eu(WAVES == 8 && sizeof(XT) == 2 && EPI == 0 ? 6
 template <typename XT, typename YT, int WAVES, int UMAX, bool VEC, int EPI>
 static hipError_t launch_gemv_w(const uint32_t *w, const float *scale, const uint32_t *w2,
                                 const float *scale2, const void *x, void *y, int B, int K, int N,
-                                hipStream_t stream) {
+                                hipStream_t stream, const float *bias) {
   constexpr int P = XBlock<XT>::P;
   constexpr int NW = EPI == GEMV_LINEAR ? 1 : 2;
   // K slices (multiples of 256 columns) small enough that the rows fit the
@@ -286,14 +288,14 @@ static hipError_t launch_gemv_w(const uint32_t *w, const float *scale, const uin
   dim3 grid((N + 15) / 16);
   hipLaunchKernelGGL((gemv_kernel<XT, YT, WAVES, UMAX, VEC, EPI>), grid, dim3(WAVES * 64), lds, stream,
                      w, scale, w2, scale2, reinterpret_cast<const XT *>(x), reinterpret_cast<YT *>(y),
-                     B, K, N, KS, rs);
+                     B, K, N, KS, rs, bias);
   return hipGetLastError();
 }
 
 template <typename XT, typename YT, int EPI>
 static hipError_t launch_gemv_t(const uint32_t *w, const float *scale, const uint32_t *w2,
                                 const float *scale2, const void *x, void *y, int B, int K, int N,
-                                hipStream_t stream) {
+                                hipStream_t stream, const float *bias = nullptr) {
   // Waves per tile grow with K so that each wave holds two to three quads
   // (short per-wave work after its loads land, many waves in flight, and few
   // enough registers that every workgroup of the decode shapes is resident
@@ -302,8 +304,8 @@ static hipError_t launch_gemv_t(const uint32_t *w, const float *scale, const uin
   const bool vec = ((K >> 4) & 3) == 0 && (reinterpret_cast<uintptr_t>(w) & 15) == 0 &&
                    (reinterpret_cast<uintptr_t>(w2) & 15) == 0;
 #define FRX_GEMV_LAUNCH(WV, UM)                                                                  \
-  return vec ? launch_gemv_w<XT, YT, WV, UM, true, EPI>(w, scale, w2, scale2, x, y, B, K, N, stream) \
-             : launch_gemv_w<XT, YT, WV, UM, false, EPI>(w, scale, w2, scale2, x, y, B, K, N, stream)
+  return vec ? launch_gemv_w<XT, YT, WV, UM, true, EPI>(w, scale, w2, scale2, x, y, B, K, N, stream, bias) \
+             : launch_gemv_w<XT, YT, WV, UM, false, EPI>(w, scale, w2, scale2, x, y, B, K, N, stream, bias)
   const int nq = (K + 255) / 256;
   if (nq <= 8) FRX_GEMV_LAUNCH(4, 2);
   if (nq <= 16) FRX_GEMV_LAUNCH(8, 2);
@@ -350,7 +352,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_direct_kernel(
     const uint32_t *__restrict__ W, const float *__restrict__ scale,
     const uint32_t *__restrict__ W2, const float *__restrict__ scale2,
     const uint16_t *__restrict__ X, const uint16_t *__restrict__ X2, YT *__restrict__ Y, int B,
-    int K, int N) {
+    int K, int N, const float *__restrict__ bias) {
   static_assert(XPL == 1 || XPL == 2, "activation planes");
   static_assert(!YSPLIT || sizeof(YT) == 2, "split output is two bf16 planes");
   constexpr int NW = EPI == GEMV_LINEAR ? 1 : 2;
@@ -488,6 +490,8 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_direct_kernel(
         YStore<uint16_t>::store4(reinterpret_cast<uint16_t *>(Y) + (size_t)B * N + (size_t)r * N + n_out,
                                  lo, min(4, N - n_out));
       } else {
+        if constexpr (NW == 1)
+          if (bias) v = add_bias4(v, bias, n_out, N);
         YStore<YT>::store4(Y + (size_t)r * N + n_out, v, min(4, N - n_out));
       }
     }
@@ -497,11 +501,11 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_direct_kernel(
 template <typename YT, int WAVES, int UMAX, int D, bool VEC, int EPI, int XPL, bool YSPLIT>
 static hipError_t launch_gemv_d(const uint32_t *w, const float *scale, const uint32_t *w2,
                                 const float *scale2, const void *x, const void *x2, void *y, int B,
-                                int K, int N, hipStream_t stream) {
+                                int K, int N, hipStream_t stream, const float *bias) {
   hipLaunchKernelGGL((gemv_direct_kernel<YT, WAVES, UMAX, D, VEC, EPI, XPL, YSPLIT>),
                      dim3((N + 15) / 16), dim3(WAVES * 64), 0, stream, w, scale, w2, scale2,
                      reinterpret_cast<const uint16_t *>(x), reinterpret_cast<const uint16_t *>(x2),
-                     reinterpret_cast<YT *>(y), B, K, N);
+                     reinterpret_cast<YT *>(y), B, K, N, bias);
   return hipGetLastError();
 }
 
@@ -522,7 +526,7 @@ static hipError_t launch_gemv_d(const uint32_t *w, const float *scale, const uin
 template <typename YT, int WAVES, int UMAX, int D, bool VEC, int RS>
 __global__ __launch_bounds__(WAVES * 64) void gemv_tall_kernel(
     const uint32_t *__restrict__ W, const float *__restrict__ scale, const uint16_t *__restrict__ X,
-    YT *__restrict__ Y, int B, int K, int N) {
+    YT *__restrict__ Y, int B, int K, int N, const float *__restrict__ bias) {
   constexpr int NWD = 4 * UMAX;  // weight words per lane and row block in one batch
   static_assert(D >= 1 && D <= NWD, "prefetch distance");
   __shared__ f32x4 red[RS * WAVES * 64];
@@ -616,16 +620,20 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_tall_kernel(
 #pragma unroll
     for (int w = 1; w < WAVES; w++) v += red[(rs * WAVES + w) * 64 + lane];
     const int n_out = n_base + 16 * rs + 4 * g;
-    if (live && n_out < N) YStore<YT>::store4(Y + (size_t)r * N + n_out, v * sc[rs] * 0.5f, min(4, N - n_out));
+    if (live && n_out < N) {
+      v = v * sc[rs] * 0.5f;
+      if (bias) v = add_bias4(v, bias, n_out, N);
+      YStore<YT>::store4(Y + (size_t)r * N + n_out, v, min(4, N - n_out));
+    }
   }
 }
 
 template <typename YT, int WAVES, int UMAX, int D, bool VEC, int RS>
 static hipError_t launch_gemv_tall_w(const uint32_t *w, const float *scale, const void *x, void *y, int B, int K,
-                                     int N, hipStream_t stream) {
+                                     int N, hipStream_t stream, const float *bias) {
   hipLaunchKernelGGL((gemv_tall_kernel<YT, WAVES, UMAX, D, VEC, RS>), dim3((N + 16 * RS - 1) / (16 * RS)),
                      dim3(WAVES * 64), 0, stream, w, scale, reinterpret_cast<const uint16_t *>(x),
-                     reinterpret_cast<YT *>(y), B, K, N);
+                     reinterpret_cast<YT *>(y), B, K, N, bias);
   return hipGetLastError();
 }
 
@@ -634,13 +642,13 @@ constexpr int GEMV_TALL_RS = 2;
 
 template <typename YT>
 static hipError_t launch_gemv_tall(const uint32_t *w, const float *scale, const void *x, void *y, int B, int K,
-                                   int N, hipStream_t stream) {
+                                   int N, hipStream_t stream, const float *bias) {
   constexpr int RS = GEMV_TALL_RS;
   const bool vec = ((K >> 4) & 3) == 0 && (reinterpret_cast<uintptr_t>(w) & 15) == 0;
   const int nq = (K + 255) / 256;
 #define FRX_GEMV_T(WV, UM)                                                                       \
-  return vec ? launch_gemv_tall_w<YT, WV, UM, 4, true, RS>(w, scale, x, y, B, K, N, stream) \
-             : launch_gemv_tall_w<YT, WV, UM, 4, false, RS>(w, scale, x, y, B, K, N, stream)
+  return vec ? launch_gemv_tall_w<YT, WV, UM, 4, true, RS>(w, scale, x, y, B, K, N, stream, bias) \
+             : launch_gemv_tall_w<YT, WV, UM, 4, false, RS>(w, scale, x, y, B, K, N, stream, bias)
   if (nq <= 8) FRX_GEMV_T(4, 2);
   if (nq <= 16) FRX_GEMV_T(8, 2);
   if (nq <= 48) FRX_GEMV_T(16, 3);
@@ -651,7 +659,7 @@ static hipError_t launch_gemv_tall(const uint32_t *w, const float *scale, const 
 template <typename YT, int EPI, int XPL = 1, bool YSPLIT = false>
 static hipError_t launch_gemv_direct(const uint32_t *w, const float *scale, const uint32_t *w2,
                                      const float *scale2, const void *x, const void *x2, void *y,
-                                     int B, int K, int N, hipStream_t stream) {
+                                     int B, int K, int N, hipStream_t stream, const float *bias = nullptr) {
   // Waves per tile as in gemv_kernel (two to three quads per wave). D words
   // of activations in flight per lane (8 registers per plane): 8 for the
   // 16-wave tiles (one workgroup per CU), 4 where several workgroups of a
@@ -660,9 +668,9 @@ static hipError_t launch_gemv_direct(const uint32_t *w, const float *scale, cons
                    (reinterpret_cast<uintptr_t>(w2) & 15) == 0;
 #define FRX_GEMV_D(WV, UM, DD)                                                                          \
   return vec ? launch_gemv_d<YT, WV, UM, DD, true, EPI, XPL, YSPLIT>(w, scale, w2, scale2, x, x2, y, B, K, \
-                                                                      N, stream)                        \
+                                                                      N, stream, bias)                  \
              : launch_gemv_d<YT, WV, UM, DD, false, EPI, XPL, YSPLIT>(w, scale, w2, scale2, x, x2, y, B,  \
-                                                                       K, N, stream)
+                                                                       K, N, stream, bias)
   const int nq = (K + 255) / 256;
   if (nq <= 8) FRX_GEMV_D(4, 2, 4);
   if (nq <= 16) FRX_GEMV_D(8, 2, 4);
@@ -715,7 +723,7 @@ template <typename YT, int WAVES, int RW, int NI, int NW = 1, int XPL = 1, int E
 __global__ __launch_bounds__(WAVES * 64) void gemv_rows_kernel(
     const uint32_t *__restrict__ W, const float *__restrict__ scale, const uint32_t *__restrict__ W2,
     const float *__restrict__ scale2, const uint16_t *__restrict__ X, const uint16_t *__restrict__ X2,
-    YT *__restrict__ Y, int K, int N) {
+    YT *__restrict__ Y, int K, int N, const float *__restrict__ bias) {
   static_assert((NW == 2) == (EPI != GEMV_LINEAR), "two matrices exactly for the GLU epilogues");
   extern __shared__ __align__(16) uint32_t lds[];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -825,10 +833,10 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_rows_kernel(
         split_bf16(h, hh, hl);
         Y[row] = (uint16_t)hh;
         Y[N + row] = (uint16_t)hl;
-      } else if constexpr (sizeof(YT) == 2) {
-        Y[row] = (uint16_t)bf16_rne(t[0]);
       } else {
-        Y[row] = t[0];
+        const float o = bias ? add_bias(t[0], bias[row]) : t[0];
+        if constexpr (sizeof(YT) == 2) Y[row] = (uint16_t)bf16_rne(o);
+        else Y[row] = o;
       }
     }
   }
@@ -836,7 +844,8 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_rows_kernel(
 
 template <typename YT, int RW, int NI, int NW = 1, int XPL = 1, int EPI = GEMV_LINEAR>
 static hipError_t launch_gemv_rows_w(const uint32_t *w, const float *scale, const uint32_t *w2, const float *scale2,
-                                     const void *x, const void *x2, void *y, int K, int N, hipStream_t stream) {
+                                     const void *x, const void *x2, void *y, int K, int N, hipStream_t stream,
+                                     const float *bias = nullptr) {
   constexpr int WAVES = 8;
   const dim3 grid((N + WAVES * RW - 1) / (WAVES * RW));
   const size_t lds = (size_t)XPL * NI * 64 * ROWS_XCH * 4;
@@ -848,7 +857,7 @@ static hipError_t launch_gemv_rows_w(const uint32_t *w, const float *scale, cons
   }
   hipLaunchKernelGGL((gemv_rows_kernel<YT, WAVES, RW, NI, NW, XPL, EPI>), grid, dim3(WAVES * 64), lds, stream, w,
                      scale, w2, scale2, reinterpret_cast<const uint16_t *>(x),
-                     reinterpret_cast<const uint16_t *>(x2), reinterpret_cast<YT *>(y), K, N);
+                     reinterpret_cast<const uint16_t *>(x2), reinterpret_cast<YT *>(y), K, N, bias);
   return hipGetLastError();
 }
 
@@ -869,7 +878,8 @@ static hipError_t launch_gemv_rows_w(const uint32_t *w, const float *scale, cons
 // MFMAs.
 template <typename YT, int NI, int RMAX, bool XF32>
 __global__ __launch_bounds__(512) void gemv_bal_kernel(const uint32_t *__restrict__ W, const float *__restrict__ scale,
-                                                       const void *__restrict__ Xv, YT *__restrict__ Y, int K, int N) {
+                                                       const void *__restrict__ Xv, YT *__restrict__ Y, int K, int N,
+                                                       const float *__restrict__ bias) {
   constexpr int WAVES = 8, NT = 512;
   constexpr int XPL = XF32 ? 2 : 1;
   constexpr int PP = NI * 512;                   // 8-value pieces of x staged (NI * 4096 values)
@@ -910,6 +920,7 @@ __global__ __launch_bounds__(512) void gemv_bal_kernel(const uint32_t *__restric
   float sc[RMAX];
 #pragma unroll
   for (int rr = 0; rr < RMAX; rr++) sc[rr] = scale[min(row0 + rr, N - 1)];
+  const float bv = bias ? bias[min(row0 + lane, N - 1)] : 0.f;  // lane's output row
   // 3. stage: piece j -> chunk j/8, slot j%8 (per plane)
 #pragma unroll
   for (int r = 0; r < XR; r++) {
@@ -985,6 +996,7 @@ __global__ __launch_bounds__(512) void gemv_bal_kernel(const uint32_t *__restric
     }
   }
   if (lane < cnt) {
+    if (bias) res = add_bias(res, bv);
     if constexpr (sizeof(YT) == 2) Y[row0 + lane] = (uint16_t)bf16_rne(res);
     else Y[row0 + lane] = res;
   }
@@ -997,7 +1009,7 @@ constexpr int GEMV_BAL_RMAX = 4;
 
 template <typename YT, int NI, int RMAX, bool XF32>
 static hipError_t launch_gemv_bal_w(const uint32_t *w, const float *scale, const void *x, void *y, int K, int N,
-                                    int G, hipStream_t stream) {
+                                    int G, hipStream_t stream, const float *bias) {
   const size_t lds = (size_t)(XF32 ? 2 : 1) * NI * 64 * ROWS_XCH * 4;
   if (lds > 64 * 1024) {
     static std::atomic<uint64_t> done;
@@ -1006,7 +1018,7 @@ static hipError_t launch_gemv_bal_w(const uint32_t *w, const float *scale, const
     if (e != hipSuccess) return e;
   }
   hipLaunchKernelGGL((gemv_bal_kernel<YT, NI, RMAX, XF32>), dim3(G), dim3(512), lds, stream, w, scale, x,
-                     reinterpret_cast<YT *>(y), K, N);
+                     reinterpret_cast<YT *>(y), K, N, bias);
   return hipGetLastError();
 }
 
@@ -1028,22 +1040,22 @@ static bool gemv_bal_grid(const uint32_t *w, const void *x, int B, int K, int N,
 
 template <typename YT, int NI, bool XF32>
 static hipError_t launch_gemv_bal_r(const uint32_t *w, const float *scale, const void *x, void *y, int K, int N, int G,
-                                    hipStream_t stream) {
+                                    hipStream_t stream, const float *bias) {
   const int rmax = ((N + G - 1) / G + 7) / 8;
-  if (rmax <= 1) return launch_gemv_bal_w<YT, NI, 1, XF32>(w, scale, x, y, K, N, G, stream);
-  if (rmax <= 2) return launch_gemv_bal_w<YT, NI, 2, XF32>(w, scale, x, y, K, N, G, stream);
-  if (rmax <= 3) return launch_gemv_bal_w<YT, NI, 3, XF32>(w, scale, x, y, K, N, G, stream);
-  return launch_gemv_bal_w<YT, NI, 4, XF32>(w, scale, x, y, K, N, G, stream);
+  if (rmax <= 1) return launch_gemv_bal_w<YT, NI, 1, XF32>(w, scale, x, y, K, N, G, stream, bias);
+  if (rmax <= 2) return launch_gemv_bal_w<YT, NI, 2, XF32>(w, scale, x, y, K, N, G, stream, bias);
+  if (rmax <= 3) return launch_gemv_bal_w<YT, NI, 3, XF32>(w, scale, x, y, K, N, G, stream, bias);
+  return launch_gemv_bal_w<YT, NI, 4, XF32>(w, scale, x, y, K, N, G, stream, bias);
 }
 
 template <typename YT, bool XF32>
 static hipError_t launch_gemv_bal(const uint32_t *w, const float *scale, const void *x, void *y, int K, int N, int G,
-                                  hipStream_t stream) {
+                                  hipStream_t stream, const float *bias) {
   const int ni = (K + 4095) / 4096;
-  if (ni == 1) return launch_gemv_bal_r<YT, 1, XF32>(w, scale, x, y, K, N, G, stream);
-  if (ni == 2) return launch_gemv_bal_r<YT, 2, XF32>(w, scale, x, y, K, N, G, stream);
-  if (ni == 3) return launch_gemv_bal_r<YT, 3, XF32>(w, scale, x, y, K, N, G, stream);
-  return launch_gemv_bal_r<YT, 4, XF32>(w, scale, x, y, K, N, G, stream);
+  if (ni == 1) return launch_gemv_bal_r<YT, 1, XF32>(w, scale, x, y, K, N, G, stream, bias);
+  if (ni == 2) return launch_gemv_bal_r<YT, 2, XF32>(w, scale, x, y, K, N, G, stream, bias);
+  if (ni == 3) return launch_gemv_bal_r<YT, 3, XF32>(w, scale, x, y, K, N, G, stream, bias);
+  return launch_gemv_bal_r<YT, 4, XF32>(w, scale, x, y, K, N, G, stream, bias);
 }
 
 // ---- tall single-token GEMV: persistent waves, next group in flight ------
@@ -1082,7 +1094,7 @@ __device__ __forceinline__ void rows_stream_load(__amdgpu_buffer_rsrc_t wr, cons
 template <typename YT, int RW, int NI>
 __device__ __forceinline__ void rows_stream_group(const uint32_t *lds, const u32x4 (&wv)[RW][NI],
                                                   const float (&sc)[RW], int g, int N, int lane,
-                                                  YT *__restrict__ Y) {
+                                                  YT *__restrict__ Y, const float *__restrict__ bias) {
   f32x4 acc[RW];
 #pragma unroll
   for (int rr = 0; rr < RW; rr++) acc[rr] = (f32x4){0.f, 0.f, 0.f, 0.f};
@@ -1123,6 +1135,7 @@ __device__ __forceinline__ void rows_stream_group(const uint32_t *lds, const u32
   }
   const int row = g * RW + lane;
   if (lane < RW && row < N) {
+    if (bias) t = add_bias(t, bias[row]);
     if constexpr (sizeof(YT) == 2) Y[row] = (uint16_t)bf16_rne(t);
     else Y[row] = t;
   }
@@ -1132,7 +1145,8 @@ template <typename YT, int WAVES, int RW, int NI>
 __global__ __launch_bounds__(WAVES * 64) void gemv_rows_stream_kernel(const uint32_t *__restrict__ W,
                                                                       const float *__restrict__ scale,
                                                                       const uint16_t *__restrict__ X,
-                                                                      YT *__restrict__ Y, int K, int N) {
+                                                                      YT *__restrict__ Y, int K, int N,
+                                                                      const float *__restrict__ bias) {
   extern __shared__ __align__(16) uint32_t lds[];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int kw = K >> 4, nxp = K >> 3;
@@ -1165,10 +1179,10 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_rows_stream_kernel(const uint
     const int g1 = g + stride, g2 = g1 + stride;
     rows_stream_load<RW, NI>(wr, scale, g1, ng, kw, N, lane, wb, sb);
     __builtin_amdgcn_sched_barrier(0);  // keep the prefetch ahead of the decode
-    rows_stream_group<YT, RW, NI>(lds, wa, sa, g, N, lane, Y);
+    rows_stream_group<YT, RW, NI>(lds, wa, sa, g, N, lane, Y, bias);
     rows_stream_load<RW, NI>(wr, scale, g2, ng, kw, N, lane, wa, sa);
     __builtin_amdgcn_sched_barrier(0);
-    if (g1 < ng) rows_stream_group<YT, RW, NI>(lds, wb, sb, g1, N, lane, Y);
+    if (g1 < ng) rows_stream_group<YT, RW, NI>(lds, wb, sb, g1, N, lane, Y, bias);
   }
 }
 
@@ -1186,13 +1200,13 @@ static int device_cu_count() {
 
 template <typename YT, int RW, int NI>
 static hipError_t launch_gemv_rows_stream(const uint32_t *w, const float *scale, const void *x, void *y, int K,
-                                          int N, hipStream_t stream) {
+                                          int N, hipStream_t stream, const float *bias) {
   constexpr int WAVES = 8;
   const int ng = (N + RW - 1) / RW;
   const int grid = std::min((ng + WAVES - 1) / WAVES, 2 * device_cu_count());
   const size_t lds = (size_t)NI * 64 * ROWS_XCH * 4;  // at most 36 KB (NI <= 4)
   hipLaunchKernelGGL((gemv_rows_stream_kernel<YT, WAVES, RW, NI>), dim3(grid), dim3(WAVES * 64), lds, stream, w,
-                     scale, reinterpret_cast<const uint16_t *>(x), reinterpret_cast<YT *>(y), K, N);
+                     scale, reinterpret_cast<const uint16_t *>(x), reinterpret_cast<YT *>(y), K, N, bias);
   return hipGetLastError();
 }
 
@@ -1237,7 +1251,7 @@ template <typename YT, int WAVES, int T, int UMAX, int NW, int EPI, int XS, bool
 __global__ __launch_bounds__(WAVES * 64) void gemv_xs_kernel(
     const uint32_t *__restrict__ W, const float *__restrict__ scale, const uint32_t *__restrict__ W2,
     const float *__restrict__ scale2, const void *__restrict__ Xv, const uint16_t *__restrict__ X2,
-    YT *__restrict__ Y, int B, int K, int N) {
+    YT *__restrict__ Y, int B, int K, int N, const float *__restrict__ bias) {
   static_assert((NW == 2) == (EPI != GEMV_LINEAR), "two matrices exactly for the GLU epilogues");
   static_assert(!YSPLIT || (NW == 2 && sizeof(YT) == 2), "split output is the GLU's bf16 planes");
   constexpr int XP = XS == XS_BF16 ? 1 : 2;  // planes staged per quad
@@ -1399,6 +1413,8 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_xs_kernel(
         YStore<uint16_t>::store4(reinterpret_cast<uint16_t *>(Y) + (size_t)t * N + n_out, hi, nok);
         YStore<uint16_t>::store4(reinterpret_cast<uint16_t *>(Y) + (size_t)B * N + (size_t)t * N + n_out, lo, nok);
       } else {
+        if constexpr (NW == 1)
+          if (bias) o = add_bias4(o, bias, n_out, N);
         YStore<YT>::store4(Y + (size_t)t * N + n_out, o, nok);
       }
     }
@@ -1408,7 +1424,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_xs_kernel(
 template <typename YT, int WAVES, int T, int UMAX, int NW, int EPI, int XS, bool YSPLIT>
 static hipError_t launch_gemv_xs_w(const uint32_t *w, const float *scale, const uint32_t *w2, const float *scale2,
                                    const void *x, const void *x2, void *y, int B, int K, int N, int G,
-                                   hipStream_t stream) {
+                                   hipStream_t stream, const float *bias) {
   constexpr int XP = XS == XS_BF16 ? 1 : 2;
   static_assert(NW * T * 1024 <= XP * XS_QUAD_BYTES, "the partial tiles reuse the staging area");
   const size_t lds = (size_t)WAVES * XP * XS_QUAD_BYTES;
@@ -1420,7 +1436,7 @@ static hipError_t launch_gemv_xs_w(const uint32_t *w, const float *scale, const 
   }
   hipLaunchKernelGGL((gemv_xs_kernel<YT, WAVES, T, UMAX, NW, EPI, XS, YSPLIT>), dim3(G), dim3(WAVES * 64), lds,
                      stream, w, scale, w2, scale2, x, reinterpret_cast<const uint16_t *>(x2),
-                     reinterpret_cast<YT *>(y), B, K, N);
+                     reinterpret_cast<YT *>(y), B, K, N, bias);
   return hipGetLastError();
 }
 
@@ -1448,11 +1464,12 @@ static int gemv_xs_grid(int N, int tmax) {
 // quads, so that a wave has 256 registers.
 template <typename YT, int NW, int EPI, int XS, bool YSPLIT>
 static hipError_t launch_gemv_xs(const uint32_t *w, const float *scale, const uint32_t *w2, const float *scale2,
-                                 const void *x, const void *x2, void *y, int B, int K, int N, hipStream_t stream) {
+                                 const void *x, const void *x2, void *y, int B, int K, int N, hipStream_t stream,
+                                 const float *bias = nullptr) {
   const int nq = (K + 255) / 256;
 #define FRX_XS(WV, TT, UM)                                                                                    \
   return launch_gemv_xs_w<YT, WV, TT, UM, NW, EPI, XS, YSPLIT>(w, scale, w2, scale2, x, x2, y, B, K, N, \
-                                                                gemv_xs_grid(N, TT), stream)
+                                                                gemv_xs_grid(N, TT), stream, bias)
 #define FRX_XS_T(WV, UM, TMAX)                                                               \
   {                                                                                          \
     const int tiles = ((N + gemv_xs_grid(N, TMAX) - 1) / gemv_xs_grid(N, TMAX) + 15) / 16; \
@@ -1507,7 +1524,8 @@ static hipError_t launch_gemv_xs(const uint32_t *w, const float *scale, const ui
 template <typename YT, int WAVES, int RW, int NI, int KS = 1, int NW = 1, int EPI = GEMV_LINEAR, bool VPL = false>
 __global__ __launch_bounds__(WAVES * 64) void gemv_rows4_kernel(
     const uint32_t *__restrict__ W, const float *__restrict__ scale, const uint32_t *__restrict__ W2,
-    const float *__restrict__ scale2, const uint16_t *__restrict__ X, YT *__restrict__ Y, int B, int K, int N) {
+    const float *__restrict__ scale2, const uint16_t *__restrict__ X, YT *__restrict__ Y, int B, int K, int N,
+    const float *__restrict__ bias) {
   static_assert((NW == 2) == (EPI != GEMV_LINEAR), "two matrices exactly for the GLU epilogues");
   static_assert(!(VPL && NW == 2), "planes feed the linear epilogue");
   extern __shared__ __align__(16) uint32_t lds[];
@@ -1628,7 +1646,8 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_rows4_kernel(
         Y[(size_t)tcol * N + row] = (uint16_t)hh;
         Y[(size_t)(B + tcol) * N + row] = (uint16_t)hl;
       } else {
-        const float yv = v[0] * sc[0][rr] * 0.5f;
+        float yv = v[0] * sc[0][rr] * 0.5f;
+        if (bias) yv = add_bias(yv, bias[row]);
         if constexpr (sizeof(YT) == 2) Y[(size_t)tcol * N + row] = (uint16_t)bf16_rne(yv);
         else Y[(size_t)tcol * N + row] = yv;
       }
@@ -1639,7 +1658,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_rows4_kernel(
 template <typename YT, int WAVES, int RW, int NI, int KS = 1, int NW = 1, int EPI = GEMV_LINEAR, bool VPL = false>
 static hipError_t launch_gemv_rows4_w(const uint32_t *w, const float *scale, const uint32_t *w2,
                                       const float *scale2, const void *x, void *y, int B, int K, int N,
-                                      hipStream_t stream) {
+                                      hipStream_t stream, const float *bias = nullptr) {
   constexpr int GW = WAVES / KS;
   const dim3 grid((N + GW * RW * 4 - 1) / (GW * RW * 4));
   const size_t lds =
@@ -1652,7 +1671,7 @@ static hipError_t launch_gemv_rows4_w(const uint32_t *w, const float *scale, con
   }
   hipLaunchKernelGGL((gemv_rows4_kernel<YT, WAVES, RW, NI, KS, NW, EPI, VPL>), grid, dim3(WAVES * 64), lds, stream,
                      w, scale, w2, scale2, reinterpret_cast<const uint16_t *>(x), reinterpret_cast<YT *>(y), B, K,
-                     N);
+                     N, bias);
   return hipGetLastError();
 }
 
@@ -1667,18 +1686,18 @@ static bool gemv_rows4_ok(const uint32_t *w, const void *x, int B, int K) {
 
 template <typename YT>
 static hipError_t launch_gemv_rows4(const uint32_t *w, const float *scale, const void *x, void *y, int B, int K,
-                                    int N, hipStream_t stream) {
+                                    int N, hipStream_t stream, const float *bias) {
   const int ni = (K + 1023) / 1024;
   // one 4-row group per wave and (above one window) each group's windows
   // split over two waves: 8 waves, 16 or 32 rows per workgroup, so N = 11008
   // gives 688 workgroups instead of 172 (11008x4096 at B = 4: 6.8 -> 6.0 us
   // per launch; 4096x11008: 7.04 -> 6.48 us against 4 waves of one group)
-  if (ni <= 1) return launch_gemv_rows4_w<YT, 8, 1, 1>(w, scale, w, scale, x, y, B, K, N, stream);
-  if (ni <= 2) return launch_gemv_rows4_w<YT, 8, 1, 2, 2>(w, scale, w, scale, x, y, B, K, N, stream);
-  if (ni <= 4) return launch_gemv_rows4_w<YT, 8, 1, 4, 2>(w, scale, w, scale, x, y, B, K, N, stream);
-  if (ni <= 8) return launch_gemv_rows4_w<YT, 8, 1, 8, 2>(w, scale, w, scale, x, y, B, K, N, stream);
-  if (ni <= 11) return launch_gemv_rows4_w<YT, 8, 1, 11, 2>(w, scale, w, scale, x, y, B, K, N, stream);
-  return launch_gemv_rows4_w<YT, 8, 1, 14, 2>(w, scale, w, scale, x, y, B, K, N, stream);
+  if (ni <= 1) return launch_gemv_rows4_w<YT, 8, 1, 1>(w, scale, w, scale, x, y, B, K, N, stream, bias);
+  if (ni <= 2) return launch_gemv_rows4_w<YT, 8, 1, 2, 2>(w, scale, w, scale, x, y, B, K, N, stream, bias);
+  if (ni <= 4) return launch_gemv_rows4_w<YT, 8, 1, 4, 2>(w, scale, w, scale, x, y, B, K, N, stream, bias);
+  if (ni <= 8) return launch_gemv_rows4_w<YT, 8, 1, 8, 2>(w, scale, w, scale, x, y, B, K, N, stream, bias);
+  if (ni <= 11) return launch_gemv_rows4_w<YT, 8, 1, 11, 2>(w, scale, w, scale, x, y, B, K, N, stream, bias);
+  return launch_gemv_rows4_w<YT, 8, 1, 14, 2>(w, scale, w, scale, x, y, B, K, N, stream, bias);
 }
 
 // Decode FFN of two bf16 tokens through the 4-segment kernels: gate/up/act
@@ -1736,26 +1755,26 @@ constexpr int GEMV_ROWS_TALL_N = 16384;  // rows from which waves persist over r
 
 template <typename YT>
 static hipError_t launch_gemv_rows(const uint32_t *w, const float *scale, const void *x, void *y, int K, int N,
-                                   hipStream_t stream) {
+                                   hipStream_t stream, const float *bias) {
   const int ni = (K + 4095) / 4096;
-  if (ni == 1) return launch_gemv_rows_w<YT, 2, 1>(w, scale, w, scale, x, x, y, K, N, stream);
+  if (ni == 1) return launch_gemv_rows_w<YT, 2, 1>(w, scale, w, scale, x, x, y, K, N, stream, bias);
   // Tall matrices (more rows than one residency pass holds at one row per
   // wave: 4 workgroups x 8 waves per CU), above one window per row.
   if (N >= GEMV_ROWS_TALL_N) {
     // persistent waves; buffer offsets are 32-bit with the out-of-range
     // marker above every weight byte
     if ((size_t)N * (size_t)K / 4 < (size_t)ROWS_STREAM_OOB) {
-      if (ni == 2) return launch_gemv_rows_stream<YT, 2, 2>(w, scale, x, y, K, N, stream);
-      if (ni == 3) return launch_gemv_rows_stream<YT, 1, 3>(w, scale, x, y, K, N, stream);
-      return launch_gemv_rows_stream<YT, 1, 4>(w, scale, x, y, K, N, stream);
+      if (ni == 2) return launch_gemv_rows_stream<YT, 2, 2>(w, scale, x, y, K, N, stream, bias);
+      if (ni == 3) return launch_gemv_rows_stream<YT, 1, 3>(w, scale, x, y, K, N, stream, bias);
+      return launch_gemv_rows_stream<YT, 1, 4>(w, scale, x, y, K, N, stream, bias);
     }
-    if (ni == 2) return launch_gemv_rows_w<YT, 2, 2>(w, scale, w, scale, x, x, y, K, N, stream);
-    if (ni == 3) return launch_gemv_rows_w<YT, 2, 3>(w, scale, w, scale, x, x, y, K, N, stream);
-    return launch_gemv_rows_w<YT, 2, 4>(w, scale, w, scale, x, x, y, K, N, stream);
+    if (ni == 2) return launch_gemv_rows_w<YT, 2, 2>(w, scale, w, scale, x, x, y, K, N, stream, bias);
+    if (ni == 3) return launch_gemv_rows_w<YT, 2, 3>(w, scale, w, scale, x, x, y, K, N, stream, bias);
+    return launch_gemv_rows_w<YT, 2, 4>(w, scale, w, scale, x, x, y, K, N, stream, bias);
   }
-  if (ni == 2) return launch_gemv_rows_w<YT, 1, 2>(w, scale, w, scale, x, x, y, K, N, stream);
-  if (ni == 3) return launch_gemv_rows_w<YT, 1, 3>(w, scale, w, scale, x, x, y, K, N, stream);
-  return launch_gemv_rows_w<YT, 1, 4>(w, scale, w, scale, x, x, y, K, N, stream);
+  if (ni == 2) return launch_gemv_rows_w<YT, 1, 2>(w, scale, w, scale, x, x, y, K, N, stream, bias);
+  if (ni == 3) return launch_gemv_rows_w<YT, 1, 3>(w, scale, w, scale, x, x, y, K, N, stream, bias);
+  return launch_gemv_rows_w<YT, 1, 4>(w, scale, w, scale, x, x, y, K, N, stream, bias);
 }
 
 // Decode FFN of one bf16 token through the rows kernels: gate/up/act into
@@ -1796,28 +1815,28 @@ hipError_t launch_gemv_rows_planes(const uint32_t *w, const float *scale, const 
 
 hipError_t launch_gemv(const uint32_t *w, const float *scale, const void *x,
                        int xt_bf16, void *y, int yt_bf16, int B, int K, int N,
-                       hipStream_t stream) {
+                       hipStream_t stream, const float *bias) {
   constexpr int L = GEMV_LINEAR;
   int G = 0;
   if (gemv_bal_grid(w, x, B, K, N, &G)) {
     if (xt_bf16) {
-      if (yt_bf16) return launch_gemv_bal<uint16_t, false>(w, scale, x, y, K, N, G, stream);
-      return launch_gemv_bal<float, false>(w, scale, x, y, K, N, G, stream);
+      if (yt_bf16) return launch_gemv_bal<uint16_t, false>(w, scale, x, y, K, N, G, stream, bias);
+      return launch_gemv_bal<float, false>(w, scale, x, y, K, N, G, stream, bias);
     }
-    if (yt_bf16) return launch_gemv_bal<uint16_t, true>(w, scale, x, y, K, N, G, stream);
-    return launch_gemv_bal<float, true>(w, scale, x, y, K, N, G, stream);
+    if (yt_bf16) return launch_gemv_bal<uint16_t, true>(w, scale, x, y, K, N, G, stream, bias);
+    return launch_gemv_bal<float, true>(w, scale, x, y, K, N, G, stream, bias);
   }
   if (xt_bf16 && gemv_rows_ok(w, x, B, K)) {
-    if (yt_bf16) return launch_gemv_rows<uint16_t>(w, scale, x, y, K, N, stream);
-    return launch_gemv_rows<float>(w, scale, x, y, K, N, stream);
+    if (yt_bf16) return launch_gemv_rows<uint16_t>(w, scale, x, y, K, N, stream, bias);
+    return launch_gemv_rows<float>(w, scale, x, y, K, N, stream, bias);
   }
   if (xt_bf16 && gemv_rows4_ok(w, x, B, K)) {
-    if (yt_bf16) return launch_gemv_rows4<uint16_t>(w, scale, x, y, B, K, N, stream);
-    return launch_gemv_rows4<float>(w, scale, x, y, B, K, N, stream);
+    if (yt_bf16) return launch_gemv_rows4<uint16_t>(w, scale, x, y, B, K, N, stream, bias);
+    return launch_gemv_rows4<float>(w, scale, x, y, B, K, N, stream, bias);
   }
   if (xt_bf16 && B >= GEMV_DIRECT_MIN_B && gemv_xs_ok(x, B, K, 1, 1)) {
-    if (yt_bf16) return launch_gemv_xs<uint16_t, 1, L, XS_BF16, false>(w, scale, w, scale, x, x, y, B, K, N, stream);
-    return launch_gemv_xs<float, 1, L, XS_BF16, false>(w, scale, w, scale, x, x, y, B, K, N, stream);
+    if (yt_bf16) return launch_gemv_xs<uint16_t, 1, L, XS_BF16, false>(w, scale, w, scale, x, x, y, B, K, N, stream, bias);
+    return launch_gemv_xs<float, 1, L, XS_BF16, false>(w, scale, w, scale, x, x, y, B, K, N, stream, bias);
   }
   if (xt_bf16 && B >= GEMV_DIRECT_MIN_B) {
     // taller tiles where their grid still covers every CU
@@ -1831,22 +1850,22 @@ hipError_t launch_gemv(const uint32_t *w, const float *scale, const void *x,
       cus.store(c, std::memory_order_relaxed);
     }
     if ((N + 16 * GEMV_TALL_RS - 1) / (16 * GEMV_TALL_RS) >= c) {
-      if (yt_bf16) return launch_gemv_tall<uint16_t>(w, scale, x, y, B, K, N, stream);
-      return launch_gemv_tall<float>(w, scale, x, y, B, K, N, stream);
+      if (yt_bf16) return launch_gemv_tall<uint16_t>(w, scale, x, y, B, K, N, stream, bias);
+      return launch_gemv_tall<float>(w, scale, x, y, B, K, N, stream, bias);
     }
-    if (yt_bf16) return launch_gemv_direct<uint16_t, L>(w, scale, w, scale, x, x, y, B, K, N, stream);
-    return launch_gemv_direct<float, L>(w, scale, w, scale, x, x, y, B, K, N, stream);
+    if (yt_bf16) return launch_gemv_direct<uint16_t, L>(w, scale, w, scale, x, x, y, B, K, N, stream, bias);
+    return launch_gemv_direct<float, L>(w, scale, w, scale, x, x, y, B, K, N, stream, bias);
   }
   if (xt_bf16) {
-    if (yt_bf16) return launch_gemv_t<uint16_t, uint16_t, L>(w, scale, w, scale, x, y, B, K, N, stream);
-    return launch_gemv_t<uint16_t, float, L>(w, scale, w, scale, x, y, B, K, N, stream);
+    if (yt_bf16) return launch_gemv_t<uint16_t, uint16_t, L>(w, scale, w, scale, x, y, B, K, N, stream, bias);
+    return launch_gemv_t<uint16_t, float, L>(w, scale, w, scale, x, y, B, K, N, stream, bias);
   }
   if (gemv_xs_ok(x, B, K, 2, 1)) {  // fp32 x, 2 to 16 tokens: staged as bf16 hi/lo planes
-    if (yt_bf16) return launch_gemv_xs<uint16_t, 1, L, XS_F32, false>(w, scale, w, scale, x, x, y, B, K, N, stream);
-    return launch_gemv_xs<float, 1, L, XS_F32, false>(w, scale, w, scale, x, x, y, B, K, N, stream);
+    if (yt_bf16) return launch_gemv_xs<uint16_t, 1, L, XS_F32, false>(w, scale, w, scale, x, x, y, B, K, N, stream, bias);
+    return launch_gemv_xs<float, 1, L, XS_F32, false>(w, scale, w, scale, x, x, y, B, K, N, stream, bias);
   }
-  if (yt_bf16) return launch_gemv_t<float, uint16_t, L>(w, scale, w, scale, x, y, B, K, N, stream);
-  return launch_gemv_t<float, float, L>(w, scale, w, scale, x, y, B, K, N, stream);
+  if (yt_bf16) return launch_gemv_t<float, uint16_t, L>(w, scale, w, scale, x, y, B, K, N, stream, bias);
+  return launch_gemv_t<float, float, L>(w, scale, w, scale, x, y, B, K, N, stream, bias);
 }
 
 hipError_t launch_gemv_glu(const uint32_t *w_gate, const float *s_gate, const uint32_t *w_up,

@@ -50,9 +50,11 @@ hipError_t launch_gemv_rows4_glu_planes(const uint32_t *w_gate, const float *s_g
                                         int gelu, hipStream_t stream);
 hipError_t launch_gemv_rows4_planes(const uint32_t *w, const float *scale, const uint16_t *x_planes, void *y,
                                     int yt_bf16, int K, int N, hipStream_t stream);
+// bias: optional per-row f32 bias [N] added to every token's output after
+// the scale (null: none).
 hipError_t launch_gemv(const uint32_t *w, const float *scale, const void *x,
                        int xt_bf16, void *y, int yt_bf16, int B, int K, int N,
-                       hipStream_t stream);
+                       hipStream_t stream, const float *bias = nullptr);
 // Decode FFN first half, B <= 16 tokens (frx_gemv.hip): h[B][N] (fp32) =
 // act(gate) * up with gate/up = (W x) * scale for two [N][K] matrices.
 hipError_t launch_gemv_glu(const uint32_t *w_gate, const float *s_gate, const uint32_t *w_up,
@@ -77,7 +79,7 @@ hipError_t launch_gemv_sp24(const uint32_t *meta, const float *scale,
 // Dense / 2:4 GEMM, any M (frx_gemm.hip). sp24 selects the metadata layout.
 hipError_t launch_gemm(const uint32_t *w, const float *scale, const void *x,
                        int xt_bf16, void *y, int yt_bf16, int M, int K, int N,
-                       int sp24, hipStream_t stream);
+                       int sp24, hipStream_t stream, const float *bias = nullptr);
 
 // One-launch decode FFN, M <= 3 tokens (frx_ffn.hip). ffn1_supported says
 // whether the shape fits the kernel on a device with `cus` compute units and

@@ -93,6 +93,22 @@ frx_status frx_ternary_linear(frx_ctx *ctx, const uint32_t *w,
                               void *y, frx_dtype yt, uint32_t M, uint32_t K,
                               uint32_t N);
 
+/* ---- dense ternary linear with bias ----------------------------------------
+ * Replaces TernaryLinear::forward / forward_packed / forward_decode with a
+ * bias (src/model/ternary_linear.rs:94-165): output = ternary_matmul(...)
+ * and then output[s][r] += bias[r] for every token s.
+ *   bias  [N] f32 device pointer, or NULL (then exactly frx_ternary_linear)
+ * y[m][n] = (scale[n] * sum_k dec(W[n][k]) x[m][k]) + bias[n], the product
+ * and the addition each rounded to f32 as the reference does (no fused
+ * multiply-add), then converted to yt. The bias is added inside the GEMV /
+ * GEMM epilogue (no extra launch). Same requirements as frx_ternary_linear;
+ * bias needs no particular alignment. */
+frx_status frx_ternary_linear_bias(frx_ctx *ctx, const uint32_t *w,
+                                   const float *scale, const float *bias,
+                                   const void *x, frx_dtype xt, void *y,
+                                   frx_dtype yt, uint32_t M, uint32_t K,
+                                   uint32_t N);
+
 /* ---- dense ternary linear with column-block scales --------------------------
  * Replaces ternary_matmul_blocked (src/model/ternary.rs:541-579): each block
  * of block_size input columns has its own scale, shared by all rows, and

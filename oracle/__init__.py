@@ -44,6 +44,7 @@ def lib():
             "frxo_ternary_matmul_decode": (None, [_vp, _f, _vp, _sz, _sz, _vp]),
             "frxo_ternary_matmul_packed": (None, [_vp, _f, _vp, _sz, _sz, _sz, _vp]),
             "frxo_ternary_matmul_packed_rows": (None, [_vp, _f, _vp, _sz, _sz, _sz, _sz, _vp]),
+            "frxo_ternary_linear_forward": (None, [_vp, _vp, _f, _vp, _vp, _sz, _sz, _sz, ctypes.c_int, _vp]),
             "frxo_ternary_matmul_blocked": (None, [_vp, _vp, _sz, _vp, _sz, _sz, _sz, _vp]),
             "frxo_ternary_sparse_indices": (None, [_vp, _sz, _sz, _vp, _vp, _vp, _vp]),
             "frxo_ternary_matmul_sparse_decode": (None, [_vp, _vp, _vp, _vp, _f, _vp, _sz, _vp]),
@@ -146,6 +147,20 @@ def ternary_matmul_packed(packed, scale, inp, out_rows, in_cols, seq):
     out = np.zeros(seq * out_rows, np.float32)
     lib().frxo_ternary_matmul_packed(_p(p), scale, _p(x), out_rows, in_cols, seq, _p(out))
     return out
+
+
+def ternary_linear_forward(ternary, scale, bias, inp, out_rows, in_cols, seq, path=0):
+    """TernaryLinear forward (path 0), forward_packed (1) or forward_decode (2)
+    with an optional bias [out_rows] (None: no bias)."""
+    t = _c(ternary, np.int8)
+    pk = pack_ternary(t) if path == 1 else np.zeros(1, np.uint8)
+    b = None if bias is None else _c(bias, np.float32)
+    x = _c(inp, np.float32)
+    n = 1 if path == 2 else seq
+    out = np.zeros(n * out_rows, np.float32)
+    lib().frxo_ternary_linear_forward(_p(t), _p(pk), scale, None if b is None else _p(b), _p(x),
+                                      out_rows, in_cols, n, path, _p(out))
+    return out.reshape(n, out_rows)
 
 
 def ternary_matmul_packed_parallel(packed, scale, inp, out_rows, in_cols):

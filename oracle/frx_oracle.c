@@ -185,6 +185,32 @@ void frxo_ternary_matmul_decode(const int8_t *ternary, float scale,
 }
 
 /*
+ * ternary_linear.rs:94-165 TernaryLinear::forward / forward_packed /
+ * forward_decode: the layer's matmul, then out[s*out_rows + r] += bias[r]
+ * for every token s (bias NULL: a layer without bias). path 0 = forward
+ * (ternary_matmul on the i8 values), 1 = forward_packed (the u8 packing of
+ * the same values), 2 = forward_decode (seq must be 1).
+ * Pinned by the hand-computed KAT of test_ternary_linear_bias_kat (2x3
+ * layer, bias [0.1, 0.2]), by bias NULL == the matmul alone, and by the
+ * three paths agreeing with bias (ternary_linear.rs:258-306).
+ */
+void frxo_ternary_linear_forward(const int8_t *ternary, const uint8_t *packed, float scale,
+                                 const float *bias, const float *input, size_t out_rows,
+                                 size_t in_cols, size_t seq, int path, float *out) {
+  if (path == 2) {
+    seq = 1;
+    frxo_ternary_matmul_decode(ternary, scale, input, out_rows, in_cols, out);
+  } else if (path == 1) {
+    frxo_ternary_matmul_packed(packed, scale, input, out_rows, in_cols, seq, out);
+  } else {
+    frxo_ternary_matmul_i8(ternary, scale, input, out_rows, in_cols, seq, out);
+  }
+  if (!bias) return;
+  for (size_t s = 0; s < seq; s++)
+    for (size_t r = 0; r < out_rows; r++) out[s * out_rows + r] += bias[r];
+}
+
+/*
  * ternary.rs:401-464 ternary_matmul_packed (u8 layout, per-tensor scale).
  * The byte index is (r*in_cols + 4q)/4 exactly as in the reference, so rows
  * with in_cols % 4 != 0 reproduce the reference's flat addressing.

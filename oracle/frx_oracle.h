@@ -43,6 +43,10 @@ void frxo_ternary_matmul_decode(const int8_t *ternary, float scale,
 void frxo_ternary_matmul_packed(const uint8_t *packed, float scale,
                                 const float *input, size_t out_rows,
                                 size_t in_cols, size_t seq, float *out);
+/* ternary_linear.rs:94-165: matmul (path 0 i8, 1 packed u8, 2 decode) + bias */
+void frxo_ternary_linear_forward(const int8_t *ternary, const uint8_t *packed, float scale,
+                                 const float *bias, const float *input, size_t out_rows,
+                                 size_t in_cols, size_t seq, int path, float *out);
 void frxo_ternary_matmul_packed_rows(const uint8_t *packed, float scale,
                                      const float *input, size_t out_rows,
                                      size_t in_cols, size_t row_begin,

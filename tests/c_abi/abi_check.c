@@ -20,6 +20,8 @@ static int failures = 0;
 /* Every declared function, taken by address with its declared type. */
 typedef frx_status (*linear_fn)(frx_ctx *, const uint32_t *, const float *, const void *, frx_dtype, void *,
                                 frx_dtype, uint32_t, uint32_t, uint32_t);
+typedef frx_status (*linear_bias_fn)(frx_ctx *, const uint32_t *, const float *, const float *, const void *,
+                                     frx_dtype, void *, frx_dtype, uint32_t, uint32_t, uint32_t);
 typedef frx_status (*ffn_fn)(frx_ctx *, const void *, frx_dtype, const uint32_t *, const float *,
                              const uint32_t *, const float *, const uint32_t *, const float *, uint32_t, uint32_t,
                              uint32_t, frx_activation, void *, frx_dtype);
@@ -27,10 +29,12 @@ typedef frx_status (*ffn_fn)(frx_ctx *, const void *, frx_dtype, const uint32_t 
 int main(void) {
   linear_fn lin = frx_ternary_linear;
   linear_fn sp = frx_sparse24_ternary_linear;
+  linear_bias_fn lin_b = frx_ternary_linear_bias;
   ffn_fn ffn = frx_ternary_ffn;
   ffn_fn ffn_na = frx_ternary_ffn_noalloc;
   (void)lin;
   (void)sp;
+  (void)lin_b;
   (void)ffn;
   (void)ffn_na;
 
@@ -65,6 +69,7 @@ int main(void) {
 
   /* error paths without a context or a GPU */
   EXPECT(frx_ternary_linear(NULL, NULL, NULL, NULL, FRX_F32, NULL, FRX_F32, 1, 16, 1) == FRX_ERR_DEVICE);
+  EXPECT(frx_ternary_linear_bias(NULL, NULL, NULL, NULL, NULL, FRX_F32, NULL, FRX_F32, 1, 16, 1) == FRX_ERR_DEVICE);
   EXPECT(frx_synchronize(NULL) == FRX_ERR_DEVICE);
   EXPECT(frx_set_stream(NULL, NULL) == FRX_ERR_DEVICE);
   EXPECT(strcmp(frx_last_error(NULL), "") == 0);

@@ -17,7 +17,7 @@ def _declared():
 
 def test_header_declares_expected_entry_points():
     names = _declared()
-    for must in ["frx_create", "frx_ternary_linear", "frx_sparse24_ternary_linear", "frx_moe_ternary_ffn",
+    for must in ["frx_create", "frx_ternary_linear", "frx_ternary_linear_bias", "frx_sparse24_ternary_linear", "frx_moe_ternary_ffn",
                  "frx_ternary_glu", "frx_ternary_ffn", "frx_set_ffn_mode", "frx_upload_ternary", "frx_upload_stm",
                  "frx_sparse24_cpu_to_gpu_device", "frx_free",
                  "frx_pack_ternary_u8", "frx_repack_u8_to_u32", "frx_pack_sparse24_gpu",

@@ -251,3 +251,80 @@ def test_shape_errors_are_statuses(ctx):
     with pytest.raises(frx.FrxError) as e:
         ctx.ternary_linear(w, s, x, y)  # K = 20 is not a multiple of 16
     assert e.value.kind == "Shape"
+
+
+# ---- TernaryLinear with a bias (frx_ternary_linear_bias) --------------------
+
+def _run_bias(ctx, w, s, bias, x, xb, xt, yt):
+    M, K = x.shape
+    N = w.shape[0]
+    xd = dev_bf16(xb) if xt == "bf16" else dev_f32(x)
+    y = torch.empty((M, N), dtype=torch.bfloat16 if yt == "bf16" else torch.float32, device="cuda:0")
+    y.fill_(float("nan"))
+    ctx.ternary_linear(dev_u32(w), dev_f32(s), xd, y, bias=None if bias is None else dev_f32(bias))
+    torch.cuda.synchronize()
+    return y
+
+
+# Every kernel family of the linear path: one token (balanced rows; whole
+# rows per wave, one-shot and persistent; 16-row tiles above 16384 columns),
+# 2-4 tokens, 5-7 tokens (16-row tiles), 8-16 tokens (staged activations;
+# above 16384 columns the per-lane operand loads, 16- and 32-row tiles), the
+# MFMA GEMM (K % 64 == 0 and not).
+BIAS_SHAPES = [(1, 2048, 2048), (1, 4096, 11008), (1, 11008, 4096), (1, 8256, 9000), (1, 4160, 16401),
+               (1, 16448, 40), (3, 4096, 300), (4, 11008, 4096), (6, 2048, 130), (16, 4096, 11008),
+               (16, 11008, 4096), (9, 16400, 40), (9, 16400, 8170), (64, 1040, 200), (300, 4096, 1000),
+               (2048, 4096, 4096)]
+
+
+@pytest.mark.parametrize("M,K,N", BIAS_SHAPES)
+def test_linear_bias_bit_exact_on_dyadic_inputs(ctx, M, K, N):
+    """y = (alpha * W x) + bias (ternary_linear.rs:94-115) with dyadic x and
+    codes, so every sum is exact; alpha and bias are random f32, which fixes
+    both roundings (the product, then the addition): a fused multiply-add
+    in an epilogue would differ in the last bit. The reference's layer has
+    one alpha for all rows. Against the oracle's TernaryLinear forward where
+    it finishes in seconds, else against the same two f32 operations on the
+    exact sums."""
+    t, w, _, x, xb = _dyadic_case(M, K, N, 7 * M + K + N)
+    rng = np.random.default_rng(M + K + 3 * N)
+    alpha = np.float32(rng.uniform(0.25, 2.0))
+    s = np.full(N, alpha, np.float32)
+    bias = rng.standard_normal(N).astype(np.float32)
+    if M * K * N <= 2e8:
+        ref = oracle.ternary_linear_forward(t, alpha, bias, x, N, K, M, 0)
+    else:
+        ref = ((x @ t.T.astype(np.float32)) * alpha).astype(np.float32) + bias[None, :]
+    for xt in ("bf16", "f32"):
+        y = host(_run_bias(ctx, w, s, bias, x, xb, xt, "f32"))
+        np.testing.assert_array_equal(y, ref)
+    yb = _run_bias(ctx, w, s, bias, x, xb, "bf16", "bf16").view(torch.int16).cpu().numpy().view(np.uint16)
+    np.testing.assert_array_equal(yb, synth.f32_to_bf16_bits(ref))
+
+
+@pytest.mark.parametrize("M,K,N", [(1, 2048, 2048), (4, 4096, 11008), (16, 11008, 4096), (2048, 2048, 2048)])
+def test_linear_bias_random_inputs(ctx, M, K, N):
+    """Normal f32 activations (hi/lo split) and bf16 activations with a
+    bias, against the oracle's TernaryLinear forward (rows sampled at
+    M = 2048), at the tolerance of the bias-free linear tests."""
+    name = f"bias/{M}x{K}x{N}"
+    t, w, _, xf, xb = _case(name, M, K, N)
+    alpha = np.float32(0.0371)
+    s = np.full(N, alpha, np.float32)
+    bias = synth.normal(synth.seed_of(name, "bias"), N).astype(np.float32)
+    rows = np.arange(M) if M <= 16 else np.array([0, 1, 127, 128, 1000, 2047])
+    ref = oracle.ternary_linear_forward(t, alpha, bias, xf[rows], N, K, len(rows), 0)
+    assert_close_f32(host(_run_bias(ctx, w, s, bias, xf, xb, "bf16", "f32"))[rows], ref)
+    x32 = synth.normal(synth.seed_of(name, "xf32"), M * K).reshape(M, K).astype(np.float32)
+    ref32 = oracle.ternary_linear_forward(t, alpha, bias, x32[rows], N, K, len(rows), 0)
+    assert_close_f32(host(_run_bias(ctx, w, s, bias, x32, xb, "f32", "f32"))[rows], ref32)
+
+
+def test_linear_bias_none_is_plain_linear(ctx):
+    t, w, s, xf, xb = _case("bias/none", 5, 1024, 96)
+    a = host(_run_bias(ctx, w, s, None, xf, xb, "bf16", "f32"))
+    b = host(_run(ctx, w, s, xf, xb, "bf16", "f32"))
+    np.testing.assert_array_equal(a, b)
+    zero = np.zeros(96, np.float32)
+    c = host(_run_bias(ctx, w, s, zero, xf, xb, "bf16", "f32"))
+    np.testing.assert_array_equal(c, b)

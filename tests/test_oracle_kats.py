@@ -164,3 +164,40 @@ def test_blocked_vs_scalar_kat():
             for j in range(b * bs, min((b + 1) * bs, cols)):
                 ref[r] = np.float32(ref[r] + np.float32(scales[b] * np.float32(t[r * cols + j])) * x[j])
     np.testing.assert_allclose(out, ref, rtol=0, atol=kat["tol"])
+
+
+def test_ternary_linear_bias_kat():
+    """ternary_linear.rs:308-324 (test_with_bias): the 2x3 layer
+    [1, -1, 0.5, -0.5, 1, 1] quantises (absmean, ternary.rs:31-57) to
+    [[1, -1, 0], [0, 1, 1]], so input [1, 2, 3] gives -alpha + 0.1 and
+    5 alpha + 0.2, each product and sum rounded to f32 once."""
+    t, alpha = oracle.quantize_ternary(np.array([1.0, -1.0, 0.5, -0.5, 1.0, 1.0], np.float32))
+    np.testing.assert_array_equal(t, [1, -1, 0, 0, 1, 1])
+    bias = np.array([0.1, 0.2], np.float32)
+    x = np.array([1.0, 2.0, 3.0], np.float32)
+    want = np.array([np.float32(-alpha) + bias[0], np.float32(alpha * np.float32(5.0)) + bias[1]], np.float32)
+    for path in (0, 2):  # forward, forward_decode
+        out = oracle.ternary_linear_forward(t, alpha, bias, x, 2, 3, 1, path)
+        np.testing.assert_array_equal(out.ravel(), want)
+        nob = oracle.ternary_linear_forward(t, alpha, None, x, 2, 3, 1, path)
+        np.testing.assert_array_equal(nob.ravel(), [-alpha, np.float32(alpha * np.float32(5.0))])
+
+
+def test_ternary_linear_paths_agree_with_bias():
+    """forward / forward_packed / forward_decode with the same bias
+    (ternary_linear.rs:258-306 pin the paths against each other without a
+    bias; in_cols % 4 == 0 so the packed path's flat byte addressing is
+    row-aligned), and seq tokens each get the bias once (:326-352)."""
+    rng = np.random.default_rng(7)
+    R, C, S = 6, 12, 3
+    t = rng.integers(-1, 2, size=(R, C)).astype(np.int8)
+    x = rng.standard_normal((S, C)).astype(np.float32)
+    bias = rng.standard_normal(R).astype(np.float32)
+    f = oracle.ternary_linear_forward(t, 0.37, bias, x, R, C, S, 0)
+    p = oracle.ternary_linear_forward(t, 0.37, bias, x, R, C, S, 1)
+    np.testing.assert_allclose(p, f, atol=1e-5, rtol=0)
+    nob = oracle.ternary_linear_forward(t, 0.37, None, x, R, C, S, 0)
+    np.testing.assert_array_equal(f, nob + bias[None, :])
+    for s in range(S):
+        d = oracle.ternary_linear_forward(t, 0.37, bias, x[s], R, C, 1, 2)
+        np.testing.assert_allclose(d.ravel(), f[s], atol=1e-5, rtol=0)
