@@ -72,6 +72,7 @@ _SIGS = {
                                        _int, _vp, _int]),
     "frx_set_ffn_mode": (_int, [_vp, _int]),
     "frx_set_moe_routing": (_int, [_vp, _int]),
+    "frx_force_status": (_int, [_vp, _int]),
     "frx_upload_ternary": (_int, [_vp, _vp, _u32, _u32, _vp, ctypes.c_float, ctypes.POINTER(_vp),
                                   ctypes.POINTER(_vp)]),
     "frx_upload_stm": (_int, [_vp, _vp, _sz, ctypes.POINTER(_vp), ctypes.POINTER(_vp), ctypes.POINTER(_u32),
@@ -440,6 +441,11 @@ class Context:
         """frx_set_moe_routing: MOE_TERNARY_MOE_LAYER (router [E,H], default)
         or MOE_CPU_MOE_LAYER (CpuMoELayer: router [H,E], top-k by logit)."""
         _check(lib().frx_set_moe_routing(self._h, routing), self._h)
+
+    def force_status(self, status: int):
+        """frx_force_status: every compute / upload call on this context
+        returns ``status`` (raised here as FrxError) until it is set to 0."""
+        _check(lib().frx_force_status(self._h, status), self._h)
 
     def set_ffn_mode(self, mode: int):
         """frx_set_ffn_mode: FFN_AUTO, FFN_ONE_LAUNCH or FFN_TWO_LAUNCH."""

@@ -49,7 +49,7 @@ hipError_t noalloc_scratch_ptr(int device, void **out) {
     if (e == hipSuccess) e = hipSetDevice(device);
     void *p = nullptr;
     if (e == hipSuccess) e = hipGetSymbolAddress(&p, HIP_SYMBOL(frx_noalloc_scratch));
-    if (prev != device) hipSetDevice(prev);
+    if (prev != device) (void)hipSetDevice(prev);
     g_noalloc_ptr[device] = e == hipSuccess ? p : nullptr;
     g_noalloc_err[device] = e;
     g_noalloc_done[device] = true;
@@ -87,6 +87,7 @@ struct frx_ctx {
   void *router_ws = nullptr;  // [E][H] copy of a [H][E] router (CpuMoELayer routing)
   size_t router_ws_bytes = 0;
   int cus = 0;  // compute units of the device
+  frx_status forced = FRX_OK;  // frx_force_status: returned by every compute / upload call
 };
 
 static frx_status fail(frx_ctx *ctx, frx_status st, const char *fmt, ...) {
@@ -104,10 +105,15 @@ static frx_status hip_fail(frx_ctx *ctx, hipError_t e, const char *what) {
   return fail(ctx, st, "%s: %s (%d)", what, hipGetErrorString(e), (int)e);
 }
 
-// Makes the context's device current for the calling thread.
-static frx_status enter(frx_ctx *ctx) {
+// Makes the context's device current for the calling thread; every entry
+// point that takes a context starts here. work: a compute or upload call,
+// which returns the status forced by frx_force_status instead (before
+// reading any argument or touching the device).
+static frx_status enter(frx_ctx *ctx, bool work = true) {
   if (!ctx) return FRX_ERR_DEVICE;
   ctx->err[0] = 0;
+  if (work && ctx->forced != FRX_OK)
+    return fail(ctx, ctx->forced, "status %d forced by frx_force_status", (int)ctx->forced);
   hipError_t e = hipSetDevice(ctx->device);
   if (e != hipSuccess) return fail(ctx, FRX_ERR_DEVICE, "hipSetDevice(%d): %s", ctx->device, hipGetErrorString(e));
   return FRX_OK;
@@ -153,16 +159,16 @@ frx_status frx_create(int device, frx_ctx **out) {
 
 void frx_destroy(frx_ctx *ctx) {
   if (!ctx) return;
-  hipSetDevice(ctx->device);
-  if (ctx->scratch) hipFree(ctx->scratch);
-  if (ctx->moe_ws) hipFree(ctx->moe_ws);
-  if (ctx->ffn_ws) hipFree(ctx->ffn_ws);
-  if (ctx->glu_ws) hipFree(ctx->glu_ws);
-  if (ctx->blk_ws) hipFree(ctx->blk_ws);
-  if (ctx->router_ws) hipFree(ctx->router_ws);
-  if (ctx->unit_ws) hipFree(ctx->unit_ws);
-  if (ctx->ffn_bar) hipFree(ctx->ffn_bar);
-  for (void *p : ctx->retired) hipFree(p);
+  (void)hipSetDevice(ctx->device);
+  if (ctx->scratch) (void)hipFree(ctx->scratch);
+  if (ctx->moe_ws) (void)hipFree(ctx->moe_ws);
+  if (ctx->ffn_ws) (void)hipFree(ctx->ffn_ws);
+  if (ctx->glu_ws) (void)hipFree(ctx->glu_ws);
+  if (ctx->blk_ws) (void)hipFree(ctx->blk_ws);
+  if (ctx->router_ws) (void)hipFree(ctx->router_ws);
+  if (ctx->unit_ws) (void)hipFree(ctx->unit_ws);
+  if (ctx->ffn_bar) (void)hipFree(ctx->ffn_bar);
+  for (void *p : ctx->retired) (void)hipFree(p);
   delete ctx;
 }
 
@@ -173,7 +179,7 @@ frx_status frx_set_stream(frx_ctx *ctx, void *hip_stream) {
 }
 
 frx_status frx_synchronize(frx_ctx *ctx) {
-  frx_status st = enter(ctx);
+  frx_status st = enter(ctx, false);
   if (st != FRX_OK) return st;
   hipError_t e = hipStreamSynchronize(ctx->stream);
   if (e != hipSuccess) return hip_fail(ctx, e, "hipStreamSynchronize");
@@ -213,6 +219,15 @@ frx_status frx_set_moe_routing(frx_ctx *ctx, frx_moe_routing routing) {
   if (routing != FRX_MOE_TERNARY_MOE_LAYER && routing != FRX_MOE_CPU_MOE_LAYER)
     return fail(ctx, FRX_ERR_UNSUPPORTED, "unknown MoE routing %d", (int)routing);
   ctx->moe_routing = routing;
+  return FRX_OK;
+}
+
+frx_status frx_force_status(frx_ctx *ctx, frx_status status) {
+  if (!ctx) return FRX_ERR_DEVICE;
+  ctx->err[0] = 0;
+  if ((int)status < (int)FRX_OK || (int)status > (int)FRX_ERR_UNSUPPORTED)
+    return fail(ctx, FRX_ERR_UNSUPPORTED, "unknown status %d", (int)status);
+  ctx->forced = status;
   return FRX_OK;
 }
 
@@ -459,7 +474,7 @@ static frx_status ffn_run(frx_ctx *ctx, const void *x, frx_dtype xt, const uint3
       // caller stream: wait for it here (first use only)
       if (e == hipSuccess) e = hipDeviceSynchronize();
       if (e != hipSuccess) {
-        hipFree(p);
+        (void)hipFree(p);
         return hip_fail(ctx, e, "FFN barrier initialisation");
       }
       ctx->ffn_bar = reinterpret_cast<unsigned *>(p);
@@ -600,7 +615,7 @@ frx_status frx_ternary_stats(frx_ctx *ctx, const uint32_t *w, uint32_t N, uint32
 static frx_status ensure_scratch(frx_ctx *ctx, size_t bytes) {
   if (bytes <= ctx->scratch_bytes) return FRX_OK;
   if (ctx->scratch) {
-    hipFree(ctx->scratch);
+    (void)hipFree(ctx->scratch);
     ctx->scratch = nullptr;
     ctx->scratch_bytes = 0;
   }
@@ -610,14 +625,17 @@ static frx_status ensure_scratch(frx_ctx *ctx, size_t bytes) {
   return FRX_OK;
 }
 
-static frx_status host_linear(frx_ctx *ctx, const uint32_t *w_host,
-                              const float *s_host, const uint32_t *w_dev,
-                              const float *s_dev, const float *input,
-                              size_t seq, size_t in_cols, size_t out_rows,
+// Host-slice linear: w / s are host arrays (uploaded per call) when
+// upload_w is set, else device pointers.
+static frx_status host_linear(frx_ctx *ctx, bool upload_w, const uint32_t *w, const float *s,
+                              const float *input, size_t seq, size_t in_cols, size_t out_rows,
                               float *out, bool sparse) {
   frx_status st = enter(ctx);
   if (st != FRX_OK) return st;
   if (!input || !out) return fail(ctx, FRX_ERR_SHAPE, "null host buffer");
+  if (!w || !s) return fail(ctx, FRX_ERR_SHAPE, upload_w ? "null host weights or scales" : "null device weight buffer");
+  const uint32_t *w_host = upload_w ? w : nullptr, *w_dev = upload_w ? nullptr : w;
+  const float *s_host = upload_w ? s : nullptr, *s_dev = upload_w ? nullptr : s;
   if (seq == 0 || in_cols == 0 || out_rows == 0) return fail(ctx, FRX_ERR_SHAPE, "empty shape");
   if (seq > 0xFFFFFFFFu || in_cols > 0xFFFFFFFFu || out_rows > 0xFFFFFFFFu)
     return fail(ctx, FRX_ERR_SHAPE, "dimension exceeds 32 bits");
@@ -640,7 +658,6 @@ static frx_status host_linear(frx_ctx *ctx, const uint32_t *w_host,
   float *dy = reinterpret_cast<float *>(base + bw + bs + bx);
   hipError_t e;
   if (w_host) {
-    if (!s_host) return fail(ctx, FRX_ERR_SHAPE, "null scales");
     if ((e = hipMemcpyAsync(dw, w_host, wwords * 4, hipMemcpyHostToDevice, ctx->stream)) != hipSuccess)
       return hip_fail(ctx, e, "weight upload");
     if ((e = hipMemcpyAsync(ds, s_host, out_rows * 4, hipMemcpyHostToDevice, ctx->stream)) != hipSuccess)
@@ -663,16 +680,14 @@ frx_status frx_gpu_ternary_matmul(frx_ctx *ctx, const uint32_t *packed_weights,
                                   const float *scales, const float *input,
                                   size_t seq_len, size_t in_cols,
                                   size_t out_rows, float *out) {
-  if (!packed_weights) return fail(ctx, FRX_ERR_SHAPE, "null packed weights");
-  return host_linear(ctx, packed_weights, scales, nullptr, nullptr, input, seq_len, in_cols, out_rows, out, false);
+  return host_linear(ctx, true, packed_weights, scales, input, seq_len, in_cols, out_rows, out, false);
 }
 
 frx_status frx_gpu_ternary_matmul_vram(frx_ctx *ctx, const uint32_t *w_dev,
                                        const float *s_dev, const float *input,
                                        size_t seq_len, size_t in_cols,
                                        size_t out_rows, float *out) {
-  if (!w_dev || !s_dev) return fail(ctx, FRX_ERR_SHAPE, "null device weight buffer");
-  return host_linear(ctx, nullptr, nullptr, w_dev, s_dev, input, seq_len, in_cols, out_rows, out, false);
+  return host_linear(ctx, false, w_dev, s_dev, input, seq_len, in_cols, out_rows, out, false);
 }
 
 frx_status frx_gpu_sparse_ternary_matmul(frx_ctx *ctx, const uint32_t *meta,
@@ -680,8 +695,7 @@ frx_status frx_gpu_sparse_ternary_matmul(frx_ctx *ctx, const uint32_t *meta,
                                          const float *input, size_t seq_len,
                                          size_t in_cols, size_t out_rows,
                                          float *out) {
-  if (!meta) return fail(ctx, FRX_ERR_SHAPE, "null sparse metadata");
-  return host_linear(ctx, meta, scales, nullptr, nullptr, input, seq_len, in_cols, out_rows, out, true);
+  return host_linear(ctx, true, meta, scales, input, seq_len, in_cols, out_rows, out, true);
 }
 
 // ---- weight ingest (resident upload, done once) ----------------------------
@@ -710,7 +724,7 @@ static frx_status upload_scales(frx_ctx *ctx, const float *row_scales, float ten
   }
   const hipError_t e = hipMemcpy(*s_dev, src, (size_t)N * 4, hipMemcpyHostToDevice);
   if (e != hipSuccess) {
-    hipFree(*s_dev);
+    (void)hipFree(*s_dev);
     *s_dev = nullptr;
     return hip_fail(ctx, e, "scale upload");
   }
@@ -732,12 +746,12 @@ frx_status frx_upload_ternary(frx_ctx *ctx, const uint8_t *packed, uint32_t N, u
   // little-endian device the u32 layout is the u8 stream itself.
   hipError_t e = hipMemcpy(*w_dev, packed, bytes, hipMemcpyHostToDevice);
   if (e != hipSuccess) {
-    hipFree(*w_dev);
+    (void)hipFree(*w_dev);
     *w_dev = nullptr;
     return hip_fail(ctx, e, "weight upload");
   }
   if ((st = upload_scales(ctx, row_scales, tensor_scale, N, s_dev)) != FRX_OK) {
-    hipFree(*w_dev);
+    (void)hipFree(*w_dev);
     *w_dev = nullptr;
   }
   return st;
@@ -799,21 +813,21 @@ frx_status frx_upload_stm(frx_ctx *ctx, const void *image, size_t len, uint32_t 
   if ((st = dev_alloc(ctx, &tmp, pb + sb, "STM staging allocation")) != FRX_OK) return st;
   if ((st = dev_alloc(ctx, reinterpret_cast<void **>(meta_dev), (size_t)rows * wpr * 4, "2:4 metadata allocation")) !=
       FRX_OK) {
-    hipFree(tmp);
+    (void)hipFree(tmp);
     return st;
   }
   hipError_t e = hipMemcpy(tmp, b + HDR, pb + sb, hipMemcpyHostToDevice);
   const uint8_t *dp = reinterpret_cast<const uint8_t *>(tmp);
   if (e == hipSuccess) e = frx::launch_sp24_cpu_to_gpu(dp, dp + pb, (int)rows, (int)cols, *meta_dev, ctx->stream);
   if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
-  hipFree(tmp);
+  (void)hipFree(tmp);
   if (e != hipSuccess) {
-    hipFree(*meta_dev);
+    (void)hipFree(*meta_dev);
     *meta_dev = nullptr;
     return hip_fail(ctx, e, "STM upload / transcode");
   }
   if ((st = upload_scales(ctx, nullptr, scale, rows, s_dev)) != FRX_OK) {
-    hipFree(*meta_dev);
+    (void)hipFree(*meta_dev);
     *meta_dev = nullptr;
     return st;
   }
@@ -823,7 +837,7 @@ frx_status frx_upload_stm(frx_ctx *ctx, const void *image, size_t len, uint32_t 
 }
 
 frx_status frx_free(frx_ctx *ctx, void *dev_ptr) {
-  frx_status st = enter(ctx);
+  frx_status st = enter(ctx, false);
   if (st != FRX_OK) return st;
   if (!dev_ptr) return FRX_OK;
   const hipError_t e = hipFree(dev_ptr);

@@ -272,6 +272,15 @@ frx_status frx_ternary_ffn_noalloc(frx_ctx *ctx, const void *x, frx_dtype xt,
  * call. */
 frx_status frx_set_moe_routing(frx_ctx *ctx, frx_moe_routing routing);
 
+/* Forced failure, for testing a caller's fallback path (no counterpart in
+ * the reference; its callers fall back to the CPU on any FerrisResError,
+ * src/model/cpu_block_attn_res.rs:1004-1031). While status != FRX_OK, every
+ * compute and upload entry point on this context returns that status, with
+ * a message, before reading its arguments or touching the device;
+ * frx_synchronize, frx_free, frx_set_* and frx_destroy still work. FRX_OK
+ * clears it. A status outside frx_status is FRX_ERR_UNSUPPORTED. */
+frx_status frx_force_status(frx_ctx *ctx, frx_status status);
+
 /* Selects the execution of frx_ternary_ffn on this context (default
  * FRX_FFN_AUTO). No counterpart in the reference, whose FFN is three
  * separate matmul calls. */

@@ -71,6 +71,7 @@ int main(void) {
   EXPECT(frx_ternary_linear(NULL, NULL, NULL, NULL, FRX_F32, NULL, FRX_F32, 1, 16, 1) == FRX_ERR_DEVICE);
   EXPECT(frx_ternary_linear_bias(NULL, NULL, NULL, NULL, NULL, FRX_F32, NULL, FRX_F32, 1, 16, 1) == FRX_ERR_DEVICE);
   EXPECT(frx_synchronize(NULL) == FRX_ERR_DEVICE);
+  EXPECT(frx_force_status(NULL, FRX_ERR_OOM) == FRX_ERR_DEVICE);
   EXPECT(frx_set_stream(NULL, NULL) == FRX_ERR_DEVICE);
   EXPECT(strcmp(frx_last_error(NULL), "") == 0);
   EXPECT(strcmp(frx_status_string(FRX_ERR_SHAPE), "shape error") == 0);

@@ -74,7 +74,7 @@ def _dyadic_case(M, K, N, seed):
 
 @pytest.mark.parametrize("M,K,N", [(1, 4096, 11008), (1, 11008, 4096), (4, 4096, 11008), (4, 11008, 4096),
                                    (16, 4096, 11008), (16, 11008, 4096), (7, 2048, 2048), (300, 4096, 1000),
-                                   (2048, 4096, 4096)])
+                                   (2048, 4096, 4096), (2048, 4096, 11008)])
 def test_dense_bit_exact_on_dyadic_inputs(ctx, M, K, N):
     """bf16 and f32 activations (the f32 drop-in path of TernaryMatMulOp,
     split into bf16 hi/lo planes) at the decode shapes and token counts."""
@@ -328,3 +328,26 @@ def test_linear_bias_none_is_plain_linear(ctx):
     zero = np.zeros(96, np.float32)
     c = host(_run_bias(ctx, w, s, zero, xf, xb, "bf16", "f32"))
     np.testing.assert_array_equal(c, b)
+
+
+def test_forced_status_for_caller_fallback(ctx):
+    """frx_force_status makes every compute call fail with the chosen
+    FerrisResError variant before touching its arguments (the output keeps
+    its contents), synchronize still works, and 0 clears it."""
+    t, w, s, xf, xb = _case("forced", 2, 256, 32)
+    y = torch.full((2, 32), 7.0, dtype=torch.float32, device="cuda:0")
+    wd, sd, xd = dev_u32(w), dev_f32(s), dev_bf16(xb)
+    for status, kind in ((5, "OOM"), (1, "Gpu"), (6, "Unsupported")):
+        ctx.force_status(status)
+        with pytest.raises(frx.FrxError) as e:
+            ctx.ternary_linear(wd, sd, xd, y)
+        assert e.value.kind == kind and "forced" in str(e.value)
+        ctx.synchronize()
+    assert (host(y) == 7.0).all()
+    with pytest.raises(frx.FrxError) as e:
+        ctx.force_status(9)
+    assert e.value.kind == "Unsupported"
+    ctx.force_status(0)
+    ctx.ternary_linear(wd, sd, xd, y)
+    torch.cuda.synchronize()
+    assert_close_f32(host(y), oracle.ternary_matmul_u32(w, s, synth.bf16_bits_to_f32(xb), 2, 256, 32))

@@ -207,3 +207,41 @@ def test_moe_routing_mode_rejects_unknown(ctx):
     with pytest.raises(frx.FrxError) as e:
         ctx.set_moe_routing(7)
     assert e.value.kind == "Unsupported"
+
+
+KATS = __import__("json").load(open(__import__("os").path.join(__import__("os").path.dirname(__file__), "golden",
+                                                                "reference_kats.json")))
+
+
+@pytest.mark.parametrize("kat", KATS["routing"], ids=lambda k: k["source"].split()[-1])
+@pytest.mark.parametrize("xt", ["f32", "bf16"])
+def test_routing_kats_through_the_gpu_router(ctx, kat, xt):
+    """The reference's routing known-answer tests (kernel_tests.rs) through
+    the device router: H padded to 16 with the logits in the first E
+    activations and the router [E][16] the identity on them, so the router
+    GEMV yields the KAT's logits (bf16 x: the logits rounded to bf16, which
+    keeps their order). Indices must be the KAT's; weights softmax over the
+    selected logits within the KAT's tolerance; every token routes alike."""
+    logits = np.array(kat["logits"], np.float32)
+    E, k, H, I, T = logits.size, kat["top_k"], 16, 16, 3
+    xf = np.zeros((T, H), np.float32)
+    xf[:, :E] = logits
+    if xt == "bf16":
+        xf = synth.bf16_bits_to_f32(synth.f32_to_bf16_bits(xf))
+    rf = np.zeros((E, H), np.float32)
+    rf[np.arange(E), np.arange(E)] = 1.0
+    ex = {}
+    for e in range(E):
+        for mat, (n, kk) in (("gate", (I, H)), ("up", (I, H)), ("down", (H, I))):
+            t = synth.ternary_uniform("moe/kat", f"{mat}{e}", n, kk)
+            ex[(mat, e)] = (synth.pack_rows_u32(t), synth.row_scales("moe/kat", f"s{mat}{e}", n, samples=16))
+    y, idx, w = run_gpu(ctx, xf, synth.f32_to_bf16_bits(xf), rf, synth.f32_to_bf16_bits(rf), ex, E, k,
+                        frx.ACT_SILU, xt=xt, rt="f32")
+    for t in range(T):
+        assert list(idx[t]) == kat["expected_idx"]
+        sel = xf[t, kat["expected_idx"]].astype(np.float64)
+        np.testing.assert_allclose(w[t], np.exp(sel) / np.exp(sel).sum(), atol=kat["weight_tol"], rtol=0)
+        if "sum_tol" in kat:
+            assert abs(float(w[t].sum()) - 1.0) < kat["sum_tol"]
+    ref, _, _ = run_oracle(xf, rf, ex, E, k, False)
+    assert_close_f32(host(y), ref)

@@ -63,8 +63,10 @@ def test_sparse_parity_random(ctx, M, K, N, xt, yt):
         assert_bf16_within_1ulp(y.view(torch.int16).cpu().numpy().view(np.uint16), ref)
 
 
-@pytest.mark.parametrize("M,K,N", [(2048, 4096, 4096), (16, 4096, 11008), (64, 11008, 512)])
+@pytest.mark.parametrize("M,K,N", [(2048, 4096, 4096), (2048, 4096, 11008), (16, 4096, 11008), (64, 11008, 512)])
 def test_sparse_bit_exact_on_dyadic(ctx, M, K, N):
+    """Whole output, bit for bit (dyadic x, power-of-two scales: every
+    partial sum exact), including the full 2048 x 4096 x 11008 prefill."""
     rng = np.random.default_rng(M + N)
     t = synth.sparse24_uniform(f"dy/{M}", "w", N, K)
     meta = frx.pack_sparse24_gpu(t)

@@ -101,3 +101,46 @@ def test_variant_shape_errors(ctx):
     with pytest.raises(frx.FrxError) as e:
         ctx.ternary_stats(dev_u32(np.zeros(4, np.uint32)), 20, torch.zeros(3, dtype=torch.int64, device=DEV))
     assert e.value.kind == "Shape"
+
+
+def _linear_from_u8(ctx, packed_u8, N, K, alpha, x, xt):
+    """The reference's u8 packing (pack_ternary, ternary.rs:146-163) as
+    uploaded by the drop-in: repacked to u32 words (ternary.rs:1317-1328,
+    row-aligned for K % 16 == 0) and one scale broadcast over the rows."""
+    w = frx.repack_u8_to_u32(packed_u8, N * K).reshape(N, K // 16)
+    M = x.shape[0]
+    xd = dev_bf16(synth.f32_to_bf16_bits(x)) if xt == "bf16" else dev_f32(x)
+    y = torch.empty((M, N), dtype=torch.float32, device=DEV)
+    ctx.ternary_linear(dev_u32(w), dev_f32(np.full(N, alpha, np.float32)), xd, y)
+    torch.cuda.synchronize()
+    return host(y)
+
+
+@pytest.mark.parametrize("form,M,K,N", [("decode", 1, 4096, 11008), ("decode", 1, 2048, 2048),
+                                        ("packed", 4, 1024, 300), ("packed", 16, 2048, 512),
+                                        ("packed", 40, 4096, 256), ("packed_parallel", 1, 11008, 4096),
+                                        ("packed_parallel", 1, 4096, 1000)])
+def test_reference_cpu_matmul_forms(ctx, form, M, K, N):
+    """ternary_matmul_decode (ternary.rs:591-633), ternary_matmul_packed
+    (:401-464) and ternary_matmul_packed_parallel (:471-539) on the GPU: the
+    same u8-packed weights and alpha through frx_ternary_linear. Dyadic
+    activations and a power-of-two alpha: bit for bit; normal f32 and bf16
+    activations: within 1e-3."""
+    rng = np.random.default_rng(hash((form, M, K, N)) % 2 ** 32)
+    t = rng.integers(-1, 2, size=(N, K)).astype(np.int8)
+    pk = oracle.pack_ternary(t)
+
+    def ref(x, alpha):
+        if form == "decode":
+            return oracle.ternary_matmul_decode(t, alpha, x[0], N, K)[None, :]
+        if form == "packed":
+            return oracle.ternary_matmul_packed(pk, alpha, x, N, K, M).reshape(M, N)
+        return oracle.ternary_matmul_packed_parallel(pk, alpha, x[0], N, K)[None, :]
+
+    xd = _dyadic(rng, M * K).reshape(M, K)
+    for xt in ("bf16", "f32"):
+        np.testing.assert_array_equal(_linear_from_u8(ctx, pk, N, K, 0.25, xd, xt), ref(xd, 0.25))
+    xn = synth.normal(synth.seed_of(f"forms/{form}/{M}x{K}x{N}", "x"), M * K).reshape(M, K).astype(np.float32)
+    assert_close_f32(_linear_from_u8(ctx, pk, N, K, 0.0371, xn, "f32"), ref(xn, np.float32(0.0371)))
+    xb = synth.bf16_bits_to_f32(synth.f32_to_bf16_bits(xn))
+    assert_close_f32(_linear_from_u8(ctx, pk, N, K, 0.0371, xb, "bf16"), ref(xb, np.float32(0.0371)))
