@@ -99,22 +99,17 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm2sp_kernel(
   Core::template store_tile<YT>(lds, acc, scale, Y, (size_t)N, m0, m_count, n0, n_count, bias);
 }
 
-#ifndef FRX_GEMM2_NS
-#define FRX_GEMM2_NS 4
-#endif
-// Waves across the token dimension of a 128 x 256 tile: 1 gives 4 waves of
-// 128 tokens x 64 rows (one per SIMD); 2 gives 2 x 2 waves of 64 tokens x
-// 128 rows, which halves the activation reads from LDS but doubles each
-// wave's weight decode, measured slower (2048 x 4096 x 4096 / 11008: dense
-// 76 / 184 us against 65 / 175 us, 2:4 87 / 195 us against 71 / 157 us).
-#ifndef FRX_GEMM2_WM
-#define FRX_GEMM2_WM 1
-#endif
-// Tokens per tile of the 2:4 launches (64 was measured slower there: 83 /
-// 203 us against 71 / 158 us at 2048 x 4096 x 4096 / 11008).
-#ifndef FRX_GEMM2_BM
-#define FRX_GEMM2_BM 128
-#endif
+// Pipeline stages of the K loop.
+constexpr int GEMM2_NS = 4;
+// One wave per SIMD, each over the tile's tokens x 64 rows. Waves split
+// 2 x 2 over tokens and rows instead (half the activation reads from LDS,
+// twice each wave's weight decode) measured slower at 2048 x 4096 x 4096 /
+// 11008: dense 76 / 184 us against 65 / 175 us, 2:4 87 / 195 us against
+// 71 / 157 us.
+constexpr int GEMM2_WM = 1, GEMM2_WN = 4;
+// Tokens per tile of the 2:4 launches (64 measured slower there: 83 / 203 us
+// against 71 / 158 us at 2048 x 4096 x 4096 / 11008).
+constexpr int GEMM2SP_BM = 128;
 
 // Compute units of the current device (queried once).
 static int device_cus() {
@@ -130,19 +125,10 @@ static int device_cus() {
   return c;
 }
 
-// Tile of the launches whose 128 x 256 grid gives each CU at most one
-// workgroup: 0 = 64 tokens x 256 rows (default); 1 = 128 x 128, which halves
-// the decode VALU per MFMA (per K step a wave decodes 32 codes per lane
-// instead of 64 for the same 32 MFMAs) but doubles the activation reads
-// from LDS: measured slower (2048x4096x4096: 66.1 against 63.8 us).
-#ifndef FRX_GEMM2_SMALL_TILE
-#define FRX_GEMM2_SMALL_TILE 0
-#endif
-
 template <int BM, typename YT, int BN = 256>
 static hipError_t launch_gemm2_bm(const uint32_t *w, const float *scale, const void *x, void *y,
                                   int M, int K, int N, hipStream_t stream, const float *bias) {
-  constexpr int WM = FRX_GEMM2_WM, WN = 4 / FRX_GEMM2_WM, NS = FRX_GEMM2_NS;
+  constexpr int WM = GEMM2_WM, WN = GEMM2_WN, NS = GEMM2_NS;
   using Core = Gemm2<BM, BN, WM, WN, NS, false>;
   constexpr int lds = Core::LDS_DWORDS * 4;
   static std::atomic<uint64_t> done;
@@ -159,25 +145,21 @@ static hipError_t launch_gemm2_bm(const uint32_t *w, const float *scale, const v
 // would give each CU at most one workgroup: the 64-token tile (48 KB of LDS,
 // 64 accumulation registers per lane) runs two workgroups per CU, so each
 // SIMD interleaves two waves (2048 x 4096 x 4096: 64 us against 70 us; at
-// N = 11008 the 128-token tile stays ahead, 175 against 198 us).
+// N = 11008 the 128-token tile stays ahead, 175 against 198 us). A 128 x 128
+// tile there (half the decode per MFMA, twice the activation reads from LDS)
+// measured 66.1 against 63.8 us.
 template <typename YT>
 static hipError_t launch_gemm2_t(const uint32_t *w, const float *scale, const void *x, void *y,
                                  int M, int K, int N, hipStream_t stream, const float *bias) {
-#if FRX_GEMM2_WM == 1
   const long tiles128 = (long)((M + 127) / 128) * ((N + 255) / 256);
-#if FRX_GEMM2_SMALL_TILE == 1
-  if (tiles128 <= device_cus()) return launch_gemm2_bm<128, YT, 128>(w, scale, x, y, M, K, N, stream, bias);
-#else
   if (tiles128 <= device_cus()) return launch_gemm2_bm<64, YT>(w, scale, x, y, M, K, N, stream, bias);
-#endif
-#endif
   return launch_gemm2_bm<128, YT>(w, scale, x, y, M, K, N, stream, bias);
 }
 
 template <typename YT>
 static hipError_t launch_gemm2sp_t(const uint32_t *meta, const float *scale, const void *x, void *y,
                                    int M, int K, int N, hipStream_t stream, const float *bias) {
-  constexpr int BM = FRX_GEMM2_BM, BN = 256, WM = FRX_GEMM2_WM, WN = 4 / FRX_GEMM2_WM, NS = FRX_GEMM2_NS;
+  constexpr int BM = GEMM2SP_BM, BN = 256, WM = GEMM2_WM, WN = GEMM2_WN, NS = GEMM2_NS;
   using Core = Gemm2<BM, BN, WM, WN, NS, false>;
   constexpr int lds = Core::LDS_DWORDS * 4;
   static std::atomic<uint64_t> done;

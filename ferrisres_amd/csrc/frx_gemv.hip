@@ -1834,7 +1834,7 @@ hipError_t launch_gemv(const uint32_t *w, const float *scale, const void *x,
     if (yt_bf16) return launch_gemv_rows4<uint16_t>(w, scale, x, y, B, K, N, stream, bias);
     return launch_gemv_rows4<float>(w, scale, x, y, B, K, N, stream, bias);
   }
-  if (xt_bf16 && B >= GEMV_DIRECT_MIN_B && gemv_xs_ok(x, B, K, 1, 1)) {
+  if (xt_bf16 && B >= GEMV_XS_MIN_B && gemv_xs_ok(x, B, K, 1, 1)) {
     if (yt_bf16) return launch_gemv_xs<uint16_t, 1, L, XS_BF16, false>(w, scale, w, scale, x, x, y, B, K, N, stream, bias);
     return launch_gemv_xs<float, 1, L, XS_BF16, false>(w, scale, w, scale, x, x, y, B, K, N, stream, bias);
   }
@@ -1871,7 +1871,7 @@ hipError_t launch_gemv(const uint32_t *w, const float *scale, const void *x,
 hipError_t launch_gemv_glu(const uint32_t *w_gate, const float *s_gate, const uint32_t *w_up,
                            const float *s_up, const void *x, int xt_bf16, float *h, int B, int K,
                            int N, int gelu, hipStream_t stream) {
-  if (xt_bf16 && B >= GEMV_DIRECT_MIN_B && gemv_xs_ok(x, B, K, 1, 2)) {
+  if (xt_bf16 && B >= GEMV_GLU_XS_MIN_B && gemv_xs_ok(x, B, K, 1, 2)) {
     if (gelu)
       return launch_gemv_xs<float, 2, GEMV_GEGLU, XS_BF16, false>(w_gate, s_gate, w_up, s_up, x, x, h, B, K, N,
                                                                    stream);
@@ -1921,7 +1921,7 @@ hipError_t launch_glu_combine(const float *g, const float *u, float *h, size_t n
 hipError_t launch_gemv_glu_planes(const uint32_t *w_gate, const float *s_gate, const uint32_t *w_up,
                                   const float *s_up, const void *x, uint16_t *h_planes, int B, int K,
                                   int N, int gelu, hipStream_t stream) {
-  if (B >= GEMV_DIRECT_MIN_B && gemv_xs_ok(x, B, K, 1, 2)) {
+  if (B >= GEMV_GLU_XS_MIN_B && gemv_xs_ok(x, B, K, 1, 2)) {
     if (gelu)
       return launch_gemv_xs<uint16_t, 2, GEMV_GEGLU, XS_BF16, true>(w_gate, s_gate, w_up, s_up, x, x, h_planes, B,
                                                                      K, N, stream);
@@ -1938,7 +1938,7 @@ hipError_t launch_gemv_glu_planes(const uint32_t *w_gate, const float *s_gate, c
 hipError_t launch_gemv_planes(const uint32_t *w, const float *scale, const uint16_t *x_planes, void *y,
                               int yt_bf16, int B, int K, int N, hipStream_t stream) {
   const uint16_t *lo = x_planes + (size_t)B * K;
-  if (B >= GEMV_DIRECT_MIN_B && gemv_xs_ok(x_planes, B, K, 2, 1) && (reinterpret_cast<uintptr_t>(lo) & 15) == 0) {
+  if (B >= GEMV_PLANES_XS_MIN_B && gemv_xs_ok(x_planes, B, K, 2, 1) && (reinterpret_cast<uintptr_t>(lo) & 15) == 0) {
     if (yt_bf16)
       return launch_gemv_xs<uint16_t, 1, GEMV_LINEAR, XS_PLANES, false>(w, scale, w, scale, x_planes, lo, y, B, K,
                                                                         N, stream);

@@ -21,15 +21,26 @@ inline hipError_t opt_in_lds(const void *fn, int bytes, std::atomic<uint64_t> &d
   return e;
 }
 
-// Smallest B that takes the direct-operand decode kernel (bf16 activations).
-// Below it the staged kernel is faster: its activation loads are fully
-// coalesced and at small B its rows fit LDS in one or two slices (measured at
-// the LLaMA-7B decode shapes: B = 4 staged 7.3 / 7.8 us per launch against
-// 9.3 / 8.7 us direct; B = 16 staged 14.5 / 21.3 us against 14.3 / 13.2 us).
-#ifndef FRX_GEMV_DIRECT_MIN_B
-#define FRX_GEMV_DIRECT_MIN_B 8
-#endif
-constexpr int GEMV_DIRECT_MIN_B = FRX_GEMV_DIRECT_MIN_B;
+// Token counts from which the bf16 decode GEMVs leave the 16-row tiles
+// with x staged in LDS (gemv_kernel) for the kernels built for many tokens,
+// measured per step at the LLaMA-7B decode shapes (11008x4096 / 4096x11008,
+// rotating weights, graph-replayed):
+//  - linear: the per-wave staged kernel (gemv_xs_kernel) from 5 tokens
+//    (B = 5, 6, 7: 7.44 / 8.26, 7.62 / 9.60, 9.19 / 9.73 us with the 16-row
+//    tiles against 6.39 / 8.14, 6.57 / 8.31, 6.74 / 8.45 us staged); 2-4
+//    tokens take the 4-segment rows kernel before either.
+//  - the FFN's gate/up launch (h as bf16 planes): per-lane operand loads
+//    (gemv_direct_kernel) below 8 tokens, staged from 8 (FFN step at 4-7
+//    tokens 25.2-28.3 us direct against 26.1-28.4 us staged);
+//  - the FFN's down launch over those planes: staged from 6 tokens (FFN step
+//    at 6 / 7 tokens 26.6 / 28.3 us with operand loads, 25.9 / 26.4 us
+//    staged; at 4 / 5 tokens 25.2 / 25.2 against 25.7 / 25.2 us).
+constexpr int GEMV_XS_MIN_B = 5;
+constexpr int GEMV_GLU_XS_MIN_B = 8;
+constexpr int GEMV_PLANES_XS_MIN_B = 6;
+// The operand-load kernels (gemv_direct_kernel, gemv_tall_kernel) serve from
+// 8 tokens where the staged kernel does not fit (K above its quad limit).
+constexpr int GEMV_DIRECT_MIN_B = 8;
 
 // Decode GEMV, B <= 16 tokens (frx_gemv.hip).
 // One bf16 token through the whole-rows kernels (M == 1, H and I multiples

@@ -721,22 +721,14 @@ __global__ __launch_bounds__(256) void moe_down_kernel(
 // layer: gate/up 85.6 -> 98.5 us, down 73.5 -> 83.8 us; half the
 // workgroups at two waves per SIMD cost more than the halved activation
 // re-reads save)
-#ifndef FRX_MOE_DOWN_BN
-#define FRX_MOE_DOWN_BN 256
-#endif
-constexpr int MOE2_BN = FRX_MOE_DOWN_BN;
+constexpr int MOE2_BN = 256;
 // gate/up tile: MOE_GU_BN / 2 gate rows and the same up rows (128 measured
 // slower at the 512-token, 16-expert layer: 92 us against 89 us, although
 // its 2112 workgroups fill the CUs more evenly than 1056)
-#ifndef FRX_MOE_GU_BN
-#define FRX_MOE_GU_BN 256
-#endif
-constexpr int MOE_GU_BN = FRX_MOE_GU_BN;
-#ifndef FRX_MOE_NS
-#define FRX_MOE_NS 4
-#endif
-using MoeGateUpCore = Gemm2<MOE_BM, MOE_GU_BN, 1, 4, FRX_MOE_NS, true>;
-using MoeDownCore = Gemm2<MOE_BM, MOE2_BN, 1, 4, FRX_MOE_NS, false>;
+constexpr int MOE_GU_BN = 256;
+constexpr int MOE_NS = 4;  // pipeline stages of the K loop
+using MoeGateUpCore = Gemm2<MOE_BM, MOE_GU_BN, 1, 4, MOE_NS, true>;
+using MoeDownCore = Gemm2<MOE_BM, MOE2_BN, 1, 4, MOE_NS, false>;
 
 __global__ __launch_bounds__(256) void moe_gateup2_kernel(
     const GateUpArgs args, const uint16_t *__restrict__ x, int T, int H, int I,
