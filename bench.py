@@ -209,9 +209,8 @@ def main():
     launch_time = 2 * t_gu + t_dn
     achieved = launch_bytes / launch_time / 1e9
     roofline = {
-        "kernel": "frx::gemv_rows_kernel (B=1, linear, bf16 in, bf16 out)" if B == 1 else
-                  "frx::gemv_rows4_kernel" if 2 <= B <= 4 else "frx::gemv_kernel (staged)" if B < 8 else
-                  "frx::gemv_xs_kernel",
+        "kernel": "frx::gemv_bal_kernel (B=1, linear, bf16 in, bf16 out)" if B == 1 else
+                  "frx::gemv_rows4_kernel" if 2 <= B <= 4 else "frx::gemv_xs_kernel",
         "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
         "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
         "avg_us": {"11008x4096": round(t_gu * 1e6, 3), "4096x11008": round(t_dn * 1e6, 3)},
@@ -223,13 +222,15 @@ def main():
     ffn_traffic = None
     if os.path.exists(traffic_file):
         try:
-            tr = json.load(open(traffic_file))
-            if tr.get("batch") == B:
+            tr = json.load(open(traffic_file)).get("by_batch", {}).get(str(B))
+            if tr:
                 by = tr["bytes_per_launch"]
                 # per-launch average over the step's three launches
                 roofline["traffic"] = int(round((2 * by["11008x4096"] + by["4096x11008"]) / 3))
                 roofline["traffic_by_shape"] = {k: by[k] for k in ("11008x4096", "4096x11008")}
-                ffn_traffic = {k: by[k] for k in ("glu_11008x4096", "down_f32_4096x11008", "ffn1_llama7b") if k in by}
+                ffn_traffic = {k: by[k] for k in ("ffn_glu_planes_11008x4096", "ffn_down_planes_4096x11008",
+                                                  "glu_f32h_11008x4096", "down_f32x_4096x11008", "ffn1_llama7b")
+                               if k in by}
         except (OSError, ValueError, KeyError):
             pass
 
@@ -477,6 +478,47 @@ def run_extra(torch, frx, synth, ctx, stream, dev, only=None, iters=200):
     return res
 
 
+def _graph_time(torch, stream, calls, reps):
+    """Seconds per call: `calls` (a list of launch closures) captured in one
+    HIP graph, replayed once untimed, then `reps` times between HIP events on
+    the launch stream; also the median, p10 and p90 per call over replays."""
+    with torch.cuda.stream(stream):
+        for c in calls:
+            c()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=stream):
+        for c in calls:
+            c()
+    torch.cuda.synchronize()
+    with torch.cuda.stream(stream):
+        g.replay()
+    torch.cuda.synchronize()
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(reps + 1)]
+    with torch.cuda.stream(stream):
+        ev[0].record(stream)
+        for r in range(reps):
+            g.replay()
+            ev[r + 1].record(stream)
+    torch.cuda.synchronize()
+    per = np.array([ev[r].elapsed_time(ev[r + 1]) * 1e-3 / len(calls) for r in range(reps)])
+    total = ev[0].elapsed_time(ev[reps]) * 1e-3 / (reps * len(calls))
+    return total, {"median_us": round(float(np.median(per)) * 1e6, 3),
+                   "p10_us": round(float(np.percentile(per, 10)) * 1e6, 3),
+                   "p90_us": round(float(np.percentile(per, 90)) * 1e6, 3),
+                   "launches": reps * len(calls)}
+
+
+def _bench_lib():
+    """libfrx_bench.so (bench-only helpers: the streaming read ceiling)."""
+    import ctypes
+    h = ctypes.CDLL(os.path.join(ROOT, "ferrisres_amd", "libfrx_bench.so"))
+    h.frxb_read.restype = ctypes.c_int
+    h.frxb_read.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p, ctypes.c_void_p]
+    h.frxb_read_grid.restype = ctypes.c_int
+    return h
+
+
 def gemv_size_sweep(torch, ctx, stream, dev, reps=40):
     """The B=1 decode GEMV (bf16 x, bf16 y) at growing weight sizes: the
     LLaMA-7B projection, the LLaMA-70B gate/up projection [28672, 8192] and
@@ -484,10 +526,15 @@ def gemv_size_sweep(torch, ctx, stream, dev, reps=40):
     (dispatch and the first HBM round trip); larger matrices spread it over
     more bytes, so the rate approaches what the kernel streams at. Weights
     are uniform ternary codes made on the device, rotating over copies that
-    total >= 0.5 GB; times are HIP events around back-to-back launches. A
-    device copy of the same words (torch, read + write) is timed beside it
-    as the rate a stock streaming kernel gets at that size."""
+    total >= 0.5 GB. Beside each GEMV, with the same rotation and timing:
+    a plain streaming read of the same packed words (libfrx_bench.so
+    frxb_read: 16-byte loads, two workgroups per CU, no decode), the ceiling
+    a launch of that many bytes reaches, and torch's device copy of them
+    (read + write). All three are timed as HIP-graph replays of one launch
+    per weight copy."""
     res = {}
+    bl = _bench_lib()
+    sink = torch.empty(bl.frxb_read_grid(), dtype=torch.int32, device=dev)
     gen = torch.Generator(device=dev)
     gen.manual_seed(20240607)
     shifts = (2 * torch.arange(16, device=dev, dtype=torch.int64))
@@ -500,33 +547,32 @@ def gemv_size_sweep(torch, ctx, stream, dev, reps=40):
         x = torch.randn((1, k), generator=gen, device=dev).to(torch.bfloat16)
         y = torch.empty((1, n), dtype=torch.bfloat16, device=dev)
         nbytes = gemv_bytes(n, k, 1)
-        copies = max(3, int(np.ceil(512e6 / (n * k // 4))) + 1)
-        ws = [w0] + [w0.clone() for _ in range(copies - 1)]
-        it = [0]
-
-        def one():
-            ctx.ternary_linear(ws[it[0] % copies], s, x, y)
-            it[0] += 1
-        st = {}
-        dt = _time_kernel(torch, stream, one, reps * copies, warm=copies, stats=st)
-        # calibration: torch's device copy of the same packed words (read +
-        # write), rotating over the same copies
-        dst = torch.empty_like(w0)
-
-        def copy_only():
-            dst.copy_(ws[it[0] % copies])
-            it[0] += 1
-        dc = _time_kernel(torch, stream, copy_only, reps * copies, warm=copies)
         wbytes = n * k // 4
+        copies = max(3, int(np.ceil(512e6 / wbytes)) + 1)
+        ws = [w0] + [w0.clone() for _ in range(copies - 1)]
+        gemv_calls = [(lambda w=w: ctx.ternary_linear(w, s, x, y)) for w in ws]
+        dt, st = _graph_time(torch, stream, gemv_calls, reps)
+
+        def rd(w):
+            rc = bl.frxb_read(w.data_ptr(), wbytes, sink.data_ptr(), stream.cuda_stream)
+            assert rc == 0, rc
+        dr, str_ = _graph_time(torch, stream, [(lambda w=w: rd(w)) for w in ws], reps)
+        dst = torch.empty_like(w0)
+        dc, _ = _graph_time(torch, stream, [(lambda w=w: dst.copy_(w)) for w in ws], reps)
         res[f"{n}x{k}"] = {"us": round(dt * 1e6, 3), "gb_s": round(nbytes / dt / 1e9, 1),
                            "hbm_fraction": round(nbytes / dt / 1e9 / HBM_PEAK_GBS, 4),
                            "algorithmic_bytes": nbytes, "weight_copies": copies, **st,
-                           "stock_copy_us": round(dc * 1e6, 3),
-                           "stock_copy_gb_s_read_plus_write": round(2 * wbytes / dc / 1e9, 1)}
+                           "read_ceiling_us": round(dr * 1e6, 3),
+                           "read_ceiling_gb_s": round(wbytes / dr / 1e9, 1),
+                           "read_ceiling_median_us": str_["median_us"],
+                           "gemv_over_read_ceiling": round(dt / dr, 3),
+                           "torch_copy_us": round(dc * 1e6, 3),
+                           "torch_copy_gb_s_read_plus_write": round(2 * wbytes / dc / 1e9, 1)}
         log(f"bench: GEMV B=1 {n}x{k}: {dt * 1e6:.2f} us, {nbytes / dt / 1e9:.1f} GB/s; "
-            f"torch copy of the weights {dc * 1e6:.2f} us, {2 * wbytes / dc / 1e9:.1f} GB/s read+write")
+            f"read ceiling {dr * 1e6:.2f} us ({wbytes / dr / 1e9:.1f} GB/s); "
+            f"torch copy {dc * 1e6:.2f} us")
         del dst
-        del ws, w0
+        del ws, w0, gemv_calls
         torch.cuda.synchronize()
     return res
 

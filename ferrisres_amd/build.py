@@ -2,7 +2,8 @@
 
 Compiles every HIP/C++ source under ferrisres_amd/csrc with hipcc into one
 shared library next to this file. No torch types cross the ABI; the library
-depends only on the HIP runtime.
+depends only on the HIP runtime. csrc/bench/ holds bench.py's measurement
+helpers (a plain streaming read), linked separately into libfrx_bench.so.
 """
 from __future__ import annotations
 
@@ -39,10 +40,20 @@ def _compile(src: str) -> str:
     return obj
 
 
+BENCH_OUT = os.path.join(HERE, "libfrx_bench.so")
+BENCH_SOURCES = ["bench/frx_bench_read.hip"]
+
+
 def build(verbose: bool = False) -> str:
-    os.makedirs(BUILD, exist_ok=True)
-    with ThreadPoolExecutor(max_workers=min(len(SOURCES), 6)) as ex:
-        objs = list(ex.map(_compile, SOURCES))
+    os.makedirs(os.path.join(BUILD, "bench"), exist_ok=True)
+    with ThreadPoolExecutor(max_workers=min(len(SOURCES) + len(BENCH_SOURCES), 6)) as ex:
+        objs_all = list(ex.map(_compile, SOURCES + BENCH_SOURCES))
+    objs, bench_objs = objs_all[:len(SOURCES)], objs_all[len(SOURCES):]
+    # measurement helpers for bench.py (not part of the ternary path)
+    r = subprocess.run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", BENCH_OUT, *bench_objs],
+                       capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"bench helper link failed:\n{r.stderr[-6000:]}")
     tmp = OUT + ".tmp"
     cmd = [HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", tmp, *objs]
     r = subprocess.run(cmd, capture_output=True, text=True)
