@@ -40,24 +40,34 @@ typedef enum frx_status {
   FRX_ERR_DEVICE = 3,
   FRX_ERR_SHADER = 4,
   FRX_ERR_OOM = 5,
-  FRX_ERR_UNSUPPORTED = 6
+  FRX_ERR_UNSUPPORTED = 6,
+  FRX_STATUS_RANGE_ = 0x7fffffff /* range sentinel, never returned */
 } frx_status;
 
-typedef enum frx_dtype { FRX_F32 = 0, FRX_BF16 = 1 } frx_dtype;
+/* Each argument enum carries a sentinel at INT_MAX so that any int a caller
+ * passes (a value from a newer header, or a corrupt one) is a valid value of
+ * the type in C++ as well as C; the library rejects it with a status. */
+typedef enum frx_dtype { FRX_F32 = 0, FRX_BF16 = 1, FRX_DTYPE_RANGE_ = 0x7fffffff } frx_dtype;
 
-typedef enum frx_activation { FRX_ACT_SILU = 0, FRX_ACT_GELU_TANH = 1 } frx_activation;
+typedef enum frx_activation {
+  FRX_ACT_SILU = 0,
+  FRX_ACT_GELU_TANH = 1,
+  FRX_ACT_RANGE_ = 0x7fffffff
+} frx_activation;
 /* How frx_ternary_ffn runs at decode sizes (see frx_set_ffn_mode). */
 typedef enum frx_ffn_mode {
   FRX_FFN_AUTO = 0,        /* M <= 2: two whole-row launches; M = 3: one
                               launch where the shape allows; else two */
   FRX_FFN_ONE_LAUNCH = 1,  /* one launch or FRX_ERR_UNSUPPORTED */
-  FRX_FFN_TWO_LAUNCH = 2   /* gate/up/act launch + down launch */
+  FRX_FFN_TWO_LAUNCH = 2,  /* gate/up/act launch + down launch */
+  FRX_FFN_MODE_RANGE_ = 0x7fffffff
 } frx_ffn_mode;
 
 /* Routing semantics of frx_moe_ternary_ffn (see frx_set_moe_routing). */
 typedef enum frx_moe_routing {
   FRX_MOE_TERNARY_MOE_LAYER = 0, /* TernaryMoELayer and the GPU-path glue */
-  FRX_MOE_CPU_MOE_LAYER = 1      /* CpuMoELayer */
+  FRX_MOE_CPU_MOE_LAYER = 1,     /* CpuMoELayer */
+  FRX_MOE_ROUTING_RANGE_ = 0x7fffffff
 } frx_moe_routing;
 
 /* ---- context -------------------------------------------------------------
@@ -337,7 +347,11 @@ frx_status frx_sparse24_cpu_to_gpu_device(frx_ctx *ctx, const uint8_t *patterns,
  * pack_ternary_u32); scale: [N] f32 alpha (the dequantised row is
  * alpha * q). Device pointers, stream-ordered, no allocation. Requires
  * K % 16 == 0 and K > 0. */
-typedef enum frx_quant_rule { FRX_QUANT_ABSMEAN = 0, FRX_QUANT_STE = 1 } frx_quant_rule;
+typedef enum frx_quant_rule {
+  FRX_QUANT_ABSMEAN = 0,
+  FRX_QUANT_STE = 1,
+  FRX_QUANT_RULE_RANGE_ = 0x7fffffff
+} frx_quant_rule;
 frx_status frx_quantize_ternary(frx_ctx *ctx, const void *w, frx_dtype wt, uint32_t N, uint32_t K,
                                 frx_quant_rule rule, uint32_t *packed, float *scale);
 
