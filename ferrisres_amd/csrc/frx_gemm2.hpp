@@ -157,7 +157,11 @@ __device__ __forceinline__ void wait_vmcnt() {
 // (their results feed MFMAs) before the barrier that precedes its reuse.
 __device__ __forceinline__ void barrier_nofence() { __builtin_amdgcn_s_barrier(); }
 
-template <int BM, int BN, int WM, int WN, int NS, bool GATHER>
+// DUALX: X-stage rows [BM/2, BM) are the rows [0, BM/2) again, read at a
+// second column offset (xoff2 bytes further along each row): one stage then
+// holds two column ranges of the same token rows, e.g. the hi and lo bf16
+// halves of an fp32 activation stored as [rows][2 K].
+template <int BM, int BN, int WM, int WN, int NS, bool GATHER, bool DUALX = false>
 struct Gemm2 {
   static constexpr int NT = WM * WN * 64;
   static constexpr int WAVES = WM * WN;
@@ -190,15 +194,17 @@ struct Gemm2 {
   // come from a second matrix (rows n - BN/2), each of n_count valid rows.
   __device__ __forceinline__ static void lane_offsets(uint32_t (&xv)[XPW], uint32_t (&wv)[WPW],
                                                       const int *rowidx, int m_count,
-                                                      int n_count, int ldx, int wk, bool dual) {
+                                                      int n_count, int ldx, int wk, bool dual,
+                                                      uint32_t xoff2) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
 #pragma unroll
     for (int i = 0; i < XPW; i++) {
       const int r = (wave * XPW + i) * 8 + (lane >> 3);
-      const int rm = min(r, m_count - 1);
+      const int second = DUALX && r >= BM / 2;
+      const int rm = min(second ? r - BM / 2 : r, m_count - 1);
       const uint32_t gr = GATHER ? (uint32_t)rowidx[rm] : (uint32_t)rm;
       const uint32_t c = (lane & 7) ^ ((r >> 1) & 7);  // swizzled source chunk
-      xv[i] = gr * (uint32_t)ldx * 2u + 16u * c;
+      xv[i] = gr * (uint32_t)ldx * 2u + 16u * c + (second ? xoff2 : 0u);
     }
 #pragma unroll
     for (int i = 0; i < WPW; i++) {
@@ -227,10 +233,12 @@ struct Gemm2 {
     return *reinterpret_cast<const u32x4 *>(stage + r * 32 + ((c ^ ((r >> 1) & 7)) * 4));
   }
 
-  // X operand i of a step (i = h * FM + fm): tokens r0 + 16 fm, columns
-  // 16 g + 8 h .. +7 (the codes of weight word g of the step, half h).
+  // X operand i of a step (i = h * F + fm, F token blocks multiplied):
+  // tokens r0 + 16 fm, columns 16 g + 8 h .. +7 (the codes of weight word g
+  // of the step, half h).
+  template <int F>
   __device__ __forceinline__ static u32x4 xop(const uint32_t *stage, int r0, int g, int i) {
-    return xread(stage, r0 + (i % FM) * 16, 2 * g + i / FM);
+    return xread(stage, r0 + (i % F) * 16, 2 * g + i / F);
   }
 
   static constexpr int XD = 4;  // X operand reads run this many MFMA groups ahead
@@ -265,17 +273,21 @@ struct Gemm2 {
   // columns, K <= 2 wk; past wk the loop multiplies X's columns by W again
   // (W column k - wk), which runs an fp32 activation stored as bf16 hi | lo
   // halves of one row in a single pass (K = 2 wk). ldx: X row stride in
-  // elements (default K).
+  // elements (default K). F: the token blocks of each wave that are
+  // multiplied (the first F of its FM; the stage holds all BM rows, rows
+  // past F blocks are loaded and left unread). xoff2: see DUALX.
+  template <int F = FM>
   __device__ static void run(uint32_t *lds, const uint16_t *X, uint32_t xbytes, const int *rowidx,
                              int m_count, const uint32_t *W, int n_count, int K,
-                             f32x4 (&acc)[FN][FM], const uint32_t *W2 = nullptr, int wk = 0, int ldx = 0) {
+                             f32x4 (&acc)[FN][F], const uint32_t *W2 = nullptr, int wk = 0, int ldx = 0,
+                             uint32_t xoff2 = 0) {
     static_assert(NS >= 3, "the ring needs a stage being read, one landing and one free");
-    static_assert(FM >= 4 && XD <= FM, "operand schedule");
+    static_assert(F >= 4 && XD <= F && F <= FM, "operand schedule");
     if (wk == 0) wk = K;
     if (ldx == 0) ldx = K;
     const bool dual = W2 != nullptr;
     uint32_t xv[XPW], wv[WPW];
-    lane_offsets(xv, wv, rowidx, m_count, n_count, ldx, wk, dual);
+    lane_offsets(xv, wv, rowidx, m_count, n_count, ldx, wk, dual, xoff2);
     const __amdgpu_buffer_rsrc_t xr = buffer_rsrc(X, xbytes);
     __amdgpu_buffer_rsrc_t wr[WPW];
     {
@@ -289,7 +301,7 @@ struct Gemm2 {
 #pragma unroll
     for (int fn = 0; fn < FN; fn++)
 #pragma unroll
-      for (int fm = 0; fm < FM; fm++) acc[fn][fm] = (f32x4){0.f, 0.f, 0.f, 0.f};
+      for (int fm = 0; fm < F; fm++) acc[fn][fm] = (f32x4){0.f, 0.f, 0.f, 0.f};
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int wm = wave % WM, wn = wave / WM;
     const int l16 = lane & 15, g = lane >> 4;
@@ -318,7 +330,7 @@ struct Gemm2 {
 #pragma unroll
       for (int fn = 0; fn < FN; fn++) wq[fn] = lds[wofs + fn * 64];
 #pragma unroll
-      for (int d = 0; d < XD; d++) bn[d] = xop(lds, r0, g, d);
+      for (int d = 0; d < XD; d++) bn[d] = xop<F>(lds, r0, g, d);
 #pragma unroll
       for (int fn = 0; fn < FN; fn++) unpack16_nat(wq[fn], a0[fn], a1[fn]);
     }
@@ -326,15 +338,15 @@ struct Gemm2 {
     for (int t = 0; t < nks; t++) {
       const uint32_t *cur = lds + (t % NS) * STAGE;
       const uint32_t *nxt = lds + ((t + 1) % NS) * STAGE;
-      u32x4 b[2 * FM];
+      u32x4 b[2 * F];
 #pragma unroll
       for (int d = 0; d < XD; d++) b[d] = bn[d];
       __builtin_amdgcn_sched_barrier(0);
       // first half: the low 8 codes of each weight word
 #pragma unroll
-      for (int fm = 0; fm < FM; fm++) {
+      for (int fm = 0; fm < F; fm++) {
         const int q = fm;
-        b[q + XD] = xop(cur, r0, g, q + XD);
+        b[q + XD] = xop<F>(cur, r0, g, q + XD);
 #pragma unroll
         for (int fn = 0; fn < FN; fn++) mfma16_acc(acc[fn][fm], a0[fn], b[q]);
         __builtin_amdgcn_sched_barrier(0);
@@ -348,10 +360,10 @@ struct Gemm2 {
       uint32_t wqn[FN];
       u32x4 a0n[FN], a1n[FN];
 #pragma unroll
-      for (int fm = 0; fm < FM; fm++) {
-        const int q = FM + fm;
-        if (q + XD < 2 * FM) b[q + XD] = xop(cur, r0, g, q + XD);
-        else bn[q + XD - 2 * FM] = xop(nxt, r0, g, q + XD - 2 * FM);
+      for (int fm = 0; fm < F; fm++) {
+        const int q = F + fm;
+        if (q + XD < 2 * F) b[q + XD] = xop<F>(cur, r0, g, q + XD);
+        else bn[q + XD - 2 * F] = xop<F>(nxt, r0, g, q + XD - 2 * F);
         if (fm == 0) {
 #pragma unroll
           for (int fn = 0; fn < FN; fn++) wqn[fn] = nxt[wofs + fn * 64];
@@ -366,7 +378,7 @@ struct Gemm2 {
         __builtin_amdgcn_sched_barrier(0);
       }
 #pragma unroll
-      for (int fn = FM - 2; fn < FN; fn++) unpack16_nat(wqn[fn], a0n[fn], a1n[fn]);
+      for (int fn = F - 2; fn < FN; fn++) unpack16_nat(wqn[fn], a0n[fn], a1n[fn]);
 #pragma unroll
       for (int fn = 0; fn < FN; fn++) {
         a0[fn] = a0n[fn];

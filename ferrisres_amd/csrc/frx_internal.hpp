@@ -138,16 +138,16 @@ struct MoeWorkspace {
   int *offsets;        // [E+1] exclusive scan of counts
   int *perm_token;     // [T*k] token of each expert-sorted row
   int *inv;            // [T*k] expert-sorted row of assignment t*k+j
-  int *tiles;          // [2*max_tiles] (expert, first row) per M tile
+  int *tiles;          // [4*max_tiles] (expert, first row, rows, token blocks)
+                       // per M tile
   int *ntiles;         // [1]
   uint16_t *h_hi;      // [T*k][I] SwiGLU output, bf16 hi plane; the bf16
                        // engine-2 path uses h_hi.. as [T*k][2I] (hi | lo
                        // halves per row; h_lo follows h_hi contiguously)
   uint16_t *h_lo;      // [T*k][I] lo plane
   float *dout;         // [T*k][H] down-projection rows
-  float *dout_lo;      // [T*k][H] second partial (engine-2 path: lo halves)
-  float *dout2;        // [2][T*k][H] engine-2 path with split K: the second
-                       // K half's hi and lo partials
+  float *dout_lo;      // [T*k][H] second partial (engine-2 path: the second
+                       // K part)
 };
 size_t moe_workspace_bytes(int T, int H, int I, int E, int top_k);
 void moe_workspace_carve(void *base, int T, int H, int I, int E, int top_k,

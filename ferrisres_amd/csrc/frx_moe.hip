@@ -10,12 +10,14 @@
 //                    descending sort of the probabilities, top-k, weights.
 //   2. group         one workgroup: per-expert histogram, exclusive scan and
 //                    a stable scatter of the (token, k) assignments into
-//                    expert-sorted rows, plus the M-tile schedule.
+//                    expert-sorted rows, plus the M-tile schedule (tiles
+//                    sized to each expert's tokens).
 //   3. gateup        grouped GEMM over the tile schedule: gathered token rows
 //                    x W_gate[e] and x W_up[e] in one workgroup, SwiGLU (or
 //                    GeLU-tanh) epilogue, h stored as bf16 hi/lo planes.
-//   4. down          grouped GEMM h x W_down[e] (hi and lo planes: two MFMAs
-//                    per operand), fp32 rows.
+//   4. down          grouped GEMM h x W_down[e] (hi and lo planes in one K
+//                    loop, on separate waves that share the weight tile),
+//                    fp32 rows.
 //   5. combine       out[t] = sum_k w[t,k] * d[row(t,k)] in k order from 0.0,
 //                    exactly the reference's accumulation (deterministic).
 #include "frx_gemm2.hpp"
@@ -38,11 +40,10 @@ size_t moe_workspace_bytes(int T, int H, int I, int E, int top_k) {
   b += align256((size_t)E * 4);         // counts
   b += align256((size_t)(E + 1) * 4);   // offsets
   b += align256(A * 4) * 2;             // perm_token, inv
-  b += align256(max_tiles * 8);         // tiles
+  b += align256(max_tiles * 16);        // tiles
   b += align256(4);                     // ntiles
   b += align256(A * I * 2) * 2;         // h planes
   b += align256(A * H * 4) * 2;         // dout, dout_lo
-  b += align256(A * H * 4 * 2);         // dout2 (second K half)
   return b;
 }
 
@@ -58,13 +59,12 @@ void moe_workspace_carve(void *base, int T, int H, int I, int E, int top_k,
   ws->offsets = reinterpret_cast<int *>(take((size_t)(E + 1) * 4));
   ws->perm_token = reinterpret_cast<int *>(take(A * 4));
   ws->inv = reinterpret_cast<int *>(take(A * 4));
-  ws->tiles = reinterpret_cast<int *>(take(max_tiles * 8));
+  ws->tiles = reinterpret_cast<int *>(take(max_tiles * 16));
   ws->ntiles = reinterpret_cast<int *>(take(4));
   ws->h_hi = reinterpret_cast<uint16_t *>(take(A * I * 2));
   ws->h_lo = reinterpret_cast<uint16_t *>(take(A * I * 2));
   ws->dout = reinterpret_cast<float *>(take(A * H * 4));
   ws->dout_lo = reinterpret_cast<float *>(take(A * H * 4));
-  ws->dout2 = reinterpret_cast<float *>(take(A * H * 4 * 2));
 }
 
 template <typename T>
@@ -545,8 +545,14 @@ __global__ __launch_bounds__(RT_NT) void moe_router_res_kernel(
 }
 
 // ---- 2. histogram / scan / stable scatter / tile schedule -----------------
+// Tiles: 4 ints each, (expert, first row within the expert, rows, token
+// blocks). An expert's rows are split into ceil(rows / bm_max) tiles of
+// equal height (the last one shorter); token blocks = max(fm_min,
+// ceil(rows / 16)) is the number of 16-row MFMA blocks a tile multiplies.
+// The list runs by descending token blocks so that the largest tiles are
+// dispatched first.
 __global__ __launch_bounds__(1024) void moe_group_kernel(
-    const uint32_t *__restrict__ idx, int A, int top_k, int E, int bm,
+    const uint32_t *__restrict__ idx, int A, int top_k, int E, int bm_max, int fm_min,
     int *__restrict__ counts, int *__restrict__ offsets,
     int *__restrict__ perm_token, int *__restrict__ inv,
     int *__restrict__ tiles, int *__restrict__ ntiles) {
@@ -581,20 +587,34 @@ __global__ __launch_bounds__(1024) void moe_group_kernel(
     __syncthreads();
   }
   if (tid == 0) {
-    int run = 0, nt = 0;
+    int run = 0;
     for (int ee = 0; ee < E; ee++) {
       offs[ee] = run;
       counts[ee] = base[ee];
       offsets[ee] = run;
-      for (int m0 = 0; m0 < base[ee]; m0 += bm) {
-        tiles[2 * nt] = ee;
-        tiles[2 * nt + 1] = m0;
-        nt++;
-      }
       run += base[ee];
     }
     offs[E] = run;
     offsets[E] = run;
+    const int fm_top = max(fm_min, (bm_max + 15) / 16);
+    int nt = 0;
+    for (int f = fm_top; f >= fm_min; f--) {
+      for (int ee = 0; ee < E; ee++) {
+        const int c = base[ee];
+        if (c == 0) continue;
+        const int n = (c + bm_max - 1) / bm_max, rows = (c + n - 1) / n;
+        // rows <= bm_max and (n - 1) * rows < c: every tile is non-empty
+        for (int i = 0; i < n; i++) {
+          const int m0 = i * rows, mc = min(rows, c - m0);
+          if (max(fm_min, (mc + 15) / 16) != f) continue;
+          tiles[4 * nt] = ee;
+          tiles[4 * nt + 1] = m0;
+          tiles[4 * nt + 2] = mc;
+          tiles[4 * nt + 3] = f;
+          nt++;
+        }
+      }
+    }
     *ntiles = nt;
   }
   __syncthreads();
@@ -627,8 +647,8 @@ __global__ __launch_bounds__(256) void moe_gateup_kernel(
   __shared__ __align__(16) uint32_t lds[Core::LDS_DWORDS];
   const int tile = blockIdx.y;
   if (tile >= *ntiles) return;
-  const int e = tiles[2 * tile], mstart = tiles[2 * tile + 1];
-  const int mcount = min(MOE_BM, counts[e] - mstart);
+  const int e = tiles[4 * tile], mstart = tiles[4 * tile + 1];
+  const int mcount = tiles[4 * tile + 2];
   const int row0 = offsets[e] + mstart;
   const int n0 = blockIdx.x * MOE_BN;
   XDesc xd{x, nullptr, perm_token + row0, 0, H, 1};
@@ -685,8 +705,8 @@ __global__ __launch_bounds__(256) void moe_down_kernel(
   __shared__ __align__(16) uint32_t lds[Core::LDS_DWORDS];
   const int tile = blockIdx.y;
   if (tile >= *ntiles) return;
-  const int e = tiles[2 * tile], mstart = tiles[2 * tile + 1];
-  const int mcount = min(MOE_BM, counts[e] - mstart);
+  const int e = tiles[4 * tile], mstart = tiles[4 * tile + 1];
+  const int mcount = tiles[4 * tile + 2];
   const int row0 = offsets[e] + mstart;
   const int n0 = blockIdx.x * MOE_BN;
   XDesc xd{h_hi, h_lo, nullptr, (long)row0, I, 1};
@@ -710,48 +730,44 @@ __global__ __launch_bounds__(256) void moe_down_kernel(
 }
 
 // ---- 3b/4b. the grouped GEMMs on the pipelined engine -------------------------
-// bf16 activations, H % 64 == 0, I % 64 == 0, 16-byte aligned weights. Tiles
-// of MOE_BM expert-sorted rows. gate/up: one 256-row weight tile holds 128
-// gate rows and the same 128 up rows (frx_gemm2.hpp dual weights), token
-// rows gathered through perm_token; the epilogue writes h = act(g) * u as
-// bf16 hi | lo halves of one row of h2 [A][2 I]. down: the hi halves and the
-// lo halves of h2's rows times W_down in separate workgroups (blockIdx.z),
-// each into its own fp32 partial [A][H]; the combine adds the two.
-// (512-row tiles measured slower for both GEMMs at the 512-token, 16-expert
-// layer: gate/up 85.6 -> 98.5 us, down 73.5 -> 83.8 us; half the
-// workgroups at two waves per SIMD cost more than the halved activation
-// re-reads save)
-constexpr int MOE2_BN = 256;
-// gate/up tile: MOE_GU_BN / 2 gate rows and the same up rows (128 measured
-// slower at the 512-token, 16-expert layer: 92 us against 89 us, although
-// its 2112 workgroups fill the CUs more evenly than 1056)
+// bf16 activations, H % 64 == 0, I % 64 == 0, 16-byte aligned weights. A tile
+// holds up to MOE3_BM expert-sorted token rows (the schedule of
+// moe_group_kernel with bm_max = MOE3_BM) and multiplies 4, 5 or 6 blocks of
+// 16 tokens, chosen per tile at run time, so that an expert with up to 96
+// tokens streams its weights once and pads to 16 rows at most.
+constexpr int MOE3_BM = 96;
+constexpr int MOE3_FMIN = 4;  // the engine's operand schedule needs 4 token blocks
+// gate/up: one 256-row weight tile holds 128 gate rows and the same 128 up
+// rows (frx_gemm2.hpp dual weights), token rows gathered through
+// perm_token; the epilogue writes h = act(g) * u as bf16 hi | lo halves of
+// one row of h2 [A][2 I].
 constexpr int MOE_GU_BN = 256;
-constexpr int MOE_NS = 4;  // pipeline stages of the K loop
-using MoeGateUpCore = Gemm2<MOE_BM, MOE_GU_BN, 1, 4, MOE_NS, true>;
-using MoeDownCore = Gemm2<MOE_BM, MOE2_BN, 1, 4, MOE_NS, false>;
+constexpr int MOE_NS = 4;  // pipeline stages of the gate/up K loop
+using MoeGateUpCore = Gemm2<MOE3_BM, MOE_GU_BN, 1, 4, MOE_NS, true>;
+// down: the X stage holds a tile's rows twice (DUALX), as their hi halves
+// (stage rows 0..95, waves 0 and 2) and their lo halves (rows 96..191, waves
+// 1 and 3); each pair of waves shares 64 weight rows, so one K loop covers
+// both planes of h and the lo waves hand their sums to the hi waves at the
+// end: d = 0.5 s (acc_hi + acc_lo), fp32 rows of dout.
+constexpr int MOE3_DBN = 128;
+constexpr int MOE3_DNS = 3;
+using MoeDownCore = Gemm2<2 * MOE3_BM, MOE3_DBN, 2, 2, MOE3_DNS, false, true>;
+static_assert(MoeGateUpCore::FM == 6 && MoeDownCore::FM == 6, "token blocks per tile");
 
-__global__ __launch_bounds__(256) void moe_gateup2_kernel(
-    const GateUpArgs args, const uint16_t *__restrict__ x, int T, int H, int I,
-    const int *__restrict__ tiles, const int *__restrict__ ntiles,
-    const int *__restrict__ counts, const int *__restrict__ offsets,
-    const int *__restrict__ perm_token, uint16_t *__restrict__ h2, int gelu) {
+template <int F>
+__device__ __forceinline__ void gateup_tile(uint32_t *lds, const GateUpArgs &args, const uint16_t *x, int T, int H,
+                                            int I, int e, int mcount, int row0, const int *perm_token,
+                                            uint16_t *h2, int gelu) {
   using Core = MoeGateUpCore;
-  extern __shared__ __align__(16) uint32_t lds[];
-  const int tile = blockIdx.y;
-  if (tile >= *ntiles) return;  // whole workgroup
-  const int e = tiles[2 * tile], mstart = tiles[2 * tile + 1];
-  const int mcount = min(MOE_BM, counts[e] - mstart);
-  const int row0 = offsets[e] + mstart;
   const int n0 = blockIdx.x * (MOE_GU_BN / 2), nc = min(MOE_GU_BN / 2, I - n0);
-  f32x4 acc[Core::FN][Core::FM];
-  Core::run(lds, x, (uint32_t)T * (uint32_t)H * 2u, perm_token + row0, mcount,
-            args.wg[e] + (size_t)n0 * (H >> 4), nc, H, acc, args.wu[e] + (size_t)n0 * (H >> 4), H);
-  // Epilogue: fragments to LDS in two passes of 32 tokens (row pitch
-  // MOE_GU_BN + 16 floats); each thread then owns 4 gate columns (and the
-  // same 4 up columns MOE_GU_BN / 2 further) of a run of tokens per pass.
-  constexpr int PF = MOE_GU_BN + 16, P = (MOE_BM / 2) * PF <= Core::LDS_DWORDS ? 2 : 4;
-  constexpr int TMP = MOE_BM / P, FMP = Core::FM / P;
-  static_assert(TMP * PF <= Core::LDS_DWORDS, "epilogue staging");
+  f32x4 acc[Core::FN][F];
+  Core::template run<F>(lds, x, (uint32_t)T * (uint32_t)H * 2u, perm_token + row0, mcount,
+                        args.wg[e] + (size_t)n0 * (H >> 4), nc, H, acc, args.wu[e] + (size_t)n0 * (H >> 4), H);
+  // Epilogue: the fragments go to LDS in passes of up to PB token blocks (row
+  // pitch MOE_GU_BN + 16 floats); each thread then owns 4 gate columns (and
+  // the same 4 up columns MOE_GU_BN / 2 further) of a run of tokens per pass.
+  constexpr int PF = MOE_GU_BN + 16, PB = 3;
+  static_assert(PB * 16 * PF <= Core::LDS_DWORDS, "epilogue staging");
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, l16 = lane & 15, g = lane >> 4;
   float *st = reinterpret_cast<float *>(lds);
   constexpr int CT = MOE_GU_BN / 8, RT = 256 / CT;  // column threads, rows per iteration
@@ -764,16 +780,18 @@ __global__ __launch_bounds__(256) void moe_gateup2_kernel(
     suv[j] = 0.5f * args.su[e][n];
   }
 #pragma unroll
-  for (int p = 0; p < P; p++) {
+  for (int f0 = 0; f0 < F; f0 += PB) {
 #pragma unroll
     for (int fn = 0; fn < Core::FN; fn++)
 #pragma unroll
-      for (int fmi = 0; fmi < FMP; fmi++)
-        *reinterpret_cast<f32x4 *>(st + (fmi * 16 + l16) * PF + wave * Core::TN + fn * 16 + 4 * g) =
-            acc[fn][p * FMP + fmi];
+      for (int fi = 0; fi < PB; fi++)
+        if (f0 + fi < F)
+          *reinterpret_cast<f32x4 *>(st + (fi * 16 + l16) * PF + wave * Core::TN + fn * 16 + 4 * g) =
+              acc[fn][f0 + fi];
     __syncthreads();
-    for (int lr = rr; lr < TMP; lr += RT) {
-      const int m = p * TMP + lr;
+    const int rows = min(PB, F - f0) * 16;
+    for (int lr = rr; lr < rows; lr += RT) {
+      const int m = f0 * 16 + lr;
       if (m >= mcount || 4 * c >= nc) continue;
       const f32x4 gv = *reinterpret_cast<const f32x4 *>(st + lr * PF + 4 * c) * sgv;
       const f32x4 uv = *reinterpret_cast<const f32x4 *>(st + lr * PF + MOE_GU_BN / 2 + 4 * c) * suv;
@@ -798,45 +816,94 @@ __global__ __launch_bounds__(256) void moe_gateup2_kernel(
   }
 }
 
-// blockIdx.z = half + 2 * part: the hi or lo half of h (two fp32 partials,
-// as in the reference's single f32 sum to 2^-17) times columns
-// [part * ks, part * ks + ks) of the down rows. ks = I / 2 when I % 128 == 0:
-// the split gives three workgroups per CU at the 512-token, 16-expert layer
-// instead of a 2 / 1 mix (384 workgroups); the partials are summed by the
-// combine in a fixed order.
-__global__ __launch_bounds__(256) void moe_down2_kernel(
-    const DownArgs args, const uint16_t *__restrict__ h2, int H, int I, int ks,
+// grid (ceil(I / 128), tile slots); slots past *ntiles exit at once.
+__global__ __launch_bounds__(256) void moe_gateup3_kernel(
+    const GateUpArgs args, const uint16_t *__restrict__ x, int T, int H, int I,
     const int *__restrict__ tiles, const int *__restrict__ ntiles,
-    const int *__restrict__ counts, const int *__restrict__ offsets,
-    float *__restrict__ dout, float *__restrict__ dout_lo, float *__restrict__ dout2, int A) {
-  using Core = MoeDownCore;
+    const int *__restrict__ offsets, const int *__restrict__ perm_token,
+    uint16_t *__restrict__ h2, int gelu) {
   extern __shared__ __align__(16) uint32_t lds[];
   const int tile = blockIdx.y;
   if (tile >= *ntiles) return;  // whole workgroup
-  const int e = tiles[2 * tile], mstart = tiles[2 * tile + 1];
-  const int mcount = min(MOE_BM, counts[e] - mstart);
-  const int row0 = offsets[e] + mstart;
-  const int n0 = blockIdx.x * MOE2_BN, nc = min(MOE2_BN, H - n0);
-  const int half = blockIdx.z & 1, part = blockIdx.z >> 1;  // half 0: hi, 1: lo
+  const int e = tiles[4 * tile], row0 = offsets[e] + tiles[4 * tile + 1];
+  const int mcount = tiles[4 * tile + 2], f = tiles[4 * tile + 3];
+  if (f <= 4) gateup_tile<4>(lds, args, x, T, H, I, e, mcount, row0, perm_token, h2, gelu);
+  else if (f == 5) gateup_tile<5>(lds, args, x, T, H, I, e, mcount, row0, perm_token, h2, gelu);
+  else gateup_tile<6>(lds, args, x, T, H, I, e, mcount, row0, perm_token, h2, gelu);
+}
+
+template <int F>
+__device__ __forceinline__ void down_tile(uint32_t *lds, const DownArgs &args, const uint16_t *h2, int H, int I,
+                                          int ks, int part, int nt, int e, int mcount, int row0, float *dout) {
+  using Core = MoeDownCore;
+  const int n0 = nt * MOE3_DBN, nc = min(MOE3_DBN, H - n0);
   const int k0 = part * ks;
-  f32x4 acc[Core::FN][Core::FM];
-  Core::run(lds, h2 + (size_t)row0 * (2 * (size_t)I) + half * I + k0,
-            (uint32_t)mcount * (uint32_t)I * 4u - (uint32_t)(half * I + k0) * 2u, nullptr, mcount,
-            args.wd[e] + (size_t)n0 * (I >> 4) + (k0 >> 4), nc, ks, acc, nullptr, I, 2 * I);
-  float *out = part == 0 ? (half ? dout_lo : dout) : dout2 + (size_t)half * A * H;
-  Core::template store_tile<float>(lds, acc, args.sd[e], out, (size_t)H, row0, mcount, n0, nc);
+  f32x4 acc[Core::FN][F];
+  // X = the tile's rows of h2 from column k0; stage rows >= 96 read the same
+  // rows I columns further (the lo halves)
+  Core::template run<F>(lds, h2 + (size_t)row0 * (2 * (size_t)I) + k0,
+                        (uint32_t)mcount * (uint32_t)I * 4u - (uint32_t)k0 * 2u, nullptr, mcount,
+                        args.wd[e] + (size_t)n0 * (I >> 4) + (k0 >> 4), nc, ks, acc, nullptr, I, 2 * I,
+                        (uint32_t)I * 2u);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, wm = wave % 2, wn = wave / 2;
+  // lane-linear exchange slots: [wn][fn][fm][lane] of 16 bytes (48 KB)
+  f32x4 *xs = reinterpret_cast<f32x4 *>(lds);
+  if (wm == 1) {
+#pragma unroll
+    for (int fn = 0; fn < Core::FN; fn++)
+#pragma unroll
+      for (int fm = 0; fm < F; fm++) xs[((wn * Core::FN + fn) * F + fm) * 64 + lane] = acc[fn][fm];
+  }
+  __syncthreads();
+  if (wm == 0) {
+    const int l16 = lane & 15, g = lane >> 4;
+#pragma unroll
+    for (int fn = 0; fn < Core::FN; fn++) {
+      const int nl = wn * Core::TN + fn * 16 + 4 * g;
+      if (nl >= nc) continue;
+      const int nok = min(4, nc - nl);
+      const f32x4 sd = load_scale4(args.sd[e], n0 + nl, nok) * 0.5f;
+#pragma unroll
+      for (int fm = 0; fm < F; fm++) {
+        const int m = fm * 16 + l16;
+        const f32x4 v = (acc[fn][fm] + xs[((wn * Core::FN + fn) * F + fm) * 64 + lane]) * sd;
+        if (m < mcount) YStore<float>::store4(dout + (size_t)(row0 + m) * H + n0 + nl, v, nok);
+      }
+    }
+  }
+}
+
+// 1-D grid of 8 * slots * NTN * KP workgroups (NTN = ceil(H / 128) column
+// tiles, KP = I / ks K parts). Workgroup L runs on XCD L % 8 (the dispatch
+// order of the 8 XCDs); each XCD takes the tiles t with t % 8 == its index
+// and all NTN * KP items of such a tile, so a tile's h rows are fetched into
+// one L2. Part p of the K range writes its own fp32 rows (dout, dout_lo);
+// the combine adds them in a fixed order.
+__global__ __launch_bounds__(256) void moe_down3_kernel(
+    const DownArgs args, const uint16_t *__restrict__ h2, int H, int I, int ks, int ntn, int kp,
+    const int *__restrict__ tiles, const int *__restrict__ ntiles, const int *__restrict__ offsets,
+    float *__restrict__ dout, float *__restrict__ dout_lo) {
+  extern __shared__ __align__(16) uint32_t lds[];
+  const int L = blockIdx.x, xcd = L & 7, j = L >> 3, per = ntn * kp;
+  const int tile = xcd + 8 * (j / per);
+  if (tile >= *ntiles) return;  // whole workgroup
+  const int item = j % per, nt = item % ntn, part = item / ntn;
+  const int e = tiles[4 * tile], row0 = offsets[e] + tiles[4 * tile + 1];
+  const int mcount = tiles[4 * tile + 2], f = tiles[4 * tile + 3];
+  float *out = part == 0 ? dout : dout_lo;
+  if (f <= 4) down_tile<4>(lds, args, h2, H, I, ks, part, nt, e, mcount, row0, out);
+  else if (f == 5) down_tile<5>(lds, args, h2, H, I, ks, part, nt, e, mcount, row0, out);
+  else down_tile<6>(lds, args, h2, H, I, ks, part, nt, e, mcount, row0, out);
 }
 
 // ---- 5. combine ---------------------------------------------------------------
 // cpu_block_attn_res.rs:1179 `expert_outputs[t*hd+d] += w * down[d]`, k order.
-// dout_lo != nullptr: the down rows arrive as two partials (hi and lo halves
-// of the activation), d = dout + dout_lo; dout2 != nullptr: two more (the
-// second K half's hi and lo, A rows apart), d = (dout + dout_lo) + (hi2 + lo2).
+// dout_lo != nullptr: the down rows arrive as two partials (the engine-2 K
+// parts), d = dout + dout_lo.
 template <typename YT>
 __global__ __launch_bounds__(256) void moe_combine_kernel(
-    const float *__restrict__ dout, const float *__restrict__ dout_lo, const float *__restrict__ dout2,
-    int A, const float *__restrict__ wts, const int *__restrict__ inv, int H, int top_k,
-    YT *__restrict__ y, int skip_small) {
+    const float *__restrict__ dout, const float *__restrict__ dout_lo, const float *__restrict__ wts,
+    const int *__restrict__ inv, int H, int top_k, YT *__restrict__ y, int skip_small) {
   const int t = blockIdx.x;
   for (int j = threadIdx.x * 4; j < H; j += 1024) {  // H % 16 == 0
     f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -849,9 +916,6 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(
       const long o = (long)inv[t * top_k + k] * H + j;
       f32x4 d = *reinterpret_cast<const f32x4 *>(dout + o);
       if (dout_lo) d = d + *reinterpret_cast<const f32x4 *>(dout_lo + o);
-      if (dout2)
-        d = d + (*reinterpret_cast<const f32x4 *>(dout2 + o) +
-                 *reinterpret_cast<const f32x4 *>(dout2 + (long)A * H + o));
       const f32x4 prod = d * w;
       acc = acc + prod;
     }
@@ -914,12 +978,19 @@ hipError_t launch_moe(const void *x, int xt_bf16, const void *router,
                        (const float *)x, (const float *)router, T, H, E, EP, top_k, rch, ws.idx, ws.wts, topk_idx, topk_w, routing);
   hipError_t err = hipGetLastError();
   if (err != hipSuccess) return err;
+  // engine 2 (pipelined MFMA GEMMs): bf16 x, H and I multiples of 64,
+  // 16-byte aligned weights; otherwise the register-staged engine 1
+  bool engine2 = xt_bf16 && H % 64 == 0 && I % 64 == 0;
+  for (int i = 0; i < E && engine2; i++)
+    engine2 = ((reinterpret_cast<uintptr_t>(w_gate[i]) | reinterpret_cast<uintptr_t>(w_up[i]) |
+                reinterpret_cast<uintptr_t>(w_down[i])) & 15) == 0;
   // 2. group
-  hipLaunchKernelGGL(moe_group_kernel, dim3(1), dim3(1024), 0, stream, ws.idx, A, top_k, E,
-                     MOE_BM, ws.counts, ws.offsets, ws.perm_token, ws.inv, ws.tiles, ws.ntiles);
+  const int bm_max = engine2 ? MOE3_BM : MOE_BM;
+  hipLaunchKernelGGL(moe_group_kernel, dim3(1), dim3(1024), 0, stream, ws.idx, A, top_k, E, bm_max,
+                     engine2 ? MOE3_FMIN : 1, ws.counts, ws.offsets, ws.perm_token, ws.inv, ws.tiles, ws.ntiles);
   if ((err = hipGetLastError()) != hipSuccess) return err;
   // 3. gate/up
-  const int max_tiles = (A + MOE_BM - 1) / MOE_BM + E;
+  const int max_tiles = (A + bm_max - 1) / bm_max + E;
   GateUpArgs ga;
   for (int i = 0; i < MOE_MAXE; i++) {
     const bool v = i < E;
@@ -928,52 +999,55 @@ hipError_t launch_moe(const void *x, int xt_bf16, const void *router,
     ga.sg[i] = v ? s_gate[i] : nullptr;
     ga.su[i] = v ? s_up[i] : nullptr;
   }
-  bool engine2 = xt_bf16 && H % 64 == 0 && I % 64 == 0;
-  bool down_split = false;  // engine-2 down GEMM in two K halves (four partials)
-  for (int i = 0; i < E && engine2; i++)
-    engine2 = ((reinterpret_cast<uintptr_t>(w_gate[i]) | reinterpret_cast<uintptr_t>(w_up[i]) |
-                reinterpret_cast<uintptr_t>(w_down[i])) & 15) == 0;
   DownArgs da;
   for (int i = 0; i < MOE_MAXE; i++) {
     da.wd[i] = i < E ? w_down[i] : nullptr;
     da.sd[i] = i < E ? s_down[i] : nullptr;
   }
+  bool two_parts = false;  // engine-2 down GEMM in two K parts (dout, dout_lo)
   if (engine2) {
+    const int gu_lds = MoeGateUpCore::LDS_DWORDS * 4, dn_lds = MoeDownCore::LDS_DWORDS * 4;
+    static std::atomic<uint64_t> done_gu, done_dn;
+    if ((err = opt_in_lds(reinterpret_cast<const void *>(&moe_gateup3_kernel), gu_lds, done_gu)) != hipSuccess)
+      return err;
+    if ((err = opt_in_lds(reinterpret_cast<const void *>(&moe_down3_kernel), dn_lds, done_dn)) != hipSuccess)
+      return err;
     const dim3 g1((I + MOE_GU_BN / 2 - 1) / (MOE_GU_BN / 2), max_tiles);
-    hipLaunchKernelGGL(moe_gateup2_kernel, g1, dim3(256), MoeGateUpCore::LDS_DWORDS * 4, stream, ga,
-                       (const uint16_t *)x, T, H, I, ws.tiles, ws.ntiles, ws.counts, ws.offsets,
-                       ws.perm_token, ws.h_hi, gelu);
+    hipLaunchKernelGGL(moe_gateup3_kernel, g1, dim3(256), gu_lds, stream, ga, (const uint16_t *)x, T, H, I,
+                       ws.tiles, ws.ntiles, ws.offsets, ws.perm_token, ws.h_hi, gelu);
     if ((err = hipGetLastError()) != hipSuccess) return err;
-    const int ks = I % 128 == 0 ? I / 2 : I;
-    const dim3 g2((H + MOE2_BN - 1) / MOE2_BN, max_tiles, ks < I ? 4 : 2);
-    hipLaunchKernelGGL(moe_down2_kernel, g2, dim3(256), MoeDownCore::LDS_DWORDS * 4, stream, da, ws.h_hi,
-                       H, I, ks, ws.tiles, ws.ntiles, ws.counts, ws.offsets, ws.dout, ws.dout_lo, ws.dout2, A);
-    down_split = ks < I;
+    // two K parts when each is a whole number of 64-column steps: twice the
+    // workgroups (two per CU at the 512-token, 16-expert layer)
+    const int ks = I % 128 == 0 ? I / 2 : I, kp = I / ks;
+    const int ntn = (H + MOE3_DBN - 1) / MOE3_DBN;
+    const int slots = (max_tiles + 7) / 8 * 8;
+    hipLaunchKernelGGL(moe_down3_kernel, dim3(slots * ntn * kp), dim3(256), dn_lds, stream, da,
+                       (const uint16_t *)ws.h_hi, H, I, ks, ntn, kp, ws.tiles, ws.ntiles, ws.offsets, ws.dout,
+                       ws.dout_lo);
+    two_parts = kp == 2;
     if ((err = hipGetLastError()) != hipSuccess) return err;
   } else {
-  dim3 g1((I + MOE_BN - 1) / MOE_BN, max_tiles);
-  if (xt_bf16)
-    hipLaunchKernelGGL((moe_gateup_kernel<XS_BF16>), g1, dim3(256), 0, stream, ga, x, H, I,
-                       ws.tiles, ws.ntiles, ws.counts, ws.offsets, ws.perm_token, ws.h_hi, ws.h_lo, gelu);
-  else
-    hipLaunchKernelGGL((moe_gateup_kernel<XS_F32>), g1, dim3(256), 0, stream, ga, x, H, I,
-                       ws.tiles, ws.ntiles, ws.counts, ws.offsets, ws.perm_token, ws.h_hi, ws.h_lo, gelu);
-  if ((err = hipGetLastError()) != hipSuccess) return err;
-  // 4. down
-  dim3 g2((H + MOE_BN - 1) / MOE_BN, max_tiles);
-  hipLaunchKernelGGL(moe_down_kernel, g2, dim3(256), 0, stream, da, ws.h_hi, ws.h_lo, H, I,
-                     ws.tiles, ws.ntiles, ws.counts, ws.offsets, ws.dout);
-  if ((err = hipGetLastError()) != hipSuccess) return err;
+    dim3 g1((I + MOE_BN - 1) / MOE_BN, max_tiles);
+    if (xt_bf16)
+      hipLaunchKernelGGL((moe_gateup_kernel<XS_BF16>), g1, dim3(256), 0, stream, ga, x, H, I,
+                         ws.tiles, ws.ntiles, ws.counts, ws.offsets, ws.perm_token, ws.h_hi, ws.h_lo, gelu);
+    else
+      hipLaunchKernelGGL((moe_gateup_kernel<XS_F32>), g1, dim3(256), 0, stream, ga, x, H, I,
+                         ws.tiles, ws.ntiles, ws.counts, ws.offsets, ws.perm_token, ws.h_hi, ws.h_lo, gelu);
+    if ((err = hipGetLastError()) != hipSuccess) return err;
+    // 4. down
+    dim3 g2((H + MOE_BN - 1) / MOE_BN, max_tiles);
+    hipLaunchKernelGGL(moe_down_kernel, g2, dim3(256), 0, stream, da, ws.h_hi, ws.h_lo, H, I,
+                       ws.tiles, ws.ntiles, ws.counts, ws.offsets, ws.dout);
+    if ((err = hipGetLastError()) != hipSuccess) return err;
   }
   // 5. combine
   if (yt_bf16)
     hipLaunchKernelGGL((moe_combine_kernel<uint16_t>), dim3(T), dim3(256), 0, stream, ws.dout,
-                       engine2 ? ws.dout_lo : nullptr, down_split ? ws.dout2 : nullptr, A, ws.wts, ws.inv,
-                       H, top_k, (uint16_t *)y, routing);
+                       two_parts ? ws.dout_lo : nullptr, ws.wts, ws.inv, H, top_k, (uint16_t *)y, routing);
   else
     hipLaunchKernelGGL((moe_combine_kernel<float>), dim3(T), dim3(256), 0, stream, ws.dout,
-                       engine2 ? ws.dout_lo : nullptr, down_split ? ws.dout2 : nullptr, A, ws.wts, ws.inv,
-                       H, top_k, (float *)y, routing);
+                       two_parts ? ws.dout_lo : nullptr, ws.wts, ws.inv, H, top_k, (float *)y, routing);
   return hipGetLastError();
 }
 

@@ -56,7 +56,8 @@ def run_oracle(xf, rf, ex, E, top_k, gelu, tokens=None, routing=0):
 
 
 @pytest.mark.parametrize("T,H,I,E,k", [(40, 128, 256, 8, 2), (7, 64, 96, 4, 1), (130, 256, 160, 16, 2),
-                                       (64, 128, 128, 6, 3), (50, 320, 192, 5, 2), (300, 192, 448, 3, 2)])
+                                       (64, 128, 128, 6, 3), (50, 320, 192, 5, 2), (300, 192, 448, 3, 2),
+                                       (200, 128, 192, 2, 1), (97, 64, 128, 1, 1)])
 @pytest.mark.parametrize("act", [frx.ACT_SILU, frx.ACT_GELU_TANH])
 def test_moe_small_parity(ctx, T, H, I, E, k, act):
     name = f"moe/{T}x{H}x{I}x{E}"
