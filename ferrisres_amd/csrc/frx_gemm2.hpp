@@ -14,8 +14,8 @@
 // advance goes in the scalar soffset. The buffer's num_records is the tile's
 // valid byte range, so the hardware range check bounds every load.
 //  - X stage: BM rows x 64 bf16 (128 B per row) in natural order, 16-byte
-//    chunks XOR-swizzled by (row/2)%8 so the 16 rows of an MFMA operand read
-//    hit 16 disjoint bank groups.
+//    chunks XOR-swizzled (xswz) so the 16 rows of an MFMA operand read hit
+//    disjoint bank groups.
 //  - W stage: BN rows x 4 words (the reference's packed u32 words).
 // Operands. Lane (i = l%16, g = l/16) of MFMA half h covers columns
 // 16g + 8h .. 16g + 8h + 7 of the step, in natural order: the X operand is
@@ -157,6 +157,14 @@ __device__ __forceinline__ void wait_vmcnt() {
 // (their results feed MFMAs) before the barrier that precedes its reuse.
 __device__ __forceinline__ void barrier_nofence() { __builtin_amdgcn_s_barrier(); }
 
+// X-stage swizzle: 16-byte chunk c of stage row r sits at chunk c ^ xswz(r).
+// An MFMA operand read has lanes 0..15 on rows r0..r0+15 (r0 % 16 == 0) at
+// one chunk. xswz takes 8 distinct values on rows r0..r0+7 and on
+// r0+8..r0+15, and (r % 2, xswz(r)) 16 distinct pairs over the 16 rows, so
+// the read spreads over all banks whether the LDS serves 8 lanes (128 bytes)
+// or 16 lanes (256 bytes) of a 16-byte read per pass.
+__device__ __forceinline__ uint32_t xswz(int r) { return (uint32_t)((r & 7) ^ ((r >> 3) & 1)); }
+
 // DUALX: X-stage rows [BM/2, BM) are the rows [0, BM/2) again, read at a
 // second column offset (xoff2 bytes further along each row): one stage then
 // holds two column ranges of the same token rows, e.g. the hi and lo bf16
@@ -203,7 +211,7 @@ struct Gemm2 {
       const int second = DUALX && r >= BM / 2;
       const int rm = min(second ? r - BM / 2 : r, m_count - 1);
       const uint32_t gr = GATHER ? (uint32_t)rowidx[rm] : (uint32_t)rm;
-      const uint32_t c = (lane & 7) ^ ((r >> 1) & 7);  // swizzled source chunk
+      const uint32_t c = (lane & 7) ^ xswz(r);  // swizzled source chunk
       xv[i] = gr * (uint32_t)ldx * 2u + 16u * c + (second ? xoff2 : 0u);
     }
 #pragma unroll
@@ -230,7 +238,7 @@ struct Gemm2 {
   }
 
   __device__ __forceinline__ static u32x4 xread(const uint32_t *stage, int r, int c) {
-    return *reinterpret_cast<const u32x4 *>(stage + r * 32 + ((c ^ ((r >> 1) & 7)) * 4));
+    return *reinterpret_cast<const u32x4 *>(stage + r * 32 + ((c ^ xswz(r)) * 4));
   }
 
   // X operand i of a step (i = h * F + fm, F token blocks multiplied):
@@ -456,7 +464,7 @@ struct Gemm2 {
     for (int i = 0; i < XPW; i++) {
       const int r = (wave * XPW + i) * 8 + (lane >> 3);
       const int rm = min(r, m_count - 1);
-      const uint32_t c = (lane & 7) ^ ((r >> 1) & 7);
+      const uint32_t c = (lane & 7) ^ xswz(r);
       xv[i] = (uint32_t)rm * (uint32_t)K * 2u + 16u * c;
     }
 #pragma unroll

@@ -545,6 +545,17 @@ __global__ __launch_bounds__(RT_NT) void moe_router_res_kernel(
 }
 
 // ---- 2. histogram / scan / stable scatter / tile schedule -----------------
+// Exclusive prefix sum of v over the 64 lanes of a wave.
+__device__ __forceinline__ int wave_excl_scan(int v) {
+  int x = v;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const int y = __shfl_up(x, d);
+    if ((threadIdx.x & 63) >= d) x += y;
+  }
+  return x - v;
+}
+
 // Tiles: 4 ints each, (expert, first row within the expert, rows, token
 // blocks). An expert's rows are split into ceil(rows / bm_max) tiles of
 // equal height (the last one shorter); token blocks = max(fm_min,
@@ -586,36 +597,41 @@ __global__ __launch_bounds__(1024) void moe_group_kernel(
     }
     __syncthreads();
   }
-  if (tid == 0) {
-    int run = 0;
-    for (int ee = 0; ee < E; ee++) {
-      offs[ee] = run;
-      counts[ee] = base[ee];
-      offsets[ee] = run;
-      run += base[ee];
+  if (wave == 0) {
+    // lane ee: expert ee's offset (exclusive scan of the counts) and tiles
+    const int c = lane < E ? base[lane] : 0;
+    const int off = wave_excl_scan(c);
+    if (lane < E) {
+      offs[lane] = off;
+      counts[lane] = c;
+      offsets[lane] = off;
     }
-    offs[E] = run;
-    offsets[E] = run;
+    if (lane == 63) {
+      offs[E] = off + c;
+      offsets[E] = off + c;
+    }
+    // n tiles: n - 1 of `rows` rows, the last of c - (n - 1) rows
+    // (rows <= bm_max and (n - 1) * rows < c: every tile is non-empty)
+    const int n = (c + bm_max - 1) / bm_max, rows = n ? (c + n - 1) / n : 0;
+    const int fa = max(fm_min, (rows + 15) / 16), fb = max(fm_min, (c - (n - 1) * rows + 15) / 16);
     const int fm_top = max(fm_min, (bm_max + 15) / 16);
     int nt = 0;
     for (int f = fm_top; f >= fm_min; f--) {
-      for (int ee = 0; ee < E; ee++) {
-        const int c = base[ee];
-        if (c == 0) continue;
-        const int n = (c + bm_max - 1) / bm_max, rows = (c + n - 1) / n;
-        // rows <= bm_max and (n - 1) * rows < c: every tile is non-empty
-        for (int i = 0; i < n; i++) {
-          const int m0 = i * rows, mc = min(rows, c - m0);
-          if (max(fm_min, (mc + 15) / 16) != f) continue;
-          tiles[4 * nt] = ee;
-          tiles[4 * nt + 1] = m0;
-          tiles[4 * nt + 2] = mc;
-          tiles[4 * nt + 3] = f;
-          nt++;
-        }
+      const int na = (n > 1 && fa == f) ? n - 1 : 0, nb = (n > 0 && fb == f) ? 1 : 0;
+      const int before = wave_excl_scan(na + nb);
+      int pos = nt + before;
+      for (int i = 0; i < n; i++) {
+        const int fi = i < n - 1 ? fa : fb;
+        if (fi != f) continue;
+        tiles[4 * pos] = lane;
+        tiles[4 * pos + 1] = i * rows;
+        tiles[4 * pos + 2] = min(rows, c - i * rows);
+        tiles[4 * pos + 3] = f;
+        pos++;
       }
+      nt += __shfl(before + na + nb, 63);
     }
-    *ntiles = nt;
+    if (lane == 0) *ntiles = nt;
   }
   __syncthreads();
   // Pass 2: final rows.
