@@ -101,6 +101,30 @@ __device__ __forceinline__ void split2_bf16(float a, float b, uint32_t &hi, uint
   lo = __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){ra, rb}, bf16x2));
 }
 
+// Two 16-code words at once: the interleaved pairs of w0 (lo0 = pairs 0..3,
+// hi0 = pairs 4..7) and of w1, pair i = ~(w << (14 - 2i)) & 0xC000C000. The
+// words shift together as one 64-bit value (v_lshlrev_b64, full rate): the
+// bits w0 pushes into w1's half land in bits 0..13, which the mask clears.
+// 7 shifts and 16 three-input bit ops per 32 weights.
+__device__ __forceinline__ void unpack32_kil(uint32_t w0, uint32_t w1, u32x4 &lo0, u32x4 &hi0, u32x4 &lo1,
+                                             u32x4 &hi1) {
+  const uint64_t p = ((uint64_t)w1 << 32) | w0;
+  uint32_t d0[8], d1[8];
+#pragma unroll
+  for (int i = 0; i < 8; i++) {
+    uint64_t q = p;
+    // the shift stays one 64-bit op (left to the compiler it becomes a
+    // 32-bit shift plus a funnel shift per pair)
+    if (i < 7) asm("v_lshlrev_b64 %0, %1, %2" : "=v"(q) : "n"(14 - 2 * i), "v"(p));
+    d0[i] = ~(uint32_t)q & 0xC000C000u;
+    d1[i] = ~(uint32_t)(q >> 32) & 0xC000C000u;
+  }
+  lo0 = (u32x4){d0[0], d0[1], d0[2], d0[3]};
+  hi0 = (u32x4){d0[4], d0[5], d0[6], d0[7]};
+  lo1 = (u32x4){d1[0], d1[1], d1[2], d1[3]};
+  hi1 = (u32x4){d1[4], d1[5], d1[6], d1[7]};
+}
+
 // Natural bf16 dwords n[0..7] of a 16-column block (x0..x15) -> interleaved
 // dwords d[i] = x[i] | x[i+8] << 16.
 // One byte permute per output dword.

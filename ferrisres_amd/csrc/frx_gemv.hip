@@ -872,6 +872,8 @@ static hipError_t launch_gemv_rows_w(const uint32_t *w, const float *scale, cons
 // x then does not wait behind weights. Row scales are scalar loads (uniform
 // rows). Measured per launch against gemv_rows_kernel: 5.66 -> 5.50 us
 // (11008x4096, G = 2 per CU) and 5.67 -> 5.28 us (4096x11008, G = 1).
+// The weight words decode in K-interleaved pairs (unpack32_kil, two words
+// per 64-bit shift) and x is staged in the same order.
 // XF32: fp32 activations, split once per workgroup at staging into bf16 hi
 // and lo planes (split2_bf16: hi = bf16(x), lo = bf16(x - hi), |x - hi - lo|
 // <= 2^-17 |x|, lo = 0 where hi is not finite); each word then runs four
@@ -879,7 +881,7 @@ static hipError_t launch_gemv_rows_w(const uint32_t *w, const float *scale, cons
 template <typename YT, int NI, int RMAX, bool XF32>
 __global__ __launch_bounds__(512) void gemv_bal_kernel(const uint32_t *__restrict__ W, const float *__restrict__ scale,
                                                        const void *__restrict__ Xv, YT *__restrict__ Y, int K, int N,
-                                                       const float *__restrict__ bias) {
+                                                       const float *__restrict__ bias, int nq, int nr) {
   constexpr int WAVES = 8, NT = 512;
   constexpr int XPL = XF32 ? 2 : 1;
   constexpr int PP = NI * 512;                   // 8-value pieces of x staged (NI * 4096 values)
@@ -889,8 +891,10 @@ __global__ __launch_bounds__(512) void gemv_bal_kernel(const uint32_t *__restric
   extern __shared__ __align__(16) uint32_t lds[];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int b0 = (int)((long long)blockIdx.x * N / gridDim.x);
-  const int cb = (int)((long long)(blockIdx.x + 1) * N / gridDim.x) - b0;
+  // rows of this workgroup: nq = N / G each, the first nr = N % G one more
+  // (the host divides; a scalar division would delay every load)
+  const int bx = blockIdx.x;
+  const int b0 = bx * nq + min(bx, nr), cb = nq + (bx < nr ? 1 : 0);
   const int row0 = b0 + wave * cb / WAVES, cnt = b0 + (wave + 1) * cb / WAVES - row0;
   const int kw = K >> 4;
   constexpr uint32_t OOB = 0x80000000u;  // a buffer offset past any range this path takes
@@ -921,24 +925,42 @@ __global__ __launch_bounds__(512) void gemv_bal_kernel(const uint32_t *__restric
 #pragma unroll
   for (int rr = 0; rr < RMAX; rr++) sc[rr] = scale[min(row0 + rr, N - 1)];
   const float bv = bias ? bias[min(row0 + lane, N - 1)] : 0.f;  // lane's output row
-  // 3. stage: piece j -> chunk j/8, slot j%8 (per plane)
+  // 3. stage: piece j -> chunk j/8, slot j%8 (per plane), K-interleaved to
+  //    match the decode: the 16-column block b is pieces 2b (columns 0..7)
+  //    and 2b+1 (8..15), held by neighbouring lanes; after swapping pieces
+  //    with its neighbour the even lane writes block dwords 0..3 and the odd
+  //    lane dwords 4..7, dword i = x[16b + i] | x[16b + i + 8] << 16. All
+  //    lanes take part in the swap (pieces past the range are zeros).
+  auto kil = [&](const u32x4 &mine) -> u32x4 {
+    u32x4 other;
+#pragma unroll
+    for (int d = 0; d < 4; d++)
+      other[d] = (uint32_t)__builtin_amdgcn_mov_dpp((int)mine[d], 0xB1, 0xF, 0xF, false);  // quad_perm [1,0,3,2]
+    const bool odd = tid & 1;
+    const u32x4 A = odd ? other : mine, B = odd ? mine : other;
+    const uint32_t a0 = odd ? A.z : A.x, a1 = odd ? A.w : A.y, c0 = odd ? B.z : B.x, c1 = odd ? B.w : B.y;
+    return (u32x4){__builtin_amdgcn_perm(c0, a0, 0x05040100u), __builtin_amdgcn_perm(c0, a0, 0x07060302u),
+                   __builtin_amdgcn_perm(c1, a1, 0x05040100u), __builtin_amdgcn_perm(c1, a1, 0x07060302u)};
+  };
 #pragma unroll
   for (int r = 0; r < XR; r++) {
     const int j = tid + r * NT;
-    if (j < PP) {
-      uint32_t *dst = lds + (j >> 3) * ROWS_XCH + (j & 7) * 4;
-      if constexpr (XF32) {
-        const float f[8] = {__uint_as_float(xs[r][0].x), __uint_as_float(xs[r][0].y), __uint_as_float(xs[r][0].z),
-                            __uint_as_float(xs[r][0].w), __uint_as_float(xs[r][1].x), __uint_as_float(xs[r][1].y),
-                            __uint_as_float(xs[r][1].z), __uint_as_float(xs[r][1].w)};
-        uint32_t hi[4], lo[4];
+    uint32_t *dst = lds + (j >> 3) * ROWS_XCH + (j & 7) * 4;
+    if constexpr (XF32) {
+      const float f[8] = {__uint_as_float(xs[r][0].x), __uint_as_float(xs[r][0].y), __uint_as_float(xs[r][0].z),
+                          __uint_as_float(xs[r][0].w), __uint_as_float(xs[r][1].x), __uint_as_float(xs[r][1].y),
+                          __uint_as_float(xs[r][1].z), __uint_as_float(xs[r][1].w)};
+      uint32_t hi[4], lo[4];
 #pragma unroll
-        for (int e = 0; e < 4; e++) split2_bf16(f[2 * e], f[2 * e + 1], hi[e], lo[e]);
-        *reinterpret_cast<u32x4 *>(dst) = (u32x4){hi[0], hi[1], hi[2], hi[3]};
-        *reinterpret_cast<u32x4 *>(dst + PD) = (u32x4){lo[0], lo[1], lo[2], lo[3]};
-      } else {
-        *reinterpret_cast<u32x4 *>(dst) = xs[r][0];
+      for (int e = 0; e < 4; e++) split2_bf16(f[2 * e], f[2 * e + 1], hi[e], lo[e]);
+      const u32x4 h = kil((u32x4){hi[0], hi[1], hi[2], hi[3]}), l = kil((u32x4){lo[0], lo[1], lo[2], lo[3]});
+      if (j < PP) {
+        *reinterpret_cast<u32x4 *>(dst) = h;
+        *reinterpret_cast<u32x4 *>(dst + PD) = l;
       }
+    } else {
+      const u32x4 v = kil(xs[r][0]);
+      if (j < PP) *reinterpret_cast<u32x4 *>(dst) = v;
     }
   }
   __syncthreads();
@@ -964,24 +986,27 @@ __global__ __launch_bounds__(512) void gemv_bal_kernel(const uint32_t *__restric
 #pragma unroll
   for (int rr = 0; rr < RMAX; rr++) {
     if (rr < cnt) {  // wave-uniform
-      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+      // two accumulation chains (even and odd words) halve the dependent
+      // MFMA latency of a row
+      f32x4 acc2[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
 #pragma unroll
       for (int i = 0; i < NI; i++) {
         u32x4 xw[XPL][8];
         if constexpr (!XREG) xread(i, xw);
         const u32x4(&xv)[XPL][8] = XREG ? xb[XREG ? i : 0] : xw;
-        const uint32_t wq[4] = {wv[rr][i].x, wv[rr][i].y, wv[rr][i].z, wv[rr][i].w};
+        u32x4 lo[4], hi[4];
+        unpack32_kil(wv[rr][i].x, wv[rr][i].y, lo[0], hi[0], lo[1], hi[1]);
+        unpack32_kil(wv[rr][i].z, wv[rr][i].w, lo[2], hi[2], lo[3], hi[3]);
 #pragma unroll
         for (int j = 0; j < 4; j++) {
-          u32x4 lo, hi;
-          unpack16_nat(wq[j], lo, hi);
 #pragma unroll
           for (int p = 0; p < XPL; p++) {
-            acc = mfma16(lo, xv[p][2 * j], acc);
-            acc = mfma16(hi, xv[p][2 * j + 1], acc);
+            acc2[j & 1] = mfma16(lo[j], xv[p][2 * j], acc2[j & 1]);
+            acc2[j & 1] = mfma16(hi[j], xv[p][2 * j + 1], acc2[j & 1]);
           }
         }
       }
+      const f32x4 acc = acc2[0] + acc2[1];
       // diagonal: lane (c = l%16, rg = l/16) holds C[4rg + e][c]
       float v = e == 0 ? acc[0] : e == 1 ? acc[1] : e == 2 ? acc[2] : acc[3];
       v = (c >> 2) == rg ? v : 0.f;
@@ -1018,7 +1043,7 @@ static hipError_t launch_gemv_bal_w(const uint32_t *w, const float *scale, const
     if (e != hipSuccess) return e;
   }
   hipLaunchKernelGGL((gemv_bal_kernel<YT, NI, RMAX, XF32>), dim3(G), dim3(512), lds, stream, w, scale, x,
-                     reinterpret_cast<YT *>(y), K, N, bias);
+                     reinterpret_cast<YT *>(y), K, N, bias, N / G, N % G);
   return hipGetLastError();
 }
 
