@@ -719,6 +719,25 @@ __device__ __forceinline__ float dpp_f32(float v) {
 // XPL = 2: the activations arrive as two bf16 planes (X hi, X2 lo) whose sum
 // is an fp32 vector to 2^-17; both are staged and each word runs four MFMAs
 // into the same accumulator.
+// K-interleaved staging of x for the decode of unpack32_kil: the 16-column
+// block b is pieces 2b (columns 0..7) and 2b+1 (8..15) of 8 bf16, held by
+// neighbouring lanes (piece index parity = lane parity). After swapping
+// pieces with its neighbour, the even lane returns block dwords 0..3 and the
+// odd lane dwords 4..7, dword i = x[16b + i] | x[16b + i + 8] << 16, to be
+// stored where its own piece would go. Every lane of the wave must call it
+// (DPP); pieces past the data are zeros.
+__device__ __forceinline__ u32x4 stage_kil(const u32x4 &mine, int tid) {
+  u32x4 other;
+#pragma unroll
+  for (int d = 0; d < 4; d++)
+    other[d] = (uint32_t)__builtin_amdgcn_mov_dpp((int)mine[d], 0xB1, 0xF, 0xF, false);  // quad_perm [1,0,3,2]
+  const bool odd = tid & 1;
+  const u32x4 A = odd ? other : mine, B = odd ? mine : other;
+  const uint32_t a0 = odd ? A.z : A.x, a1 = odd ? A.w : A.y, c0 = odd ? B.z : B.x, c1 = odd ? B.w : B.y;
+  return (u32x4){__builtin_amdgcn_perm(c0, a0, 0x05040100u), __builtin_amdgcn_perm(c0, a0, 0x07060302u),
+                 __builtin_amdgcn_perm(c1, a1, 0x05040100u), __builtin_amdgcn_perm(c1, a1, 0x07060302u)};
+}
+
 template <typename YT, int WAVES, int RW, int NI, int NW = 1, int XPL = 1, int EPI = GEMV_LINEAR>
 __global__ __launch_bounds__(WAVES * 64) void gemv_rows_kernel(
     const uint32_t *__restrict__ W, const float *__restrict__ scale, const uint32_t *__restrict__ W2,
@@ -758,11 +777,13 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_rows_kernel(
         wv[m][rr][i] = *reinterpret_cast<const u32x4 *>(wr + min(i * 256 + 4 * lane, kw - 4));
       sc[m][rr] = (m ? scale2 : scale)[row];
     }
-  // 3. stage: plane p, 16-byte piece j -> chunk j/8, slot j%8
+  // 3. stage: plane p, 16-byte piece j -> chunk j/8, slot j%8, K-interleaved
+  //    (stage_kil; PP is even, so neighbouring pieces share a plane)
 #pragma unroll
   for (int r = 0; r < XR; r++) {
     const int j = tid + r * NT, pl = j >= PP ? 1 : 0, jp = j - pl * PP;
-    if (pl < XPL) *reinterpret_cast<u32x4 *>(lds + pl * PD + (jp >> 3) * ROWS_XCH + (jp & 7) * 4) = xs[r];
+    const u32x4 v = stage_kil(xs[r], tid);
+    if (pl < XPL) *reinterpret_cast<u32x4 *>(lds + pl * PD + (jp >> 3) * ROWS_XCH + (jp & 7) * 4) = v;
   }
   __syncthreads();
   // 4. per window: the lane's 64 activations (per plane), then each row's 4 words
@@ -784,15 +805,15 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_rows_kernel(
     for (int m = 0; m < NW; m++)
 #pragma unroll
       for (int rr = 0; rr < RW; rr++) {
-        const uint32_t wq[4] = {wv[m][rr][i].x, wv[m][rr][i].y, wv[m][rr][i].z, wv[m][rr][i].w};
+        u32x4 lo[4], hi[4];
+        unpack32_kil(wv[m][rr][i].x, wv[m][rr][i].y, lo[0], hi[0], lo[1], hi[1]);
+        unpack32_kil(wv[m][rr][i].z, wv[m][rr][i].w, lo[2], hi[2], lo[3], hi[3]);
 #pragma unroll
         for (int j = 0; j < 4; j++) {
-          u32x4 lo, hi;
-          unpack16_nat(wq[j], lo, hi);
 #pragma unroll
           for (int p = 0; p < XPL; p++) {
-            acc[m][rr] = mfma16(lo, xb[p][2 * j], acc[m][rr]);
-            acc[m][rr] = mfma16(hi, xb[p][2 * j + 1], acc[m][rr]);
+            acc[m][rr] = mfma16(lo[j], xb[p][2 * j], acc[m][rr]);
+            acc[m][rr] = mfma16(hi[j], xb[p][2 * j + 1], acc[m][rr]);
           }
         }
       }
@@ -926,22 +947,7 @@ __global__ __launch_bounds__(512) void gemv_bal_kernel(const uint32_t *__restric
   for (int rr = 0; rr < RMAX; rr++) sc[rr] = scale[min(row0 + rr, N - 1)];
   const float bv = bias ? bias[min(row0 + lane, N - 1)] : 0.f;  // lane's output row
   // 3. stage: piece j -> chunk j/8, slot j%8 (per plane), K-interleaved to
-  //    match the decode: the 16-column block b is pieces 2b (columns 0..7)
-  //    and 2b+1 (8..15), held by neighbouring lanes; after swapping pieces
-  //    with its neighbour the even lane writes block dwords 0..3 and the odd
-  //    lane dwords 4..7, dword i = x[16b + i] | x[16b + i + 8] << 16. All
-  //    lanes take part in the swap (pieces past the range are zeros).
-  auto kil = [&](const u32x4 &mine) -> u32x4 {
-    u32x4 other;
-#pragma unroll
-    for (int d = 0; d < 4; d++)
-      other[d] = (uint32_t)__builtin_amdgcn_mov_dpp((int)mine[d], 0xB1, 0xF, 0xF, false);  // quad_perm [1,0,3,2]
-    const bool odd = tid & 1;
-    const u32x4 A = odd ? other : mine, B = odd ? mine : other;
-    const uint32_t a0 = odd ? A.z : A.x, a1 = odd ? A.w : A.y, c0 = odd ? B.z : B.x, c1 = odd ? B.w : B.y;
-    return (u32x4){__builtin_amdgcn_perm(c0, a0, 0x05040100u), __builtin_amdgcn_perm(c0, a0, 0x07060302u),
-                   __builtin_amdgcn_perm(c1, a1, 0x05040100u), __builtin_amdgcn_perm(c1, a1, 0x07060302u)};
-  };
+  //    match the decode (stage_kil: all lanes take part)
 #pragma unroll
   for (int r = 0; r < XR; r++) {
     const int j = tid + r * NT;
@@ -953,13 +959,14 @@ __global__ __launch_bounds__(512) void gemv_bal_kernel(const uint32_t *__restric
       uint32_t hi[4], lo[4];
 #pragma unroll
       for (int e = 0; e < 4; e++) split2_bf16(f[2 * e], f[2 * e + 1], hi[e], lo[e]);
-      const u32x4 h = kil((u32x4){hi[0], hi[1], hi[2], hi[3]}), l = kil((u32x4){lo[0], lo[1], lo[2], lo[3]});
+      const u32x4 h = stage_kil((u32x4){hi[0], hi[1], hi[2], hi[3]}, tid),
+                  l = stage_kil((u32x4){lo[0], lo[1], lo[2], lo[3]}, tid);
       if (j < PP) {
         *reinterpret_cast<u32x4 *>(dst) = h;
         *reinterpret_cast<u32x4 *>(dst + PD) = l;
       }
     } else {
-      const u32x4 v = kil(xs[r][0]);
+      const u32x4 v = stage_kil(xs[r][0], tid);
       if (j < PP) *reinterpret_cast<u32x4 *>(dst) = v;
     }
   }
