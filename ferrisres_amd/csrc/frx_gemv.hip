@@ -899,16 +899,25 @@ static hipError_t launch_gemv_rows_w(const uint32_t *w, const float *scale, cons
 // and lo planes (split2_bf16: hi = bf16(x), lo = bf16(x - hi), |x - hi - lo|
 // <= 2^-17 |x|, lo = 0 where hi is not finite); each word then runs four
 // MFMAs.
-template <typename YT, int NI, int RMAX, bool XF32>
+// XPLN: the activations arrive as two bf16 planes, hi at Xv and lo K values
+// further (h of the decode FFN, |h - hi - lo| <= 2^-17 |h|): both are staged
+// and each word runs four MFMAs. NW = 2 (EPI = GEMV_SWIGLU / GEMV_GEGLU):
+// the same rows of the gate (W) and up (W2) matrices against the same x;
+// h = act(g) * u is written as bf16 hi and lo planes (Y = [2][N]).
+template <typename YT, int NI, int RMAX, bool XF32, bool XPLN = false, int NW = 1, int EPI = GEMV_LINEAR>
 __global__ __launch_bounds__(512) void gemv_bal_kernel(const uint32_t *__restrict__ W, const float *__restrict__ scale,
+                                                       const uint32_t *__restrict__ W2,
+                                                       const float *__restrict__ scale2,
                                                        const void *__restrict__ Xv, YT *__restrict__ Y, int K, int N,
                                                        const float *__restrict__ bias, int nq, int nr) {
+  static_assert((NW == 2) == (EPI != GEMV_LINEAR), "two matrices exactly for the GLU epilogues");
+  static_assert(!(XF32 && XPLN), "one activation source");
   constexpr int WAVES = 8, NT = 512;
-  constexpr int XPL = XF32 ? 2 : 1;
+  constexpr int XPL = (XF32 || XPLN) ? 2 : 1;
   constexpr int PP = NI * 512;                   // 8-value pieces of x staged (NI * 4096 values)
   constexpr int PD = NI * 64 * ROWS_XCH;         // LDS dwords per plane
   constexpr int XR = (PP + NT - 1) / NT;         // pieces per thread
-  constexpr int XL = XF32 ? 2 : 1;               // 16-byte loads per piece
+  constexpr int XL = (XF32 || XPLN) ? 2 : 1;     // 16-byte loads per piece
   extern __shared__ __align__(16) uint32_t lds[];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -919,8 +928,15 @@ __global__ __launch_bounds__(512) void gemv_bal_kernel(const uint32_t *__restric
   const int row0 = b0 + wave * cb / WAVES, cnt = b0 + (wave + 1) * cb / WAVES - row0;
   const int kw = K >> 4;
   constexpr uint32_t OOB = 0x80000000u;  // a buffer offset past any range this path takes
+  // x range: K values (f32 or bf16); planes: one descriptor per plane, each
+  // K bf16 long, so that pieces past K read zeros in both (the weight words
+  // past K decode to -1 and must meet zeros)
   const __amdgpu_buffer_rsrc_t xr = buffer_rsrc(Xv, (uint32_t)K * (XF32 ? 4u : 2u));
-  const __amdgpu_buffer_rsrc_t wr = buffer_rsrc(W, (uint32_t)N * (uint32_t)kw * 4u);
+  const __amdgpu_buffer_rsrc_t xr2 =
+      buffer_rsrc(XPLN ? reinterpret_cast<const char *>(Xv) + (size_t)K * 2 : Xv, (uint32_t)K * 2u);
+  __amdgpu_buffer_rsrc_t wr[NW];
+#pragma unroll
+  for (int m = 0; m < NW; m++) wr[m] = buffer_rsrc(m ? W2 : W, (uint32_t)N * (uint32_t)kw * 4u);
   // 1. x pieces (zero past K), then a barrier: all of the CU's x loads are
   //    ahead of its weight loads
   u32x4 xs[XR][XL];
@@ -928,23 +944,31 @@ __global__ __launch_bounds__(512) void gemv_bal_kernel(const uint32_t *__restric
   for (int r = 0; r < XR; r++) {
     const int j = tid + r * NT;
     const uint32_t off = j < PP ? (uint32_t)j * (XF32 ? 32u : 16u) : OOB;
+    // f32: the piece's two 16-byte halves; planes: the piece in each plane
 #pragma unroll
-    for (int l = 0; l < XL; l++) xs[r][l] = __builtin_amdgcn_raw_buffer_load_b128(xr, off + 16u * l, 0, 0);
+    for (int l = 0; l < XL; l++)
+      xs[r][l] = XPLN ? __builtin_amdgcn_raw_buffer_load_b128(l ? xr2 : xr, off, 0, 0)
+                      : __builtin_amdgcn_raw_buffer_load_b128(xr, off + 16u * l, 0, 0);
   }
   __syncthreads();
   // 2. the wave's rows (rows past cnt read zeros without touching memory)
-  u32x4 wv[RMAX][NI];
+  u32x4 wv[RMAX][NW][NI];
 #pragma unroll
   for (int rr = 0; rr < RMAX; rr++)
 #pragma unroll
-    for (int i = 0; i < NI; i++) {
-      const int wi = i * 256 + 4 * lane;
-      const uint32_t off = (rr < cnt && wi < kw) ? ((uint32_t)(row0 + rr) * (uint32_t)kw + (uint32_t)wi) * 4u : OOB;
-      wv[rr][i] = __builtin_amdgcn_raw_buffer_load_b128(wr, off, 0, 0);
-    }
-  float sc[RMAX];
+    for (int m = 0; m < NW; m++)
 #pragma unroll
-  for (int rr = 0; rr < RMAX; rr++) sc[rr] = scale[min(row0 + rr, N - 1)];
+      for (int i = 0; i < NI; i++) {
+        const int wi = i * 256 + 4 * lane;
+        const uint32_t off =
+            (rr < cnt && wi < kw) ? ((uint32_t)(row0 + rr) * (uint32_t)kw + (uint32_t)wi) * 4u : OOB;
+        wv[rr][m][i] = __builtin_amdgcn_raw_buffer_load_b128(wr[m], off, 0, 0);
+      }
+  float sc[RMAX][NW];
+#pragma unroll
+  for (int rr = 0; rr < RMAX; rr++)
+#pragma unroll
+    for (int m = 0; m < NW; m++) sc[rr][m] = (m ? scale2 : scale)[min(row0 + rr, N - 1)];
   const float bv = bias ? bias[min(row0 + lane, N - 1)] : 0.f;  // lane's output row
   // 3. stage: piece j -> chunk j/8, slot j%8 (per plane), K-interleaved to
   //    match the decode (stage_kil: all lanes take part)
@@ -952,7 +976,13 @@ __global__ __launch_bounds__(512) void gemv_bal_kernel(const uint32_t *__restric
   for (int r = 0; r < XR; r++) {
     const int j = tid + r * NT;
     uint32_t *dst = lds + (j >> 3) * ROWS_XCH + (j & 7) * 4;
-    if constexpr (XF32) {
+    if constexpr (XPLN) {
+      const u32x4 h = stage_kil(xs[r][0], tid), l = stage_kil(xs[r][1], tid);
+      if (j < PP) {
+        *reinterpret_cast<u32x4 *>(dst) = h;
+        *reinterpret_cast<u32x4 *>(dst + PD) = l;
+      }
+    } else if constexpr (XF32) {
       const float f[8] = {__uint_as_float(xs[r][0].x), __uint_as_float(xs[r][0].y), __uint_as_float(xs[r][0].z),
                           __uint_as_float(xs[r][0].w), __uint_as_float(xs[r][1].x), __uint_as_float(xs[r][1].y),
                           __uint_as_float(xs[r][1].z), __uint_as_float(xs[r][1].w)};
@@ -988,49 +1018,64 @@ __global__ __launch_bounds__(512) void gemv_bal_kernel(const uint32_t *__restric
 #pragma unroll
     for (int i = 0; i < NI; i++) xread(i, xb[i]);
   }
-  float res = 0.f;
+  float res[NW];
+#pragma unroll
+  for (int m = 0; m < NW; m++) res[m] = 0.f;
   const int c = lane & 15, rg = lane >> 4, e = c & 3;
 #pragma unroll
   for (int rr = 0; rr < RMAX; rr++) {
     if (rr < cnt) {  // wave-uniform
-      // two accumulation chains (even and odd words) halve the dependent
-      // MFMA latency of a row
-      f32x4 acc2[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
 #pragma unroll
-      for (int i = 0; i < NI; i++) {
-        u32x4 xw[XPL][8];
-        if constexpr (!XREG) xread(i, xw);
-        const u32x4(&xv)[XPL][8] = XREG ? xb[XREG ? i : 0] : xw;
-        u32x4 lo[4], hi[4];
-        unpack32_kil(wv[rr][i].x, wv[rr][i].y, lo[0], hi[0], lo[1], hi[1]);
-        unpack32_kil(wv[rr][i].z, wv[rr][i].w, lo[2], hi[2], lo[3], hi[3]);
+      for (int m = 0; m < NW; m++) {
+        // two accumulation chains (even and odd words) halve the dependent
+        // MFMA latency of a row
+        f32x4 acc2[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
 #pragma unroll
-        for (int j = 0; j < 4; j++) {
+        for (int i = 0; i < NI; i++) {
+          u32x4 xw[XPL][8];
+          if constexpr (!XREG) xread(i, xw);
+          const u32x4(&xv)[XPL][8] = XREG ? xb[XREG ? i : 0] : xw;
+          u32x4 lo[4], hi[4];
+          unpack32_kil(wv[rr][m][i].x, wv[rr][m][i].y, lo[0], hi[0], lo[1], hi[1]);
+          unpack32_kil(wv[rr][m][i].z, wv[rr][m][i].w, lo[2], hi[2], lo[3], hi[3]);
 #pragma unroll
-          for (int p = 0; p < XPL; p++) {
-            acc2[j & 1] = mfma16(lo[j], xv[p][2 * j], acc2[j & 1]);
-            acc2[j & 1] = mfma16(hi[j], xv[p][2 * j + 1], acc2[j & 1]);
+          for (int j = 0; j < 4; j++) {
+#pragma unroll
+            for (int p = 0; p < XPL; p++) {
+              acc2[j & 1] = mfma16(lo[j], xv[p][2 * j], acc2[j & 1]);
+              acc2[j & 1] = mfma16(hi[j], xv[p][2 * j + 1], acc2[j & 1]);
+            }
           }
         }
+        const f32x4 acc = acc2[0] + acc2[1];
+        // diagonal: lane (c = l%16, rg = l/16) holds C[4rg + e][c]
+        float v = e == 0 ? acc[0] : e == 1 ? acc[1] : e == 2 ? acc[2] : acc[3];
+        v = (c >> 2) == rg ? v : 0.f;
+        v += dpp_f32<0xB1>(v);  // quad_perm [1,0,3,2]
+        v += dpp_f32<0x4E>(v);  // quad_perm [2,3,0,1]
+        const float a = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+        const float b = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 20));
+        const float d = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 40));
+        const float f = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 60));
+        const float tot = ((a + b) + (d + f)) * sc[rr][m] * 0.5f;  // 0.5 undoes the 2*dec(c) encoding
+        if (lane == rr) res[m] = tot;
       }
-      const f32x4 acc = acc2[0] + acc2[1];
-      // diagonal: lane (c = l%16, rg = l/16) holds C[4rg + e][c]
-      float v = e == 0 ? acc[0] : e == 1 ? acc[1] : e == 2 ? acc[2] : acc[3];
-      v = (c >> 2) == rg ? v : 0.f;
-      v += dpp_f32<0xB1>(v);  // quad_perm [1,0,3,2]
-      v += dpp_f32<0x4E>(v);  // quad_perm [2,3,0,1]
-      const float a = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
-      const float b = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 20));
-      const float d = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 40));
-      const float f = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 60));
-      const float tot = ((a + b) + (d + f)) * sc[rr] * 0.5f;  // 0.5 undoes the 2*dec(c) encoding
-      if (lane == rr) res = tot;
     }
   }
   if (lane < cnt) {
-    if (bias) res = add_bias(res, bv);
-    if constexpr (sizeof(YT) == 2) Y[row0 + lane] = (uint16_t)bf16_rne(res);
-    else Y[row0 + lane] = res;
+    const int row = row0 + lane;
+    if constexpr (EPI != GEMV_LINEAR) {
+      const float h = (EPI == GEMV_GEGLU ? act_gelu_tanh(res[0]) : act_silu(res[0])) * res[NW - 1];
+      uint32_t hh, hl;
+      split_bf16(h, hh, hl);
+      Y[row] = (uint16_t)hh;
+      Y[N + row] = (uint16_t)hl;
+    } else {
+      float o = res[0];
+      if (bias) o = add_bias(o, bv);
+      if constexpr (sizeof(YT) == 2) Y[row] = (uint16_t)bf16_rne(o);
+      else Y[row] = o;
+    }
   }
 }
 
@@ -1039,18 +1084,19 @@ __global__ __launch_bounds__(512) void gemv_bal_kernel(const uint32_t *__restric
 // four slots for two rows measured 6.30 against 5.31 us).
 constexpr int GEMV_BAL_RMAX = 4;
 
-template <typename YT, int NI, int RMAX, bool XF32>
+template <typename YT, int NI, int RMAX, bool XF32, bool XPLN = false, int NW = 1, int EPI = GEMV_LINEAR>
 static hipError_t launch_gemv_bal_w(const uint32_t *w, const float *scale, const void *x, void *y, int K, int N,
-                                    int G, hipStream_t stream, const float *bias) {
-  const size_t lds = (size_t)(XF32 ? 2 : 1) * NI * 64 * ROWS_XCH * 4;
+                                    int G, hipStream_t stream, const float *bias, const uint32_t *w2 = nullptr,
+                                    const float *scale2 = nullptr) {
+  const size_t lds = (size_t)((XF32 || XPLN) ? 2 : 1) * NI * 64 * ROWS_XCH * 4;
   if (lds > 64 * 1024) {
     static std::atomic<uint64_t> done;
-    const hipError_t e =
-        opt_in_lds(reinterpret_cast<const void *>(&gemv_bal_kernel<YT, NI, RMAX, XF32>), (int)lds, done);
+    const hipError_t e = opt_in_lds(
+        reinterpret_cast<const void *>(&gemv_bal_kernel<YT, NI, RMAX, XF32, XPLN, NW, EPI>), (int)lds, done);
     if (e != hipSuccess) return e;
   }
-  hipLaunchKernelGGL((gemv_bal_kernel<YT, NI, RMAX, XF32>), dim3(G), dim3(512), lds, stream, w, scale, x,
-                     reinterpret_cast<YT *>(y), K, N, bias, N / G, N % G);
+  hipLaunchKernelGGL((gemv_bal_kernel<YT, NI, RMAX, XF32, XPLN, NW, EPI>), dim3(G), dim3(512), lds, stream, w, scale,
+                     w2 ? w2 : w, scale2 ? scale2 : scale, x, reinterpret_cast<YT *>(y), K, N, bias, N / G, N % G);
   return hipGetLastError();
 }
 
@@ -1815,9 +1861,45 @@ bool gemv_rows_ffn_ok(int M, int H, int I) {
   return M == 1 && H % 64 == 0 && I % 64 == 0 && H <= 4 * 4096 && I <= 4 * 4096;
 }
 
+// The two FFN launches on the balanced one-token kernel (rows split evenly
+// over one or two workgroups per CU): GLU into h planes, down over them.
+template <typename YT, int NI, bool XPLN, int NW, int EPI>
+static hipError_t launch_gemv_bal_ffn_r(const uint32_t *w, const float *scale, const uint32_t *w2,
+                                        const float *scale2, const void *x, void *y, int K, int N, int G,
+                                        hipStream_t stream) {
+  const int rmax = ((N + G - 1) / G + 7) / 8;
+#define FRX_BAL_FFN(R) \
+  return launch_gemv_bal_w<YT, NI, R, false, XPLN, NW, EPI>(w, scale, x, y, K, N, G, stream, nullptr, w2, scale2)
+  if (rmax <= 1) FRX_BAL_FFN(1);
+  if (rmax <= 2) FRX_BAL_FFN(2);
+  if (rmax <= 3) FRX_BAL_FFN(3);
+  FRX_BAL_FFN(4);
+#undef FRX_BAL_FFN
+}
+
+template <typename YT, bool XPLN, int NW, int EPI>
+static hipError_t launch_gemv_bal_ffn(const uint32_t *w, const float *scale, const uint32_t *w2, const float *scale2,
+                                      const void *x, void *y, int K, int N, int G, hipStream_t stream) {
+  const int ni = (K + 4095) / 4096;
+  if (ni == 1) return launch_gemv_bal_ffn_r<YT, 1, XPLN, NW, EPI>(w, scale, w2, scale2, x, y, K, N, G, stream);
+  if (ni == 2) return launch_gemv_bal_ffn_r<YT, 2, XPLN, NW, EPI>(w, scale, w2, scale2, x, y, K, N, G, stream);
+  if (ni == 3) return launch_gemv_bal_ffn_r<YT, 3, XPLN, NW, EPI>(w, scale, w2, scale2, x, y, K, N, G, stream);
+  // two matrices of four windows per row would spill (callers stop at three)
+  if constexpr (NW == 2) return hipErrorInvalidValue;
+  else return launch_gemv_bal_ffn_r<YT, 4, XPLN, NW, EPI>(w, scale, w2, scale2, x, y, K, N, G, stream);
+}
+
 hipError_t launch_gemv_rows_glu_planes(const uint32_t *w_gate, const float *s_gate, const uint32_t *w_up,
                                        const float *s_up, const void *x, uint16_t *h_planes, int K, int N,
                                        int gelu, hipStream_t stream) {
+  int G = 0;
+  if (K <= 3 * 4096 && gemv_bal_grid(w_gate, x, 1, K, N, &G) && (reinterpret_cast<uintptr_t>(w_up) & 15) == 0) {
+    if (gelu)
+      return launch_gemv_bal_ffn<uint16_t, false, 2, GEMV_GEGLU>(w_gate, s_gate, w_up, s_up, x, h_planes, K, N, G,
+                                                                 stream);
+    return launch_gemv_bal_ffn<uint16_t, false, 2, GEMV_SWIGLU>(w_gate, s_gate, w_up, s_up, x, h_planes, K, N, G,
+                                                                stream);
+  }
   const int ni = (K + 4095) / 4096;
 #define FRX_ROWS_GLU(NI)                                                                                        \
   return gelu ? launch_gemv_rows_w<uint16_t, 1, NI, 2, 1, GEMV_GEGLU>(w_gate, s_gate, w_up, s_up, x, x, h_planes, \
@@ -1833,6 +1915,13 @@ hipError_t launch_gemv_rows_glu_planes(const uint32_t *w_gate, const float *s_ga
 
 hipError_t launch_gemv_rows_planes(const uint32_t *w, const float *scale, const uint16_t *x_planes, void *y,
                                    int yt_bf16, int K, int N, hipStream_t stream) {
+  int G = 0;
+  if (gemv_bal_grid(w, x_planes, 1, K, N, &G) && (K * 2) % 16 == 0) {  // the lo plane 16-byte aligned too
+    if (yt_bf16)
+      return launch_gemv_bal_ffn<uint16_t, true, 1, GEMV_LINEAR>(w, scale, nullptr, nullptr, x_planes, y, K, N, G,
+                                                                 stream);
+    return launch_gemv_bal_ffn<float, true, 1, GEMV_LINEAR>(w, scale, nullptr, nullptr, x_planes, y, K, N, G, stream);
+  }
   const int ni = (K + 4095) / 4096;
   const uint16_t *lo = x_planes + K;
 #define FRX_ROWS_PL(RW, NI)                                                                                   \
