@@ -264,7 +264,7 @@ def main():
     ctx.set_ffn_mode(frx.FFN_AUTO)
     fused["default"]["launches_per_step"] = 1 if B == 3 else 2
     fused["default"]["kernels"] = (
-        "gemv_rows_kernel gate/up/SiLU -> h planes, gemv_rows_kernel down over both planes" if B == 1 else
+        "gemv_bal_kernel gate/up/SiLU -> h planes, gemv_bal_kernel down over both planes" if B == 1 else
         "gemv_rows4_kernel gate/up/SiLU -> h planes, gemv_rows4_kernel down over both planes" if B == 2 else
         "ffn1_kernel" if B == 3 else "GLU + down GEMV (planes at B >= 4)")
     fused["two_launch"]["launches_per_step"] = 2
