@@ -39,6 +39,14 @@ class FrxError(RuntimeError):
 
 _lib = None
 
+
+class MoeLora(ctypes.Structure):
+    """frx_moe_lora (include/frx_ternary.h)."""
+    _fields_ = [("rank", ctypes.c_uint32), ("scaling", ctypes.c_float),
+                ("a_gate", ctypes.c_void_p), ("b_gate", ctypes.c_void_p),
+                ("a_up", ctypes.c_void_p), ("b_up", ctypes.c_void_p),
+                ("a_down", ctypes.c_void_p), ("b_down", ctypes.c_void_p)]
+
 _u32p = ctypes.POINTER(ctypes.c_uint32)
 _f32p = ctypes.POINTER(ctypes.c_float)
 _vp = ctypes.c_void_p
@@ -72,6 +80,7 @@ _SIGS = {
                                        _int, _vp, _int]),
     "frx_set_ffn_mode": (_int, [_vp, _int]),
     "frx_set_moe_routing": (_int, [_vp, _int]),
+    "frx_set_moe_lora": (_int, [_vp, _vp, _u32]),
     "frx_force_status": (_int, [_vp, _int]),
     "frx_upload_ternary": (_int, [_vp, _vp, _u32, _u32, _vp, ctypes.c_float, ctypes.POINTER(_vp),
                                   ctypes.POINTER(_vp)]),
@@ -441,6 +450,33 @@ class Context:
         """frx_set_moe_routing: MOE_TERNARY_MOE_LAYER (router [E,H], default)
         or MOE_CPU_MOE_LAYER (CpuMoELayer: router [H,E], top-k by logit)."""
         _check(lib().frx_set_moe_routing(self._h, routing), self._h)
+
+    def set_moe_lora(self, rank=None, scaling=0.0, experts=0, a_gate=None, b_gate=None, a_up=None, b_up=None,
+                     a_down=None, b_down=None):
+        """frx_set_moe_lora: per-expert LoRA adapters of the MoE experts
+        (lists of ``experts`` f32 device tensors or None; a list may be None).
+        rank=None removes the adapters."""
+        if rank is None:
+            _check(lib().frx_set_moe_lora(self._h, None, 0), self._h)
+            return
+        for name, lst in (("a_gate", a_gate), ("b_gate", b_gate), ("a_up", a_up), ("b_up", b_up),
+                          ("a_down", a_down), ("b_down", b_down)):
+            for t in (lst or []):
+                if t is not None and (t.dtype.__str__() != "torch.float32" or not t.is_contiguous()):
+                    raise ValueError(f"{name}: LoRA matrices are contiguous float32 device tensors")
+        keep = []
+
+        def arr(lst):
+            if lst is None:
+                return None
+            if len(lst) != experts:
+                raise ValueError("one LoRA matrix (or None) per expert")
+            a = (_vp * experts)(*[None if t is None else t.data_ptr() for t in lst])
+            keep.append(a)
+            return ctypes.cast(a, _vp)
+        cfg = MoeLora(int(rank), float(scaling), arr(a_gate), arr(b_gate), arr(a_up), arr(b_up), arr(a_down),
+                      arr(b_down))
+        _check(lib().frx_set_moe_lora(self._h, ctypes.byref(cfg), int(experts)), self._h)
 
     def force_status(self, status: int):
         """frx_force_status: every compute / upload call on this context

@@ -84,6 +84,11 @@ struct frx_ctx {
   unsigned *ffn_bar = nullptr;  // grid-barrier words of the one-launch FFN
   int ffn_mode = FRX_FFN_AUTO;
   int moe_routing = FRX_MOE_TERNARY_MOE_LAYER;
+  // MoE LoRA adapters: device table of 6 x 64 pointers (frx_set_moe_lora)
+  const float **lora_tbl = nullptr;
+  uint32_t lora_rank = 0, lora_experts = 0;
+  float lora_scaling = 0.f;
+  bool lora_on = false;
   void *router_ws = nullptr;  // [E][H] copy of a [H][E] router (CpuMoELayer routing)
   size_t router_ws_bytes = 0;
   int cus = 0;  // compute units of the device
@@ -162,6 +167,7 @@ void frx_destroy(frx_ctx *ctx) {
   (void)hipSetDevice(ctx->device);
   if (ctx->scratch) (void)hipFree(ctx->scratch);
   if (ctx->moe_ws) (void)hipFree(ctx->moe_ws);
+  if (ctx->lora_tbl) (void)hipFree(ctx->lora_tbl);
   if (ctx->ffn_ws) (void)hipFree(ctx->ffn_ws);
   if (ctx->glu_ws) (void)hipFree(ctx->glu_ws);
   if (ctx->blk_ws) (void)hipFree(ctx->blk_ws);
@@ -219,6 +225,37 @@ frx_status frx_set_moe_routing(frx_ctx *ctx, frx_moe_routing routing) {
   if (routing != FRX_MOE_TERNARY_MOE_LAYER && routing != FRX_MOE_CPU_MOE_LAYER)
     return fail(ctx, FRX_ERR_UNSUPPORTED, "unknown MoE routing %d", (int)routing);
   ctx->moe_routing = routing;
+  return FRX_OK;
+}
+
+frx_status frx_set_moe_lora(frx_ctx *ctx, const frx_moe_lora *lora, uint32_t experts) {
+  if (!ctx) return FRX_ERR_DEVICE;
+  ctx->err[0] = 0;
+  if (!lora) {
+    ctx->lora_on = false;
+    return FRX_OK;
+  }
+  if (lora->rank == 0 || lora->rank > (uint32_t)frx::MOE_LORA_MAXR)
+    return fail(ctx, FRX_ERR_SHAPE, "LoRA rank=%u must be in [1, %d]", lora->rank, frx::MOE_LORA_MAXR);
+  if (experts == 0 || experts > 64) return fail(ctx, FRX_ERR_SHAPE, "LoRA experts=%u must be in [1, 64]", experts);
+  const float *host[6 * 64] = {nullptr};
+  const float *const *src[6] = {lora->a_gate, lora->b_gate, lora->a_up, lora->b_up, lora->a_down, lora->b_down};
+  for (int k = 0; k < 6; k++)
+    for (uint32_t e = 0; e < experts && src[k]; e++) host[k * 64 + e] = src[k][e];
+  hipError_t e = hipSetDevice(ctx->device);
+  if (e != hipSuccess) return hip_fail(ctx, e, "LoRA setup");
+  if (!ctx->lora_tbl) {
+    e = hipMalloc(reinterpret_cast<void **>(&ctx->lora_tbl), sizeof(host));
+    if (e != hipSuccess) return hip_fail(ctx, e, "LoRA table allocation");
+  }
+  // earlier MoE launches on the context stream may still read the table
+  if ((e = hipStreamSynchronize(ctx->stream)) != hipSuccess) return hip_fail(ctx, e, "LoRA setup wait");
+  if ((e = hipMemcpy(ctx->lora_tbl, host, sizeof(host), hipMemcpyHostToDevice)) != hipSuccess)
+    return hip_fail(ctx, e, "LoRA table copy");
+  ctx->lora_rank = lora->rank;
+  ctx->lora_scaling = lora->scaling;
+  ctx->lora_experts = experts;
+  ctx->lora_on = true;
   return FRX_OK;
 }
 
@@ -331,6 +368,8 @@ frx_status frx_moe_ternary_ffn(
     if (!w_gate[e] || !s_gate[e] || !w_up[e] || !s_up[e] || !w_down[e] || !s_down[e])
       return fail(ctx, FRX_ERR_SHAPE, "null weight pointer for expert %u", e);
   if ((size_t)T * top_k * I > (size_t)0x7FFFFFFF) return fail(ctx, FRX_ERR_SHAPE, "T*top_k*I too large");
+  if (ctx->lora_on && ctx->lora_experts != E)
+    return fail(ctx, FRX_ERR_SHAPE, "LoRA adapters were set for %u experts, the call has %u", ctx->lora_experts, E);
   const size_t need = frx::moe_workspace_bytes((int)T, (int)H, (int)I, (int)E, (int)top_k);
   if ((st = ensure_buffer(ctx, &ctx->moe_ws, &ctx->moe_ws_bytes, need, "MoE workspace allocation")) != FRX_OK)
     return st;
@@ -347,9 +386,15 @@ frx_status frx_moe_ternary_ffn(
     if (e != hipSuccess) return hip_fail(ctx, e, "router transpose launch");
     router_eh = ctx->router_ws;
   }
+  frx::MoeLora lora;
+  if (ctx->lora_on) {
+    lora.tbl = ctx->lora_tbl;
+    lora.rank = (int)ctx->lora_rank;
+    lora.scaling = ctx->lora_scaling;
+  }
   hipError_t e = frx::launch_moe(x, xt == FRX_BF16, router_eh, rt == FRX_BF16, w_gate, s_gate, w_up, s_up, w_down,
                                  s_down, (int)T, (int)H, (int)I, (int)E, (int)top_k, act == FRX_ACT_GELU_TANH, y,
-                                 yt == FRX_BF16, topk_idx, topk_w, ws, ctx->moe_routing, ctx->stream);
+                                 yt == FRX_BF16, topk_idx, topk_w, ws, ctx->moe_routing, lora, ctx->stream);
   if (e != hipSuccess) return hip_fail(ctx, e, "moe launch");
   return FRX_OK;
 }

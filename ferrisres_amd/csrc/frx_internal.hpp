@@ -137,6 +137,9 @@ struct MoeWorkspace {
   int *counts;         // [E] tokens per expert
   int *offsets;        // [E+1] exclusive scan of counts
   int *perm_token;     // [T*k] token of each expert-sorted row
+  int *row_expert;     // [T*k] expert of each expert-sorted row
+  float *lora_ax;      // [T*k][2 * MOE_LORA_MAXR] LoRA A x of the gate and up adapters
+  float *lora_ah;      // [T*k][MOE_LORA_MAXR] LoRA A h of the down adapter
   int *inv;            // [T*k] expert-sorted row of assignment t*k+j
   int *tiles;          // [4*max_tiles] (expert, first row, rows, token blocks)
                        // per M tile
@@ -149,6 +152,16 @@ struct MoeWorkspace {
   float *dout_lo;      // [T*k][H] second partial (engine-2 path: the second
                        // K part)
 };
+// Largest LoRA rank of the MoE adapters.
+constexpr int MOE_LORA_MAXR = 64;
+// LoRA adapters of the MoE experts: tbl is a device array of 6 x 64
+// pointers, [2 k] = A and [2 k + 1] = B of kind k (0 gate, 1 up, 2 down) at
+// index 64 * slot + expert; nullptr tbl: no adapters.
+struct MoeLora {
+  const float *const *tbl = nullptr;
+  int rank = 0;
+  float scaling = 0.f;
+};
 size_t moe_workspace_bytes(int T, int H, int I, int E, int top_k);
 void moe_workspace_carve(void *base, int T, int H, int I, int E, int top_k,
                          MoeWorkspace *ws);
@@ -159,6 +172,6 @@ hipError_t launch_moe(const void *x, int xt_bf16, const void *router,
                       const float *const *s_down, int T, int H, int I, int E,
                       int top_k, int gelu, void *y, int yt_bf16,
                       uint32_t *topk_idx, float *topk_w, const MoeWorkspace &ws,
-                      int routing, hipStream_t stream);
+                      int routing, const MoeLora &lora, hipStream_t stream);
 
 }  // namespace frx

@@ -39,7 +39,8 @@ size_t moe_workspace_bytes(int T, int H, int I, int E, int top_k) {
   b += align256(A * 4) * 2;             // idx, wts
   b += align256((size_t)E * 4);         // counts
   b += align256((size_t)(E + 1) * 4);   // offsets
-  b += align256(A * 4) * 2;             // perm_token, inv
+  b += align256(A * 4) * 3;             // perm_token, inv, row_expert
+  b += align256(A * 4 * 3 * MOE_LORA_MAXR);  // LoRA A x (gate, up) and A h (down)
   b += align256(max_tiles * 16);        // tiles
   b += align256(4);                     // ntiles
   b += align256(A * I * 2) * 2;         // h planes
@@ -59,6 +60,9 @@ void moe_workspace_carve(void *base, int T, int H, int I, int E, int top_k,
   ws->offsets = reinterpret_cast<int *>(take((size_t)(E + 1) * 4));
   ws->perm_token = reinterpret_cast<int *>(take(A * 4));
   ws->inv = reinterpret_cast<int *>(take(A * 4));
+  ws->row_expert = reinterpret_cast<int *>(take(A * 4));
+  ws->lora_ax = reinterpret_cast<float *>(take(A * 4 * 3 * MOE_LORA_MAXR));
+  ws->lora_ah = ws->lora_ax + A * 2 * MOE_LORA_MAXR;
   ws->tiles = reinterpret_cast<int *>(take(max_tiles * 16));
   ws->ntiles = reinterpret_cast<int *>(take(4));
   ws->h_hi = reinterpret_cast<uint16_t *>(take(A * I * 2));
@@ -566,7 +570,7 @@ __global__ __launch_bounds__(1024) void moe_group_kernel(
     const uint32_t *__restrict__ idx, int A, int top_k, int E, int bm_max, int fm_min,
     int *__restrict__ counts, int *__restrict__ offsets,
     int *__restrict__ perm_token, int *__restrict__ inv,
-    int *__restrict__ tiles, int *__restrict__ ntiles) {
+    int *__restrict__ tiles, int *__restrict__ ntiles, int *__restrict__ row_expert) {
   __shared__ int wave_cnt[16][MOE_MAXE];
   __shared__ int base[MOE_MAXE];
   __shared__ int offs[MOE_MAXE + 1];
@@ -640,7 +644,55 @@ __global__ __launch_bounds__(1024) void moe_group_kernel(
     const int pos = offs[e] + inv[a];
     inv[a] = pos;
     perm_token[pos] = a / top_k;
+    row_expert[pos] = e;
   }
+}
+
+// ---- LoRA adapters of the experts --------------------------------------------
+// CpuMoELayer::expert_forward_*_with_lora (src/model/cpu_moe.rs:281-363) with
+// LoraLayer::forward (src/training/lora.rs:138-167): lora(v) = scaling *
+// B (A v). Per expert-sorted row a, this kernel writes A v for the adapter
+// kinds [kind0, kind0 + nk) (0 gate, 1 up: v = x of the row's token; 2 down:
+// v = h = hi + lo of the row) to out[a][(k - kind0) * rank + r], zeros where
+// the row's expert has no adapter of that kind. One workgroup per row, one
+// wave per rank index at a time, lane-strided dot products reduced across
+// the wave. The epilogues of the grouped GEMMs add scaling * B (A v).
+template <typename XT>
+__global__ __launch_bounds__(256) void moe_lora_a_kernel(
+    const float *const *__restrict__ tbl, int rank, const XT *__restrict__ x, const int *__restrict__ perm_token,
+    const int *__restrict__ row_expert, const uint16_t *__restrict__ hh, const uint16_t *__restrict__ hl,
+    long hstride, int D, int kind0, int nk, float *__restrict__ out, int out_stride) {
+  const int a = blockIdx.x, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int e = row_expert[a];
+  for (int k = kind0; k < kind0 + nk; k++) {
+    const float *Am = tbl[(2 * k) * MOE_MAXE + e], *Bm = tbl[(2 * k + 1) * MOE_MAXE + e];
+    for (int r = wave; r < rank; r += 4) {
+      float sum = 0.f;
+      if (Am && Bm) {
+        if (k < 2) {
+          const long t = perm_token[a];
+          for (int d = lane; d < D; d += 64) sum += Am[(long)r * D + d] * ld_f32(x, t * D + d);
+        } else {
+          for (int d = lane; d < D; d += 64) {
+            const float h = __uint_as_float((uint32_t)hh[a * hstride + d] << 16) +
+                            __uint_as_float((uint32_t)hl[a * hstride + d] << 16);
+            sum += Am[(long)r * D + d] * h;
+          }
+        }
+#pragma unroll
+        for (int o = 32; o >= 1; o >>= 1) sum += __shfl_xor(sum, o);
+      }
+      if (lane == 0) out[(long)a * out_stride + (k - kind0) * rank + r] = sum;
+    }
+  }
+}
+
+// scaling * sum_r B[n][r] * av[r] (0 without the adapter's B matrix).
+__device__ __forceinline__ float lora_b(const float *Bm, int n, int rank, const float *av, float scaling) {
+  if (!Bm) return 0.f;
+  float s = 0.f;
+  for (int r = 0; r < rank; r++) s += Bm[(long)n * rank + r] * av[r];
+  return s * scaling;
 }
 
 // ---- 3. grouped gate/up GEMM + activation -----------------------------------
@@ -658,7 +710,8 @@ __global__ __launch_bounds__(256) void moe_gateup_kernel(
     const int *__restrict__ tiles, const int *__restrict__ ntiles,
     const int *__restrict__ counts, const int *__restrict__ offsets,
     const int *__restrict__ perm_token, uint16_t *__restrict__ h_hi,
-    uint16_t *__restrict__ h_lo, int gelu) {
+    uint16_t *__restrict__ h_lo, int gelu, const float *const *__restrict__ ltbl, int lrank, float lscale,
+    const float *__restrict__ lax) {
   using Core = GemmCore<MOE_BM, MOE_BN, 1, 4, XS, 2>;
   __shared__ __align__(16) uint32_t lds[Core::LDS_DWORDS];
   const int tile = blockIdx.y;
@@ -683,7 +736,15 @@ __global__ __launch_bounds__(256) void moe_gateup_kernel(
     for (int fm = 0; fm < Core::FM; fm++) {
       const int m = Core::tok(fm);
       if (m >= mcount) continue;
-      const f32x4 g = acc[0][fn][fm] * sg, u = acc[1][fn][fm] * su;
+      f32x4 g = acc[0][fn][fm] * sg, u = acc[1][fn][fm] * su;
+      if (ltbl) {  // LoRA: gated += lora_gate(x), upped += lora_up(x)
+        const float *av = lax + (long)(row0 + m) * (2 * MOE_LORA_MAXR);
+        const float *Bg = ltbl[1 * MOE_MAXE + e], *Bu = ltbl[3 * MOE_MAXE + e];
+        for (int j = 0; j < nok; j++) {
+          g[j] += lora_b(Bg, n + j, lrank, av, lscale);
+          u[j] += lora_b(Bu, n + j, lrank, av + lrank, lscale);
+        }
+      }
       float hv[4];
       for (int j = 0; j < 4; j++) {
         const float a = gelu ? act_gelu_tanh(g[j]) : act_silu(g[j]);
@@ -716,7 +777,8 @@ __global__ __launch_bounds__(256) void moe_down_kernel(
     const uint16_t *__restrict__ h_lo, int H, int I,
     const int *__restrict__ tiles, const int *__restrict__ ntiles,
     const int *__restrict__ counts, const int *__restrict__ offsets,
-    float *__restrict__ dout) {
+    float *__restrict__ dout, const float *const *__restrict__ ltbl, int lrank, float lscale,
+    const float *__restrict__ lah) {
   using Core = GemmCore<MOE_BM, MOE_BN, 1, 4, XS_BF16X2, 1>;
   __shared__ __align__(16) uint32_t lds[Core::LDS_DWORDS];
   const int tile = blockIdx.y;
@@ -739,8 +801,13 @@ __global__ __launch_bounds__(256) void moe_down_kernel(
 #pragma unroll
     for (int fm = 0; fm < Core::FM; fm++) {
       const int m = Core::tok(fm);
-      if (m < mcount)
-        YStore<float>::store4(dout + (long)(row0 + m) * H + n, acc[0][fn][fm] * sd, nok);
+      if (m >= mcount) continue;
+      f32x4 v = acc[0][fn][fm] * sd;
+      if (ltbl) {  // LoRA: down += lora_down(h)
+        const float *av = lah + (long)(row0 + m) * MOE_LORA_MAXR;
+        for (int j = 0; j < nok; j++) v[j] += lora_b(ltbl[5 * MOE_MAXE + e], n + j, lrank, av, lscale);
+      }
+      YStore<float>::store4(dout + (long)(row0 + m) * H + n, v, nok);
     }
   }
 }
@@ -773,7 +840,7 @@ static_assert(MoeGateUpCore::FM == 6 && MoeDownCore::FM == 6, "token blocks per 
 template <int F>
 __device__ __forceinline__ void gateup_tile(uint32_t *lds, const GateUpArgs &args, const uint16_t *x, int T, int H,
                                             int I, int e, int mcount, int row0, const int *perm_token,
-                                            uint16_t *h2, int gelu) {
+                                            uint16_t *h2, int gelu, const MoeLora &lora, const float *lax) {
   using Core = MoeGateUpCore;
   const int n0 = blockIdx.x * (MOE_GU_BN / 2), nc = min(MOE_GU_BN / 2, I - n0);
   f32x4 acc[Core::FN][F];
@@ -809,8 +876,16 @@ __device__ __forceinline__ void gateup_tile(uint32_t *lds, const GateUpArgs &arg
     for (int lr = rr; lr < rows; lr += RT) {
       const int m = f0 * 16 + lr;
       if (m >= mcount || 4 * c >= nc) continue;
-      const f32x4 gv = *reinterpret_cast<const f32x4 *>(st + lr * PF + 4 * c) * sgv;
-      const f32x4 uv = *reinterpret_cast<const f32x4 *>(st + lr * PF + MOE_GU_BN / 2 + 4 * c) * suv;
+      f32x4 gv = *reinterpret_cast<const f32x4 *>(st + lr * PF + 4 * c) * sgv;
+      f32x4 uv = *reinterpret_cast<const f32x4 *>(st + lr * PF + MOE_GU_BN / 2 + 4 * c) * suv;
+      if (lora.tbl) {  // LoRA: gated += lora_gate(x), upped += lora_up(x)
+        const float *av = lax + (long)(row0 + m) * (2 * MOE_LORA_MAXR);
+        const float *Bg = lora.tbl[1 * MOE_MAXE + e], *Bu = lora.tbl[3 * MOE_MAXE + e];
+        for (int j = 0; j < 4 && 4 * c + j < nc; j++) {
+          gv[j] += lora_b(Bg, n0 + 4 * c + j, lora.rank, av, lora.scaling);
+          uv[j] += lora_b(Bu, n0 + 4 * c + j, lora.rank, av + lora.rank, lora.scaling);
+        }
+      }
       uint32_t hh[4], hl[4];
 #pragma unroll
       for (int j = 0; j < 4; j++) {
@@ -837,20 +912,21 @@ __global__ __launch_bounds__(256) void moe_gateup3_kernel(
     const GateUpArgs args, const uint16_t *__restrict__ x, int T, int H, int I,
     const int *__restrict__ tiles, const int *__restrict__ ntiles,
     const int *__restrict__ offsets, const int *__restrict__ perm_token,
-    uint16_t *__restrict__ h2, int gelu) {
+    uint16_t *__restrict__ h2, int gelu, const MoeLora lora, const float *__restrict__ lax) {
   extern __shared__ __align__(16) uint32_t lds[];
   const int tile = blockIdx.y;
   if (tile >= *ntiles) return;  // whole workgroup
   const int e = tiles[4 * tile], row0 = offsets[e] + tiles[4 * tile + 1];
   const int mcount = tiles[4 * tile + 2], f = tiles[4 * tile + 3];
-  if (f <= 4) gateup_tile<4>(lds, args, x, T, H, I, e, mcount, row0, perm_token, h2, gelu);
-  else if (f == 5) gateup_tile<5>(lds, args, x, T, H, I, e, mcount, row0, perm_token, h2, gelu);
-  else gateup_tile<6>(lds, args, x, T, H, I, e, mcount, row0, perm_token, h2, gelu);
+  if (f <= 4) gateup_tile<4>(lds, args, x, T, H, I, e, mcount, row0, perm_token, h2, gelu, lora, lax);
+  else if (f == 5) gateup_tile<5>(lds, args, x, T, H, I, e, mcount, row0, perm_token, h2, gelu, lora, lax);
+  else gateup_tile<6>(lds, args, x, T, H, I, e, mcount, row0, perm_token, h2, gelu, lora, lax);
 }
 
 template <int F>
 __device__ __forceinline__ void down_tile(uint32_t *lds, const DownArgs &args, const uint16_t *h2, int H, int I,
-                                          int ks, int part, int nt, int e, int mcount, int row0, float *dout) {
+                                          int ks, int part, int nt, int e, int mcount, int row0, float *dout,
+                                          const MoeLora &lora, const float *lah) {
   using Core = MoeDownCore;
   const int n0 = nt * MOE3_DBN, nc = min(MOE3_DBN, H - n0);
   const int k0 = part * ks;
@@ -882,8 +958,14 @@ __device__ __forceinline__ void down_tile(uint32_t *lds, const DownArgs &args, c
 #pragma unroll
       for (int fm = 0; fm < F; fm++) {
         const int m = fm * 16 + l16;
-        const f32x4 v = (acc[fn][fm] + xs[((wn * Core::FN + fn) * F + fm) * 64 + lane]) * sd;
-        if (m < mcount) YStore<float>::store4(dout + (size_t)(row0 + m) * H + n0 + nl, v, nok);
+        f32x4 v = (acc[fn][fm] + xs[((wn * Core::FN + fn) * F + fm) * 64 + lane]) * sd;
+        if (m >= mcount) continue;
+        if (lora.tbl && part == 0) {  // LoRA: down += lora_down(h), in the first K part only
+          const float *av = lah + (long)(row0 + m) * MOE_LORA_MAXR;
+          for (int j = 0; j < nok; j++)
+            v[j] += lora_b(lora.tbl[5 * MOE_MAXE + e], n0 + nl + j, lora.rank, av, lora.scaling);
+        }
+        YStore<float>::store4(dout + (size_t)(row0 + m) * H + n0 + nl, v, nok);
       }
     }
   }
@@ -898,7 +980,7 @@ __device__ __forceinline__ void down_tile(uint32_t *lds, const DownArgs &args, c
 __global__ __launch_bounds__(256) void moe_down3_kernel(
     const DownArgs args, const uint16_t *__restrict__ h2, int H, int I, int ks, int ntn, int kp,
     const int *__restrict__ tiles, const int *__restrict__ ntiles, const int *__restrict__ offsets,
-    float *__restrict__ dout, float *__restrict__ dout_lo) {
+    float *__restrict__ dout, float *__restrict__ dout_lo, const MoeLora lora, const float *__restrict__ lah) {
   extern __shared__ __align__(16) uint32_t lds[];
   const int L = blockIdx.x, xcd = L & 7, j = L >> 3, per = ntn * kp;
   const int tile = xcd + 8 * (j / per);
@@ -907,9 +989,9 @@ __global__ __launch_bounds__(256) void moe_down3_kernel(
   const int e = tiles[4 * tile], row0 = offsets[e] + tiles[4 * tile + 1];
   const int mcount = tiles[4 * tile + 2], f = tiles[4 * tile + 3];
   float *out = part == 0 ? dout : dout_lo;
-  if (f <= 4) down_tile<4>(lds, args, h2, H, I, ks, part, nt, e, mcount, row0, out);
-  else if (f == 5) down_tile<5>(lds, args, h2, H, I, ks, part, nt, e, mcount, row0, out);
-  else down_tile<6>(lds, args, h2, H, I, ks, part, nt, e, mcount, row0, out);
+  if (f <= 4) down_tile<4>(lds, args, h2, H, I, ks, part, nt, e, mcount, row0, out, lora, lah);
+  else if (f == 5) down_tile<5>(lds, args, h2, H, I, ks, part, nt, e, mcount, row0, out, lora, lah);
+  else down_tile<6>(lds, args, h2, H, I, ks, part, nt, e, mcount, row0, out, lora, lah);
 }
 
 // ---- 5. combine ---------------------------------------------------------------
@@ -947,7 +1029,7 @@ hipError_t launch_moe(const void *x, int xt_bf16, const void *router,
                       const float *const *s_down, int T, int H, int I, int E,
                       int top_k, int gelu, void *y, int yt_bf16,
                       uint32_t *topk_idx, float *topk_w, const MoeWorkspace &ws,
-                      int routing, hipStream_t stream) {
+                      int routing, const MoeLora &lora, hipStream_t stream) {
   const int A = T * top_k;
   // 1. router
   int EP = 1;
@@ -1003,8 +1085,29 @@ hipError_t launch_moe(const void *x, int xt_bf16, const void *router,
   // 2. group
   const int bm_max = engine2 ? MOE3_BM : MOE_BM;
   hipLaunchKernelGGL(moe_group_kernel, dim3(1), dim3(1024), 0, stream, ws.idx, A, top_k, E, bm_max,
-                     engine2 ? MOE3_FMIN : 1, ws.counts, ws.offsets, ws.perm_token, ws.inv, ws.tiles, ws.ntiles);
+                     engine2 ? MOE3_FMIN : 1, ws.counts, ws.offsets, ws.perm_token, ws.inv, ws.tiles, ws.ntiles,
+                     ws.row_expert);
   if ((err = hipGetLastError()) != hipSuccess) return err;
+  // LoRA A x of the gate and up adapters, per expert-sorted row
+  if (lora.tbl) {
+    if (xt_bf16)
+      hipLaunchKernelGGL((moe_lora_a_kernel<uint16_t>), dim3(A), dim3(256), 0, stream, lora.tbl, lora.rank,
+                         (const uint16_t *)x, ws.perm_token, ws.row_expert, nullptr, nullptr, 0L, H, 0, 2,
+                         ws.lora_ax, 2 * MOE_LORA_MAXR);
+    else
+      hipLaunchKernelGGL((moe_lora_a_kernel<float>), dim3(A), dim3(256), 0, stream, lora.tbl, lora.rank,
+                         (const float *)x, ws.perm_token, ws.row_expert, nullptr, nullptr, 0L, H, 0, 2, ws.lora_ax,
+                         2 * MOE_LORA_MAXR);
+    if ((err = hipGetLastError()) != hipSuccess) return err;
+  }
+  // LoRA A h of the down adapter (h as bf16 hi + lo, row stride hs)
+  auto lora_down_a = [&](const uint16_t *hh, const uint16_t *hl, long hs) -> hipError_t {
+    if (!lora.tbl) return hipSuccess;
+    hipLaunchKernelGGL((moe_lora_a_kernel<uint16_t>), dim3(A), dim3(256), 0, stream, lora.tbl, lora.rank,
+                       (const uint16_t *)nullptr, ws.perm_token, ws.row_expert, hh, hl, hs, I, 2, 1, ws.lora_ah,
+                       MOE_LORA_MAXR);
+    return hipGetLastError();
+  };
   // 3. gate/up
   const int max_tiles = (A + bm_max - 1) / bm_max + E;
   GateUpArgs ga;
@@ -1030,8 +1133,9 @@ hipError_t launch_moe(const void *x, int xt_bf16, const void *router,
       return err;
     const dim3 g1((I + MOE_GU_BN / 2 - 1) / (MOE_GU_BN / 2), max_tiles);
     hipLaunchKernelGGL(moe_gateup3_kernel, g1, dim3(256), gu_lds, stream, ga, (const uint16_t *)x, T, H, I,
-                       ws.tiles, ws.ntiles, ws.offsets, ws.perm_token, ws.h_hi, gelu);
+                       ws.tiles, ws.ntiles, ws.offsets, ws.perm_token, ws.h_hi, gelu, lora, ws.lora_ax);
     if ((err = hipGetLastError()) != hipSuccess) return err;
+    if ((err = lora_down_a(ws.h_hi, ws.h_hi + I, 2L * I)) != hipSuccess) return err;
     // two K parts when each is a whole number of 64-column steps: twice the
     // workgroups (two per CU at the 512-token, 16-expert layer)
     const int ks = I % 128 == 0 ? I / 2 : I, kp = I / ks;
@@ -1039,22 +1143,26 @@ hipError_t launch_moe(const void *x, int xt_bf16, const void *router,
     const int slots = (max_tiles + 7) / 8 * 8;
     hipLaunchKernelGGL(moe_down3_kernel, dim3(slots * ntn * kp), dim3(256), dn_lds, stream, da,
                        (const uint16_t *)ws.h_hi, H, I, ks, ntn, kp, ws.tiles, ws.ntiles, ws.offsets, ws.dout,
-                       ws.dout_lo);
+                       ws.dout_lo, lora, ws.lora_ah);
     two_parts = kp == 2;
     if ((err = hipGetLastError()) != hipSuccess) return err;
   } else {
     dim3 g1((I + MOE_BN - 1) / MOE_BN, max_tiles);
     if (xt_bf16)
       hipLaunchKernelGGL((moe_gateup_kernel<XS_BF16>), g1, dim3(256), 0, stream, ga, x, H, I,
-                         ws.tiles, ws.ntiles, ws.counts, ws.offsets, ws.perm_token, ws.h_hi, ws.h_lo, gelu);
+                         ws.tiles, ws.ntiles, ws.counts, ws.offsets, ws.perm_token, ws.h_hi, ws.h_lo, gelu,
+                         lora.tbl, lora.rank, lora.scaling, (const float *)ws.lora_ax);
     else
       hipLaunchKernelGGL((moe_gateup_kernel<XS_F32>), g1, dim3(256), 0, stream, ga, x, H, I,
-                         ws.tiles, ws.ntiles, ws.counts, ws.offsets, ws.perm_token, ws.h_hi, ws.h_lo, gelu);
+                         ws.tiles, ws.ntiles, ws.counts, ws.offsets, ws.perm_token, ws.h_hi, ws.h_lo, gelu,
+                         lora.tbl, lora.rank, lora.scaling, (const float *)ws.lora_ax);
     if ((err = hipGetLastError()) != hipSuccess) return err;
+    if ((err = lora_down_a(ws.h_hi, ws.h_lo, (long)I)) != hipSuccess) return err;
     // 4. down
     dim3 g2((H + MOE_BN - 1) / MOE_BN, max_tiles);
     hipLaunchKernelGGL(moe_down_kernel, g2, dim3(256), 0, stream, da, ws.h_hi, ws.h_lo, H, I,
-                       ws.tiles, ws.ntiles, ws.counts, ws.offsets, ws.dout);
+                       ws.tiles, ws.ntiles, ws.counts, ws.offsets, ws.dout, lora.tbl, lora.rank, lora.scaling,
+                       (const float *)ws.lora_ah);
     if ((err = hipGetLastError()) != hipSuccess) return err;
   }
   // 5. combine

@@ -278,9 +278,38 @@ frx_status frx_ternary_ffn_noalloc(frx_ctx *ctx, const void *x, frx_dtype xt,
  * their sum, and experts whose weight is below 1e-8 in magnitude are
  * skipped. The logits are sequential f32 dot products over H; the
  * reference's matrixmultiply::sgemm sums in an order this library does not
- * reproduce. CpuMoELayer's LoRA adapters (training-time) are not part of the
- * call. */
+ * reproduce. CpuMoELayer's LoRA adapters are set with frx_set_moe_lora. */
 frx_status frx_set_moe_routing(frx_ctx *ctx, frx_moe_routing routing);
+
+/* LoRA adapters on the MoE experts: CpuMoELayer::expert_forward_*_with_lora
+ * (src/model/cpu_moe.rs:281-363) with LoraLayer::forward
+ * (src/training/lora.rs:138-167), for LoraManager::forward's per-expert
+ * modules "moe.expert.{e}.gate/up/down" (src/training/lora.rs:447-457):
+ *   gated = W_gate x + scaling * B_gate (A_gate x)   (before the activation)
+ *   upped = W_up x   + scaling * B_up (A_up x)
+ *   down  = W_down h + scaling * B_down (A_down h),  h = act(gated) * upped
+ * for each expert and projection whose A and B are both non-NULL. Device
+ * f32, row-major: A_gate, A_up [rank][H]; B_gate, B_up [I][rank]; A_down
+ * [rank][I]; B_down [H][rank]. Each member below is a host array of
+ * `experts` device pointers (the array itself may be NULL: no adapter of
+ * that projection). The pointer arrays are copied by this call (which first
+ * waits for the context stream); the matrices are read by every later
+ * frx_moe_ternary_ffn on the context, whose expert count must then equal
+ * `experts` (FRX_ERR_SHAPE otherwise), until frx_set_moe_lora(ctx, NULL, 0)
+ * removes them. 1 <= rank <= 64, 1 <= experts <= 64. Both routing modes. The
+ * low-rank sums run in another order than the reference's sequential f32
+ * loops (outputs within 1e-3). */
+typedef struct frx_moe_lora {
+  uint32_t rank;
+  float scaling; /* LoraConfig alpha / rank */
+  const float *const *a_gate;
+  const float *const *b_gate;
+  const float *const *a_up;
+  const float *const *b_up;
+  const float *const *a_down;
+  const float *const *b_down;
+} frx_moe_lora;
+frx_status frx_set_moe_lora(frx_ctx *ctx, const frx_moe_lora *lora, uint32_t experts);
 
 /* Forced failure, for testing a caller's fallback path (no counterpart in
  * the reference; its callers fall back to the CPU on any FerrisResError,

@@ -65,6 +65,10 @@ def lib():
             "frxo_moe_route": (None, [_vp, _vp, _sz, _sz, _sz, _sz, _vp, _vp, _vp]),
             "frxo_moe_forward": (None, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
                                         _sz, _sz, _sz, _sz, _sz, ctypes.c_int, _vp, _vp, _vp]),
+            "frxo_lora_forward": (None, [_vp, _vp, _sz, _sz, _sz, _f, _vp, _vp]),
+            "frxo_moe_forward_lora": (None, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _sz, _sz, _sz, _sz,
+                                             ctypes.c_int, ctypes.c_int, _sz, _f, _vp, _vp, _vp, _vp, _vp, _vp,
+                                             _vp, _vp, _vp]),
             "frxo_gelu_tanh": (_f, [_f]),
             "frxo_ffn_forward": (None, [_vp, _sz, _sz, _sz, _vp, _vp, _vp, _vp, _vp, _vp,
                                         ctypes.c_int, _vp]),
@@ -340,6 +344,51 @@ def moe_forward(x, router, w_gate, s_gate, w_up, s_up, w_down, s_down, top_k, ge
     w = np.zeros((T, top_k), np.float32)
     lib().frxo_moe_forward_routed(_p(xx), _p(r), arr(wg), arr(sg), arr(wu), arr(su), arr(wd), arr(sd),
                                   T, H, I, E, top_k, int(gelu), int(routing), _p(out), _p(idx), _p(w))
+    return out, idx, w
+
+
+def lora_forward(a, b, scaling, x):
+    """LoraLayer::forward (lora.rs:138-167) of one position: A [rank][in],
+    B [out][rank], x [in] -> [out]."""
+    aa = _c(a, np.float32)
+    bb = _c(b, np.float32)
+    xx = _c(x, np.float32)
+    rank, n_in = aa.shape
+    n_out = bb.shape[0]
+    out = np.zeros(n_out, np.float32)
+    lib().frxo_lora_forward(_p(aa), _p(bb), rank, n_in, n_out, scaling, _p(xx), _p(out))
+    return out
+
+
+def moe_forward_lora(x, router, w_gate, s_gate, w_up, s_up, w_down, s_down, top_k, lora, gelu=False, routing=0):
+    """moe_forward with LoRA adapters (CpuMoELayer, cpu_moe.rs:321-363).
+    lora: dict with rank, scaling and per-expert lists a_gate, b_gate, a_up,
+    b_up, a_down, b_down (entries None where an expert has no adapter)."""
+    xx = _c(x, np.float32)
+    r = _c(router, np.float32)
+    T, H = xx.shape
+    E = len(w_gate)
+    I = w_gate[0].shape[0]
+    keep = [_c(a, np.uint32) for a in (*w_gate, *w_up, *w_down)] + \
+           [_c(a, np.float32) for a in (*s_gate, *s_up, *s_down)]
+
+    def arr(lst):
+        return (_vp * E)(*[a.ctypes.data for a in lst])
+    wg, wu, wd = keep[0:E], keep[E:2 * E], keep[2 * E:3 * E]
+    sg, su, sd = keep[3 * E:4 * E], keep[4 * E:5 * E], keep[5 * E:6 * E]
+    lk = {}
+    for name in ("a_gate", "b_gate", "a_up", "b_up", "a_down", "b_down"):
+        mats = [None if m is None else _c(m, np.float32) for m in lora[name]]
+        lk[name] = mats
+    def larr(name):
+        return (_vp * E)(*[None if m is None else m.ctypes.data for m in lk[name]])
+    out = np.zeros((T, H), np.float32)
+    idx = np.zeros((T, top_k), np.uint32)
+    w = np.zeros((T, top_k), np.float32)
+    lib().frxo_moe_forward_lora(_p(xx), _p(r), arr(wg), arr(sg), arr(wu), arr(su), arr(wd), arr(sd), T, H, I, E,
+                                top_k, int(gelu), int(routing), int(lora["rank"]), float(lora["scaling"]),
+                                larr("a_gate"), larr("b_gate"), larr("a_up"), larr("b_up"), larr("a_down"),
+                                larr("b_down"), _p(out), _p(idx), _p(w))
     return out, idx, w
 
 

@@ -810,6 +810,88 @@ void frxo_moe_forward(const float *x, const float *router,
                           top_k, use_gelu, 0, out, topk_idx, topk_w);
 }
 
+/*
+ * LoraLayer::forward for one position, src/training/lora.rs:138-167:
+ * ax[r] = sum_d A[r][d] * in[d] (A: [rank][in]), then
+ * out[o] = (sum_r B[o][r] * ax[r]) * scaling (B: [out][rank]), both sums
+ * left to right in f32 from 0.0, the product rounded before its add.
+ */
+void frxo_lora_forward(const float *a, const float *b, size_t rank, size_t in_f, size_t out_f, float scaling,
+                       const float *input, float *out) {
+  float *ax = (float *)malloc((rank ? rank : 1) * sizeof(float));
+  for (size_t r = 0; r < rank; r++) {
+    float sum = 0.0f;
+    for (size_t d = 0; d < in_f; d++) sum += a[r * in_f + d] * input[d];
+    ax[r] = sum;
+  }
+  for (size_t o = 0; o < out_f; o++) {
+    float sum = 0.0f;
+    for (size_t r = 0; r < rank; r++) sum += b[o * rank + r] * ax[r];
+    out[o] = sum * scaling;
+  }
+  free(ax);
+}
+
+/*
+ * The MoE forward with LoRA adapters on the experts, as
+ * CpuMoELayer::expert_forward_packed_parallel_with_lora
+ * (src/model/cpu_moe.rs:321-363): gated = W_gate x (+ lora_gate(x)),
+ * activation, upped = W_up x (+ lora_up(x)), combined = act(gated) * upped,
+ * down = W_down combined (+ lora_down(combined)); then the routed combine of
+ * frxo_moe_forward_routed. lora_*[e] may be NULL (no adapter on that expert
+ * and projection). Adapter shapes: gate/up A [rank][hidden], B [inter][rank];
+ * down A [rank][inter], B [hidden][rank].
+ */
+void frxo_moe_forward_lora(const float *x, const float *router, const uint32_t *const *w_gate,
+                           const float *const *s_gate, const uint32_t *const *w_up, const float *const *s_up,
+                           const uint32_t *const *w_down, const float *const *s_down, size_t tokens,
+                           size_t hidden, size_t inter, size_t experts, size_t top_k, int use_gelu, int routing,
+                           size_t rank, float scaling, const float *const *a_gate, const float *const *b_gate,
+                           const float *const *a_up, const float *const *b_up, const float *const *a_down,
+                           const float *const *b_down, float *out, uint32_t *topk_idx, float *topk_w) {
+  if (routing == 1)
+    frxo_moe_route_cpu_layer(x, router, tokens, hidden, experts, top_k, topk_idx, topk_w);
+  else
+    frxo_moe_route(x, router, tokens, hidden, experts, top_k, topk_idx, topk_w, NULL);
+  float *g = (float *)malloc(inter * sizeof(float));
+  float *u = (float *)malloc(inter * sizeof(float));
+  float *l = (float *)malloc((inter > hidden ? inter : hidden) * sizeof(float));
+  float *d = (float *)malloc(hidden * sizeof(float));
+  size_t k = top_k < experts ? top_k : experts;
+  for (size_t t = 0; t < tokens; t++) {
+    const float *xr = x + t * hidden;
+    float *orow = out + t * hidden;
+    for (size_t j = 0; j < hidden; j++) orow[j] = 0.0f;
+    for (size_t i = 0; i < k; i++) {
+      uint32_t e = topk_idx[t * top_k + i];
+      float w = topk_w[t * top_k + i];
+      if (routing == 1 && fabsf(w) < 1e-8f) continue;
+      frxo_ternary_matmul_u32(w_gate[e], s_gate[e], xr, 1, hidden, inter, g);
+      if (a_gate && a_gate[e] && b_gate[e]) {
+        frxo_lora_forward(a_gate[e], b_gate[e], rank, hidden, inter, scaling, xr, l);
+        for (size_t j = 0; j < inter; j++) g[j] += l[j];
+      }
+      for (size_t j = 0; j < inter; j++) g[j] = use_gelu ? frxo_gelu_tanh(g[j]) : g[j] / (1.0f + expf(-g[j]));
+      frxo_ternary_matmul_u32(w_up[e], s_up[e], xr, 1, hidden, inter, u);
+      if (a_up && a_up[e] && b_up[e]) {
+        frxo_lora_forward(a_up[e], b_up[e], rank, hidden, inter, scaling, xr, l);
+        for (size_t j = 0; j < inter; j++) u[j] += l[j];
+      }
+      for (size_t j = 0; j < inter; j++) g[j] = g[j] * u[j];
+      frxo_ternary_matmul_u32(w_down[e], s_down[e], g, 1, inter, hidden, d);
+      if (a_down && a_down[e] && b_down[e]) {
+        frxo_lora_forward(a_down[e], b_down[e], rank, inter, hidden, scaling, g, l);
+        for (size_t j = 0; j < hidden; j++) d[j] += l[j];
+      }
+      for (size_t j = 0; j < hidden; j++) orow[j] += w * d[j];
+    }
+  }
+  free(g);
+  free(u);
+  free(l);
+  free(d);
+}
+
 void frxo_moe_forward_routed(const float *x, const float *router,
                              const uint32_t *const *w_gate,
                              const float *const *s_gate,

@@ -119,6 +119,15 @@ void frxo_moe_forward(const float *x, const float *router,
                       const float *const *s_down, size_t tokens, size_t hidden,
                       size_t inter, size_t experts, size_t top_k, int use_gelu,
                       float *out, uint32_t *topk_idx, float *topk_w);
+void frxo_lora_forward(const float *a, const float *b, size_t rank, size_t in_f, size_t out_f, float scaling,
+                       const float *input, float *out);
+void frxo_moe_forward_lora(const float *x, const float *router, const uint32_t *const *w_gate,
+                           const float *const *s_gate, const uint32_t *const *w_up, const float *const *s_up,
+                           const uint32_t *const *w_down, const float *const *s_down, size_t tokens,
+                           size_t hidden, size_t inter, size_t experts, size_t top_k, int use_gelu, int routing,
+                           size_t rank, float scaling, const float *const *a_gate, const float *const *b_gate,
+                           const float *const *a_up, const float *const *b_up, const float *const *a_down,
+                           const float *const *b_down, float *out, uint32_t *topk_idx, float *topk_w);
 float frxo_gelu_tanh(float x);
 void frxo_ffn_forward(const float *x, size_t seq, size_t hidden, size_t inter,
                       const uint32_t *w_gate, const float *s_gate,

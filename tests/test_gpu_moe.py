@@ -246,3 +246,83 @@ def test_routing_kats_through_the_gpu_router(ctx, kat, xt):
             assert abs(float(w[t].sum()) - 1.0) < kat["sum_tol"]
     ref, _, _ = run_oracle(xf, rf, ex, E, k, False)
     assert_close_f32(host(y), ref)
+
+
+def make_lora(name, H, I, E, rank, skip):
+    """Random f32 LoRA adapters (A ~ N(0, 0.1), B ~ N(0, 0.1)) for every
+    (projection, expert) except those in `skip` (no adapter there)."""
+    shapes = {"gate": ((rank, H), (I, rank)), "up": ((rank, H), (I, rank)), "down": ((rank, I), (H, rank))}
+    host_l = {"rank": rank, "scaling": 2.0}
+    dev_l = {}
+    for proj, (sa, sb) in shapes.items():
+        a_l, b_l = [], []
+        for e in range(E):
+            if (proj, e) in skip:
+                a_l.append(None)
+                b_l.append(None)
+                continue
+            a_l.append(synth.normal(synth.seed_of(name, f"la_{proj}{e}"), sa[0] * sa[1], 0.1).reshape(sa))
+            b_l.append(synth.normal(synth.seed_of(name, f"lb_{proj}{e}"), sb[0] * sb[1], 0.1).reshape(sb))
+        host_l["a_" + proj], host_l["b_" + proj] = a_l, b_l
+        dev_l["a_" + proj] = [None if m is None else dev_f32(m) for m in a_l]
+        dev_l["b_" + proj] = [None if m is None else dev_f32(m) for m in b_l]
+    return host_l, dev_l
+
+
+@pytest.mark.parametrize("T,H,I,E,k,xt,routing", [(40, 128, 256, 8, 2, "bf16", 0), (50, 320, 192, 5, 2, "bf16", 1),
+                                                  (33, 192, 128, 5, 3, "f32", 0), (7, 64, 96, 4, 1, "bf16", 1),
+                                                  (300, 192, 448, 3, 2, "bf16", 0)])
+def test_moe_lora_parity(ctx, T, H, I, E, k, xt, routing):
+    """LoRA adapters on the experts (CpuMoELayer::expert_forward_*_with_lora,
+    cpu_moe.rs:321-363; LoraLayer::forward, lora.rs:138-167), on some experts
+    and projections only: gated/upped gain scaling * B (A x) before the
+    activation, the down output scaling * B (A h). Both GEMM engines (bf16 x
+    with H, I multiples of 64; f32 x or I % 64 != 0), one and two K parts of
+    the down GEMM, both routing modes; routing bit-exact, outputs within
+    1e-3 of the oracle."""
+    name = f"moe/lora/{T}x{H}x{I}x{E}"
+    xf, xb, rf, rb, ex = make_moe(name, T, H, I, E)
+    if xt == "f32":
+        xf = synth.normal(91, T * H).reshape(T, H)
+    if routing == 1:
+        rf, rb = np.ascontiguousarray(rf.T), np.ascontiguousarray(rb.T)
+    skip = {("gate", 1), ("up", 0), ("down", 2), ("up", E - 1)}
+    hl, dl = make_lora(name, H, I, E, 8, skip)
+    ctx.set_moe_routing(routing)
+    ctx.set_moe_lora(8, 2.0, E, **dl)
+    try:
+        y, idx, w = run_gpu(ctx, xf, xb, rf, rb, ex, E, k, frx.ACT_SILU, xt=xt)
+    finally:
+        ctx.set_moe_lora(None)
+        ctx.set_moe_routing(frx.MOE_TERNARY_MOE_LAYER)
+    g = lambda m, i: [ex[(m, e)][i] for e in range(E)]  # noqa: E731
+    ref, ridx, rw = oracle.moe_forward_lora(xf, rf, g("gate", 0), g("gate", 1), g("up", 0), g("up", 1),
+                                            g("down", 0), g("down", 1), k, hl, routing=routing)
+    np.testing.assert_array_equal(idx, ridx)
+    assert_close_f32(host(y), ref)
+    plain, _, _ = run_oracle(xf, rf, ex, E, k, False, routing=routing)
+    assert np.abs(ref - plain).max() > 1e-2 * np.abs(plain).max()  # the adapters change the output
+
+
+def test_moe_lora_cleared_and_shape_checks(ctx):
+    """Removing the adapters restores the plain layer bit for bit; a rank
+    outside [1, 64] and an expert count that differs from the call's are
+    shape errors."""
+    T, H, I, E, k = 40, 128, 256, 8, 2
+    xf, xb, rf, rb, ex = make_moe("moe/lora/clear", T, H, I, E)
+    a = run_gpu(ctx, xf, xb, rf, rb, ex, E, k, frx.ACT_SILU)
+    _, dl = make_lora("moe/lora/clear", H, I, E, 4, set())
+    ctx.set_moe_lora(4, 1.0, E, **dl)
+    ctx.set_moe_lora(None)
+    b = run_gpu(ctx, xf, xb, rf, rb, ex, E, k, frx.ACT_SILU)
+    np.testing.assert_array_equal(host(a[0]), host(b[0]))
+    for rank in (0, 65):
+        with pytest.raises(frx.FrxError):
+            ctx.set_moe_lora(rank, 1.0, E, **dl)
+    ctx.set_moe_lora(4, 1.0, E, **dl)
+    try:
+        with pytest.raises(frx.FrxError):
+            run_gpu(ctx, xf[:, :], xb, rf[:4], rb[:4], {kk: v for kk, v in ex.items() if kk[1] < 4}, 4, k,
+                    frx.ACT_SILU)
+    finally:
+        ctx.set_moe_lora(None)

@@ -475,3 +475,67 @@ def test_ternary_stats_counts_every_value_once():
     counts, ratios, _ = oracle.ternary_stats(t)
     assert list(counts) == [(t == -1).sum(), (t == 0).sum(), (t == 1).sum()]
     np.testing.assert_allclose(ratios.sum(), 1.0, atol=1e-6)
+
+
+def test_lora_forward_closed_form_and_vs_f64():
+    """LoraLayer::forward (lora.rs:138-167): rank 1 with A = e_0 and B = ones
+    is scaling * x[0] in every output, exactly; random adapters match float64."""
+    rng = np.random.default_rng(41)
+    x = rng.standard_normal(24).astype(np.float32)
+    a = np.zeros((1, 24), np.float32)
+    a[0, 0] = 1.0
+    out = oracle.lora_forward(a, np.ones((7, 1), np.float32), 0.5, x)
+    np.testing.assert_array_equal(out, np.full(7, np.float32(0.5) * x[0], np.float32))
+    a = rng.standard_normal((8, 96)).astype(np.float32)
+    b = rng.standard_normal((40, 8)).astype(np.float32)
+    x = rng.standard_normal(96).astype(np.float32)
+    ref = 2.0 * (b.astype(np.float64) @ (a.astype(np.float64) @ x))
+    assert np.abs(oracle.lora_forward(a, b, 2.0, x) - ref).max() <= 1e-5 * np.abs(ref).max()
+    # rank 0 rows of B: the output is zero
+    np.testing.assert_array_equal(oracle.lora_forward(a, np.zeros((5, 8), np.float32), 3.0, x), np.zeros(5))
+
+
+def _moe_lora_f64(x, r, wg, sg, wu, su, wd, sd, k, lora):
+    idx, w = _softmax_route_f64(x, r, k)
+    out = np.zeros((x.shape[0], x.shape[1]))
+    sc = lora["scaling"]
+    lo = lambda n, e, v: (sc * (lora["b_" + n][e].astype(np.float64) @  # noqa: E731
+                                (lora["a_" + n][e].astype(np.float64) @ v))
+                          if lora["a_" + n][e] is not None else 0.0)
+    for t in range(x.shape[0]):
+        for j in range(k):
+            e = idx[t, j]
+            g = (wg[e].astype(np.float64) @ x[t]) * sg[e] + lo("gate", e, x[t])
+            u = (wu[e].astype(np.float64) @ x[t]) * su[e] + lo("up", e, x[t])
+            h = g / (1 + np.exp(-g)) * u
+            out[t] += w[t, j] * ((wd[e].astype(np.float64) @ h) * sd[e] + lo("down", e, h))
+    return out, idx
+
+
+def test_moe_forward_lora_vs_f64_and_without_adapters():
+    """The MoE forward with LoRA adapters (cpu_moe.rs:321-363) against a
+    float64 composition, adapters on some experts and projections only; with
+    no adapters it equals moe_forward bit for bit."""
+    rng = np.random.default_rng(43)
+    T, H, I, E, k, rank = 7, 32, 48, 4, 2, 4
+    x = rng.standard_normal((T, H)).astype(np.float32)
+    r = (rng.standard_normal((E, H)) * 0.3).astype(np.float32)
+    mk = lambda n, kk: rng.integers(-1, 2, size=(n, kk)).astype(np.int8)  # noqa: E731
+    wg, wu, wd = [mk(I, H) for _ in range(E)], [mk(I, H) for _ in range(E)], [mk(H, I) for _ in range(E)]
+    sc = lambda n: (np.abs(rng.standard_normal(n)) * 0.1 + 0.05).astype(np.float32)  # noqa: E731
+    sg, su, sd = [sc(I) for _ in range(E)], [sc(I) for _ in range(E)], [sc(H) for _ in range(E)]
+    f = lambda *s: (rng.standard_normal(s) * 0.2).astype(np.float32)  # noqa: E731
+    lora = {"rank": rank, "scaling": 2.0,
+            "a_gate": [f(rank, H), None, f(rank, H), f(rank, H)], "b_gate": [f(I, rank), None, f(I, rank), f(I, rank)],
+            "a_up": [None, f(rank, H), f(rank, H), None], "b_up": [None, f(I, rank), f(I, rank), None],
+            "a_down": [f(rank, I), f(rank, I), None, f(rank, I)], "b_down": [f(H, rank), f(H, rank), None, f(H, rank)]}
+    pk = oracle.pack_rows_u32
+    args = (x, r, [pk(a) for a in wg], sg, [pk(a) for a in wu], su, [pk(a) for a in wd], sd, k)
+    out, idx, w = oracle.moe_forward_lora(*args, lora)
+    ref, idx2 = _moe_lora_f64(x, r, wg, sg, wu, su, wd, sd, k, lora)
+    np.testing.assert_array_equal(idx, idx2)
+    assert np.abs(out - ref).max() <= 1e-5 * np.sqrt((ref ** 2).mean())
+    plain, _, _ = oracle.moe_forward(*args)
+    assert np.abs(out - plain).max() > 1e-2 * np.abs(plain).max()  # the adapters matter here
+    none = {**lora, **{n: [None] * E for n in ("a_gate", "b_gate", "a_up", "b_up", "a_down", "b_down")}}
+    np.testing.assert_array_equal(oracle.moe_forward_lora(*args, none)[0], plain)
