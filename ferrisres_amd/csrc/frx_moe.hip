@@ -406,8 +406,9 @@ __global__ __launch_bounds__(RT_NT) void moe_router_kernel(
 // (E = 16, H = 2048: 100 KB). Measured on the chunked kernel above, staging
 // (per-chunk global loads, conversion, LDS writes) cost as much as the
 // dependent chains and did not overlap them: one wave does both. Here the
-// router rows arrive once by LDS DMA as bf16 (no registers, no VALU), the
-// block's token rows once as f32, and the chains then read LDS only; a
+// router rows arrive by LDS DMA as bf16 (no registers, no VALU) in
+// 512-column chunks: the first together with the block's token rows (once,
+// as f32), the others while the chains run on the chunks before them; a
 // router value is widened from its bf16 pair with one shift or mask, which
 // fits the latency of the dependent add. Row strides are padded by 16 bytes
 // so the 16 experts' (and the tokens') 16-byte reads hit disjoint banks.
@@ -429,20 +430,24 @@ __global__ __launch_bounds__(RT_NT) void moe_router_res_kernel(
   float *xs = reinterpret_cast<float *>(smr);             // [TPB][XS] f32
   uint32_t *rs = smr + TPB * XS;                           // [E][RSB / 4] bf16 pairs
   float *logit = reinterpret_cast<float *>(rs + E * (RSB >> 2));
-  // 1. router rows, 1 KB DMA instructions (lanes past a row's end fill that
-  //    row's padding; past the matrix the descriptor returns zeros)
-  {
-    const __amdgpu_buffer_rsrc_t rr = buffer_rsrc(router, (uint32_t)E * (uint32_t)H * 2u);
-    const int ipr = (H * 2 + 1023) >> 10;
-    for (int i = 0; i < E * ipr; i++) {
-      const int row = i / ipr, j = i - row * ipr;
+  static_assert(RT_NT == 64, "one wave per workgroup: LDS order needs no barrier");
+  // 1. router rows by LDS DMA in 1 KB instructions, column-chunk order (the
+  //    512 columns j of every row, then j + 1, ...): chunk 0 now, the rest
+  //    after the token rows, so that the chains start on chunk 0 while the
+  //    later chunks land (lanes past a row's end fill that row's padding;
+  //    past the matrix the descriptor returns zeros)
+  const int ipr = (H * 2 + 1023) >> 10;
+  const __amdgpu_buffer_rsrc_t rr = buffer_rsrc(router, (uint32_t)E * (uint32_t)H * 2u);
+  auto dma_chunk = [&](int j) {
+    for (int row = 0; row < E; row++)
       lds_load16(rr, rs + row * (RSB >> 2) + j * 256, (uint32_t)row * (uint32_t)H * 2u + (uint32_t)j * 1024u + 16u * tid,
                  0u);
-    }
-  }
+  };
+  dma_chunk(0);
   // 2. the block's token rows as f32 (zeros for tokens past T): UB 8-column
   //    units per lane in flight per batch (one batch at H = 2048, E = 16);
-  //    loads are unconditional from clamped addresses
+  //    loads are unconditional from clamped addresses. Vector loads complete
+  //    in issue order, so converting them waits for chunk 0 as well.
   {
     constexpr int NV = sizeof(XT) == 2 ? 1 : 2;  // 16-byte loads per unit
     constexpr int UB = sizeof(XT) == 2 ? 16 : 8;
@@ -485,8 +490,21 @@ __global__ __launch_bounds__(RT_NT) void moe_router_res_kernel(
       }
     }
   }
-  wait_vmcnt<0>();  // the router rows landed
-  __syncthreads();
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the token rows are in LDS
+  for (int j = 1; j < ipr; j++) dma_chunk(j);
+  // chunk c has landed once at most (ipr - 1 - c) * E DMA instructions are
+  // outstanding (rounded down to a multiple of 16 for the immediate wait:
+  // waiting longer is safe); nothing else is in flight during the chains
+  int landed = 1;  // chunk 0 landed before the token rows were converted
+  auto ensure_chunk = [&](int c) {
+    if (c < landed) return;  // wave-uniform
+    const int rem = (ipr - 1 - c) * E;
+    if (rem >= 48) wait_vmcnt<48>();
+    else if (rem >= 32) wait_vmcnt<32>();
+    else if (rem >= 16) wait_vmcnt<16>();
+    else wait_vmcnt<0>();
+    landed = c + 1;
+  };
   // 3. one dependent chain per lane (left to right, as the reference)
   float sum = 0.0f;
   if (e < E && t < T) {
@@ -503,6 +521,7 @@ __global__ __launch_bounds__(RT_NT) void moe_router_res_kernel(
     const int nblk = H >> 5;
     auto rd = [&](int b, f32x4 *xv, u32x4 *rv) {
       const int j = min(b, max(nblk - 1, 0)) * 32;
+      ensure_chunk(j >> 9);
 #pragma unroll
       for (int q = 0; q < 8; q++) xv[q] = *reinterpret_cast<const f32x4 *>(xr + j + 4 * q);
 #pragma unroll
@@ -534,6 +553,7 @@ __global__ __launch_bounds__(RT_NT) void moe_router_res_kernel(
       __builtin_amdgcn_sched_barrier(0);
     }
     if (b < nblk) run(xa, ra);
+    ensure_chunk(ipr - 1);
     for (int j = nblk * 32; j < H; j += 8) {  // H % 32 columns, 8 at a time
       const f32x4 x0 = *reinterpret_cast<const f32x4 *>(xr + j), x1 = *reinterpret_cast<const f32x4 *>(xr + j + 4);
       const u32x4 r = *reinterpret_cast<const u32x4 *>(rw + (j >> 1));
@@ -545,6 +565,7 @@ __global__ __launch_bounds__(RT_NT) void moe_router_res_kernel(
       }
     }
   }
+  wait_vmcnt<0>();  // every DMA landed (lanes without a chain skip the waits above)
   router_softmax_topk(sum, logit, tid, e, tl, t, T, E, EP, top_k, idx_out, w_out, user_idx, user_w, by_logit);
 }
 
