@@ -894,7 +894,10 @@ static hipError_t launch_gemv_rows_w(const uint32_t *w, const float *scale, cons
 // rows). Measured per launch against gemv_rows_kernel: 5.66 -> 5.50 us
 // (11008x4096, G = 2 per CU) and 5.67 -> 5.28 us (4096x11008, G = 1).
 // The weight words decode in K-interleaved pairs (unpack32_kil, two words
-// per 64-bit shift) and x is staged in the same order.
+// per 64-bit shift) and x is staged in the same order. One matrix (NW = 1):
+// each row's diagonal is summed within its quads as the row completes, and
+// the cross-quad sums of all the wave's rows run once at the end, merged
+// into one register (row r at position r of each quad).
 // XF32: fp32 activations, split once per workgroup at staging into bf16 hi
 // and lo planes (split2_bf16: hi = bf16(x), lo = bf16(x - hi), |x - hi - lo|
 // <= 2^-17 |x|, lo = 0 where hi is not finite); each word then runs four
@@ -1022,8 +1025,11 @@ __global__ __launch_bounds__(512) void gemv_bal_kernel(const uint32_t *__restric
 #pragma unroll
   for (int m = 0; m < NW; m++) res[m] = 0.f;
   const int c = lane & 15, rg = lane >> 4, e = c & 3;
+  const bool e_odd = e & 1, e_hi = e & 2, diag = (c >> 2) == rg;
+  float vq[RMAX];  // NW == 1: each row's diagonal, summed within its quads
 #pragma unroll
   for (int rr = 0; rr < RMAX; rr++) {
+    vq[rr] = 0.f;
     if (rr < cnt) {  // wave-uniform
 #pragma unroll
       for (int m = 0; m < NW; m++) {
@@ -1049,18 +1055,41 @@ __global__ __launch_bounds__(512) void gemv_bal_kernel(const uint32_t *__restric
         }
         const f32x4 acc = acc2[0] + acc2[1];
         // diagonal: lane (c = l%16, rg = l/16) holds C[4rg + e][c]
-        float v = e == 0 ? acc[0] : e == 1 ? acc[1] : e == 2 ? acc[2] : acc[3];
-        v = (c >> 2) == rg ? v : 0.f;
+        const float t0 = e_odd ? acc[1] : acc[0], t1 = e_odd ? acc[3] : acc[2];
+        float v = diag ? (e_hi ? t1 : t0) : 0.f;
         v += dpp_f32<0xB1>(v);  // quad_perm [1,0,3,2]
         v += dpp_f32<0x4E>(v);  // quad_perm [2,3,0,1]
-        const float a = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
-        const float b = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 20));
-        const float d = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 40));
-        const float f = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 60));
-        const float tot = ((a + b) + (d + f)) * sc[rr][m] * 0.5f;  // 0.5 undoes the 2*dec(c) encoding
-        if (lane == rr) res[m] = tot;
+        if constexpr (NW == 1) {
+          vq[rr] = v;
+        } else {
+          const float a = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+          const float b = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 20));
+          const float d = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 40));
+          const float f = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 60));
+          const float tot = ((a + b) + (d + f)) * sc[rr][m] * 0.5f;  // 0.5 undoes the 2*dec(c) encoding
+          if (lane == rr) res[m] = tot;
+        }
       }
     }
+  }
+  if constexpr (NW == 1) {
+    // All rows at once: row r's quad sums move to position r of their quads
+    // (the diagonal quads are quad g of 16-lane row g, all other lanes 0),
+    // rotations by 8 and 4 bring every 16-lane row's quad to positions 0..3,
+    // and two exchanges add the four 16-lane rows: lane r < RMAX then holds
+    // row r's dot product.
+    const int q = lane & 3;
+    float mv = vq[0];
+#pragma unroll
+    for (int rr = 1; rr < RMAX; rr++) mv = q == rr ? vq[rr] : mv;
+    mv += dpp_f32<0x128>(mv);  // row_ror:8
+    mv += dpp_f32<0x124>(mv);  // row_ror:4
+    mv += __shfl_xor(mv, 32);
+    mv += __shfl_xor(mv, 16);
+    float s = sc[0][0];
+#pragma unroll
+    for (int rr = 1; rr < RMAX; rr++) s = q == rr ? sc[rr][0] : s;
+    res[0] = mv * s * 0.5f;  // 0.5 undoes the 2*dec(c) encoding
   }
   if (lane < cnt) {
     const int row = row0 + lane;
