@@ -6,27 +6,31 @@
 // compute unit; each wave streams its own contiguous share of the buffer in
 // 1 KB units (16 bytes per lane), eight units in flight per lane, and
 // XOR-folds the words (one store, under a condition the data never meets,
-// keeps the loads live). No decode, no arithmetic, no reduction: what is
-// left of a launch is dispatch, the first HBM round trip and the streaming.
+// keeps the loads live). Units past a wave's share are not loaded (a
+// wave-uniform branch), so a wave whose share is under eight units issues
+// no extra reads. No decode,
+// no arithmetic, no reduction: what is left of a launch is dispatch, the
+// first HBM round trip and the streaming.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
 namespace {
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 constexpr int RD_WAVES = 8, RD_UNITS = 8;
+constexpr size_t RD_MAX = 0x80000000u;  // bytes read at most (unit indices fit 32 bits)
 
-__global__ __launch_bounds__(RD_WAVES * 64) void read_kernel(const u32x4 *__restrict__ p, size_t nu,
+__global__ __launch_bounds__(RD_WAVES * 64) void read_kernel(const u32x4 *__restrict__ p, uint32_t nu,
                                                             uint32_t *__restrict__ sink) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const size_t waves = (size_t)gridDim.x * RD_WAVES, t = (size_t)blockIdx.x * RD_WAVES + wave;
-  const size_t a = t * nu / waves, b = (t + 1) * nu / waves;  // this wave's 1 KB units
+  const uint32_t waves = gridDim.x * RD_WAVES, t = blockIdx.x * RD_WAVES + wave;
+  const uint32_t a = (uint32_t)((uint64_t)t * nu / waves), b = (uint32_t)((uint64_t)(t + 1) * nu / waves);
   uint32_t acc = 0;
-  for (size_t u0 = a; u0 < b; u0 += RD_UNITS) {
+  for (uint32_t u0 = a; u0 < b; u0 += RD_UNITS) {
     u32x4 v[RD_UNITS];
 #pragma unroll
     for (int u = 0; u < RD_UNITS; u++) {
-      const size_t uu = u0 + u < b ? u0 + u : b - 1;  // past the range: reload the last unit
-      v[u] = p[uu * 64 + lane];
+      v[u] = (u32x4){0u, 0u, 0u, 0u};
+      if (u0 + u < b) v[u] = p[(size_t)(u0 + u) * 64 + lane];  // wave-uniform
     }
 #pragma unroll
     for (int u = 0; u < RD_UNITS; u++) acc ^= v[u].x ^ v[u].y ^ v[u].z ^ v[u].w;
@@ -36,7 +40,7 @@ __global__ __launch_bounds__(RD_WAVES * 64) void read_kernel(const u32x4 *__rest
 }  // namespace
 
 extern "C" {
-// Reads `bytes` (a multiple of 1024) at the 16-byte aligned device address p
+// Reads `bytes` (a multiple of 1024, under 2 GiB) at the 16-byte aligned device address p
 // on `stream`; sink: device buffer of at least frxb_read_grid() words.
 int frxb_read_grid(void) {
   int dev = 0, cus = 256;
@@ -47,9 +51,12 @@ int frxb_read_grid(void) {
 }
 
 int frxb_read(const void *p, size_t bytes, uint32_t *sink, void *stream) {
-  if (!p || !sink || bytes == 0 || (bytes & 1023) != 0 || (reinterpret_cast<uintptr_t>(p) & 15) != 0) return 1;
+  if (!p || !sink || bytes == 0 || (bytes & 1023) != 0 || bytes >= RD_MAX ||
+      (reinterpret_cast<uintptr_t>(p) & 15) != 0)
+    return 1;
   hipLaunchKernelGGL(read_kernel, dim3(frxb_read_grid()), dim3(RD_WAVES * 64), 0,
-                     reinterpret_cast<hipStream_t>(stream), reinterpret_cast<const u32x4 *>(p), bytes / 1024, sink);
+                     reinterpret_cast<hipStream_t>(stream), reinterpret_cast<const u32x4 *>(p),
+                     (uint32_t)(bytes / 1024), sink);
   return hipGetLastError() == hipSuccess ? 0 : 2;
 }
 }
