@@ -44,8 +44,8 @@ def _run(ctx, w, s, xf, xb, xt, yt):
     return y
 
 
-SHAPES = [(1, 256, 64), (3, 512, 100), (16, 1024, 48), (1, 2064, 33), (5, 4096, 130),
-          (9, 2064, 33), (12, 4096, 130), (10, 1040, 8200),
+SHAPES = [(1, 256, 64), (2, 512, 100), (3, 512, 100), (16, 1024, 48), (1, 2064, 33), (5, 4096, 130),
+          (8, 11008, 72), (9, 2064, 33), (12, 4096, 130), (10, 1040, 8200),
           (17, 256, 64), (64, 1040, 200), (130, 512, 136), (257, 128, 19)]
 
 
