@@ -570,14 +570,18 @@ __global__ __launch_bounds__(RT_NT) void moe_router_res_kernel(
 }
 
 // ---- 2. histogram / scan / stable scatter / tile schedule -----------------
-// Exclusive prefix sum of v over the 64 lanes of a wave.
+// Exclusive prefix sum of v over the 64 lanes of a wave: shifts by 1, 2, 4
+// and 8 within each row of 16 lanes, then row 0's total into row 1 and row
+// 2's into row 3 (row_bcast:15), then rows 0-1's total into rows 2-3
+// (row_bcast:31). Lanes without a source add 0.
 __device__ __forceinline__ int wave_excl_scan(int v) {
   int x = v;
-#pragma unroll
-  for (int d = 1; d < 64; d <<= 1) {
-    const int y = __shfl_up(x, d);
-    if ((threadIdx.x & 63) >= d) x += y;
-  }
+  x += __builtin_amdgcn_update_dpp(0, x, 0x111, 0xF, 0xF, false);  // row_shr:1
+  x += __builtin_amdgcn_update_dpp(0, x, 0x112, 0xF, 0xF, false);  // row_shr:2
+  x += __builtin_amdgcn_update_dpp(0, x, 0x114, 0xF, 0xF, false);  // row_shr:4
+  x += __builtin_amdgcn_update_dpp(0, x, 0x118, 0xF, 0xF, false);  // row_shr:8
+  x += __builtin_amdgcn_update_dpp(0, x, 0x142, 0xA, 0xF, false);  // row_bcast:15
+  x += __builtin_amdgcn_update_dpp(0, x, 0x143, 0xC, 0xF, false);  // row_bcast:31
   return x - v;
 }
 
@@ -598,10 +602,13 @@ __global__ __launch_bounds__(1024) void moe_group_kernel(
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   if (tid < MOE_MAXE) base[tid] = 0;
   __syncthreads();
-  // Pass 1: rank of each assignment within its expert, in (t, k) order.
+  // Pass 1: rank of each assignment within its expert, in (t, k) order (the
+  // last chunk's expert and rank stay in registers for pass 2).
+  int e_last = -1, r_last = 0;
   for (int c0 = 0; c0 < A; c0 += 1024) {
     const int a = c0 + tid;
     const int e = a < A ? (int)idx[a] : -1;
+    e_last = e;
     int rank = 0;
     for (int ee = 0; ee < E; ee++) {
       const unsigned long long m = __ballot(e == ee);
@@ -612,7 +619,8 @@ __global__ __launch_bounds__(1024) void moe_group_kernel(
     if (e >= 0) {
       int before = base[e];
       for (int w = 0; w < wave; w++) before += wave_cnt[w][e];
-      inv[a] = before + rank;  // position within the expert (fixed below)
+      r_last = before + rank;  // position within the expert (fixed below)
+      if (c0 + 1024 < A) inv[a] = r_last;
     }
     __syncthreads();
     if (tid < E) {
@@ -660,9 +668,11 @@ __global__ __launch_bounds__(1024) void moe_group_kernel(
   }
   __syncthreads();
   // Pass 2: final rows.
+  const int a_last = (A - 1) / 1024 * 1024 + tid;  // this thread's assignment of the last chunk
   for (int a = tid; a < A; a += 1024) {
-    const int e = (int)idx[a];
-    const int pos = offs[e] + inv[a];
+    const bool reg = a == a_last;
+    const int e = reg ? e_last : (int)idx[a];
+    const int pos = offs[e] + (reg ? r_last : inv[a]);
     inv[a] = pos;
     perm_token[pos] = a / top_k;
     row_expert[pos] = e;
