@@ -18,7 +18,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libfrx_ternary.so")
 
 FRX_F32, FRX_BF16 = 0, 1
-ACT_SILU, ACT_GELU_TANH = 0, 1
+ACT_SILU, ACT_GELU_TANH, ACT_GELU_TANH_GATE = 0, 1, 2
 FFN_AUTO, FFN_ONE_LAUNCH, FFN_TWO_LAUNCH = 0, 1, 2
 MOE_TERNARY_MOE_LAYER, MOE_CPU_MOE_LAYER = 0, 1
 QUANT_ABSMEAN, QUANT_STE = 0, 1
@@ -88,6 +88,11 @@ _SIGS = {
                               ctypes.POINTER(_u32)]),
     "frx_sparse24_cpu_to_gpu_device": (_int, [_vp, _vp, _vp, _u32, _u32, _vp]),
     "frx_quantize_ternary": (_int, [_vp, _vp, _int, _u32, _u32, _int, _vp, _vp]),
+    "frx_quantize_ternary_blocked": (_int, [_vp, _vp, _int, _sz, _u32, _vp, _vp]),
+    "frx_dequantize_ternary_blocked": (_int, [_vp, _vp, _vp, _sz, _u32, _vp]),
+    "frx_prune_sparse24": (_int, [_vp, _vp, _int, _u32, _u32, _int, _vp, _vp, _vp, _vp]),
+    "frx_workspace_stats": (_int, [_vp, ctypes.POINTER(_sz), ctypes.POINTER(_sz), ctypes.POINTER(_u32)]),
+    "frx_release_retired": (_int, [_vp]),
     "frx_free": (_int, [_vp, _vp]),
     "frx_pack_ternary_u8": (_int, [_vp, _sz, _vp]),
     "frx_unpack_ternary_u8": (_int, [_vp, _sz, _vp]),
@@ -371,7 +376,7 @@ class Context:
         _expect_numel(router, E * H, "router")
         I = _rows(w_gate[0], H // 16, "w_gate[0]") if H % 16 == 0 else int(w_gate[0].shape[0])
         _expect_shape(y, (T, H), "y")
-        arr = lambda ts: (_vp * E)(*[t.data_ptr() for t in ts])  # noqa: E731
+        arr = lambda ts: None if ts is None else (_vp * E)(*[t.data_ptr() for t in ts])  # noqa: E731
         _check(lib().frx_moe_ternary_ffn(
             self._h, _ptr(x), _dtype_code(x), _ptr(router), _dtype_code(router),
             arr(w_gate), arr(s_gate), arr(w_up), arr(s_up), arr(w_down), arr(s_down),
@@ -445,6 +450,48 @@ class Context:
         _check(lib().frx_quantize_ternary(self._h, _ptr(w), _dtype_code(w), N, K, rule, _ptr(packed),
                                           _ptr(scale)), self._h)
         return packed, scale
+
+    def quantize_ternary_blocked(self, w, block_size: int, packed, scales):
+        """frx_quantize_ternary_blocked: the flat tensor w (f32 or bf16
+        device tensor, n values) in blocks of block_size values, each with
+        its own absmean alpha (quantize_ternary_blocked, ternary.rs:76-110),
+        into packed [ceil(n/16)] u32 codes and scales [ceil(n/block)] f32."""
+        n = int(w.numel())
+        _expect_numel(packed, -(-n // 16), "packed")
+        _expect_numel(scales, -(-n // block_size) if block_size else 0, "scales")
+        _check(lib().frx_quantize_ternary_blocked(self._h, _ptr(w), _dtype_code(w), n, block_size, _ptr(packed),
+                                                  _ptr(scales)), self._h)
+        return packed, scales
+
+    def dequantize_ternary_blocked(self, packed, scales, n: int, block_size: int, out):
+        """frx_dequantize_ternary_blocked: out[i] = scales[i / block] *
+        dec(code i) (dequantize_ternary_blocked, ternary.rs:113-128)."""
+        _expect_numel(out, n, "out")
+        _check(lib().frx_dequantize_ternary_blocked(self._h, _ptr(packed), _ptr(scales), n, block_size,
+                                                    _ptr(out)), self._h)
+        return out
+
+    def prune_sparse24(self, w, scale, patterns=None, signs=None, meta=None, per_row: bool = False):
+        """frx_prune_sparse24: prune_fp32_to_sparse_ternary
+        (sparse_ternary.rs:598-663) of w [N][K] (f32 or bf16 device tensor)
+        into the CPU layout (patterns, signs) and / or the GPU layout (meta
+        [N][ceil(K/24)]), scale [N] f32 (the tensor scale on every row, or
+        one per row)."""
+        N, K = _shape2(w, "w")
+        _expect_numel(scale, N, "scale")
+        _check(lib().frx_prune_sparse24(self._h, _ptr(w), _dtype_code(w), N, K, int(per_row), _ptr(patterns),
+                                        _ptr(signs), _ptr(meta), _ptr(scale)), self._h)
+        return patterns, signs, meta, scale
+
+    def workspace_stats(self):
+        """frx_workspace_stats: (live bytes, retired bytes, allocations)."""
+        live, ret, n = _sz(0), _sz(0), _u32(0)
+        _check(lib().frx_workspace_stats(self._h, ctypes.byref(live), ctypes.byref(ret), ctypes.byref(n)), self._h)
+        return int(live.value), int(ret.value), int(n.value)
+
+    def release_retired(self):
+        """frx_release_retired: frees workspaces replaced by larger ones."""
+        _check(lib().frx_release_retired(self._h), self._h)
 
     def set_moe_routing(self, routing: int):
         """frx_set_moe_routing: MOE_TERNARY_MOE_LAYER (router [E,H], default)

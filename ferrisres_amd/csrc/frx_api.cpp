@@ -21,6 +21,7 @@
 
 #include "../../include/frx_ternary.h"
 #include "frx_internal.hpp"
+#include "frx_policy.hpp"
 
 // Device scratch of frx_ternary_ffn_noalloc: one array per GPU, held until
 // the process ends. Its host-side name is only a handle: kernels and copies
@@ -66,6 +67,9 @@ struct frx_ctx {
   // Workspaces replaced by larger ones stay allocated until frx_destroy: a
   // graph captured at a smaller size still holds their addresses.
   std::vector<void *> retired;
+  size_t retired_bytes = 0;
+  size_t live_bytes = 0;    // bytes of the current (not retired) context buffers
+  uint32_t allocations = 0;  // device allocations made by this context
   void *noalloc = nullptr;  // device address of frx_noalloc_scratch on this device
   hipError_t noalloc_err = hipSuccess;
   // growable device scratch for the host-slice API and the MoE workspace
@@ -81,6 +85,8 @@ struct frx_ctx {
   size_t blk_ws_bytes = 0;
   void *unit_ws = nullptr;  // unit row scales of the column-block linear
   size_t unit_ws_bytes = 0;
+  void *stage_ws = nullptr;  // 16-byte aligned copies of unaligned x / scale / y
+  size_t stage_ws_bytes = 0;
   unsigned *ffn_bar = nullptr;  // grid-barrier words of the one-launch FFN
   int ffn_mode = FRX_FFN_AUTO;
   int moe_routing = FRX_MOE_TERNARY_MOE_LAYER;
@@ -173,6 +179,7 @@ void frx_destroy(frx_ctx *ctx) {
   if (ctx->blk_ws) (void)hipFree(ctx->blk_ws);
   if (ctx->router_ws) (void)hipFree(ctx->router_ws);
   if (ctx->unit_ws) (void)hipFree(ctx->unit_ws);
+  if (ctx->stage_ws) (void)hipFree(ctx->stage_ws);
   if (ctx->ffn_bar) (void)hipFree(ctx->ffn_bar);
   for (void *p : ctx->retired) (void)hipFree(p);
   delete ctx;
@@ -244,14 +251,25 @@ frx_status frx_set_moe_lora(frx_ctx *ctx, const frx_moe_lora *lora, uint32_t exp
     for (uint32_t e = 0; e < experts && src[k]; e++) host[k * 64 + e] = src[k][e];
   hipError_t e = hipSetDevice(ctx->device);
   if (e != hipSuccess) return hip_fail(ctx, e, "LoRA setup");
-  if (!ctx->lora_tbl) {
-    e = hipMalloc(reinterpret_cast<void **>(&ctx->lora_tbl), sizeof(host));
-    if (e != hipSuccess) return hip_fail(ctx, e, "LoRA table allocation");
-  }
-  // earlier MoE launches on the context stream may still read the table
-  if ((e = hipStreamSynchronize(ctx->stream)) != hipSuccess) return hip_fail(ctx, e, "LoRA setup wait");
-  if ((e = hipMemcpy(ctx->lora_tbl, host, sizeof(host), hipMemcpyHostToDevice)) != hipSuccess)
+  // Every call gets a table of its own: launches already enqueued, and
+  // graphs captured with the previous adapters, keep reading the previous
+  // table (retired like a replaced workspace) with the rank they were
+  // launched with, so no launch sees a table and a rank that do not match.
+  const float **tbl = nullptr;
+  e = hipMalloc(reinterpret_cast<void **>(&tbl), sizeof(host));
+  if (e != hipSuccess) return hip_fail(ctx, e, "LoRA table allocation");
+  ctx->allocations++;
+  if ((e = hipMemcpy(tbl, host, sizeof(host), hipMemcpyHostToDevice)) != hipSuccess) {
+    (void)hipFree(tbl);
     return hip_fail(ctx, e, "LoRA table copy");
+  }
+  if (ctx->lora_tbl) {
+    ctx->retired.push_back(ctx->lora_tbl);
+    ctx->retired_bytes += sizeof(host);
+  } else {
+    ctx->live_bytes += sizeof(host);
+  }
+  ctx->lora_tbl = tbl;
   ctx->lora_rank = lora->rank;
   ctx->lora_scaling = lora->scaling;
   ctx->lora_experts = experts;
@@ -281,11 +299,68 @@ static frx_status check_linear(frx_ctx *ctx, const void *w, const void *scale,
   if (sparse && K % 4 != 0) return fail(ctx, FRX_ERR_SHAPE, "in_cols=%u must be a multiple of 4 for 2:4", K);
   if ((xt != FRX_F32 && xt != FRX_BF16) || (yt != FRX_F32 && yt != FRX_BF16))
     return fail(ctx, FRX_ERR_UNSUPPORTED, "dtype must be FRX_F32 or FRX_BF16");
-  if (!aligned16(x) || !aligned16(y) || !aligned16(scale))
-    return fail(ctx, FRX_ERR_UNSUPPORTED, "x, y and scale must be 16-byte aligned device pointers");
+  const uintptr_t xa = xt == FRX_BF16 ? 1 : 3, ya = yt == FRX_BF16 ? 1 : 3;
+  if ((reinterpret_cast<uintptr_t>(x) & xa) || (reinterpret_cast<uintptr_t>(y) & ya) ||
+      (reinterpret_cast<uintptr_t>(scale) & 3) || (reinterpret_cast<uintptr_t>(w) & 3))
+    return fail(ctx, FRX_ERR_SHAPE, "x, y, scale and weights must be aligned to their element size");
   if ((size_t)M * K > (size_t)0x7FFFFFFF || (size_t)M * N > (size_t)0x7FFFFFFF)
     return fail(ctx, FRX_ERR_SHAPE, "M*K or M*N exceeds 2^31 elements");
+  // the kernels address the weights through 32-bit buffer ranges
+  const size_t wbytes = sparse ? (size_t)N * (((size_t)K / 4 + 5) / 6) * 4 : (size_t)N * K / 4;
+  if (wbytes > (size_t)0xFFFFFFF0u)
+    return fail(ctx, FRX_ERR_SHAPE, "weight matrix of %zu bytes exceeds 4 GiB (N=%u K=%u)", wbytes, N, K);
   return FRX_OK;
+}
+
+static frx_status ensure_buffer(frx_ctx *ctx, void **buf, size_t *have, size_t need, const char *what);
+
+// x, scale and y as the kernels take them: 16-byte aligned. A caller's sub-
+// slice at another offset is copied into the context's staging workspace
+// (x and scale before the launch, y back after it), on the context stream.
+struct Staged {
+  const void *x;
+  const float *scale;
+  void *y;
+  void *y_user = nullptr;
+  size_t y_bytes = 0;
+};
+
+static frx_status stage_linear(frx_ctx *ctx, const void *x, frx_dtype xt, const float *scale, void *y,
+                               frx_dtype yt, uint32_t M, uint32_t K, uint32_t N, Staged *out) {
+  out->x = x;
+  out->scale = scale;
+  out->y = y;
+  const bool sx = !aligned16(x), ss = !aligned16(scale), sy = !aligned16(y);
+  if (!sx && !ss && !sy) return FRX_OK;
+  const size_t xb = (size_t)M * K * (xt == FRX_BF16 ? 2 : 4), sb = (size_t)N * 4;
+  const size_t yb = (size_t)M * N * (yt == FRX_BF16 ? 2 : 4);
+  const size_t need = (sx ? a256(xb) : 0) + (ss ? a256(sb) : 0) + (sy ? a256(yb) : 0);
+  frx_status st = ensure_buffer(ctx, &ctx->stage_ws, &ctx->stage_ws_bytes, need, "staging workspace allocation");
+  if (st != FRX_OK) return st;
+  char *base = reinterpret_cast<char *>(ctx->stage_ws);
+  hipError_t e = hipSuccess;
+  if (sx) {
+    e = hipMemcpyAsync(base, x, xb, hipMemcpyDeviceToDevice, ctx->stream);
+    out->x = base;
+    base += a256(xb);
+  }
+  if (ss && e == hipSuccess) {
+    e = hipMemcpyAsync(base, scale, sb, hipMemcpyDeviceToDevice, ctx->stream);
+    out->scale = reinterpret_cast<const float *>(base);
+    base += a256(sb);
+  }
+  if (sy) {
+    out->y = base;
+    out->y_user = y;
+    out->y_bytes = yb;
+  }
+  if (e != hipSuccess) return hip_fail(ctx, e, "staging copy");
+  return FRX_OK;
+}
+
+static hipError_t unstage_linear(frx_ctx *ctx, const Staged &sg) {
+  if (!sg.y_user) return hipSuccess;
+  return hipMemcpyAsync(sg.y_user, sg.y, sg.y_bytes, hipMemcpyDeviceToDevice, ctx->stream);
 }
 
 static frx_status ternary_linear_run(frx_ctx *ctx, const uint32_t *w, const float *scale, const float *bias,
@@ -294,12 +369,16 @@ static frx_status ternary_linear_run(frx_ctx *ctx, const uint32_t *w, const floa
   frx_status st = enter(ctx);
   if (st != FRX_OK) return st;
   if ((st = check_linear(ctx, w, scale, x, xt, y, yt, M, K, N, false)) != FRX_OK) return st;
+  Staged sg;
+  if ((st = stage_linear(ctx, x, xt, scale, y, yt, M, K, N, &sg)) != FRX_OK) return st;
   hipError_t e;
   if (M <= 16)
-    e = frx::launch_gemv(w, scale, x, xt == FRX_BF16, y, yt == FRX_BF16, (int)M, (int)K, (int)N, ctx->stream, bias);
+    e = frx::launch_gemv(w, sg.scale, sg.x, xt == FRX_BF16, sg.y, yt == FRX_BF16, (int)M, (int)K, (int)N,
+                         ctx->stream, bias);
   else
-    e = frx::launch_gemm(w, scale, x, xt == FRX_BF16, y, yt == FRX_BF16, (int)M, (int)K, (int)N, 0, ctx->stream,
-                         bias);
+    e = frx::launch_gemm(w, sg.scale, sg.x, xt == FRX_BF16, sg.y, yt == FRX_BF16, (int)M, (int)K, (int)N, 0,
+                         ctx->stream, bias);
+  if (e == hipSuccess) e = unstage_linear(ctx, sg);
   if (e != hipSuccess) return hip_fail(ctx, e, "ternary_linear launch");
   return FRX_OK;
 }
@@ -324,24 +403,74 @@ frx_status frx_sparse24_ternary_linear(frx_ctx *ctx, const uint32_t *meta,
   frx_status st = enter(ctx);
   if (st != FRX_OK) return st;
   if ((st = check_linear(ctx, meta, scale, x, xt, y, yt, M, K, N, true)) != FRX_OK) return st;
-  hipError_t e = frx::launch_gemm(meta, scale, x, xt == FRX_BF16, y, yt == FRX_BF16, (int)M, (int)K, (int)N, 1,
-                                  ctx->stream);
+  Staged sg;
+  if ((st = stage_linear(ctx, x, xt, scale, y, yt, M, K, N, &sg)) != FRX_OK) return st;
+  hipError_t e = frx::launch_gemm(meta, sg.scale, sg.x, xt == FRX_BF16, sg.y, yt == FRX_BF16, (int)M, (int)K,
+                                  (int)N, 1, ctx->stream);
+  if (e == hipSuccess) e = unstage_linear(ctx, sg);
   if (e != hipSuccess) return hip_fail(ctx, e, "sparse24_ternary_linear launch");
   return FRX_OK;
 }
 
 // Grows a context-owned device buffer. The buffer it replaces is retired,
 // not freed: a graph captured at a smaller size still writes to it, so it
-// stays allocated until frx_destroy. The first call at a larger size
+// stays allocated until frx_release_retired or frx_destroy. Sizes grow
+// geometrically (frx::grow_bytes: at least 1.5x the old size), so rising
+// requests make O(log) allocations and the retired buffers of one workspace
+// total less than twice its current size. The first call at a larger size
 // allocates and must not be under graph capture.
 static frx_status ensure_buffer(frx_ctx *ctx, void **buf, size_t *have, size_t need, const char *what) {
   if (need <= *have) return FRX_OK;
+  const size_t bytes = frx::grow_bytes(*have, need);
   void *p = nullptr;
-  hipError_t e = hipMalloc(&p, need);
+  hipError_t e = hipMalloc(&p, bytes);
+  if (e == hipErrorOutOfMemory && bytes > a256(need)) {
+    (void)hipGetLastError();  // the geometric size did not fit: take what was asked
+    e = hipMalloc(&p, a256(need));
+    if (e == hipSuccess) {
+      ctx->allocations++;
+      if (*buf) {
+        ctx->retired.push_back(*buf);
+        ctx->retired_bytes += *have;
+        ctx->live_bytes -= *have;
+      }
+      *buf = p;
+      *have = a256(need);
+      ctx->live_bytes += *have;
+      return FRX_OK;
+    }
+  }
   if (e != hipSuccess) return hip_fail(ctx, e, what);
-  if (*buf) ctx->retired.push_back(*buf);
+  ctx->allocations++;
+  if (*buf) {
+    ctx->retired.push_back(*buf);
+    ctx->retired_bytes += *have;
+    ctx->live_bytes -= *have;
+  }
   *buf = p;
-  *have = need;
+  *have = bytes;
+  ctx->live_bytes += bytes;
+  return FRX_OK;
+}
+
+frx_status frx_workspace_stats(frx_ctx *ctx, size_t *live_bytes, size_t *retired_bytes, uint32_t *allocations) {
+  if (!ctx) return FRX_ERR_DEVICE;
+  ctx->err[0] = 0;
+  if (live_bytes) *live_bytes = ctx->live_bytes;
+  if (retired_bytes) *retired_bytes = ctx->retired_bytes;
+  if (allocations) *allocations = ctx->allocations;
+  return FRX_OK;
+}
+
+frx_status frx_release_retired(frx_ctx *ctx) {
+  frx_status st = enter(ctx, false);
+  if (st != FRX_OK) return st;
+  // launches already enqueued on the context stream may still use them
+  hipError_t e = hipStreamSynchronize(ctx->stream);
+  if (e != hipSuccess) return hip_fail(ctx, e, "release wait");
+  for (void *p : ctx->retired) (void)hipFree(p);
+  ctx->retired.clear();
+  ctx->retired_bytes = 0;
   return FRX_OK;
 }
 
@@ -354,6 +483,13 @@ frx_status frx_moe_ternary_ffn(
     void *y, frx_dtype yt, uint32_t *topk_idx, float *topk_w) {
   frx_status st = enter(ctx);
   if (st != FRX_OK) return st;
+  // TernaryMoELayer's GeLU experts read no up projection: w_up / s_up may be
+  // NULL, and the gate matrices stand in for them in the kernels' operands
+  const bool gate_only = act == FRX_ACT_GELU_TANH_GATE;
+  if (gate_only) {
+    if (!w_up) w_up = w_gate;
+    if (!s_up) s_up = s_gate;
+  }
   if (!x || !router || !w_gate || !s_gate || !w_up || !s_up || !w_down || !s_down || !y)
     return fail(ctx, FRX_ERR_SHAPE, "null pointer argument");
   if (T == 0 || H == 0 || I == 0 || E == 0) return fail(ctx, FRX_ERR_SHAPE, "empty shape");
@@ -363,7 +499,20 @@ frx_status frx_moe_ternary_ffn(
     return fail(ctx, FRX_ERR_SHAPE, "hidden=%u and intermediate=%u must be multiples of 16", H, I);
   if ((xt != FRX_F32 && xt != FRX_BF16) || (rt != FRX_F32 && rt != FRX_BF16) || (yt != FRX_F32 && yt != FRX_BF16))
     return fail(ctx, FRX_ERR_UNSUPPORTED, "dtype must be FRX_F32 or FRX_BF16");
-  if (act != FRX_ACT_SILU && act != FRX_ACT_GELU_TANH) return fail(ctx, FRX_ERR_UNSUPPORTED, "activation");
+  if (act != FRX_ACT_SILU && act != FRX_ACT_GELU_TANH && act != FRX_ACT_GELU_TANH_GATE)
+    return fail(ctx, FRX_ERR_UNSUPPORTED, "activation");
+  std::vector<const uint32_t *> wu_sub;
+  std::vector<const float *> su_sub;
+  if (gate_only) {
+    wu_sub.assign(w_up, w_up + E);
+    su_sub.assign(s_up, s_up + E);
+    for (uint32_t e = 0; e < E; e++) {
+      if (!wu_sub[e]) wu_sub[e] = w_gate[e];
+      if (!su_sub[e]) su_sub[e] = s_gate[e];
+    }
+    w_up = wu_sub.data();
+    s_up = su_sub.data();
+  }
   for (uint32_t e = 0; e < E; e++)
     if (!w_gate[e] || !s_gate[e] || !w_up[e] || !s_up[e] || !w_down[e] || !s_down[e])
       return fail(ctx, FRX_ERR_SHAPE, "null weight pointer for expert %u", e);
@@ -393,7 +542,7 @@ frx_status frx_moe_ternary_ffn(
     lora.scaling = ctx->lora_scaling;
   }
   hipError_t e = frx::launch_moe(x, xt == FRX_BF16, router_eh, rt == FRX_BF16, w_gate, s_gate, w_up, s_up, w_down,
-                                 s_down, (int)T, (int)H, (int)I, (int)E, (int)top_k, act == FRX_ACT_GELU_TANH, y,
+                                 s_down, (int)T, (int)H, (int)I, (int)E, (int)top_k, (int)act, y,
                                  yt == FRX_BF16, topk_idx, topk_w, ws, ctx->moe_routing, lora, ctx->stream);
   if (e != hipSuccess) return hip_fail(ctx, e, "moe launch");
   return FRX_OK;
@@ -609,18 +758,24 @@ frx_status frx_ternary_linear_blocked(frx_ctx *ctx, const uint32_t *w, const flo
       return st;
     hipError_t e = frx::launch_fill(reinterpret_cast<float *>(ctx->unit_ws), 1.0f, ctx->unit_ws_bytes / 4,
                                     ctx->stream);
+    // wait for the fill: a later call may run on another stream (frx_set_stream)
+    // and must not read the scales before they are written
+    if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
     if (e != hipSuccess) return hip_fail(ctx, e, "unit scale fill");
   }
   float *xs = reinterpret_cast<float *>(ctx->blk_ws);
   const float *ones = reinterpret_cast<const float *>(ctx->unit_ws);
+  Staged sg;  // xs and ones are aligned workspaces: at most y is staged
+  if ((st = stage_linear(ctx, xs, FRX_F32, ones, y, yt, M, K, N, &sg)) != FRX_OK) return st;
   hipError_t e = frx::launch_block_prescale(x, xt == FRX_BF16, block_scales, (int)block_size, xs, (int)M, (int)K,
                                             ctx->stream);
   if (e == hipSuccess) {
     if (M <= 16)
-      e = frx::launch_gemv(w, ones, xs, 0, y, yt == FRX_BF16, (int)M, (int)K, (int)N, ctx->stream);
+      e = frx::launch_gemv(w, ones, xs, 0, sg.y, yt == FRX_BF16, (int)M, (int)K, (int)N, ctx->stream);
     else
-      e = frx::launch_gemm(w, ones, xs, 0, y, yt == FRX_BF16, (int)M, (int)K, (int)N, 0, ctx->stream);
+      e = frx::launch_gemm(w, ones, xs, 0, sg.y, yt == FRX_BF16, (int)M, (int)K, (int)N, 0, ctx->stream);
   }
+  if (e == hipSuccess) e = unstage_linear(ctx, sg);
   if (e != hipSuccess) return hip_fail(ctx, e, "column-block linear launch");
   return FRX_OK;
 }
@@ -814,6 +969,52 @@ frx_status frx_quantize_ternary(frx_ctx *ctx, const void *w, frx_dtype wt, uint3
   const hipError_t e =
       frx::launch_quantize(w, wt == FRX_BF16, (int)N, (int)K, (int)rule, packed, scale, ctx->stream);
   if (e != hipSuccess) return hip_fail(ctx, e, "quantise launch");
+  return FRX_OK;
+}
+
+frx_status frx_quantize_ternary_blocked(frx_ctx *ctx, const void *w, frx_dtype wt, size_t n, uint32_t block_size,
+                                        uint32_t *packed, float *scales) {
+  frx_status st = enter(ctx);
+  if (st != FRX_OK) return st;
+  if (n == 0) return FRX_OK;  // the reference returns two empty vectors
+  if (!w || !packed || !scales) return fail(ctx, FRX_ERR_SHAPE, "null pointer argument");
+  if (block_size == 0) return fail(ctx, FRX_ERR_SHAPE, "block_size must be positive");
+  if (wt != FRX_F32 && wt != FRX_BF16) return fail(ctx, FRX_ERR_UNSUPPORTED, "dtype must be FRX_F32 or FRX_BF16");
+  if ((n + block_size - 1) / block_size > 0x7FFFFFFFu || n > ((size_t)1 << 40))
+    return fail(ctx, FRX_ERR_SHAPE, "n=%zu with block_size=%u: too many blocks", n, block_size);
+  const hipError_t e =
+      frx::launch_quantize_flat(w, wt == FRX_BF16, n, block_size, 0, packed, scales, ctx->stream);
+  if (e != hipSuccess) return hip_fail(ctx, e, "blocked quantise launch");
+  return FRX_OK;
+}
+
+frx_status frx_dequantize_ternary_blocked(frx_ctx *ctx, const uint32_t *packed, const float *scales, size_t n,
+                                          uint32_t block_size, float *out) {
+  frx_status st = enter(ctx);
+  if (st != FRX_OK) return st;
+  if (n == 0) return FRX_OK;
+  if (!packed || !scales || !out) return fail(ctx, FRX_ERR_SHAPE, "null pointer argument");
+  if (block_size == 0) return fail(ctx, FRX_ERR_SHAPE, "block_size must be positive");
+  if (n > ((size_t)1 << 40)) return fail(ctx, FRX_ERR_SHAPE, "n=%zu too large", n);
+  const hipError_t e = frx::launch_dequantize(packed, scales, n, block_size, out, ctx->stream);
+  if (e != hipSuccess) return hip_fail(ctx, e, "dequantise launch");
+  return FRX_OK;
+}
+
+frx_status frx_prune_sparse24(frx_ctx *ctx, const void *w, frx_dtype wt, uint32_t N, uint32_t K, int per_row,
+                              uint8_t *patterns, uint8_t *signs, uint32_t *meta, float *scale) {
+  frx_status st = enter(ctx);
+  if (st != FRX_OK) return st;
+  if (!w || !scale) return fail(ctx, FRX_ERR_SHAPE, "null pointer argument");
+  if (!patterns != !signs) return fail(ctx, FRX_ERR_SHAPE, "patterns and signs must both be given or both NULL");
+  if (N == 0 || K == 0) return fail(ctx, FRX_ERR_SHAPE, "empty matrix N=%u K=%u", N, K);
+  if (K % 4 != 0) return fail(ctx, FRX_ERR_SHAPE, "K=%u must be a multiple of 4 for 2:4", K);
+  if (wt != FRX_F32 && wt != FRX_BF16) return fail(ctx, FRX_ERR_UNSUPPORTED, "dtype must be FRX_F32 or FRX_BF16");
+  if (N > 0x7FFFFFFFu || K > 0x7FFFFFF0u || (size_t)N * K > ((size_t)1 << 38))
+    return fail(ctx, FRX_ERR_SHAPE, "N=%u K=%u too large", N, K);
+  const hipError_t e = frx::launch_prune_sparse24(w, wt == FRX_BF16, (int)N, (int)K, per_row != 0, patterns, signs,
+                                                  meta, scale, ctx->stream);
+  if (e != hipSuccess) return hip_fail(ctx, e, "2:4 prune launch");
   return FRX_OK;
 }
 

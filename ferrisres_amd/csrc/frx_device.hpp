@@ -234,11 +234,23 @@ struct XBlock<float> {
 // ternary_moe.rs:204, cpu_block_attn_res.rs:2323; GeLU-tanh,
 // gemma_mapper.rs:2073-2077).
 __device__ __forceinline__ float act_silu(float g) { return g / (1.0f + expf(-g)); }
-// gemma_mapper.rs:2073-2077
-__device__ __forceinline__ float act_gelu_tanh(float x) {
-  const float c = 0.7978845608028654f;  // sqrt(2/pi)
+// GeLU-tanh with the constant c given: 0.5 x (1 + tanh(c (x + 0.044715 x^3))).
+__device__ __forceinline__ float gelu_tanh_c(float x, float c) {
   const float inner = c * (x + 0.044715f * x * x * x);
   return 0.5f * x * (1.0f + tanhf(inner));
+}
+// gemma_mapper.rs:2073-2077: c = (2 / PI).sqrt() evaluated in f32, which is
+// 0x3F4C4229, one ulp below the nearest f32 to sqrt(2/pi).
+__device__ __forceinline__ float act_gelu_tanh(float x) { return gelu_tanh_c(x, __uint_as_float(0x3F4C4229u)); }
+// ternary_moe.rs:196-199: the literal 0.7978845608 (0x3F4C422A).
+__device__ __forceinline__ float act_gelu_tanh_lit(float x) { return gelu_tanh_c(x, 0.7978845608f); }
+
+// Expert activation of the MoE kernels, by frx_activation: 0 silu(g) * u,
+// 1 gelu_tanh(g) * u (the model glue, CpuMoELayer), 2 gelu_tanh(g) alone
+// (TernaryMoELayer::forward with use_gelu, ternary_moe.rs:193-200).
+__device__ __forceinline__ float moe_act(int act, float g, float u) {
+  if (act == 2) return act_gelu_tanh_lit(g);
+  return (act == 1 ? act_gelu_tanh(g) : act_silu(g)) * u;
 }
 
 // Output bias, added to the scaled f32 result as a separate rounding step:

@@ -110,6 +110,12 @@ hipError_t launch_ffn1(const void *x, int xt_bf16, const uint32_t *wg, const flo
 // Per-row ternary quantisation (rule 0: quantize_ternary, 1: the STE rule of
 // BitLinear::forward_ste) of W [N][K] (f32, or bf16 when wt_bf16), K % 16 ==
 // 0: scale [N], packed [N][K/16].
+hipError_t launch_quantize_flat(const void *w, int wt_bf16, size_t n, size_t block, int rule, uint32_t *packed,
+                                float *scale, hipStream_t stream);
+hipError_t launch_dequantize(const uint32_t *packed, const float *scales, size_t n, size_t block, float *out,
+                             hipStream_t stream);
+hipError_t launch_prune_sparse24(const void *w, int wt_bf16, int N, int K, int per_row, uint8_t *patterns,
+                                 uint8_t *signs, uint32_t *meta, float *scale, hipStream_t stream);
 hipError_t launch_quantize(const void *w, int wt_bf16, int N, int K, int rule, uint32_t *packed, float *scale,
                            hipStream_t stream);
 hipError_t launch_sp24_cpu_to_gpu(const uint8_t *patterns, const uint8_t *signs, int N, int K, uint32_t *meta,
@@ -170,7 +176,7 @@ hipError_t launch_moe(const void *x, int xt_bf16, const void *router,
                       const float *const *s_gate, const uint32_t *const *w_up,
                       const float *const *s_up, const uint32_t *const *w_down,
                       const float *const *s_down, int T, int H, int I, int E,
-                      int top_k, int gelu, void *y, int yt_bf16,
+                      int top_k, int act, void *y, int yt_bf16,
                       uint32_t *topk_idx, float *topk_w, const MoeWorkspace &ws,
                       int routing, const MoeLora &lora, hipStream_t stream);
 

@@ -1,8 +1,11 @@
 // frx_moe.hip — MoE ternary expert layer on gfx950.
 //
 // Semantics: the model's GPU-path MoE glue, src/model/cpu_block_attn_res.rs
-// :1148-1184 (= TernaryMoELayer::forward, src/model/ternary_moe.rs:145-223,
-// with per-row scales). The reference runs it as host loops over tokens and
+// :1148-1184, and TernaryMoELayer::forward, src/model/ternary_moe.rs:145-223,
+// with per-row scales. Their routing is the same; their GeLU experts differ
+// (the glue: gelu(g) * u; TernaryMoELayer: gelu(g) alone, ternary_moe.rs:
+// 193-200), selected by the activation code (moe_act). The reference runs it
+// as host loops over tokens and
 // experts with 3 GEMV dispatches per (token, expert); here it is five
 // launches:
 //   1. router_topk   one lane per (token, expert): logits (sequential f32
@@ -13,8 +16,9 @@
 //                    expert-sorted rows, plus the M-tile schedule (tiles
 //                    sized to each expert's tokens).
 //   3. gateup        grouped GEMM over the tile schedule: gathered token rows
-//                    x W_gate[e] and x W_up[e] in one workgroup, SwiGLU (or
-//                    GeLU-tanh) epilogue, h stored as bf16 hi/lo planes.
+//                    x W_gate[e] and x W_up[e] in one workgroup, SwiGLU or
+//                    GeLU-tanh epilogue (moe_act), h stored as bf16 hi/lo
+//                    planes.
 //   4. down          grouped GEMM h x W_down[e] (hi and lo planes in one K
 //                    loop, on separate waves that share the weight tile),
 //                    fp32 rows.
@@ -741,7 +745,7 @@ __global__ __launch_bounds__(256) void moe_gateup_kernel(
     const int *__restrict__ tiles, const int *__restrict__ ntiles,
     const int *__restrict__ counts, const int *__restrict__ offsets,
     const int *__restrict__ perm_token, uint16_t *__restrict__ h_hi,
-    uint16_t *__restrict__ h_lo, int gelu, const float *const *__restrict__ ltbl, int lrank, float lscale,
+    uint16_t *__restrict__ h_lo, int act, const float *const *__restrict__ ltbl, int lrank, float lscale,
     const float *__restrict__ lax) {
   using Core = GemmCore<MOE_BM, MOE_BN, 1, 4, XS, 2>;
   __shared__ __align__(16) uint32_t lds[Core::LDS_DWORDS];
@@ -777,10 +781,7 @@ __global__ __launch_bounds__(256) void moe_gateup_kernel(
         }
       }
       float hv[4];
-      for (int j = 0; j < 4; j++) {
-        const float a = gelu ? act_gelu_tanh(g[j]) : act_silu(g[j]);
-        hv[j] = a * u[j];
-      }
+      for (int j = 0; j < 4; j++) hv[j] = moe_act(act, g[j], u[j]);
       uint32_t hh[4], hl[4];
       for (int j = 0; j < 4; j++) split_bf16(hv[j], hh[j], hl[j]);
       const long o = (long)(row0 + m) * I + n;
@@ -871,7 +872,7 @@ static_assert(MoeGateUpCore::FM == 6 && MoeDownCore::FM == 6, "token blocks per 
 template <int F>
 __device__ __forceinline__ void gateup_tile(uint32_t *lds, const GateUpArgs &args, const uint16_t *x, int T, int H,
                                             int I, int e, int mcount, int row0, const int *perm_token,
-                                            uint16_t *h2, int gelu, const MoeLora &lora, const float *lax) {
+                                            uint16_t *h2, int act, const MoeLora &lora, const float *lax) {
   using Core = MoeGateUpCore;
   const int n0 = blockIdx.x * (MOE_GU_BN / 2), nc = min(MOE_GU_BN / 2, I - n0);
   f32x4 acc[Core::FN][F];
@@ -919,10 +920,7 @@ __device__ __forceinline__ void gateup_tile(uint32_t *lds, const GateUpArgs &arg
       }
       uint32_t hh[4], hl[4];
 #pragma unroll
-      for (int j = 0; j < 4; j++) {
-        const float a = gelu ? act_gelu_tanh(gv[j]) : act_silu(gv[j]);
-        split_bf16(a * uv[j], hh[j], hl[j]);
-      }
+      for (int j = 0; j < 4; j++) split_bf16(moe_act(act, gv[j], uv[j]), hh[j], hl[j]);
       uint16_t *d = h2 + (size_t)(row0 + m) * (2 * (size_t)I) + n0 + 4 * c;
       if (4 * c + 4 <= nc) {
         *reinterpret_cast<u32x2 *>(d) = (u32x2){hh[0] | (hh[1] << 16), hh[2] | (hh[3] << 16)};
@@ -943,15 +941,15 @@ __global__ __launch_bounds__(256) void moe_gateup3_kernel(
     const GateUpArgs args, const uint16_t *__restrict__ x, int T, int H, int I,
     const int *__restrict__ tiles, const int *__restrict__ ntiles,
     const int *__restrict__ offsets, const int *__restrict__ perm_token,
-    uint16_t *__restrict__ h2, int gelu, const MoeLora lora, const float *__restrict__ lax) {
+    uint16_t *__restrict__ h2, int act, const MoeLora lora, const float *__restrict__ lax) {
   extern __shared__ __align__(16) uint32_t lds[];
   const int tile = blockIdx.y;
   if (tile >= *ntiles) return;  // whole workgroup
   const int e = tiles[4 * tile], row0 = offsets[e] + tiles[4 * tile + 1];
   const int mcount = tiles[4 * tile + 2], f = tiles[4 * tile + 3];
-  if (f <= 4) gateup_tile<4>(lds, args, x, T, H, I, e, mcount, row0, perm_token, h2, gelu, lora, lax);
-  else if (f == 5) gateup_tile<5>(lds, args, x, T, H, I, e, mcount, row0, perm_token, h2, gelu, lora, lax);
-  else gateup_tile<6>(lds, args, x, T, H, I, e, mcount, row0, perm_token, h2, gelu, lora, lax);
+  if (f <= 4) gateup_tile<4>(lds, args, x, T, H, I, e, mcount, row0, perm_token, h2, act, lora, lax);
+  else if (f == 5) gateup_tile<5>(lds, args, x, T, H, I, e, mcount, row0, perm_token, h2, act, lora, lax);
+  else gateup_tile<6>(lds, args, x, T, H, I, e, mcount, row0, perm_token, h2, act, lora, lax);
 }
 
 template <int F>
@@ -1058,7 +1056,7 @@ hipError_t launch_moe(const void *x, int xt_bf16, const void *router,
                       const float *const *s_gate, const uint32_t *const *w_up,
                       const float *const *s_up, const uint32_t *const *w_down,
                       const float *const *s_down, int T, int H, int I, int E,
-                      int top_k, int gelu, void *y, int yt_bf16,
+                      int top_k, int act, void *y, int yt_bf16,
                       uint32_t *topk_idx, float *topk_w, const MoeWorkspace &ws,
                       int routing, const MoeLora &lora, hipStream_t stream) {
   const int A = T * top_k;
@@ -1164,7 +1162,7 @@ hipError_t launch_moe(const void *x, int xt_bf16, const void *router,
       return err;
     const dim3 g1((I + MOE_GU_BN / 2 - 1) / (MOE_GU_BN / 2), max_tiles);
     hipLaunchKernelGGL(moe_gateup3_kernel, g1, dim3(256), gu_lds, stream, ga, (const uint16_t *)x, T, H, I,
-                       ws.tiles, ws.ntiles, ws.offsets, ws.perm_token, ws.h_hi, gelu, lora, ws.lora_ax);
+                       ws.tiles, ws.ntiles, ws.offsets, ws.perm_token, ws.h_hi, act, lora, ws.lora_ax);
     if ((err = hipGetLastError()) != hipSuccess) return err;
     if ((err = lora_down_a(ws.h_hi, ws.h_hi + I, 2L * I)) != hipSuccess) return err;
     // two K parts when each is a whole number of 64-column steps: twice the
@@ -1181,11 +1179,11 @@ hipError_t launch_moe(const void *x, int xt_bf16, const void *router,
     dim3 g1((I + MOE_BN - 1) / MOE_BN, max_tiles);
     if (xt_bf16)
       hipLaunchKernelGGL((moe_gateup_kernel<XS_BF16>), g1, dim3(256), 0, stream, ga, x, H, I,
-                         ws.tiles, ws.ntiles, ws.counts, ws.offsets, ws.perm_token, ws.h_hi, ws.h_lo, gelu,
+                         ws.tiles, ws.ntiles, ws.counts, ws.offsets, ws.perm_token, ws.h_hi, ws.h_lo, act,
                          lora.tbl, lora.rank, lora.scaling, (const float *)ws.lora_ax);
     else
       hipLaunchKernelGGL((moe_gateup_kernel<XS_F32>), g1, dim3(256), 0, stream, ga, x, H, I,
-                         ws.tiles, ws.ntiles, ws.counts, ws.offsets, ws.perm_token, ws.h_hi, ws.h_lo, gelu,
+                         ws.tiles, ws.ntiles, ws.counts, ws.offsets, ws.perm_token, ws.h_hi, ws.h_lo, act,
                          lora.tbl, lora.rank, lora.scaling, (const float *)ws.lora_ax);
     if ((err = hipGetLastError()) != hipSuccess) return err;
     if ((err = lora_down_a(ws.h_hi, ws.h_lo, (long)I)) != hipSuccess) return err;

@@ -49,9 +49,19 @@ typedef enum frx_status {
  * the type in C++ as well as C; the library rejects it with a status. */
 typedef enum frx_dtype { FRX_F32 = 0, FRX_BF16 = 1, FRX_DTYPE_RANGE_ = 0x7fffffff } frx_dtype;
 
+/* Expert / FFN activation. FRX_ACT_SILU and FRX_ACT_GELU_TANH gate the up
+ * projection: h = act(g) * u (the dense FFN branch,
+ * src/model/cpu_block_attn_res.rs:2319-2324, the MoE glue :1176-1178 and
+ * CpuMoELayer, src/model/cpu_moe.rs:337-352; GeLU-tanh as
+ * gemma_mapper::gelu_tanh, src/model/gemma_mapper.rs:2073-2077, with
+ * c = sqrt(2/pi) evaluated in f32). FRX_ACT_GELU_TANH_GATE is
+ * TernaryMoELayer::forward's use_gelu branch (src/model/ternary_moe.rs:
+ * 193-200): h = gelu_tanh(g) with the literal c = 0.7978845608 and no up
+ * product; frx_moe_ternary_ffn only. */
 typedef enum frx_activation {
   FRX_ACT_SILU = 0,
   FRX_ACT_GELU_TANH = 1,
+  FRX_ACT_GELU_TANH_GATE = 2,
   FRX_ACT_RANGE_ = 0x7fffffff
 } frx_activation;
 /* How frx_ternary_ffn runs at decode sizes (see frx_set_ffn_mode). */
@@ -96,8 +106,14 @@ const char *frx_version(void);
  *   w     [N][K/16] u32      scale [N] f32
  *   x     [M][K]  xt         y     [M][N] yt
  * M = seq_len, K = in_cols, N = out_rows. Requires K % 16 == 0 (the u32
- * repack of ternary.rs:1317-1328 is row-aligned only then), M, N >= 1.
- * M <= 16 runs the decode GEMV kernel, larger M the MFMA GEMM kernel. */
+ * repack of ternary.rs:1317-1328 is row-aligned only then), M, N >= 1,
+ * N*K/4 bytes of weights below 4 GiB, and pointers aligned to their element
+ * size. M <= 16 runs the decode GEMV kernel, larger M the MFMA GEMM kernel.
+ * The kernels read x and scale and write y 16 bytes at a time: a sub-slice
+ * at another offset is copied into an aligned context workspace on the
+ * stream (x and scale before the launch, y back after it; allocated on the
+ * first such call at a larger size, which must not be under graph
+ * capture). */
 frx_status frx_ternary_linear(frx_ctx *ctx, const uint32_t *w,
                               const float *scale, const void *x, frx_dtype xt,
                               void *y, frx_dtype yt, uint32_t M, uint32_t K,
@@ -169,18 +185,23 @@ frx_status frx_sparse24_ternary_linear(frx_ctx *ctx, const uint32_t *meta,
 
 /* ---- MoE ternary expert layer -----------------------------------------------
  * Replaces the GPU-path MoE glue of the model (router, softmax, stable top-k,
- * per-expert ternary SwiGLU FFN, weighted sum; src/model/
- * cpu_block_attn_res.rs:1148-1184 and :2284-2316), whose semantics are
- * TernaryMoELayer::forward (src/model/ternary_moe.rs:145-223) with per-row
- * scales. Routing is done on the device (router GEMV, softmax, stable sort,
- * per-expert histogram and scan, token permutation); the experts run as
- * grouped ternary GEMMs.
+ * per-expert ternary FFN, weighted sum; src/model/cpu_block_attn_res.rs:
+ * 1148-1184 and :2284-2316) and TernaryMoELayer::forward
+ * (src/model/ternary_moe.rs:145-223), with per-row scales. Their routing is
+ * the same; their experts differ only for GeLU: the glue computes
+ * gelu(g) * u (act = FRX_ACT_GELU_TANH), TernaryMoELayer gelu(g) alone
+ * (act = FRX_ACT_GELU_TANH_GATE). With SiLU both are silu(g) * u. Routing
+ * is done on the device (router GEMV, softmax, stable sort, per-expert
+ * histogram and scan, token permutation); the experts run as grouped ternary
+ * GEMMs.
  *   x [T][H] xt; router [E][H] rt (row e = expert e, ternary_moe.rs:157)
  *   w_gate[e], w_up[e]: [I][H/16] u32, s_gate[e], s_up[e]: [I] f32
  *   w_down[e]: [H][I/16] u32, s_down[e]: [H] f32   (device pointers; the
  *   pointer arrays themselves are host arrays of length E)
  *   y [T][H] yt; topk_idx [T][top_k] u32 and topk_w [T][top_k] f32 (device,
  *   may be NULL).
+ * With FRX_ACT_GELU_TANH_GATE the up projection is not used: w_up and s_up
+ * may be NULL (the arrays or their entries).
  * Requires H % 16 == 0, I % 16 == 0, 1 <= top_k <= E <= 64.
  * Workspace is allocated on the context on first use and grown on the first
  * call at a larger size (not under graph capture); a replaced workspace is
@@ -292,11 +313,15 @@ frx_status frx_set_moe_routing(frx_ctx *ctx, frx_moe_routing routing);
  * f32, row-major: A_gate, A_up [rank][H]; B_gate, B_up [I][rank]; A_down
  * [rank][I]; B_down [H][rank]. Each member below is a host array of
  * `experts` device pointers (the array itself may be NULL: no adapter of
- * that projection). The pointer arrays are copied by this call (which first
- * waits for the context stream); the matrices are read by every later
+ * that projection). The pointer arrays are copied by this call
+ * (synchronously); the matrices are read by every later
  * frx_moe_ternary_ffn on the context, whose expert count must then equal
  * `experts` (FRX_ERR_SHAPE otherwise), until frx_set_moe_lora(ctx, NULL, 0)
- * removes them. 1 <= rank <= 64, 1 <= experts <= 64. Both routing modes. The
+ * removes them. Each call builds a new device table of the pointers and
+ * retires the previous one (frx_release_retired frees it): launches already
+ * enqueued and graphs captured earlier keep the adapters and rank they were
+ * captured with, and read those matrices on every replay, so a caller that
+ * changes, removes or frees adapters must recapture such graphs. 1 <= rank <= 64, 1 <= experts <= 64. Both routing modes. The
  * low-rank sums run in another order than the reference's sequential f32
  * loops (outputs within 1e-3). */
 typedef struct frx_moe_lora {
@@ -310,6 +335,21 @@ typedef struct frx_moe_lora {
   const float *const *b_down;
 } frx_moe_lora;
 frx_status frx_set_moe_lora(frx_ctx *ctx, const frx_moe_lora *lora, uint32_t experts);
+
+/* Device memory held by the context's workspaces (no counterpart in the
+ * reference, whose wgpu buffers are allocated per call): live_bytes in the
+ * current workspaces, retired_bytes in workspaces replaced by larger ones
+ * (kept because graphs captured at the smaller size still address them),
+ * allocations = device allocations made so far. Workspaces grow by at
+ * least 1.5x, so rising sizes make O(log) allocations and the retired bytes
+ * of a workspace stay below twice its current size. Any pointer may be
+ * NULL. */
+frx_status frx_workspace_stats(frx_ctx *ctx, size_t *live_bytes, size_t *retired_bytes,
+                               uint32_t *allocations);
+/* Frees the retired workspaces (and LoRA tables replaced by
+ * frx_set_moe_lora) after waiting for the context stream. Only for callers
+ * that know no captured graph still uses them. */
+frx_status frx_release_retired(frx_ctx *ctx);
 
 /* Forced failure, for testing a caller's fallback path (no counterpart in
  * the reference; its callers fall back to the CPU on any FerrisResError,
@@ -383,6 +423,51 @@ typedef enum frx_quant_rule {
 } frx_quant_rule;
 frx_status frx_quantize_ternary(frx_ctx *ctx, const void *w, frx_dtype wt, uint32_t N, uint32_t K,
                                 frx_quant_rule rule, uint32_t *packed, float *scale);
+
+/* Replaces quantize_ternary_blocked (src/model/ternary.rs:76-110): the flat
+ * n-value tensor w is cut into blocks of block_size values (the last one
+ * shorter when block_size does not divide n) and each block is quantised as
+ * quantize_ternary with its own alpha (FRX_QUANT_ABSMEAN above; sum|w|
+ * left to right in f32 within the block, len as f32), so alpha and every
+ * code are bit-identical to the reference.
+ *   w [n] f32 or bf16 (device); packed [ceil(n/16)] u32: the codes of
+ *   pack_ternary then pack_ternary_u32 over the flat tensor (zero padding
+ *   bits past n); scales [ceil(n/block_size)] f32.
+ * n = 0 writes nothing (the reference returns empty vectors). A row-aligned
+ * matrix view needs block_size % 16 == 0 and block_size dividing n; then
+ * this equals frx_quantize_ternary on [n/block_size][block_size]. Stream-
+ * ordered, no allocation. */
+frx_status frx_quantize_ternary_blocked(frx_ctx *ctx, const void *w, frx_dtype wt, size_t n,
+                                        uint32_t block_size, uint32_t *packed, float *scales);
+/* Replaces dequantize_ternary_blocked (src/model/ternary.rs:113-128):
+ * out[i] = scales[i / block_size] * dec(code i) for i < n, over the flat
+ * packed codes of frx_quantize_ternary_blocked (one f32 product each: exact;
+ * codes 0b01 and 0b11 give alpha * 0). packed [ceil(n/16)] u32, scales
+ * [ceil(n/block_size)] f32, out [n] f32 (device). */
+frx_status frx_dequantize_ternary_blocked(frx_ctx *ctx, const uint32_t *packed, const float *scales,
+                                          size_t n, uint32_t block_size, float *out);
+/* Replaces prune_fp32_to_sparse_ternary (src/model/sparse_ternary.rs:598-663),
+ * the producer of 2:4 expert weights (quantized_model.rs:191,
+ * expert_loader.rs:380-390): per group of 4 values the two largest |w|
+ * (ties to the lower position, as the reference's stable sort) become
+ * +-1, the other two 0. Sign bits are packed as the reference packs them:
+ * bit 0 from the larger |w|, bit 1 from the second, and read back as the
+ * signs of the lower and higher positions (so a group whose larger |w| sits
+ * at the higher position with the two signs different decodes with them
+ * exchanged, exactly as the reference's SparseTernaryMatrix does).
+ *   w [N][K] f32 or bf16 (device), K % 4 == 0.
+ *   patterns [ceil(N*K/8)] u8, signs [ceil(N*K/16)] u8: the CPU layout
+ *     SparseTernaryMatrix holds (both NULL: not written);
+ *   meta [N][ceil(K/24)] u32: the same matrix in the GPU 5-bit layout, as
+ *     frx_sparse24_cpu_to_gpu would transcode it (NULL: not written);
+ *   scale [N] f32: per_row = 0 gives the reference's tensor scale
+ *     (sum|w| / (N*K)) / 0.7978845608 (1 when the sum is not > 0), summed
+ *     left to right over the whole tensor on one lane, on every row;
+ *     per_row != 0 takes each row as its own tensor.
+ * Stream-ordered, no allocation. */
+frx_status frx_prune_sparse24(frx_ctx *ctx, const void *w, frx_dtype wt, uint32_t N, uint32_t K,
+                              int per_row, uint8_t *patterns, uint8_t *signs, uint32_t *meta,
+                              float *scale);
 
 /* Releases a buffer returned by frx_upload_ternary / frx_upload_stm. */
 frx_status frx_free(frx_ctx *ctx, void *dev_ptr);

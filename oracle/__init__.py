@@ -54,6 +54,9 @@ def lib():
                                                ctypes.c_int, ctypes.c_int, _vp, _vp, _vp]),
             "frxo_bench_ternary_matmul": (None, [_vp, _vp, _f, _sz, _sz, _sz, _vp]),
             "frxo_quantize_ternary": (_f, [_vp, _sz, _vp]),
+            "frxo_quantize_ternary_blocked": (None, [_vp, _sz, _sz, _vp, _vp]),
+            "frxo_dequantize_ternary_blocked": (_sz, [_vp, _sz, _vp, _sz, _sz, _vp]),
+            "frxo_prune_sparse24": (_f, [_vp, _sz, _sz, _vp, _vp]),
             "frxo_quantize_ste": (_f, [_vp, _sz, _vp]),
             "frxo_pack_sparse24_gpu": (ctypes.c_int, [_vp, _sz, _sz, _vp, _vp]),
             "frxo_sparse24_gpu_matmul": (None, [_vp, _vp, _vp, _sz, _sz, _sz, _vp]),
@@ -70,6 +73,7 @@ def lib():
                                              ctypes.c_int, ctypes.c_int, _sz, _f, _vp, _vp, _vp, _vp, _vp, _vp,
                                              _vp, _vp, _vp]),
             "frxo_gelu_tanh": (_f, [_f]),
+            "frxo_gelu_tanh_lit": (_f, [_f]),
             "frxo_ffn_forward": (None, [_vp, _sz, _sz, _sz, _vp, _vp, _vp, _vp, _vp, _vp,
                                         ctypes.c_int, _vp]),
             "frxo_time_packed_parallel": (ctypes.c_double, [_vp, _f, _vp, _sz, _sz, ctypes.c_int,
@@ -199,6 +203,36 @@ def quantize_ternary(weights):
     return out, np.float32(alpha)
 
 
+def quantize_ternary_blocked(weights, block_size):
+    """quantize_ternary_blocked (ternary.rs:76-110): (codes i8 [n], scales
+    f32 [ceil(n / block_size)])."""
+    w = _c(weights, np.float32).ravel()
+    out = np.zeros(w.size, np.int8)
+    scales = np.zeros(-(-w.size // block_size), np.float32)
+    lib().frxo_quantize_ternary_blocked(_p(w), w.size, block_size, _p(out), _p(scales))
+    return out, scales
+
+
+def dequantize_ternary_blocked(ternary, scales, block_size):
+    """dequantize_ternary_blocked (ternary.rs:113-128)."""
+    t = _c(ternary, np.int8).ravel()
+    sc = _c(scales, np.float32).ravel()
+    out = np.zeros(t.size, np.float32)
+    n = lib().frxo_dequantize_ternary_blocked(_p(t), t.size, _p(sc), sc.size, block_size, _p(out))
+    return out[:n]
+
+
+def prune_sparse24(weights, rows, cols):
+    """prune_fp32_to_sparse_ternary (sparse_ternary.rs:598-663): CPU-layout
+    (patterns, signs, scale)."""
+    w = _c(weights, np.float32).ravel()
+    ng = rows * cols // 4
+    pats = np.zeros((ng + 1) // 2, np.uint8)
+    signs = np.zeros((ng + 3) // 4, np.uint8)
+    scale = lib().frxo_prune_sparse24(_p(w), rows, cols, _p(pats), _p(signs))
+    return pats, signs, np.float32(scale)
+
+
 def quantize_ste(weights):
     """BitLinear::forward_ste's quantisation (shadow_weights.rs:203-231):
     (codes i8, alpha)."""
@@ -324,7 +358,11 @@ def moe_route_cpu_layer(x, router_he, top_k):
 
 
 def moe_forward(x, router, w_gate, s_gate, w_up, s_up, w_down, s_down, top_k, gelu=False, routing=0):
-    """Expert weights: lists of u32 [rows][cols/16] arrays and f32 scale arrays."""
+    """Expert weights: lists of u32 [rows][cols/16] arrays and f32 scale arrays.
+    gelu: 0 (False) silu(g)*u, 1 (True) gelu_tanh(g)*u, 2 TernaryMoELayer's
+    gelu_tanh(g) without the up projection (w_up / s_up may then be None)."""
+    if int(gelu) == 2 and w_up is None:
+        w_up, s_up = w_gate, s_gate  # not read
     xx = _c(x, np.float32)
     r = _c(router, np.float32)
     T, H = xx.shape
@@ -407,6 +445,10 @@ def ffn_forward(x, w_gate, s_gate, w_up, s_up, w_down, s_down, gelu=False):
 
 def gelu_tanh(x):
     return lib().frxo_gelu_tanh(float(x))
+
+
+def gelu_tanh_lit(x):
+    return lib().frxo_gelu_tanh_lit(float(x))
 
 
 def time_packed_parallel(packed, scale, inp, out_rows, in_cols, threads, reps, pct=None):

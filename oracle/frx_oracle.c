@@ -433,6 +433,48 @@ float frxo_quantize_ternary(const float *weights, size_t n, int8_t *out) {
 }
 
 /*
+ * ternary.rs:76-110 quantize_ternary_blocked: blocks of block_size values
+ * (the last one shorter when block_size does not divide n), each quantised
+ * as quantize_ternary with its own alpha = (sum|block| / len) / ABSMEAN_NORM
+ * (1.0 when the sum is not > 0); scales[b] receives block b's alpha, out the
+ * codes in order. Pinned by its reduction to frxo_quantize_ternary on each
+ * block (itself pinned by KATs and float64) and by the round trip of
+ * dequantize below.
+ */
+void frxo_quantize_ternary_blocked(const float *weights, size_t n, size_t block_size, int8_t *out,
+                                   float *scales) {
+  size_t nb = (n + block_size - 1) / block_size;
+  for (size_t b = 0; b < nb; b++) {
+    size_t start = b * block_size, end = start + block_size < n ? start + block_size : n;
+    float sum_abs = 0.0f;
+    for (size_t i = start; i < end; i++) sum_abs += fabsf(weights[i]);
+    float alpha = sum_abs > 0.0f ? (sum_abs / (float)(end - start)) / ABSMEAN_NORM : 1.0f;
+    scales[b] = alpha;
+    float inv = 1.0f / alpha;
+    for (size_t i = start; i < end; i++) {
+      int32_t r = rust_f32_to_i32(roundf(weights[i] * inv));
+      out[i] = (int8_t)(r < -1 ? -1 : r > 1 ? 1 : r);
+    }
+  }
+}
+
+/*
+ * ternary.rs:113-128 dequantize_ternary_blocked: for each of the n_scales
+ * blocks, out[i] = alpha * (ternary[i] as f32) over the block's range (the
+ * output ends with the last scale's block). Returns the number of values
+ * written. Pinned by closed form: alpha * {-1, 0, +1} is exact.
+ */
+size_t frxo_dequantize_ternary_blocked(const int8_t *ternary, size_t n, const float *scales, size_t n_scales,
+                                       size_t block_size, float *out) {
+  size_t w = 0;
+  for (size_t b = 0; b < n_scales; b++) {
+    size_t start = b * block_size, end = start + block_size < n ? start + block_size : n;
+    for (size_t i = start; i < end; i++) out[w++] = scales[b] * (float)ternary[i];
+  }
+  return w;
+}
+
+/*
  * shadow_weights.rs:203-231 BitLinear::forward_ste, the on-the-fly
  * quantisation: alpha = sum|w| / n (left-to-right f32 sum), then per value
  * normalized = w / alpha; +1 if > 0.5, -1 if < -0.5, else 0; all 0 when
@@ -606,6 +648,59 @@ void frxo_sparse24_cpu_from_ternary(const int8_t *ternary, size_t rows,
   }
 }
 
+/*
+ * sparse_ternary.rs:598-663 prune_fp32_to_sparse_ternary (CPU layout): per
+ * group of 4 f32 values, the two largest |v| by Rust's stable sort_by with
+ * b.abs().partial_cmp(a.abs()).unwrap_or(Equal). On 4 elements that sort is
+ * an insertion sort (Rust's merge sort below its insertion threshold, from
+ * 1.75 on): an element moves left past its neighbour only while its |v| is
+ * strictly greater, so ties keep the lower position and a NaN moves past
+ * nothing and lets nothing past it. Positions are then ordered (p0 < p1) for
+ * the pattern, but the sign bits are taken in magnitude order: bit 0 =
+ * (val0 >= 0) of the LARGEST |v|, bit 1 = (val1 >= 0) of the second, exactly
+ * as the reference packs them (:642-644). Decoding reads bit 0 as the sign
+ * of the lower position, so a group whose larger |v| sits at the higher
+ * position and whose two signs differ decodes with the signs exchanged; this
+ * restatement keeps that. NaN >= 0 is false (sign -1); -0.0 >= 0 is true.
+ * scale = (sum|w| / n) / ABSMEAN_NORM with sum|w| left to right in f32 over
+ * all rows*cols values, 1.0 when the sum is not > 0. cols % 4 == 0.
+ * Pinned by the KAT sparse_ternary.rs:523-544 (tests/golden), brute force of
+ * the kept positions (top-2 by |v|, lower index on ties) and of the absmean
+ * scale in float64. The exchanged-sign case is covered by no reference
+ * fixture (parity unpinned for it beyond this reading of :626-644).
+ */
+float frxo_prune_sparse24(const float *weights, size_t rows, size_t cols, uint8_t *patterns,
+                          uint8_t *signs) {
+  size_t ng = rows * cols / 4;
+  memset(patterns, 0, (ng + 1) / 2);
+  memset(signs, 0, (ng + 3) / 4);
+  for (size_t g = 0; g < ng; g++) {
+    const float *v = weights + g * 4;
+    int idx[4] = {0, 1, 2, 3};
+    for (int i = 1; i < 4; i++) {
+      int cur = idx[i], j = i;
+      while (j > 0 && fabsf(v[cur]) > fabsf(v[idx[j - 1]])) {
+        idx[j] = idx[j - 1];
+        j--;
+      }
+      idx[j] = cur;
+    }
+    int pos0 = idx[0], pos1 = idx[1];
+    float val0 = v[pos0], val1 = v[pos1];
+    int p0 = pos0 < pos1 ? pos0 : pos1, p1 = pos0 < pos1 ? pos1 : pos0;
+    int pat = find_pattern(p0, p1);
+    if (g % 2 == 0)
+      patterns[g / 2] |= (uint8_t)(pat & 7);
+    else
+      patterns[g / 2] |= (uint8_t)((pat & 7) << 4);
+    uint8_t s0 = val0 >= 0.0f ? 1 : 0, s1 = val1 >= 0.0f ? 1 : 0;
+    signs[g / 4] |= (uint8_t)((s0 | (s1 << 1)) << ((g % 4) * 2));
+  }
+  float sum_abs = 0.0f;
+  for (size_t i = 0; i < rows * cols; i++) sum_abs += fabsf(weights[i]);
+  return sum_abs > 0.0f ? (sum_abs / (float)(rows * cols)) / ABSMEAN_NORM : 1.0f;
+}
+
 /* sparse_ternary.rs:159-190 to_ternary (pattern > 5 falls back to 0). */
 void frxo_sparse24_cpu_to_ternary(const uint8_t *patterns,
                                   const uint8_t *signs, size_t rows,
@@ -669,6 +764,29 @@ float frxo_gelu_tanh(float x) {
   t = t * x;
   float inner = c * (x + t);
   return (0.5f * x) * (1.0f + tanhf(inner));
+}
+
+/*
+ * The GeLU of TernaryMoELayer::forward, src/model/ternary_moe.rs:196-199:
+ * tanh_arg = 0.7978845608 * (x + 0.044715 * x * x * x) with the f32 literal
+ * 0.7978845608 (one ulp above the f32 sqrt(2/pi) of frxo_gelu_tanh), then
+ * 0.5 * x * (1.0 + tanh_arg.tanh()), each operation rounded to f32 left to
+ * right as Rust evaluates it.
+ */
+float frxo_gelu_tanh_lit(float x) {
+  float t = 0.044715f * x;
+  t = t * x;
+  t = t * x;
+  float inner = 0.7978845608f * (x + t);
+  return (0.5f * x) * (1.0f + tanhf(inner));
+}
+
+/* Expert activation by code: 0 silu(g) * u, 1 gelu_tanh(g) * u,
+ * 2 gelu_tanh_lit(g) (no up product). */
+static float moe_act(int act, float g, float u) {
+  if (act == 2) return frxo_gelu_tanh_lit(g);
+  float a = act == 1 ? frxo_gelu_tanh(g) : g / (1.0f + expf(-g));
+  return a * u;
 }
 
 /*
@@ -776,15 +894,18 @@ void frxo_moe_route_cpu_layer(const float *x, const float *router_he, size_t tok
 }
 
 /*
- * MoE forward of the GPU-path glue, cpu_block_attn_res.rs:1148-1184, which is
- * TernaryMoELayer::forward (ternary_moe.rs:145-223) with per-row scales:
+ * MoE forward of the GPU-path glue, cpu_block_attn_res.rs:1148-1184, and of
+ * TernaryMoELayer::forward (ternary_moe.rs:145-223), with per-row scales:
  * per token, route (above), then for each selected expert in sorted order:
- * g = W_gate x, u = W_up x (u32 matmul), h = act(g) * u with act = SiLU
- * g/(1+exp(-g)) or gelu_tanh, d = W_down h, out += w_k * d (out starts at
- * 0.0). Pinned by: the decomposition MoE = sum_k w_k FFN_e(x) where each
- * matmul is the pinned u32 matmul, a float64 restatement on tiny shapes,
- * and the reference's shape / non-zero / GeLU != SwiGLU tests
- * (ternary_moe.rs:311-443).
+ * g = W_gate x, u = W_up x (u32 matmul), h by the activation code use_gelu:
+ *   0: silu(g) * u, silu = g / (1 + exp(-g))  (both; ternary_moe.rs:202-204)
+ *   1: gelu_tanh(g) * u                       (the glue, :1176-1178)
+ *   2: gelu_tanh_lit(g), no up projection      (TernaryMoELayer, :193-200;
+ *      w_up / s_up are not read and may be NULL)
+ * then d = W_down h, out += w_k * d (out starts at 0.0). Pinned by: the
+ * decomposition MoE = sum_k w_k FFN_e(x) where each matmul is the pinned u32
+ * matmul, a float64 restatement on tiny shapes, and the reference's shape /
+ * non-zero / GeLU != SwiGLU tests (ternary_moe.rs:311-443).
  */
 /* routing 0: TernaryMoELayer / GPU glue; 1: CpuMoELayer (router [H][E],
  * frxo_moe_route_cpu_layer, experts with |w| < 1e-8 skipped as
@@ -871,13 +992,17 @@ void frxo_moe_forward_lora(const float *x, const float *router, const uint32_t *
         frxo_lora_forward(a_gate[e], b_gate[e], rank, hidden, inter, scaling, xr, l);
         for (size_t j = 0; j < inter; j++) g[j] += l[j];
       }
-      for (size_t j = 0; j < inter; j++) g[j] = use_gelu ? frxo_gelu_tanh(g[j]) : g[j] / (1.0f + expf(-g[j]));
-      frxo_ternary_matmul_u32(w_up[e], s_up[e], xr, 1, hidden, inter, u);
-      if (a_up && a_up[e] && b_up[e]) {
-        frxo_lora_forward(a_up[e], b_up[e], rank, hidden, inter, scaling, xr, l);
-        for (size_t j = 0; j < inter; j++) u[j] += l[j];
+      if (use_gelu == 2) {
+        for (size_t j = 0; j < inter; j++) g[j] = frxo_gelu_tanh_lit(g[j]);
+      } else {
+        for (size_t j = 0; j < inter; j++) g[j] = use_gelu ? frxo_gelu_tanh(g[j]) : g[j] / (1.0f + expf(-g[j]));
+        frxo_ternary_matmul_u32(w_up[e], s_up[e], xr, 1, hidden, inter, u);
+        if (a_up && a_up[e] && b_up[e]) {
+          frxo_lora_forward(a_up[e], b_up[e], rank, hidden, inter, scaling, xr, l);
+          for (size_t j = 0; j < inter; j++) u[j] += l[j];
+        }
+        for (size_t j = 0; j < inter; j++) g[j] = g[j] * u[j];
       }
-      for (size_t j = 0; j < inter; j++) g[j] = g[j] * u[j];
       frxo_ternary_matmul_u32(w_down[e], s_down[e], g, 1, inter, hidden, d);
       if (a_down && a_down[e] && b_down[e]) {
         frxo_lora_forward(a_down[e], b_down[e], rank, inter, hidden, scaling, g, l);
@@ -917,11 +1042,8 @@ void frxo_moe_forward_routed(const float *x, const float *router,
       float w = topk_w[t * top_k + i];
       if (routing == 1 && fabsf(w) < 1e-8f) continue;
       frxo_ternary_matmul_u32(w_gate[e], s_gate[e], xr, 1, hidden, inter, g);
-      frxo_ternary_matmul_u32(w_up[e], s_up[e], xr, 1, hidden, inter, u);
-      for (size_t j = 0; j < inter; j++) {
-        float a = use_gelu ? frxo_gelu_tanh(g[j]) : g[j] / (1.0f + expf(-g[j]));
-        g[j] = a * u[j];
-      }
+      if (use_gelu != 2) frxo_ternary_matmul_u32(w_up[e], s_up[e], xr, 1, hidden, inter, u);
+      for (size_t j = 0; j < inter; j++) g[j] = moe_act(use_gelu, g[j], use_gelu == 2 ? 0.0f : u[j]);
       frxo_ternary_matmul_u32(w_down[e], s_down[e], g, 1, inter, hidden, d);
       for (size_t j = 0; j < hidden; j++) orow[j] += w * d[j];
     }

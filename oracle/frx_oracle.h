@@ -129,6 +129,13 @@ void frxo_moe_forward_lora(const float *x, const float *router, const uint32_t *
                            const float *const *a_up, const float *const *b_up, const float *const *a_down,
                            const float *const *b_down, float *out, uint32_t *topk_idx, float *topk_w);
 float frxo_gelu_tanh(float x);
+float frxo_prune_sparse24(const float *weights, size_t rows, size_t cols, uint8_t *patterns,
+                          uint8_t *signs);
+void frxo_quantize_ternary_blocked(const float *weights, size_t n, size_t block_size, int8_t *out,
+                                   float *scales);
+size_t frxo_dequantize_ternary_blocked(const int8_t *ternary, size_t n, const float *scales, size_t n_scales,
+                                       size_t block_size, float *out);
+float frxo_gelu_tanh_lit(float x);
 void frxo_ffn_forward(const float *x, size_t seq, size_t hidden, size_t inter,
                       const uint32_t *w_gate, const float *s_gate,
                       const uint32_t *w_up, const float *s_up,

@@ -199,7 +199,12 @@ static void check_validation(void) {
   EXPECT(frx_ternary_linear(ctx, w, f, f, FRX_F32, y, FRX_F32, 1, 20, 1) == FRX_ERR_SHAPE);   /* K % 16 */
   EXPECT(frx_ternary_linear(ctx, NULL, f, f, FRX_F32, y, FRX_F32, 1, 16, 1) == FRX_ERR_SHAPE);
   EXPECT(frx_ternary_linear(ctx, w, f, f, (frx_dtype)7, y, FRX_F32, 1, 16, 1) == FRX_ERR_UNSUPPORTED);
-  EXPECT(frx_ternary_linear(ctx, w, f, (const char *)f + 4, FRX_F32, y, FRX_F32, 1, 16, 1) == FRX_ERR_UNSUPPORTED);
+  /* x not aligned to its element size (sub-slices at element offsets are
+   * staged, not rejected) */
+  EXPECT(frx_ternary_linear(ctx, w, f, (const char *)f + 2, FRX_F32, y, FRX_F32, 1, 16, 1) == FRX_ERR_SHAPE);
+  EXPECT(frx_ternary_linear(ctx, w, f, f, FRX_F32, (char *)y + 1, FRX_BF16, 1, 16, 1) == FRX_ERR_SHAPE);
+  /* weights of 4 GiB or more */
+  EXPECT(frx_ternary_linear(ctx, w, f, f, FRX_F32, y, FRX_F32, 1, 0x10000, 0x40000) == FRX_ERR_SHAPE);
   EXPECT(strlen(frx_last_error(ctx)) > 0);
   EXPECT(frx_ternary_linear(ctx, w, f, f, FRX_F32, y, FRX_F32, 0x10000, 0x10000, 1) == FRX_ERR_SHAPE); /* > 2^31 */
   EXPECT(frx_ternary_linear_bias(ctx, w, f, f, f, FRX_F32, y, FRX_F32, 1, 24, 1) == FRX_ERR_SHAPE);
@@ -214,6 +219,22 @@ static void check_validation(void) {
                              FRX_F32, NULL, NULL) == FRX_ERR_SHAPE); /* top_k > E */
   EXPECT(frx_moe_ternary_ffn(ctx, f, FRX_F32, f, FRX_F32, wp, sp, wp, sp, wp, sp, 1, 20, 16, 2, 1, FRX_ACT_SILU, y,
                              FRX_F32, NULL, NULL) == FRX_ERR_SHAPE); /* H % 16 */
+  EXPECT(frx_moe_ternary_ffn(ctx, f, FRX_F32, f, FRX_F32, wp, sp, wp, sp, wp, sp, 1, 16, 16, 2, 1,
+                             (frx_activation)7, y, FRX_F32, NULL, NULL) == FRX_ERR_UNSUPPORTED);
+  EXPECT(frx_ternary_ffn(ctx, f, FRX_F32, w, f, w, f, w, f, 1, 16, 16, FRX_ACT_GELU_TANH_GATE, y, FRX_F32) ==
+         FRX_ERR_UNSUPPORTED); /* the MoE layer's activation only */
+  EXPECT(frx_prune_sparse24(ctx, f, FRX_F32, 1, 6, 0, NULL, NULL, (uint32_t *)y, (float *)y) == FRX_ERR_SHAPE);
+  EXPECT(frx_prune_sparse24(ctx, f, FRX_F32, 1, 8, 0, (uint8_t *)y, NULL, NULL, (float *)y) == FRX_ERR_SHAPE);
+  EXPECT(frx_quantize_ternary_blocked(ctx, f, FRX_F32, 16, 0, (uint32_t *)y, (float *)y) == FRX_ERR_SHAPE);
+  EXPECT(frx_quantize_ternary_blocked(ctx, f, FRX_F32, 0, 0, NULL, NULL) == FRX_OK); /* empty: nothing */
+  EXPECT(frx_dequantize_ternary_blocked(ctx, w, f, 16, 0, (float *)y) == FRX_ERR_SHAPE);
+  {
+    size_t live = 1, retired = 1;
+    uint32_t allocs = 1;
+    EXPECT(frx_workspace_stats(ctx, &live, &retired, &allocs) == FRX_OK);
+    EXPECT(live == 0 && retired == 0 && allocs == 0);
+    EXPECT(frx_release_retired(ctx) == FRX_OK);
+  }
   EXPECT(frx_set_ffn_mode(ctx, (frx_ffn_mode)9) == FRX_ERR_UNSUPPORTED);
   EXPECT(frx_set_moe_routing(ctx, (frx_moe_routing)9) == FRX_ERR_UNSUPPORTED);
   /* forced status: returned before any argument is read */

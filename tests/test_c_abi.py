@@ -63,3 +63,19 @@ def test_api_validation_under_address_sanitizer_on_device():
                        env={**os.environ, **ASAN_ENV})
     assert r.returncode == 0, r.stdout + r.stderr
     assert "asan_check ok (device validation)" in r.stdout
+
+
+@pytest.mark.skipif(shutil.which("g++") is None, reason="needs g++")
+def test_workspace_growth_policy(tmp_path):
+    """The context workspaces grow by at least 1.5x (frx_policy.hpp): rising
+    sizes (prefill M = 17..2048 at I = 11008 among them) make O(log)
+    allocations and retire less than twice the final size."""
+    exe = tmp_path / "policy_check"
+    cmd = ["g++", "-std=c++17", "-O1", "-Wall", "-Wextra", "-Werror", "-I",
+           os.path.join(ROOT, "ferrisres_amd", "csrc"), os.path.join(ROOT, "tests", "c_abi", "policy_check.cpp"),
+           "-o", str(exe)]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    assert r.returncode == 0, r.stderr
+    r = subprocess.run([str(exe)], capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0, r.stdout + r.stderr
+    assert "policy_check ok" in r.stdout

@@ -351,3 +351,75 @@ def test_forced_status_for_caller_fallback(ctx):
     ctx.ternary_linear(wd, sd, xd, y)
     torch.cuda.synchronize()
     assert_close_f32(host(y), oracle.ternary_matmul_u32(w, s, synth.bf16_bits_to_f32(xb), 2, 256, 32))
+
+
+@pytest.mark.parametrize("M", [1, 4, 16, 40])
+@pytest.mark.parametrize("xt,yt", [("bf16", "bf16"), ("f32", "f32")])
+def test_unaligned_subslices_are_staged(ctx, M, xt, yt):
+    """x, scale and y as sub-slices at element offsets that are not 16-byte
+    aligned (a caller slicing a larger tensor, as the reference's &[f32]
+    slices allow): the call stages them through an aligned workspace and
+    gives the aligned call's output bit for bit; the 2:4 GEMM as well."""
+    K, N = 1024, 200
+    t, w, s, xf, xb = _case(f"unaligned/{M}", M, K, N)
+    xe = 1  # one element past a 16-byte boundary
+    if xt == "bf16":
+        big = torch.zeros(M * K + 8, dtype=torch.int16, device="cuda:0")
+        big[xe:xe + M * K] = torch.from_numpy(xb.reshape(-1).view(np.int16)).to("cuda:0")
+        x_un = big[xe:xe + M * K].view(torch.bfloat16).view(M, K)
+    else:
+        big = torch.zeros(M * K + 8, dtype=torch.float32, device="cuda:0")
+        big[xe:xe + M * K] = torch.from_numpy(xf.reshape(-1)).to("cuda:0")
+        x_un = big[xe:xe + M * K].view(M, K)
+    assert x_un.data_ptr() % 16 != 0
+    sbig = torch.zeros(N + 4, dtype=torch.float32, device="cuda:0")
+    sbig[1:1 + N] = dev_f32(s)
+    s_un = sbig[1:1 + N]
+    ydt = torch.bfloat16 if yt == "bf16" else torch.float32
+    ybig = torch.full((M * N + 8,), float("nan"), dtype=ydt, device="cuda:0")
+    y_un = ybig[3:3 + M * N].view(M, N)
+    assert y_un.data_ptr() % 16 != 0 and s_un.data_ptr() % 16 != 0
+    ctx.ternary_linear(dev_u32(w), s_un, x_un, y_un)
+    ref = _run(ctx, w, s, xf, xb, xt, yt)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(host(y_un), host(ref))
+    assert torch.isnan(ybig[:3].float()).all() and torch.isnan(ybig[3 + M * N:].float()).all()
+    # 2:4 on the same sub-slices
+    t24 = synth.sparse24_uniform(f"unaligned24/{M}", "w", N, K)
+    meta = frx.pack_sparse24_gpu(t24)
+    y24 = torch.empty((M, N), dtype=ydt, device="cuda:0")
+    ctx.sparse24_ternary_linear(dev_u32(meta), s_un, x_un, y_un)
+    ctx.sparse24_ternary_linear(dev_u32(meta), dev_f32(s), x_un.contiguous().clone(), y24)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(host(y_un), host(y24))
+
+
+def test_workspaces_grow_geometrically(ctx):
+    """Rising sizes through a workspace-backed entry point (the column-block
+    linear's prescaled activations, M*K*4 bytes) make O(log) allocations,
+    retire less than twice the live bytes, and frx_release_retired frees the
+    retired ones; results stay correct after the release."""
+    c = frx.Context(0)
+    try:
+        K, N, bs = 1024, 64, 128
+        t, w, s, _, _ = _case("ws/grow", 1, K, N)
+        wd = dev_u32(w)
+        bsc = dev_f32(np.linspace(0.5, 1.5, K // bs).astype(np.float32))
+        for M in range(1, 161, 3):
+            x = torch.randn((M, K), dtype=torch.float32, device="cuda:0")
+            y = torch.empty((M, N), dtype=torch.float32, device="cuda:0")
+            c.ternary_linear_blocked(wd, bsc, bs, x, y)
+        torch.cuda.synchronize()
+        live, retired, allocs = c.workspace_stats()
+        assert allocs <= 16, allocs
+        assert retired < 2 * live, (retired, live)
+        c.release_retired()
+        assert c.workspace_stats()[1] == 0
+        xf = synth.normal(5, 160 * K).reshape(160, K)
+        y = torch.empty((160, N), dtype=torch.float32, device="cuda:0")
+        c.ternary_linear_blocked(wd, bsc, bs, dev_f32(xf), y)
+        torch.cuda.synchronize()
+        ref = oracle.ternary_matmul_blocked(t.astype(np.int8), host(bsc), bs, xf, N, K, 160)
+        assert_close_f32(host(y), np.asarray(ref).reshape(160, N))
+    finally:
+        c.close()

@@ -1,6 +1,8 @@
-"""MoE ternary expert layer on the GPU against the oracle (GPU-path MoE glue
-semantics, cpu_block_attn_res.rs:1148-1184 = TernaryMoELayer::forward with
-per-row scales). Routing indices must be bit-exact; outputs within 1e-3."""
+"""MoE ternary expert layer on the GPU against the oracle (the GPU-path MoE
+glue, cpu_block_attn_res.rs:1148-1184, and TernaryMoELayer::forward,
+ternary_moe.rs:145-223, with per-row scales; their GeLU experts differ:
+gelu(g)*u in the glue, gelu(g) alone in TernaryMoELayer). Routing indices
+must be bit-exact; outputs within 1e-3."""
 import numpy as np
 import pytest
 import torch
@@ -32,7 +34,7 @@ def make_moe(name, T, H, I, E):
     return xf, xb, rf, rb, ex
 
 
-def run_gpu(ctx, xf, xb, rf, rb, ex, E, top_k, act, xt="bf16", yt="f32", rt=None):
+def run_gpu(ctx, xf, xb, rf, rb, ex, E, top_k, act, xt="bf16", yt="f32", rt=None, no_up=False):
     T, H = xf.shape
     rt = xt if rt is None else rt
     dw = {k: (dev_u32(v[0]), dev_f32(v[1])) for k, v in ex.items()}
@@ -42,7 +44,8 @@ def run_gpu(ctx, xf, xb, rf, rb, ex, E, top_k, act, xt="bf16", yt="f32", rt=None
     idx = torch.zeros((T, top_k), dtype=torch.int32, device="cuda:0")
     w = torch.zeros((T, top_k), dtype=torch.float32, device="cuda:0")
     g = lambda m, i: [dw[(m, e)][i] for e in range(E)]  # noqa: E731
-    ctx.moe_ternary_ffn(x, r, g("gate", 0), g("gate", 1), g("up", 0), g("up", 1), g("down", 0), g("down", 1),
+    up_w, up_s = (None, None) if no_up else (g("up", 0), g("up", 1))
+    ctx.moe_ternary_ffn(x, r, g("gate", 0), g("gate", 1), up_w, up_s, g("down", 0), g("down", 1),
                         y, top_k=top_k, act=act, topk_idx=idx, topk_w=w)
     torch.cuda.synchronize()
     return y, idx.cpu().numpy().astype(np.uint32), w.cpu().numpy()
@@ -58,12 +61,12 @@ def run_oracle(xf, rf, ex, E, top_k, gelu, tokens=None, routing=0):
 @pytest.mark.parametrize("T,H,I,E,k", [(40, 128, 256, 8, 2), (7, 64, 96, 4, 1), (130, 256, 160, 16, 2),
                                        (64, 128, 128, 6, 3), (50, 320, 192, 5, 2), (300, 192, 448, 3, 2),
                                        (200, 128, 192, 2, 1), (97, 64, 128, 1, 1)])
-@pytest.mark.parametrize("act", [frx.ACT_SILU, frx.ACT_GELU_TANH])
+@pytest.mark.parametrize("act", [frx.ACT_SILU, frx.ACT_GELU_TANH, frx.ACT_GELU_TANH_GATE])
 def test_moe_small_parity(ctx, T, H, I, E, k, act):
     name = f"moe/{T}x{H}x{I}x{E}"
     xf, xb, rf, rb, ex = make_moe(name, T, H, I, E)
     y, idx, w = run_gpu(ctx, xf, xb, rf, rb, ex, E, k, act)
-    ref, ridx, rw = run_oracle(xf, rf, ex, E, k, act == frx.ACT_GELU_TANH)
+    ref, ridx, rw = run_oracle(xf, rf, ex, E, k, act)
     np.testing.assert_array_equal(idx, ridx)
     np.testing.assert_allclose(w, rw, rtol=0, atol=1e-6)
     assert_close_f32(host(y), ref)
@@ -111,6 +114,43 @@ def test_moe_config_shape(ctx):
     ref, _, _ = run_oracle(xf, rf, ex, E, k, False, tokens=tok)
     assert_close_f32(host(y)[tok], ref)
     assert np.isfinite(host(y)).all()
+
+
+def test_moe_gelu_gate_only_config_shape(ctx):
+    """TernaryMoELayer's GeLU experts (h = gelu_tanh(g) with the literal
+    0.7978845608, no up projection; ternary_moe.rs:193-200) at 512 tokens,
+    H=2048, I=5632, 16 experts, top-2, called without up matrices: routing
+    for all tokens bit-exact, 16 sampled tokens in full within 1e-3."""
+    T, H, I, E, k = 512, 2048, 5632, 16, 2
+    xf, xb, rf, rb, ex = make_moe("moe/config", T, H, I, E)
+    y, idx, w = run_gpu(ctx, xf, xb, rf, rb, ex, E, k, frx.ACT_GELU_TANH_GATE, no_up=True)
+    ridx, rw, _ = oracle.moe_route(xf, rf, k)
+    np.testing.assert_array_equal(idx, ridx)
+    np.testing.assert_allclose(w, rw, rtol=0, atol=1e-6)
+    tok = np.array([0, 5, 63, 64, 127, 128, 255, 256, 300, 383, 384, 447, 448, 500, 510, 511])
+    g = lambda m, i: [ex[(m, e)][i] for e in range(E)]  # noqa: E731
+    ref, _, _ = oracle.moe_forward(xf[tok], rf, g("gate", 0), g("gate", 1), None, None, g("down", 0),
+                                   g("down", 1), k, 2)
+    assert_close_f32(host(y)[tok], ref)
+    # the glue's GeLU (gelu(g) * u) is a different function
+    ref_glue, _, _ = run_oracle(xf, rf, ex, E, k, 1, tokens=tok[:2])
+    assert np.abs(ref_glue - ref[:2]).max() > 1e-2 * np.abs(ref[:2]).max()
+
+
+@pytest.mark.parametrize("T,H,I,E,k,xt", [(40, 128, 256, 8, 2, "bf16"), (33, 128, 192, 5, 2, "f32"),
+                                          (50, 320, 192, 5, 2, "bf16")])
+def test_moe_gelu_gate_only_without_up(ctx, T, H, I, E, k, xt):
+    """FRX_ACT_GELU_TANH_GATE with the up arrays NULL equals the call with up
+    matrices given (they are not read), on both grouped-GEMM engines."""
+    xf, xb, rf, rb, ex = make_moe(f"moe/gate_only/{T}x{H}x{I}", T, H, I, E)
+    if xt == "f32":
+        xf, xb = synth.normal(95, T * H).reshape(T, H), None
+    a = run_gpu(ctx, xf, xb, rf, rb, ex, E, k, frx.ACT_GELU_TANH_GATE, xt=xt, no_up=True)
+    b = run_gpu(ctx, xf, xb, rf, rb, ex, E, k, frx.ACT_GELU_TANH_GATE, xt=xt)
+    np.testing.assert_array_equal(host(a[0]), host(b[0]))
+    ref, ridx, _ = run_oracle(xf, rf, ex, E, k, 2)
+    np.testing.assert_array_equal(a[1], ridx)
+    assert_close_f32(host(a[0]), ref)
 
 
 def test_moe_routing_deterministic_and_repeatable(ctx):
@@ -326,3 +366,58 @@ def test_moe_lora_cleared_and_shape_checks(ctx):
                     frx.ACT_SILU)
     finally:
         ctx.set_moe_lora(None)
+
+
+def test_moe_lora_graph_keeps_its_adapters(ctx):
+    """A graph captured with rank-8 adapters keeps reading the table it was
+    captured with after frx_set_moe_lora installs rank-2 adapters (each call
+    builds its own table): its replays equal the eager rank-8 output bit for
+    bit while eager calls between them use rank 2; then the retired tables
+    are released."""
+    T, H, I, E, k = 40, 128, 256, 8, 2
+    name = "moe/lora/graph"
+    xf, xb, rf, rb, ex = make_moe(name, T, H, I, E)
+    h8, d8 = make_lora(name, H, I, E, 8, set())
+    h2, d2 = make_lora(name + "/r2", H, I, E, 2, {("down", 3)})
+    dw = {kk: (dev_u32(v[0]), dev_f32(v[1])) for kk, v in ex.items()}
+    g = lambda m, i: [dw[(m, e)][i] for e in range(E)]  # noqa: E731
+    x, r = dev_bf16(xb), dev_bf16(rb)
+    y8 = torch.empty((T, H), dtype=torch.float32, device="cuda:0")
+    yg = torch.empty((T, H), dtype=torch.float32, device="cuda:0")
+    y2 = torch.empty((T, H), dtype=torch.float32, device="cuda:0")
+    c = frx.Context(0)
+    s = torch.cuda.Stream()
+    c.set_stream(s)
+    try:
+        def call(y):
+            c.moe_ternary_ffn(x, r, g("gate", 0), g("gate", 1), g("up", 0), g("up", 1), g("down", 0),
+                              g("down", 1), y, top_k=k)
+        c.set_moe_lora(8, 2.0, E, **d8)
+        with torch.cuda.stream(s):
+            call(y8)  # workspace exists before capture
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=s):
+            call(yg)
+        torch.cuda.synchronize()
+        c.set_moe_lora(2, 2.0, E, **d2)
+        for rep in range(3):
+            yg.fill_(float("nan"))
+            y2.fill_(float("nan"))
+            with torch.cuda.stream(s):
+                graph.replay()
+                call(y2)
+            torch.cuda.synchronize()
+            np.testing.assert_array_equal(host(yg), host(y8))
+            ex_h = lambda m, i: [ex[(m, e)][i] for e in range(E)]  # noqa: E731
+            ref2, _, _ = oracle.moe_forward_lora(xf, rf, ex_h("gate", 0), ex_h("gate", 1), ex_h("up", 0),
+                                                 ex_h("up", 1), ex_h("down", 0), ex_h("down", 1), k, h2)
+            assert_close_f32(host(y2), ref2)
+        del graph
+        torch.cuda.synchronize()
+        assert c.workspace_stats()[1] > 0  # the rank-8 table is retired, not freed
+        c.release_retired()
+        assert c.workspace_stats()[1] == 0
+    finally:
+        c.set_stream(None)
+        c.close()

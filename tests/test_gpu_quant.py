@@ -124,3 +124,120 @@ def test_quantize_shape_errors(ctx):
     with pytest.raises(frx.FrxError) as ei:
         ctx.quantize_ternary(w, frx.QUANT_ABSMEAN, packed, scale)
     assert ei.value.kind == "Shape"
+
+
+# ---- quantize_ternary_blocked / dequantize_ternary_blocked ------------------
+
+@pytest.mark.parametrize("n,block", [(512, 64), (1000, 64), (37, 8), (4096, 4096), (45056, 1000),
+                                     (11008 * 16, 4096), (100, 128), (17, 1)])
+@pytest.mark.parametrize("wt", ["f32", "bf16"])
+def test_quantize_blocked_matches_oracle(ctx, n, block, wt):
+    """frx_quantize_ternary_blocked = quantize_ternary_blocked
+    (ternary.rs:76-110): scales bit-identical, packed words equal to
+    pack_ternary + pack_ternary_u32 of the oracle's codes (zero padding past
+    n), ragged last blocks included; the device dequantise equals the
+    oracle's dequantize_ternary_blocked bit for bit."""
+    rng = np.random.default_rng(n + block)
+    w = (rng.standard_normal(n) * np.where(np.arange(n) % 700 < 350, 0.02, 1.0)).astype(np.float32)
+    w[::29] = 0.0
+    if wt == "bf16":
+        bits = synth.f32_to_bf16_bits(w)
+        w, w_dev = synth.bf16_bits_to_f32(bits), dev_bf16(bits)
+    else:
+        w_dev = dev_f32(w)
+    q, sc = oracle.quantize_ternary_blocked(w, block)
+    packed = torch.full((-(-n // 16),), -1, dtype=torch.int32, device=DEV)
+    scales = torch.full((sc.size,), float("nan"), dtype=torch.float32, device=DEV)
+    ctx.quantize_ternary_blocked(w_dev, block, packed, scales)
+    out = torch.full((n,), float("nan"), dtype=torch.float32, device=DEV)
+    ctx.dequantize_ternary_blocked(packed, scales, n, block, out)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(host(scales).view(np.uint32), sc.view(np.uint32))
+    ref_words = oracle.pack_ternary_u32(oracle.pack_ternary(q), n)
+    np.testing.assert_array_equal(packed.cpu().numpy().view(np.uint32), ref_words)
+    deq = oracle.dequantize_ternary_blocked(q, sc, block)
+    np.testing.assert_array_equal(host(out).view(np.uint32), deq.view(np.uint32))
+
+
+def test_quantize_blocked_equals_row_view(ctx):
+    """With block_size % 16 == 0 dividing n, the blocked call is
+    frx_quantize_ternary on the [n/block][block] view, word for word."""
+    n, block = 64 * 4096, 4096
+    w = synth.normal(synth.seed_of("quant/blocked_view", "w"), n, std=0.02)
+    w_dev = dev_f32(w)
+    packed = torch.zeros((n // 16,), dtype=torch.int32, device=DEV)
+    scales = torch.zeros((n // block,), dtype=torch.float32, device=DEV)
+    ctx.quantize_ternary_blocked(w_dev, block, packed, scales)
+    p2, s2 = _quantize(ctx, w_dev.view(n // block, block), frx.QUANT_ABSMEAN)
+    np.testing.assert_array_equal(packed.cpu().numpy().view(np.uint32), p2.ravel())
+    np.testing.assert_array_equal(host(scales), s2)
+
+
+# ---- prune_fp32_to_sparse_ternary -----------------------------------------------
+
+def _prune_dev(ctx, w_dev, per_row=False):
+    N, K = w_dev.shape
+    ng = N * K // 4
+    pats = torch.full(((ng + 1) // 2,), 0xEE, dtype=torch.uint8, device=DEV)
+    signs = torch.full(((ng + 3) // 4,), 0xEE, dtype=torch.uint8, device=DEV)
+    meta = torch.full((N, -(-(K // 4) // 6)), -1, dtype=torch.int32, device=DEV)
+    scale = torch.full((N,), float("nan"), dtype=torch.float32, device=DEV)
+    ctx.prune_sparse24(w_dev, scale, pats, signs, meta, per_row=per_row)
+    torch.cuda.synchronize()
+    return pats.cpu().numpy(), signs.cpu().numpy(), meta.cpu().numpy().view(np.uint32), host(scale)
+
+
+@pytest.mark.parametrize("N,K", [(2, 4), (1, 12), (3, 20), (64, 256), (257, 4096), (5, 2052)])
+@pytest.mark.parametrize("wt", ["f32", "bf16"])
+def test_prune_sparse24_matches_oracle(ctx, N, K, wt):
+    """frx_prune_sparse24 = prune_fp32_to_sparse_ternary
+    (sparse_ternary.rs:598-663): CPU-layout patterns and signs bit-exact
+    (odd group counts share no byte between threads), the GPU layout equal
+    to the transcoder's output of the oracle's CPU layout, and the tensor
+    scale bit-identical on every row. Ties, zeros and mixed-sign groups are
+    forced into the input."""
+    rng = np.random.default_rng(N * 7 + K)
+    w = rng.standard_normal(N * K).astype(np.float32) * 0.05
+    w[rng.random(w.size) < 0.1] = 0.0
+    t = rng.random(w.size) < 0.1
+    w[t] = np.float32(0.03) * np.sign(rng.standard_normal(t.sum())).astype(np.float32)
+    if wt == "bf16":
+        bits = synth.f32_to_bf16_bits(w)
+        w, w_dev = synth.bf16_bits_to_f32(bits), dev_bf16(bits.reshape(N, K))
+    else:
+        w_dev = dev_f32(w.reshape(N, K))
+    pats, signs, meta, scale = _prune_dev(ctx, w_dev)
+    rp, rs, rsc = oracle.prune_sparse24(w, N, K)
+    np.testing.assert_array_equal(pats, rp)
+    np.testing.assert_array_equal(signs, rs)
+    np.testing.assert_array_equal(meta.ravel(), frx.sparse24_cpu_to_gpu(rp, rs, N, K).ravel())
+    assert (scale.view(np.uint32) == np.float32(rsc).view(np.uint32)).all()
+    # per-row scales: each row as its own tensor
+    _, _, meta_r, scale_r = _prune_dev(ctx, w_dev, per_row=True)
+    np.testing.assert_array_equal(meta_r, meta)
+    for r in range(N):
+        assert scale_r[r].view(np.uint32) == np.float32(oracle.prune_sparse24(w[r * K:(r + 1) * K], 1, K)[2]).view(
+            np.uint32)
+
+
+def test_prune_sparse24_kat_and_matmul(ctx):
+    """The reference's KAT (sparse_ternary.rs:523-544) through the device
+    prune, and the pruned 2:4 matrix multiplied on the GPU equals the oracle's
+    2:4 matmul of the same pruned matrix (the producer feeds the kernels)."""
+    import json
+    import os
+    kat = json.load(open(os.path.join(os.path.dirname(__file__), "golden", "reference_kats.json")))["prune_fp32"]
+    w = np.array(kat["weights"], np.float32)
+    pats, signs, meta, scale = _prune_dev(ctx, dev_f32(w.reshape(kat["rows"], kat["cols"])))
+    dec = oracle.sparse24_cpu_to_ternary(pats, signs, kat["rows"], kat["cols"])
+    np.testing.assert_array_equal(dec, kat["expected_decompressed"])
+    N, K, M = 256, 1024, 8
+    wf = synth.normal(synth.seed_of("prune/mm", "w"), N * K, std=0.02).reshape(N, K)
+    pats, signs, meta, scale = _prune_dev(ctx, dev_f32(wf), per_row=True)
+    xf, xb = synth.activations("prune/mm", "x", M, K)
+    y = torch.empty((M, N), dtype=torch.float32, device=DEV)
+    from _gpu import dev_u32, assert_close_f32
+    ctx.sparse24_ternary_linear(dev_u32(meta), dev_f32(scale), dev_bf16(xb), y)
+    torch.cuda.synchronize()
+    ref = oracle.sparse24_gpu_matmul(meta, scale, xf, M, K, N)
+    assert_close_f32(host(y), np.asarray(ref).reshape(M, N))

@@ -368,12 +368,16 @@ def _moe_f64(x, r, wg, sg, wu, su, wd, sd, k, gelu):
                 a = 0.5 * g * (1 + np.tanh(np.sqrt(2 / np.pi) * (g + 0.044715 * g ** 3)))
             else:
                 a = g / (1 + np.exp(-g))
-            out[t] += w[t, j] * ((wd[e].astype(np.float64) @ (a * u)) * sd[e])
+            h = a if gelu == 2 else a * u  # 2: TernaryMoELayer's GeLU, no up product
+            out[t] += w[t, j] * ((wd[e].astype(np.float64) @ h) * sd[e])
     return out, idx
 
 
-@pytest.mark.parametrize("gelu", [False, True])
+@pytest.mark.parametrize("gelu", [0, 1, 2])
 def test_moe_forward_vs_f64(gelu):
+    """Activation codes: 0 silu(g)*u, 1 gelu(g)*u (the model glue,
+    cpu_block_attn_res.rs:1176-1178), 2 gelu(g) alone (TernaryMoELayer,
+    ternary_moe.rs:193-200)."""
     rng = np.random.default_rng(21 + gelu)
     T, H, I, E, k = 9, 32, 48, 4, 2
     x = rng.standard_normal((T, H)).astype(np.float32)
@@ -399,6 +403,40 @@ def test_gelu_tanh_vs_f64():
     for v in [-3.0, -0.5, 0.0, 0.3, 2.0]:
         ref = 0.5 * v * (1 + np.tanh(np.sqrt(2 / np.pi) * (v + 0.044715 * v ** 3)))
         assert abs(oracle.gelu_tanh(v) - ref) <= 1e-6 * max(1.0, abs(ref))
+        assert abs(oracle.gelu_tanh_lit(v) - ref) <= 1e-6 * max(1.0, abs(ref))
+
+
+def test_gelu_tanh_special_values():
+    """GeLU-tanh fixed points: gelu(0) = 0 exactly, gelu(x) -> x for large x
+    and -> -0 for large negative x (tanh saturates to +-1 in f32), and
+    gelu(-x) = gelu(x) - x (odd tanh) to f32 rounding."""
+    for f in (oracle.gelu_tanh, oracle.gelu_tanh_lit):
+        assert f(0.0) == 0.0
+        assert f(20.0) == 20.0
+        assert f(-20.0) == 0.0
+        for v in (0.25, 1.0, 1.7, 3.0):
+            assert abs(f(-v) - (f(v) - v)) <= 4e-7 * max(1.0, v)
+
+
+def test_moe_forward_gate_only_does_not_read_up():
+    """Activation 2 (TernaryMoELayer's GeLU) never reads W_up: garbage up
+    matrices give the same output bit for bit as None."""
+    rng = np.random.default_rng(5)
+    T, H, I, E, k = 6, 32, 48, 3, 2
+    x = rng.standard_normal((T, H)).astype(np.float32)
+    r = (rng.standard_normal((E, H)) * 0.3).astype(np.float32)
+    pk = oracle.pack_rows_u32
+    wg = [pk(rng.integers(-1, 2, (I, H)).astype(np.int8)) for _ in range(E)]
+    wd = [pk(rng.integers(-1, 2, (H, I)).astype(np.int8)) for _ in range(E)]
+    sg = [np.full(I, 0.1, np.float32)] * E
+    sd = [np.full(H, 0.1, np.float32)] * E
+    wu = [pk(rng.integers(-1, 2, (I, H)).astype(np.int8)) for _ in range(E)]
+    su = [np.full(I, 7.0, np.float32)] * E
+    a, _, _ = oracle.moe_forward(x, r, wg, sg, None, None, wd, sd, k, 2)
+    b, _, _ = oracle.moe_forward(x, r, wg, sg, wu, su, wd, sd, k, 2)
+    np.testing.assert_array_equal(a, b)
+    c, _, _ = oracle.moe_forward(x, r, wg, sg, wu, su, wd, sd, k, 1)
+    assert np.abs(c - a).max() > 1e-2 * np.abs(a).max()
 
 
 @pytest.mark.parametrize("gelu", [False, True])
@@ -539,3 +577,85 @@ def test_moe_forward_lora_vs_f64_and_without_adapters():
     assert np.abs(out - plain).max() > 1e-2 * np.abs(plain).max()  # the adapters matter here
     none = {**lora, **{n: [None] * E for n in ("a_gate", "b_gate", "a_up", "b_up", "a_down", "b_down")}}
     np.testing.assert_array_equal(oracle.moe_forward_lora(*args, none)[0], plain)
+
+
+@pytest.mark.parametrize("n,block", [(512, 64), (1000, 64), (37, 8), (96, 96), (100, 128), (4096, 1000)])
+def test_quantize_blocked_reduces_to_per_block_quantize(n, block):
+    """quantize_ternary_blocked (ternary.rs:76-110) = quantize_ternary on
+    each block of block_size values (the last block shorter), bit for bit;
+    dequantize_ternary_blocked is alpha * q per block (exact)."""
+    rng = np.random.default_rng(n + block)
+    w = (rng.standard_normal(n) * np.where(np.arange(n) % 300 < 150, 0.02, 1.5)).astype(np.float32)
+    w[::17] = 0.0
+    q, sc = oracle.quantize_ternary_blocked(w, block)
+    assert sc.size == -(-n // block)
+    for b in range(sc.size):
+        qb, ab = oracle.quantize_ternary(w[b * block:(b + 1) * block])
+        np.testing.assert_array_equal(q[b * block:(b + 1) * block], qb)
+        assert sc[b].view(np.uint32) == np.float32(ab).view(np.uint32)
+        seg = w[b * block:(b + 1) * block].astype(np.float64)
+        assert abs(sc[b] - np.abs(seg).mean() / 0.7978845608) <= 1e-5 * sc[b]
+    r = oracle.dequantize_ternary_blocked(q, sc, block)
+    np.testing.assert_array_equal(r, np.repeat(sc, block)[:n] * q.astype(np.float32))
+    # an all-zero block takes alpha = 1 and codes 0
+    z = np.zeros(2 * block, np.float32)
+    z[block:] = 1.0
+    qz, sz = oracle.quantize_ternary_blocked(z, block)
+    assert sz[0] == 1.0 and (qz[:block] == 0).all()
+
+
+def _prune_bruteforce(w, rows, cols):
+    """Kept positions and magnitude-ordered values of each group: the top 2
+    by |v|, the lower index first among equals (float64 brute force)."""
+    out = []
+    g = w.reshape(-1, 4).astype(np.float64)
+    for v in g:
+        order = sorted(range(4), key=lambda i: (-abs(v[i]), i))
+        out.append((order[0], order[1], v[order[0]], v[order[1]]))
+    return out
+
+
+@pytest.mark.parametrize("rows,cols,seed", [(1, 4, 0), (3, 8, 1), (16, 64, 2), (5, 12, 3), (64, 256, 4)])
+def test_prune_sparse24_vs_bruteforce(rows, cols, seed):
+    """prune_fp32_to_sparse_ternary (sparse_ternary.rs:598-663): the kept
+    positions are the stable top 2 by |v| (checked with ties forced), the
+    sign of each kept position is the sign of the value the reference's
+    sign bit names (bit 0: the larger |v|, bit 1: the second), and the
+    scale is the float64 absmean within f32 rounding of the sequential sum."""
+    rng = np.random.default_rng(seed)
+    w = rng.standard_normal(rows * cols).astype(np.float32)
+    w[rng.random(w.size) < 0.15] = 0.0
+    ties = rng.random(w.size) < 0.2
+    w[ties] = np.float32(0.5) * np.sign(w[ties])  # equal magnitudes, mixed signs
+    pats, signs, scale = oracle.prune_sparse24(w, rows, cols)
+    dec = oracle.sparse24_cpu_to_ternary(pats, signs, rows, cols).reshape(-1, 4)
+    for g, (pa, pb, va, vb) in enumerate(_prune_bruteforce(w, rows, cols)):
+        lo, hi = min(pa, pb), max(pa, pb)
+        kept = [i for i in range(4) if dec[g][i] != 0]
+        assert kept == [lo, hi], g
+        # bit 0 (read as the lower position) carries sign(va), bit 1 sign(vb)
+        assert dec[g][lo] == (1 if va >= 0 else -1), g
+        assert dec[g][hi] == (1 if vb >= 0 else -1), g
+    ref = np.abs(w.astype(np.float64)).mean() / 0.7978845608
+    assert abs(float(scale) - ref) <= 1e-5 * ref
+
+
+def test_prune_sparse24_sign_order_and_special_values():
+    """Closed cases of the reference's packing order: when the larger |v| is
+    at the higher position, its sign lands on the lower position (the
+    reference packs signs in magnitude order, :642-644); all-zero groups keep
+    positions (0, 1) with + signs (0.0 >= 0); -0.0 counts as +; the scale of
+    an all-zero matrix is 1."""
+    w = np.array([0.1, -0.5, 0.0, 3.0,      # larger at pos 3 (+), second at pos 1 (-)
+                  -3.0, 0.0, 0.5, 0.1,      # larger at pos 0 (-), second at pos 2 (+)
+                  0.0, 0.0, 0.0, 0.0,       # all zero
+                  -0.0, -0.0, 0.25, 0.0],   # one nonzero, then the first -0.0
+                 np.float32)
+    pats, signs, scale = oracle.prune_sparse24(w, 1, 16)
+    dec = oracle.sparse24_cpu_to_ternary(pats, signs, 1, 16).reshape(4, 4)
+    np.testing.assert_array_equal(dec[0], [0, 1, 0, -1])
+    np.testing.assert_array_equal(dec[1], [-1, 0, 1, 0])
+    np.testing.assert_array_equal(dec[2], [1, 1, 0, 0])
+    np.testing.assert_array_equal(dec[3], [1, 0, 1, 0])
+    z = np.zeros(8, np.float32)
+    assert oracle.prune_sparse24(z, 2, 4)[2] == np.float32(1.0)

@@ -201,3 +201,36 @@ def test_ternary_linear_paths_agree_with_bias():
     for s in range(S):
         d = oracle.ternary_linear_forward(t, 0.37, bias, x[s], R, C, 1, 2)
         np.testing.assert_allclose(d.ravel(), f[s], atol=1e-5, rtol=0)
+
+
+def test_prune_fp32_kat():
+    """prune_fp32_to_sparse_ternary (sparse_ternary.rs:523-544
+    test_prune_fp32_to_sparse): top-2 by |v| per group, decompressed."""
+    kat = KATS["prune_fp32"]
+    w = np.array(kat["weights"], np.float32)
+    pats, signs, scale = oracle.prune_sparse24(w, kat["rows"], kat["cols"])
+    dec = oracle.sparse24_cpu_to_ternary(pats, signs, kat["rows"], kat["cols"])
+    np.testing.assert_array_equal(dec, kat["expected_decompressed"])
+    # the absmean of the fp32 values, ternary.rs:15 ABSMEAN_NORM
+    assert abs(float(scale) - np.abs(w.astype(np.float64)).mean() / 0.7978845608) <= 1e-6 * float(scale)
+
+
+def _quantization_cos(w, r):
+    w = w.astype(np.float64)
+    r = r.astype(np.float64)
+    return float((w @ r) / (np.linalg.norm(w) * np.linalg.norm(r)))
+
+
+def test_blocked_vs_per_tensor_kat():
+    """ternary.rs:845-873 test_blocked_vs_per_tensor: bimodal weights (i *
+    0.001 - 0.128 for i < 256, i * 0.01 - 2.56 above), block 64: the blocked
+    round trip's cosine is at least the per-tensor one minus 0.01."""
+    i = np.arange(512, dtype=np.float32)
+    w = np.where(i < 256, i * np.float32(0.001) - np.float32(0.128),
+                 i * np.float32(0.01) - np.float32(2.56)).astype(np.float32)
+    q_t, s_t = oracle.quantize_ternary(w)
+    r_t = s_t * q_t.astype(np.float32)
+    q_b, s_b = oracle.quantize_ternary_blocked(w, 64)
+    assert s_b.size == 8
+    r_b = oracle.dequantize_ternary_blocked(q_b, s_b, 64)
+    assert _quantization_cos(w, r_b) >= _quantization_cos(w, r_t) - 0.01
