@@ -4,16 +4,19 @@
 Headline workload (value): decode ternary GEMV at LLaMA-7B FFN shapes. One
 step = one decode pass of B tokens through the three FFN projections
 (W_gate, W_up [11008,4096] on x, W_down [4096,11008] on its own [B,11008]
-input), bf16 activations, fp32 accumulation, bf16 outputs, three
-frx_ternary_linear launches. Weights, scales and activations are resident in
+input), bf16 activations, fp32 accumulation, bf16 outputs: gate and up as
+one frx_ternary_linear_group launch (they share x, as the model's decode
+step issues them), down as frx_ternary_linear; the step as three launches
+is reported beside it. Weights, scales and activations are resident in
 HBM before timing; the weights rotate over enough distinct copies (>= 0.5 GB)
-that the 256 MB Infinity Cache cannot serve them. value = algorithmic bytes
+that the 256 MB Infinity Cache cannot serve them (one copy per timed step).
+value = algorithmic bytes
 per step (packed weights + scales + x + y) / time per step, the K timed steps
 replayed from one HIP graph.
 
-roofline: algorithmic bytes per GEMV launch / its average launch time over
-back-to-back launches of one shape (HIP events on the launch stream around
-the sequence), weighted over the step's three launches.
+roofline: the dominant kernel, the gate/up group launch (two thirds of the
+step): its algorithmic bytes / its average launch time over back-to-back
+launches (HIP events on the launch stream around the sequence).
 cpu_baseline: the reference's CPU decode path (ternary_matmul_packed_parallel,
 src/model/ternary.rs:471-529, restated in C by the oracle) on the same three
 matrices at B=1, timed on this host's cores; its breakdown adds the branchy
@@ -102,7 +105,13 @@ def main():
     s_d = torch.from_numpy(synth.row_scales("bench/decode", "s_down", H, samples=256)).to(dev)
     step_weight_bytes = (w_g.numel() + w_u.numel() + w_d.numel()) * 4
     copies = max(2, int(np.ceil(512e6 / step_weight_bytes)) + 1)
-    W = [(w_g.clone(), w_u.clone(), w_d.clone()) for _ in range(copies)]
+    # The timed graph gives every step a copy of its own (steps + 3 copies at
+    # least): each copy it reads was last read a whole replay (>= 0.5 GB)
+    # earlier, so no timed step is served by the 256 MB Infinity Cache.
+    # The per-launch timings rotate over all of them too: >= 56 copies keep
+    # even the one-matrix rotations (56 x 11.3 MB) above twice the cache.
+    step_copies = max(copies, args.steps + 3, 56)
+    W = [(w_g.clone(), w_u.clone(), w_d.clone()) for _ in range(step_copies)]
     del w_g, w_u, w_d
     _, xb = synth.activations("bench/decode", "x", B, H)
     _, hb = synth.activations("bench/decode", "h", B, I)
@@ -116,16 +125,27 @@ def main():
 
     b_gu = gemv_bytes(I, H, B)
     b_dn = gemv_bytes(H, I, B)
-    step_bytes = 2 * b_gu + b_dn
+    # gate and up share x: one same-x group launch reads it once
+    b_grp = 2 * (I * H // 4 + 4 * I) + 2 * B * H + 2 * 2 * B * I
+    step_bytes = b_grp + b_dn
 
     def step(i):
-        """One decode step: the three LLaMA-7B FFN projections as GEMVs."""
-        wg, wu, wd = W[i % copies]
+        """One decode step: the three LLaMA-7B FFN projections as GEMVs,
+        gate and up (same x) as one frx_ternary_linear_group launch, down as
+        frx_ternary_linear on its own input."""
+        wg, wu, wd = W[i % step_copies]
+        ctx.ternary_linear_group(x, [wg, wu], [s_g, s_u], [g, u])
+        ctx.ternary_linear(wd, s_d, xd, y)
+
+    def step3(i):
+        """The same step as three frx_ternary_linear launches."""
+        wg, wu, wd = W[i % step_copies]
         ctx.ternary_linear(wg, s_g, x, g)
         ctx.ternary_linear(wu, s_u, x, u)
         ctx.ternary_linear(wd, s_d, xd, y)
 
-    log(f"bench: warmup {args.warmup} steps ({copies} weight copies, {copies * step_weight_bytes / 1e6:.0f} MB)")
+    log(f"bench: warmup {args.warmup} steps ({step_copies} weight copies, "
+        f"{step_copies * step_weight_bytes / 1e6:.0f} MB)")
     with torch.cuda.stream(stream):
         for i in range(args.warmup):
             step(i)
@@ -169,6 +189,11 @@ def main():
     ms_per_step = elapsed / args.steps * 1e3
     value = step_bytes / (elapsed / args.steps) / 1e9
     log(f"bench: decode GEMV B={B}: {ms_per_step * 1e3:.1f} us/step, {value:.1f} GB/s ({timing})")
+    el3, _ = timed(lambda: [step3(i) for i in range(args.steps)])
+    step3_res = {"us_per_step": round(el3 / args.steps * 1e6, 2),
+                 "gb_s": round((2 * b_gu + b_dn) / (el3 / args.steps) / 1e9, 1),
+                 "hbm_fraction": round((2 * b_gu + b_dn) / (el3 / args.steps) / 1e9 / HBM_PEAK_GBS, 4)}
+    log(f"bench: decode GEMV B={B} as three launches: {step3_res['us_per_step']} us/step, {step3_res['gb_s']} GB/s")
 
     # Per-launch kernel time: back-to-back launches of one kernel (weights
     # rotating over the copies), HIP events on the launch stream around the
@@ -177,7 +202,7 @@ def main():
         """Average seconds per launch; with `stats` (a dict) also the median,
         p10 and p90 of the per-launch time over the individual replays."""
         def seq():
-            for i in range(copies):
+            for i in range(step_copies):
                 fn_one(i)
         gr = capture(seq) if graphed else None
         with torch.cuda.stream(stream):
@@ -190,7 +215,7 @@ def main():
                 (gr.replay() if gr is not None else seq())
                 ev[r + 1].record(stream)
         torch.cuda.synchronize()
-        per = copies * per_copy
+        per = step_copies * per_copy
         if stats is not None:
             samples = np.array([ev[r].elapsed_time(ev[r + 1]) * 1e3 / per for r in range(reps)])
             stats.update({"median_us": round(float(np.median(samples)), 3),
@@ -199,23 +224,29 @@ def main():
                           "samples": reps, "launches_per_sample": per})
         return ev[0].elapsed_time(ev[reps]) * 1e-3 / (reps * per)
 
-    reps = max(3, args.steps // copies)
+    reps = max(3, args.steps // step_copies)
     dist_reps = max(reps, 30)  # enough replays for the percentiles (>= 200 launches per shape)
-    dist = {"11008x4096": {}, "4096x11008": {}}
+    dist = {"group_2x11008x4096": {}, "11008x4096": {}, "4096x11008": {}}
+    t_grp = per_launch(lambda i: ctx.ternary_linear_group(x, [W[i][0], W[i][1]], [s_g, s_u], [g, u]), 1,
+                       dist_reps, dist["group_2x11008x4096"])
     t_gu = per_launch(lambda i: (ctx.ternary_linear(W[i][0], s_g, x, g), ctx.ternary_linear(W[i][1], s_u, x, u)),
                       2, dist_reps, dist["11008x4096"])
     t_dn = per_launch(lambda i: ctx.ternary_linear(W[i][2], s_d, xd, y), 1, dist_reps, dist["4096x11008"])
-    launch_bytes = 2 * b_gu + b_dn
-    launch_time = 2 * t_gu + t_dn
-    achieved = launch_bytes / launch_time / 1e9
+    # the dominant kernel: the gate/up group launch (two thirds of the step)
+    achieved = b_grp / t_grp / 1e9
     roofline = {
-        "kernel": "frx::gemv_bal_kernel (B=1, linear, bf16 in, bf16 out)" if B == 1 else
-                  "frx::gemv_rows4_kernel" if 2 <= B <= 4 else "frx::gemv_xs_kernel",
+        "kernel": ("frx::gemv_bal_kernel same-x group (gate + up, 22016 rows, B=1, bf16 in, bf16 out)" if B == 1
+                   else "gate and up as separate launches (the group is one launch at B=1 only): "
+                        + ("frx::gemv_rows4_kernel" if 2 <= B <= 4 else "frx::gemv_xs_kernel")),
         "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
         "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-        "avg_us": {"11008x4096": round(t_gu * 1e6, 3), "4096x11008": round(t_dn * 1e6, 3)},
+        "algorithmic_bytes_per_launch": b_grp,
+        "avg_us": {"group_2x11008x4096": round(t_grp * 1e6, 3), "11008x4096": round(t_gu * 1e6, 3),
+                   "4096x11008": round(t_dn * 1e6, 3)},
+        "step_launches_weighted": {"achieved": round((b_grp + b_dn) / (t_grp + t_dn) / 1e9, 1),
+                                   "frac": round((b_grp + b_dn) / (t_grp + t_dn) / 1e9 / HBM_PEAK_GBS, 4)},
         "launch_time_distribution": dist,
-        "bytes_per_launch": {"11008x4096": b_gu, "4096x11008": b_dn},
+        "bytes_per_launch": {"group_2x11008x4096": b_grp, "11008x4096": b_gu, "4096x11008": b_dn},
         "timing": timing,
     }
     traffic_file = os.path.join(ROOT, "profiles", "gemv_traffic.json")
@@ -225,9 +256,9 @@ def main():
             tr = json.load(open(traffic_file)).get("by_batch", {}).get(str(B))
             if tr:
                 by = tr["bytes_per_launch"]
-                # per-launch average over the step's three launches
-                roofline["traffic"] = int(round((2 * by["11008x4096"] + by["4096x11008"]) / 3))
-                roofline["traffic_by_shape"] = {k: by[k] for k in ("11008x4096", "4096x11008")}
+                roofline["traffic"] = by.get("group_2x11008x4096")
+                roofline["traffic_by_shape"] = {k: by[k] for k in ("group_2x11008x4096", "11008x4096", "4096x11008")
+                                                if k in by}
                 ffn_traffic = {k: by[k] for k in ("ffn_glu_planes_11008x4096", "ffn_down_planes_4096x11008",
                                                   "glu_f32h_11008x4096", "down_f32x_4096x11008", "ffn1_llama7b")
                                if k in by}
@@ -245,7 +276,7 @@ def main():
     b_ffn = 2 * (I * H // 4 + 4 * I) + (H * I // 4 + 4 * H) + 2 * B * H + 2 * B * H
 
     def ffn_step(i):
-        wg, wu, wd = W[i % copies]
+        wg, wu, wd = W[i % step_copies]
         ctx.ternary_ffn(x, wg, s_g, wu, s_u, wd, s_d, y)
     fused = {"algorithmic_bytes_per_step": b_ffn}
     modes = [(frx.FFN_AUTO, "default"), (frx.FFN_TWO_LAUNCH, "two_launch")]
@@ -284,7 +315,7 @@ def main():
         + (f", one-launch {fused['one_launch']['us_per_step']} us" if "one_launch" in fused else "")
         + f"; frx_ternary_glu {t_glu * 1e6:.2f} us, fp32-input down {t_d32 * 1e6:.2f} us")
 
-    extra = {"decode_ffn_fused_llama7b": fused}
+    extra = {"decode_ffn_fused_llama7b": fused, "decode_step_three_launches": step3_res}
     if B == 1 and not args.no_extra:
         # The decode configuration's other batch sizes: the same three
         # projections, weights rotating, timed the same way (B = 4: the
@@ -300,7 +331,7 @@ def main():
             yx = torch.empty((bx, H), dtype=torch.bfloat16, device=dev)
 
             def stepx(i, xx=xx, xdx=xdx, gx=gx, ux=ux, yx=yx):
-                wg, wu, wd = W[i % copies]
+                wg, wu, wd = W[i % step_copies]
                 ctx.ternary_linear(wg, s_g, xx, gx)
                 ctx.ternary_linear(wu, s_u, xx, ux)
                 ctx.ternary_linear(wd, s_d, xdx, yx)
@@ -319,7 +350,7 @@ def main():
             yfx = torch.empty((bx, H), dtype=torch.bfloat16, device=dev)
 
             def ffnx(i, xx=xx, yfx=yfx):
-                wg, wu, wd = W[i % copies]
+                wg, wu, wd = W[i % step_copies]
                 ctx.ternary_ffn(xx, wg, s_g, wu, s_u, wd, s_d, yfx)
             with torch.cuda.stream(stream):  # first call outside capture (workspace)
                 ffnx(0)
@@ -388,7 +419,7 @@ def main():
             "batch_tokens": B,
             "projections": ["gate 11008x4096", "up 11008x4096", "down 4096x11008"],
             "x_dtype": "bf16", "y_dtype": "bf16", "accumulate": "fp32",
-            "weight_copies": copies,
+            "weight_copies": step_copies,
             "hbm_fraction": round(value / HBM_PEAK_GBS, 4),
         },
         "roofline": roofline,
@@ -449,6 +480,8 @@ def run_extra(torch, frx, synth, ctx, stream, dev, only=None, iters=200):
             log(f"bench: 2:4 N={N}: {dt * 1e6:.1f} us, {tf:.1f} TFLOP/s dense-equivalent")
             del meta
         del w, Y
+    if only is None:
+        res["gemm_ceilings"] = gemm_ceilings(torch, stream, dev, X)
     if only not in (None, "moe"):
         return res
     # MoE expert layer
@@ -476,6 +509,42 @@ def run_extra(torch, frx, synth, ctx, stream, dev, only=None, iters=200):
                                               "frac_bf16_peak": round(tf / BF16_PEAK_TFLOPS, 4), **st}
     log(f"bench: MoE: {dt * 1e6:.1f} us, {tf:.1f} TFLOP/s")
     return res
+
+
+def gemm_ceilings(torch, stream, dev, X, iters=100):
+    """What the matrix pipe and the vendor GEMM reach on this box, beside the
+    ternary GEMMs: (i) frxb_mfma (libfrx_bench.so), back-to-back 16x16x32
+    bf16 MFMAs on register operands with no memory traffic, 4 and 8 waves
+    per compute unit; (ii) torch.matmul in bf16 (hipBLASLt) on the prefill
+    shapes X[2048,4096] x W[4096,N] with W dense bf16 (N in {4096, 11008}),
+    the same flops as the ternary prefill GEMM."""
+    out = {}
+    bl = _bench_lib()
+    sink = torch.empty(bl.frxb_read_grid(), dtype=torch.float32, device=dev)
+    cus = bl.frxb_read_grid() // 2
+    mi = 20000
+    for wpc in (4, 8):
+        def run(wpc=wpc):
+            rc = bl.frxb_mfma(mi, wpc, sink.data_ptr(), stream.cuda_stream)
+            assert rc == 0, rc
+        dt = _time_kernel(torch, stream, run, 10)
+        fl = cus * wpc * mi * 8 * 16384.0
+        out[f"mfma_loop_{wpc}_waves_per_cu"] = {"tflops": round(fl / dt / 1e12, 1),
+                                                "frac_bf16_peak": round(fl / dt / 1e12 / BF16_PEAK_TFLOPS, 4),
+                                                "us": round(dt * 1e6, 1)}
+        log(f"bench: MFMA loop ({wpc} waves/CU): {fl / dt / 1e12:.0f} TFLOP/s")
+    M, K = X.shape
+    for N in (4096, 11008):
+        Wt = torch.randn((K, N), device=dev).to(torch.bfloat16).contiguous()
+        Y = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+        st = {}
+        dt = _time_kernel(torch, stream, lambda: torch.matmul(X, Wt, out=Y), iters, stats=st)
+        tf = 2.0 * M * N * K / dt / 1e12
+        out[f"torch_matmul_bf16_{M}x{K}x{N}"] = {"us": round(dt * 1e6, 2), "tflops": round(tf, 1),
+                                                  "frac_bf16_peak": round(tf / BF16_PEAK_TFLOPS, 4), **st}
+        log(f"bench: torch.matmul bf16 N={N}: {dt * 1e6:.1f} us, {tf:.1f} TFLOP/s")
+        del Wt, Y
+    return out
 
 
 def _graph_time(torch, stream, calls, reps):
@@ -516,6 +585,8 @@ def _bench_lib():
     h.frxb_read.restype = ctypes.c_int
     h.frxb_read.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p, ctypes.c_void_p]
     h.frxb_read_grid.restype = ctypes.c_int
+    h.frxb_mfma.restype = ctypes.c_int
+    h.frxb_mfma.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p]
     return h
 
 
@@ -685,7 +756,13 @@ def cpu_baseline(t_gu, t_dn, B, seconds):
                            oracle.sparse24_cpu_matmul_decode(pd, sgd, 0.01, n_dn, k_dn, h)), budget, max_reps=20),
         2 * (pg.nbytes + sgg.nbytes + 4 * k_gu + 4 * n_gu) + pd.nbytes + sgd.nbytes + 4 * k_dn + 4 * n_dn,
         fl_step, 1))
+    try:
+        avail = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        avail = os.cpu_count() or 1
     return {"value": round(byts / step_t / 1e9, 2), "unit": "GB/s", "cores": threads, "kind": "port",
+            "host_cores": {"os_cpu_count": os.cpu_count(), "affinity": avail, "threads_used": threads,
+                           "note": "threads capped at 16, the host share of one GPU on this machine"},
             "sample": f"ternary_matmul_packed_parallel (ternary.rs:471-529) restated in C, u8 layout, f32 x, "
                       f"1 token through 11008x4096 x2 + 4096x11008, median of {reps} reps each "
                       f"({step_t * 1e3:.2f} ms/step on {threads} threads)",

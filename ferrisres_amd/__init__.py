@@ -91,6 +91,7 @@ _SIGS = {
     "frx_quantize_ternary_blocked": (_int, [_vp, _vp, _int, _sz, _u32, _vp, _vp]),
     "frx_dequantize_ternary_blocked": (_int, [_vp, _vp, _vp, _sz, _u32, _vp]),
     "frx_prune_sparse24": (_int, [_vp, _vp, _int, _u32, _u32, _int, _vp, _vp, _vp, _vp]),
+    "frx_ternary_linear_group": (_int, [_vp, _vp, _int, _u32, _u32, _u32, _vp, _vp, _vp, _vp, _int]),
     "frx_workspace_stats": (_int, [_vp, ctypes.POINTER(_sz), ctypes.POINTER(_sz), ctypes.POINTER(_u32)]),
     "frx_release_retired": (_int, [_vp]),
     "frx_free": (_int, [_vp, _vp]),
@@ -328,6 +329,27 @@ class Context:
         _check(lib().frx_ternary_linear(self._h, _ptr(w), _ptr(scale), _ptr(x), _dtype_code(x),
                                         _ptr(y), _dtype_code(y), M, K, N), self._h)
         return y
+
+    def ternary_linear_group(self, x, ws, scales, ys):
+        """frx_ternary_linear_group: y_i = x W_i^T * s_i for up to four
+        matrices with the same K against one x (one launch at one token)."""
+        M, K = _shape2(x, "x")
+        count = len(ws)
+        if not (len(scales) == len(ys) == count):
+            raise _shape_err("ws, scales and ys must have the same length")
+        Ns = []
+        for i, (w, sc, y) in enumerate(zip(ws, scales, ys)):
+            n = _rows(w, K // 16, f"w[{i}]") if K % 16 == 0 else int(w.shape[0])
+            _expect_numel(sc, n, f"scale[{i}]")
+            _expect_shape(y, (M, n), f"y[{i}]")
+            Ns.append(n)
+        arr = lambda ts: (_vp * max(count, 1))(*[t.data_ptr() for t in ts])  # noqa: E731
+        ydt = _dtype_code(ys[0]) if ys else FRX_F32
+        if any(_dtype_code(y) != ydt for y in ys):
+            raise TypeError("all outputs of a group must have the same dtype")
+        _check(lib().frx_ternary_linear_group(self._h, _ptr(x), _dtype_code(x), M, K, count, arr(ws), arr(scales),
+                                              (_u32 * max(count, 1))(*Ns), arr(ys), ydt), self._h)
+        return ys
 
     def sparse24_ternary_linear(self, meta, scale, x, y):
         M, K = _shape2(x, "x")

@@ -396,6 +396,37 @@ frx_status frx_ternary_linear_bias(frx_ctx *ctx, const uint32_t *w, const float 
   return ternary_linear_run(ctx, w, scale, bias, x, xt, y, yt, M, K, N);
 }
 
+frx_status frx_ternary_linear_group(frx_ctx *ctx, const void *x, frx_dtype xt, uint32_t M, uint32_t K,
+                                    uint32_t count, const uint32_t *const *w, const float *const *scale,
+                                    const uint32_t *N, void *const *y, frx_dtype yt) {
+  frx_status st = enter(ctx);
+  if (st != FRX_OK) return st;
+  if (!w || !scale || !N || !y) return fail(ctx, FRX_ERR_SHAPE, "null pointer array");
+  if (count == 0 || count > (uint32_t)frx::GEMV_GROUP_MAX)
+    return fail(ctx, FRX_ERR_SHAPE, "count=%u must be in [1, %d]", count, frx::GEMV_GROUP_MAX);
+  bool aligned = aligned16(x);
+  size_t rows = 0;
+  for (uint32_t i = 0; i < count; i++) {
+    if ((st = check_linear(ctx, w[i], scale[i], x, xt, y[i], yt, M, K, N[i], false)) != FRX_OK) return st;
+    aligned = aligned && aligned16(scale[i]) && aligned16(y[i]);
+    rows += N[i];
+  }
+  if (rows > (size_t)0x7FFFFFFF) return fail(ctx, FRX_ERR_SHAPE, "too many rows in the group");
+  hipError_t e = hipSuccess;
+  if (M <= 16 && aligned) {
+    int n[frx::GEMV_GROUP_MAX];
+    for (uint32_t i = 0; i < count; i++) n[i] = (int)N[i];
+    e = frx::launch_gemv_group(x, xt == FRX_BF16, yt == FRX_BF16, (int)M, (int)K, (int)count, w, scale, y, n,
+                               ctx->stream);
+  } else {
+    // prefill, or sub-slices that need staging: one linear per matrix
+    for (uint32_t i = 0; i < count; i++)
+      if ((st = ternary_linear_run(ctx, w[i], scale[i], nullptr, x, xt, y[i], yt, M, K, N[i])) != FRX_OK) return st;
+  }
+  if (e != hipSuccess) return hip_fail(ctx, e, "ternary_linear_group launch");
+  return FRX_OK;
+}
+
 frx_status frx_sparse24_ternary_linear(frx_ctx *ctx, const uint32_t *meta,
                                        const float *scale, const void *x,
                                        frx_dtype xt, void *y, frx_dtype yt,

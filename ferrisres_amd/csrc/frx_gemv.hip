@@ -907,14 +907,17 @@ static hipError_t launch_gemv_rows_w(const uint32_t *w, const float *scale, cons
 // and each word runs four MFMAs. NW = 2 (EPI = GEMV_SWIGLU / GEMV_GEGLU):
 // the same rows of the gate (W) and up (W2) matrices against the same x;
 // h = act(g) * u is written as bf16 hi and lo planes (Y = [2][N]).
-template <typename YT, int NI, int RMAX, bool XF32, bool XPLN = false, int NW = 1, int EPI = GEMV_LINEAR>
+template <typename YT, int NI, int RMAX, bool XF32, bool XPLN = false, int NW = 1, int EPI = GEMV_LINEAR,
+          bool GRP = false>
 __global__ __launch_bounds__(512) void gemv_bal_kernel(const uint32_t *__restrict__ W, const float *__restrict__ scale,
                                                        const uint32_t *__restrict__ W2,
                                                        const float *__restrict__ scale2,
                                                        const void *__restrict__ Xv, YT *__restrict__ Y, int K, int N,
-                                                       const float *__restrict__ bias, int nq, int nr) {
+                                                       const float *__restrict__ bias, int nq, int nr,
+                                                       const GemvGroup grp) {
   static_assert((NW == 2) == (EPI != GEMV_LINEAR), "two matrices exactly for the GLU epilogues");
   static_assert(!(XF32 && XPLN), "one activation source");
+  static_assert(!GRP || (NW == 1 && !XPLN), "a group of linear matrices over one x");
   constexpr int WAVES = 8, NT = 512;
   constexpr int XPL = (XF32 || XPLN) ? 2 : 1;
   constexpr int PP = NI * 512;                   // 8-value pieces of x staged (NI * 4096 values)
@@ -940,6 +943,16 @@ __global__ __launch_bounds__(512) void gemv_bal_kernel(const uint32_t *__restric
   __amdgpu_buffer_rsrc_t wr[NW];
 #pragma unroll
   for (int m = 0; m < NW; m++) wr[m] = buffer_rsrc(m ? W2 : W, (uint32_t)N * (uint32_t)kw * 4u);
+  // GRP: the rows of the group's matrices, concatenated, are the rows of the
+  // launch; launch row r lives in matrix grp.matrix_of(r) (wave-uniform for
+  // the wave's rows) and is read through a descriptor of its own row, built
+  // where it is loaded (no arrays of descriptors: they would go to scratch)
+  auto grp_row = [&](int rr, const uint32_t *&wp, const float *&sp) {
+    const int r = min(row0 + rr, N - 1);
+    const int m = grp.matrix_of(r), l = r - grp.start_of(m);
+    wp = grp.w_of(m) + (size_t)l * (uint32_t)kw;
+    sp = grp.s_of(m) + l;
+  };
   // 1. x pieces (zero past K), then a barrier: all of the CU's x loads are
   //    ahead of its weight loads
   u32x4 xs[XR][XL];
@@ -963,15 +976,31 @@ __global__ __launch_bounds__(512) void gemv_bal_kernel(const uint32_t *__restric
 #pragma unroll
       for (int i = 0; i < NI; i++) {
         const int wi = i * 256 + 4 * lane;
-        const uint32_t off =
-            (rr < cnt && wi < kw) ? ((uint32_t)(row0 + rr) * (uint32_t)kw + (uint32_t)wi) * 4u : OOB;
-        wv[rr][m][i] = __builtin_amdgcn_raw_buffer_load_b128(wr[m], off, 0, 0);
+        if constexpr (GRP) {
+          const uint32_t *wp;
+          const float *sp;
+          grp_row(rr, wp, sp);
+          const uint32_t off = (rr < cnt && wi < kw) ? (uint32_t)wi * 4u : OOB;
+          wv[rr][m][i] = __builtin_amdgcn_raw_buffer_load_b128(buffer_rsrc(wp, (uint32_t)kw * 4u), off, 0, 0);
+        } else {
+          const uint32_t off =
+              (rr < cnt && wi < kw) ? ((uint32_t)(row0 + rr) * (uint32_t)kw + (uint32_t)wi) * 4u : OOB;
+          wv[rr][m][i] = __builtin_amdgcn_raw_buffer_load_b128(wr[m], off, 0, 0);
+        }
       }
   float sc[RMAX][NW];
 #pragma unroll
   for (int rr = 0; rr < RMAX; rr++)
 #pragma unroll
-    for (int m = 0; m < NW; m++) sc[rr][m] = (m ? scale2 : scale)[min(row0 + rr, N - 1)];
+    for (int m = 0; m < NW; m++) {
+      if constexpr (GRP) {
+        const uint32_t *wp;
+        const float *sp;
+        grp_row(rr, wp, sp);
+        sc[rr][m] = *sp;
+      }
+      else sc[rr][m] = (m ? scale2 : scale)[min(row0 + rr, N - 1)];
+    }
   const float bv = bias ? bias[min(row0 + lane, N - 1)] : 0.f;  // lane's output row
   // 3. stage: piece j -> chunk j/8, slot j%8 (per plane), K-interleaved to
   //    match the decode (stage_kil: all lanes take part)
@@ -1079,17 +1108,45 @@ __global__ __launch_bounds__(512) void gemv_bal_kernel(const uint32_t *__restric
     // and two exchanges add the four 16-lane rows: lane r < RMAX then holds
     // row r's dot product.
     const int q = lane & 3;
-    float mv = vq[0];
+    if constexpr (!GRP) {
+      float mv = vq[0];
 #pragma unroll
-    for (int rr = 1; rr < RMAX; rr++) mv = q == rr ? vq[rr] : mv;
-    mv += dpp_f32<0x128>(mv);  // row_ror:8
-    mv += dpp_f32<0x124>(mv);  // row_ror:4
-    mv += __shfl_xor(mv, 32);
-    mv += __shfl_xor(mv, 16);
-    float s = sc[0][0];
+      for (int rr = 1; rr < RMAX; rr++) mv = q == rr ? vq[rr] : mv;
+      mv += dpp_f32<0x128>(mv);  // row_ror:8
+      mv += dpp_f32<0x124>(mv);  // row_ror:4
+      mv += __shfl_xor(mv, 32);
+      mv += __shfl_xor(mv, 16);
+      float s = sc[0][0];
 #pragma unroll
-    for (int rr = 1; rr < RMAX; rr++) s = q == rr ? sc[rr][0] : s;
-    res[0] = mv * s * 0.5f;  // 0.5 undoes the 2*dec(c) encoding
+      for (int rr = 1; rr < RMAX; rr++) s = q == rr ? sc[rr][0] : s;
+      res[0] = mv * s * 0.5f;  // 0.5 undoes the 2*dec(c) encoding
+    } else {
+      // Groups take up to 8 rows per wave: every lane l ends with the total
+      // of row (l % 4) of its pass, and above four rows a second pass takes
+      // rows 4..7, which lanes 4..7 keep. Rows are picked with bit masks (a
+      // select chain here became an indexed load from a scratch copy).
+      auto pass = [&](auto base_c) {
+        constexpr int base = decltype(base_c)::value;
+        uint32_t mb = 0, sb = 0;
+#pragma unroll
+        for (int rr = base; rr < min(RMAX, base + 4); rr++) {
+          const uint32_t k = q == rr - base ? 0xFFFFFFFFu : 0u;
+          mb |= __float_as_uint(vq[rr]) & k;
+          sb |= __float_as_uint(sc[rr][0]) & k;
+        }
+        float mv = __uint_as_float(mb);
+        mv += dpp_f32<0x128>(mv);  // row_ror:8
+        mv += dpp_f32<0x124>(mv);  // row_ror:4
+        mv += __shfl_xor(mv, 32);
+        mv += __shfl_xor(mv, 16);
+        return mv * __uint_as_float(sb) * 0.5f;  // 0.5 undoes the 2*dec(c) encoding
+      };
+      res[0] = pass(std::integral_constant<int, 0>{});
+      if constexpr (RMAX > 4) {
+        const float r1 = pass(std::integral_constant<int, 4>{});
+        if (lane >= 4) res[0] = r1;
+      }
+    }
   }
   if (lane < cnt) {
     const int row = row0 + lane;
@@ -1099,6 +1156,12 @@ __global__ __launch_bounds__(512) void gemv_bal_kernel(const uint32_t *__restric
       split_bf16(h, hh, hl);
       Y[row] = (uint16_t)hh;
       Y[N + row] = (uint16_t)hl;
+    } else if constexpr (GRP) {
+      const int m = grp.matrix_of(row);
+      YT *Ym = reinterpret_cast<YT *>(grp.y_of(m));
+      const int lr = row - grp.start_of(m);
+      if constexpr (sizeof(YT) == 2) Ym[lr] = (uint16_t)bf16_rne(res[0]);
+      else Ym[lr] = res[0];
     } else {
       float o = res[0];
       if (bias) o = add_bias(o, bv);
@@ -1112,20 +1175,24 @@ __global__ __launch_bounds__(512) void gemv_bal_kernel(const uint32_t *__restric
 // launch (a slot past the wave's rows still costs its loads: at 4096x11008,
 // four slots for two rows measured 6.30 against 5.31 us).
 constexpr int GEMV_BAL_RMAX = 4;
+constexpr int GEMV_GROUP_RMAX = 8;  // most rows per wave of a same-x group launch
 
-template <typename YT, int NI, int RMAX, bool XF32, bool XPLN = false, int NW = 1, int EPI = GEMV_LINEAR>
+template <typename YT, int NI, int RMAX, bool XF32, bool XPLN = false, int NW = 1, int EPI = GEMV_LINEAR,
+          bool GRP = false>
 static hipError_t launch_gemv_bal_w(const uint32_t *w, const float *scale, const void *x, void *y, int K, int N,
                                     int G, hipStream_t stream, const float *bias, const uint32_t *w2 = nullptr,
-                                    const float *scale2 = nullptr) {
+                                    const float *scale2 = nullptr, const GemvGroup *grp = nullptr) {
   const size_t lds = (size_t)((XF32 || XPLN) ? 2 : 1) * NI * 64 * ROWS_XCH * 4;
   if (lds > 64 * 1024) {
     static std::atomic<uint64_t> done;
     const hipError_t e = opt_in_lds(
-        reinterpret_cast<const void *>(&gemv_bal_kernel<YT, NI, RMAX, XF32, XPLN, NW, EPI>), (int)lds, done);
+        reinterpret_cast<const void *>(&gemv_bal_kernel<YT, NI, RMAX, XF32, XPLN, NW, EPI, GRP>), (int)lds, done);
     if (e != hipSuccess) return e;
   }
-  hipLaunchKernelGGL((gemv_bal_kernel<YT, NI, RMAX, XF32, XPLN, NW, EPI>), dim3(G), dim3(512), lds, stream, w, scale,
-                     w2 ? w2 : w, scale2 ? scale2 : scale, x, reinterpret_cast<YT *>(y), K, N, bias, N / G, N % G);
+  const GemvGroup g = grp ? *grp : GemvGroup{};
+  hipLaunchKernelGGL((gemv_bal_kernel<YT, NI, RMAX, XF32, XPLN, NW, EPI, GRP>), dim3(G), dim3(512), lds, stream, w,
+                     scale, w2 ? w2 : w, scale2 ? scale2 : scale, x, reinterpret_cast<YT *>(y), K, N, bias, N / G,
+                     N % G, g);
   return hipGetLastError();
 }
 
@@ -1134,35 +1201,54 @@ static int device_cu_count();
 // One token, K % 64 == 0 up to 16384, 16-byte aligned weights and x, and at
 // most GEMV_BAL_RMAX rows per wave at G workgroups (two per CU for one
 // window per row, one above).
-static bool gemv_bal_grid(const uint32_t *w, const void *x, int B, int K, int N, int *G) {
+static bool gemv_bal_grid(const uint32_t *w, const void *x, int B, int K, int N, int *G,
+                          int rmax = GEMV_BAL_RMAX) {
   if (B != 1 || K % 64 != 0 || K > 4 * 4096 || (reinterpret_cast<uintptr_t>(w) & 15) != 0 ||
       (reinterpret_cast<uintptr_t>(x) & 15) != 0)
     return false;
   const int ni = (K + 4095) / 4096;
   const int g = std::min((ni == 1 ? 2 : 1) * device_cu_count(), (N + 7) / 8);
-  if ((N + g - 1) / g > 8 * GEMV_BAL_RMAX) return false;
+  if ((N + g - 1) / g > 8 * rmax) return false;
   *G = g;
   return true;
 }
 
-template <typename YT, int NI, bool XF32>
+template <typename YT, int NI, bool XF32, bool GRP = false>
 static hipError_t launch_gemv_bal_r(const uint32_t *w, const float *scale, const void *x, void *y, int K, int N, int G,
-                                    hipStream_t stream, const float *bias) {
+                                    hipStream_t stream, const float *bias, const GemvGroup *grp = nullptr) {
   const int rmax = ((N + G - 1) / G + 7) / 8;
-  if (rmax <= 1) return launch_gemv_bal_w<YT, NI, 1, XF32>(w, scale, x, y, K, N, G, stream, bias);
-  if (rmax <= 2) return launch_gemv_bal_w<YT, NI, 2, XF32>(w, scale, x, y, K, N, G, stream, bias);
-  if (rmax <= 3) return launch_gemv_bal_w<YT, NI, 3, XF32>(w, scale, x, y, K, N, G, stream, bias);
-  return launch_gemv_bal_w<YT, NI, 4, XF32>(w, scale, x, y, K, N, G, stream, bias);
+  constexpr int L = GEMV_LINEAR;
+  if (rmax <= 1)
+    return launch_gemv_bal_w<YT, NI, 1, XF32, false, 1, L, GRP>(w, scale, x, y, K, N, G, stream, bias, nullptr,
+                                                                 nullptr, grp);
+  if (rmax <= 2)
+    return launch_gemv_bal_w<YT, NI, 2, XF32, false, 1, L, GRP>(w, scale, x, y, K, N, G, stream, bias, nullptr,
+                                                                 nullptr, grp);
+  if (rmax <= 3)
+    return launch_gemv_bal_w<YT, NI, 3, XF32, false, 1, L, GRP>(w, scale, x, y, K, N, G, stream, bias, nullptr,
+                                                                 nullptr, grp);
+  // groups (gate + up: 22016 rows) take up to GEMV_GROUP_RMAX rows per wave
+  // up to 12288 columns; above, the registers hold 4 rows at most
+  if constexpr (GRP && NI < 4) {
+    if (rmax > 6)
+      return launch_gemv_bal_w<YT, NI, GEMV_GROUP_RMAX, XF32, false, 1, L, GRP>(w, scale, x, y, K, N, G, stream,
+                                                                                 bias, nullptr, nullptr, grp);
+    if (rmax > 4)
+      return launch_gemv_bal_w<YT, NI, 6, XF32, false, 1, L, GRP>(w, scale, x, y, K, N, G, stream, bias, nullptr,
+                                                                   nullptr, grp);
+  }
+  return launch_gemv_bal_w<YT, NI, 4, XF32, false, 1, L, GRP>(w, scale, x, y, K, N, G, stream, bias, nullptr,
+                                                               nullptr, grp);
 }
 
-template <typename YT, bool XF32>
+template <typename YT, bool XF32, bool GRP = false>
 static hipError_t launch_gemv_bal(const uint32_t *w, const float *scale, const void *x, void *y, int K, int N, int G,
-                                  hipStream_t stream, const float *bias) {
+                                  hipStream_t stream, const float *bias, const GemvGroup *grp = nullptr) {
   const int ni = (K + 4095) / 4096;
-  if (ni == 1) return launch_gemv_bal_r<YT, 1, XF32>(w, scale, x, y, K, N, G, stream, bias);
-  if (ni == 2) return launch_gemv_bal_r<YT, 2, XF32>(w, scale, x, y, K, N, G, stream, bias);
-  if (ni == 3) return launch_gemv_bal_r<YT, 3, XF32>(w, scale, x, y, K, N, G, stream, bias);
-  return launch_gemv_bal_r<YT, 4, XF32>(w, scale, x, y, K, N, G, stream, bias);
+  if (ni == 1) return launch_gemv_bal_r<YT, 1, XF32, GRP>(w, scale, x, y, K, N, G, stream, bias, grp);
+  if (ni == 2) return launch_gemv_bal_r<YT, 2, XF32, GRP>(w, scale, x, y, K, N, G, stream, bias, grp);
+  if (ni == 3) return launch_gemv_bal_r<YT, 3, XF32, GRP>(w, scale, x, y, K, N, G, stream, bias, grp);
+  return launch_gemv_bal_r<YT, 4, XF32, GRP>(w, scale, x, y, K, N, G, stream, bias, grp);
 }
 
 // ---- tall single-token GEMV: persistent waves, next group in flight ------
@@ -2016,6 +2102,43 @@ hipError_t launch_gemv(const uint32_t *w, const float *scale, const void *x,
   }
   if (yt_bf16) return launch_gemv_t<float, uint16_t, L>(w, scale, w, scale, x, y, B, K, N, stream, bias);
   return launch_gemv_t<float, float, L>(w, scale, w, scale, x, y, B, K, N, stream, bias);
+}
+
+// Same-x group: at one token, when every matrix suits the balanced kernel
+// (16-byte aligned, K % 64 == 0 up to 16384) and the rows fit its slots, one
+// launch over the concatenated rows; otherwise one launch per matrix.
+hipError_t launch_gemv_group(const void *x, int xt_bf16, int yt_bf16, int B, int K, int count,
+                             const uint32_t *const *w, const float *const *s, void *const *y, const int *N,
+                             hipStream_t stream) {
+  int total = 0;
+  bool one = count >= 1 && count <= GEMV_GROUP_MAX;
+  for (int i = 0; i < count; i++) {
+    total += N[i];
+    one = one && (reinterpret_cast<uintptr_t>(w[i]) & 15) == 0;
+  }
+  int G = 0;
+  if (one && gemv_bal_grid(w[0], x, B, K, total, &G, K > 3 * 4096 ? GEMV_BAL_RMAX : GEMV_GROUP_RMAX)) {
+    GemvGroup g{};
+    int st = 0;
+    for (int i = 0; i < GEMV_GROUP_MAX; i++) {
+      g.w[i] = i < count ? w[i] : w[0];
+      g.s[i] = i < count ? s[i] : s[0];
+      g.y[i] = i < count ? y[i] : y[0];
+      g.start[i] = i < count ? st : 0x7fffffff;
+      if (i < count) st += N[i];
+    }
+    if (xt_bf16) {
+      if (yt_bf16) return launch_gemv_bal<uint16_t, false, true>(w[0], s[0], x, y[0], K, total, G, stream, nullptr, &g);
+      return launch_gemv_bal<float, false, true>(w[0], s[0], x, y[0], K, total, G, stream, nullptr, &g);
+    }
+    if (yt_bf16) return launch_gemv_bal<uint16_t, true, true>(w[0], s[0], x, y[0], K, total, G, stream, nullptr, &g);
+    return launch_gemv_bal<float, true, true>(w[0], s[0], x, y[0], K, total, G, stream, nullptr, &g);
+  }
+  for (int i = 0; i < count; i++) {
+    const hipError_t e = launch_gemv(w[i], s[i], x, xt_bf16, y[i], yt_bf16, B, K, N[i], stream, nullptr);
+    if (e != hipSuccess) return e;
+  }
+  return hipSuccess;
 }
 
 hipError_t launch_gemv_glu(const uint32_t *w_gate, const float *s_gate, const uint32_t *w_up,

@@ -42,6 +42,37 @@ constexpr int GEMV_PLANES_XS_MIN_B = 6;
 // 8 tokens where the staged kernel does not fit (K above its quad limit).
 constexpr int GEMV_DIRECT_MIN_B = 8;
 
+// Up to GEMV_GROUP_MAX matrices with the same K against one x, launched as
+// one GEMV over their concatenated rows (frx_ternary_linear_group).
+constexpr int GEMV_GROUP_MAX = 4;
+struct GemvGroup {
+  const uint32_t *w[GEMV_GROUP_MAX];
+  const float *s[GEMV_GROUP_MAX];
+  void *y[GEMV_GROUP_MAX];
+  int start[GEMV_GROUP_MAX];  // first row of each matrix in the launch; 0x7fffffff past the group
+  // matrix holding launch row r (r below the total)
+  __host__ __device__ __forceinline__ int matrix_of(int r) const {
+    int m = 0;
+#pragma unroll
+    for (int i = 1; i < GEMV_GROUP_MAX; i++) m += r >= start[i] ? 1 : 0;
+    return m;
+  }
+  // members by a run-time index through selects with constant indices (an
+  // indexed access to the by-value kernel argument would copy it to scratch)
+  template <typename T>
+  __host__ __device__ __forceinline__ static T pick(const T (&a)[GEMV_GROUP_MAX], int m) {
+    static_assert(GEMV_GROUP_MAX == 4, "select chain");
+    return m == 0 ? a[0] : m == 1 ? a[1] : m == 2 ? a[2] : a[3];
+  }
+  __host__ __device__ __forceinline__ const uint32_t *w_of(int m) const { return pick(w, m); }
+  __host__ __device__ __forceinline__ const float *s_of(int m) const { return pick(s, m); }
+  __host__ __device__ __forceinline__ void *y_of(int m) const { return pick(y, m); }
+  __host__ __device__ __forceinline__ int start_of(int m) const { return pick(start, m); }
+};
+hipError_t launch_gemv_group(const void *x, int xt_bf16, int yt_bf16, int B, int K, int count,
+                             const uint32_t *const *w, const float *const *s, void *const *y, const int *N,
+                             hipStream_t stream);
+
 // Decode GEMV, B <= 16 tokens (frx_gemv.hip).
 // One bf16 token through the whole-rows kernels (M == 1, H and I multiples
 // of 64 up to 16384): gate/up/act into bf16 hi/lo planes h_planes [2][N],

@@ -135,6 +135,25 @@ frx_status frx_ternary_linear_bias(frx_ctx *ctx, const uint32_t *w,
                                    frx_dtype yt, uint32_t M, uint32_t K,
                                    uint32_t N);
 
+/* ---- same-x group of dense ternary linears -----------------------------------
+ * Several matrices with the same in_cols applied to one x: the decode step's
+ * Q/K/V projections (src/model/cpu_block_attn_res.rs:2254-2263) and the
+ * FFN's gate and up projections (:2319-2320), which the reference issues as
+ * separate gpu_ternary_matmul_vram calls on the same input. For each
+ * i < count: y[i] = x W[i]^T * scale[i], exactly frx_ternary_linear(w[i],
+ * scale[i], x, y[i], M, K, N[i]).
+ *   x [M][K] xt; w[i] [N[i]][K/16] u32; scale[i] [N[i]] f32; y[i] [M][N[i]]
+ *   yt. w, scale, N and y are host arrays of count entries (device pointers
+ *   in w, scale and y); 1 <= count <= 4.
+ * At one token (bf16 or f32 x, K % 64 == 0 up to 16384, 16-byte aligned
+ * weights, x, scales and outputs) the group is one launch over the
+ * matrices' concatenated rows, so x is read once and the launch's fixed
+ * cost is paid once; otherwise each matrix runs as frx_ternary_linear. */
+frx_status frx_ternary_linear_group(frx_ctx *ctx, const void *x, frx_dtype xt, uint32_t M,
+                                    uint32_t K, uint32_t count, const uint32_t *const *w,
+                                    const float *const *scale, const uint32_t *N, void *const *y,
+                                    frx_dtype yt);
+
 /* ---- dense ternary linear with column-block scales --------------------------
  * Replaces ternary_matmul_blocked (src/model/ternary.rs:541-579): each block
  * of block_size input columns has its own scale, shared by all rows, and

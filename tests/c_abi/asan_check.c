@@ -152,6 +152,12 @@ static void check_null_context(void) {
   const frx_status D = FRX_ERR_DEVICE;
   EXPECT(frx_ternary_linear(NULL, NULL, NULL, NULL, FRX_F32, NULL, FRX_F32, 1, 16, 1) == D);
   EXPECT(frx_ternary_linear_bias(NULL, NULL, NULL, NULL, NULL, FRX_F32, NULL, FRX_F32, 1, 16, 1) == D);
+  EXPECT(frx_ternary_linear_group(NULL, NULL, FRX_F32, 1, 16, 1, NULL, NULL, NULL, NULL, FRX_F32) == D);
+  EXPECT(frx_quantize_ternary_blocked(NULL, NULL, FRX_F32, 16, 16, NULL, NULL) == D);
+  EXPECT(frx_dequantize_ternary_blocked(NULL, NULL, NULL, 16, 16, NULL) == D);
+  EXPECT(frx_prune_sparse24(NULL, NULL, FRX_F32, 1, 4, 0, NULL, NULL, NULL, NULL) == D);
+  EXPECT(frx_workspace_stats(NULL, NULL, NULL, NULL) == D);
+  EXPECT(frx_release_retired(NULL) == D);
   EXPECT(frx_sparse24_ternary_linear(NULL, NULL, NULL, NULL, FRX_F32, NULL, FRX_F32, 1, 16, 1) == D);
   EXPECT(frx_ternary_linear_blocked(NULL, NULL, NULL, 16, NULL, FRX_F32, NULL, FRX_F32, 1, 16, 1) == D);
   EXPECT(frx_ternary_sparse_decode(NULL, NULL, NULL, NULL, NULL, 1.0f, NULL, FRX_F32, NULL, FRX_F32, 1, 16, 1) == D);
@@ -210,6 +216,16 @@ static void check_validation(void) {
   EXPECT(frx_ternary_linear_bias(ctx, w, f, f, f, FRX_F32, y, FRX_F32, 1, 24, 1) == FRX_ERR_SHAPE);
   EXPECT(frx_sparse24_ternary_linear(ctx, w, f, f, FRX_F32, y, FRX_F32, 1, 6, 1) == FRX_ERR_SHAPE);
   EXPECT(frx_ternary_linear_blocked(ctx, w, f, 0, f, FRX_F32, y, FRX_F32, 1, 16, 1) != FRX_OK);
+  {
+    const uint32_t *gw[5] = {w, w, w, w, w};
+    const float *gs[5] = {f, f, f, f, f};
+    void *gy[5] = {y, y, y, y, y};
+    const uint32_t gn[5] = {1, 1, 1, 1, 1};
+    EXPECT(frx_ternary_linear_group(ctx, f, FRX_F32, 1, 16, 0, gw, gs, gn, gy, FRX_F32) == FRX_ERR_SHAPE);
+    EXPECT(frx_ternary_linear_group(ctx, f, FRX_F32, 1, 16, 5, gw, gs, gn, gy, FRX_F32) == FRX_ERR_SHAPE);
+    EXPECT(frx_ternary_linear_group(ctx, f, FRX_F32, 1, 20, 2, gw, gs, gn, gy, FRX_F32) == FRX_ERR_SHAPE);
+    EXPECT(frx_ternary_linear_group(ctx, f, FRX_F32, 1, 16, 2, NULL, gs, gn, gy, FRX_F32) == FRX_ERR_SHAPE);
+  }
   EXPECT(frx_ternary_glu(ctx, f, FRX_F32, w, f, w, f, 1, 20, 16, FRX_ACT_SILU, y) == FRX_ERR_SHAPE);
   EXPECT(frx_ternary_ffn(ctx, f, FRX_F32, w, f, w, f, w, f, 1, 16, 20, FRX_ACT_SILU, y, FRX_F32) == FRX_ERR_SHAPE);
   EXPECT(frx_ternary_ffn(ctx, f, FRX_F32, w, f, w, f, w, f, 1, 16, 16, (frx_activation)5, y, FRX_F32) != FRX_OK);

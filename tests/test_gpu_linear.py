@@ -423,3 +423,58 @@ def test_workspaces_grow_geometrically(ctx):
         assert_close_f32(host(y), np.asarray(ref).reshape(160, N))
     finally:
         c.close()
+
+
+@pytest.mark.parametrize("M,K,Ns,xt,yt", [
+    (1, 4096, (11008, 11008), "bf16", "bf16"),      # LLaMA-7B gate + up
+    (1, 4096, (4096, 4096, 4096), "bf16", "f32"),   # Q / K / V
+    (1, 2048, (4096, 1024, 512, 33), "f32", "bf16"),
+    (1, 11008, (4096, 300), "bf16", "f32"),
+    (4, 4096, (1024, 2048), "bf16", "bf16"),        # per-matrix launches
+    (40, 1024, (256, 100, 64), "bf16", "f32"),      # prefill: per-matrix GEMMs
+])
+def test_linear_group_equals_separate_calls(ctx, M, K, Ns, xt, yt):
+    """frx_ternary_linear_group (the Q/K/V and gate/up calls on one x,
+    cpu_block_attn_res.rs:2254-2263, :2319-2320): each output equals the
+    separate frx_ternary_linear call bit for bit (every row is one wave's
+    chain in both, whatever launch it is part of) and the oracle within
+    1e-3."""
+    name = f"group/{M}x{K}x{'_'.join(map(str, Ns))}"
+    xf, xb = synth.activations(name, "x", M, K)
+    if xt == "f32":
+        xf = synth.normal(synth.seed_of(name, "xf"), M * K).reshape(M, K)
+    x = dev_bf16(xb) if xt == "bf16" else dev_f32(xf)
+    ydt = torch.bfloat16 if yt == "bf16" else torch.float32
+    ws, ss, refs, ts = [], [], [], []
+    for i, n in enumerate(Ns):
+        t = synth.ternary_uniform(name, f"w{i}", n, K)
+        w = synth.pack_rows_u32(t)
+        s = synth.row_scales(name, f"s{i}", n, samples=256)
+        ws.append(dev_u32(w))
+        ss.append(dev_f32(s))
+        refs.append(np.asarray(oracle.ternary_matmul_u32(w, s, xf, M, K, n)).reshape(M, n))
+    ys = [torch.full((M, n), float("nan"), dtype=ydt, device="cuda:0") for n in Ns]
+    ctx.ternary_linear_group(x, ws, ss, ys)
+    sep = [torch.empty((M, n), dtype=ydt, device="cuda:0") for n in Ns]
+    for w, s, y in zip(ws, ss, sep):
+        ctx.ternary_linear(w, s, x, y)
+    torch.cuda.synchronize()
+    for y, y2, ref in zip(ys, sep, refs):
+        np.testing.assert_array_equal(host(y), host(y2))
+        if yt == "bf16":
+            assert_bf16_within_1ulp(y.view(torch.int16).cpu().numpy().view(np.uint16), ref)
+        else:
+            assert_close_f32(host(y), ref)
+
+
+def test_linear_group_errors(ctx):
+    x = torch.zeros((1, 64), dtype=torch.bfloat16, device="cuda:0")
+    w = torch.zeros((8, 4), dtype=torch.int32, device="cuda:0")
+    s = torch.zeros(8, dtype=torch.float32, device="cuda:0")
+    y = torch.zeros((1, 8), dtype=torch.float32, device="cuda:0")
+    with pytest.raises(frx.FrxError) as e:
+        ctx.ternary_linear_group(x, [w] * 5, [s] * 5, [y] * 5)
+    assert e.value.kind == "Shape"
+    with pytest.raises(frx.FrxError) as e:
+        ctx.ternary_linear_group(x, [], [], [])
+    assert e.value.kind == "Shape"
