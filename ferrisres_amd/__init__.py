@@ -19,6 +19,7 @@ LIB_PATH = os.path.join(HERE, "libfrx_ternary.so")
 
 FRX_F32, FRX_BF16 = 0, 1
 ACT_SILU, ACT_GELU_TANH, ACT_GELU_TANH_GATE = 0, 1, 2
+GEMV_SPLIT_AUTO, GEMV_SPLIT_ALWAYS, GEMV_SPLIT_NEVER = 0, 1, 2
 FFN_AUTO, FFN_ONE_LAUNCH, FFN_TWO_LAUNCH = 0, 1, 2
 MOE_TERNARY_MOE_LAYER, MOE_CPU_MOE_LAYER = 0, 1
 QUANT_ABSMEAN, QUANT_STE = 0, 1
@@ -92,6 +93,7 @@ _SIGS = {
     "frx_dequantize_ternary_blocked": (_int, [_vp, _vp, _vp, _sz, _u32, _vp]),
     "frx_prune_sparse24": (_int, [_vp, _vp, _int, _u32, _u32, _int, _vp, _vp, _vp, _vp]),
     "frx_ternary_linear_group": (_int, [_vp, _vp, _int, _u32, _u32, _u32, _vp, _vp, _vp, _vp, _int]),
+    "frx_set_gemv_split": (_int, [_vp, _int]),
     "frx_workspace_stats": (_int, [_vp, ctypes.POINTER(_sz), ctypes.POINTER(_sz), ctypes.POINTER(_u32)]),
     "frx_release_retired": (_int, [_vp]),
     "frx_free": (_int, [_vp, _vp]),
@@ -504,6 +506,11 @@ class Context:
         _check(lib().frx_prune_sparse24(self._h, _ptr(w), _dtype_code(w), N, K, int(per_row), _ptr(patterns),
                                         _ptr(signs), _ptr(meta), _ptr(scale)), self._h)
         return patterns, signs, meta, scale
+
+    def set_gemv_split(self, mode: int):
+        """frx_set_gemv_split: GEMV_SPLIT_AUTO, _ALWAYS or _NEVER (the
+        split-K decode GEMV at 2-16 tokens)."""
+        _check(lib().frx_set_gemv_split(self._h, mode), self._h)
 
     def workspace_stats(self):
         """frx_workspace_stats: (live bytes, retired bytes, allocations)."""

@@ -17,7 +17,7 @@ CSRC = os.path.join(HERE, "csrc")
 OUT = os.path.join(HERE, "libfrx_ternary.so")
 BUILD = os.path.join(HERE, "_build")
 
-SOURCES = ["frx_api.cpp", "frx_pack.cpp", "frx_gemv.hip", "frx_gemm.hip", "frx_moe.hip", "frx_ffn.hip", "frx_ingest.hip", "frx_variants.hip"]
+SOURCES = ["frx_api.cpp", "frx_pack.cpp", "frx_gemv.hip", "frx_gemv_sk.hip", "frx_gemm.hip", "frx_moe.hip", "frx_ffn.hip", "frx_ingest.hip", "frx_variants.hip"]
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 COMMON = [

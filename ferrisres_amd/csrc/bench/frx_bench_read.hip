@@ -4,10 +4,11 @@
 // frxb_read: a plain streaming read of a buffer, the ceiling a decode GEMV
 // launch of the same bytes can approach. Two workgroups of 8 waves per
 // compute unit; each wave streams its own contiguous share of the buffer in
-// 1 KB units (16 bytes per lane), issuing up to RD_UNITS = 32 units before it
-// consumes any: every share up to 32 units (buffers up to 128 MiB on 256
+// 1 KB units (16 bytes per lane), issuing up to RD_UNITS = 28 units before it
+// consumes any: every share up to 28 units (buffers up to 112 MiB on 256
 // compute units: the whole weight-size sweep) is one batch with all of its
-// loads in flight at once, and larger shares drain only every 32 units.
+// loads in flight at once, and larger shares drain only every 28 units. 28
+// units (112 VGPRs) keep both workgroups of a compute unit resident.
 // Units past the share are not loaded (wave-uniform branches). The words
 // are XOR-folded (one store, under a condition the data never meets, keeps
 // the loads live). No decode, no arithmetic, no reduction: what is left of
@@ -24,7 +25,7 @@ namespace {
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-constexpr int RD_WAVES = 8, RD_UNITS = 32;
+constexpr int RD_WAVES = 8, RD_UNITS = 28;
 constexpr size_t RD_MAX = 0x80000000u;  // bytes read at most (unit indices fit 32 bits)
 
 __global__ __launch_bounds__(RD_WAVES * 64) void read_kernel(const u32x4 *__restrict__ p, uint32_t nu,

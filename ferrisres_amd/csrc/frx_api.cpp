@@ -87,6 +87,10 @@ struct frx_ctx {
   size_t unit_ws_bytes = 0;
   void *stage_ws = nullptr;  // 16-byte aligned copies of unaligned x / scale / y
   size_t stage_ws_bytes = 0;
+  void *sk_ws = nullptr;  // fp32 partial tiles of the split-K decode GEMV
+  size_t sk_ws_bytes = 0;
+  unsigned *sk_cnt = nullptr;  // its per-row-tile arrival counters (zero between launches)
+  int gemv_split = FRX_GEMV_SPLIT_AUTO;
   unsigned *ffn_bar = nullptr;  // grid-barrier words of the one-launch FFN
   int ffn_mode = FRX_FFN_AUTO;
   int moe_routing = FRX_MOE_TERNARY_MOE_LAYER;
@@ -180,6 +184,8 @@ void frx_destroy(frx_ctx *ctx) {
   if (ctx->router_ws) (void)hipFree(ctx->router_ws);
   if (ctx->unit_ws) (void)hipFree(ctx->unit_ws);
   if (ctx->stage_ws) (void)hipFree(ctx->stage_ws);
+  if (ctx->sk_ws) (void)hipFree(ctx->sk_ws);
+  if (ctx->sk_cnt) (void)hipFree(ctx->sk_cnt);
   if (ctx->ffn_bar) (void)hipFree(ctx->ffn_bar);
   for (void *p : ctx->retired) (void)hipFree(p);
   delete ctx;
@@ -223,6 +229,15 @@ frx_status frx_set_ffn_mode(frx_ctx *ctx, frx_ffn_mode mode) {
   if (mode != FRX_FFN_AUTO && mode != FRX_FFN_ONE_LAUNCH && mode != FRX_FFN_TWO_LAUNCH)
     return fail(ctx, FRX_ERR_UNSUPPORTED, "unknown FFN mode %d", (int)mode);
   ctx->ffn_mode = mode;
+  return FRX_OK;
+}
+
+frx_status frx_set_gemv_split(frx_ctx *ctx, frx_gemv_split mode) {
+  if (!ctx) return FRX_ERR_DEVICE;
+  ctx->err[0] = 0;
+  if (mode != FRX_GEMV_SPLIT_AUTO && mode != FRX_GEMV_SPLIT_ALWAYS && mode != FRX_GEMV_SPLIT_NEVER)
+    return fail(ctx, FRX_ERR_UNSUPPORTED, "unknown split mode %d", (int)mode);
+  ctx->gemv_split = mode;
   return FRX_OK;
 }
 
@@ -363,6 +378,43 @@ static hipError_t unstage_linear(frx_ctx *ctx, const Staged &sg) {
   return hipMemcpyAsync(sg.y_user, sg.y, sg.y_bytes, hipMemcpyDeviceToDevice, ctx->stream);
 }
 
+// Split-K decode GEMV (frx_gemv_sk.hip) for 2-16 tokens: chosen where it
+// measured faster than the whole-K kernels, i.e. f32 activations at
+// K >= 8192, where the f32 stream each compute unit pulls through L1 bounds
+// those (4096x11008, 2 / 4 / 8 / 16 tokens: 11.2 / 11.8 / 13.8 / 17.8 us
+// whole-K against 9.9 / 10.0 / 10.3 / 11.8 us split); at K = 4096 and with
+// bf16 activations the whole-K kernels are ahead. frx_set_gemv_split
+// forces either.
+static bool use_split(const frx_ctx *ctx, uint32_t M, uint32_t K, uint32_t N, frx_dtype xt) {
+  if (M < 2 || M > 16 || ctx->gemv_split == FRX_GEMV_SPLIT_NEVER) return false;
+  if ((size_t)M * K * 4 >= ((size_t)1 << 32) || (N + 127) / 128 > (uint32_t)frx::GEMV_SK_MAX_TILES) return false;
+  if (ctx->gemv_split == FRX_GEMV_SPLIT_ALWAYS) return true;
+  return xt == FRX_F32 && K >= 8192;
+}
+
+// The split-K GEMV's tile counters: allocated and zeroed once per context
+// (the first split-K call, not under graph capture); every launch leaves
+// them zero.
+static frx_status ensure_sk_counters(frx_ctx *ctx) {
+  if (ctx->sk_cnt) return FRX_OK;
+  void *p = nullptr;
+  const size_t bytes = (size_t)frx::GEMV_SK_MAX_TILES * 4;
+  hipError_t e = hipMalloc(&p, bytes);
+  if (e != hipSuccess) return hip_fail(ctx, e, "split-K counter allocation");
+  e = hipMemset(p, 0, bytes);
+  // the legacy stream of hipMemset does not order against a non-blocking
+  // caller stream: wait for it here (first use only)
+  if (e == hipSuccess) e = hipDeviceSynchronize();
+  if (e != hipSuccess) {
+    (void)hipFree(p);
+    return hip_fail(ctx, e, "split-K counter initialisation");
+  }
+  ctx->allocations++;
+  ctx->live_bytes += bytes;
+  ctx->sk_cnt = reinterpret_cast<unsigned *>(p);
+  return FRX_OK;
+}
+
 static frx_status ternary_linear_run(frx_ctx *ctx, const uint32_t *w, const float *scale, const float *bias,
                                      const void *x, frx_dtype xt, void *y, frx_dtype yt, uint32_t M, uint32_t K,
                                      uint32_t N) {
@@ -372,7 +424,16 @@ static frx_status ternary_linear_run(frx_ctx *ctx, const uint32_t *w, const floa
   Staged sg;
   if ((st = stage_linear(ctx, x, xt, scale, y, yt, M, K, N, &sg)) != FRX_OK) return st;
   hipError_t e;
-  if (M <= 16)
+  if (use_split(ctx, M, K, N, xt)) {
+    if ((st = ensure_buffer(ctx, &ctx->sk_ws, &ctx->sk_ws_bytes,
+                            frx::gemv_sk_workspace_bytes((int)K, (int)N, ctx->cus),
+                            "split-K workspace allocation")) != FRX_OK)
+      return st;
+    if ((st = ensure_sk_counters(ctx)) != FRX_OK) return st;
+    e = frx::launch_gemv_sk(w, sg.scale, sg.x, nullptr, xt == FRX_BF16 ? 0 : 1, sg.y, yt == FRX_BF16, (int)M, (int)K,
+                            (int)N, reinterpret_cast<float *>(ctx->sk_ws), ctx->sk_cnt, bias, ctx->cus,
+                            ctx->stream);
+  } else if (M <= 16)
     e = frx::launch_gemv(w, sg.scale, sg.x, xt == FRX_BF16, sg.y, yt == FRX_BF16, (int)M, (int)K, (int)N,
                          ctx->stream, bias);
   else
@@ -413,13 +474,14 @@ frx_status frx_ternary_linear_group(frx_ctx *ctx, const void *x, frx_dtype xt, u
   }
   if (rows > (size_t)0x7FFFFFFF) return fail(ctx, FRX_ERR_SHAPE, "too many rows in the group");
   hipError_t e = hipSuccess;
-  if (M <= 16 && aligned) {
+  if (M == 1 && aligned) {
     int n[frx::GEMV_GROUP_MAX];
     for (uint32_t i = 0; i < count; i++) n[i] = (int)N[i];
     e = frx::launch_gemv_group(x, xt == FRX_BF16, yt == FRX_BF16, (int)M, (int)K, (int)count, w, scale, y, n,
                                ctx->stream);
   } else {
-    // prefill, or sub-slices that need staging: one linear per matrix
+    // several tokens, prefill, or sub-slices that need staging: one linear
+    // per matrix
     for (uint32_t i = 0; i < count; i++)
       if ((st = ternary_linear_run(ctx, w[i], scale[i], nullptr, x, xt, y[i], yt, M, K, N[i])) != FRX_OK) return st;
   }

@@ -73,6 +73,19 @@ hipError_t launch_gemv_group(const void *x, int xt_bf16, int yt_bf16, int B, int
                              const uint32_t *const *w, const float *const *s, void *const *y, const int *N,
                              hipStream_t stream);
 
+// Decode GEMV for 2-16 tokens with K split over workgroups (frx_gemv_sk.hip):
+// 128-row tiles x slices of up to 1024 columns write fp32 partials into
+// `part` (gemv_sk_workspace_bytes); the last slice of each row tile adds
+// them in slice order. counters: one zero-initialised word per 128-row tile
+// (GEMV_SK_MAX_TILES at most), left zero by every launch. xs: 0 bf16 x, 1
+// f32 x, 2 bf16 planes (x hi, x2 lo). K % 16 == 0, x 16-byte aligned,
+// B * K * 4 < 2^32.
+constexpr int GEMV_SK_MAX_TILES = 65536;
+size_t gemv_sk_workspace_bytes(int K, int N, int cus);
+hipError_t launch_gemv_sk(const uint32_t *w, const float *scale, const void *x, const void *x2, int xs,
+                          void *y, int yt_bf16, int B, int K, int N, float *part, unsigned *counters,
+                          const float *bias, int cus, hipStream_t stream);
+
 // Decode GEMV, B <= 16 tokens (frx_gemv.hip).
 // One bf16 token through the whole-rows kernels (M == 1, H and I multiples
 // of 64 up to 16384): gate/up/act into bf16 hi/lo planes h_planes [2][N],

@@ -73,6 +73,14 @@ typedef enum frx_ffn_mode {
   FRX_FFN_MODE_RANGE_ = 0x7fffffff
 } frx_ffn_mode;
 
+/* Decode GEMV kernels at 2-16 tokens (see frx_set_gemv_split). */
+typedef enum frx_gemv_split {
+  FRX_GEMV_SPLIT_AUTO = 0,   /* split K where it measured faster */
+  FRX_GEMV_SPLIT_ALWAYS = 1, /* split K at every 2-16 token call */
+  FRX_GEMV_SPLIT_NEVER = 2,  /* whole-K kernels only */
+  FRX_GEMV_SPLIT_RANGE_ = 0x7fffffff
+} frx_gemv_split;
+
 /* Routing semantics of frx_moe_ternary_ffn (see frx_set_moe_routing). */
 typedef enum frx_moe_routing {
   FRX_MOE_TERNARY_MOE_LAYER = 0, /* TernaryMoELayer and the GPU-path glue */
@@ -378,6 +386,17 @@ frx_status frx_release_retired(frx_ctx *ctx);
  * frx_synchronize, frx_free, frx_set_* and frx_destroy still work. FRX_OK
  * clears it. A status outside frx_status is FRX_ERR_UNSUPPORTED. */
 frx_status frx_force_status(frx_ctx *ctx, frx_status status);
+
+/* Selects the decode GEMV of frx_ternary_linear / _bias / _group at 2-16
+ * tokens on this context (default FRX_GEMV_SPLIT_AUTO). No counterpart in the
+ * reference. The split-K kernel gives each workgroup 128 weight rows and a
+ * slice of 256 to 1024 columns, stages that slice of the activations once
+ * for all 128 rows, and writes fp32 partial sums to a context workspace of
+ * at most ceil(K/256) * 16 * N * 4 bytes (allocated on the first call at a
+ * larger size, not under graph capture); a second launch adds the slices of
+ * each output in slice order. Results differ from the whole-K kernels only
+ * in fp32 summation order. */
+frx_status frx_set_gemv_split(frx_ctx *ctx, frx_gemv_split mode);
 
 /* Selects the execution of frx_ternary_ffn on this context (default
  * FRX_FFN_AUTO). No counterpart in the reference, whose FFN is three

@@ -478,3 +478,53 @@ def test_linear_group_errors(ctx):
     with pytest.raises(frx.FrxError) as e:
         ctx.ternary_linear_group(x, [], [], [])
     assert e.value.kind == "Shape"
+
+
+@pytest.mark.parametrize("M,K,N", [(2, 4096, 11008), (4, 11008, 4096), (16, 11008, 4096), (16, 4096, 11008),
+                                   (5, 1040, 300), (8, 256, 130), (16, 2064, 33), (3, 16, 7)])
+@pytest.mark.parametrize("xt,yt", [("f32", "f32"), ("bf16", "bf16"), ("f32", "bf16")])
+def test_split_k_gemv_parity(ctx, M, K, N, xt, yt):
+    """The split-K decode GEMV (frx_set_gemv_split ALWAYS: 128-row tiles x
+    1024-column slices, fp32 partials added in slice order) against the
+    oracle, K not a multiple of 256 and ragged N included; with a bias; and
+    the whole-K kernels (NEVER) on the same inputs."""
+    name = f"splitk/{M}x{K}x{N}"
+    t, w, s, xf, xb = _case(name, M, K, N)
+    if xt == "f32":
+        xf = synth.normal(synth.seed_of(name, "xf"), M * K).reshape(M, K)
+    ref = np.asarray(oracle.ternary_matmul_u32(w, s, xf, M, K, N)).reshape(M, N)
+    bias = synth.normal(synth.seed_of(name, "b"), N, 0.1)
+    outs = {}
+    try:
+        for mode in (frx.GEMV_SPLIT_ALWAYS, frx.GEMV_SPLIT_NEVER):
+            ctx.set_gemv_split(mode)
+            y = _run(ctx, w, s, xf, xb, xt, yt)
+            yb = torch.empty_like(y)
+            x = dev_bf16(xb) if xt == "bf16" else dev_f32(xf)
+            ctx.ternary_linear(dev_u32(w), dev_f32(s), x, yb, bias=dev_f32(bias))
+            torch.cuda.synchronize()
+            outs[mode] = (y, yb)
+    finally:
+        ctx.set_gemv_split(frx.GEMV_SPLIT_AUTO)
+    for mode, (y, yb) in outs.items():
+        refb = (ref * 1.0 + bias[None, :]).astype(np.float32)
+        if yt == "bf16":
+            assert_bf16_within_1ulp(y.view(torch.int16).cpu().numpy().view(np.uint16), ref)
+            assert_bf16_within_1ulp(yb.view(torch.int16).cpu().numpy().view(np.uint16), refb)
+        else:
+            assert_close_f32(host(y), ref)
+            assert_close_f32(host(yb), refb)
+
+
+@pytest.mark.parametrize("M,K,N", [(16, 11008, 4096), (7, 4096, 1100), (2, 1024, 200)])
+def test_split_k_gemv_bit_exact_on_dyadic_inputs(ctx, M, K, N):
+    """Dyadic activations make every partial sum exact: the split-K kernel
+    equals the f64 product bit for bit, bf16 and f32 activations."""
+    t, w, s, x, xb = _dyadic_case(M, K, N, 7 * M + K + N)
+    ref = (x @ t.T.astype(np.float32)) * s[None, :]
+    try:
+        ctx.set_gemv_split(frx.GEMV_SPLIT_ALWAYS)
+        np.testing.assert_array_equal(host(_run(ctx, w, s, x, xb, "bf16", "f32")), ref)
+        np.testing.assert_array_equal(host(_run(ctx, w, s, x, xb, "f32", "f32")), ref)
+    finally:
+        ctx.set_gemv_split(frx.GEMV_SPLIT_AUTO)
