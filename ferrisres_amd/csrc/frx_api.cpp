@@ -713,12 +713,38 @@ static frx_status check_ffn_down(frx_ctx *ctx, const uint32_t *w_down, const flo
 // aligned). u_ws: the GEMM path's up projection (M > 16; null = the
 // context's workspace). allow_one: the one-launch kernel may run (it needs
 // the context's barrier words).
+// The down launch over h's bf16 planes [2][M][I] at 3-16 tokens: the split-K
+// GEMV (planes staged once per 128-row tile and column slice) where it
+// measured faster, i.e. I >= 8192, and only where the call may allocate its
+// workspace; else the planes kernels of frx_gemv.hip.
+static frx_status ffn_down_planes(frx_ctx *ctx, const uint32_t *w_down, const float *s_down, const uint16_t *hp,
+                                  void *y, frx_dtype yt, uint32_t M, uint32_t H, uint32_t I, bool may_alloc) {
+  const bool split = may_alloc && ctx->gemv_split != FRX_GEMV_SPLIT_NEVER &&
+                     (ctx->gemv_split == FRX_GEMV_SPLIT_ALWAYS || I >= 8192) &&
+                     (H + 127) / 128 <= (uint32_t)frx::GEMV_SK_MAX_TILES && (size_t)M * I * 4 < ((size_t)1 << 32);
+  hipError_t e;
+  if (split) {
+    frx_status st = ensure_buffer(ctx, &ctx->sk_ws, &ctx->sk_ws_bytes,
+                                  frx::gemv_sk_workspace_bytes((int)I, (int)H, ctx->cus), "split-K workspace allocation");
+    if (st != FRX_OK) return st;
+    if ((st = ensure_sk_counters(ctx)) != FRX_OK) return st;
+    e = frx::launch_gemv_sk(w_down, s_down, hp, hp + (size_t)M * I, 2, y, yt == FRX_BF16, (int)M, (int)I, (int)H,
+                            reinterpret_cast<float *>(ctx->sk_ws), ctx->sk_cnt, nullptr, ctx->cus, ctx->stream);
+  } else {
+    e = frx::launch_gemv_planes(w_down, s_down, hp, y, yt == FRX_BF16, (int)M, (int)I, (int)H, ctx->stream);
+  }
+  if (e != hipSuccess) return hip_fail(ctx, e, "ffn down launch");
+  return FRX_OK;
+}
+
 static frx_status ffn_run(frx_ctx *ctx, const void *x, frx_dtype xt, const uint32_t *w_gate, const float *s_gate,
                           const uint32_t *w_up, const float *s_up, const uint32_t *w_down, const float *s_down,
                           uint32_t M, uint32_t H, uint32_t I, frx_activation act, void *y, frx_dtype yt, void *ws,
                           float *u_ws, bool allow_one) {
   hipError_t e;
   const bool two_only = ctx->ffn_mode == FRX_FFN_TWO_LAUNCH || !allow_one;
+  // the one-launch kernel's context (allow_one) is the allocating entry point
+  const bool may_alloc = allow_one;
   if ((!allow_one || ctx->ffn_mode != FRX_FFN_ONE_LAUNCH) && xt == FRX_BF16 && aligned16(w_gate) &&
       aligned16(w_up) && aligned16(w_down) && frx::gemv_rows_ffn_ok((int)M, (int)H, (int)I)) {
     // one token: gate/up/act into bf16 hi/lo planes of h (the first 4*I
@@ -742,6 +768,17 @@ static frx_status ffn_run(frx_ctx *ctx, const void *x, frx_dtype xt, const uint3
     e = frx::launch_gemv_rows4_planes(w_down, s_down, hp, y, yt == FRX_BF16, (int)I, (int)H, ctx->stream);
     if (e != hipSuccess) return hip_fail(ctx, e, "ffn down launch");
     return FRX_OK;
+  }
+  if (ctx->ffn_mode != FRX_FFN_ONE_LAUNCH && xt == FRX_BF16 && aligned16(w_gate) && aligned16(w_up) &&
+      aligned16(w_down) && (M == 3 || M == 4) && frx::gemv_rows4_ffn_ok(2, (int)H, (int)I)) {
+    // three or four tokens: gate/up/act in the 4-segment kernel into h's
+    // planes [2][M][I], then the down launch over both planes (LLaMA-7B
+    // shapes, M = 4: 25.7 us with the operand-load kernels, 19.6 us so)
+    uint16_t *hp = reinterpret_cast<uint16_t *>(ws);
+    e = frx::launch_gemv_rows4_glu_planes(w_gate, s_gate, w_up, s_up, x, hp, (int)M, (int)H, (int)I,
+                                          act == FRX_ACT_GELU_TANH, ctx->stream);
+    if (e != hipSuccess) return hip_fail(ctx, e, "ffn gate/up launch");
+    return ffn_down_planes(ctx, w_down, s_down, hp, y, yt, M, H, I, may_alloc);
   }
   int grid = 0;
   size_t lds = 0;
@@ -779,9 +816,7 @@ static frx_status ffn_run(frx_ctx *ctx, const void *x, frx_dtype xt, const uint3
     e = frx::launch_gemv_glu_planes(w_gate, s_gate, w_up, s_up, x, hp, (int)M, (int)H, (int)I,
                                     act == FRX_ACT_GELU_TANH, ctx->stream);
     if (e != hipSuccess) return hip_fail(ctx, e, "ffn gate/up launch");
-    e = frx::launch_gemv_planes(w_down, s_down, hp, y, yt == FRX_BF16, (int)M, (int)I, (int)H, ctx->stream);
-    if (e != hipSuccess) return hip_fail(ctx, e, "ffn down launch");
-    return FRX_OK;
+    return ffn_down_planes(ctx, w_down, s_down, hp, y, yt, M, H, I, may_alloc);
   }
   float *h = reinterpret_cast<float *>(ws);
   frx_status st = glu_into(ctx, x, xt, w_gate, s_gate, w_up, s_up, M, H, I, act == FRX_ACT_GELU_TANH, h, u_ws);

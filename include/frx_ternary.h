@@ -298,7 +298,9 @@ frx_status frx_ternary_ffn(frx_ctx *ctx, const void *x, frx_dtype xt,
  * No counterpart in the reference. For callers that cannot allocate device
  * memory: code under HIP graph capture, tight serving loops, harnesses that
  * forbid hipMalloc. Same arguments, semantics and kernels as frx_ternary_ffn
- * in FRX_FFN_TWO_LAUNCH execution (whatever frx_set_ffn_mode selected), but
+ * in FRX_FFN_TWO_LAUNCH execution with FRX_GEMV_SPLIT_NEVER (whatever
+ * frx_set_ffn_mode and frx_set_gemv_split selected: the split-K down launch
+ * needs a context workspace), but
  * the intermediate lives in a fixed device array of the library
  * (FRX_NOALLOC_SCRATCH_BYTES per GPU, held until the process ends) and the
  * call allocates nothing. It needs M*I*4 bytes of that array (rounded up to

@@ -1,6 +1,8 @@
 """frx_ternary_ffn_noalloc (intermediate in the library's fixed per-GPU
 scratch array, no device allocation) against frx_ternary_ffn in two-launch
-execution, which runs the same kernels on a context-owned workspace: the
+execution with the whole-K decode GEMVs (FRX_GEMV_SPLIT_NEVER: the split-K
+down launch needs a workspace, so the no-allocation entry never takes it),
+which runs the same kernels on a context-owned workspace: the
 outputs must be identical bit for bit, and both within 1e-3 of the oracle
 (dense FFN branch of cpu_block_attn_res.rs:2317-2326 with per-row scales).
 Two calls in a row on one GPU, the second smaller, then a graph-captured call
@@ -42,6 +44,7 @@ def ctxs():
     assert torch.cuda.is_available(), "GPU tests need a gfx950 device"
     ref = frx.Context(0)
     ref.set_ffn_mode(frx.FFN_TWO_LAUNCH)
+    ref.set_gemv_split(frx.GEMV_SPLIT_NEVER)
     na = frx.Context(0)
     yield ref, na
     na.close()
