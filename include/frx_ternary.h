@@ -66,8 +66,9 @@ typedef enum frx_activation {
 } frx_activation;
 /* How frx_ternary_ffn runs at decode sizes (see frx_set_ffn_mode). */
 typedef enum frx_ffn_mode {
-  FRX_FFN_AUTO = 0,        /* M <= 2: two whole-row launches; M = 3: one
-                              launch where the shape allows; else two */
+  FRX_FFN_AUTO = 0,        /* M <= 4: two whole-row launches where the
+                              shape allows, else the one-launch kernel at
+                              M <= 3 where it allows; otherwise two */
   FRX_FFN_ONE_LAUNCH = 1,  /* one launch or FRX_ERR_UNSUPPORTED */
   FRX_FFN_TWO_LAUNCH = 2,  /* gate/up/act launch + down launch */
   FRX_FFN_MODE_RANGE_ = 0x7fffffff
@@ -267,14 +268,19 @@ frx_status frx_ternary_glu(frx_ctx *ctx, const void *x, frx_dtype xt,
  * Requires H % 16 == 0, I % 16 == 0. The intermediate h = act(g) * u
  * ([M][I]) lives in a context workspace of M*I*4 bytes. Paths, by M and the
  * dtype of x (FRX_FFN_AUTO):
- *  - bf16 x, M = 1 (H, I multiples of 64 up to 16384) or M = 2 (up to
+ *  - bf16 x, M = 1 (H, I multiples of 64 up to 16384) or M = 2 to 4 (up to
  *    14336), 16-byte aligned weights: two launches that read whole weight
- *    rows per wave; h as bf16 hi + lo planes, |h - hi - lo| <= 2^-17 |h|.
- *  - M = 3 (H <= 4096, I <= 11520, multiples of 64, 16-byte aligned
- *    weights; LLaMA-7B's 4096/11008 included): one launch with a grid
- *    barrier between the halves; h as bf16 hi + lo planes (2^-17).
- *  - bf16 x, 4 <= M <= 16: gate/up/act launch writing h as bf16 hi + lo
- *    planes (2^-17), then the down GEMV over both planes.
+ *    rows per wave (4 row segments per MFMA from 2 tokens); h as bf16 hi +
+ *    lo planes, |h - hi - lo| <= 2^-17 |h|. At M = 3 and 4 the down launch
+ *    is the split-K GEMV over both planes (frx_set_gemv_split) where I >=
+ *    8192.
+ *  - bf16 x, 5 <= M <= 16: gate/up/act launch writing h as bf16 hi + lo
+ *    planes (2^-17), then the down GEMV over both planes (split-K where
+ *    I >= 8192).
+ *  - M = 3 in FRX_FFN_ONE_LAUNCH mode (H <= 4096, I <= 11520, multiples of
+ *    64, 16-byte aligned weights): one launch with a grid barrier between
+ *    the halves; h as bf16 hi + lo planes (2^-17). Other M <= 3 shapes that
+ *    the paths above do not take run it in FRX_FFN_AUTO too.
  *  - f32 x at M <= 16, and every other shape at M <= 16: h in fp32, then the
  *    down GEMV with fp32 input, as the reference keeps it.
  *  - M > 16: gate and up GEMMs (the up projection in a second context
@@ -286,7 +292,7 @@ frx_status frx_ternary_glu(frx_ctx *ctx, const void *x, frx_dtype xt,
  * once; if another kernel holds CUs so that they are not, its barrier times
  * out, the outputs are invalid and the next frx_synchronize returns
  * FRX_ERR_GPU. Callers that share the GPU with concurrent kernels select
- * FRX_FFN_TWO_LAUNCH (M = 3 then takes the fp32-h path). */
+ * FRX_FFN_TWO_LAUNCH. */
 frx_status frx_ternary_ffn(frx_ctx *ctx, const void *x, frx_dtype xt,
                            const uint32_t *w_gate, const float *s_gate,
                            const uint32_t *w_up, const float *s_up,

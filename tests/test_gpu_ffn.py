@@ -125,15 +125,16 @@ def test_ffn_single_token_rows_matches_one_launch(ctx):
     assert np.max(np.abs(y_rows - y_one)) <= 1e-4 * rms
 
 
-@pytest.mark.parametrize("M", [4, 5, 7, 8, 16])
+@pytest.mark.parametrize("M", [3, 4, 5, 7, 8, 16])
 @pytest.mark.parametrize("H,I", [(4096, 11008), (2112, 4160), (320, 1088)])
-def test_ffn_bf16_in_bf16_out_4_to_16_tokens(ctx, M, H, I):
-    """bf16 x and bf16 y at 4-16 tokens (the dense FFN branch,
+def test_ffn_bf16_in_bf16_out_3_to_16_tokens(ctx, M, H, I):
+    """bf16 x and bf16 y at 3-16 tokens (the dense FFN branch,
     cpu_block_attn_res.rs:2317-2326): the gate/up/act launch writing h as
-    bf16 hi/lo planes and the down GEMV over both planes with a bf16
-    epilogue, for every planes kernel the dispatcher picks (direct and
-    staged, for gate/up and for down), at LLaMA-7B and ragged shapes;
-    within 1 bf16 ulp of bf16(reference), and the f32 output within 1e-3."""
+    bf16 hi/lo planes (the 4-segment kernel at 3-4 tokens, operand-load and
+    staged kernels above) and the down GEMV over both planes with a bf16
+    epilogue (split-K at I >= 8192, whole-K below), at LLaMA-7B and ragged
+    shapes; within 1 bf16 ulp of bf16(reference), and the f32 output within
+    1e-3."""
     xf, xb, mats = make_ffn(f"ffn/bf16out{M}_{H}_{I}", M, H, I)
     xw = synth.bf16_bits_to_f32(xb)
     ref = ref_ffn(xw, mats, False)
