@@ -1031,22 +1031,55 @@ template <typename YT>
 __global__ __launch_bounds__(256) void moe_combine_kernel(
     const float *__restrict__ dout, const float *__restrict__ dout_lo, const float *__restrict__ wts,
     const int *__restrict__ inv, int H, int top_k, YT *__restrict__ y, int skip_small) {
+  // The token's routes are read once; then per group of up to CK routes all
+  // of their rows (and the second K part) are loaded before any is added, so
+  // a thread waits one memory round trip per group rather than per route.
+  // The additions keep the reference's order: acc from 0, k = 0, 1, ...
+  constexpr int CK = 4, CJ = 2;  // routes per group, column quads per thread
+  __shared__ float sw[64];
+  __shared__ long so[64];
   const int t = blockIdx.x;
-  for (int j = threadIdx.x * 4; j < H; j += 1024) {  // H % 16 == 0
-    f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
-    for (int k = 0; k < top_k; k++) {
+  if ((int)threadIdx.x < top_k) {
+    sw[threadIdx.x] = wts[t * top_k + threadIdx.x];
+    so[threadIdx.x] = (long)inv[t * top_k + threadIdx.x] * H;
+  }
+  __syncthreads();
+  for (int j0 = threadIdx.x * 4; j0 < H; j0 += 1024 * CJ) {  // H % 16 == 0
+    f32x4 acc[CJ];
+#pragma unroll
+    for (int c = 0; c < CJ; c++) acc[c] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+    for (int k0 = 0; k0 < top_k; k0 += CK) {
+      f32x4 d[CK][CJ];
+#pragma unroll
+      for (int q = 0; q < CK; q++)
+#pragma unroll
+        for (int c = 0; c < CJ; c++) {
+          const int j = j0 + c * 1024;
+          d[q][c] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+          if (k0 + q < top_k && j < H) {
+            const long o = so[k0 + q] + j;
+            d[q][c] = *reinterpret_cast<const f32x4 *>(dout + o);
+            if (dout_lo) d[q][c] = d[q][c] + *reinterpret_cast<const f32x4 *>(dout_lo + o);
+          }
+        }
+#pragma unroll
+      for (int q = 0; q < CK; q++) {
 #pragma clang fp contract(off)
-      const float w = wts[t * top_k + k];
-      // CpuMoELayer skips experts whose weight is below 1e-8 in magnitude
-      // (src/model/cpu_moe.rs:172)
-      if (skip_small && fabsf(w) < 1e-8f) continue;
-      const long o = (long)inv[t * top_k + k] * H + j;
-      f32x4 d = *reinterpret_cast<const f32x4 *>(dout + o);
-      if (dout_lo) d = d + *reinterpret_cast<const f32x4 *>(dout_lo + o);
-      const f32x4 prod = d * w;
-      acc = acc + prod;
+        if (k0 + q >= top_k) break;
+        const float w = sw[k0 + q];
+        // CpuMoELayer skips experts whose weight is below 1e-8 in magnitude
+        // (src/model/cpu_moe.rs:172)
+        if (skip_small && fabsf(w) < 1e-8f) continue;
+#pragma unroll
+        for (int c = 0; c < CJ; c++) {
+          const f32x4 prod = d[q][c] * w;
+          acc[c] = acc[c] + prod;
+        }
+      }
     }
-    YStore<YT>::store4(y + (long)t * H + j, acc, 4);
+#pragma unroll
+    for (int c = 0; c < CJ; c++)
+      if (j0 + c * 1024 < H) YStore<YT>::store4(y + (long)t * H + j0 + c * 1024, acc[c], 4);
   }
 }
 #pragma clang fp contract(on)
