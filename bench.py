@@ -394,6 +394,7 @@ def main():
         extra["decode_gemv_f32_in_out"] = f32res
     if B == 1 and not args.no_extra:
         extra["decode_gemv_b1_by_weight_size"] = gemv_size_sweep(torch, ctx, stream, dev)
+        extra["decode_gemv_b1_qkv_3x4096x4096"] = qkv_group(torch, ctx, stream, dev)
     if not args.no_extra:
         extra.update(run_extra(torch, frx, synth, ctx, stream, dev))
 
@@ -645,6 +646,46 @@ def gemv_size_sweep(torch, ctx, stream, dev, reps=40):
         del dst
         del ws, w0, gemv_calls
         torch.cuda.synchronize()
+    return res
+
+
+def qkv_group(torch, ctx, stream, dev, reps=40):
+    """The decode step's Q, K and V projections of one token (three
+    [4096, 4096] ternary matrices against the same bf16 x, bf16 outputs),
+    as three frx_ternary_linear launches and as one frx_ternary_linear_group
+    launch, timed as HIP-graph replays over weight copies totalling >= 0.5 GB.
+    Algorithmic bytes: 3 (N K / 4 + 4 N + 2 N) for the weights, scales and
+    outputs, plus 2 K for x, which the group reads once and the separate
+    launches three times."""
+    n = k = 4096
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(20240611)
+    shifts = (2 * torch.arange(16, device=dev, dtype=torch.int64))
+    base = []
+    for _ in range(3):
+        codes = torch.randint(0, 3, (n, k // 16, 16), generator=gen, device=dev, dtype=torch.int64)
+        w = (codes << shifts).sum(dim=2)
+        base.append(torch.where(w >= 2 ** 31, w - 2 ** 32, w).to(torch.int32))
+    del codes
+    copies = int(np.ceil(512e6 / (3 * n * k // 4))) + 1
+    ws = [[b.clone() for b in base] for _ in range(copies)]
+    s = [torch.full((n,), 0.0159, dtype=torch.float32, device=dev) for _ in range(3)]
+    x = torch.randn((1, k), generator=gen, device=dev).to(torch.bfloat16)
+    ys = [torch.empty((1, n), dtype=torch.bfloat16, device=dev) for _ in range(3)]
+    nbytes = 3 * (n * k // 4 + 4 * n + 2 * n) + 2 * k
+    sep = [(lambda w=w: [ctx.ternary_linear(w[j], s[j], x, ys[j]) for j in range(3)]) for w in ws]
+    grp = [(lambda w=w: ctx.ternary_linear_group(x, w, s, ys)) for w in ws]
+    t_sep, st_sep = _graph_time(torch, stream, sep, reps)
+    t_grp, st_grp = _graph_time(torch, stream, grp, reps)
+    log(f"bench: Q/K/V 3x4096x4096 B=1: three launches {t_sep * 1e6:.2f} us, "
+        f"one group launch {t_grp * 1e6:.2f} us ({nbytes / t_grp / 1e9:.1f} GB/s)")
+    res = {"algorithmic_bytes": nbytes, "weight_copies": copies,
+           "group_launch": {"us": round(t_grp * 1e6, 3), "gb_s": round(nbytes / t_grp / 1e9, 1),
+                            "hbm_fraction": round(nbytes / t_grp / 1e9 / HBM_PEAK_GBS, 4), **st_grp},
+           "three_launches": {"us": round(t_sep * 1e6, 3), "gb_s": round(nbytes / t_sep / 1e9, 1),
+                              "hbm_fraction": round(nbytes / t_sep / 1e9 / HBM_PEAK_GBS, 4), **st_sep}}
+    del ws, base
+    torch.cuda.synchronize()
     return res
 
 

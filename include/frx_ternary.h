@@ -400,10 +400,12 @@ frx_status frx_force_status(frx_ctx *ctx, frx_status status);
  * reference. The split-K kernel gives each workgroup 128 weight rows and a
  * slice of 256 to 1024 columns, stages that slice of the activations once
  * for all 128 rows, and writes fp32 partial sums to a context workspace of
- * at most ceil(K/256) * 16 * N * 4 bytes (allocated on the first call at a
- * larger size, not under graph capture); a second launch adds the slices of
- * each output in slice order. Results differ from the whole-K kernels only
- * in fp32 summation order. */
+ * at most ceil(K/256) * 16 * N4 * 4 bytes (N4 = N rounded up to a multiple
+ * of 4), plus 256 KiB of tile counters (both allocated on the first split
+ * call at a larger size, not under graph capture). The last slice of a row
+ * tile to finish adds the slices of each output in slice order, in the same
+ * launch. Results differ from the whole-K kernels only in fp32 summation
+ * order. */
 frx_status frx_set_gemv_split(frx_ctx *ctx, frx_gemv_split mode);
 
 /* Selects the execution of frx_ternary_ffn on this context (default
