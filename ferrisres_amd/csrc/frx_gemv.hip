@@ -944,14 +944,16 @@ __global__ __launch_bounds__(512) void gemv_bal_kernel(const uint32_t *__restric
 #pragma unroll
   for (int m = 0; m < NW; m++) wr[m] = buffer_rsrc(m ? W2 : W, (uint32_t)N * (uint32_t)kw * 4u);
   // GRP: the rows of the group's matrices, concatenated, are the rows of the
-  // launch; launch row r lives in matrix grp.matrix_of(r) (wave-uniform for
-  // the wave's rows) and is read through a descriptor of its own row, built
+  // launch; launch row r (wave-uniform) is located by scalar selects
+  // (GemvGroup::locate) and read through a descriptor of its own row, built
   // where it is loaded (no arrays of descriptors: they would go to scratch)
   auto grp_row = [&](int rr, const uint32_t *&wp, const float *&sp) {
     const int r = min(row0 + rr, N - 1);
-    const int m = grp.matrix_of(r), l = r - grp.start_of(m);
-    wp = grp.w_of(m) + (size_t)l * (uint32_t)kw;
-    sp = grp.s_of(m) + l;
+    int first;
+    grp.locate(r, wp, sp, first);
+    const int l = r - first;
+    wp += (size_t)l * (uint32_t)kw;
+    sp += l;
   };
   // 1. x pieces (zero past K), then a barrier: all of the CU's x loads are
   //    ahead of its weight loads
