@@ -1290,9 +1290,12 @@ template <typename YT, int RW, int NI>
 __device__ __forceinline__ void rows_stream_group(const uint32_t *lds, const u32x4 (&wv)[RW][NI],
                                                   const float (&sc)[RW], int g, int N, int lane,
                                                   YT *__restrict__ Y, const float *__restrict__ bias) {
-  f32x4 acc[RW];
+  // x is staged K-interleaved (stage_kil) and the words decode in pairs
+  // (unpack32_kil: 11.5 VALU ops per word against 15 in natural order);
+  // each row runs two accumulation chains (even and odd words)
+  f32x4 acc[RW][2];
 #pragma unroll
-  for (int rr = 0; rr < RW; rr++) acc[rr] = (f32x4){0.f, 0.f, 0.f, 0.f};
+  for (int rr = 0; rr < RW; rr++) acc[rr][0] = acc[rr][1] = (f32x4){0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int i = 0; i < NI; i++) {
     u32x4 xb[8];
@@ -1301,13 +1304,13 @@ __device__ __forceinline__ void rows_stream_group(const uint32_t *lds, const u32
     for (int q = 0; q < 8; q++) xb[q] = *reinterpret_cast<const u32x4 *>(xp + 4 * q);
 #pragma unroll
     for (int rr = 0; rr < RW; rr++) {
-      const uint32_t wq[4] = {wv[rr][i].x, wv[rr][i].y, wv[rr][i].z, wv[rr][i].w};
+      u32x4 lo[4], hi[4];
+      unpack32_kil(wv[rr][i].x, wv[rr][i].y, lo[0], hi[0], lo[1], hi[1]);
+      unpack32_kil(wv[rr][i].z, wv[rr][i].w, lo[2], hi[2], lo[3], hi[3]);
 #pragma unroll
       for (int j = 0; j < 4; j++) {
-        u32x4 lo, hi;
-        unpack16_nat(wq[j], lo, hi);
-        acc[rr] = mfma16(lo, xb[2 * j], acc[rr]);
-        acc[rr] = mfma16(hi, xb[2 * j + 1], acc[rr]);
+        acc[rr][j & 1] = mfma16(lo[j], xb[2 * j], acc[rr][j & 1]);
+        acc[rr][j & 1] = mfma16(hi[j], xb[2 * j + 1], acc[rr][j & 1]);
       }
     }
   }
@@ -1316,7 +1319,7 @@ __device__ __forceinline__ void rows_stream_group(const uint32_t *lds, const u32
   float t = 0.f;
 #pragma unroll
   for (int rr = 0; rr < RW; rr++) {
-    const f32x4 A = acc[rr];
+    const f32x4 A = acc[rr][0] + acc[rr][1];
     float v = e == 0 ? A[0] : e == 1 ? A[1] : e == 2 ? A[2] : A[3];
     v = diag ? v : 0.f;
     v += dpp_f32<0xB1>(v);
@@ -1364,10 +1367,13 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_rows_stream_kernel(const uint
   u32x4 wa[RW][NI], wb[RW][NI];
   float sa[RW], sb[RW];
   rows_stream_load<RW, NI>(wr, scale, g, ng, kw, N, lane, wa, sa);
+  // K-interleaved staging (all lanes take part in the exchange; PP and NT
+  // are even, so neighbouring pieces are neighbouring lanes)
 #pragma unroll
   for (int r = 0; r < XR; r++) {
     const int j = tid + r * NT;
-    if (j < PP) *reinterpret_cast<u32x4 *>(lds + (j >> 3) * ROWS_XCH + (j & 7) * 4) = xs[r];
+    const u32x4 v = stage_kil(xs[r], tid);
+    if (j < PP) *reinterpret_cast<u32x4 *>(lds + (j >> 3) * ROWS_XCH + (j & 7) * 4) = v;
   }
   __syncthreads();
   for (; g < ng; g += 2 * stride) {  // wave-uniform; no barrier below
