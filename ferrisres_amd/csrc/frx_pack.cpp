@@ -105,8 +105,9 @@ frx_status frx_pack_sparse24_gpu(const int8_t *w, uint32_t N, uint32_t K, uint32
 // CPU SparseTernaryMatrix layout (src/model/sparse_ternary.rs:52-70: flat
 // group index r*K/4+g, pattern nibble at bits 0-2 / 4-6, sign pair at
 // 2*(g%4) with bit 1 = +1) -> GPU layout (row-aligned words of six 5-bit
-// groups, bit 1 = -1). Pattern ids 6/7 (never produced) are copied as-is;
-// the GPU decode clamps them to 5 (kernels/sparse_ternary.rs:91).
+// groups, bit 1 = -1). Pattern ids 6/7 (never produced) become pattern 0,
+// as SparseTernaryMatrix::to_ternary decodes them (sparse_ternary.rs:172-176),
+// so both layouts decode to the same matrix.
 frx_status frx_sparse24_cpu_to_gpu(const uint8_t *patterns, const uint8_t *signs, uint32_t N, uint32_t K,
                                    uint32_t *meta) {
   if (!patterns || !signs || !meta) return FRX_ERR_SHAPE;
