@@ -115,6 +115,18 @@ def test_single_token_rows_tall(ctx, K, N):
     assert_bf16_within_1ulp(yb.view(torch.int16).cpu().numpy().view(np.uint16), ref)
 
 
+@pytest.mark.parametrize("K,N", [(8192, 28672), (8192, 57344)])
+def test_single_token_tall_llama70b_bit_exact_on_dyadic_inputs(ctx, K, N):
+    """The LLaMA-70B gate projection [28672, 8192] and gate + up stacked
+    [57344, 8192] at one token (the persistent kernel, bf16 and f32 outputs):
+    every output equals the exact sum (bf16: its round-to-nearest-even)."""
+    t, w, s, x, xb = _dyadic_case(1, K, N, K + N)
+    ref = (x @ t.T.astype(np.float32)) * s[None, :]
+    np.testing.assert_array_equal(host(_run(ctx, w, s, x, xb, "bf16", "f32")), ref)
+    yb = _run(ctx, w, s, x, xb, "bf16", "bf16")
+    np.testing.assert_array_equal(yb.view(torch.int16).cpu().numpy().view(np.uint16), synth.f32_to_bf16_bits(ref))
+
+
 @pytest.mark.parametrize("K,N", [(4160, 300), (12352, 40), (4096, 64), (4160, 16390)])
 def test_single_token_rows_bit_exact_on_dyadic_inputs(ctx, K, N):
     t, w, s, x, xb = _dyadic_case(1, K, N, K + N)
