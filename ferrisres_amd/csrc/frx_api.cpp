@@ -63,6 +63,7 @@ hipError_t noalloc_scratch_ptr(int device, void **out) {
 struct frx_ctx {
   int device = 0;
   hipStream_t stream = nullptr;
+  hipEvent_t handoff = nullptr;  // orders a new stream after the previous one (frx_set_stream)
   char err[512] = {0};
   // Workspaces replaced by larger ones stay allocated until frx_destroy: a
   // graph captured at a smaller size still holds their addresses.
@@ -175,6 +176,10 @@ frx_status frx_create(int device, frx_ctx **out) {
 void frx_destroy(frx_ctx *ctx) {
   if (!ctx) return;
   (void)hipSetDevice(ctx->device);
+  // the buffers below may still be read by work enqueued on the context's
+  // stream (which frx_set_stream ordered after any earlier stream's)
+  (void)hipStreamSynchronize(ctx->stream);
+  if (ctx->handoff) (void)hipEventDestroy(ctx->handoff);
   if (ctx->scratch) (void)hipFree(ctx->scratch);
   if (ctx->moe_ws) (void)hipFree(ctx->moe_ws);
   if (ctx->lora_tbl) (void)hipFree(ctx->lora_tbl);
@@ -193,7 +198,22 @@ void frx_destroy(frx_ctx *ctx) {
 
 frx_status frx_set_stream(frx_ctx *ctx, void *hip_stream) {
   if (!ctx) return FRX_ERR_DEVICE;
-  ctx->stream = reinterpret_cast<hipStream_t>(hip_stream);
+  const hipStream_t next = reinterpret_cast<hipStream_t>(hip_stream);
+  if (next == ctx->stream) return FRX_OK;
+  // The context's workspaces serve one stream at a time: the new stream
+  // waits (on the device, without blocking the host) for the work already
+  // enqueued on the previous one. Streams under graph capture are left as
+  // they are (an event would join the capture).
+  hipStreamCaptureStatus a = hipStreamCaptureStatusNone, b = hipStreamCaptureStatusNone;
+  hipError_t e = hipStreamIsCapturing(ctx->stream, &a);
+  if (e == hipSuccess) e = hipStreamIsCapturing(next, &b);
+  if (e == hipSuccess && a == hipStreamCaptureStatusNone && b == hipStreamCaptureStatusNone) {
+    if (!ctx->handoff) e = hipEventCreateWithFlags(&ctx->handoff, hipEventDisableTiming);
+    if (e == hipSuccess) e = hipEventRecord(ctx->handoff, ctx->stream);
+    if (e == hipSuccess) e = hipStreamWaitEvent(next, ctx->handoff, 0);
+  }
+  if (e != hipSuccess) return hip_fail(ctx, e, "stream hand-off");
+  ctx->stream = next;
   return FRX_OK;
 }
 

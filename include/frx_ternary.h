@@ -96,7 +96,11 @@ typedef enum frx_moe_routing {
 frx_status frx_create(int device, frx_ctx **out);
 void frx_destroy(frx_ctx *ctx);
 /* Caller-owned hipStream_t (NULL = the device's null stream); the analogue of
- * the caller-owned CommandEncoder in TernaryMatMulOp::dispatch. */
+ * the caller-owned CommandEncoder in TernaryMatMulOp::dispatch. Switching to
+ * another stream makes it wait, on the device, for the work already enqueued
+ * on the previous one (the context's workspaces serve one stream at a time);
+ * not while either stream is being captured into a graph. frx_destroy waits
+ * for the context's stream before it frees the workspaces. */
 frx_status frx_set_stream(frx_ctx *ctx, void *hip_stream);
 /* Waits for all work enqueued on the context's stream. Returns FRX_ERR_GPU
  * if a one-launch FFN since the last call timed out at its grid barrier

@@ -540,3 +540,31 @@ def test_split_k_gemv_bit_exact_on_dyadic_inputs(ctx, M, K, N):
         np.testing.assert_array_equal(host(_run(ctx, w, s, x, xb, "f32", "f32")), ref)
     finally:
         ctx.set_gemv_split(frx.GEMV_SPLIT_AUTO)
+
+
+def test_stream_switch_orders_workspace_use():
+    """frx_set_stream makes the new stream wait for the work already enqueued
+    on the previous one, so two split-K calls on one context, the second on
+    another stream right after the switch, do not share the partial-sum
+    workspace and counters at the same time: both outputs stay exact."""
+    c = frx.Context(0)
+    sa, sb = torch.cuda.Stream(), torch.cuda.Stream()
+    try:
+        c.set_gemv_split(frx.GEMV_SPLIT_ALWAYS)
+        cases = [_dyadic_case(16, 11008, 4096, 91), _dyadic_case(16, 11008, 4096, 92)]
+        dev = [(dev_u32(w), dev_f32(s), dev_f32(x)) for (t, w, s, x, xb) in cases]
+        refs = [(x @ t.T.astype(np.float32)) * s[None, :] for (t, w, s, x, xb) in cases]
+        torch.cuda.synchronize()
+        for rep in range(3):
+            ys = [torch.full((16, 4096), float("nan"), device="cuda:0") for _ in cases]
+            torch.cuda.synchronize()
+            for i, (st, (w, s, x)) in enumerate(zip((sa, sb), dev)):
+                c.set_stream(st)
+                with torch.cuda.stream(st):
+                    c.ternary_linear(w, s, x, ys[i])
+            torch.cuda.synchronize()
+            for y, ref in zip(ys, refs):
+                np.testing.assert_array_equal(host(y), ref)
+            c.set_stream(sa)
+    finally:
+        c.close()
