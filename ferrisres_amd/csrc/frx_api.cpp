@@ -409,7 +409,12 @@ static bool use_split(const frx_ctx *ctx, uint32_t M, uint32_t K, uint32_t N, fr
   if (M < 2 || M > 16 || ctx->gemv_split == FRX_GEMV_SPLIT_NEVER) return false;
   if ((size_t)M * K * 4 >= ((size_t)1 << 32) || (N + 127) / 128 > (uint32_t)frx::GEMV_SK_MAX_TILES) return false;
   if (ctx->gemv_split == FRX_GEMV_SPLIT_ALWAYS) return true;
-  return xt == FRX_F32 && K >= 8192;
+  // where it measured faster: f32 x from 8192 columns (every whole-K tile
+  // streams all of x); bf16 x from 5 tokens at 14336 columns and from 3
+  // tokens above 16384 (8192 x 28672, B = 16: 38.1 -> 26.8 us), with enough
+  // 128-row tiles to fill the grid (at N = 2048 the slices get too thin)
+  if (xt == FRX_F32) return K >= 8192;
+  return N >= 3072 && ((M >= 5 && K >= 14336) || (M >= 3 && K > 16384));
 }
 
 // The split-K GEMV's tile counters: allocated and zeroed once per context

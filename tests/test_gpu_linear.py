@@ -568,3 +568,16 @@ def test_stream_switch_orders_workspace_use():
             c.set_stream(sa)
     finally:
         c.close()
+
+
+@pytest.mark.parametrize("M,K,N", [(5, 28672, 8192), (16, 28672, 8192), (3, 16448, 4096), (8, 14336, 4096),
+                                   (16, 14336, 3072)])
+def test_auto_split_bf16_bit_exact_on_dyadic_inputs(ctx, M, K, N):
+    """bf16 activations at 3-16 tokens over long rows take the split-K GEMV
+    under FRX_GEMV_SPLIT_AUTO (the LLaMA-70B down projection 8192 x 28672
+    among them): dyadic inputs, exact sums, f32 and bf16 outputs."""
+    t, w, s, x, xb = _dyadic_case(M, K, N, 5 * M + K + N)
+    ref = (x @ t.T.astype(np.float32)) * s[None, :]
+    np.testing.assert_array_equal(host(_run(ctx, w, s, x, xb, "bf16", "f32")), ref)
+    yb = _run(ctx, w, s, x, xb, "bf16", "bf16")
+    np.testing.assert_array_equal(yb.view(torch.int16).cpu().numpy().view(np.uint16), synth.f32_to_bf16_bits(ref))
