@@ -76,9 +76,9 @@ typedef enum frx_ffn_mode {
 
 /* Decode GEMV kernels at 2-16 tokens (see frx_set_gemv_split). */
 typedef enum frx_gemv_split {
-  FRX_GEMV_SPLIT_AUTO = 0,   /* split K where it measured faster: f32 x from 8192 columns; bf16 x
-                                from 5 tokens at 14336 columns and from 3 tokens above 16384,
-                                at least 3072 rows */
+  FRX_GEMV_SPLIT_AUTO = 0,   /* split K where it measured faster: f32 x from 8192 columns (one
+                                token: above 16384); bf16 x from 5 tokens at 14336 columns and
+                                from 3 tokens above 16384, at least 3072 rows */
   FRX_GEMV_SPLIT_ALWAYS = 1, /* split K at every 2-16 token call */
   FRX_GEMV_SPLIT_NEVER = 2,  /* whole-K kernels only */
   FRX_GEMV_SPLIT_RANGE_ = 0x7fffffff
@@ -402,7 +402,8 @@ frx_status frx_release_retired(frx_ctx *ctx);
 frx_status frx_force_status(frx_ctx *ctx, frx_status status);
 
 /* Selects the decode GEMV of frx_ternary_linear / _bias / _group at 2-16
- * tokens on this context (default FRX_GEMV_SPLIT_AUTO). No counterpart in the
+ * tokens (and at one f32 token above 16384 columns) on this context (default
+ * FRX_GEMV_SPLIT_AUTO). No counterpart in the
  * reference. The split-K kernel gives each workgroup 128 weight rows and a
  * slice of 256 to 1024 columns, stages that slice of the activations once
  * for all 128 rows, and writes fp32 partial sums to a context workspace of

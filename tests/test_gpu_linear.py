@@ -581,3 +581,18 @@ def test_auto_split_bf16_bit_exact_on_dyadic_inputs(ctx, M, K, N):
     np.testing.assert_array_equal(host(_run(ctx, w, s, x, xb, "bf16", "f32")), ref)
     yb = _run(ctx, w, s, x, xb, "bf16", "bf16")
     np.testing.assert_array_equal(yb.view(torch.int16).cpu().numpy().view(np.uint16), synth.f32_to_bf16_bits(ref))
+
+
+@pytest.mark.parametrize("K,N", [(28672, 8192), (16448, 3000)])
+def test_auto_split_one_f32_token_long_rows(ctx, K, N):
+    """One f32 token past 16384 columns takes the split-K GEMV under
+    FRX_GEMV_SPLIT_AUTO: dyadic inputs give the exact sums, with and without
+    a bias (added after the scale)."""
+    t, w, s, x, xb = _dyadic_case(1, K, N, K + 3 * N)
+    ref = (x @ t.T.astype(np.float32)) * s[None, :]
+    np.testing.assert_array_equal(host(_run(ctx, w, s, x, xb, "f32", "f32")), ref)
+    bias = (np.arange(N) % 7 - 3).astype(np.float32) / 4
+    y = torch.full((1, N), float("nan"), device="cuda:0")
+    ctx.ternary_linear(dev_u32(w), dev_f32(s), dev_f32(x), y, bias=dev_f32(bias))
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(host(y), ref + bias[None, :])
