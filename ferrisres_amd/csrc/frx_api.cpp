@@ -405,11 +405,14 @@ static hipError_t unstage_linear(frx_ctx *ctx, const Staged &sg) {
 // whole-K against 9.9 / 10.0 / 10.3 / 11.8 us split); at K = 4096 and with
 // bf16 activations the whole-K kernels are ahead. frx_set_gemv_split
 // forces either.
-static bool use_split(const frx_ctx *ctx, uint32_t M, uint32_t K, uint32_t N, frx_dtype xt) {
-  // one f32 token past the balanced kernel's 16384 columns: its 16-row tiles
-  // stream all of x per tile (8192 x 28672: 40.7 -> 26.5 us split)
-  if (M == 1 && xt == FRX_F32 && K > 16384 && ctx->gemv_split != FRX_GEMV_SPLIT_NEVER &&
-      (size_t)K * 4 < ((size_t)1 << 32) && (N + 127) / 128 <= (uint32_t)frx::GEMV_SK_MAX_TILES)
+static bool use_split(const frx_ctx *ctx, const uint32_t *w, const void *x, uint32_t M, uint32_t K, uint32_t N,
+                      frx_dtype xt) {
+  // one f32 token that the balanced kernel does not take (past its 16384
+  // columns, or more rows than its slots): the 16-row tiles that would run
+  // instead stream all of x per tile (8192 x 28672: 40.7 -> 26.5 us split)
+  if (M == 1 && xt == FRX_F32 && ctx->gemv_split != FRX_GEMV_SPLIT_NEVER &&
+      !frx::gemv_bal_fits(w, x, 1, (int)K, (int)N) && (size_t)K * 4 < ((size_t)1 << 32) &&
+      (N + 127) / 128 <= (uint32_t)frx::GEMV_SK_MAX_TILES)
     return true;
   if (M < 2 || M > 16 || ctx->gemv_split == FRX_GEMV_SPLIT_NEVER) return false;
   if ((size_t)M * K * 4 >= ((size_t)1 << 32) || (N + 127) / 128 > (uint32_t)frx::GEMV_SK_MAX_TILES) return false;
@@ -445,6 +448,30 @@ static frx_status ensure_sk_counters(frx_ctx *ctx) {
   return FRX_OK;
 }
 
+// y = x W^T * scale (+ bias) on aligned operands: the split-K GEMV where
+// use_split picks it (allocating its workspace on first use), else the
+// decode GEMVs up to 16 tokens and the GEMM above.
+static frx_status gemv_auto(frx_ctx *ctx, const uint32_t *w, const float *scale, const float *bias, const void *x,
+                            frx_dtype xt, void *y, frx_dtype yt, uint32_t M, uint32_t K, uint32_t N) {
+  frx_status st;
+  hipError_t e;
+  if (use_split(ctx, w, x, M, K, N, xt)) {
+    if ((st = ensure_buffer(ctx, &ctx->sk_ws, &ctx->sk_ws_bytes,
+                            frx::gemv_sk_workspace_bytes((int)K, (int)N, ctx->cus),
+                            "split-K workspace allocation")) != FRX_OK)
+      return st;
+    if ((st = ensure_sk_counters(ctx)) != FRX_OK) return st;
+    e = frx::launch_gemv_sk(w, scale, x, nullptr, xt == FRX_BF16 ? 0 : 1, y, yt == FRX_BF16, (int)M, (int)K, (int)N,
+                            reinterpret_cast<float *>(ctx->sk_ws), ctx->sk_cnt, bias, ctx->cus, ctx->stream);
+  } else if (M <= 16)
+    e = frx::launch_gemv(w, scale, x, xt == FRX_BF16, y, yt == FRX_BF16, (int)M, (int)K, (int)N, ctx->stream, bias);
+  else
+    e = frx::launch_gemm(w, scale, x, xt == FRX_BF16, y, yt == FRX_BF16, (int)M, (int)K, (int)N, 0, ctx->stream,
+                         bias);
+  if (e != hipSuccess) return hip_fail(ctx, e, "ternary_linear launch");
+  return FRX_OK;
+}
+
 static frx_status ternary_linear_run(frx_ctx *ctx, const uint32_t *w, const float *scale, const float *bias,
                                      const void *x, frx_dtype xt, void *y, frx_dtype yt, uint32_t M, uint32_t K,
                                      uint32_t N) {
@@ -453,23 +480,8 @@ static frx_status ternary_linear_run(frx_ctx *ctx, const uint32_t *w, const floa
   if ((st = check_linear(ctx, w, scale, x, xt, y, yt, M, K, N, false)) != FRX_OK) return st;
   Staged sg;
   if ((st = stage_linear(ctx, x, xt, scale, y, yt, M, K, N, &sg)) != FRX_OK) return st;
-  hipError_t e;
-  if (use_split(ctx, M, K, N, xt)) {
-    if ((st = ensure_buffer(ctx, &ctx->sk_ws, &ctx->sk_ws_bytes,
-                            frx::gemv_sk_workspace_bytes((int)K, (int)N, ctx->cus),
-                            "split-K workspace allocation")) != FRX_OK)
-      return st;
-    if ((st = ensure_sk_counters(ctx)) != FRX_OK) return st;
-    e = frx::launch_gemv_sk(w, sg.scale, sg.x, nullptr, xt == FRX_BF16 ? 0 : 1, sg.y, yt == FRX_BF16, (int)M, (int)K,
-                            (int)N, reinterpret_cast<float *>(ctx->sk_ws), ctx->sk_cnt, bias, ctx->cus,
-                            ctx->stream);
-  } else if (M <= 16)
-    e = frx::launch_gemv(w, sg.scale, sg.x, xt == FRX_BF16, sg.y, yt == FRX_BF16, (int)M, (int)K, (int)N,
-                         ctx->stream, bias);
-  else
-    e = frx::launch_gemm(w, sg.scale, sg.x, xt == FRX_BF16, sg.y, yt == FRX_BF16, (int)M, (int)K, (int)N, 0,
-                         ctx->stream, bias);
-  if (e == hipSuccess) e = unstage_linear(ctx, sg);
+  if ((st = gemv_auto(ctx, w, sg.scale, bias, sg.x, xt, sg.y, yt, M, K, N)) != FRX_OK) return st;
+  const hipError_t e = unstage_linear(ctx, sg);
   if (e != hipSuccess) return hip_fail(ctx, e, "ternary_linear launch");
   return FRX_OK;
 }
@@ -504,14 +516,14 @@ frx_status frx_ternary_linear_group(frx_ctx *ctx, const void *x, frx_dtype xt, u
   }
   if (rows > (size_t)0x7FFFFFFF) return fail(ctx, FRX_ERR_SHAPE, "too many rows in the group");
   hipError_t e = hipSuccess;
-  if (M == 1 && aligned) {
-    int n[frx::GEMV_GROUP_MAX];
-    for (uint32_t i = 0; i < count; i++) n[i] = (int)N[i];
+  int n[frx::GEMV_GROUP_MAX];
+  for (uint32_t i = 0; i < count; i++) n[i] = (int)N[i];
+  if (M == 1 && aligned && frx::gemv_group_fits(x, 1, (int)K, (int)count, w, n)) {
     e = frx::launch_gemv_group(x, xt == FRX_BF16, yt == FRX_BF16, (int)M, (int)K, (int)count, w, scale, y, n,
                                ctx->stream);
   } else {
-    // several tokens, prefill, or sub-slices that need staging: one linear
-    // per matrix
+    // several tokens, prefill, shapes past the one-launch group, or
+    // sub-slices that need staging: one linear per matrix
     for (uint32_t i = 0; i < count; i++)
       if ((st = ternary_linear_run(ctx, w[i], scale[i], nullptr, x, xt, y[i], yt, M, K, N[i])) != FRX_OK) return st;
   }
@@ -851,6 +863,9 @@ static frx_status ffn_run(frx_ctx *ctx, const void *x, frx_dtype xt, const uint3
   float *h = reinterpret_cast<float *>(ws);
   frx_status st = glu_into(ctx, x, xt, w_gate, s_gate, w_up, s_up, M, H, I, act == FRX_ACT_GELU_TANH, h, u_ws);
   if (st != FRX_OK) return st;
+  // fp32 h: the allocating entry takes the split-K down launch where it is
+  // faster (long rows of h)
+  if (may_alloc) return gemv_auto(ctx, w_down, s_down, nullptr, h, FRX_F32, y, yt, M, I, H);
   if (M <= 16)
     e = frx::launch_gemv(w_down, s_down, h, 0, y, yt == FRX_BF16, (int)M, (int)I, (int)H, ctx->stream);
   else

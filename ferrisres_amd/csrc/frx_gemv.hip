@@ -1215,6 +1215,11 @@ static bool gemv_bal_grid(const uint32_t *w, const void *x, int B, int K, int N,
   return true;
 }
 
+bool gemv_bal_fits(const uint32_t *w, const void *x, int B, int K, int N) {
+  int G = 0;
+  return gemv_bal_grid(w, x, B, K, N, &G);
+}
+
 template <typename YT, int NI, bool XF32, bool GRP = false>
 static hipError_t launch_gemv_bal_r(const uint32_t *w, const float *scale, const void *x, void *y, int K, int N, int G,
                                     hipStream_t stream, const float *bias, const GemvGroup *grp = nullptr) {
@@ -2115,17 +2120,27 @@ hipError_t launch_gemv(const uint32_t *w, const float *scale, const void *x,
 // Same-x group: at one token, when every matrix suits the balanced kernel
 // (16-byte aligned, K % 64 == 0 up to 16384) and the rows fit its slots, one
 // launch over the concatenated rows; otherwise one launch per matrix.
+static bool gemv_group_grid(const void *x, int B, int K, int count, const uint32_t *const *w, const int *N,
+                            int *total, int *G) {
+  *total = 0;
+  bool one = count >= 1 && count <= GEMV_GROUP_MAX;
+  for (int i = 0; i < count; i++) {
+    *total += N[i];
+    one = one && (reinterpret_cast<uintptr_t>(w[i]) & 15) == 0;
+  }
+  return one && gemv_bal_grid(w[0], x, B, K, *total, G, K > 3 * 4096 ? GEMV_BAL_RMAX : GEMV_GROUP_RMAX);
+}
+
+bool gemv_group_fits(const void *x, int B, int K, int count, const uint32_t *const *w, const int *N) {
+  int total = 0, G = 0;
+  return gemv_group_grid(x, B, K, count, w, N, &total, &G);
+}
+
 hipError_t launch_gemv_group(const void *x, int xt_bf16, int yt_bf16, int B, int K, int count,
                              const uint32_t *const *w, const float *const *s, void *const *y, const int *N,
                              hipStream_t stream) {
-  int total = 0;
-  bool one = count >= 1 && count <= GEMV_GROUP_MAX;
-  for (int i = 0; i < count; i++) {
-    total += N[i];
-    one = one && (reinterpret_cast<uintptr_t>(w[i]) & 15) == 0;
-  }
-  int G = 0;
-  if (one && gemv_bal_grid(w[0], x, B, K, total, &G, K > 3 * 4096 ? GEMV_BAL_RMAX : GEMV_GROUP_RMAX)) {
+  int total = 0, G = 0;
+  if (gemv_group_grid(x, B, K, count, w, N, &total, &G)) {
     GemvGroup g{};
     int st = 0;
     for (int i = 0; i < GEMV_GROUP_MAX; i++) {

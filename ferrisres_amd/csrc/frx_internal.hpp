@@ -86,6 +86,10 @@ struct GemvGroup {
     }
   }
 };
+// The group runs as one balanced launch (one token, aligned operands, K %
+// 64 == 0 up to 16384, rows within the slots); else launch_gemv_group runs
+// one launch per matrix.
+bool gemv_group_fits(const void *x, int B, int K, int count, const uint32_t *const *w, const int *N);
 hipError_t launch_gemv_group(const void *x, int xt_bf16, int yt_bf16, int B, int K, int count,
                              const uint32_t *const *w, const float *const *s, void *const *y, const int *N,
                              hipStream_t stream);
@@ -98,6 +102,9 @@ hipError_t launch_gemv_group(const void *x, int xt_bf16, int yt_bf16, int B, int
 // f32 x, 2 bf16 planes (x hi, x2 lo). K % 16 == 0, x 16-byte aligned,
 // B * K * 4 < 2^32.
 constexpr int GEMV_SK_MAX_TILES = 65536;
+// The balanced one-token kernel takes this launch (one token, K % 64 == 0
+// up to 16384, aligned operands, rows within its per-wave slots).
+bool gemv_bal_fits(const uint32_t *w, const void *x, int B, int K, int N);
 size_t gemv_sk_workspace_bytes(int K, int N, int cus);
 hipError_t launch_gemv_sk(const uint32_t *w, const float *scale, const void *x, const void *x2, int xs,
                           void *y, int yt_bf16, int B, int K, int N, float *part, unsigned *counters,
