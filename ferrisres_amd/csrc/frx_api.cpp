@@ -398,13 +398,11 @@ static hipError_t unstage_linear(frx_ctx *ctx, const Staged &sg) {
   return hipMemcpyAsync(sg.y_user, sg.y, sg.y_bytes, hipMemcpyDeviceToDevice, ctx->stream);
 }
 
-// Split-K decode GEMV (frx_gemv_sk.hip) for 2-16 tokens: chosen where it
-// measured faster than the whole-K kernels, i.e. f32 activations at
-// K >= 8192, where the f32 stream each compute unit pulls through L1 bounds
-// those (4096x11008, 2 / 4 / 8 / 16 tokens: 11.2 / 11.8 / 13.8 / 17.8 us
-// whole-K against 9.9 / 10.0 / 10.3 / 11.8 us split); at K = 4096 and with
-// bf16 activations the whole-K kernels are ahead. frx_set_gemv_split
-// forces either.
+// Split-K decode GEMV (frx_gemv_sk.hip): chosen where it measured faster
+// than the whole-K kernels (below); the f32 stream each compute unit pulls
+// through L1 bounds those (4096x11008, 2 / 4 / 8 / 16 tokens: 11.2 / 11.8 /
+// 13.8 / 17.8 us whole-K against 9.9 / 10.0 / 10.3 / 11.8 us split).
+// frx_set_gemv_split forces either.
 static bool use_split(const frx_ctx *ctx, const uint32_t *w, const void *x, uint32_t M, uint32_t K, uint32_t N,
                       frx_dtype xt) {
   // one f32 token that the balanced kernel does not take (past its 16384
@@ -417,11 +415,12 @@ static bool use_split(const frx_ctx *ctx, const uint32_t *w, const void *x, uint
   if (M < 2 || M > 16 || ctx->gemv_split == FRX_GEMV_SPLIT_NEVER) return false;
   if ((size_t)M * K * 4 >= ((size_t)1 << 32) || (N + 127) / 128 > (uint32_t)frx::GEMV_SK_MAX_TILES) return false;
   if (ctx->gemv_split == FRX_GEMV_SPLIT_ALWAYS) return true;
-  // where it measured faster: f32 x from 8192 columns (every whole-K tile
-  // streams all of x); bf16 x from 5 tokens at 14336 columns and from 3
+  // where it measured faster: f32 x above 4096 columns (every whole-K tile
+  // streams all of x: 13824 x 5120, B = 16: 23.0 -> 15.4 us; at 4096 the
+  // whole-K kernels stay ahead); bf16 x from 5 tokens at 14336 columns and from 3
   // tokens above 16384 (8192 x 28672, B = 16: 38.1 -> 26.8 us), with enough
   // 128-row tiles to fill the grid (at N = 2048 the slices get too thin)
-  if (xt == FRX_F32) return K >= 8192;
+  if (xt == FRX_F32) return K > 4096;
   return N >= 3072 && ((M >= 5 && K >= 14336) || (M >= 3 && K > 16384));
 }
 

@@ -76,9 +76,10 @@ typedef enum frx_ffn_mode {
 
 /* Decode GEMV kernels at 2-16 tokens (see frx_set_gemv_split). */
 typedef enum frx_gemv_split {
-  FRX_GEMV_SPLIT_AUTO = 0,   /* split K where it measured faster: f32 x from 8192 columns (one
-                                token: above 16384); bf16 x from 5 tokens at 14336 columns and
-                                from 3 tokens above 16384, at least 3072 rows */
+  FRX_GEMV_SPLIT_AUTO = 0,   /* split K where it measured faster: f32 x above 4096 columns (one
+                                token: where the balanced kernel does not apply); bf16 x from 5
+                                tokens at 14336 columns and from 3 tokens above 16384, at least
+                                3072 rows */
   FRX_GEMV_SPLIT_ALWAYS = 1, /* split K at every 2-16 token call */
   FRX_GEMV_SPLIT_NEVER = 2,  /* whole-K kernels only */
   FRX_GEMV_SPLIT_RANGE_ = 0x7fffffff
