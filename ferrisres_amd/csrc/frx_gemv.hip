@@ -1392,6 +1392,117 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_rows_stream_kernel(const uint
   }
 }
 
+// ---- one token over rows of 16448 to 32768 codes ------------------------
+//
+// The persistent form above with each row read in NP passes of NH windows
+// (1 KB per lane group and window), so that one register set holds a pass
+// and the next pass (of the same row, or the next row's first) is in
+// flight while the current one decodes: a row longer than the four windows
+// a register set holds (8192 x 28672, the LLaMA-70B down projection) still
+// streams two sets deep. One row per wave unit; the x of the whole row is
+// staged once per workgroup, K-interleaved. The passes of a row accumulate
+// into the same two chains; the row is reduced and stored after its last.
+template <int NH>
+__device__ __forceinline__ void rows_pass_load(__amdgpu_buffer_rsrc_t wr, int row, int pass, bool live, int kw,
+                                               int lane, u32x4 (&wv)[NH]) {
+  const uint32_t base = (uint32_t)row * (uint32_t)kw * 4u;
+#pragma unroll
+  for (int i = 0; i < NH; i++) {
+    const int wi = (pass * NH + i) * 256 + 4 * lane;
+    const uint32_t off = live ? base + 4u * (uint32_t)min(wi, kw - 4) : ROWS_STREAM_OOB;
+    wv[i] = __builtin_amdgcn_raw_buffer_load_b128(wr, off, 0, 0);
+  }
+}
+
+template <int NH>
+__device__ __forceinline__ void rows_pass_acc(const uint32_t *lds, const u32x4 (&wv)[NH], int pass, int lane,
+                                              f32x4 (&acc)[2]) {
+#pragma unroll
+  for (int i = 0; i < NH; i++) {
+    u32x4 xb[8];
+    const uint32_t *xp = lds + ((pass * NH + i) * 64 + lane) * ROWS_XCH;
+#pragma unroll
+    for (int q = 0; q < 8; q++) xb[q] = *reinterpret_cast<const u32x4 *>(xp + 4 * q);
+    u32x4 lo[4], hi[4];
+    unpack32_kil(wv[i].x, wv[i].y, lo[0], hi[0], lo[1], hi[1]);
+    unpack32_kil(wv[i].z, wv[i].w, lo[2], hi[2], lo[3], hi[3]);
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      acc[j & 1] = mfma16(lo[j], xb[2 * j], acc[j & 1]);
+      acc[j & 1] = mfma16(hi[j], xb[2 * j + 1], acc[j & 1]);
+    }
+  }
+}
+
+template <typename YT>
+__device__ __forceinline__ void rows_pass_store(const f32x4 (&acc)[2], float sc, int row, int N, int lane,
+                                                YT *__restrict__ Y, const float *__restrict__ bias) {
+  const int c = lane & 15, rg = lane >> 4, e = c & 3;
+  const f32x4 A = acc[0] + acc[1];
+  float v = e == 0 ? A[0] : e == 1 ? A[1] : e == 2 ? A[2] : A[3];
+  v = (c >> 2) == rg ? v : 0.f;  // the diagonal
+  v += dpp_f32<0xB1>(v);
+  v += dpp_f32<0x4E>(v);
+  const float a = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+  const float b = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 20));
+  const float d = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 40));
+  const float f = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 60));
+  float t = ((a + b) + (d + f)) * sc * 0.5f;  // 0.5 undoes the 2*dec(c) encoding
+  if (lane == 0 && row < N) {
+    if (bias) t = add_bias(t, bias[row]);
+    if constexpr (sizeof(YT) == 2) Y[row] = (uint16_t)bf16_rne(t);
+    else Y[row] = t;
+  }
+}
+
+template <typename YT, int WAVES, int NH, int NP>
+__global__ __launch_bounds__(WAVES * 64) void gemv_rows_pass_kernel(const uint32_t *__restrict__ W,
+                                                                    const float *__restrict__ scale,
+                                                                    const uint16_t *__restrict__ X,
+                                                                    YT *__restrict__ Y, int K, int N,
+                                                                    const float *__restrict__ bias) {
+  static_assert(NP == 2, "the loop below alternates two register sets over two passes per row");
+  extern __shared__ __align__(16) uint32_t lds[];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int kw = K >> 4, nxp = K >> 3;
+  const int stride = (int)gridDim.x * WAVES;
+  int row = (int)blockIdx.x * WAVES + wave;
+  const __amdgpu_buffer_rsrc_t wr = buffer_rsrc(W, (uint32_t)N * (uint32_t)kw * 4u);
+  constexpr int NT = WAVES * 64;
+  constexpr int PP = NH * NP * 512;
+  constexpr int XR = (PP + NT - 1) / NT;
+  // activations first (zero past K), then the first row's first pass
+  u32x4 xs[XR];
+  const u32x4 *X4 = reinterpret_cast<const u32x4 *>(X);
+#pragma unroll
+  for (int r = 0; r < XR; r++) {
+    const int j = tid + r * NT;
+    xs[r] = (u32x4){0u, 0u, 0u, 0u};
+    if (j < PP && j < nxp) xs[r] = X4[j];
+  }
+  u32x4 wa[NH], wb[NH];
+  rows_pass_load<NH>(wr, min(row, N - 1), 0, row < N, kw, lane, wa);
+#pragma unroll
+  for (int r = 0; r < XR; r++) {
+    const int j = tid + r * NT;
+    const u32x4 v = stage_kil(xs[r], tid);  // all lanes take part
+    if (j < PP) *reinterpret_cast<u32x4 *>(lds + (j >> 3) * ROWS_XCH + (j & 7) * 4) = v;
+  }
+  __syncthreads();
+  for (; row < N; row += stride) {  // wave-uniform; no barrier below
+    const int next = row + stride;
+    const float sc = scale[row];
+    rows_pass_load<NH>(wr, row, 1, true, kw, lane, wb);
+    __builtin_amdgcn_sched_barrier(0);  // keep the prefetch ahead of the decode
+    f32x4 acc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+    rows_pass_acc<NH>(lds, wa, 0, lane, acc);
+    rows_pass_load<NH>(wr, min(next, N - 1), 0, next < N, kw, lane, wa);
+    __builtin_amdgcn_sched_barrier(0);
+    rows_pass_acc<NH>(lds, wb, 1, lane, acc);
+    rows_pass_store<YT>(acc, sc, row, N, lane, Y, bias);
+  }
+}
+
 static int device_cu_count() {
   static std::atomic<int> cus[64];
   int dev = 0;
@@ -1413,6 +1524,23 @@ static hipError_t launch_gemv_rows_stream(const uint32_t *w, const float *scale,
   const size_t lds = (size_t)NI * 64 * ROWS_XCH * 4;  // at most 36 KB (NI <= 4)
   hipLaunchKernelGGL((gemv_rows_stream_kernel<YT, WAVES, RW, NI>), dim3(grid), dim3(WAVES * 64), lds, stream, w,
                      scale, reinterpret_cast<const uint16_t *>(x), reinterpret_cast<YT *>(y), K, N, bias);
+  return hipGetLastError();
+}
+
+template <typename YT, int NH>
+static hipError_t launch_gemv_rows_pass(const uint32_t *w, const float *scale, const void *x, void *y, int K, int N,
+                                        hipStream_t stream, const float *bias) {
+  constexpr int WAVES = 8;
+  const int grid = std::min((N + WAVES - 1) / WAVES, 2 * device_cu_count());
+  const size_t lds = (size_t)2 * NH * 64 * ROWS_XCH * 4;  // at most 72 KB (NH <= 4)
+  if (lds > 64 * 1024) {
+    static std::atomic<uint64_t> done;
+    const hipError_t e =
+        opt_in_lds(reinterpret_cast<const void *>(&gemv_rows_pass_kernel<YT, WAVES, NH, 2>), (int)lds, done);
+    if (e != hipSuccess) return e;
+  }
+  hipLaunchKernelGGL((gemv_rows_pass_kernel<YT, WAVES, NH, 2>), dim3(grid), dim3(WAVES * 64), lds, stream, w, scale,
+                     reinterpret_cast<const uint16_t *>(x), reinterpret_cast<YT *>(y), K, N, bias);
   return hipGetLastError();
 }
 
@@ -1959,6 +2087,14 @@ static bool gemv_rows_ok(const uint32_t *w, const void *x, int B, int K) {
 
 constexpr int GEMV_ROWS_TALL_N = 16384;  // rows from which waves persist over row groups above 4096 codes
 
+// One bf16 token over rows of 16448 to 32768 codes (K % 64 == 0, aligned),
+// weights addressable by 32-bit buffer offsets: the two-pass persistent
+// kernel.
+static bool gemv_rows_pass_ok(const uint32_t *w, const void *x, int B, int K, int N) {
+  return B == 1 && K % 64 == 0 && K > 4 * 4096 && K <= 8 * 4096 && (reinterpret_cast<uintptr_t>(w) & 15) == 0 &&
+         (reinterpret_cast<uintptr_t>(x) & 15) == 0 && (size_t)N * (size_t)K / 4 < (size_t)ROWS_STREAM_OOB;
+}
+
 template <typename YT>
 static hipError_t launch_gemv_rows(const uint32_t *w, const float *scale, const void *x, void *y, int K, int N,
                                    hipStream_t stream, const float *bias) {
@@ -2078,6 +2214,14 @@ hipError_t launch_gemv(const uint32_t *w, const float *scale, const void *x,
   if (xt_bf16 && gemv_rows_ok(w, x, B, K)) {
     if (yt_bf16) return launch_gemv_rows<uint16_t>(w, scale, x, y, K, N, stream, bias);
     return launch_gemv_rows<float>(w, scale, x, y, K, N, stream, bias);
+  }
+  if (xt_bf16 && gemv_rows_pass_ok(w, x, B, K, N)) {
+    const bool four = K > 6 * 4096;  // windows per pass: 3 up to 24576 columns, else 4
+    if (yt_bf16)
+      return four ? launch_gemv_rows_pass<uint16_t, 4>(w, scale, x, y, K, N, stream, bias)
+                  : launch_gemv_rows_pass<uint16_t, 3>(w, scale, x, y, K, N, stream, bias);
+    return four ? launch_gemv_rows_pass<float, 4>(w, scale, x, y, K, N, stream, bias)
+                : launch_gemv_rows_pass<float, 3>(w, scale, x, y, K, N, stream, bias);
   }
   if (xt_bf16 && gemv_rows4_ok(w, x, B, K)) {
     if (yt_bf16) return launch_gemv_rows4<uint16_t>(w, scale, x, y, B, K, N, stream, bias);

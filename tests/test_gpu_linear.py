@@ -596,3 +596,35 @@ def test_auto_split_one_f32_token_long_rows(ctx, K, N):
     ctx.ternary_linear(dev_u32(w), dev_f32(s), dev_f32(x), y, bias=dev_f32(bias))
     torch.cuda.synchronize()
     np.testing.assert_array_equal(host(y), ref + bias[None, :])
+
+
+@pytest.mark.parametrize("K,N", [(16448, 37), (20480, 1001), (24576, 64), (24640, 515), (32768, 300)])
+@pytest.mark.parametrize("yt", ["f32", "bf16"])
+def test_single_token_long_rows(ctx, K, N, yt):
+    """One bf16 token over rows of 16448 to 32768 codes: two passes of three
+    or four 1 KB windows per row (the last window partial at 16448, 20480
+    and 24640; passes past K multiply staged zeros), rows past N in the last
+    workgroup, against the oracle."""
+    t, w, s, xf, xb = _case(f"rows/long/{K}x{N}", 1, K, N)
+    ref = oracle.ternary_matmul_u32(w, s, xf, 1, K, N)
+    y = _run(ctx, w, s, xf, xb, "bf16", yt)
+    if yt == "f32":
+        assert_close_f32(host(y), ref)
+    else:
+        assert_bf16_within_1ulp(y.view(torch.int16).cpu().numpy().view(np.uint16), ref)
+
+
+@pytest.mark.parametrize("K,N", [(28672, 8192), (20544, 3000)])
+def test_single_token_long_rows_bit_exact_on_dyadic_inputs(ctx, K, N):
+    """The LLaMA-70B down projection [8192, 28672] at one bf16 token: exact
+    sums, f32 and bf16 outputs, and with a bias."""
+    t, w, s, x, xb = _dyadic_case(1, K, N, 2 * K + N)
+    ref = (x @ t.T.astype(np.float32)) * s[None, :]
+    np.testing.assert_array_equal(host(_run(ctx, w, s, x, xb, "bf16", "f32")), ref)
+    yb = _run(ctx, w, s, x, xb, "bf16", "bf16")
+    np.testing.assert_array_equal(yb.view(torch.int16).cpu().numpy().view(np.uint16), synth.f32_to_bf16_bits(ref))
+    bias = (np.arange(N) % 5 - 2).astype(np.float32) / 8
+    y = torch.full((1, N), float("nan"), device="cuda:0")
+    ctx.ternary_linear(dev_u32(w), dev_f32(s), dev_bf16(xb), y, bias=dev_f32(bias))
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(host(y), ref + bias[None, :])
