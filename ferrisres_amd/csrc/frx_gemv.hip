@@ -2029,6 +2029,10 @@ static hipError_t launch_gemv_rows4(const uint32_t *w, const float *scale, const
   if (ni <= 1) return launch_gemv_rows4_w<YT, 8, 1, 1>(w, scale, w, scale, x, y, B, K, N, stream, bias);
   if (ni <= 2) return launch_gemv_rows4_w<YT, 8, 1, 2, 2>(w, scale, w, scale, x, y, B, K, N, stream, bias);
   if (ni <= 4) return launch_gemv_rows4_w<YT, 8, 1, 4, 2>(w, scale, w, scale, x, y, B, K, N, stream, bias);
+  // 5120 and 6144 columns (LLaMA-13B-sized rows) without rounding up to 8
+  // windows of loads
+  if (ni <= 5) return launch_gemv_rows4_w<YT, 8, 1, 5, 2>(w, scale, w, scale, x, y, B, K, N, stream, bias);
+  if (ni <= 6) return launch_gemv_rows4_w<YT, 8, 1, 6, 2>(w, scale, w, scale, x, y, B, K, N, stream, bias);
   if (ni <= 8) return launch_gemv_rows4_w<YT, 8, 1, 8, 2>(w, scale, w, scale, x, y, B, K, N, stream, bias);
   if (ni <= 11) return launch_gemv_rows4_w<YT, 8, 1, 11, 2>(w, scale, w, scale, x, y, B, K, N, stream, bias);
   return launch_gemv_rows4_w<YT, 8, 1, 14, 2>(w, scale, w, scale, x, y, B, K, N, stream, bias);
