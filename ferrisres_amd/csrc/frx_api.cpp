@@ -810,6 +810,18 @@ static frx_status ffn_run(frx_ctx *ctx, const void *x, frx_dtype xt, const uint3
     if (e != hipSuccess) return hip_fail(ctx, e, "ffn down launch");
     return FRX_OK;
   }
+  if (may_alloc && ctx->ffn_mode != FRX_FFN_ONE_LAUNCH && ctx->gemv_split != FRX_GEMV_SPLIT_NEVER &&
+      xt == FRX_BF16 && M == 1 && aligned16(w_gate) && aligned16(w_up) && aligned16(w_down) && H % 64 == 0 &&
+      H <= 16384 && I % 64 == 0 && I > 16384) {
+    // one token over an intermediate longer than the rows kernels take
+    // (LLaMA-70B: I = 28672): gate/up/act in the rows kernel into h's bf16
+    // planes, then the split-K down launch over both planes
+    uint16_t *hp = reinterpret_cast<uint16_t *>(ws);
+    e = frx::launch_gemv_rows_glu_planes(w_gate, s_gate, w_up, s_up, x, hp, (int)H, (int)I,
+                                         act == FRX_ACT_GELU_TANH, ctx->stream);
+    if (e != hipSuccess) return hip_fail(ctx, e, "ffn gate/up launch");
+    return ffn_down_planes(ctx, w_down, s_down, hp, y, yt, M, H, I, may_alloc);
+  }
   if (ctx->ffn_mode != FRX_FFN_ONE_LAUNCH && xt == FRX_BF16 && aligned16(w_gate) && aligned16(w_up) &&
       aligned16(w_down) && (M == 3 || M == 4) && frx::gemv_rows4_ffn_ok(2, (int)H, (int)I)) {
     // three or four tokens: gate/up/act in the 4-segment kernel into h's

@@ -143,6 +143,21 @@ def test_ffn_bf16_in_bf16_out_3_to_16_tokens(ctx, M, H, I):
     assert_close_f32(host(run_ffn(ctx, xf, xb, mats, frx.ACT_SILU)), ref)
 
 
+@pytest.mark.parametrize("H,I", [(1024, 16448), (2048, 28672), (16384, 20480)])
+@pytest.mark.parametrize("act", [frx.ACT_SILU, frx.ACT_GELU_TANH])
+def test_ffn_single_token_long_intermediate(ctx, H, I, act):
+    """One bf16 token with an intermediate longer than 16384 (LLaMA-70B:
+    I = 28672): gate/up/act into h's bf16 hi/lo planes (rows kernel), then
+    the split-K down launch over both planes; f32 and bf16 outputs against
+    the reference FFN."""
+    xf, xb, mats = make_ffn(f"ffn/long{H}_{I}", 1, H, I)
+    xw = synth.bf16_bits_to_f32(xb)
+    ref = ref_ffn(xw, mats, act == frx.ACT_GELU_TANH)
+    assert_close_f32(host(run_ffn(ctx, xf, xb, mats, act)), ref)
+    yb = run_ffn(ctx, xf, xb, mats, act, yt="bf16")
+    assert_bf16_within_1ulp(yb.view(torch.int16).cpu().numpy().view(np.uint16), ref)
+
+
 @pytest.mark.parametrize("M", [2, 24])
 def test_ffn_f32_in_bf16_out(ctx, M):
     xf, xb, mats = make_ffn(f"ffn/f32_{M}", M, 128, 208)
