@@ -90,6 +90,8 @@ struct frx_ctx {
   size_t stage_ws_bytes = 0;
   void *sk_ws = nullptr;  // fp32 partial tiles of the split-K decode GEMV
   size_t sk_ws_bytes = 0;
+  void *gk_ws = nullptr;  // fp32 K parts of the split-K GEMM
+  size_t gk_ws_bytes = 0;
   unsigned *sk_cnt = nullptr;  // its per-row-tile arrival counters (zero between launches)
   int gemv_split = FRX_GEMV_SPLIT_AUTO;
   unsigned *ffn_bar = nullptr;  // grid-barrier words of the one-launch FFN
@@ -190,6 +192,7 @@ void frx_destroy(frx_ctx *ctx) {
   if (ctx->unit_ws) (void)hipFree(ctx->unit_ws);
   if (ctx->stage_ws) (void)hipFree(ctx->stage_ws);
   if (ctx->sk_ws) (void)hipFree(ctx->sk_ws);
+  if (ctx->gk_ws) (void)hipFree(ctx->gk_ws);
   if (ctx->sk_cnt) (void)hipFree(ctx->sk_cnt);
   if (ctx->ffn_bar) (void)hipFree(ctx->ffn_bar);
   for (void *p : ctx->retired) (void)hipFree(p);
@@ -462,11 +465,24 @@ static frx_status gemv_auto(frx_ctx *ctx, const uint32_t *w, const float *scale,
     if ((st = ensure_sk_counters(ctx)) != FRX_OK) return st;
     e = frx::launch_gemv_sk(w, scale, x, nullptr, xt == FRX_BF16 ? 0 : 1, y, yt == FRX_BF16, (int)M, (int)K, (int)N,
                             reinterpret_cast<float *>(ctx->sk_ws), ctx->sk_cnt, bias, ctx->cus, ctx->stream);
-  } else if (M <= 16)
+  } else if (M <= 16) {
     e = frx::launch_gemv(w, scale, x, xt == FRX_BF16, y, yt == FRX_BF16, (int)M, (int)K, (int)N, ctx->stream, bias);
-  else
-    e = frx::launch_gemm(w, scale, x, xt == FRX_BF16, y, yt == FRX_BF16, (int)M, (int)K, (int)N, 0, ctx->stream,
-                         bias);
+  } else {
+    int S = 0, kp = 0;
+    if (ctx->gemv_split != FRX_GEMV_SPLIT_NEVER && xt == FRX_BF16 && aligned16(w) && aligned16(x) &&
+        (size_t)M * K * 2 < ((size_t)1 << 31) && frx::gemm_splitk_plan((int)M, (int)K, (int)N, ctx->cus, &S, &kp)) {
+      // 17 to a few hundred tokens: K split over workgroups so that the
+      // grid covers the compute units
+      if ((st = ensure_buffer(ctx, &ctx->gk_ws, &ctx->gk_ws_bytes, frx::gemm_splitk_workspace_bytes((int)M, (int)N, S),
+                              "split-K GEMM workspace allocation")) != FRX_OK)
+        return st;
+      e = frx::launch_gemm_splitk(w, scale, x, y, yt == FRX_BF16, (int)M, (int)K, (int)N, S, kp,
+                                  reinterpret_cast<float *>(ctx->gk_ws), ctx->stream, bias);
+    } else {
+      e = frx::launch_gemm(w, scale, x, xt == FRX_BF16, y, yt == FRX_BF16, (int)M, (int)K, (int)N, 0, ctx->stream,
+                           bias);
+    }
+  }
   if (e != hipSuccess) return hip_fail(ctx, e, "ternary_linear launch");
   return FRX_OK;
 }

@@ -99,6 +99,95 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm2sp_kernel(
   Core::template store_tile<YT>(lds, acc, scale, Y, (size_t)N, m0, m_count, n0, n_count, bias);
 }
 
+// Split-K dense GEMM for launches with fewer tiles than compute units (17
+// to a few hundred tokens): workgroup (nt, mt, s) multiplies K columns
+// [s kp, (s + 1) kp) of its tile with the pipelined engine and stores the
+// raw fp32 accumulators to part[s][M][N]; gemm_splitk_reduce adds the parts
+// in order s = 0, 1, ... and applies the scale (and bias).
+template <int BM, int BN, int WM, int WN, int NS>
+__global__ __launch_bounds__(WM *WN * 64) void gemm2_splitk_kernel(
+    const uint32_t *__restrict__ W, const uint16_t *__restrict__ X, float *__restrict__ part, int M, int K, int N,
+    int kp) {
+  using Core = Gemm2<BM, BN, WM, WN, NS, false>;
+  extern __shared__ __align__(16) uint32_t lds[];
+  const int nt = blockIdx.x, mt = blockIdx.y, s = blockIdx.z;
+  const int n0 = nt * BN, m0 = mt * BM, k0 = s * kp, kl = min(kp, K - k0);
+  f32x4 acc[Core::FN][Core::FM];
+  const int m_count = min(BM, M - m0), n_count = min(BN, N - n0);
+  // X from row m0, column k0 (row stride K); W from row n0, word k0 / 16 (row
+  // stride K / 16 words): the engine's K loop runs kl columns
+  Core::run(lds, X + (size_t)m0 * K + k0, (uint32_t)m_count * (uint32_t)K * 2u - (uint32_t)k0 * 2u, nullptr,
+            m_count, W + (size_t)n0 * (K >> 4) + (k0 >> 4), n_count, kl, acc, nullptr, K, K);
+  Core::template store_tile<float, true>(lds, acc, nullptr, part + (size_t)s * M * N, (size_t)N, m0, m_count, n0,
+                                         n_count, nullptr);
+}
+
+template <typename YT>
+__global__ __launch_bounds__(256) void gemm_splitk_reduce(const float *__restrict__ part, int S, int M, int N,
+                                                          const float *__restrict__ scale,
+                                                          const float *__restrict__ bias, YT *__restrict__ Y) {
+  const size_t i = ((size_t)blockIdx.x * 256 + threadIdx.x) * 4;  // N % 4 == 0
+  const size_t MN = (size_t)M * N;
+  if (i >= MN) return;
+  f32x4 sum = *reinterpret_cast<const f32x4 *>(part + i);
+  for (int s = 1; s < S; s++) sum = sum + *reinterpret_cast<const f32x4 *>(part + (size_t)s * MN + i);
+  const int n = (int)(i % (size_t)N);
+  f32x4 o;
+#pragma unroll
+  for (int e = 0; e < 4; e++) {
+    o[e] = sum[e] * (0.5f * scale[n + e]);  // 0.5 undoes the 2*dec(c) encoding
+    if (bias) o[e] = add_bias(o[e], bias[n + e]);
+  }
+  YStore<YT>::store4(Y + i, o, 4);
+}
+
+constexpr int GEMM_SK_BM = 64;
+
+// The split: 64-token tiles; when they leave at least half of the compute
+// units idle, S K parts (whole 64-column steps) bring the grid to about two
+// workgroups per CU. (With more tiles the fp32 parts cost more than the
+// idle units: 11008 x 4096 at 256 tokens, 172 tiles, 40.2 us whole against
+// 46.9 us in three parts; 4096 x 11008 at 512 tokens, 128 tiles, 91.8 us
+// whole against 54.5 us in four.)
+bool gemm_splitk_plan(int M, int K, int N, int cus, int *S, int *kp) {
+  if (M <= 16 || K % 64 != 0 || N % 4 != 0) return false;
+  const long tiles = (long)((M + GEMM_SK_BM - 1) / GEMM_SK_BM) * ((N + 255) / 256);
+  if (2 * tiles > cus) return false;
+  const int nks = K / 64;
+  // at least 8 steps of 64 columns per part: shorter parts are mostly the
+  // pipeline's fill and drain, and their fp32 partials outweigh the weights
+  int s = (int)std::min<long>((2L * cus + tiles - 1) / tiles, nks / 8);
+  if (s < 2) return false;
+  const int steps = (nks + s - 1) / s;
+  *kp = steps * 64;
+  *S = (K + *kp - 1) / *kp;
+  return *S >= 2;
+}
+
+size_t gemm_splitk_workspace_bytes(int M, int N, int S) { return (size_t)S * M * N * 4; }
+
+hipError_t launch_gemm_splitk(const uint32_t *w, const float *scale, const void *x, void *y, int yt_bf16, int M, int K,
+                              int N, int S, int kp, float *part, hipStream_t stream, const float *bias) {
+  constexpr int BM = GEMM_SK_BM, BN = 256, WM = 1, WN = 4, NS = 4;
+  using Core = Gemm2<BM, BN, WM, WN, NS, false>;
+  constexpr int lds = Core::LDS_DWORDS * 4;
+  static std::atomic<uint64_t> done;
+  hipError_t e = opt_in_lds(reinterpret_cast<const void *>(&gemm2_splitk_kernel<BM, BN, WM, WN, NS>), lds, done);
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL((gemm2_splitk_kernel<BM, BN, WM, WN, NS>), dim3((N + BN - 1) / BN, (M + BM - 1) / BM, S),
+                     dim3(WM * WN * 64), lds, stream, w, reinterpret_cast<const uint16_t *>(x), part, M, K, N, kp);
+  if ((e = hipGetLastError()) != hipSuccess) return e;
+  const size_t quads = (size_t)M * N / 4;
+  const dim3 g((unsigned)((quads + 255) / 256));
+  if (yt_bf16)
+    hipLaunchKernelGGL(gemm_splitk_reduce<uint16_t>, g, dim3(256), 0, stream, part, S, M, N, scale, bias,
+                       reinterpret_cast<uint16_t *>(y));
+  else
+    hipLaunchKernelGGL(gemm_splitk_reduce<float>, g, dim3(256), 0, stream, part, S, M, N, scale, bias,
+                       reinterpret_cast<float *>(y));
+  return hipGetLastError();
+}
+
 // Pipeline stages of the K loop.
 constexpr int GEMM2_NS = 4;
 // One wave per SIMD, each over the tile's tokens x 64 rows. Waves split

@@ -560,7 +560,9 @@ struct Gemm2 {
   // load once). Stores cover full cache lines and the code stays compact: a
   // fully unrolled per-fragment store sequence is tens of KB that each
   // workgroup runs once, and fetching it costs more than the stores.
-  template <typename YT>
+  // RAW: the accumulators as they are (scale unused), e.g. the fp32 partial
+  // sums of a K part that a later launch scales.
+  template <typename YT, bool RAW = false>
   __device__ static void store_tile(uint32_t *lds, const f32x4 (&acc)[FN][FM],
                                     const float *scale, YT *Y, size_t ldy, int m0, int m_count,
                                     int n0, int n_count, const float *bias = nullptr) {
@@ -580,7 +582,7 @@ struct Gemm2 {
     const int nl = c * CE;
     float sc[CE];
 #pragma unroll
-    for (int e = 0; e < CE; e++) sc[e] = 0.5f * scale[n0 + min(nl + e, n_count - 1)];
+    for (int e = 0; e < CE; e++) sc[e] = RAW ? 1.0f : 0.5f * scale[n0 + min(nl + e, n_count - 1)];
     float bv[CE];  // row bias (added after the scale, its own rounding)
 #pragma unroll
     for (int e = 0; e < CE; e++) bv[e] = bias ? bias[n0 + min(nl + e, n_count - 1)] : 0.f;

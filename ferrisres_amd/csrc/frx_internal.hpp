@@ -102,6 +102,15 @@ hipError_t launch_gemv_group(const void *x, int xt_bf16, int yt_bf16, int B, int
 // f32 x, 2 bf16 planes (x hi, x2 lo). K % 16 == 0, x 16-byte aligned,
 // B * K * 4 < 2^32.
 constexpr int GEMV_SK_MAX_TILES = 65536;
+// Split-K dense GEMM (frx_gemm.hip) for 17 to a few hundred bf16 tokens,
+// where 64-token tiles give fewer workgroups than compute units: S parts of
+// kp columns (K % 64 == 0, N % 4 == 0, 16-byte aligned weights and x),
+// fp32 partials in `part` (gemm_splitk_workspace_bytes), then an ordered
+// reduction with the scale and bias.
+bool gemm_splitk_plan(int M, int K, int N, int cus, int *S, int *kp);
+size_t gemm_splitk_workspace_bytes(int M, int N, int S);
+hipError_t launch_gemm_splitk(const uint32_t *w, const float *scale, const void *x, void *y, int yt_bf16, int M, int K,
+                              int N, int S, int kp, float *part, hipStream_t stream, const float *bias);
 // The balanced one-token kernel takes this launch (one token, K % 64 == 0
 // up to 16384, aligned operands, rows within its per-wave slots).
 bool gemv_bal_fits(const uint32_t *w, const void *x, int B, int K, int N);

@@ -628,3 +628,30 @@ def test_single_token_long_rows_bit_exact_on_dyadic_inputs(ctx, K, N):
     ctx.ternary_linear(dev_u32(w), dev_f32(s), dev_bf16(xb), y, bias=dev_f32(bias))
     torch.cuda.synchronize()
     np.testing.assert_array_equal(host(y), ref + bias[None, :])
+
+
+@pytest.mark.parametrize("M,K,N", [(17, 4096, 11008), (32, 11008, 4096), (64, 4096, 4096), (100, 2048, 5632),
+                                   (256, 4096, 11008), (500, 1024, 1028)])
+def test_split_k_gemm_bit_exact_on_dyadic_inputs(ctx, M, K, N):
+    """17 to a few hundred bf16 tokens, where 64-token tiles leave compute
+    units idle: the GEMM splits K into parts whose fp32 partials are added in
+    part order. Dyadic inputs: exact sums, f32 and bf16 outputs, and a bias."""
+    t, w, s, x, xb = _dyadic_case(M, K, N, 3 * M + K + N)
+    ref = (x @ t.T.astype(np.float32)) * s[None, :]
+    np.testing.assert_array_equal(host(_run(ctx, w, s, x, xb, "bf16", "f32")), ref)
+    yb = _run(ctx, w, s, x, xb, "bf16", "bf16")
+    np.testing.assert_array_equal(yb.view(torch.int16).cpu().numpy().view(np.uint16), synth.f32_to_bf16_bits(ref))
+    bias = (np.arange(N) % 9 - 4).astype(np.float32) / 16
+    y = torch.full((M, N), float("nan"), device="cuda:0")
+    ctx.ternary_linear(dev_u32(w), dev_f32(s), dev_bf16(xb), y, bias=dev_f32(bias))
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(host(y), ref + bias[None, :])
+
+
+@pytest.mark.parametrize("M,K,N", [(24, 4096, 11008), (130, 11008, 4096)])
+def test_split_k_gemm_random_parity(ctx, M, K, N):
+    t, w, s, xf, xb = _case(f"gemmsk/{M}x{K}x{N}", M, K, N)
+    ref = oracle.ternary_matmul_u32(w, s, xf, M, K, N)
+    assert_close_f32(host(_run(ctx, w, s, xf, xb, "bf16", "f32")), ref)
+    yb = _run(ctx, w, s, xf, xb, "bf16", "bf16")
+    assert_bf16_within_1ulp(yb.view(torch.int16).cpu().numpy().view(np.uint16), ref)
