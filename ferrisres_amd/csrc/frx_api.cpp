@@ -92,6 +92,8 @@ struct frx_ctx {
   size_t sk_ws_bytes = 0;
   void *gk_ws = nullptr;  // fp32 K parts of the split-K GEMM
   size_t gk_ws_bytes = 0;
+  void *xpl_ws = nullptr;  // f32 activations as bf16 hi | lo rows (GEMM above 16 tokens)
+  size_t xpl_ws_bytes = 0;
   unsigned *sk_cnt = nullptr;  // its per-row-tile arrival counters (zero between launches)
   int gemv_split = FRX_GEMV_SPLIT_AUTO;
   unsigned *ffn_bar = nullptr;  // grid-barrier words of the one-launch FFN
@@ -193,6 +195,7 @@ void frx_destroy(frx_ctx *ctx) {
   if (ctx->stage_ws) (void)hipFree(ctx->stage_ws);
   if (ctx->sk_ws) (void)hipFree(ctx->sk_ws);
   if (ctx->gk_ws) (void)hipFree(ctx->gk_ws);
+  if (ctx->xpl_ws) (void)hipFree(ctx->xpl_ws);
   if (ctx->sk_cnt) (void)hipFree(ctx->sk_cnt);
   if (ctx->ffn_bar) (void)hipFree(ctx->ffn_bar);
   for (void *p : ctx->retired) (void)hipFree(p);
@@ -450,6 +453,29 @@ static frx_status ensure_sk_counters(frx_ctx *ctx) {
   return FRX_OK;
 }
 
+// y = x W^T * scale (+ bias) for x2 = [M][2K] bf16 hi | lo rows (an fp32
+// activation), M > 16: K split over workgroups where the tiles leave compute
+// units idle (and the call may allocate), else one pass over both halves.
+static frx_status gemm_planes_auto(frx_ctx *ctx, const uint32_t *w, const float *scale, const float *bias,
+                                   const uint16_t *x2, void *y, frx_dtype yt, uint32_t M, uint32_t K, uint32_t N,
+                                   bool may_alloc) {
+  frx_status st;
+  hipError_t e;
+  int S = 0, kp = 0;
+  if (may_alloc && ctx->gemv_split != FRX_GEMV_SPLIT_NEVER &&
+      frx::gemm_splitk_plan((int)M, (int)K, (int)N, ctx->cus, &S, &kp, 2)) {
+    if ((st = ensure_buffer(ctx, &ctx->gk_ws, &ctx->gk_ws_bytes, frx::gemm_splitk_workspace_bytes((int)M, (int)N, S),
+                            "split-K GEMM workspace allocation")) != FRX_OK)
+      return st;
+    e = frx::launch_gemm_splitk(w, scale, x2, y, yt == FRX_BF16, (int)M, (int)K, (int)N, S, kp,
+                                reinterpret_cast<float *>(ctx->gk_ws), ctx->stream, bias, 2);
+  } else {
+    e = frx::launch_gemm_planes(w, scale, x2, y, yt == FRX_BF16, (int)M, (int)K, (int)N, ctx->stream, bias);
+  }
+  if (e != hipSuccess) return hip_fail(ctx, e, "ternary_linear launch");
+  return FRX_OK;
+}
+
 // y = x W^T * scale (+ bias) on aligned operands: the split-K GEMV where
 // use_split picks it (allocating its workspace on first use), else the
 // decode GEMVs up to 16 tokens and the GEMM above.
@@ -467,6 +493,16 @@ static frx_status gemv_auto(frx_ctx *ctx, const uint32_t *w, const float *scale,
                             reinterpret_cast<float *>(ctx->sk_ws), ctx->sk_cnt, bias, ctx->cus, ctx->stream);
   } else if (M <= 16) {
     e = frx::launch_gemv(w, scale, x, xt == FRX_BF16, y, yt == FRX_BF16, (int)M, (int)K, (int)N, ctx->stream, bias);
+  } else if (xt == FRX_F32 && K % 64 == 0 && aligned16(w) && aligned16(x) && (size_t)M * K * 4 < ((size_t)1 << 31)) {
+    // f32 activations, 17 tokens and more: split once into bf16 hi | lo rows
+    // (the same bytes), then the bf16 engine over both halves
+    if ((st = ensure_buffer(ctx, &ctx->xpl_ws, &ctx->xpl_ws_bytes, a256((size_t)M * K * 4),
+                            "activation planes workspace allocation")) != FRX_OK)
+      return st;
+    uint16_t *x2 = reinterpret_cast<uint16_t *>(ctx->xpl_ws);
+    e = frx::launch_to_planes(reinterpret_cast<const float *>(x), x2, (int)M, (int)K, ctx->stream);
+    if (e != hipSuccess) return hip_fail(ctx, e, "activation planes launch");
+    return gemm_planes_auto(ctx, w, scale, bias, x2, y, yt, M, K, N, true);
   } else {
     int S = 0, kp = 0;
     if (ctx->gemv_split != FRX_GEMV_SPLIT_NEVER && xt == FRX_BF16 && aligned16(w) && aligned16(x) &&
@@ -728,15 +764,21 @@ static frx_status glu_into(frx_ctx *ctx, const void *x, frx_dtype xt, const uint
   } else {
     float *u = u_ws;
     if (!u) {
+      // the allocating entries: gate and up as linears (split over K where
+      // the tiles leave compute units idle; f32 x as bf16 hi | lo rows)
       const size_t ub = a256((size_t)M * I * 4);
       frx_status st = ensure_buffer(ctx, &ctx->glu_ws, &ctx->glu_ws_bytes, ub, "GLU workspace allocation");
       if (st != FRX_OK) return st;
       u = reinterpret_cast<float *>(ctx->glu_ws);
+      if ((st = gemv_auto(ctx, w_gate, s_gate, nullptr, x, xt, h, FRX_F32, M, H, I)) != FRX_OK) return st;
+      if ((st = gemv_auto(ctx, w_up, s_up, nullptr, x, xt, u, FRX_F32, M, H, I)) != FRX_OK) return st;
+      e = frx::launch_glu_combine(h, u, h, (size_t)M * I, gelu, ctx->stream);
+    } else {
+      e = frx::launch_gemm(w_gate, s_gate, x, xt == FRX_BF16, h, 0, (int)M, (int)H, (int)I, 0, ctx->stream);
+      if (e == hipSuccess)
+        e = frx::launch_gemm(w_up, s_up, x, xt == FRX_BF16, u, 0, (int)M, (int)H, (int)I, 0, ctx->stream);
+      if (e == hipSuccess) e = frx::launch_glu_combine(h, u, h, (size_t)M * I, gelu, ctx->stream);
     }
-    e = frx::launch_gemm(w_gate, s_gate, x, xt == FRX_BF16, h, 0, (int)M, (int)H, (int)I, 0, ctx->stream);
-    if (e == hipSuccess)
-      e = frx::launch_gemm(w_up, s_up, x, xt == FRX_BF16, u, 0, (int)M, (int)H, (int)I, 0, ctx->stream);
-    if (e == hipSuccess) e = frx::launch_glu_combine(h, u, h, (size_t)M * I, gelu, ctx->stream);
   }
   if (e != hipSuccess) return hip_fail(ctx, e, "gate/up launch");
   return FRX_OK;
@@ -890,6 +932,14 @@ static frx_status ffn_run(frx_ctx *ctx, const void *x, frx_dtype xt, const uint3
   float *h = reinterpret_cast<float *>(ws);
   frx_status st = glu_into(ctx, x, xt, w_gate, s_gate, w_up, s_up, M, H, I, act == FRX_ACT_GELU_TANH, h, u_ws);
   if (st != FRX_OK) return st;
+  if (M > 16 && I % 64 == 0 && aligned16(w_down)) {
+    // h as bf16 hi | lo rows in the up projection's buffer (no longer
+    // read), then the bf16 engine over both halves
+    uint16_t *h2 = reinterpret_cast<uint16_t *>(u_ws ? u_ws : reinterpret_cast<float *>(ctx->glu_ws));
+    e = frx::launch_to_planes(h, h2, (int)M, (int)I, ctx->stream);
+    if (e != hipSuccess) return hip_fail(ctx, e, "ffn planes launch");
+    return gemm_planes_auto(ctx, w_down, s_down, nullptr, h2, y, yt, M, I, H, may_alloc);
+  }
   // fp32 h: the allocating entry takes the split-K down launch where it is
   // faster (long rows of h)
   if (may_alloc) return gemv_auto(ctx, w_down, s_down, nullptr, h, FRX_F32, y, yt, M, I, H);

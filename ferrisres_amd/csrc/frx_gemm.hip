@@ -104,22 +104,67 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm2sp_kernel(
 // [s kp, (s + 1) kp) of its tile with the pipelined engine and stores the
 // raw fp32 accumulators to part[s][M][N]; gemm_splitk_reduce adds the parts
 // in order s = 0, 1, ... and applies the scale (and bias).
-template <int BM, int BN, int WM, int WN, int NS>
+// HV = 2: X rows are an fp32 activation as bf16 hi | lo halves ([M][2K]);
+// parts 0 .. S/2 - 1 run over the hi half and S/2 .. S - 1 over the lo half,
+// each against the same weight columns.
+template <int BM, int BN, int WM, int WN, int NS, int HV>
 __global__ __launch_bounds__(WM *WN * 64) void gemm2_splitk_kernel(
     const uint32_t *__restrict__ W, const uint16_t *__restrict__ X, float *__restrict__ part, int M, int K, int N,
     int kp) {
   using Core = Gemm2<BM, BN, WM, WN, NS, false>;
   extern __shared__ __align__(16) uint32_t lds[];
   const int nt = blockIdx.x, mt = blockIdx.y, s = blockIdx.z;
-  const int n0 = nt * BN, m0 = mt * BM, k0 = s * kp, kl = min(kp, K - k0);
+  const int sh = (int)gridDim.z / HV, half = s / sh, j = s - half * sh;
+  const int n0 = nt * BN, m0 = mt * BM, k0 = j * kp, kl = min(kp, K - k0);
+  const int ldx = HV * K;  // X row stride (elements)
   f32x4 acc[Core::FN][Core::FM];
   const int m_count = min(BM, M - m0), n_count = min(BN, N - n0);
-  // X from row m0, column k0 (row stride K); W from row n0, word k0 / 16 (row
+  // X from row m0, column half K + k0; W from row n0, word k0 / 16 (row
   // stride K / 16 words): the engine's K loop runs kl columns
-  Core::run(lds, X + (size_t)m0 * K + k0, (uint32_t)m_count * (uint32_t)K * 2u - (uint32_t)k0 * 2u, nullptr,
-            m_count, W + (size_t)n0 * (K >> 4) + (k0 >> 4), n_count, kl, acc, nullptr, K, K);
+  const uint32_t xo = (uint32_t)(half * K + k0);
+  Core::run(lds, X + (size_t)m0 * ldx + xo, (uint32_t)m_count * (uint32_t)ldx * 2u - xo * 2u, nullptr, m_count,
+            W + (size_t)n0 * (K >> 4) + (k0 >> 4), n_count, kl, acc, nullptr, K, ldx);
   Core::template store_tile<float, true>(lds, acc, nullptr, part + (size_t)s * M * N, (size_t)N, m0, m_count, n0,
                                          n_count, nullptr);
+}
+
+// Whole-K GEMM over an fp32 activation stored as bf16 hi | lo halves of
+// each row ([M][2K]): one pass of 2K columns in which the weight columns
+// wrap at K (the engine's wk), i.e. acc = W x_hi + W x_lo.
+template <int BM, int BN, int WM, int WN, int NS, typename YT>
+__global__ __launch_bounds__(WM *WN * 64) void gemm2_planes_kernel(
+    const uint32_t *__restrict__ W, const float *__restrict__ scale, const uint16_t *__restrict__ X,
+    YT *__restrict__ Y, int M, int K, int N, const float *__restrict__ bias) {
+  using Core = Gemm2<BM, BN, WM, WN, NS, false>;
+  extern __shared__ __align__(16) uint32_t lds[];
+  int nt, mt;
+  xcd_tile(nt, mt);
+  const int n0 = nt * BN, m0 = mt * BM;
+  f32x4 acc[Core::FN][Core::FM];
+  const int m_count = min(BM, M - m0), n_count = min(BN, N - n0);
+  Core::run(lds, X + (size_t)m0 * 2 * K, (uint32_t)m_count * (uint32_t)K * 4u, nullptr, m_count,
+            W + (size_t)n0 * (K >> 4), n_count, 2 * K, acc, nullptr, K, 2 * K);
+  Core::template store_tile<YT>(lds, acc, scale, Y, (size_t)N, m0, m_count, n0, n_count, bias);
+}
+
+// x [M][K] f32 -> x2 [M][2K] bf16: hi = bf16(x), lo = bf16(x - hi) (split2_bf16,
+// |x - hi - lo| <= 2^-17 |x|), two values per thread.
+__global__ __launch_bounds__(256) void to_planes_kernel(const float *__restrict__ x, uint16_t *__restrict__ x2,
+                                                        int M, int K) {
+  const size_t i = ((size_t)blockIdx.x * 256 + threadIdx.x) * 2;  // K even
+  if (i >= (size_t)M * K) return;
+  const size_t m = i / (size_t)K, k = i - m * (size_t)K;
+  const float2 v = *reinterpret_cast<const float2 *>(x + i);
+  uint32_t hi, lo;
+  split2_bf16(v.x, v.y, hi, lo);
+  *reinterpret_cast<uint32_t *>(x2 + m * 2 * K + k) = hi;
+  *reinterpret_cast<uint32_t *>(x2 + m * 2 * K + K + k) = lo;
+}
+
+hipError_t launch_to_planes(const float *x, uint16_t *x2, int M, int K, hipStream_t stream) {
+  const size_t pairs = (size_t)M * K / 2;
+  hipLaunchKernelGGL(to_planes_kernel, dim3((unsigned)((pairs + 255) / 256)), dim3(256), 0, stream, x, x2, M, K);
+  return hipGetLastError();
 }
 
 template <typename YT>
@@ -149,33 +194,44 @@ constexpr int GEMM_SK_BM = 64;
 // idle units: 11008 x 4096 at 256 tokens, 172 tiles, 40.2 us whole against
 // 46.9 us in three parts; 4096 x 11008 at 512 tokens, 128 tiles, 91.8 us
 // whole against 54.5 us in four.)
-bool gemm_splitk_plan(int M, int K, int N, int cus, int *S, int *kp) {
+bool gemm_splitk_plan(int M, int K, int N, int cus, int *S, int *kp, int halves) {
   if (M <= 16 || K % 64 != 0 || N % 4 != 0) return false;
   const long tiles = (long)((M + GEMM_SK_BM - 1) / GEMM_SK_BM) * ((N + 255) / 256);
   if (2 * tiles > cus) return false;
   const int nks = K / 64;
   // at least 8 steps of 64 columns per part: shorter parts are mostly the
   // pipeline's fill and drain, and their fp32 partials outweigh the weights
-  int s = (int)std::min<long>((2L * cus + tiles - 1) / tiles, nks / 8);
-  if (s < 2) return false;
+  int s = (int)std::min<long>((2L * cus + tiles * halves - 1) / (tiles * halves), nks / 8);
+  if (s < 1 || halves * s < 2) return false;
   const int steps = (nks + s - 1) / s;
   *kp = steps * 64;
-  *S = (K + *kp - 1) / *kp;
-  return *S >= 2;
+  *S = halves * ((K + *kp - 1) / *kp);
+  return true;
 }
+
 
 size_t gemm_splitk_workspace_bytes(int M, int N, int S) { return (size_t)S * M * N * 4; }
 
 hipError_t launch_gemm_splitk(const uint32_t *w, const float *scale, const void *x, void *y, int yt_bf16, int M, int K,
-                              int N, int S, int kp, float *part, hipStream_t stream, const float *bias) {
+                              int N, int S, int kp, float *part, hipStream_t stream, const float *bias, int halves) {
   constexpr int BM = GEMM_SK_BM, BN = 256, WM = 1, WN = 4, NS = 4;
   using Core = Gemm2<BM, BN, WM, WN, NS, false>;
   constexpr int lds = Core::LDS_DWORDS * 4;
-  static std::atomic<uint64_t> done;
-  hipError_t e = opt_in_lds(reinterpret_cast<const void *>(&gemm2_splitk_kernel<BM, BN, WM, WN, NS>), lds, done);
-  if (e != hipSuccess) return e;
-  hipLaunchKernelGGL((gemm2_splitk_kernel<BM, BN, WM, WN, NS>), dim3((N + BN - 1) / BN, (M + BM - 1) / BM, S),
-                     dim3(WM * WN * 64), lds, stream, w, reinterpret_cast<const uint16_t *>(x), part, M, K, N, kp);
+  const dim3 grid((N + BN - 1) / BN, (M + BM - 1) / BM, S);
+  hipError_t e;
+  if (halves == 2) {
+    static std::atomic<uint64_t> done2;
+    e = opt_in_lds(reinterpret_cast<const void *>(&gemm2_splitk_kernel<BM, BN, WM, WN, NS, 2>), lds, done2);
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL((gemm2_splitk_kernel<BM, BN, WM, WN, NS, 2>), grid, dim3(WM * WN * 64), lds, stream, w,
+                       reinterpret_cast<const uint16_t *>(x), part, M, K, N, kp);
+  } else {
+    static std::atomic<uint64_t> done;
+    e = opt_in_lds(reinterpret_cast<const void *>(&gemm2_splitk_kernel<BM, BN, WM, WN, NS, 1>), lds, done);
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL((gemm2_splitk_kernel<BM, BN, WM, WN, NS, 1>), grid, dim3(WM * WN * 64), lds, stream, w,
+                       reinterpret_cast<const uint16_t *>(x), part, M, K, N, kp);
+  }
   if ((e = hipGetLastError()) != hipSuccess) return e;
   const size_t quads = (size_t)M * N / 4;
   const dim3 g((unsigned)((quads + 255) / 256));
@@ -212,6 +268,33 @@ static int device_cus() {
     cus.store(c, std::memory_order_relaxed);
   }
   return c;
+}
+
+// The planes GEMM over x2 = [M][2K] bf16 (an fp32 activation as hi | lo).
+hipError_t launch_gemm_planes(const uint32_t *w, const float *scale, const uint16_t *x2, void *y, int yt_bf16, int M,
+                              int K, int N, hipStream_t stream, const float *bias) {
+  constexpr int BN = 256, WM = GEMM2_WM, WN = GEMM2_WN, NS = GEMM2_NS;
+  const long tiles128 = (long)((M + 127) / 128) * ((N + BN - 1) / BN);
+  const bool small = tiles128 <= device_cus();
+#define FRX_PLANES(BM, YT)                                                                                    \
+  {                                                                                                           \
+    using Core = Gemm2<BM, BN, WM, WN, NS, false>;                                                            \
+    constexpr int lds = Core::LDS_DWORDS * 4;                                                                 \
+    static std::atomic<uint64_t> done;                                                                        \
+    const hipError_t e =                                                                                      \
+        opt_in_lds(reinterpret_cast<const void *>(&gemm2_planes_kernel<BM, BN, WM, WN, NS, YT>), lds, done);  \
+    if (e != hipSuccess) return e;                                                                            \
+    hipLaunchKernelGGL((gemm2_planes_kernel<BM, BN, WM, WN, NS, YT>), dim3((N + BN - 1) / BN, (M + BM - 1) / BM), \
+                       dim3(WM * WN * 64), lds, stream, w, scale, x2, reinterpret_cast<YT *>(y), M, K, N, bias);   \
+    return hipGetLastError();                                                                                 \
+  }
+  if (small) {
+    if (yt_bf16) FRX_PLANES(64, uint16_t)
+    FRX_PLANES(64, float)
+  }
+  if (yt_bf16) FRX_PLANES(128, uint16_t)
+  FRX_PLANES(128, float)
+#undef FRX_PLANES
 }
 
 template <int BM, typename YT, int BN = 256>

@@ -107,10 +107,17 @@ constexpr int GEMV_SK_MAX_TILES = 65536;
 // kp columns (K % 64 == 0, N % 4 == 0, 16-byte aligned weights and x),
 // fp32 partials in `part` (gemm_splitk_workspace_bytes), then an ordered
 // reduction with the scale and bias.
-bool gemm_splitk_plan(int M, int K, int N, int cus, int *S, int *kp);
+// halves = 2: x is an fp32 activation as bf16 hi | lo rows ([M][2K]), S
+// counts the parts of both halves.
+bool gemm_splitk_plan(int M, int K, int N, int cus, int *S, int *kp, int halves = 1);
 size_t gemm_splitk_workspace_bytes(int M, int N, int S);
 hipError_t launch_gemm_splitk(const uint32_t *w, const float *scale, const void *x, void *y, int yt_bf16, int M, int K,
-                              int N, int S, int kp, float *part, hipStream_t stream, const float *bias);
+                              int N, int S, int kp, float *part, hipStream_t stream, const float *bias, int halves = 1);
+// Whole-K GEMM over x2 = [M][2K] bf16 hi | lo rows (K % 64 == 0, aligned).
+hipError_t launch_gemm_planes(const uint32_t *w, const float *scale, const uint16_t *x2, void *y, int yt_bf16, int M,
+                              int K, int N, hipStream_t stream, const float *bias);
+// x [M][K] f32 -> [M][2K] bf16 hi | lo rows (K even).
+hipError_t launch_to_planes(const float *x, uint16_t *x2, int M, int K, hipStream_t stream);
 // The balanced one-token kernel takes this launch (one token, K % 64 == 0
 // up to 16384, aligned operands, rows within its per-wave slots).
 bool gemv_bal_fits(const uint32_t *w, const void *x, int B, int K, int N);

@@ -158,6 +158,21 @@ def test_ffn_single_token_long_intermediate(ctx, H, I, act):
     assert_bf16_within_1ulp(yb.view(torch.int16).cpu().numpy().view(np.uint16), ref)
 
 
+@pytest.mark.parametrize("M,H,I", [(17, 1024, 2816), (40, 4096, 11008), (300, 512, 1344)])
+@pytest.mark.parametrize("xt", ["bf16", "f32"])
+def test_ffn_prefill_tokens(ctx, M, H, I, xt):
+    """Above 16 tokens: gate and up as linears (split over K where the tiles
+    leave compute units idle), the activation product in fp32, h as bf16
+    hi | lo rows and the down projection over both halves; bf16 output within
+    1 ulp, f32 within 1e-3 of the reference FFN."""
+    xf, xb, mats = make_ffn(f"ffn/prefill{M}_{H}_{I}", M, H, I)
+    xin = synth.bf16_bits_to_f32(xb) if xt == "bf16" else xf
+    ref = ref_ffn(xin, mats, False)
+    assert_close_f32(host(run_ffn(ctx, xf, xb, mats, frx.ACT_SILU, xt=xt)), ref)
+    yb = run_ffn(ctx, xf, xb, mats, frx.ACT_SILU, xt=xt, yt="bf16")
+    assert_bf16_within_1ulp(yb.view(torch.int16).cpu().numpy().view(np.uint16), ref)
+
+
 @pytest.mark.parametrize("M", [2, 24])
 def test_ffn_f32_in_bf16_out(ctx, M):
     xf, xb, mats = make_ffn(f"ffn/f32_{M}", M, 128, 208)

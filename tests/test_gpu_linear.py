@@ -655,3 +655,28 @@ def test_split_k_gemm_random_parity(ctx, M, K, N):
     assert_close_f32(host(_run(ctx, w, s, xf, xb, "bf16", "f32")), ref)
     yb = _run(ctx, w, s, xf, xb, "bf16", "bf16")
     assert_bf16_within_1ulp(yb.view(torch.int16).cpu().numpy().view(np.uint16), ref)
+
+
+@pytest.mark.parametrize("M,K,N", [(17, 4096, 11008), (300, 1024, 1000), (2048, 4096, 4096), (64, 11008, 4096)])
+def test_f32_prefill_planes_bit_exact_on_dyadic_inputs(ctx, M, K, N):
+    """f32 activations above 16 tokens: split once into bf16 hi | lo rows and
+    multiplied by the bf16 engine over both halves (split over K at small
+    token counts). Dyadic inputs are exact in the hi half."""
+    t, w, s, x, xb = _dyadic_case(M, K, N, 11 * M + K + N)
+    ref = (x @ t.T.astype(np.float32)) * s[None, :]
+    np.testing.assert_array_equal(host(_run(ctx, w, s, x, xb, "f32", "f32")), ref)
+    yb = _run(ctx, w, s, x, xb, "f32", "bf16")
+    np.testing.assert_array_equal(yb.view(torch.int16).cpu().numpy().view(np.uint16), synth.f32_to_bf16_bits(ref))
+
+
+@pytest.mark.parametrize("M,K,N", [(40, 2048, 3000), (17, 11008, 4096), (700, 4096, 1100)])
+def test_f32_prefill_planes_random_parity(ctx, M, K, N):
+    """Genuine f32 activations (the lo half matters) above 16 tokens against
+    the oracle, f32 and bf16 outputs."""
+    name = f"f32planes/{M}x{K}x{N}"
+    t, w, s, xf, xb = _case(name, M, K, N)
+    xf = synth.normal(synth.seed_of(name, "xf32"), M * K).reshape(M, K)
+    ref = oracle.ternary_matmul_u32(w, s, xf, M, K, N)
+    assert_close_f32(host(_run(ctx, w, s, xf, xb, "f32", "f32")), ref)
+    yb = _run(ctx, w, s, xf, xb, "f32", "bf16")
+    assert_bf16_within_1ulp(yb.view(torch.int16).cpu().numpy().view(np.uint16), ref)
