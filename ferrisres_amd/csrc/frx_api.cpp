@@ -591,8 +591,20 @@ frx_status frx_sparse24_ternary_linear(frx_ctx *ctx, const uint32_t *meta,
   if ((st = check_linear(ctx, meta, scale, x, xt, y, yt, M, K, N, true)) != FRX_OK) return st;
   Staged sg;
   if ((st = stage_linear(ctx, x, xt, scale, y, yt, M, K, N, &sg)) != FRX_OK) return st;
-  hipError_t e = frx::launch_gemm(meta, sg.scale, sg.x, xt == FRX_BF16, sg.y, yt == FRX_BF16, (int)M, (int)K,
-                                  (int)N, 1, ctx->stream);
+  hipError_t e;
+  int S = 0, sp = 0;
+  if (ctx->gemv_split != FRX_GEMV_SPLIT_NEVER && xt == FRX_BF16 && aligned16(sg.x) &&
+      (size_t)M * K * 2 < ((size_t)1 << 31) && frx::gemm_sp_splitk_plan((int)M, (int)K, (int)N, ctx->cus, &S, &sp)) {
+    // decode and small prefill: K split over workgroups on the sparse pipe
+    if ((st = ensure_buffer(ctx, &ctx->gk_ws, &ctx->gk_ws_bytes, frx::gemm_splitk_workspace_bytes((int)M, (int)N, S),
+                            "split-K GEMM workspace allocation")) != FRX_OK)
+      return st;
+    e = frx::launch_gemm_sp_splitk(meta, sg.scale, sg.x, sg.y, yt == FRX_BF16, (int)M, (int)K, (int)N, S, sp,
+                                   reinterpret_cast<float *>(ctx->gk_ws), ctx->stream, nullptr);
+  } else {
+    e = frx::launch_gemm(meta, sg.scale, sg.x, xt == FRX_BF16, sg.y, yt == FRX_BF16, (int)M, (int)K, (int)N, 1,
+                         ctx->stream);
+  }
   if (e == hipSuccess) e = unstage_linear(ctx, sg);
   if (e != hipSuccess) return hip_fail(ctx, e, "sparse24_ternary_linear launch");
   return FRX_OK;

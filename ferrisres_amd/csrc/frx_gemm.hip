@@ -128,6 +128,26 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm2_splitk_kernel(
                                          n_count, nullptr);
 }
 
+// The same split over 2:4 weights (GPU 5-bit layout, wpr words per row):
+// part s multiplies steps [s sp, (s + 1) sp) on the sparse matrix pipe.
+template <int BM, int BN, int WM, int WN, int NS>
+__global__ __launch_bounds__(WM *WN * 64) void gemm2sp_splitk_kernel(
+    const uint32_t *__restrict__ meta, const uint16_t *__restrict__ X, float *__restrict__ part, int M, int K, int N,
+    int sp) {
+  using Core = Gemm2<BM, BN, WM, WN, NS, false>;
+  extern __shared__ __align__(16) uint32_t lds[];
+  const int nt = blockIdx.x, mt = blockIdx.y, s = blockIdx.z;
+  const int n0 = nt * BN, m0 = mt * BM;
+  const int nks = K >> 6, s0 = s * sp, ns = min(sp, nks - s0);
+  const int wpr = ((K >> 2) + 5) / 6;
+  f32x4 acc[Core::FN][Core::FM];
+  const int m_count = min(BM, M - m0), n_count = min(BN, N - n0);
+  Core::run_sp(lds, X + (size_t)m0 * K, (uint32_t)m_count * (uint32_t)K * 2u, m_count, meta + (size_t)n0 * wpr,
+               n_count, K, wpr, acc, s0, ns);
+  Core::template store_tile<float, true>(lds, acc, nullptr, part + (size_t)s * M * N, (size_t)N, m0, m_count, n0,
+                                         n_count, nullptr);
+}
+
 // Whole-K GEMM over an fp32 activation stored as bf16 hi | lo halves of
 // each row ([M][2K]): one pass of 2K columns in which the weight columns
 // wrap at K (the engine's wk), i.e. acc = W x_hi + W x_lo.
@@ -212,6 +232,47 @@ bool gemm_splitk_plan(int M, int K, int N, int cus, int *S, int *kp, int halves)
 
 size_t gemm_splitk_workspace_bytes(int M, int N, int S) { return (size_t)S * M * N * 4; }
 
+constexpr int GEMM_SPSK_BM = 64;  // 4 token blocks, the fewest the sparse schedule takes
+
+// 2:4 weights, 1 token and more, where 64-token tiles leave at least half of
+// the compute units idle, or at rows of 16384 codes and more any of them
+// (there a second workgroup per CU outweighs the partials' traffic: 8192 x
+// 28672 at 512 tokens 283 -> 242 us; at 11008 x 4096, 256 tokens, 47 ->
+// 53 us): parts of at least 8 steps, about two workgroups per CU.
+bool gemm_sp_splitk_plan(int M, int K, int N, int cus, int *S, int *sp) {
+  if (M < 1 || K % 64 != 0 || N % 4 != 0) return false;
+  const long tiles = (long)((M + GEMM_SPSK_BM - 1) / GEMM_SPSK_BM) * ((N + 255) / 256);
+  if (2 * tiles > cus && (tiles > cus || K < 16384)) return false;
+  const int nks = K / 64;
+  const int s = (int)std::min<long>((2L * cus + tiles - 1) / tiles, nks / 8);
+  if (s < 2) return false;
+  *sp = (nks + s - 1) / s;
+  *S = (nks + *sp - 1) / *sp;
+  return *S >= 2;
+}
+
+hipError_t launch_gemm_sp_splitk(const uint32_t *meta, const float *scale, const void *x, void *y, int yt_bf16, int M,
+                                 int K, int N, int S, int sp, float *part, hipStream_t stream, const float *bias) {
+  constexpr int BM = GEMM_SPSK_BM, BN = 256, WM = 1, WN = 4, NS = 4;
+  using Core = Gemm2<BM, BN, WM, WN, NS, false>;
+  constexpr int lds = Core::LDS_DWORDS * 4;
+  static std::atomic<uint64_t> done;
+  hipError_t e = opt_in_lds(reinterpret_cast<const void *>(&gemm2sp_splitk_kernel<BM, BN, WM, WN, NS>), lds, done);
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL((gemm2sp_splitk_kernel<BM, BN, WM, WN, NS>), dim3((N + BN - 1) / BN, (M + BM - 1) / BM, S),
+                     dim3(WM * WN * 64), lds, stream, meta, reinterpret_cast<const uint16_t *>(x), part, M, K, N, sp);
+  if ((e = hipGetLastError()) != hipSuccess) return e;
+  const size_t quads = (size_t)M * N / 4;
+  const dim3 g((unsigned)((quads + 255) / 256));
+  if (yt_bf16)
+    hipLaunchKernelGGL(gemm_splitk_reduce<uint16_t>, g, dim3(256), 0, stream, part, S, M, N, scale, bias,
+                       reinterpret_cast<uint16_t *>(y));
+  else
+    hipLaunchKernelGGL(gemm_splitk_reduce<float>, g, dim3(256), 0, stream, part, S, M, N, scale, bias,
+                       reinterpret_cast<float *>(y));
+  return hipGetLastError();
+}
+
 hipError_t launch_gemm_splitk(const uint32_t *w, const float *scale, const void *x, void *y, int yt_bf16, int M, int K,
                               int N, int S, int kp, float *part, hipStream_t stream, const float *bias, int halves) {
   constexpr int BM = GEMM_SK_BM, BN = 256, WM = 1, WN = 4, NS = 4;
@@ -252,8 +313,9 @@ constexpr int GEMM2_NS = 4;
 // 11008: dense 76 / 184 us against 65 / 175 us, 2:4 87 / 195 us against
 // 71 / 157 us.
 constexpr int GEMM2_WM = 1, GEMM2_WN = 4;
-// Tokens per tile of the 2:4 launches (64 measured slower there: 83 / 203 us
-// against 71 / 158 us at 2048 x 4096 x 4096 / 11008).
+// Tokens per tile of the 2:4 launches with at least one 128-token tile per
+// compute unit (64 measured slower there: 83 / 203 us against 71 / 158 us at
+// 2048 x 4096 x 4096 / 11008).
 constexpr int GEMM2SP_BM = 128;
 
 // Compute units of the current device (queried once).
@@ -328,10 +390,10 @@ static hipError_t launch_gemm2_t(const uint32_t *w, const float *scale, const vo
   return launch_gemm2_bm<128, YT>(w, scale, x, y, M, K, N, stream, bias);
 }
 
-template <typename YT>
-static hipError_t launch_gemm2sp_t(const uint32_t *meta, const float *scale, const void *x, void *y,
-                                   int M, int K, int N, hipStream_t stream, const float *bias) {
-  constexpr int BM = GEMM2SP_BM, BN = 256, WM = GEMM2_WM, WN = GEMM2_WN, NS = GEMM2_NS;
+template <int BM, typename YT>
+static hipError_t launch_gemm2sp_bm(const uint32_t *meta, const float *scale, const void *x, void *y,
+                                    int M, int K, int N, hipStream_t stream, const float *bias) {
+  constexpr int BN = 256, WM = GEMM2_WM, WN = GEMM2_WN, NS = GEMM2_NS;
   using Core = Gemm2<BM, BN, WM, WN, NS, false>;
   constexpr int lds = Core::LDS_DWORDS * 4;
   static std::atomic<uint64_t> done;
@@ -342,6 +404,16 @@ static hipError_t launch_gemm2sp_t(const uint32_t *meta, const float *scale, con
   hipLaunchKernelGGL((gemm2sp_kernel<BM, BN, WM, WN, NS, YT>), grid, dim3(WM * WN * 64), lds, stream, meta,
                      scale, reinterpret_cast<const uint16_t *>(x), reinterpret_cast<YT *>(y), M, K, N, bias);
   return hipGetLastError();
+}
+
+// 64-token tiles while even those do not outnumber the compute units (at
+// 11008 x 4096, 512 tokens: 344 tiles of 64 took 72 us, 172 of 128 64 us).
+template <typename YT>
+static hipError_t launch_gemm2sp_t(const uint32_t *meta, const float *scale, const void *x, void *y,
+                                   int M, int K, int N, hipStream_t stream, const float *bias) {
+  const long tiles128 = (long)((M + GEMM2SP_BM - 1) / GEMM2SP_BM) * ((N + 255) / 256);
+  if (2 * tiles128 <= device_cus()) return launch_gemm2sp_bm<64, YT>(meta, scale, x, y, M, K, N, stream, bias);
+  return launch_gemm2sp_bm<GEMM2SP_BM, YT>(meta, scale, x, y, M, K, N, stream, bias);
 }
 
 template <int XS, int WF, typename YT>

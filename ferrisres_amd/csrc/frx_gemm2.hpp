@@ -455,8 +455,12 @@ struct Gemm2 {
   // (row block, token block) and step; the first half of a step covers token
   // blocks 0 .. FM/2-1, the second half the rest plus the next stage's loads,
   // window reads and operand decode. Requires K % 64 == 0.
+  // s0 / nsteps: the steps (64 columns each) multiplied, default all of K;
+  // X and W stay addressed from column 0 (a step's metadata window depends
+  // on its absolute index).
   __device__ static void run_sp(uint32_t *lds, const uint16_t *X, uint32_t xbytes, int m_count,
-                                const uint32_t *W, int n_count, int K, int wpr, f32x4 (&acc)[FN][FM]) {
+                                const uint32_t *W, int n_count, int K, int wpr, f32x4 (&acc)[FN][FM], int s0 = 0,
+                                int nsteps = -1) {
     static_assert(NS >= 3 && FM % 2 == 0 && FM / 2 >= XDS, "sparse schedule");
     uint32_t xv[XPW], wv[SWPW];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -482,10 +486,10 @@ struct Gemm2 {
     const int l16 = lane & 15, g = lane >> 4;
     const int r0 = wm * TM + l16;
     const int wrow = wn * TN + l16;
-    const int nks = (K + 63) >> 6;
+    const int nks = nsteps < 0 ? (K + 63) >> 6 : nsteps;
 
 #pragma unroll
-    for (int s = 0; s < NS - 1; s++) issue_sp(lds + s * STAGE, xr, wr, xv, wv, min(s, nks - 1));
+    for (int s = 0; s < NS - 1; s++) issue_sp(lds + s * STAGE, xr, wr, xv, wv, s0 + min(s, nks - 1));
     wait_vmcnt<(NS - 2) * SLPW>();
     barrier_nofence();
 
@@ -495,7 +499,7 @@ struct Gemm2 {
     {
       uint32_t wa[FN], wb[FN];
       int o5;
-      sp_read(lds + XSTAGE, 0, wrow, g, wa, wb, o5);
+      sp_read(lds + XSTAGE, s0, wrow, g, wa, wb, o5);
 #pragma unroll
       for (int d = 0; d < XDS; d++) bn[d] = xop_sp(lds, r0, g, d);
 #pragma unroll
@@ -527,10 +531,11 @@ struct Gemm2 {
       for (int fm = FM / 2; fm < FM; fm++) {
         if (fm + XDS < FM) b[fm + XDS] = xop_sp(cur, r0, g, fm + XDS);
         else bn[fm + XDS - FM] = xop_sp(nxt, r0, g, fm + XDS - FM);
-        if (fm == FM / 2) sp_read(nxt + XSTAGE, t + 1, wrow, g, wa, wb, o5);
+        if (fm == FM / 2) sp_read(nxt + XSTAGE, s0 + t + 1, wrow, g, wa, wb, o5);
 #pragma unroll
         for (int fn = 0; fn < FN; fn++) smfmac16_acc(acc[fn][fm], a[fn], b[fm], ix[fn]);
-        if (fm == FM / 2) issue_sp(lds + ((t + NS - 1) % NS) * STAGE, xr, wr, xv, wv, min(t + NS - 1, nks - 1));
+        if (fm == FM / 2)
+          issue_sp(lds + ((t + NS - 1) % NS) * STAGE, xr, wr, xv, wv, s0 + min(t + NS - 1, nks - 1));
         if (fm > FM / 2 && fm - FM / 2 - 1 < FN) {
           const int fn = fm - FM / 2 - 1;
           sp_decode(wa[fn], wb[fn], o5, an[fn], ixn[fn]);

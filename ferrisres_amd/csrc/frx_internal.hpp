@@ -113,6 +113,10 @@ bool gemm_splitk_plan(int M, int K, int N, int cus, int *S, int *kp, int halves 
 size_t gemm_splitk_workspace_bytes(int M, int N, int S);
 hipError_t launch_gemm_splitk(const uint32_t *w, const float *scale, const void *x, void *y, int yt_bf16, int M, int K,
                               int N, int S, int kp, float *part, hipStream_t stream, const float *bias, int halves = 1);
+// The split for 2:4 weights (GPU layout), any token count from 1, bf16 x.
+bool gemm_sp_splitk_plan(int M, int K, int N, int cus, int *S, int *sp);
+hipError_t launch_gemm_sp_splitk(const uint32_t *meta, const float *scale, const void *x, void *y, int yt_bf16, int M,
+                                 int K, int N, int S, int sp, float *part, hipStream_t stream, const float *bias);
 // Whole-K GEMM over x2 = [M][2K] bf16 hi | lo rows (K % 64 == 0, aligned).
 hipError_t launch_gemm_planes(const uint32_t *w, const float *scale, const uint16_t *x2, void *y, int yt_bf16, int M,
                               int K, int N, hipStream_t stream, const float *bias);

@@ -119,3 +119,44 @@ def test_sparse_prefill_11008_sampled(ctx):
     xw = synth.bf16_bits_to_f32(xb)[rows]
     ref = oracle.sparse24_gpu_matmul(meta, s, np.ascontiguousarray(xw), len(rows), K, N)
     assert_close_f32(y[rows], ref.reshape(len(rows), N))
+
+
+@pytest.mark.parametrize("M,K,N", [(1, 4096, 11008), (5, 11008, 4096), (16, 4096, 11008), (17, 11008, 4096),
+                                   (200, 4096, 4096), (3, 2048, 300), (1600, 16384, 2048)])
+def test_sparse_split_k_bit_exact_on_dyadic(ctx, M, K, N):
+    """Decode and small prefill, where 64-token tiles leave compute units
+    idle: K is split into parts of whole 64-column steps (each reading its
+    own metadata windows) whose fp32 partials are added in part order. Dyadic
+    inputs: every sum exact, the same bits as the unsplit kernels (split mode
+    NEVER) and as the dense product, f32 and bf16 outputs."""
+    rng = np.random.default_rng(5 * M + K + N)
+    t = synth.sparse24_uniform(f"dysk/{M}x{K}x{N}", "w", N, K)
+    meta = frx.pack_sparse24_gpu(t)
+    x = (rng.integers(-64, 65, size=(M, K)) / 8.0).astype(np.float32)
+    s = (2.0 ** rng.integers(-4, 2, size=N)).astype(np.float32)
+    ref = (x @ t.T.astype(np.float32)) * s[None, :]
+    xb = synth.f32_to_bf16_bits(x)
+    np.testing.assert_array_equal(host(_run(ctx, meta, s, x, xb, "bf16", "f32")), ref)
+    yb = _run(ctx, meta, s, x, xb, "bf16", "bf16")
+    np.testing.assert_array_equal(yb.view(torch.int16).cpu().numpy().view(np.uint16), synth.f32_to_bf16_bits(ref))
+    ctx.set_gemv_split(frx.GEMV_SPLIT_NEVER)
+    try:
+        y0 = host(_run(ctx, meta, s, x, xb, "bf16", "f32"))
+    finally:
+        ctx.set_gemv_split(frx.GEMV_SPLIT_AUTO)
+    np.testing.assert_array_equal(y0, ref)
+
+
+@pytest.mark.parametrize("M", [1, 7, 48])
+def test_sparse_split_k_raw_metadata(ctx, M):
+    """Raw metadata words (patterns 6 and 7, stray bits 30-31) through the
+    split path: windows that straddle words at every step phase, against
+    the oracle."""
+    K, N = 4096, 512
+    rng = np.random.default_rng(91 + M)
+    wpr = (K // 4 + 5) // 6
+    meta = rng.integers(0, 2**32, size=(N, wpr), dtype=np.uint64).astype(np.uint32)
+    s = (rng.random(N) * 0.05 + 0.01).astype(np.float32)
+    xf, xb = synth.activations(f"sp24/rawsk{M}", "x", M, K)
+    ref = oracle.sparse24_gpu_matmul(meta, s, synth.bf16_bits_to_f32(xb), M, K, N)
+    assert_close_f32(host(_run(ctx, meta, s, xf, xb, "bf16", "f32")), ref)
