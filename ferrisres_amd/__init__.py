@@ -67,6 +67,8 @@ _SIGS = {
     "frx_ternary_linear": (_int, [_vp, _vp, _vp, _vp, _int, _vp, _int, _u32, _u32, _u32]),
     "frx_ternary_linear_bias": (_int, [_vp, _vp, _vp, _vp, _vp, _int, _vp, _int, _u32, _u32, _u32]),
     "frx_sparse24_ternary_linear": (_int, [_vp, _vp, _vp, _vp, _int, _vp, _int, _u32, _u32, _u32]),
+    "frx_sparse24_prepare": (_int, [_vp, _vp, _u32, _u32, _vp]),
+    "frx_sparse24_prepared_linear": (_int, [_vp, _vp, _vp, _vp, _int, _vp, _int, _u32, _u32, _u32]),
     "frx_ternary_linear_blocked": (_int, [_vp, _vp, _vp, _u32, _vp, _int, _vp, _int, _u32, _u32, _u32]),
     "frx_ternary_sparse_decode": (_int, [_vp, _vp, _vp, _vp, _vp, ctypes.c_float, _vp, _int, _vp, _int,
                                          _u32, _u32, _u32]),
@@ -361,6 +363,25 @@ class Context:
         _check(lib().frx_sparse24_ternary_linear(self._h, _ptr(meta), _ptr(scale), _ptr(x),
                                                  _dtype_code(x), _ptr(y), _dtype_code(y), M, K, N),
                self._h)
+        return y
+
+    def sparse24_prepare(self, meta, K: int, prepared):
+        """frx_sparse24_prepare: 2:4 metadata [N][ceil(ceil(K/4)/6)] u32 into
+        its prepared form [N][K/16] u32 (K % 64 == 0)."""
+        N = _rows(meta, ((K + 3) // 4 + 5) // 6, "meta")
+        _expect_numel(prepared, N * (K // 16), "prepared")
+        _check(lib().frx_sparse24_prepare(self._h, _ptr(meta), K, N, _ptr(prepared)), self._h)
+        return prepared
+
+    def sparse24_prepared_linear(self, prepared, scale, x, y):
+        """frx_sparse24_prepared_linear: the 2:4 linear over prepared
+        metadata (bf16 x)."""
+        M, K = _shape2(x, "x")
+        N = _rows(prepared, K // 16, "prepared")
+        _expect_numel(scale, N, "scale")
+        _expect_shape(y, (M, N), "y")
+        _check(lib().frx_sparse24_prepared_linear(self._h, _ptr(prepared), _ptr(scale), _ptr(x), _dtype_code(x),
+                                                  _ptr(y), _dtype_code(y), M, K, N), self._h)
         return y
 
     def ternary_linear_blocked(self, w, block_scales, block_size: int, x, y):

@@ -94,6 +94,8 @@ struct frx_ctx {
   size_t gk_ws_bytes = 0;
   void *xpl_ws = nullptr;  // f32 activations as bf16 hi | lo rows (GEMM above 16 tokens)
   size_t xpl_ws_bytes = 0;
+  void *spp_ws = nullptr;  // 2:4 metadata in its prepared form (GEMM above a few tokens)
+  size_t spp_ws_bytes = 0;
   unsigned *sk_cnt = nullptr;  // its per-row-tile arrival counters (zero between launches)
   int gemv_split = FRX_GEMV_SPLIT_AUTO;
   unsigned *ffn_bar = nullptr;  // grid-barrier words of the one-launch FFN
@@ -196,6 +198,7 @@ void frx_destroy(frx_ctx *ctx) {
   if (ctx->sk_ws) (void)hipFree(ctx->sk_ws);
   if (ctx->gk_ws) (void)hipFree(ctx->gk_ws);
   if (ctx->xpl_ws) (void)hipFree(ctx->xpl_ws);
+  if (ctx->spp_ws) (void)hipFree(ctx->spp_ws);
   if (ctx->sk_cnt) (void)hipFree(ctx->sk_cnt);
   if (ctx->ffn_bar) (void)hipFree(ctx->ffn_bar);
   for (void *p : ctx->retired) (void)hipFree(p);
@@ -582,6 +585,12 @@ frx_status frx_ternary_linear_group(frx_ctx *ctx, const void *x, frx_dtype xt, u
   return FRX_OK;
 }
 
+// Token count from which a 2:4 linear decodes its metadata once into the
+// prepared form (one pass over the matrix, 10.6 us at 11008 x 4096) before
+// the GEMM: at 512 tokens and more the cheaper operand decode repays it
+// (4096 x 11008 at 2048 tokens: 160 -> 145 us; at 256 tokens it is even).
+constexpr uint32_t SP24_PREP_MIN_TOKENS = 512;
+
 frx_status frx_sparse24_ternary_linear(frx_ctx *ctx, const uint32_t *meta,
                                        const float *scale, const void *x,
                                        frx_dtype xt, void *y, frx_dtype yt,
@@ -591,22 +600,83 @@ frx_status frx_sparse24_ternary_linear(frx_ctx *ctx, const uint32_t *meta,
   if ((st = check_linear(ctx, meta, scale, x, xt, y, yt, M, K, N, true)) != FRX_OK) return st;
   Staged sg;
   if ((st = stage_linear(ctx, x, xt, scale, y, yt, M, K, N, &sg)) != FRX_OK) return st;
-  hipError_t e;
+  hipError_t e = hipSuccess;
   int S = 0, sp = 0;
-  if (ctx->gemv_split != FRX_GEMV_SPLIT_NEVER && xt == FRX_BF16 && aligned16(sg.x) &&
-      (size_t)M * K * 2 < ((size_t)1 << 31) && frx::gemm_sp_splitk_plan((int)M, (int)K, (int)N, ctx->cus, &S, &sp)) {
+  const bool engine = xt == FRX_BF16 && aligned16(sg.x) && K % 64 == 0 && (size_t)M * K * 2 < ((size_t)1 << 31);
+  const bool split = engine && ctx->gemv_split != FRX_GEMV_SPLIT_NEVER &&
+                     frx::gemm_sp_splitk_plan((int)M, (int)K, (int)N, ctx->cus, &S, &sp);
+  const uint32_t *wm = meta;
+  int prepared = 0;
+  if (engine && M >= SP24_PREP_MIN_TOKENS) {
+    // the metadata decoded once into its prepared form for every token tile
+    if ((st = ensure_buffer(ctx, &ctx->spp_ws, &ctx->spp_ws_bytes, (size_t)N * K / 4,
+                            "2:4 prepared metadata allocation")) != FRX_OK)
+      return st;
+    e = frx::launch_sp24_prepare(meta, reinterpret_cast<uint32_t *>(ctx->spp_ws), (int)N, (int)K, ctx->stream);
+    if (e != hipSuccess) return hip_fail(ctx, e, "sparse24_ternary_linear prepare");
+    wm = reinterpret_cast<const uint32_t *>(ctx->spp_ws);
+    prepared = 1;
+  }
+  if (split) {
     // decode and small prefill: K split over workgroups on the sparse pipe
     if ((st = ensure_buffer(ctx, &ctx->gk_ws, &ctx->gk_ws_bytes, frx::gemm_splitk_workspace_bytes((int)M, (int)N, S),
                             "split-K GEMM workspace allocation")) != FRX_OK)
       return st;
-    e = frx::launch_gemm_sp_splitk(meta, sg.scale, sg.x, sg.y, yt == FRX_BF16, (int)M, (int)K, (int)N, S, sp,
-                                   reinterpret_cast<float *>(ctx->gk_ws), ctx->stream, nullptr);
+    e = frx::launch_gemm_sp_splitk(wm, sg.scale, sg.x, sg.y, yt == FRX_BF16, (int)M, (int)K, (int)N, S, sp,
+                                   reinterpret_cast<float *>(ctx->gk_ws), ctx->stream, nullptr, prepared);
+  } else if (prepared) {
+    e = frx::launch_gemm_sp_prepared(wm, sg.scale, sg.x, sg.y, yt == FRX_BF16, (int)M, (int)K, (int)N, ctx->stream,
+                                     nullptr);
   } else {
     e = frx::launch_gemm(meta, sg.scale, sg.x, xt == FRX_BF16, sg.y, yt == FRX_BF16, (int)M, (int)K, (int)N, 1,
                          ctx->stream);
   }
   if (e == hipSuccess) e = unstage_linear(ctx, sg);
   if (e != hipSuccess) return hip_fail(ctx, e, "sparse24_ternary_linear launch");
+  return FRX_OK;
+}
+
+frx_status frx_sparse24_prepare(frx_ctx *ctx, const uint32_t *meta, uint32_t K, uint32_t N, uint32_t *prepared) {
+  frx_status st = enter(ctx);
+  if (st != FRX_OK) return st;
+  if (!meta || !prepared) return fail(ctx, FRX_ERR_SHAPE, "null buffer pointer");
+  if (K == 0 || N == 0 || K % 64 != 0)
+    return fail(ctx, FRX_ERR_SHAPE, "prepared 2:4 form needs K a positive multiple of 64 (K=%u N=%u)", K, N);
+  if ((reinterpret_cast<uintptr_t>(meta) & 3) || !aligned16(prepared))
+    return fail(ctx, FRX_ERR_SHAPE, "meta must be 4-byte and prepared 16-byte aligned");
+  if ((size_t)N * K / 4 > (size_t)0xFFFFFFF0u)
+    return fail(ctx, FRX_ERR_SHAPE, "prepared matrix of %zu bytes exceeds 4 GiB", (size_t)N * K / 4);
+  const hipError_t e = frx::launch_sp24_prepare(meta, prepared, (int)N, (int)K, ctx->stream);
+  if (e != hipSuccess) return hip_fail(ctx, e, "sparse24_prepare launch");
+  return FRX_OK;
+}
+
+frx_status frx_sparse24_prepared_linear(frx_ctx *ctx, const uint32_t *prepared, const float *scale, const void *x,
+                                        frx_dtype xt, void *y, frx_dtype yt, uint32_t M, uint32_t K, uint32_t N) {
+  frx_status st = enter(ctx);
+  if (st != FRX_OK) return st;
+  if ((st = check_linear(ctx, prepared, scale, x, xt, y, yt, M, K, N, false)) != FRX_OK) return st;
+  if (K % 64 != 0) return fail(ctx, FRX_ERR_SHAPE, "prepared 2:4 form needs K a multiple of 64 (K=%u)", K);
+  if (xt != FRX_BF16) return fail(ctx, FRX_ERR_UNSUPPORTED, "the prepared 2:4 linear takes bf16 activations");
+  if (!aligned16(prepared)) return fail(ctx, FRX_ERR_SHAPE, "prepared must be 16-byte aligned");
+  if ((size_t)M * K * 2 >= ((size_t)1 << 31))
+    return fail(ctx, FRX_ERR_UNSUPPORTED, "x of %zu bytes exceeds 2 GiB", (size_t)M * K * 2);
+  Staged sg;
+  if ((st = stage_linear(ctx, x, xt, scale, y, yt, M, K, N, &sg)) != FRX_OK) return st;
+  hipError_t e;
+  int S = 0, sp = 0;
+  if (ctx->gemv_split != FRX_GEMV_SPLIT_NEVER && frx::gemm_sp_splitk_plan((int)M, (int)K, (int)N, ctx->cus, &S, &sp)) {
+    if ((st = ensure_buffer(ctx, &ctx->gk_ws, &ctx->gk_ws_bytes, frx::gemm_splitk_workspace_bytes((int)M, (int)N, S),
+                            "split-K GEMM workspace allocation")) != FRX_OK)
+      return st;
+    e = frx::launch_gemm_sp_splitk(prepared, sg.scale, sg.x, sg.y, yt == FRX_BF16, (int)M, (int)K, (int)N, S, sp,
+                                   reinterpret_cast<float *>(ctx->gk_ws), ctx->stream, nullptr, 1);
+  } else {
+    e = frx::launch_gemm_sp_prepared(prepared, sg.scale, sg.x, sg.y, yt == FRX_BF16, (int)M, (int)K, (int)N,
+                                     ctx->stream, nullptr);
+  }
+  if (e == hipSuccess) e = unstage_linear(ctx, sg);
+  if (e != hipSuccess) return hip_fail(ctx, e, "sparse24_prepared_linear launch");
   return FRX_OK;
 }
 

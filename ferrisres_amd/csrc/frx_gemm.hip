@@ -79,9 +79,10 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm2_kernel(
   Core::template store_tile<YT>(lds, acc, scale, Y, (size_t)N, m0, m_count, n0, n_count, bias);
 }
 
-// 2:4 weights (GPU 5-bit layout), bf16 activations, K % 64 == 0: the
-// pipelined engine on the sparse matrix pipe.
-template <int BM, int BN, int WM, int WN, int NS, typename YT>
+// 2:4 weights (GPU 5-bit layout, or PREP: its prepared form, [N][K/16]
+// words), bf16 activations, K % 64 == 0: the pipelined engine on the sparse
+// matrix pipe.
+template <int BM, int BN, int WM, int WN, int NS, typename YT, bool PREP>
 __global__ __launch_bounds__(WM *WN * 64) void gemm2sp_kernel(
     const uint32_t *__restrict__ meta, const float *__restrict__ scale,
     const uint16_t *__restrict__ X, YT *__restrict__ Y, int M, int K, int N,
@@ -94,9 +95,37 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm2sp_kernel(
   const int wpr = ((K >> 2) + 5) / 6;
   f32x4 acc[Core::FN][Core::FM];
   const int m_count = min(BM, M - m0), n_count = min(BN, N - n0);
-  Core::run_sp(lds, X + (size_t)m0 * K, (uint32_t)m_count * (uint32_t)K * 2u, m_count,
-               meta + (size_t)n0 * wpr, n_count, K, wpr, acc);
+  Core::template run_sp<PREP>(lds, X + (size_t)m0 * K, (uint32_t)m_count * (uint32_t)K * 2u, m_count,
+                              meta + (size_t)n0 * (PREP ? K >> 4 : wpr), n_count, K, wpr, acc);
   Core::template store_tile<YT>(lds, acc, scale, Y, (size_t)N, m0, m_count, n0, n_count, bias);
+}
+
+// The prepared form of 2:4 metadata (K % 64 == 0): word j of row n covers
+// groups 16 (j / 4) + 4 (j % 4) .. + 3 (sp24p_word), [N][K/16] words.
+// One thread per (row, step): the step's 16 groups lie in the 4-word window
+// from word floor(16 s / 6) of the row (6 groups of 5 bits per word, bits
+// 30-31 belong to no group); its 4 prepared words are one 16-byte store.
+__global__ void sp24_prepare_kernel(const uint32_t *__restrict__ meta, u32x4 *__restrict__ out, int N, int K) {
+  const uint32_t wpr = ((uint32_t)(K >> 2) + 5u) / 6u, nks = (uint32_t)K >> 6;
+  const uint32_t total = (uint32_t)N * nks;
+  for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < total; i += gridDim.x * blockDim.x) {
+    const uint32_t n = i / nks, st = i - n * nks;
+    const uint32_t q0 = (16u * st) / 6u, r = 16u * st - 6u * q0;
+    const uint32_t *row = meta + (size_t)n * wpr;
+    uint32_t w[4];
+#pragma unroll
+    for (int u = 0; u < 4; u++) w[u] = row[min(q0 + (uint32_t)u, wpr - 1u)] & 0x3FFFFFFFu;
+    u32x4 o;
+#pragma unroll
+    for (int g = 0; g < 4; g++) {
+      const uint32_t l0 = r + 4u * g, jw = l0 / 6u, sh = 5u * (l0 - 6u * jw);
+      const uint32_t lo = jw == 0 ? w[0] : jw == 1 ? w[1] : w[2];
+      const uint32_t hi = jw == 0 ? w[1] : jw == 1 ? w[2] : w[3];
+      const uint32_t F = (lo >> sh) | (sh > 10u ? hi << (30u - sh) : 0u);
+      o[g] = sp24p_word(F);
+    }
+    out[i] = o;
+  }
 }
 
 // Split-K dense GEMM for launches with fewer tiles than compute units (17
@@ -130,7 +159,7 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm2_splitk_kernel(
 
 // The same split over 2:4 weights (GPU 5-bit layout, wpr words per row):
 // part s multiplies steps [s sp, (s + 1) sp) on the sparse matrix pipe.
-template <int BM, int BN, int WM, int WN, int NS>
+template <int BM, int BN, int WM, int WN, int NS, bool PREP>
 __global__ __launch_bounds__(WM *WN * 64) void gemm2sp_splitk_kernel(
     const uint32_t *__restrict__ meta, const uint16_t *__restrict__ X, float *__restrict__ part, int M, int K, int N,
     int sp) {
@@ -142,8 +171,8 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm2sp_splitk_kernel(
   const int wpr = ((K >> 2) + 5) / 6;
   f32x4 acc[Core::FN][Core::FM];
   const int m_count = min(BM, M - m0), n_count = min(BN, N - n0);
-  Core::run_sp(lds, X + (size_t)m0 * K, (uint32_t)m_count * (uint32_t)K * 2u, m_count, meta + (size_t)n0 * wpr,
-               n_count, K, wpr, acc, s0, ns);
+  Core::template run_sp<PREP>(lds, X + (size_t)m0 * K, (uint32_t)m_count * (uint32_t)K * 2u, m_count,
+                              meta + (size_t)n0 * (PREP ? K >> 4 : wpr), n_count, K, wpr, acc, s0, ns);
   Core::template store_tile<float, true>(lds, acc, nullptr, part + (size_t)s * M * N, (size_t)N, m0, m_count, n0,
                                          n_count, nullptr);
 }
@@ -195,7 +224,16 @@ __global__ __launch_bounds__(256) void gemm_splitk_reduce(const float *__restric
   const size_t MN = (size_t)M * N;
   if (i >= MN) return;
   f32x4 sum = *reinterpret_cast<const f32x4 *>(part + i);
-  for (int s = 1; s < S; s++) sum = sum + *reinterpret_cast<const f32x4 *>(part + (size_t)s * MN + i);
+  // eight parts' loads in flight at a time, added in part order
+  for (int s0 = 1; s0 < S; s0 += 8) {
+    f32x4 v[8];
+#pragma unroll
+    for (int u = 0; u < 8; u++)
+      if (s0 + u < S) v[u] = *reinterpret_cast<const f32x4 *>(part + (size_t)(s0 + u) * MN + i);
+#pragma unroll
+    for (int u = 0; u < 8; u++)
+      if (s0 + u < S) sum = sum + v[u];
+  }
   const int n = (int)(i % (size_t)N);
   f32x4 o;
 #pragma unroll
@@ -251,17 +289,36 @@ bool gemm_sp_splitk_plan(int M, int K, int N, int cus, int *S, int *sp) {
   return *S >= 2;
 }
 
-hipError_t launch_gemm_sp_splitk(const uint32_t *meta, const float *scale, const void *x, void *y, int yt_bf16, int M,
-                                 int K, int N, int S, int sp, float *part, hipStream_t stream, const float *bias) {
+template <bool PREP>
+static hipError_t launch_gemm2sp_parts(const uint32_t *meta, const void *x, int M, int K, int N, int S, int sp,
+                                       float *part, hipStream_t stream) {
   constexpr int BM = GEMM_SPSK_BM, BN = 256, WM = 1, WN = 4, NS = 4;
   using Core = Gemm2<BM, BN, WM, WN, NS, false>;
   constexpr int lds = Core::LDS_DWORDS * 4;
   static std::atomic<uint64_t> done;
-  hipError_t e = opt_in_lds(reinterpret_cast<const void *>(&gemm2sp_splitk_kernel<BM, BN, WM, WN, NS>), lds, done);
+  hipError_t e =
+      opt_in_lds(reinterpret_cast<const void *>(&gemm2sp_splitk_kernel<BM, BN, WM, WN, NS, PREP>), lds, done);
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL((gemm2sp_splitk_kernel<BM, BN, WM, WN, NS>), dim3((N + BN - 1) / BN, (M + BM - 1) / BM, S),
-                     dim3(WM * WN * 64), lds, stream, meta, reinterpret_cast<const uint16_t *>(x), part, M, K, N, sp);
-  if ((e = hipGetLastError()) != hipSuccess) return e;
+  hipLaunchKernelGGL((gemm2sp_splitk_kernel<BM, BN, WM, WN, NS, PREP>),
+                     dim3((N + BN - 1) / BN, (M + BM - 1) / BM, S), dim3(WM * WN * 64), lds, stream, meta,
+                     reinterpret_cast<const uint16_t *>(x), part, M, K, N, sp);
+  return hipGetLastError();
+}
+
+hipError_t launch_sp24_prepare(const uint32_t *meta, uint32_t *out, int N, int K, hipStream_t stream) {
+  const size_t total = (size_t)N * (K >> 6);
+  const unsigned blocks = (unsigned)std::min<size_t>((total + 255) / 256, 65536);
+  hipLaunchKernelGGL(sp24_prepare_kernel, dim3(blocks), dim3(256), 0, stream, meta, reinterpret_cast<u32x4 *>(out),
+                     N, K);
+  return hipGetLastError();
+}
+
+hipError_t launch_gemm_sp_splitk(const uint32_t *meta, const float *scale, const void *x, void *y, int yt_bf16, int M,
+                                 int K, int N, int S, int sp, float *part, hipStream_t stream, const float *bias,
+                                 int prepared) {
+  hipError_t e = prepared ? launch_gemm2sp_parts<true>(meta, x, M, K, N, S, sp, part, stream)
+                          : launch_gemm2sp_parts<false>(meta, x, M, K, N, S, sp, part, stream);
+  if (e != hipSuccess) return e;
   const size_t quads = (size_t)M * N / 4;
   const dim3 g((unsigned)((quads + 255) / 256));
   if (yt_bf16)
@@ -390,7 +447,7 @@ static hipError_t launch_gemm2_t(const uint32_t *w, const float *scale, const vo
   return launch_gemm2_bm<128, YT>(w, scale, x, y, M, K, N, stream, bias);
 }
 
-template <int BM, typename YT>
+template <int BM, typename YT, bool PREP>
 static hipError_t launch_gemm2sp_bm(const uint32_t *meta, const float *scale, const void *x, void *y,
                                     int M, int K, int N, hipStream_t stream, const float *bias) {
   constexpr int BN = 256, WM = GEMM2_WM, WN = GEMM2_WN, NS = GEMM2_NS;
@@ -398,22 +455,28 @@ static hipError_t launch_gemm2sp_bm(const uint32_t *meta, const float *scale, co
   constexpr int lds = Core::LDS_DWORDS * 4;
   static std::atomic<uint64_t> done;
   const hipError_t e =
-      opt_in_lds(reinterpret_cast<const void *>(&gemm2sp_kernel<BM, BN, WM, WN, NS, YT>), lds, done);
+      opt_in_lds(reinterpret_cast<const void *>(&gemm2sp_kernel<BM, BN, WM, WN, NS, YT, PREP>), lds, done);
   if (e != hipSuccess) return e;
   dim3 grid((N + BN - 1) / BN, (M + BM - 1) / BM);
-  hipLaunchKernelGGL((gemm2sp_kernel<BM, BN, WM, WN, NS, YT>), grid, dim3(WM * WN * 64), lds, stream, meta,
+  hipLaunchKernelGGL((gemm2sp_kernel<BM, BN, WM, WN, NS, YT, PREP>), grid, dim3(WM * WN * 64), lds, stream, meta,
                      scale, reinterpret_cast<const uint16_t *>(x), reinterpret_cast<YT *>(y), M, K, N, bias);
   return hipGetLastError();
 }
 
 // 64-token tiles while even those do not outnumber the compute units (at
 // 11008 x 4096, 512 tokens: 344 tiles of 64 took 72 us, 172 of 128 64 us).
-template <typename YT>
+template <typename YT, bool PREP>
 static hipError_t launch_gemm2sp_t(const uint32_t *meta, const float *scale, const void *x, void *y,
                                    int M, int K, int N, hipStream_t stream, const float *bias) {
   const long tiles128 = (long)((M + GEMM2SP_BM - 1) / GEMM2SP_BM) * ((N + 255) / 256);
-  if (2 * tiles128 <= device_cus()) return launch_gemm2sp_bm<64, YT>(meta, scale, x, y, M, K, N, stream, bias);
-  return launch_gemm2sp_bm<GEMM2SP_BM, YT>(meta, scale, x, y, M, K, N, stream, bias);
+  if (2 * tiles128 <= device_cus()) return launch_gemm2sp_bm<64, YT, PREP>(meta, scale, x, y, M, K, N, stream, bias);
+  return launch_gemm2sp_bm<GEMM2SP_BM, YT, PREP>(meta, scale, x, y, M, K, N, stream, bias);
+}
+
+hipError_t launch_gemm_sp_prepared(const uint32_t *prep, const float *scale, const void *x, void *y, int yt_bf16,
+                                   int M, int K, int N, hipStream_t stream, const float *bias) {
+  if (yt_bf16) return launch_gemm2sp_t<uint16_t, true>(prep, scale, x, y, M, K, N, stream, bias);
+  return launch_gemm2sp_t<float, true>(prep, scale, x, y, M, K, N, stream, bias);
 }
 
 template <int XS, int WF, typename YT>
@@ -450,8 +513,8 @@ hipError_t launch_gemm(const uint32_t *w, const float *scale, const void *x,
     return launch_gemm2_t<float>(w, scale, x, y, M, K, N, stream, bias);
   }
   if (sp24 && xt_bf16 && K % 64 == 0 && M > 16) {
-    if (yt_bf16) return launch_gemm2sp_t<uint16_t>(w, scale, x, y, M, K, N, stream, bias);
-    return launch_gemm2sp_t<float>(w, scale, x, y, M, K, N, stream, bias);
+    if (yt_bf16) return launch_gemm2sp_t<uint16_t, false>(w, scale, x, y, M, K, N, stream, bias);
+    return launch_gemm2sp_t<float, false>(w, scale, x, y, M, K, N, stream, bias);
   }
   if (sp24) return launch_gemm_wf<WF_SP24>(w, scale, x, xt_bf16, y, yt_bf16, M, K, N, stream, bias);
   return launch_gemm_wf<WF_DENSE>(w, scale, x, xt_bf16, y, yt_bf16, M, K, N, stream, bias);

@@ -127,6 +127,29 @@ __device__ __forceinline__ void sp24_operand(uint32_t F, u32x4 &a, uint32_t &idx
   idx = ix;
 }
 
+// The prepared form of four 2:4 groups (16 s + 4 g + q, q = 0..3, of one
+// row): position nibble q at bits 4q (q < 3) and 16 (q = 3), sign of the
+// lower / higher nonzero of group q at bit 12 + q / 28 + q. One word per
+// (row, step, lane group) decodes in 9 ops instead of the 5-bit layout's
+// window funnel and per-group lookups. F: the four 5-bit groups at bits 5q.
+// The signs (bits 5q + 3 and 5q + 4 of F) are gathered by one multiply:
+// bit 5q times 2^(12 - 4q') lands on 16 distinct positions, the q' = q ones
+// on 12 + q, so nothing carries into them.
+__device__ __forceinline__ uint32_t sp24p_word(uint32_t F) {
+  uint32_t d = 0;
+#pragma unroll
+  for (int q = 0; q < 4; q++)
+    d |= __builtin_amdgcn_ubfe(0xEEED9C84u, __builtin_amdgcn_ubfe(F, 5 * q, 3) << 2, 4) << (q < 3 ? 4 * q : 16);
+  const uint32_t sa = (((F >> 3) & 0x8421u) * 0x1111u) & 0xF000u;
+  const uint32_t sb = (((F >> 4) & 0x8421u) * 0x1111u) & 0xF000u;
+  return d | sa | (sb << 16);
+}
+__device__ __forceinline__ void sp24p_operand(uint32_t d, u32x4 &a, uint32_t &idx) {
+#pragma unroll
+  for (int q = 0; q < 4; q++) a[q] = ((d << (3 - q)) & 0x80008000u) | 0x40004000u;
+  idx = (d & 0xFFFu) | ((d >> 4) & 0xF000u);
+}
+
 __device__ __forceinline__ void lds_load4(__amdgpu_buffer_rsrc_t r, uint32_t *ldst,
                                           uint32_t voffset, uint32_t soffset) {
   __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_ptr_t)ldst, 4, voffset, soffset, 0, 0);
@@ -458,26 +481,44 @@ struct Gemm2 {
   // s0 / nsteps: the steps (64 columns each) multiplied, default all of K;
   // X and W stay addressed from column 0 (a step's metadata window depends
   // on its absolute index).
+  // PREP: W is the prepared form of the metadata (sp24p_operand: one word
+  // per row, step and lane group, [N][K/16] words like the dense codes), so
+  // the stage loads are the dense engine's and a fragment's operand is one
+  // LDS word; wpr is unused.
+  template <bool PREP = false>
   __device__ static void run_sp(uint32_t *lds, const uint16_t *X, uint32_t xbytes, int m_count,
                                 const uint32_t *W, int n_count, int K, int wpr, f32x4 (&acc)[FN][FM], int s0 = 0,
                                 int nsteps = -1) {
     static_assert(NS >= 3 && FM % 2 == 0 && FM / 2 >= XDS, "sparse schedule");
-    uint32_t xv[XPW], wv[SWPW];
+    constexpr int LP = PREP ? LPW : SLPW;  // load instructions per wave per stage
+    constexpr int WL = PREP ? WPW : SWPW;
+    uint32_t xv[XPW], wv[WL];
+    __amdgpu_buffer_rsrc_t wr[PREP ? WPW : 1];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    if constexpr (PREP) {
+      lane_offsets(xv, wv, nullptr, m_count, n_count, K, K, false, 0u);
 #pragma unroll
-    for (int i = 0; i < XPW; i++) {
-      const int r = (wave * XPW + i) * 8 + (lane >> 3);
-      const int rm = min(r, m_count - 1);
-      const uint32_t c = (lane & 7) ^ xswz(r);
-      xv[i] = (uint32_t)rm * (uint32_t)K * 2u + 16u * c;
-    }
+      for (int i = 0; i < WPW; i++) wr[i] = buffer_rsrc(W, (uint32_t)n_count * (uint32_t)(K >> 4) * 4u);
+    } else {
 #pragma unroll
-    for (int i = 0; i < SWPW; i++) {
-      const int n = min((wave * SWPW + i) * 16 + (lane >> 2), n_count - 1);
-      wv[i] = ((uint32_t)n * (uint32_t)wpr + (uint32_t)(lane & 3)) * 4u;
+      for (int i = 0; i < XPW; i++) {
+        const int r = (wave * XPW + i) * 8 + (lane >> 3);
+        const int rm = min(r, m_count - 1);
+        const uint32_t c = (lane & 7) ^ xswz(r);
+        xv[i] = (uint32_t)rm * (uint32_t)K * 2u + 16u * c;
+      }
+#pragma unroll
+      for (int i = 0; i < SWPW; i++) {
+        const int n = min((wave * SWPW + i) * 16 + (lane >> 2), n_count - 1);
+        wv[i] = ((uint32_t)n * (uint32_t)wpr + (uint32_t)(lane & 3)) * 4u;
+      }
+      wr[0] = buffer_rsrc(W, (uint32_t)n_count * (uint32_t)wpr * 4u);
     }
     const __amdgpu_buffer_rsrc_t xr = buffer_rsrc(X, xbytes);
-    const __amdgpu_buffer_rsrc_t wr = buffer_rsrc(W, (uint32_t)n_count * (uint32_t)wpr * 4u);
+    auto load = [&](uint32_t *stage, int s) {
+      if constexpr (PREP) issue(stage, xr, wr, xv, wv, 64 * s, 64 * s);
+      else issue_sp(stage, xr, wr[0], xv, wv, s);
+    };
 #pragma unroll
     for (int fn = 0; fn < FN; fn++)
 #pragma unroll
@@ -487,10 +528,23 @@ struct Gemm2 {
     const int r0 = wm * TM + l16;
     const int wrow = wn * TN + l16;
     const int nks = nsteps < 0 ? (K + 63) >> 6 : nsteps;
+    // the fragment words of step s from its W stage, and their operands
+    auto wread = [&](const uint32_t *ws, int s, uint32_t (&wa)[FN], uint32_t (&wb)[FN], int &o5) {
+      if constexpr (PREP) {
+#pragma unroll
+        for (int fn = 0; fn < FN; fn++) wa[fn] = ws[(wrow + fn * 16) * 4 + g];
+      } else {
+        sp_read(ws, s, wrow, g, wa, wb, o5);
+      }
+    };
+    auto decode = [&](uint32_t wa, uint32_t wb, int o5, u32x4 &a, uint32_t &ix) {
+      if constexpr (PREP) sp24p_operand(wa, a, ix);
+      else sp_decode(wa, wb, o5, a, ix);
+    };
 
 #pragma unroll
-    for (int s = 0; s < NS - 1; s++) issue_sp(lds + s * STAGE, xr, wr, xv, wv, s0 + min(s, nks - 1));
-    wait_vmcnt<(NS - 2) * SLPW>();
+    for (int s = 0; s < NS - 1; s++) load(lds + s * STAGE, s0 + min(s, nks - 1));
+    wait_vmcnt<(NS - 2) * LP>();
     barrier_nofence();
 
     u32x4 a[FN];
@@ -498,12 +552,12 @@ struct Gemm2 {
     u32x8 bn[XDS];
     {
       uint32_t wa[FN], wb[FN];
-      int o5;
-      sp_read(lds + XSTAGE, s0, wrow, g, wa, wb, o5);
+      int o5 = 0;
+      wread(lds + XSTAGE, s0, wa, wb, o5);
 #pragma unroll
       for (int d = 0; d < XDS; d++) bn[d] = xop_sp(lds, r0, g, d);
 #pragma unroll
-      for (int fn = 0; fn < FN; fn++) sp_decode(wa[fn], wb[fn], o5, a[fn], ix[fn]);
+      for (int fn = 0; fn < FN; fn++) decode(wa[fn], wb[fn], o5, a[fn], ix[fn]);
     }
 
     for (int t = 0; t < nks; t++) {
@@ -520,7 +574,7 @@ struct Gemm2 {
         for (int fn = 0; fn < FN; fn++) smfmac16_acc(acc[fn][fm], a[fn], b[fm], ix[fn]);
         __builtin_amdgcn_sched_barrier(0);
       }
-      wait_vmcnt<(NS - 3) * SLPW>();
+      wait_vmcnt<(NS - 3) * LP>();
       barrier_nofence();
       __builtin_amdgcn_sched_barrier(0);
       uint32_t wa[FN], wb[FN];
@@ -531,19 +585,18 @@ struct Gemm2 {
       for (int fm = FM / 2; fm < FM; fm++) {
         if (fm + XDS < FM) b[fm + XDS] = xop_sp(cur, r0, g, fm + XDS);
         else bn[fm + XDS - FM] = xop_sp(nxt, r0, g, fm + XDS - FM);
-        if (fm == FM / 2) sp_read(nxt + XSTAGE, s0 + t + 1, wrow, g, wa, wb, o5);
+        if (fm == FM / 2) wread(nxt + XSTAGE, s0 + t + 1, wa, wb, o5);
 #pragma unroll
         for (int fn = 0; fn < FN; fn++) smfmac16_acc(acc[fn][fm], a[fn], b[fm], ix[fn]);
-        if (fm == FM / 2)
-          issue_sp(lds + ((t + NS - 1) % NS) * STAGE, xr, wr, xv, wv, s0 + min(t + NS - 1, nks - 1));
+        if (fm == FM / 2) load(lds + ((t + NS - 1) % NS) * STAGE, s0 + min(t + NS - 1, nks - 1));
         if (fm > FM / 2 && fm - FM / 2 - 1 < FN) {
           const int fn = fm - FM / 2 - 1;
-          sp_decode(wa[fn], wb[fn], o5, an[fn], ixn[fn]);
+          decode(wa[fn], wb[fn], o5, an[fn], ixn[fn]);
         }
         __builtin_amdgcn_sched_barrier(0);
       }
 #pragma unroll
-      for (int fn = FM / 2 - 1; fn < FN; fn++) sp_decode(wa[fn], wb[fn], o5, an[fn], ixn[fn]);
+      for (int fn = FM / 2 - 1; fn < FN; fn++) decode(wa[fn], wb[fn], o5, an[fn], ixn[fn]);
 #pragma unroll
       for (int fn = 0; fn < FN; fn++) {
         a[fn] = an[fn];

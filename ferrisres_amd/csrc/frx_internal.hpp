@@ -116,7 +116,13 @@ hipError_t launch_gemm_splitk(const uint32_t *w, const float *scale, const void 
 // The split for 2:4 weights (GPU layout), any token count from 1, bf16 x.
 bool gemm_sp_splitk_plan(int M, int K, int N, int cus, int *S, int *sp);
 hipError_t launch_gemm_sp_splitk(const uint32_t *meta, const float *scale, const void *x, void *y, int yt_bf16, int M,
-                                 int K, int N, int S, int sp, float *part, hipStream_t stream, const float *bias);
+                                 int K, int N, int S, int sp, float *part, hipStream_t stream, const float *bias,
+                                 int prepared);
+// 2:4 metadata (GPU 5-bit layout) -> its prepared form, [N][K/16] words
+// (K % 64 == 0), and the whole-K GEMM over it (bf16 x, aligned).
+hipError_t launch_sp24_prepare(const uint32_t *meta, uint32_t *out, int N, int K, hipStream_t stream);
+hipError_t launch_gemm_sp_prepared(const uint32_t *prep, const float *scale, const void *x, void *y, int yt_bf16,
+                                   int M, int K, int N, hipStream_t stream, const float *bias);
 // Whole-K GEMM over x2 = [M][2K] bf16 hi | lo rows (K % 64 == 0, aligned).
 hipError_t launch_gemm_planes(const uint32_t *w, const float *scale, const uint16_t *x2, void *y, int yt_bf16, int M,
                               int K, int N, hipStream_t stream, const float *bias);

@@ -218,6 +218,32 @@ frx_status frx_sparse24_ternary_linear(frx_ctx *ctx, const uint32_t *meta,
                                        frx_dtype xt, void *y, frx_dtype yt,
                                        uint32_t M, uint32_t K, uint32_t N);
 
+/* ---- 2:4 metadata in its prepared form --------------------------------------
+ * No counterpart in the reference (its WGSL kernel decodes the 5-bit groups
+ * per use). For callers that keep 2:4 weights resident and run prefill-sized
+ * batches: the GPU 5-bit layout re-encoded once so that each (row, 64-column
+ * step, 16-column quarter) is one u32 from which the sparse matrix pipe's
+ * operands decode in 9 ops (position nibbles as the pipe's index, the 8 sign
+ * bits gathered), instead of a window funnel and a lookup per group.
+ *   meta [N][ceil(ceil(K/4)/6)] u32 -> prepared [N][K/16] u32 (device,
+ *   16-byte aligned), K % 64 == 0; patterns 6 and 7 read as 5 and bits
+ *   30-31 of a word are ignored, as in frx_sparse24_ternary_linear.
+ * frx_sparse24_ternary_linear prepares into a context workspace by itself
+ * from 512 tokens; a caller that prepares at upload saves that pass
+ * (10.6 us at 11008 x 4096). */
+frx_status frx_sparse24_prepare(frx_ctx *ctx, const uint32_t *meta, uint32_t K,
+                                uint32_t N, uint32_t *prepared);
+
+/* frx_sparse24_ternary_linear over prepared metadata (frx_sparse24_prepare):
+ * the same products on the sparse matrix pipe, equal to it up to fp32
+ * summation order (bit for bit where both take the same engine, i.e. bf16 x
+ * with K % 64 == 0 at more than 16 tokens or where the K split applies).
+ * x must be FRX_BF16 (FRX_ERR_UNSUPPORTED otherwise); y f32 or bf16. */
+frx_status frx_sparse24_prepared_linear(frx_ctx *ctx, const uint32_t *prepared,
+                                        const float *scale, const void *x,
+                                        frx_dtype xt, void *y, frx_dtype yt,
+                                        uint32_t M, uint32_t K, uint32_t N);
+
 /* ---- MoE ternary expert layer -----------------------------------------------
  * Replaces the GPU-path MoE glue of the model (router, softmax, stable top-k,
  * per-expert ternary FFN, weighted sum; src/model/cpu_block_attn_res.rs:

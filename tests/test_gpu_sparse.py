@@ -147,12 +147,12 @@ def test_sparse_split_k_bit_exact_on_dyadic(ctx, M, K, N):
     np.testing.assert_array_equal(y0, ref)
 
 
-@pytest.mark.parametrize("M", [1, 7, 48])
-def test_sparse_split_k_raw_metadata(ctx, M):
+@pytest.mark.parametrize("M,K,N", [(1, 4096, 512), (7, 4096, 512), (48, 4096, 512), (600, 4096, 512),
+                                   (1024, 1024, 4096)])
+def test_sparse_split_k_raw_metadata(ctx, M, K, N):
     """Raw metadata words (patterns 6 and 7, stray bits 30-31) through the
-    split path: windows that straddle words at every step phase, against
-    the oracle."""
-    K, N = 4096, 512
+    split path (windows that straddle words at every step phase) and, from
+    512 tokens, the prepared form (split and whole-K), against the oracle."""
     rng = np.random.default_rng(91 + M)
     wpr = (K // 4 + 5) // 6
     meta = rng.integers(0, 2**32, size=(N, wpr), dtype=np.uint64).astype(np.uint32)
@@ -160,3 +160,78 @@ def test_sparse_split_k_raw_metadata(ctx, M):
     xf, xb = synth.activations(f"sp24/rawsk{M}", "x", M, K)
     ref = oracle.sparse24_gpu_matmul(meta, s, synth.bf16_bits_to_f32(xb), M, K, N)
     assert_close_f32(host(_run(ctx, meta, s, xf, xb, "bf16", "f32")), ref)
+
+
+def _prepare(ctx, meta, K):
+    N = meta.shape[0]
+    prep = torch.empty((N, K // 16), dtype=torch.int32, device="cuda:0")
+    ctx.sparse24_prepare(dev_u32(meta), K, prep)
+    return prep
+
+
+@pytest.mark.parametrize("M,K,N", [(1, 4096, 11008), (16, 1024, 300), (64, 4096, 4096), (700, 2048, 1000),
+                                   (2048, 4096, 4096)])
+def test_prepared_linear_bit_exact_on_dyadic(ctx, M, K, N):
+    """frx_sparse24_prepare + frx_sparse24_prepared_linear: dyadic inputs give
+    the exact product, and the same bits as frx_sparse24_ternary_linear,
+    bf16 and f32 outputs."""
+    rng = np.random.default_rng(7 * M + K + N)
+    t = synth.sparse24_uniform(f"prep/{M}x{K}x{N}", "w", N, K)
+    meta = frx.pack_sparse24_gpu(t)
+    x = (rng.integers(-64, 65, size=(M, K)) / 8.0).astype(np.float32)
+    s = (2.0 ** rng.integers(-4, 2, size=N)).astype(np.float32)
+    ref = (x @ t.T.astype(np.float32)) * s[None, :]
+    xb = dev_bf16(synth.f32_to_bf16_bits(x))
+    prep = _prepare(ctx, meta, K)
+    y = torch.empty((M, N), dtype=torch.float32, device="cuda:0")
+    ctx.sparse24_prepared_linear(prep, dev_f32(s), xb, y)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(host(y), ref)
+    yb = torch.empty((M, N), dtype=torch.bfloat16, device="cuda:0")
+    ctx.sparse24_prepared_linear(prep, dev_f32(s), xb, yb)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(yb.view(torch.int16).cpu().numpy().view(np.uint16), synth.f32_to_bf16_bits(ref))
+
+
+@pytest.mark.parametrize("M", [3, 130, 1024])
+def test_prepared_linear_raw_metadata(ctx, M):
+    """Raw metadata words (patterns 6 and 7, stray bits 30-31) through the
+    prepared form, against the oracle and against the 5-bit entry."""
+    K, N = 2048, 768
+    rng = np.random.default_rng(5 + M)
+    wpr = (K // 4 + 5) // 6
+    meta = rng.integers(0, 2**32, size=(N, wpr), dtype=np.uint64).astype(np.uint32)
+    s = (rng.random(N) * 0.05 + 0.01).astype(np.float32)
+    xf, xb = synth.activations(f"sp24/prepraw{M}", "x", M, K)
+    ref = oracle.sparse24_gpu_matmul(meta, s, synth.bf16_bits_to_f32(xb), M, K, N)
+    prep = _prepare(ctx, meta, K)
+    y = torch.empty((M, N), dtype=torch.float32, device="cuda:0")
+    ctx.sparse24_prepared_linear(prep, dev_f32(s), dev_bf16(xb), y)
+    torch.cuda.synchronize()
+    assert_close_f32(host(y), ref)
+    y5 = host(_run(ctx, meta, s, xf, xb, "bf16", "f32"))
+    if M > 16:
+        np.testing.assert_array_equal(host(y), y5)
+
+
+def test_prepared_entry_errors(ctx):
+    """K % 64 != 0 and f32 activations are refused with a status, before any
+    launch; the context stays usable."""
+    N, K = 64, 256
+    t = synth.sparse24_uniform("prep/err", "w", N, K)
+    meta = dev_u32(frx.pack_sparse24_gpu(t))
+    bad = torch.empty((N, 96 // 16), dtype=torch.int32, device="cuda:0")
+    with pytest.raises(frx.FrxError) as e:
+        ctx.sparse24_prepare(dev_u32(frx.pack_sparse24_gpu(synth.sparse24_uniform("prep/err96", "w", N, 96))), 96,
+                             bad)
+    assert e.value.kind == "Shape"
+    prep = _prepare(ctx, frx.pack_sparse24_gpu(t), K)
+    s = dev_f32(np.full(N, 0.5, np.float32))
+    y = torch.empty((2, N), dtype=torch.float32, device="cuda:0")
+    with pytest.raises(frx.FrxError) as e:
+        ctx.sparse24_prepared_linear(prep, s, torch.zeros((2, K), dtype=torch.float32, device="cuda:0"), y)
+    assert e.value.kind == "Unsupported"
+    ctx.sparse24_prepared_linear(prep, s, torch.zeros((2, K), dtype=torch.bfloat16, device="cuda:0"), y)
+    torch.cuda.synchronize()
+    assert float(y.abs().max()) == 0.0
+    del meta
