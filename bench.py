@@ -479,7 +479,20 @@ def run_extra(torch, frx, synth, ctx, stream, dev, only=None, iters=200):
             res[f"sparse24_gemm_{M}x{K}x{N}"] = {"us": round(dt * 1e6, 2), "tflops_dense_equiv": round(tf, 1),
                                                  "frac_bf16_peak": round(tf / BF16_PEAK_TFLOPS, 4), **st}
             log(f"bench: 2:4 N={N}: {dt * 1e6:.1f} us, {tf:.1f} TFLOP/s dense-equivalent")
-            del meta
+            # the same weights prepared once (frx_sparse24_prepare at upload):
+            # the GEMM alone, and the preparing pass alone
+            prep = torch.empty((N, K // 16), dtype=torch.int32, device=dev)
+            st = {}
+            dtp = _time_kernel(torch, stream, lambda: ctx.sparse24_prepare(meta, K, prep), iters, stats=st)
+            res[f"sparse24_prepare_{N}x{K}"] = {"us": round(dtp * 1e6, 2), **st}
+            st = {}
+            dt = _time_kernel(torch, stream, lambda: ctx.sparse24_prepared_linear(prep, s, X, Y), iters, stats=st)
+            tf = 2.0 * M * N * K / dt / 1e12
+            res[f"sparse24_prepared_gemm_{M}x{K}x{N}"] = {
+                "us": round(dt * 1e6, 2), "tflops_dense_equiv": round(tf, 1),
+                "frac_bf16_peak": round(tf / BF16_PEAK_TFLOPS, 4), **st}
+            log(f"bench: 2:4 prepared N={N}: {dt * 1e6:.1f} us (prepare {dtp * 1e6:.1f} us)")
+            del meta, prep
         del w, Y
     if only is None:
         res["gemm_ceilings"] = gemm_ceilings(torch, stream, dev, X)
