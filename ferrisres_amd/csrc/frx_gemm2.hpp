@@ -473,6 +473,12 @@ struct Gemm2 {
   }
 
   static constexpr int XDS = 2;  // sparse: B operands read this many token blocks ahead
+  // More weight fragments per wave than second-half token blocks after the
+  // window read: the next step's operands are decoded in place, each right
+  // after its fragment's last sparse MFMA of the step (one operand set in
+  // registers; 2048 x 4096 x {4096, 11008} over prepared metadata 52.0 /
+  // 124.0 -> 50.5 / 120.5 us against a second set filled over the half).
+  static constexpr bool SP_INPLACE = FN > FM - FM / 2 - 1;
 
   // The 2:4 K loop: the schedule of run() with one sparse MFMA per
   // (row block, token block) and step; the first half of a step covers token
@@ -586,21 +592,33 @@ struct Gemm2 {
         if (fm + XDS < FM) b[fm + XDS] = xop_sp(cur, r0, g, fm + XDS);
         else bn[fm + XDS - FM] = xop_sp(nxt, r0, g, fm + XDS - FM);
         if (fm == FM / 2) wread(nxt + XSTAGE, s0 + t + 1, wa, wb, o5);
+        if (SP_INPLACE && fm == FM - 1) {
+          // the next step's operands decoded into a[fn] right after its last
+          // use (more fragments than decode slots: no second operand set)
 #pragma unroll
-        for (int fn = 0; fn < FN; fn++) smfmac16_acc(acc[fn][fm], a[fn], b[fm], ix[fn]);
+          for (int fn = 0; fn < FN; fn++) {
+            smfmac16_acc(acc[fn][fm], a[fn], b[fm], ix[fn]);
+            decode(wa[fn], wb[fn], o5, a[fn], ix[fn]);
+          }
+        } else {
+#pragma unroll
+          for (int fn = 0; fn < FN; fn++) smfmac16_acc(acc[fn][fm], a[fn], b[fm], ix[fn]);
+        }
         if (fm == FM / 2) load(lds + ((t + NS - 1) % NS) * STAGE, s0 + min(t + NS - 1, nks - 1));
-        if (fm > FM / 2 && fm - FM / 2 - 1 < FN) {
+        if (!SP_INPLACE && fm > FM / 2 && fm - FM / 2 - 1 < FN) {
           const int fn = fm - FM / 2 - 1;
           decode(wa[fn], wb[fn], o5, an[fn], ixn[fn]);
         }
         __builtin_amdgcn_sched_barrier(0);
       }
+      if constexpr (!SP_INPLACE) {
 #pragma unroll
-      for (int fn = FM / 2 - 1; fn < FN; fn++) decode(wa[fn], wb[fn], o5, an[fn], ixn[fn]);
+        for (int fn = FM / 2 - 1; fn < FN; fn++) decode(wa[fn], wb[fn], o5, an[fn], ixn[fn]);
 #pragma unroll
-      for (int fn = 0; fn < FN; fn++) {
-        a[fn] = an[fn];
-        ix[fn] = ixn[fn];
+        for (int fn = 0; fn < FN; fn++) {
+          a[fn] = an[fn];
+          ix[fn] = ixn[fn];
+        }
       }
     }
     mfma_drain();
