@@ -602,11 +602,26 @@ frx_status frx_sparse24_ternary_linear(frx_ctx *ctx, const uint32_t *meta,
   if ((st = stage_linear(ctx, x, xt, scale, y, yt, M, K, N, &sg)) != FRX_OK) return st;
   hipError_t e = hipSuccess;
   int S = 0, sp = 0;
-  const bool engine = xt == FRX_BF16 && aligned16(sg.x) && K % 64 == 0 && (size_t)M * K * 2 < ((size_t)1 << 31);
+  // f32 x runs as bf16 hi | lo rows ([M][2K], |x - hi - lo| <= 2^-17 |x|)
+  // through the same sparse engine, both halves against the same weights
+  const bool planes = xt == FRX_F32 && aligned16(sg.x) && K % 64 == 0 && (size_t)M * K * 4 < ((size_t)1 << 31);
+  const bool engine =
+      planes || (xt == FRX_BF16 && aligned16(sg.x) && K % 64 == 0 && (size_t)M * K * 2 < ((size_t)1 << 31));
+  const int halves = planes ? 2 : 1;
   const bool split = engine && ctx->gemv_split != FRX_GEMV_SPLIT_NEVER &&
-                     frx::gemm_sp_splitk_plan((int)M, (int)K, (int)N, ctx->cus, &S, &sp);
+                     frx::gemm_sp_splitk_plan((int)M, (int)K, (int)N, ctx->cus, &S, &sp, halves);
   const uint32_t *wm = meta;
+  const void *xin = sg.x;
   int prepared = 0;
+  if (planes) {
+    if ((st = ensure_buffer(ctx, &ctx->xpl_ws, &ctx->xpl_ws_bytes, a256((size_t)M * K * 4),
+                            "activation planes allocation")) != FRX_OK)
+      return st;
+    e = frx::launch_to_planes(reinterpret_cast<const float *>(sg.x), reinterpret_cast<uint16_t *>(ctx->xpl_ws),
+                              (int)M, (int)K, ctx->stream);
+    if (e != hipSuccess) return hip_fail(ctx, e, "sparse24_ternary_linear planes");
+    xin = ctx->xpl_ws;
+  }
   if (engine && M >= SP24_PREP_MIN_TOKENS) {
     // the metadata decoded once into its prepared form for every token tile
     if ((st = ensure_buffer(ctx, &ctx->spp_ws, &ctx->spp_ws_bytes, (size_t)N * K / 4,
@@ -622,8 +637,11 @@ frx_status frx_sparse24_ternary_linear(frx_ctx *ctx, const uint32_t *meta,
     if ((st = ensure_buffer(ctx, &ctx->gk_ws, &ctx->gk_ws_bytes, frx::gemm_splitk_workspace_bytes((int)M, (int)N, S),
                             "split-K GEMM workspace allocation")) != FRX_OK)
       return st;
-    e = frx::launch_gemm_sp_splitk(wm, sg.scale, sg.x, sg.y, yt == FRX_BF16, (int)M, (int)K, (int)N, S, sp,
-                                   reinterpret_cast<float *>(ctx->gk_ws), ctx->stream, nullptr, prepared);
+    e = frx::launch_gemm_sp_splitk(wm, sg.scale, xin, sg.y, yt == FRX_BF16, (int)M, (int)K, (int)N, S, sp,
+                                   reinterpret_cast<float *>(ctx->gk_ws), ctx->stream, nullptr, prepared, halves);
+  } else if (planes) {
+    e = frx::launch_gemm_sp_planes(wm, prepared, sg.scale, reinterpret_cast<const uint16_t *>(xin), sg.y,
+                                   yt == FRX_BF16, (int)M, (int)K, (int)N, ctx->stream);
   } else if (prepared) {
     e = frx::launch_gemm_sp_prepared(wm, sg.scale, sg.x, sg.y, yt == FRX_BF16, (int)M, (int)K, (int)N, ctx->stream,
                                      nullptr);

@@ -82,7 +82,9 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm2_kernel(
 // 2:4 weights (GPU 5-bit layout, or PREP: its prepared form, [N][K/16]
 // words), bf16 activations, K % 64 == 0: the pipelined engine on the sparse
 // matrix pipe.
-template <int BM, int BN, int WM, int WN, int NS, typename YT, bool PREP>
+// HV = 2: X is an fp32 activation as bf16 hi | lo halves of each row
+// ([M][2K]); one K loop of 2K columns multiplies both by the same weights.
+template <int BM, int BN, int WM, int WN, int NS, typename YT, bool PREP, int HV>
 __global__ __launch_bounds__(WM *WN * 64) void gemm2sp_kernel(
     const uint32_t *__restrict__ meta, const float *__restrict__ scale,
     const uint16_t *__restrict__ X, YT *__restrict__ Y, int M, int K, int N,
@@ -92,11 +94,12 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm2sp_kernel(
   int nt, mt;
   xcd_tile(nt, mt);
   const int n0 = nt * BN, m0 = mt * BM;
-  const int wpr = ((K >> 2) + 5) / 6;
+  const int wpr = ((K >> 2) + 5) / 6, ldx = HV * K;
   f32x4 acc[Core::FN][Core::FM];
   const int m_count = min(BM, M - m0), n_count = min(BN, N - n0);
-  Core::template run_sp<PREP>(lds, X + (size_t)m0 * K, (uint32_t)m_count * (uint32_t)K * 2u, m_count,
-                              meta + (size_t)n0 * (PREP ? K >> 4 : wpr), n_count, K, wpr, acc);
+  Core::template run_sp<PREP, HV == 2>(lds, X + (size_t)m0 * ldx, (uint32_t)m_count * (uint32_t)ldx * 2u, m_count,
+                                       meta + (size_t)n0 * (PREP ? K >> 4 : wpr), n_count, K, wpr, acc, 0,
+                                       HV * (K >> 6), ldx);
   Core::template store_tile<YT>(lds, acc, scale, Y, (size_t)N, m0, m_count, n0, n_count, bias);
 }
 
@@ -159,20 +162,25 @@ __global__ __launch_bounds__(WM *WN * 64) void gemm2_splitk_kernel(
 
 // The same split over 2:4 weights (GPU 5-bit layout, wpr words per row):
 // part s multiplies steps [s sp, (s + 1) sp) on the sparse matrix pipe.
-template <int BM, int BN, int WM, int WN, int NS, bool PREP>
+// HV = 2: X rows are bf16 hi | lo halves ([M][2K]); parts 0 .. S/2 - 1 run
+// over the hi half and S/2 .. S - 1 over the lo half.
+template <int BM, int BN, int WM, int WN, int NS, bool PREP, int HV>
 __global__ __launch_bounds__(WM *WN * 64) void gemm2sp_splitk_kernel(
     const uint32_t *__restrict__ meta, const uint16_t *__restrict__ X, float *__restrict__ part, int M, int K, int N,
     int sp) {
   using Core = Gemm2<BM, BN, WM, WN, NS, false>;
   extern __shared__ __align__(16) uint32_t lds[];
   const int nt = blockIdx.x, mt = blockIdx.y, s = blockIdx.z;
+  const int sh = (int)gridDim.z / HV, half = s / sh, j = s - half * sh;
   const int n0 = nt * BN, m0 = mt * BM;
-  const int nks = K >> 6, s0 = s * sp, ns = min(sp, nks - s0);
-  const int wpr = ((K >> 2) + 5) / 6;
+  const int nks = K >> 6, s0 = j * sp, ns = min(sp, nks - s0);
+  const int wpr = ((K >> 2) + 5) / 6, ldx = HV * K;
   f32x4 acc[Core::FN][Core::FM];
   const int m_count = min(BM, M - m0), n_count = min(BN, N - n0);
-  Core::template run_sp<PREP>(lds, X + (size_t)m0 * K, (uint32_t)m_count * (uint32_t)K * 2u, m_count,
-                              meta + (size_t)n0 * (PREP ? K >> 4 : wpr), n_count, K, wpr, acc, s0, ns);
+  const uint32_t xo = (uint32_t)(half * K);  // the half's first column
+  Core::template run_sp<PREP>(lds, X + (size_t)m0 * ldx + xo, (uint32_t)m_count * (uint32_t)ldx * 2u - xo * 2u,
+                              m_count, meta + (size_t)n0 * (PREP ? K >> 4 : wpr), n_count, K, wpr, acc, s0, ns,
+                              ldx);
   Core::template store_tile<float, true>(lds, acc, nullptr, part + (size_t)s * M * N, (size_t)N, m0, m_count, n0,
                                          n_count, nullptr);
 }
@@ -277,19 +285,19 @@ constexpr int GEMM_SPSK_BM = 64;  // 4 token blocks, the fewest the sparse sched
 // (there a second workgroup per CU outweighs the partials' traffic: 8192 x
 // 28672 at 512 tokens 283 -> 242 us; at 11008 x 4096, 256 tokens, 47 ->
 // 53 us): parts of at least 8 steps, about two workgroups per CU.
-bool gemm_sp_splitk_plan(int M, int K, int N, int cus, int *S, int *sp) {
+bool gemm_sp_splitk_plan(int M, int K, int N, int cus, int *S, int *sp, int halves) {
   if (M < 1 || K % 64 != 0 || N % 4 != 0) return false;
   const long tiles = (long)((M + GEMM_SPSK_BM - 1) / GEMM_SPSK_BM) * ((N + 255) / 256);
   if (2 * tiles > cus && (tiles > cus || K < 16384)) return false;
   const int nks = K / 64;
-  const int s = (int)std::min<long>((2L * cus + tiles - 1) / tiles, nks / 8);
-  if (s < 2) return false;
+  const int s = (int)std::min<long>((2L * cus + tiles * halves - 1) / (tiles * halves), nks / 8);
+  if (s < 1 || halves * s < 2) return false;
   *sp = (nks + s - 1) / s;
-  *S = (nks + *sp - 1) / *sp;
-  return *S >= 2;
+  *S = halves * ((nks + *sp - 1) / *sp);
+  return true;
 }
 
-template <bool PREP>
+template <bool PREP, int HV>
 static hipError_t launch_gemm2sp_parts(const uint32_t *meta, const void *x, int M, int K, int N, int S, int sp,
                                        float *part, hipStream_t stream) {
   constexpr int BM = GEMM_SPSK_BM, BN = 256, WM = 1, WN = 4, NS = 4;
@@ -297,9 +305,9 @@ static hipError_t launch_gemm2sp_parts(const uint32_t *meta, const void *x, int 
   constexpr int lds = Core::LDS_DWORDS * 4;
   static std::atomic<uint64_t> done;
   hipError_t e =
-      opt_in_lds(reinterpret_cast<const void *>(&gemm2sp_splitk_kernel<BM, BN, WM, WN, NS, PREP>), lds, done);
+      opt_in_lds(reinterpret_cast<const void *>(&gemm2sp_splitk_kernel<BM, BN, WM, WN, NS, PREP, HV>), lds, done);
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL((gemm2sp_splitk_kernel<BM, BN, WM, WN, NS, PREP>),
+  hipLaunchKernelGGL((gemm2sp_splitk_kernel<BM, BN, WM, WN, NS, PREP, HV>),
                      dim3((N + BN - 1) / BN, (M + BM - 1) / BM, S), dim3(WM * WN * 64), lds, stream, meta,
                      reinterpret_cast<const uint16_t *>(x), part, M, K, N, sp);
   return hipGetLastError();
@@ -315,9 +323,14 @@ hipError_t launch_sp24_prepare(const uint32_t *meta, uint32_t *out, int N, int K
 
 hipError_t launch_gemm_sp_splitk(const uint32_t *meta, const float *scale, const void *x, void *y, int yt_bf16, int M,
                                  int K, int N, int S, int sp, float *part, hipStream_t stream, const float *bias,
-                                 int prepared) {
-  hipError_t e = prepared ? launch_gemm2sp_parts<true>(meta, x, M, K, N, S, sp, part, stream)
-                          : launch_gemm2sp_parts<false>(meta, x, M, K, N, S, sp, part, stream);
+                                 int prepared, int halves) {
+  hipError_t e;
+  if (halves == 2)
+    e = prepared ? launch_gemm2sp_parts<true, 2>(meta, x, M, K, N, S, sp, part, stream)
+                 : launch_gemm2sp_parts<false, 2>(meta, x, M, K, N, S, sp, part, stream);
+  else
+    e = prepared ? launch_gemm2sp_parts<true, 1>(meta, x, M, K, N, S, sp, part, stream)
+                 : launch_gemm2sp_parts<false, 1>(meta, x, M, K, N, S, sp, part, stream);
   if (e != hipSuccess) return e;
   const size_t quads = (size_t)M * N / 4;
   const dim3 g((unsigned)((quads + 255) / 256));
@@ -447,7 +460,7 @@ static hipError_t launch_gemm2_t(const uint32_t *w, const float *scale, const vo
   return launch_gemm2_bm<128, YT>(w, scale, x, y, M, K, N, stream, bias);
 }
 
-template <int BM, typename YT, bool PREP>
+template <int BM, typename YT, bool PREP, int HV>
 static hipError_t launch_gemm2sp_bm(const uint32_t *meta, const float *scale, const void *x, void *y,
                                     int M, int K, int N, hipStream_t stream, const float *bias) {
   constexpr int BN = 256, WM = GEMM2_WM, WN = GEMM2_WN, NS = GEMM2_NS;
@@ -455,28 +468,39 @@ static hipError_t launch_gemm2sp_bm(const uint32_t *meta, const float *scale, co
   constexpr int lds = Core::LDS_DWORDS * 4;
   static std::atomic<uint64_t> done;
   const hipError_t e =
-      opt_in_lds(reinterpret_cast<const void *>(&gemm2sp_kernel<BM, BN, WM, WN, NS, YT, PREP>), lds, done);
+      opt_in_lds(reinterpret_cast<const void *>(&gemm2sp_kernel<BM, BN, WM, WN, NS, YT, PREP, HV>), lds, done);
   if (e != hipSuccess) return e;
   dim3 grid((N + BN - 1) / BN, (M + BM - 1) / BM);
-  hipLaunchKernelGGL((gemm2sp_kernel<BM, BN, WM, WN, NS, YT, PREP>), grid, dim3(WM * WN * 64), lds, stream, meta,
-                     scale, reinterpret_cast<const uint16_t *>(x), reinterpret_cast<YT *>(y), M, K, N, bias);
+  hipLaunchKernelGGL((gemm2sp_kernel<BM, BN, WM, WN, NS, YT, PREP, HV>), grid, dim3(WM * WN * 64), lds, stream,
+                     meta, scale, reinterpret_cast<const uint16_t *>(x), reinterpret_cast<YT *>(y), M, K, N, bias);
   return hipGetLastError();
 }
 
 // 64-token tiles while even those do not outnumber the compute units (at
 // 11008 x 4096, 512 tokens: 344 tiles of 64 took 72 us, 172 of 128 64 us).
-template <typename YT, bool PREP>
+template <typename YT, bool PREP, int HV = 1>
 static hipError_t launch_gemm2sp_t(const uint32_t *meta, const float *scale, const void *x, void *y,
                                    int M, int K, int N, hipStream_t stream, const float *bias) {
   const long tiles128 = (long)((M + GEMM2SP_BM - 1) / GEMM2SP_BM) * ((N + 255) / 256);
-  if (2 * tiles128 <= device_cus()) return launch_gemm2sp_bm<64, YT, PREP>(meta, scale, x, y, M, K, N, stream, bias);
-  return launch_gemm2sp_bm<GEMM2SP_BM, YT, PREP>(meta, scale, x, y, M, K, N, stream, bias);
+  if (2 * tiles128 <= device_cus())
+    return launch_gemm2sp_bm<64, YT, PREP, HV>(meta, scale, x, y, M, K, N, stream, bias);
+  return launch_gemm2sp_bm<GEMM2SP_BM, YT, PREP, HV>(meta, scale, x, y, M, K, N, stream, bias);
 }
 
 hipError_t launch_gemm_sp_prepared(const uint32_t *prep, const float *scale, const void *x, void *y, int yt_bf16,
                                    int M, int K, int N, hipStream_t stream, const float *bias) {
   if (yt_bf16) return launch_gemm2sp_t<uint16_t, true>(prep, scale, x, y, M, K, N, stream, bias);
   return launch_gemm2sp_t<float, true>(prep, scale, x, y, M, K, N, stream, bias);
+}
+
+hipError_t launch_gemm_sp_planes(const uint32_t *meta, int prepared, const float *scale, const uint16_t *x2, void *y,
+                                 int yt_bf16, int M, int K, int N, hipStream_t stream) {
+  if (prepared) {
+    if (yt_bf16) return launch_gemm2sp_t<uint16_t, true, 2>(meta, scale, x2, y, M, K, N, stream, nullptr);
+    return launch_gemm2sp_t<float, true, 2>(meta, scale, x2, y, M, K, N, stream, nullptr);
+  }
+  if (yt_bf16) return launch_gemm2sp_t<uint16_t, false, 2>(meta, scale, x2, y, M, K, N, stream, nullptr);
+  return launch_gemm2sp_t<float, false, 2>(meta, scale, x2, y, M, K, N, stream, nullptr);
 }
 
 template <int XS, int WF, typename YT>

@@ -436,15 +436,16 @@ struct Gemm2 {
 
   __device__ __forceinline__ static uint32_t sp_window_bytes(int s) { return 4u * (uint32_t)((16 * s) / 6); }
 
+  // s: the X step (64 columns), sw: the metadata step
   __device__ __forceinline__ static void issue_sp(uint32_t *stage, __amdgpu_buffer_rsrc_t xr,
                                                   __amdgpu_buffer_rsrc_t wr, const uint32_t (&xv)[XPW],
-                                                  const uint32_t (&wv)[SWPW], int s) {
+                                                  const uint32_t (&wv)[SWPW], int s, int sw) {
     const int wave = threadIdx.x >> 6;
 #pragma unroll
     for (int i = 0; i < XPW; i++) lds_load16(xr, stage + (wave * XPW + i) * 256, xv[i], 128u * (uint32_t)s);
 #pragma unroll
     for (int i = 0; i < SWPW; i++)
-      lds_load4(wr, stage + XSTAGE + (wave * SWPW + i) * 64, wv[i], sp_window_bytes(s));
+      lds_load4(wr, stage + XSTAGE + (wave * SWPW + i) * 64, wv[i], sp_window_bytes(sw));
   }
 
   // The A operands of fragment rows wn*TN + fn*16 + l16 for step s from the
@@ -491,18 +492,24 @@ struct Gemm2 {
   // per row, step and lane group, [N][K/16] words like the dense codes), so
   // the stage loads are the dense engine's and a fragment's operand is one
   // LDS word; wpr is unused.
-  template <bool PREP = false>
+  // ldx: X row stride in elements (default K). WRAP: X has 2K columns (an
+  // fp32 activation as bf16 hi | lo halves of each row) and steps K/64 ..
+  // 2K/64 - 1 multiply them by the weight steps 0 .. K/64 - 1 again.
+  template <bool PREP = false, bool WRAP = false>
   __device__ static void run_sp(uint32_t *lds, const uint16_t *X, uint32_t xbytes, int m_count,
                                 const uint32_t *W, int n_count, int K, int wpr, f32x4 (&acc)[FN][FM], int s0 = 0,
-                                int nsteps = -1) {
+                                int nsteps = -1, int ldx = 0) {
     static_assert(NS >= 3 && FM % 2 == 0 && FM / 2 >= XDS, "sparse schedule");
     constexpr int LP = PREP ? LPW : SLPW;  // load instructions per wave per stage
     constexpr int WL = PREP ? WPW : SWPW;
+    if (ldx == 0) ldx = K;
+    const int nkw = K >> 6;  // weight steps
+    auto wstep = [&](int s) { return WRAP && s >= nkw ? s - nkw : s; };
     uint32_t xv[XPW], wv[WL];
     __amdgpu_buffer_rsrc_t wr[PREP ? WPW : 1];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     if constexpr (PREP) {
-      lane_offsets(xv, wv, nullptr, m_count, n_count, K, K, false, 0u);
+      lane_offsets(xv, wv, nullptr, m_count, n_count, ldx, K, false, 0u);
 #pragma unroll
       for (int i = 0; i < WPW; i++) wr[i] = buffer_rsrc(W, (uint32_t)n_count * (uint32_t)(K >> 4) * 4u);
     } else {
@@ -511,7 +518,7 @@ struct Gemm2 {
         const int r = (wave * XPW + i) * 8 + (lane >> 3);
         const int rm = min(r, m_count - 1);
         const uint32_t c = (lane & 7) ^ xswz(r);
-        xv[i] = (uint32_t)rm * (uint32_t)K * 2u + 16u * c;
+        xv[i] = (uint32_t)rm * (uint32_t)ldx * 2u + 16u * c;
       }
 #pragma unroll
       for (int i = 0; i < SWPW; i++) {
@@ -522,8 +529,8 @@ struct Gemm2 {
     }
     const __amdgpu_buffer_rsrc_t xr = buffer_rsrc(X, xbytes);
     auto load = [&](uint32_t *stage, int s) {
-      if constexpr (PREP) issue(stage, xr, wr, xv, wv, 64 * s, 64 * s);
-      else issue_sp(stage, xr, wr[0], xv, wv, s);
+      if constexpr (PREP) issue(stage, xr, wr, xv, wv, 64 * s, 64 * wstep(s));
+      else issue_sp(stage, xr, wr[0], xv, wv, s, wstep(s));
     };
 #pragma unroll
     for (int fn = 0; fn < FN; fn++)
@@ -559,7 +566,7 @@ struct Gemm2 {
     {
       uint32_t wa[FN], wb[FN];
       int o5 = 0;
-      wread(lds + XSTAGE, s0, wa, wb, o5);
+      wread(lds + XSTAGE, wstep(s0), wa, wb, o5);
 #pragma unroll
       for (int d = 0; d < XDS; d++) bn[d] = xop_sp(lds, r0, g, d);
 #pragma unroll
@@ -591,7 +598,7 @@ struct Gemm2 {
       for (int fm = FM / 2; fm < FM; fm++) {
         if (fm + XDS < FM) b[fm + XDS] = xop_sp(cur, r0, g, fm + XDS);
         else bn[fm + XDS - FM] = xop_sp(nxt, r0, g, fm + XDS - FM);
-        if (fm == FM / 2) wread(nxt + XSTAGE, s0 + t + 1, wa, wb, o5);
+        if (fm == FM / 2) wread(nxt + XSTAGE, wstep(s0 + t + 1), wa, wb, o5);
         if (SP_INPLACE && fm == FM - 1) {
           // the next step's operands decoded into a[fn] right after its last
           // use (more fragments than decode slots: no second operand set)

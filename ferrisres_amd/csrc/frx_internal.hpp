@@ -114,10 +114,16 @@ size_t gemm_splitk_workspace_bytes(int M, int N, int S);
 hipError_t launch_gemm_splitk(const uint32_t *w, const float *scale, const void *x, void *y, int yt_bf16, int M, int K,
                               int N, int S, int kp, float *part, hipStream_t stream, const float *bias, int halves = 1);
 // The split for 2:4 weights (GPU layout), any token count from 1, bf16 x.
-bool gemm_sp_splitk_plan(int M, int K, int N, int cus, int *S, int *sp);
+// halves = 2: x2 [M][2K] bf16 hi | lo rows (an fp32 activation), parts over
+// both halves.
+bool gemm_sp_splitk_plan(int M, int K, int N, int cus, int *S, int *sp, int halves = 1);
 hipError_t launch_gemm_sp_splitk(const uint32_t *meta, const float *scale, const void *x, void *y, int yt_bf16, int M,
                                  int K, int N, int S, int sp, float *part, hipStream_t stream, const float *bias,
-                                 int prepared);
+                                 int prepared, int halves = 1);
+// Whole-K 2:4 GEMM over x2 = [M][2K] bf16 hi | lo rows (5-bit or prepared
+// metadata), one K loop of 2K columns.
+hipError_t launch_gemm_sp_planes(const uint32_t *meta, int prepared, const float *scale, const uint16_t *x2, void *y,
+                                 int yt_bf16, int M, int K, int N, hipStream_t stream);
 // 2:4 metadata (GPU 5-bit layout) -> its prepared form, [N][K/16] words
 // (K % 64 == 0), and the whole-K GEMM over it (bf16 x, aligned).
 hipError_t launch_sp24_prepare(const uint32_t *meta, uint32_t *out, int N, int K, hipStream_t stream);

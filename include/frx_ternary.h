@@ -212,7 +212,11 @@ frx_status frx_ternary_stats(frx_ctx *ctx, const uint32_t *w, uint32_t N,
 /* ---- 2:4 sparse ternary linear ---------------------------------------------
  * Replaces SparseTernaryMatMulOp::dispatch (src/compute/kernels/
  * sparse_ternary.rs:194-247), WGSL entry sparse_ternary_matmul_main (:54-112).
- *   meta [N][ceil(ceil(K/4)/6)] u32, scale [N] f32. Requires K % 4 == 0. */
+ *   meta [N][ceil(ceil(K/4)/6)] u32, scale [N] f32. Requires K % 4 == 0.
+ * With K % 64 == 0 both dtypes of x run on the sparse matrix pipe (f32 x as
+ * bf16 hi | lo rows in a context workspace); below 512 tokens the K range is
+ * split over workgroups where the token tiles leave compute units idle
+ * (fp32 partials in a context workspace, added in a fixed order). */
 frx_status frx_sparse24_ternary_linear(frx_ctx *ctx, const uint32_t *meta,
                                        const float *scale, const void *x,
                                        frx_dtype xt, void *y, frx_dtype yt,

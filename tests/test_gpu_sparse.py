@@ -235,3 +235,36 @@ def test_prepared_entry_errors(ctx):
     torch.cuda.synchronize()
     assert float(y.abs().max()) == 0.0
     del meta
+
+
+@pytest.mark.parametrize("M,K,N", [(1, 4096, 11008), (7, 2048, 1000), (130, 4096, 512), (700, 1024, 2048),
+                                   (300, 1024, 11008), (2048, 1024, 2048)])
+def test_sparse_f32_activations_bit_exact_on_dyadic(ctx, M, K, N):
+    """f32 activations (the reference's dtype) split once into bf16 hi | lo
+    rows and multiplied on the sparse pipe over both halves: split over K,
+    whole-K, and from 512 tokens over the prepared form. Dyadic x lies in
+    the hi half: exact products and sums, f32 and bf16 outputs."""
+    rng = np.random.default_rng(3 * M + K + N)
+    t = synth.sparse24_uniform(f"f32sp/{M}x{K}x{N}", "w", N, K)
+    meta = frx.pack_sparse24_gpu(t)
+    x = (rng.integers(-64, 65, size=(M, K)) / 8.0).astype(np.float32)
+    s = (2.0 ** rng.integers(-4, 2, size=N)).astype(np.float32)
+    ref = (x @ t.T.astype(np.float32)) * s[None, :]
+    np.testing.assert_array_equal(host(_run(ctx, meta, s, x, None, "f32", "f32")), ref)
+    yb = _run(ctx, meta, s, x, None, "f32", "bf16")
+    np.testing.assert_array_equal(yb.view(torch.int16).cpu().numpy().view(np.uint16), synth.f32_to_bf16_bits(ref))
+
+
+@pytest.mark.parametrize("M,K,N", [(3, 4096, 4096), (64, 2048, 3000), (600, 2048, 1024)])
+def test_sparse_f32_activations_random_parity(ctx, M, K, N):
+    """Genuine f32 activations (the lo half matters) against the oracle's
+    sequential f32 sums, f32 and bf16 outputs."""
+    name = f"sp24f32/{M}x{K}x{N}"
+    t = synth.sparse24_uniform(name, "w", N, K)
+    meta = frx.pack_sparse24_gpu(t)
+    s = synth.row_scales(name, "s", N, samples=256)
+    xf = synth.normal(synth.seed_of(name, "xf32"), M * K).reshape(M, K)
+    ref = oracle.sparse24_gpu_matmul(meta, s, xf, M, K, N)
+    assert_close_f32(host(_run(ctx, meta, s, xf, None, "f32", "f32")), ref)
+    yb = _run(ctx, meta, s, xf, None, "f32", "bf16")
+    assert_bf16_within_1ulp(yb.view(torch.int16).cpu().numpy().view(np.uint16), ref)
