@@ -257,6 +257,7 @@ struct MoeWorkspace {
   float *dout;         // [T*k][H] down-projection rows
   float *dout_lo;      // [T*k][H] second partial (engine-2 path: the second
                        // K part)
+  uint16_t *x2;        // [T][2H] f32 x as bf16 hi | lo rows (engine-2 path)
 };
 // Largest LoRA rank of the MoE adapters.
 constexpr int MOE_LORA_MAXR = 64;

@@ -49,6 +49,7 @@ size_t moe_workspace_bytes(int T, int H, int I, int E, int top_k) {
   b += align256(4);                     // ntiles
   b += align256(A * I * 2) * 2;         // h planes
   b += align256(A * H * 4) * 2;         // dout, dout_lo
+  b += align256((size_t)T * H * 4);     // f32 x as bf16 hi | lo rows
   return b;
 }
 
@@ -73,6 +74,7 @@ void moe_workspace_carve(void *base, int T, int H, int I, int E, int top_k,
   ws->h_lo = reinterpret_cast<uint16_t *>(take(A * I * 2));
   ws->dout = reinterpret_cast<float *>(take(A * H * 4));
   ws->dout_lo = reinterpret_cast<float *>(take(A * H * 4));
+  ws->x2 = reinterpret_cast<uint16_t *>(take((size_t)T * H * 4));
 }
 
 template <typename T>
@@ -870,14 +872,17 @@ using MoeDownCore = Gemm2<2 * MOE3_BM, MOE3_DBN, 2, 2, MOE3_DNS, false, true>;
 static_assert(MoeGateUpCore::FM == 6 && MoeDownCore::FM == 6, "token blocks per tile");
 
 template <int F>
-__device__ __forceinline__ void gateup_tile(uint32_t *lds, const GateUpArgs &args, const uint16_t *x, int T, int H,
-                                            int I, int e, int mcount, int row0, const int *perm_token,
+__device__ __forceinline__ void gateup_tile(uint32_t *lds, const GateUpArgs &args, const uint16_t *x, int ldx, int T,
+                                            int H, int I, int e, int mcount, int row0, const int *perm_token,
                                             uint16_t *h2, int act, const MoeLora &lora, const float *lax) {
   using Core = MoeGateUpCore;
   const int n0 = blockIdx.x * (MOE_GU_BN / 2), nc = min(MOE_GU_BN / 2, I - n0);
   f32x4 acc[Core::FN][F];
-  Core::template run<F>(lds, x, (uint32_t)T * (uint32_t)H * 2u, perm_token + row0, mcount,
-                        args.wg[e] + (size_t)n0 * (H >> 4), nc, H, acc, args.wu[e] + (size_t)n0 * (H >> 4), H);
+  // ldx = 2 H: x rows are an fp32 activation as bf16 hi | lo halves, one K
+  // loop of 2 H columns whose weight columns wrap at H
+  Core::template run<F>(lds, x, (uint32_t)T * (uint32_t)ldx * 2u, perm_token + row0, mcount,
+                        args.wg[e] + (size_t)n0 * (H >> 4), nc, ldx, acc, args.wu[e] + (size_t)n0 * (H >> 4), H,
+                        ldx);
   // Epilogue: the fragments go to LDS in passes of up to PB token blocks (row
   // pitch MOE_GU_BN + 16 floats); each thread then owns 4 gate columns (and
   // the same 4 up columns MOE_GU_BN / 2 further) of a run of tokens per pass.
@@ -938,7 +943,7 @@ __device__ __forceinline__ void gateup_tile(uint32_t *lds, const GateUpArgs &arg
 
 // grid (ceil(I / 128), tile slots); slots past *ntiles exit at once.
 __global__ __launch_bounds__(256) void moe_gateup3_kernel(
-    const GateUpArgs args, const uint16_t *__restrict__ x, int T, int H, int I,
+    const GateUpArgs args, const uint16_t *__restrict__ x, int ldx, int T, int H, int I,
     const int *__restrict__ tiles, const int *__restrict__ ntiles,
     const int *__restrict__ offsets, const int *__restrict__ perm_token,
     uint16_t *__restrict__ h2, int act, const MoeLora lora, const float *__restrict__ lax) {
@@ -947,9 +952,9 @@ __global__ __launch_bounds__(256) void moe_gateup3_kernel(
   if (tile >= *ntiles) return;  // whole workgroup
   const int e = tiles[4 * tile], row0 = offsets[e] + tiles[4 * tile + 1];
   const int mcount = tiles[4 * tile + 2], f = tiles[4 * tile + 3];
-  if (f <= 4) gateup_tile<4>(lds, args, x, T, H, I, e, mcount, row0, perm_token, h2, act, lora, lax);
-  else if (f == 5) gateup_tile<5>(lds, args, x, T, H, I, e, mcount, row0, perm_token, h2, act, lora, lax);
-  else gateup_tile<6>(lds, args, x, T, H, I, e, mcount, row0, perm_token, h2, act, lora, lax);
+  if (f <= 4) gateup_tile<4>(lds, args, x, ldx, T, H, I, e, mcount, row0, perm_token, h2, act, lora, lax);
+  else if (f == 5) gateup_tile<5>(lds, args, x, ldx, T, H, I, e, mcount, row0, perm_token, h2, act, lora, lax);
+  else gateup_tile<6>(lds, args, x, ldx, T, H, I, e, mcount, row0, perm_token, h2, act, lora, lax);
 }
 
 template <int F>
@@ -1138,9 +1143,10 @@ hipError_t launch_moe(const void *x, int xt_bf16, const void *router,
                        (const float *)x, (const float *)router, T, H, E, EP, top_k, rch, ws.idx, ws.wts, topk_idx, topk_w, routing);
   hipError_t err = hipGetLastError();
   if (err != hipSuccess) return err;
-  // engine 2 (pipelined MFMA GEMMs): bf16 x, H and I multiples of 64,
-  // 16-byte aligned weights; otherwise the register-staged engine 1
-  bool engine2 = xt_bf16 && H % 64 == 0 && I % 64 == 0;
+  // engine 2 (pipelined MFMA GEMMs): H and I multiples of 64, 16-byte
+  // aligned weights, bf16 x or f32 x (8-byte aligned, split into bf16 hi | lo
+  // rows for the gate/up GEMM); otherwise the register-staged engine 1
+  bool engine2 = (xt_bf16 || (reinterpret_cast<uintptr_t>(x) & 7) == 0) && H % 64 == 0 && I % 64 == 0;
   for (int i = 0; i < E && engine2; i++)
     engine2 = ((reinterpret_cast<uintptr_t>(w_gate[i]) | reinterpret_cast<uintptr_t>(w_up[i]) |
                 reinterpret_cast<uintptr_t>(w_down[i])) & 15) == 0;
@@ -1193,8 +1199,13 @@ hipError_t launch_moe(const void *x, int xt_bf16, const void *router,
       return err;
     if ((err = opt_in_lds(reinterpret_cast<const void *>(&moe_down3_kernel), dn_lds, done_dn)) != hipSuccess)
       return err;
+    const uint16_t *xg = reinterpret_cast<const uint16_t *>(x);
+    if (!xt_bf16) {
+      if ((err = launch_to_planes(reinterpret_cast<const float *>(x), ws.x2, T, H, stream)) != hipSuccess) return err;
+      xg = ws.x2;
+    }
     const dim3 g1((I + MOE_GU_BN / 2 - 1) / (MOE_GU_BN / 2), max_tiles);
-    hipLaunchKernelGGL(moe_gateup3_kernel, g1, dim3(256), gu_lds, stream, ga, (const uint16_t *)x, T, H, I,
+    hipLaunchKernelGGL(moe_gateup3_kernel, g1, dim3(256), gu_lds, stream, ga, xg, xt_bf16 ? H : 2 * H, T, H, I,
                        ws.tiles, ws.ntiles, ws.offsets, ws.perm_token, ws.h_hi, act, lora, ws.lora_ax);
     if ((err = hipGetLastError()) != hipSuccess) return err;
     if ((err = lora_down_a(ws.h_hi, ws.h_hi + I, 2L * I)) != hipSuccess) return err;

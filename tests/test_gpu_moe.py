@@ -116,6 +116,24 @@ def test_moe_config_shape(ctx):
     assert np.isfinite(host(y)).all()
 
 
+@pytest.mark.parametrize("T,H,I,E,k", [(512, 2048, 5632, 16, 2), (70, 256, 320, 6, 2)])
+def test_moe_f32_tokens_engine2(ctx, T, H, I, E, k):
+    """Genuine f32 tokens (the reference's dtype; the lo half matters): the
+    router reads them as f32 (bit-exact routing), the gate/up GEMM takes
+    them as bf16 hi | lo rows in one K loop of 2H columns. Sampled tokens in
+    full within 1e-3."""
+    name = f"moe/f32e2/{T}x{H}"
+    _, _, rf, rb, ex = make_moe(name, T, H, I, E)
+    xf = synth.normal(synth.seed_of(name, "xf32"), T * H).reshape(T, H)
+    y, idx, w = run_gpu(ctx, xf, None, rf, rb, ex, E, k, frx.ACT_SILU, xt="f32")
+    ridx, rw, _ = oracle.moe_route(xf, rf, k)
+    np.testing.assert_array_equal(idx, ridx)
+    np.testing.assert_allclose(w, rw, rtol=0, atol=1e-6)
+    tok = np.arange(T) if T <= 70 else np.array([0, 1, 63, 64, 127, 255, 256, 300, 400, 511])
+    ref, _, _ = run_oracle(xf, rf, ex, E, k, False, tokens=tok)
+    assert_close_f32(host(y)[tok], ref)
+
+
 def test_moe_gelu_gate_only_config_shape(ctx):
     """TernaryMoELayer's GeLU experts (h = gelu_tanh(g) with the literal
     0.7978845608, no up projection; ternary_moe.rs:193-200) at 512 tokens,
