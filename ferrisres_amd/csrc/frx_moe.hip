@@ -1028,6 +1028,209 @@ __global__ __launch_bounds__(256) void moe_down3_kernel(
   else down_tile<6>(lds, args, h2, H, I, ks, part, nt, e, mcount, row0, out, lora, lah);
 }
 
+// ---- 3c/4c. decode: a few routed rows ------------------------------------------
+// With T * top_k <= MOE_DEC_MAXA routed rows (decode: one token, top-2) the
+// grouped GEMMs leave almost every workgroup empty and run each expert's K
+// loop on one tile, latency-bound. These two kernels are GEMVs per routed
+// row instead, in routing order (row a = token a / top_k, its j-th expert),
+// so the group kernel is not needed: the combine reads row a for assignment
+// a (inv = identity, written here). Weights stream once per routed row (top-k
+// experts of one token are distinct).
+//
+// MFMA GEMV: a wave multiplies 16 weight rows by the row's activation; lane
+// (i, g) loads 16 bytes of row i (4 code words = 64 consecutive columns, the
+// g-th 64 of each 256), unpacks each word into two 8-column operands, and
+// the B operand of lane group g is the activation at the same columns (every
+// B column holds the same activation, so any output column is the result).
+// fp32 activations are multiplied as bf16 hi and lo planes (two MFMAs).
+constexpr int MOE_DEC_MAXA = 4;
+constexpr int MOE_DEC_ROWS = 64;  // weight rows of each matrix per workgroup
+
+// The activation slice [0, n) of one row into LDS as bf16 hi (and, for f32,
+// lo) planes, zero-padded to np columns; n and np multiples of 8, src 16-byte
+// aligned. Each thread moves 8 columns per unit and issues the loads of up
+// to 4 units before converting any.
+template <typename XT>
+__device__ __forceinline__ void dec_stage_row(const XT *src, int n, int np, uint16_t *hi, uint16_t *lo) {
+  constexpr int U = 4;
+  const int step = (int)blockDim.x * 8;
+  for (int c0 = (int)threadIdx.x * 8; c0 < np; c0 += step * U) {
+    u32x4 raw[U][sizeof(XT) == 2 ? 1 : 2];
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+      const int c = c0 + u * step;
+#pragma unroll
+      for (int v = 0; v < (sizeof(XT) == 2 ? 1 : 2); v++) {
+        raw[u][v] = (u32x4){0u, 0u, 0u, 0u};
+        if (c < n) raw[u][v] = *reinterpret_cast<const u32x4 *>(src + c + 4 * v);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+      const int c = c0 + u * step;
+      if (c >= np) break;
+      if constexpr (sizeof(XT) == 2) {
+        *reinterpret_cast<u32x4 *>(hi + c) = raw[u][0];
+      } else {
+        u32x4 h, l;
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+          const float a = __uint_as_float(raw[u][q >> 1][2 * (q & 1)]);
+          const float b = __uint_as_float(raw[u][q >> 1][2 * (q & 1) + 1]);
+          uint32_t hq, lq;
+          split2_bf16(a, b, hq, lq);
+          h[q] = hq;
+          l[q] = lq;
+        }
+        *reinterpret_cast<u32x4 *>(hi + c) = h;
+        *reinterpret_cast<u32x4 *>(lo + c) = l;
+      }
+    }
+  }
+}
+
+// acc[f] += W[row f][0 .. kl) . act for NF 16-row fragments (rows clamped by
+// the caller), kl % 64 == 0. The weight loads of CH 256-column blocks of
+// every fragment are issued before any is used (the first batch before the
+// activation is staged: stage() fills LDS and meets the block barrier), so
+// a wave waits one memory round trip per batch rather than per block.
+template <bool LO, int NF, int CH, typename Stage>
+__device__ __forceinline__ void dec_gemv(const uint32_t *const (&wrow)[NF], int kl, const uint16_t *hi,
+                                         const uint16_t *lo, f32x4 (&acc)[NF], Stage stage) {
+  const int g = (threadIdx.x & 63) >> 4;
+  u32x4 wq[NF][CH];
+  // independent accumulation chains (the two word halves, each plane)
+  f32x4 part[NF][LO ? 4 : 2];
+#pragma unroll
+  for (int f = 0; f < NF; f++)
+#pragma unroll
+    for (int q = 0; q < (LO ? 4 : 2); q++) part[f][q] = (f32x4){0.f, 0.f, 0.f, 0.f};
+  auto fetch = [&](int c00) {
+#pragma unroll
+    for (int f = 0; f < NF; f++)
+#pragma unroll
+      for (int c = 0; c < CH; c++) {
+        const int col = c00 + 256 * c + 64 * g;
+        wq[f][c] = (u32x4){0x55555555u, 0x55555555u, 0x55555555u, 0x55555555u};  // code 1: zero
+        if (col < kl) wq[f][c] = *reinterpret_cast<const u32x4 *>(wrow[f] + (col >> 4));
+      }
+  };
+  fetch(0);
+  stage();
+  for (int c00 = 0; c00 < kl; c00 += 256 * CH) {
+    if (c00 > 0) fetch(c00);
+#pragma unroll
+    for (int c = 0; c < CH; c++) {
+      const int col = c00 + 256 * c + 64 * g;  // past kl: zero weights, zero-padded activation
+#pragma unroll
+      for (int w = 0; w < 4; w++) {
+        const int cc = col + 16 * w;
+        const u32x4 b0 = *reinterpret_cast<const u32x4 *>(hi + cc), b1 = *reinterpret_cast<const u32x4 *>(hi + cc + 8);
+        u32x4 l0, l1;
+        if constexpr (LO) {
+          l0 = *reinterpret_cast<const u32x4 *>(lo + cc);
+          l1 = *reinterpret_cast<const u32x4 *>(lo + cc + 8);
+        }
+#pragma unroll
+        for (int f = 0; f < NF; f++) {
+          u32x4 a0, a1;
+          unpack16_nat(wq[f][c][w], a0, a1);
+          part[f][0] = mfma16(a0, b0, part[f][0]);
+          part[f][1] = mfma16(a1, b1, part[f][1]);
+          if constexpr (LO) {
+            part[f][2] = mfma16(a0, l0, part[f][2]);
+            part[f][3] = mfma16(a1, l1, part[f][3]);
+          }
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int f = 0; f < NF; f++) {
+    acc[f] = acc[f] + part[f][0] + part[f][1];
+    if constexpr (LO) acc[f] = acc[f] + part[f][2] + part[f][3];
+  }
+}
+
+// Columns of LDS staging for a row of n activations: whole 256-column
+// blocks of the CH-block batches (the batch past the end reads zeros).
+__host__ __device__ constexpr int dec_pad(int n, int ch) { return (n + 256 * ch - 1) / (256 * ch) * (256 * ch); }
+constexpr int MOE_DEC_GU_CH = 8, MOE_DEC_DN_CH = 12;
+
+// grid (ceil(I / 64), A): waves 0-1 gate rows n0 .. n0 + 63, waves 2-3 the
+// same up rows; h[a][n] = act(g, u) as fp32 rows [A][I].
+template <typename XT>
+__global__ __launch_bounds__(256) void moe_dec_gateup_kernel(const GateUpArgs args, const XT *__restrict__ x, int H,
+                                                             int I, int top_k, const uint32_t *__restrict__ idx,
+                                                             float *__restrict__ h, int *__restrict__ inv, int act) {
+  extern __shared__ __align__(16) uint16_t dsm[];
+  const int hp = dec_pad(H, MOE_DEC_GU_CH);
+  uint16_t *xh = dsm, *xl = dsm + hp;
+  float *gu = reinterpret_cast<float *>(dsm + 2 * hp);  // [2][64]
+  const int a = blockIdx.y, t = a / top_k, e = (int)idx[a];
+  if (blockIdx.x == 0 && threadIdx.x == 0) inv[a] = a;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, mat = wave >> 1;
+  const int n0 = blockIdx.x * MOE_DEC_ROWS;
+  const uint32_t *W = mat ? args.wu[e] : args.wg[e];
+  const uint32_t *wrow[2];
+#pragma unroll
+  for (int f = 0; f < 2; f++)
+    wrow[f] = W + (size_t)min(n0 + (wave & 1) * 32 + f * 16 + (lane & 15), I - 1) * (H >> 4);
+  f32x4 acc[2] = {(f32x4){0.f, 0.f, 0.f, 0.f}, (f32x4){0.f, 0.f, 0.f, 0.f}};
+  auto stage = [&]() {
+    dec_stage_row<XT>(x + (size_t)t * H, H, hp, xh, xl);
+    __syncthreads();
+  };
+  if (W) {
+    dec_gemv<sizeof(XT) == 4, 2, MOE_DEC_GU_CH>(wrow, H, xh, xl, acc, stage);
+  } else {  // gate-only experts: no up rows
+    stage();
+  }
+  if ((lane & 15) == 0) {
+#pragma unroll
+    for (int f = 0; f < 2; f++)
+#pragma unroll
+      for (int j = 0; j < 4; j++) gu[mat * 64 + (wave & 1) * 32 + f * 16 + 4 * (lane >> 4) + j] = acc[f][j];
+  }
+  __syncthreads();
+  const int n = n0 + (int)threadIdx.x;
+  if (threadIdx.x < MOE_DEC_ROWS && n < I) {
+    const float gv = gu[threadIdx.x] * (0.5f * args.sg[e][n]);  // 0.5 undoes the 2*dec(c) encoding
+    const float uv = args.wu[e] ? gu[64 + threadIdx.x] * (0.5f * args.su[e][n]) : 0.f;
+    h[(size_t)a * I + n] = moe_act(act, gv, uv);
+  }
+}
+
+// grid (ceil(H / 64), 2, A): rows n0 .. n0 + 63 of W_down[e] over K part
+// part (columns [part ks, part ks + ks)), h as bf16 hi and lo planes;
+// part 0 -> dout, part 1 -> dout_lo (the combine adds them).
+__global__ __launch_bounds__(256) void moe_dec_down_kernel(const DownArgs args, const float *__restrict__ h, int H,
+                                                           int I, int ks, const uint32_t *__restrict__ idx,
+                                                           float *__restrict__ dout, float *__restrict__ dout_lo) {
+  extern __shared__ __align__(16) uint16_t dsm[];
+  const int kp = dec_pad(ks, MOE_DEC_DN_CH);
+  uint16_t *hh = dsm, *hl = dsm + kp;
+  const int a = blockIdx.z, part = blockIdx.y, e = (int)idx[a];
+  const int k0 = part * ks, kl = max(0, min(ks, I - k0));
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int n0 = blockIdx.x * MOE_DEC_ROWS;
+  const uint32_t *wrow[1] = {args.wd[e] + (size_t)min(n0 + wave * 16 + (lane & 15), H - 1) * (I >> 4) + (k0 >> 4)};
+  f32x4 acc[1] = {(f32x4){0.f, 0.f, 0.f, 0.f}};
+  auto stage = [&]() {
+    dec_stage_row<float>(h + (size_t)a * I + k0, kl, kp, hh, hl);
+    __syncthreads();
+  };
+  dec_gemv<true, 1, MOE_DEC_DN_CH>(wrow, kl, hh, hl, acc, stage);
+  if ((lane & 15) == 0) {
+    float *out = (part == 0 ? dout : dout_lo) + (size_t)a * H;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      const int n = n0 + wave * 16 + 4 * (lane >> 4) + j;
+      if (n < H) out[n] = acc[0][j] * (0.5f * args.sd[e][n]);
+    }
+  }
+}
+
 // ---- 5. combine ---------------------------------------------------------------
 // cpu_block_attn_res.rs:1179 `expert_outputs[t*hd+d] += w * down[d]`, k order.
 // dout_lo != nullptr: the down rows arrive as two partials (the engine-2 K
@@ -1150,6 +1353,43 @@ hipError_t launch_moe(const void *x, int xt_bf16, const void *router,
   for (int i = 0; i < E && engine2; i++)
     engine2 = ((reinterpret_cast<uintptr_t>(w_gate[i]) | reinterpret_cast<uintptr_t>(w_up[i]) |
                 reinterpret_cast<uintptr_t>(w_down[i])) & 15) == 0;
+  DownArgs da;
+  for (int i = 0; i < MOE_MAXE; i++) {
+    da.wd[i] = i < E ? w_down[i] : nullptr;
+    da.sd[i] = i < E ? s_down[i] : nullptr;
+  }
+  GateUpArgs ga;
+  for (int i = 0; i < MOE_MAXE; i++) {
+    const bool v = i < E;
+    ga.wg[i] = v ? w_gate[i] : nullptr;
+    ga.wu[i] = v ? w_up[i] : nullptr;
+    ga.sg[i] = v ? s_gate[i] : nullptr;
+    ga.su[i] = v ? s_up[i] : nullptr;
+  }
+  if (engine2 && A <= MOE_DEC_MAXA && !lora.tbl && H <= 8192 && I <= 16384 &&  // LDS <= 40 KB
+      (reinterpret_cast<uintptr_t>(x) & 15) == 0) {
+    // decode: GEMVs per routed row (no grouping), down in two K parts
+    const int ks = (I / 2 + 63) / 64 * 64;
+    const size_t gl = (size_t)dec_pad(H, MOE_DEC_GU_CH) * 4 + 2 * MOE_DEC_ROWS * 4;
+    const size_t dl = (size_t)dec_pad(ks, MOE_DEC_DN_CH) * 4;
+    if (xt_bf16)
+      hipLaunchKernelGGL((moe_dec_gateup_kernel<uint16_t>), dim3((I + MOE_DEC_ROWS - 1) / MOE_DEC_ROWS, A), dim3(256),
+                         gl, stream, ga, (const uint16_t *)x, H, I, top_k, ws.idx, (float *)ws.h_hi, ws.inv, act);
+    else
+      hipLaunchKernelGGL((moe_dec_gateup_kernel<float>), dim3((I + MOE_DEC_ROWS - 1) / MOE_DEC_ROWS, A), dim3(256),
+                         gl, stream, ga, (const float *)x, H, I, top_k, ws.idx, (float *)ws.h_hi, ws.inv, act);
+    if ((err = hipGetLastError()) != hipSuccess) return err;
+    hipLaunchKernelGGL(moe_dec_down_kernel, dim3((H + MOE_DEC_ROWS - 1) / MOE_DEC_ROWS, 2, A), dim3(256), dl, stream,
+                       da, (const float *)ws.h_hi, H, I, ks, ws.idx, ws.dout, ws.dout_lo);
+    if ((err = hipGetLastError()) != hipSuccess) return err;
+    if (yt_bf16)
+      hipLaunchKernelGGL((moe_combine_kernel<uint16_t>), dim3(T), dim3(256), 0, stream, ws.dout, ws.dout_lo, ws.wts,
+                         ws.inv, H, top_k, (uint16_t *)y, routing);
+    else
+      hipLaunchKernelGGL((moe_combine_kernel<float>), dim3(T), dim3(256), 0, stream, ws.dout, ws.dout_lo, ws.wts,
+                         ws.inv, H, top_k, (float *)y, routing);
+    return hipGetLastError();
+  }
   // 2. group
   const int bm_max = engine2 ? MOE3_BM : MOE_BM;
   hipLaunchKernelGGL(moe_group_kernel, dim3(1), dim3(1024), 0, stream, ws.idx, A, top_k, E, bm_max,
@@ -1178,19 +1418,6 @@ hipError_t launch_moe(const void *x, int xt_bf16, const void *router,
   };
   // 3. gate/up
   const int max_tiles = (A + bm_max - 1) / bm_max + E;
-  GateUpArgs ga;
-  for (int i = 0; i < MOE_MAXE; i++) {
-    const bool v = i < E;
-    ga.wg[i] = v ? w_gate[i] : nullptr;
-    ga.wu[i] = v ? w_up[i] : nullptr;
-    ga.sg[i] = v ? s_gate[i] : nullptr;
-    ga.su[i] = v ? s_up[i] : nullptr;
-  }
-  DownArgs da;
-  for (int i = 0; i < MOE_MAXE; i++) {
-    da.wd[i] = i < E ? w_down[i] : nullptr;
-    da.sd[i] = i < E ? s_down[i] : nullptr;
-  }
   bool two_parts = false;  // engine-2 down GEMM in two K parts (dout, dout_lo)
   if (engine2) {
     const int gu_lds = MoeGateUpCore::LDS_DWORDS * 4, dn_lds = MoeDownCore::LDS_DWORDS * 4;

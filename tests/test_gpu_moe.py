@@ -10,7 +10,7 @@ import torch
 import ferrisres_amd as frx
 import oracle
 from ferrisres_amd import synth
-from _gpu import assert_close_f32, dev_bf16, dev_f32, dev_u32, host
+from _gpu import assert_bf16_within_1ulp, assert_close_f32, dev_bf16, dev_f32, dev_u32, host
 
 pytestmark = pytest.mark.gpu
 
@@ -70,6 +70,27 @@ def test_moe_small_parity(ctx, T, H, I, E, k, act):
     np.testing.assert_array_equal(idx, ridx)
     np.testing.assert_allclose(w, rw, rtol=0, atol=1e-6)
     assert_close_f32(host(y), ref)
+
+
+@pytest.mark.parametrize("T,H,I,E,k,act,xt", [
+    (1, 2048, 5632, 16, 2, frx.ACT_SILU, "bf16"), (1, 2048, 5632, 16, 2, frx.ACT_SILU, "f32"),
+    (2, 128, 192, 5, 2, frx.ACT_GELU_TANH, "bf16"), (1, 256, 320, 8, 4, frx.ACT_SILU, "f32"),
+    (3, 64, 128, 4, 1, frx.ACT_GELU_TANH_GATE, "bf16"), (4, 128, 64, 3, 1, frx.ACT_SILU, "f32")])
+def test_moe_decode_rows_parity(ctx, T, H, I, E, k, act, xt):
+    """A few routed rows (T * top_k <= 4, decode): one GEMV per routed row for
+    gate/up and for down (two K parts), no grouping. Routing bit-exact,
+    outputs within 1e-3, f32 and bf16 outputs."""
+    name = f"moe/dec/{T}x{H}x{I}x{E}x{k}"
+    xf, xb, rf, rb, ex = make_moe(name, T, H, I, E)
+    if xt == "f32":
+        xf = synth.normal(synth.seed_of(name, "xf32"), T * H).reshape(T, H)
+    y, idx, w = run_gpu(ctx, xf, xb, rf, rb, ex, E, k, act, xt=xt, no_up=act == frx.ACT_GELU_TANH_GATE)
+    ref, ridx, rw = run_oracle(xf, rf, ex, E, k, act)
+    np.testing.assert_array_equal(idx, ridx)
+    np.testing.assert_allclose(w, rw, rtol=0, atol=1e-6)
+    assert_close_f32(host(y), ref)
+    yb, _, _ = run_gpu(ctx, xf, xb, rf, rb, ex, E, k, act, xt=xt, yt="bf16", no_up=act == frx.ACT_GELU_TANH_GATE)
+    assert_bf16_within_1ulp(yb.view(torch.int16).cpu().numpy().view(np.uint16), ref)
 
 
 def test_moe_f32_inputs(ctx):
