@@ -284,13 +284,17 @@ constexpr int GEMM_SPSK_BM = 64;  // 4 token blocks, the fewest the sparse sched
 // the compute units idle, or at rows of 16384 codes and more any of them
 // (there a second workgroup per CU outweighs the partials' traffic: 8192 x
 // 28672 at 512 tokens 283 -> 242 us; at 11008 x 4096, 256 tokens, 47 ->
-// 53 us): parts of at least 8 steps, about two workgroups per CU.
+// 53 us): parts of at least 8 steps (4 for bf16 decode), about two
+// workgroups per CU.
 bool gemm_sp_splitk_plan(int M, int K, int N, int cus, int *S, int *sp, int halves) {
   if (M < 1 || K % 64 != 0 || N % 4 != 0) return false;
   const long tiles = (long)((M + GEMM_SPSK_BM - 1) / GEMM_SPSK_BM) * ((N + 255) / 256);
   if (2 * tiles > cus && (tiles > cus || K < 16384)) return false;
   const int nks = K / 64;
-  const int s = (int)std::min<long>((2L * cus + tiles * halves - 1) / (tiles * halves), nks / 8);
+  // bf16 decode (16 tokens at most): parts of 4 steps (11008 x 4096 at one
+  // token 18.2 -> 16.6 us; the two halves of f32 tokens keep 8)
+  const int mins = M <= 16 && halves == 1 ? 4 : 8;
+  const int s = (int)std::min<long>((2L * cus + tiles * halves - 1) / (tiles * halves), nks / mins);
   if (s < 1 || halves * s < 2) return false;
   *sp = (nks + s - 1) / s;
   *S = halves * ((nks + *sp - 1) / *sp);
