@@ -1155,42 +1155,61 @@ __device__ __forceinline__ void dec_gemv(const uint32_t *const (&wrow)[NF], int 
 // Columns of LDS staging for a row of n activations: whole 256-column
 // blocks of the CH-block batches (the batch past the end reads zeros).
 __host__ __device__ constexpr int dec_pad(int n, int ch) { return (n + 256 * ch - 1) / (256 * ch) * (256 * ch); }
-constexpr int MOE_DEC_GU_CH = 8, MOE_DEC_DN_CH = 12;
+// The two K halves of a workgroup: [0, kc) and [kc, n), kc a multiple of 64,
+// and the staged columns both halves read (each reads whole batches).
+__host__ __device__ constexpr int dec_half(int n) { return (n / 2 + 63) / 64 * 64; }
+__host__ __device__ constexpr int dec_pad2(int n, int ch) {
+  return dec_pad(dec_half(n), ch) > dec_half(n) + dec_pad(n - dec_half(n), ch)
+             ? dec_pad(dec_half(n), ch)
+             : dec_half(n) + dec_pad(n - dec_half(n), ch);
+}
+constexpr int MOE_DEC_GU_CH = 4, MOE_DEC_DN_CH = 6;
 
-// grid (ceil(I / 64), A): waves 0-1 gate rows n0 .. n0 + 63, waves 2-3 the
-// same up rows; h[a][n] = act(g, u) as fp32 rows [A][I].
+// grid (ceil(I / 64), A), 8 waves: waves 0-1 (and 4-5) gate rows n0 .. n0 +
+// 63, waves 2-3 (6-7) the same up rows; waves 0-3 multiply the first K half,
+// 4-7 the second, and add their sums through LDS (first half + second);
+// h[a][n] = act(g, u) as fp32 rows [A][I].
 template <typename XT>
-__global__ __launch_bounds__(256) void moe_dec_gateup_kernel(const GateUpArgs args, const XT *__restrict__ x, int H,
+__global__ __launch_bounds__(512) void moe_dec_gateup_kernel(const GateUpArgs args, const XT *__restrict__ x, int H,
                                                              int I, int top_k, const uint32_t *__restrict__ idx,
                                                              float *__restrict__ h, int *__restrict__ inv, int act) {
   extern __shared__ __align__(16) uint16_t dsm[];
-  const int hp = dec_pad(H, MOE_DEC_GU_CH);
+  const int kc = dec_half(H), hp = dec_pad2(H, MOE_DEC_GU_CH);
   uint16_t *xh = dsm, *xl = dsm + hp;
   float *gu = reinterpret_cast<float *>(dsm + 2 * hp);  // [2][64]
+  f32x4 *red = reinterpret_cast<f32x4 *>(gu + 2 * MOE_DEC_ROWS);  // [4 waves][2][64 lanes]
   const int a = blockIdx.y, t = a / top_k, e = (int)idx[a];
   if (blockIdx.x == 0 && threadIdx.x == 0) inv[a] = a;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, mat = wave >> 1;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, kh = wave >> 2, wl = wave & 3, mat = wl >> 1;
   const int n0 = blockIdx.x * MOE_DEC_ROWS;
+  const int ko = kh ? kc : 0, kl = kh ? H - kc : kc;
   const uint32_t *W = mat ? args.wu[e] : args.wg[e];
   const uint32_t *wrow[2];
 #pragma unroll
   for (int f = 0; f < 2; f++)
-    wrow[f] = W + (size_t)min(n0 + (wave & 1) * 32 + f * 16 + (lane & 15), I - 1) * (H >> 4);
+    wrow[f] = W + (size_t)min(n0 + (wl & 1) * 32 + f * 16 + (lane & 15), I - 1) * (H >> 4) + (ko >> 4);
   f32x4 acc[2] = {(f32x4){0.f, 0.f, 0.f, 0.f}, (f32x4){0.f, 0.f, 0.f, 0.f}};
   auto stage = [&]() {
     dec_stage_row<XT>(x + (size_t)t * H, H, hp, xh, xl);
     __syncthreads();
   };
   if (W) {
-    dec_gemv<sizeof(XT) == 4, 2, MOE_DEC_GU_CH>(wrow, H, xh, xl, acc, stage);
+    dec_gemv<sizeof(XT) == 4, 2, MOE_DEC_GU_CH>(wrow, kl, xh + ko, xl + ko, acc, stage);
   } else {  // gate-only experts: no up rows
     stage();
   }
-  if ((lane & 15) == 0) {
+  if (kh) {
 #pragma unroll
-    for (int f = 0; f < 2; f++)
+    for (int f = 0; f < 2; f++) red[(wl * 2 + f) * 64 + lane] = acc[f];
+  }
+  __syncthreads();
+  if (!kh && (lane & 15) == 0) {
 #pragma unroll
-      for (int j = 0; j < 4; j++) gu[mat * 64 + (wave & 1) * 32 + f * 16 + 4 * (lane >> 4) + j] = acc[f][j];
+    for (int f = 0; f < 2; f++) {
+      const f32x4 v = acc[f] + red[(wl * 2 + f) * 64 + lane];
+#pragma unroll
+      for (int j = 0; j < 4; j++) gu[mat * 64 + (wl & 1) * 32 + f * 16 + 4 * (lane >> 4) + j] = v[j];
+    }
   }
   __syncthreads();
   const int n = n0 + (int)threadIdx.x;
@@ -1201,32 +1220,40 @@ __global__ __launch_bounds__(256) void moe_dec_gateup_kernel(const GateUpArgs ar
   }
 }
 
-// grid (ceil(H / 64), 2, A): rows n0 .. n0 + 63 of W_down[e] over K part
-// part (columns [part ks, part ks + ks)), h as bf16 hi and lo planes;
-// part 0 -> dout, part 1 -> dout_lo (the combine adds them).
-__global__ __launch_bounds__(256) void moe_dec_down_kernel(const DownArgs args, const float *__restrict__ h, int H,
+// grid (ceil(H / 64), 2, A), 8 waves: rows n0 .. n0 + 63 of W_down[e] over
+// K part part (columns [part ks, part ks + ks)), waves 0-3 its first half and
+// 4-7 its second (added through LDS), h as bf16 hi and lo planes; part 0 ->
+// dout, part 1 -> dout_lo (the combine adds them).
+__global__ __launch_bounds__(512) void moe_dec_down_kernel(const DownArgs args, const float *__restrict__ h, int H,
                                                            int I, int ks, const uint32_t *__restrict__ idx,
                                                            float *__restrict__ dout, float *__restrict__ dout_lo) {
   extern __shared__ __align__(16) uint16_t dsm[];
-  const int kp = dec_pad(ks, MOE_DEC_DN_CH);
+  const int kp = dec_pad2(ks, MOE_DEC_DN_CH);
   uint16_t *hh = dsm, *hl = dsm + kp;
+  f32x4 *red = reinterpret_cast<f32x4 *>(dsm + 2 * kp);  // [4 waves][64 lanes]
   const int a = blockIdx.z, part = blockIdx.y, e = (int)idx[a];
   const int k0 = part * ks, kl = max(0, min(ks, I - k0));
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int kc = dec_half(kl);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, kh = wave >> 2, wl = wave & 3;
+  const int ko = kh ? kc : 0, kw = kh ? kl - kc : kc;
   const int n0 = blockIdx.x * MOE_DEC_ROWS;
-  const uint32_t *wrow[1] = {args.wd[e] + (size_t)min(n0 + wave * 16 + (lane & 15), H - 1) * (I >> 4) + (k0 >> 4)};
+  const uint32_t *wrow[1] = {args.wd[e] + (size_t)min(n0 + wl * 16 + (lane & 15), H - 1) * (I >> 4) +
+                             ((k0 + ko) >> 4)};
   f32x4 acc[1] = {(f32x4){0.f, 0.f, 0.f, 0.f}};
   auto stage = [&]() {
-    dec_stage_row<float>(h + (size_t)a * I + k0, kl, kp, hh, hl);
+    dec_stage_row<float>(h + (size_t)a * I + k0, kl, dec_pad2(kl, MOE_DEC_DN_CH), hh, hl);
     __syncthreads();
   };
-  dec_gemv<true, 1, MOE_DEC_DN_CH>(wrow, kl, hh, hl, acc, stage);
-  if ((lane & 15) == 0) {
+  dec_gemv<true, 1, MOE_DEC_DN_CH>(wrow, kw, hh + ko, hl + ko, acc, stage);
+  if (kh) red[wl * 64 + lane] = acc[0];
+  __syncthreads();
+  if (!kh && (lane & 15) == 0) {
+    const f32x4 v = acc[0] + red[wl * 64 + lane];
     float *out = (part == 0 ? dout : dout_lo) + (size_t)a * H;
 #pragma unroll
     for (int j = 0; j < 4; j++) {
-      const int n = n0 + wave * 16 + 4 * (lane >> 4) + j;
-      if (n < H) out[n] = acc[0][j] * (0.5f * args.sd[e][n]);
+      const int n = n0 + wl * 16 + 4 * (lane >> 4) + j;
+      if (n < H) out[n] = v[j] * (0.5f * args.sd[e][n]);
     }
   }
 }
@@ -1370,16 +1397,16 @@ hipError_t launch_moe(const void *x, int xt_bf16, const void *router,
       (reinterpret_cast<uintptr_t>(x) & 15) == 0) {
     // decode: GEMVs per routed row (no grouping), down in two K parts
     const int ks = (I / 2 + 63) / 64 * 64;
-    const size_t gl = (size_t)dec_pad(H, MOE_DEC_GU_CH) * 4 + 2 * MOE_DEC_ROWS * 4;
-    const size_t dl = (size_t)dec_pad(ks, MOE_DEC_DN_CH) * 4;
+    const size_t gl = (size_t)dec_pad2(H, MOE_DEC_GU_CH) * 4 + 2 * MOE_DEC_ROWS * 4 + 4 * 2 * 64 * 16;
+    const size_t dl = (size_t)dec_pad2(ks, MOE_DEC_DN_CH) * 4 + 4 * 64 * 16;
     if (xt_bf16)
-      hipLaunchKernelGGL((moe_dec_gateup_kernel<uint16_t>), dim3((I + MOE_DEC_ROWS - 1) / MOE_DEC_ROWS, A), dim3(256),
+      hipLaunchKernelGGL((moe_dec_gateup_kernel<uint16_t>), dim3((I + MOE_DEC_ROWS - 1) / MOE_DEC_ROWS, A), dim3(512),
                          gl, stream, ga, (const uint16_t *)x, H, I, top_k, ws.idx, (float *)ws.h_hi, ws.inv, act);
     else
-      hipLaunchKernelGGL((moe_dec_gateup_kernel<float>), dim3((I + MOE_DEC_ROWS - 1) / MOE_DEC_ROWS, A), dim3(256),
+      hipLaunchKernelGGL((moe_dec_gateup_kernel<float>), dim3((I + MOE_DEC_ROWS - 1) / MOE_DEC_ROWS, A), dim3(512),
                          gl, stream, ga, (const float *)x, H, I, top_k, ws.idx, (float *)ws.h_hi, ws.inv, act);
     if ((err = hipGetLastError()) != hipSuccess) return err;
-    hipLaunchKernelGGL(moe_dec_down_kernel, dim3((H + MOE_DEC_ROWS - 1) / MOE_DEC_ROWS, 2, A), dim3(256), dl, stream,
+    hipLaunchKernelGGL(moe_dec_down_kernel, dim3((H + MOE_DEC_ROWS - 1) / MOE_DEC_ROWS, 2, A), dim3(512), dl, stream,
                        da, (const float *)ws.h_hi, H, I, ks, ws.idx, ws.dout, ws.dout_lo);
     if ((err = hipGetLastError()) != hipSuccess) return err;
     if (yt_bf16)
