@@ -602,6 +602,17 @@ frx_status frx_sparse24_ternary_linear(frx_ctx *ctx, const uint32_t *meta,
   if ((st = stage_linear(ctx, x, xt, scale, y, yt, M, K, N, &sg)) != FRX_OK) return st;
   hipError_t e = hipSuccess;
   int S = 0, sp = 0;
+  if (frx::sp24_gemv_plan((int)M, (int)K, (int)N, xt == FRX_BF16, &S)) {
+    // decode: the metadata read once by a table-driven GEMV
+    if ((st = ensure_buffer(ctx, &ctx->gk_ws, &ctx->gk_ws_bytes, frx::gemm_splitk_workspace_bytes((int)M, (int)N, S),
+                            "split-K GEMM workspace allocation")) != FRX_OK)
+      return st;
+    e = frx::launch_sp24_gemv(meta, sg.scale, sg.x, xt == FRX_BF16, sg.y, yt == FRX_BF16, (int)M, (int)K, (int)N, S,
+                              reinterpret_cast<float *>(ctx->gk_ws), ctx->stream);
+    if (e == hipSuccess) e = unstage_linear(ctx, sg);
+    if (e != hipSuccess) return hip_fail(ctx, e, "sparse24_ternary_linear launch");
+    return FRX_OK;
+  }
   // f32 x runs as bf16 hi | lo rows ([M][2K], |x - hi - lo| <= 2^-17 |x|)
   // through the same sparse engine, both halves against the same weights
   const bool planes = xt == FRX_F32 && aligned16(sg.x) && K % 64 == 0 && (size_t)M * K * 4 < ((size_t)1 << 31);

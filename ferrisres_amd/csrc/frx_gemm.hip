@@ -6,6 +6,8 @@
 // kernels launch one thread per output with a 1-D grid, which cannot even be
 // dispatched at 2048 x 4096 (over 65,535 workgroups); here each workgroup
 // owns a 128 x 128 output tile (see frx_gemm_core.hpp).
+#include <type_traits>
+
 #include "frx_gemm2.hpp"
 #include "frx_gemm_core.hpp"
 #include "frx_internal.hpp"
@@ -314,6 +316,119 @@ static hipError_t launch_gemm2sp_parts(const uint32_t *meta, const void *x, int 
   hipLaunchKernelGGL((gemm2sp_splitk_kernel<BM, BN, WM, WN, NS, PREP, HV>),
                      dim3((N + BN - 1) / BN, (M + BM - 1) / BM, S), dim3(WM * WN * 64), lds, stream, meta,
                      reinterpret_cast<const uint16_t *>(x), part, M, K, N, sp);
+  return hipGetLastError();
+}
+
+// ---- 2:4 decode GEMV over the 5-bit layout (1-4 tokens, VALU) ----------------
+// The metadata is read once at 1.25 bits per weight. A workgroup owns 256
+// rows (one per lane) and a chunk of W metadata words of each row (6 groups
+// of 4 columns per word). It first tabulates, for each group of the chunk
+// and each of the 32 five-bit codes, the value the group adds:
+// 2 (s0 x[4g + p0] + s1 x[4g + p1]) (pattern > 5 read as 5, sign bits 3 and
+// 4; twice the sum, the 2 dec(c) scale of the other kernels). A code then
+// costs one LDS read and one add per token; the lanes of a wave read the same
+// group's 32 entries at a time, one bank each. The chunks' sums go to
+// part[chunk][M][N], added in chunk order by gemm_splitk_reduce.
+template <int MT>
+__host__ __device__ constexpr int spv_words() { return 16; }  // LDS <= 54 KB at 4 tokens
+
+template <typename XT, int MT>
+__global__ __launch_bounds__(256) void sp24_gemv_kernel(const uint32_t *__restrict__ meta, const XT *__restrict__ x,
+                                                        float *__restrict__ part, int M, int N, int K) {
+  constexpr int W = spv_words<MT>(), G = 6 * W;
+  static_assert(W == 16, "one metadata load per 16 lanes and row");
+  __shared__ float xs[MT][4 * G];
+  __shared__ float tab[MT][G * 32];
+  __shared__ uint32_t mw[256][W + 1];  // the block's rows' words (padded: conflict-free row reads)
+  const int wpr = ((K >> 2) + 5) / 6, chunk = blockIdx.y;
+  const int w0 = chunk * W, nw = min(W, wpr - w0);
+  const int c0 = 24 * w0;  // first column of the chunk
+  // the chunk's metadata first (its loads overlap the tabulation): load i of
+  // thread t is word t % 16 of row 16 i + t / 16, 64 contiguous bytes per row
+  const int r0 = blockIdx.x * 256, lw = threadIdx.x & 15, lr = threadIdx.x >> 4;
+  uint32_t wl[16];
+#pragma unroll
+  for (int i = 0; i < 16; i++) {
+    const int r = min(r0 + 16 * i + lr, N - 1);
+    wl[i] = lw < nw ? meta[(size_t)r * wpr + w0 + lw] : 0u;
+  }
+  for (int i = threadIdx.x; i < MT * 4 * G; i += 256) {
+    const int m = i / (4 * G), c = i - m * 4 * G;
+    float v = 0.f;
+    if (m < M && c0 + c < K) {
+      if constexpr (sizeof(XT) == 2) v = __uint_as_float((uint32_t)x[(size_t)m * K + c0 + c] << 16);
+      else v = x[(size_t)m * K + c0 + c];
+    }
+    xs[m][c] = v;
+  }
+  __syncthreads();
+  for (int i = threadIdx.x; i < MT * G * 32; i += 256) {
+    const int m = i / (G * 32), r = i - m * G * 32, gl = r >> 5, code = r & 31;
+    const uint32_t nib = __builtin_amdgcn_ubfe(0xEEED9C84u, (uint32_t)(code & 7) << 2, 4);
+    const float a = xs[m][4 * gl + (nib & 3)], b = xs[m][4 * gl + (nib >> 2)];
+    tab[m][r] = 2.0f * ((code & 8 ? -a : a) + (code & 16 ? -b : b));
+  }
+#pragma unroll
+  for (int i = 0; i < 16; i++) mw[16 * i + lr][lw] = wl[i];
+  __syncthreads();
+  const int row = r0 + (int)threadIdx.x;
+  if (row >= N) return;
+  uint32_t wq[W];
+#pragma unroll
+  for (int w = 0; w < W; w++) wq[w] = mw[threadIdx.x][w];
+  // two chains per token (even and odd words), added at the end
+  float acc[MT][2];
+#pragma unroll
+  for (int m = 0; m < MT; m++) acc[m][0] = acc[m][1] = 0.f;
+#pragma unroll
+  for (int w = 0; w < W; w++) {
+    if (w >= nw) break;
+#pragma unroll
+    for (int q = 0; q < 6; q++) {
+      const uint32_t code = (wq[w] >> (5 * q)) & 31u;
+#pragma unroll
+      for (int m = 0; m < MT; m++) acc[m][w & 1] += tab[m][(w * 6 + q) * 32 + code];
+    }
+  }
+#pragma unroll
+  for (int m = 0; m < MT; m++)
+    if (m < M) part[((size_t)chunk * M + m) * N + row] = acc[m][0] + acc[m][1];
+}
+
+// 1-2 tokens, or 3-4 fp32 tokens over matrices of 32 M codes and more with
+// rows up to 16384 (bf16 ones are faster on the sparse pipe, split over K:
+// 16.8 against about 21 us at 11008 x 4096; fp32 ones there run twice, as hi
+// and lo: 28 against 21.5 us; at 4096 x 4096 and 8192 x 28672 the split
+// stays ahead: 16.3 / 68 against 17.3 / 84 us)
+bool sp24_gemv_plan(int M, int K, int N, int xt_bf16, int *S) {
+  if (M < 1 || K % 4 != 0 || N % 4 != 0) return false;
+  if (M > 2 && (xt_bf16 || M > 4 || K > 16384 || (long)N * K < (1L << 25))) return false;
+  const int wpr = ((K >> 2) + 5) / 6, w = M <= 2 ? spv_words<2>() : spv_words<4>();
+  *S = (wpr + w - 1) / w;
+  return true;
+}
+
+hipError_t launch_sp24_gemv(const uint32_t *meta, const float *scale, const void *x, int xt_bf16, void *y,
+                            int yt_bf16, int M, int K, int N, int S, float *part, hipStream_t stream) {
+  const dim3 g((N + 255) / 256, S);
+  auto run = [&](auto xp) {
+    using XT = std::remove_const_t<std::remove_pointer_t<decltype(xp)>>;
+    if (M == 1) hipLaunchKernelGGL((sp24_gemv_kernel<XT, 1>), g, dim3(256), 0, stream, meta, xp, part, M, N, K);
+    else if (M == 2) hipLaunchKernelGGL((sp24_gemv_kernel<XT, 2>), g, dim3(256), 0, stream, meta, xp, part, M, N, K);
+    else hipLaunchKernelGGL((sp24_gemv_kernel<XT, 4>), g, dim3(256), 0, stream, meta, xp, part, M, N, K);
+  };
+  if (xt_bf16) run(reinterpret_cast<const uint16_t *>(x));
+  else run(reinterpret_cast<const float *>(x));
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  const size_t quads = (size_t)M * N / 4;
+  const dim3 gr((unsigned)((quads + 255) / 256));
+  if (yt_bf16)
+    hipLaunchKernelGGL(gemm_splitk_reduce<uint16_t>, gr, dim3(256), 0, stream, part, S, M, N, scale, nullptr,
+                       reinterpret_cast<uint16_t *>(y));
+  else
+    hipLaunchKernelGGL(gemm_splitk_reduce<float>, gr, dim3(256), 0, stream, part, S, M, N, scale, nullptr,
+                       reinterpret_cast<float *>(y));
   return hipGetLastError();
 }
 

@@ -122,7 +122,8 @@ def test_sparse_prefill_11008_sampled(ctx):
 
 
 @pytest.mark.parametrize("M,K,N", [(1, 4096, 11008), (5, 11008, 4096), (16, 4096, 11008), (17, 11008, 4096),
-                                   (200, 4096, 4096), (3, 2048, 300), (1600, 16384, 2048)])
+                                   (200, 4096, 4096), (3, 2048, 300), (1600, 16384, 2048), (2, 4100, 1000),
+                                   (4, 11008, 4096)])
 def test_sparse_split_k_bit_exact_on_dyadic(ctx, M, K, N):
     """Decode and small prefill, where 64-token tiles leave compute units
     idle: K is split into parts of whole 64-column steps (each reading its
@@ -147,8 +148,8 @@ def test_sparse_split_k_bit_exact_on_dyadic(ctx, M, K, N):
     np.testing.assert_array_equal(y0, ref)
 
 
-@pytest.mark.parametrize("M,K,N", [(1, 4096, 512), (7, 4096, 512), (48, 4096, 512), (600, 4096, 512),
-                                   (1024, 1024, 4096)])
+@pytest.mark.parametrize("M,K,N", [(1, 4096, 512), (2, 4100, 512), (7, 4096, 512), (48, 4096, 512),
+                                   (600, 4096, 512), (1024, 1024, 4096)])
 def test_sparse_split_k_raw_metadata(ctx, M, K, N):
     """Raw metadata words (patterns 6 and 7, stray bits 30-31) through the
     split path (windows that straddle words at every step phase) and, from
@@ -238,7 +239,7 @@ def test_prepared_entry_errors(ctx):
 
 
 @pytest.mark.parametrize("M,K,N", [(1, 4096, 11008), (7, 2048, 1000), (130, 4096, 512), (700, 1024, 2048),
-                                   (300, 1024, 11008), (2048, 1024, 2048)])
+                                   (300, 1024, 11008), (2048, 1024, 2048), (4, 4096, 11008), (3, 11008, 4096)])
 def test_sparse_f32_activations_bit_exact_on_dyadic(ctx, M, K, N):
     """f32 activations (the reference's dtype) split once into bf16 hi | lo
     rows and multiplied on the sparse pipe over both halves: split over K,
@@ -255,7 +256,8 @@ def test_sparse_f32_activations_bit_exact_on_dyadic(ctx, M, K, N):
     np.testing.assert_array_equal(yb.view(torch.int16).cpu().numpy().view(np.uint16), synth.f32_to_bf16_bits(ref))
 
 
-@pytest.mark.parametrize("M,K,N", [(3, 4096, 4096), (64, 2048, 3000), (600, 2048, 1024)])
+@pytest.mark.parametrize("M,K,N", [(3, 4096, 4096), (64, 2048, 3000), (600, 2048, 1024), (4, 4096, 11008),
+                                   (1, 4100, 1000)])
 def test_sparse_f32_activations_random_parity(ctx, M, K, N):
     """Genuine f32 activations (the lo half matters) against the oracle's
     sequential f32 sums, f32 and bf16 outputs."""
