@@ -607,8 +607,9 @@ frx_status frx_sparse24_ternary_linear(frx_ctx *ctx, const uint32_t *meta,
     if ((st = ensure_buffer(ctx, &ctx->gk_ws, &ctx->gk_ws_bytes, frx::gemm_splitk_workspace_bytes((int)M, (int)N, S),
                             "split-K GEMM workspace allocation")) != FRX_OK)
       return st;
+    if ((st = ensure_sk_counters(ctx)) != FRX_OK) return st;
     e = frx::launch_sp24_gemv(meta, sg.scale, sg.x, xt == FRX_BF16, sg.y, yt == FRX_BF16, (int)M, (int)K, (int)N, S,
-                              reinterpret_cast<float *>(ctx->gk_ws), ctx->stream);
+                              reinterpret_cast<float *>(ctx->gk_ws), ctx->sk_cnt, ctx->stream);
     if (e == hipSuccess) e = unstage_linear(ctx, sg);
     if (e != hipSuccess) return hip_fail(ctx, e, "sparse24_ternary_linear launch");
     return FRX_OK;

@@ -332,9 +332,11 @@ static hipError_t launch_gemm2sp_parts(const uint32_t *meta, const void *x, int 
 template <int MT>
 __host__ __device__ constexpr int spv_words() { return 16; }  // LDS <= 54 KB at 4 tokens
 
-template <typename XT, int MT>
+template <typename XT, int MT, typename YT>
 __global__ __launch_bounds__(256) void sp24_gemv_kernel(const uint32_t *__restrict__ meta, const XT *__restrict__ x,
-                                                        float *__restrict__ part, int M, int N, int K) {
+                                                        float *__restrict__ part, unsigned *__restrict__ counters,
+                                                        const float *__restrict__ scale, YT *__restrict__ Y, int M,
+                                                        int N, int K, int S) {
   constexpr int W = spv_words<MT>(), G = 6 * W;
   static_assert(W == 16, "one metadata load per 16 lanes and row");
   __shared__ float xs[MT][4 * G];
@@ -372,7 +374,6 @@ __global__ __launch_bounds__(256) void sp24_gemv_kernel(const uint32_t *__restri
   for (int i = 0; i < 16; i++) mw[16 * i + lr][lw] = wl[i];
   __syncthreads();
   const int row = r0 + (int)threadIdx.x;
-  if (row >= N) return;
   uint32_t wq[W];
 #pragma unroll
   for (int w = 0; w < W; w++) wq[w] = mw[threadIdx.x][w];
@@ -390,9 +391,52 @@ __global__ __launch_bounds__(256) void sp24_gemv_kernel(const uint32_t *__restri
       for (int m = 0; m < MT; m++) acc[m][w & 1] += tab[m][(w * 6 + q) * 32 + code];
     }
   }
+  // the chunk's sums, stored device-coherent (the workgroup that adds the
+  // chunks may run on another XCD); the last chunk of this row block to
+  // arrive adds them in chunk order (a per-block counter, reset by that
+  // workgroup for the next launch)
+  constexpr int SC1 = 16;  // cache policy: performed at the point of coherence of all XCDs
+  constexpr uint32_t OOB = 0x80000000u;
+  const __amdgpu_buffer_rsrc_t pr = buffer_rsrc(part, (uint32_t)S * (uint32_t)M * (uint32_t)N * 4u);
 #pragma unroll
-  for (int m = 0; m < MT; m++)
-    if (m < M) part[((size_t)chunk * M + m) * N + row] = acc[m][0] + acc[m][1];
+  for (int m = 0; m < MT; m++) {
+    const uint32_t off =
+        (m < M && row < N) ? (((uint32_t)chunk * (uint32_t)M + (uint32_t)m) * (uint32_t)N + (uint32_t)row) * 4u : OOB;
+    __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(acc[m][0] + acc[m][1]), pr, off, 0, SC1);
+  }
+  if (!counters) return;  // a separate launch adds the chunks
+  __shared__ int last;
+  wait_vmcnt<0>();
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const unsigned old = __hip_atomic_fetch_add(counters + blockIdx.x, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    last = old == (unsigned)S - 1u;
+    if (last) __hip_atomic_store(counters + blockIdx.x, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  __syncthreads();
+  if (!last || row >= N) return;
+  const float sc = 0.5f * scale[row];  // 0.5 undoes the 2 dec(c) scale of the table
+#pragma unroll
+  for (int m = 0; m < MT; m++) {
+    if (m >= M) break;
+    float sum = 0.f;
+    for (int c0 = 0; c0 < S; c0 += 8) {
+      float v[8];
+#pragma unroll
+      for (int k = 0; k < 8; k++) {
+        const uint32_t off = c0 + k < S ? (((uint32_t)(c0 + k) * (uint32_t)M + (uint32_t)m) * (uint32_t)N +
+                                           (uint32_t)row) * 4u
+                                        : OOB;
+        v[k] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(pr, off, 0, SC1));
+      }
+#pragma unroll
+      for (int k = 0; k < 8; k++)
+        if (c0 + k < S) sum = (c0 + k == 0) ? v[k] : sum + v[k];
+    }
+    const float o = sum * sc;
+    if constexpr (sizeof(YT) == 4) Y[(size_t)m * N + row] = o;
+    else Y[(size_t)m * N + row] = (uint16_t)bf16_rne(o);
+  }
 }
 
 // 1-2 tokens, or 3-4 fp32 tokens over matrices of 32 M codes and more with
@@ -401,7 +445,7 @@ __global__ __launch_bounds__(256) void sp24_gemv_kernel(const uint32_t *__restri
 // and lo: 28 against 21.5 us; at 4096 x 4096 and 8192 x 28672 the split
 // stays ahead: 16.3 / 68 against 17.3 / 84 us)
 bool sp24_gemv_plan(int M, int K, int N, int xt_bf16, int *S) {
-  if (M < 1 || K % 4 != 0 || N % 4 != 0) return false;
+  if (M < 1 || K % 4 != 0 || N % 4 != 0 || (N + 255) / 256 > GEMV_SK_MAX_TILES) return false;
   if (M > 2 && (xt_bf16 || M > 4 || K > 16384 || (long)N * K < (1L << 25))) return false;
   const int wpr = ((K >> 2) + 5) / 6, w = M <= 2 ? spv_words<2>() : spv_words<4>();
   *S = (wpr + w - 1) / w;
@@ -409,18 +453,35 @@ bool sp24_gemv_plan(int M, int K, int N, int xt_bf16, int *S) {
 }
 
 hipError_t launch_sp24_gemv(const uint32_t *meta, const float *scale, const void *x, int xt_bf16, void *y,
-                            int yt_bf16, int M, int K, int N, int S, float *part, hipStream_t stream) {
+                            int yt_bf16, int M, int K, int N, int S, float *part, unsigned *counters,
+                            hipStream_t stream) {
   const dim3 g((N + 255) / 256, S);
-  auto run = [&](auto xp) {
+  auto run = [&](auto xp, auto yp) {
     using XT = std::remove_const_t<std::remove_pointer_t<decltype(xp)>>;
-    if (M == 1) hipLaunchKernelGGL((sp24_gemv_kernel<XT, 1>), g, dim3(256), 0, stream, meta, xp, part, M, N, K);
-    else if (M == 2) hipLaunchKernelGGL((sp24_gemv_kernel<XT, 2>), g, dim3(256), 0, stream, meta, xp, part, M, N, K);
-    else hipLaunchKernelGGL((sp24_gemv_kernel<XT, 4>), g, dim3(256), 0, stream, meta, xp, part, M, N, K);
+    using YT = std::remove_pointer_t<decltype(yp)>;
+    if (M == 1)
+      hipLaunchKernelGGL((sp24_gemv_kernel<XT, 1, YT>), g, dim3(256), 0, stream, meta, xp, part, counters, scale, yp,
+                         M, N, K, S);
+    else if (M == 2)
+      hipLaunchKernelGGL((sp24_gemv_kernel<XT, 2, YT>), g, dim3(256), 0, stream, meta, xp, part, counters, scale, yp,
+                         M, N, K, S);
+    else
+      hipLaunchKernelGGL((sp24_gemv_kernel<XT, 4, YT>), g, dim3(256), 0, stream, meta, xp, part, counters, scale, yp,
+                         M, N, K, S);
   };
-  if (xt_bf16) run(reinterpret_cast<const uint16_t *>(x));
-  else run(reinterpret_cast<const float *>(x));
+  auto runx = [&](auto yp) {
+    if (xt_bf16) run(reinterpret_cast<const uint16_t *>(x), yp);
+    else run(reinterpret_cast<const float *>(x), yp);
+  };
+  // up to 12 chunks the last chunk of each row block adds them; with more,
+  // its serial device-coherent reads cost more than a separate launch
+  // (4096 x 11008, 29 chunks: 12.9 against 10.8 us)
+  const bool fused = S <= 12;
+  if (!fused) counters = nullptr;
+  if (yt_bf16) runx(reinterpret_cast<uint16_t *>(y));
+  else runx(reinterpret_cast<float *>(y));
   hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return e;
+  if (e != hipSuccess || fused) return e;
   const size_t quads = (size_t)M * N / 4;
   const dim3 gr((unsigned)((quads + 255) / 256));
   if (yt_bf16)

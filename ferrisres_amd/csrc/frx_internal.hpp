@@ -126,10 +126,12 @@ hipError_t launch_gemm_sp_planes(const uint32_t *meta, int prepared, const float
                                  int yt_bf16, int M, int K, int N, hipStream_t stream);
 // 1-2 tokens (3-4 fp32 tokens) over 2:4 metadata (GPU 5-bit layout, K % 4
 // == 0, N % 4 == 0): S chunk partials of M * N fp32 in part, added in order
-// into y.
+// into y by the last chunk of each 256-row block (counters: the split-K
+// GEMV's, zero between launches).
 bool sp24_gemv_plan(int M, int K, int N, int xt_bf16, int *S);
 hipError_t launch_sp24_gemv(const uint32_t *meta, const float *scale, const void *x, int xt_bf16, void *y,
-                            int yt_bf16, int M, int K, int N, int S, float *part, hipStream_t stream);
+                            int yt_bf16, int M, int K, int N, int S, float *part, unsigned *counters,
+                            hipStream_t stream);
 // 2:4 metadata (GPU 5-bit layout) -> its prepared form, [N][K/16] words
 // (K % 64 == 0), and the whole-K GEMM over it (bf16 x, aligned).
 hipError_t launch_sp24_prepare(const uint32_t *meta, uint32_t *out, int N, int K, hipStream_t stream);
