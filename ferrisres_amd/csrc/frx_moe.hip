@@ -575,6 +575,154 @@ __global__ __launch_bounds__(RT_NT) void moe_router_res_kernel(
   router_softmax_topk(sum, logit, tid, e, tl, t, T, E, EP, top_k, idx_out, w_out, user_idx, user_w, by_logit);
 }
 
+// Two-wave variant of the resident router (bf16 router weights): wave 1
+// brings the router rows by LDS DMA and widens them to f32, 256 columns at a
+// time, into a two-slot ring; wave 0 converts the token rows and runs the
+// chains on the widened chunks, one chunk behind (one block barrier per
+// chunk). A chain step is then one fused multiply-add (or multiply and add)
+// and half a 16-byte read, the widening runs beside it on another SIMD.
+constexpr int RP_CW = 256;  // columns per widened chunk
+static inline size_t router_pair_lds(int H, int E, int tpb) {
+  return (size_t)tpb * (H + 4) * 4 + (size_t)E * router_res_row_bytes(H) + (size_t)2 * E * (RP_CW + 4) * 4 +
+         2 * 4 * RT_NT * 4;
+}
+template <typename XT>
+__global__ __launch_bounds__(2 * RT_NT) void moe_router_pair_kernel(
+    const XT *__restrict__ x, const uint16_t *__restrict__ router, int T, int H, int E, int EP,
+    int top_k, int RSB, uint32_t *__restrict__ idx_out, float *__restrict__ w_out,
+    uint32_t *__restrict__ user_idx, float *__restrict__ user_w, int by_logit) {
+  extern __shared__ __align__(16) uint32_t smr[];
+  const int tid = threadIdx.x & 63, wave = threadIdx.x >> 6, e = tid % EP, tl = tid / EP;
+  const int TPB = RT_NT / EP;
+  const int t = blockIdx.x * TPB + tl;
+  const int XS = H + 4, RW = RP_CW + 4;
+  float *xs = reinterpret_cast<float *>(smr);                  // [TPB][XS] f32
+  uint32_t *rs = smr + TPB * XS;                                 // [E][RSB / 4] bf16 pairs (DMA)
+  float *ring = reinterpret_cast<float *>(rs + E * (RSB >> 2));  // [2][E][RW] f32
+  float *logit = ring + 2 * E * RW;                              // [2][4 RT_NT] (one per wave)
+  const int ipr = (H * 2 + 1023) >> 10;    // 1 KB DMA instructions per row
+  const int nch = (H + RP_CW - 1) / RP_CW;  // widened chunks
+  if (wave == 1) {
+    // every router row by LDS DMA, 1 KB instructions in column-block order
+    const __amdgpu_buffer_rsrc_t rr = buffer_rsrc(router, (uint32_t)E * (uint32_t)H * 2u);
+    for (int j = 0; j < ipr; j++)
+      for (int row = 0; row < E; row++)
+        lds_load16(rr, rs + row * (RSB >> 2) + j * 256,
+                   (uint32_t)row * (uint32_t)H * 2u + (uint32_t)j * 1024u + 16u * tid, 0u);
+  } else {
+    // the block's token rows as f32 (zeros for tokens past T)
+    constexpr int NV = sizeof(XT) == 2 ? 1 : 2;
+    constexpr int UB = sizeof(XT) == 2 ? 16 : 8;
+    const int upr = H >> 3, units = TPB * upr;
+    for (int u0 = 0; u0 < units; u0 += UB * RT_NT) {
+      u32x4 raw[UB][NV];
+#pragma unroll
+      for (int q = 0; q < UB; q++) {
+        const int u = min(u0 + q * RT_NT + tid, units - 1), rrow = u / upr, c = (u - rrow * upr) * 8;
+        const int tt = min(blockIdx.x * TPB + rrow, T - 1);
+        const u32x4 *src = reinterpret_cast<const u32x4 *>(x + (size_t)tt * H + c);
+#pragma unroll
+        for (int v = 0; v < NV; v++) raw[q][v] = src[v];
+      }
+#pragma unroll
+      for (int q = 0; q < UB; q++) {
+        const int u = u0 + q * RT_NT + tid;
+        if (u < units) {
+          const int rrow = u / upr, c = (u - rrow * upr) * 8;
+          const uint32_t m = blockIdx.x * TPB + rrow < T ? 0xFFFFFFFFu : 0u;
+          float v8[8];
+          if constexpr (NV == 1) {
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+              const uint32_t w = raw[q][0][k] & m;
+              v8[2 * k] = __uint_as_float(w << 16);
+              v8[2 * k + 1] = __uint_as_float(w & 0xFFFF0000u);
+            }
+          } else {
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+              v8[k] = __uint_as_float(raw[q][0][k] & m);
+              v8[4 + k] = __uint_as_float(raw[q][1][k] & m);
+            }
+          }
+          float4 *d = reinterpret_cast<float4 *>(xs + rrow * XS + c);
+          d[0] = make_float4(v8[0], v8[1], v8[2], v8[3]);
+          d[1] = make_float4(v8[4], v8[5], v8[6], v8[7]);
+        }
+      }
+    }
+  }
+  float sum = 0.0f;
+  for (int c = 0; c < nch; c++) {
+    float *slot = ring + (c & 1) * E * RW;
+    if (wave == 1) {
+      // chunk c lies in 1 KB column block jc: wait until at most the DMA
+      // instructions of the blocks after jc are outstanding (rounded down
+      // to the immediate waits; waiting longer is safe)
+      const int jc = (c * RP_CW) >> 9, rem = (ipr - 1 - jc) * E;
+      if (rem >= 48) wait_vmcnt<48>();
+      else if (rem >= 32) wait_vmcnt<32>();
+      else if (rem >= 16) wait_vmcnt<16>();
+      else wait_vmcnt<0>();
+      for (int u = tid; u < E * (RP_CW / 8); u += RT_NT) {
+        const int row = u / (RP_CW / 8), c8 = (u % (RP_CW / 8)) * 8, col = c * RP_CW + c8;
+        u32x4 r = (u32x4){0u, 0u, 0u, 0u};
+        if (col < H) r = *reinterpret_cast<const u32x4 *>(rs + row * (RSB >> 2) + (col >> 1));
+        float4 *d = reinterpret_cast<float4 *>(slot + row * RW + c8);
+        d[0] = make_float4(__uint_as_float(r[0] << 16), __uint_as_float(r[0] & 0xFFFF0000u),
+                           __uint_as_float(r[1] << 16), __uint_as_float(r[1] & 0xFFFF0000u));
+        d[1] = make_float4(__uint_as_float(r[2] << 16), __uint_as_float(r[2] & 0xFFFF0000u),
+                           __uint_as_float(r[3] << 16), __uint_as_float(r[3] & 0xFFFF0000u));
+      }
+    }
+    __syncthreads();  // chunk c widened; chunk c - 1 consumed, its slot free again
+    if (wave == 0 && e < E && t < T) {
+#pragma clang fp contract(off)
+      const int c0 = c * RP_CW, n = min(RP_CW, H - c0);
+      const float *xr = xs + tl * XS + c0, *rw = slot + e * RW;
+      constexpr bool EXACT_PRODUCT = sizeof(XT) == 2;  // bf16 x bf16: exact in f32
+      auto step = [&](float xe, float re) {
+        if constexpr (EXACT_PRODUCT) sum = __fmaf_rn(xe, re, sum);
+        else sum = sum + xe * re;
+      };
+      const int nb = n >> 5;
+      auto rd = [&](int b, f32x4 *xv, f32x4 *rv) {
+        const int j = min(b, max(nb - 1, 0)) * 32;
+#pragma unroll
+        for (int q = 0; q < 8; q++) {
+          xv[q] = *reinterpret_cast<const f32x4 *>(xr + j + 4 * q);
+          rv[q] = *reinterpret_cast<const f32x4 *>(rw + j + 4 * q);
+        }
+      };
+      auto run = [&](const f32x4 *xv, const f32x4 *rv) {
+#pragma unroll
+        for (int q = 0; q < 8; q++)
+#pragma unroll
+          for (int i = 0; i < 4; i++) step(xv[q][i], rv[q][i]);
+      };
+      f32x4 xa[8], xb[8], ra[8], rb[8];
+      rd(0, xa, ra);
+      int b = 0;
+      for (; b + 2 <= nb; b += 2) {
+        rd(b + 1, xb, rb);
+        run(xa, ra);
+        rd(b + 2, xa, ra);
+        run(xb, rb);
+      }
+      if (b < nb) run(xa, ra);
+      for (int j = nb * 32; j < n; j += 4) {  // n % 32 columns, 4 at a time (H % 16 == 0)
+        const f32x4 xv = *reinterpret_cast<const f32x4 *>(xr + j), rv = *reinterpret_cast<const f32x4 *>(rw + j);
+#pragma unroll
+        for (int i = 0; i < 4; i++) step(xv[i], rv[i]);
+      }
+    }
+  }
+  // wave 1 joins the softmax's barriers on its own LDS, as no token (t = T)
+  router_softmax_topk(sum, logit + wave * 4 * RT_NT, tid, e, tl, wave == 0 ? t : T, T, E, EP, top_k, idx_out, w_out,
+                      user_idx, user_w, by_logit);
+}
+#pragma clang fp contract(on)
+
 // ---- 2. histogram / scan / stable scatter / tile schedule -----------------
 // Exclusive prefix sum of v over the 64 lanes of a wave: shifts by 1, 2, 4
 // and 8 within each row of 16 lanes, then row 0's total into row 1 and row
@@ -1346,7 +1494,23 @@ hipError_t launch_moe(const void *x, int xt_bf16, const void *router,
     if (e != hipSuccess) return e;
   }
   const size_t res_lds = router_res_lds(H, E, tpb);
-  if (rt_bf16 && res_lds <= 160 * 1024) {
+  const size_t pair_lds = router_pair_lds(H, E, tpb);
+  if (rt_bf16 && H % 16 == 0 && pair_lds <= 160 * 1024) {
+    static std::atomic<uint64_t> done_p[2];
+    const void *fn = xt_bf16 ? reinterpret_cast<const void *>(&moe_router_pair_kernel<uint16_t>)
+                             : reinterpret_cast<const void *>(&moe_router_pair_kernel<float>);
+    const hipError_t e = opt_in_lds(fn, 160 * 1024, done_p[xt_bf16 ? 0 : 1]);
+    if (e != hipSuccess) return e;
+    const int rsb = router_res_row_bytes(H);
+    if (xt_bf16)
+      hipLaunchKernelGGL((moe_router_pair_kernel<uint16_t>), rg, dim3(2 * RT_NT), pair_lds, stream,
+                         (const uint16_t *)x, (const uint16_t *)router, T, H, E, EP, top_k, rsb, ws.idx, ws.wts,
+                         topk_idx, topk_w, routing);
+    else
+      hipLaunchKernelGGL((moe_router_pair_kernel<float>), rg, dim3(2 * RT_NT), pair_lds, stream, (const float *)x,
+                         (const uint16_t *)router, T, H, E, EP, top_k, rsb, ws.idx, ws.wts, topk_idx, topk_w,
+                         routing);
+  } else if (rt_bf16 && res_lds <= 160 * 1024) {
     static std::atomic<uint64_t> done_res[2];
     const void *fn = xt_bf16 ? reinterpret_cast<const void *>(&moe_router_res_kernel<uint16_t>)
                              : reinterpret_cast<const void *>(&moe_router_res_kernel<float>);
