@@ -460,3 +460,48 @@ def test_moe_lora_graph_keeps_its_adapters(ctx):
     finally:
         c.set_stream(None)
         c.close()
+
+
+def test_moe_decode_rows_repeat_and_graph(ctx):
+    """The decode path (GEMVs per routed row, routing order): back-to-back
+    calls with different tokens, then replays of a captured call with eager
+    calls between, each equal to its first eager run bit for bit."""
+    H, I, E, k = 256, 320, 8, 2
+    name = "moe/dec/graph"
+    _, _, rf, rb, ex = make_moe(name, 1, H, I, E)
+    dw = {kk: (dev_u32(v[0]), dev_f32(v[1])) for kk, v in ex.items()}
+    g = lambda m, i: [dw[(m, e)][i] for e in range(E)]  # noqa: E731
+    r = dev_bf16(rb)
+    xs = [dev_bf16(synth.activations(f"{name}/{i}", "x", 1, H)[1]) for i in range(3)]
+    ys = [torch.empty((1, H), dtype=torch.float32, device="cuda:0") for _ in range(3)]
+    s = torch.cuda.Stream()
+    ctx.set_stream(s)
+    try:
+        def call(i):
+            ctx.moe_ternary_ffn(xs[i], r, g("gate", 0), g("gate", 1), g("up", 0), g("up", 1), g("down", 0),
+                                g("down", 1), ys[i], top_k=k)
+        with torch.cuda.stream(s):
+            for i in range(3):
+                call(i)
+        torch.cuda.synchronize()
+        refs = [host(y).copy() for y in ys]
+        for i in range(3):
+            ref, _, _ = run_oracle(synth.bf16_bits_to_f32(synth.activations(f"{name}/{i}", "x", 1, H)[1]), rf, ex,
+                                   E, k, False)
+            assert_close_f32(refs[i], ref)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=s):
+            call(0)
+        torch.cuda.synchronize()
+        for rep in range(4):
+            for y in ys:
+                y.fill_(float("nan"))
+            with torch.cuda.stream(s):
+                graph.replay()
+                call(1)
+                call(2)
+            torch.cuda.synchronize()
+            for i in range(3):
+                np.testing.assert_array_equal(host(ys[i]), refs[i])
+    finally:
+        ctx.set_stream(None)

@@ -270,3 +270,57 @@ def test_sparse_f32_activations_random_parity(ctx, M, K, N):
     assert_close_f32(host(_run(ctx, meta, s, xf, None, "f32", "f32")), ref)
     yb = _run(ctx, meta, s, xf, None, "f32", "bf16")
     assert_bf16_within_1ulp(yb.view(torch.int16).cpu().numpy().view(np.uint16), ref)
+
+
+def test_sparse_decode_paths_repeat_and_graph(ctx):
+    """The decode GEMV (chunk sums added by the last-arriving chunk, its
+    arrival counters left zero by every launch; and with a separate
+    reduction over long rows) and the split-K engine: back-to-back launches
+    of different shapes, then replays of captured launches with eager
+    launches between, every result equal to its first eager run bit for
+    bit."""
+    shapes = [(1, 4096, 11008), (1, 11008, 4096), (2, 4096, 4096), (16, 4096, 4096)]
+    cases = []
+    for M, K, N in shapes:
+        name = f"sp24/graph/{M}x{K}x{N}"
+        t = synth.sparse24_uniform(name, "w", N, K)
+        meta = dev_u32(frx.pack_sparse24_gpu(t))
+        s = dev_f32(synth.row_scales(name, "s", N, samples=256))
+        _, xb = synth.activations(name, "x", M, K)
+        cases.append((meta, s, dev_bf16(xb), torch.empty((M, N), dtype=torch.float32, device="cuda:0")))
+
+    def call(i):
+        meta, s, x, y = cases[i]
+        ctx.sparse24_ternary_linear(meta, s, x, y)
+
+    for i in range(len(cases)):
+        call(i)
+    torch.cuda.synchronize()
+    refs = [host(c[3]).copy() for c in cases]
+    for rep in range(12):
+        call(rep % len(cases))
+    torch.cuda.synchronize()
+    for i, c in enumerate(cases):
+        np.testing.assert_array_equal(host(c[3]), refs[i])
+    st = torch.cuda.Stream()
+    ctx.set_stream(st)
+    try:
+        graphs = []
+        for i in range(3):
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g, stream=st):
+                call(i)
+            graphs.append(g)
+        torch.cuda.synchronize()
+        for rep in range(4):
+            for i, g in enumerate(graphs):
+                cases[i][3].fill_(float("nan"))
+                with torch.cuda.stream(st):
+                    g.replay()
+                    call(3)  # an eager launch between replays
+            torch.cuda.synchronize()
+            ctx.synchronize()
+            for i in range(4):
+                np.testing.assert_array_equal(host(cases[i][3]), refs[i])
+    finally:
+        ctx.set_stream(None)
