@@ -345,23 +345,39 @@ __global__ __launch_bounds__(256) void sp24_gemv_kernel(const uint32_t *__restri
   const int wpr = ((K >> 2) + 5) / 6, chunk = blockIdx.y;
   const int w0 = chunk * W, nw = min(W, wpr - w0);
   const int c0 = 24 * w0;  // first column of the chunk
-  // the chunk's metadata first (its loads overlap the tabulation): load i of
-  // thread t is word t % 16 of row 16 i + t / 16, 64 contiguous bytes per row
-  const int r0 = blockIdx.x * 256, lw = threadIdx.x & 15, lr = threadIdx.x >> 4;
-  uint32_t wl[16];
+  // the chunk's activations first, then its metadata: vector loads complete
+  // in issue order, so the tabulation waits only for the activations and
+  // runs while the metadata streams in (11008 x 4096, one token: the table
+  // was ready only after all 16 KB of a workgroup's metadata had landed)
+  constexpr int XPT = (MT * 4 * G + 255) / 256;  // activations per thread
+  float xv[XPT];
 #pragma unroll
-  for (int i = 0; i < 16; i++) {
-    const int r = min(r0 + 16 * i + lr, N - 1);
-    wl[i] = lw < nw ? meta[(size_t)r * wpr + w0 + lw] : 0u;
-  }
-  for (int i = threadIdx.x; i < MT * 4 * G; i += 256) {
-    const int m = i / (4 * G), c = i - m * 4 * G;
-    float v = 0.f;
-    if (m < M && c0 + c < K) {
-      if constexpr (sizeof(XT) == 2) v = __uint_as_float((uint32_t)x[(size_t)m * K + c0 + c] << 16);
-      else v = x[(size_t)m * K + c0 + c];
+  for (int q = 0; q < XPT; q++) {
+    const int i = (int)threadIdx.x + 256 * q, m = i / (4 * G), c = i - m * 4 * G;
+    xv[q] = 0.f;
+    if (i < MT * 4 * G && m < M && c0 + c < K) {
+      if constexpr (sizeof(XT) == 2) xv[q] = __uint_as_float((uint32_t)x[(size_t)m * K + c0 + c] << 16);
+      else xv[q] = x[(size_t)m * K + c0 + c];
     }
-    xs[m][c] = v;
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  // 16-byte loads (dword-aligned: rows are wpr words long): load i of thread
+  // t is words 4 (t % 4) .. + 3 of row 64 i + t / 4, 64 contiguous bytes per
+  // row and 16 rows per wave instruction; words past the row's end belong to
+  // the next row and are cleared, past the matrix the descriptor reads zeros
+  const int r0 = blockIdx.x * 256, lq = threadIdx.x & 3, lr = threadIdx.x >> 2;
+  const __amdgpu_buffer_rsrc_t mr = buffer_rsrc(meta, (uint32_t)N * (uint32_t)wpr * 4u);
+  u32x4 wl[4];
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    const int r = min(r0 + 64 * i + lr, N - 1);
+    wl[i] = __builtin_amdgcn_raw_buffer_load_b128(mr, ((uint32_t)r * (uint32_t)wpr + (uint32_t)(w0 + 4 * lq)) * 4u, 0, 0);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int q = 0; q < XPT; q++) {
+    const int i = (int)threadIdx.x + 256 * q, m = i / (4 * G), c = i - m * 4 * G;
+    if (i < MT * 4 * G) xs[m][c] = xv[q];
   }
   __syncthreads();
   for (int i = threadIdx.x; i < MT * G * 32; i += 256) {
@@ -371,7 +387,9 @@ __global__ __launch_bounds__(256) void sp24_gemv_kernel(const uint32_t *__restri
     tab[m][r] = 2.0f * ((code & 8 ? -a : a) + (code & 16 ? -b : b));
   }
 #pragma unroll
-  for (int i = 0; i < 16; i++) mw[16 * i + lr][lw] = wl[i];
+  for (int i = 0; i < 4; i++)
+#pragma unroll
+    for (int k = 0; k < 4; k++) mw[64 * i + lr][4 * lq + k] = 4 * lq + k < nw ? wl[i][k] : 0u;
   __syncthreads();
   const int row = r0 + (int)threadIdx.x;
   uint32_t wq[W];
@@ -448,6 +466,7 @@ bool sp24_gemv_plan(int M, int K, int N, int xt_bf16, int *S) {
   if (M < 1 || K % 4 != 0 || N % 4 != 0 || (N + 255) / 256 > GEMV_SK_MAX_TILES) return false;
   if (M > 2 && (xt_bf16 || M > 4 || K > 16384 || (long)N * K < (1L << 25))) return false;
   const int wpr = ((K >> 2) + 5) / 6, w = M <= 2 ? spv_words<2>() : spv_words<4>();
+  if ((long)N * wpr * 4 >= (1L << 32)) return false;  // the metadata's buffer range
   *S = (wpr + w - 1) / w;
   return true;
 }
