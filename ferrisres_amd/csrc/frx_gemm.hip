@@ -331,6 +331,11 @@ static hipError_t launch_gemm2sp_parts(const uint32_t *meta, const void *x, int 
 // part[chunk][M][N], added in chunk order by gemm_splitk_reduce.
 template <int MT>
 __host__ __device__ constexpr int spv_words() { return 16; }  // LDS <= 54 KB at 4 tokens
+// Most chunks that the last-arriving workgroup adds itself, all loads in
+// flight at once; above, a second launch does (4096 x 11008, 29 chunks:
+// 12.9 against 10.8 us with 8 loads in flight, 11.5 against 10.4 with all
+// 29; a limit of 32 also slowed the shapes of 11 chunks, 9.3 -> 9.5 us).
+constexpr int SPV_FUSED_MAX = 12;
 
 template <typename XT, int MT, typename YT>
 __global__ __launch_bounds__(256) void sp24_gemv_kernel(const uint32_t *__restrict__ meta, const XT *__restrict__ x,
@@ -437,18 +442,20 @@ __global__ __launch_bounds__(256) void sp24_gemv_kernel(const uint32_t *__restri
 #pragma unroll
   for (int m = 0; m < MT; m++) {
     if (m >= M) break;
+    // every chunk's partial in flight at once (the fused path takes up to
+    // SPV_FUSED_MAX chunks): one round trip to the point of coherence
     float sum = 0.f;
-    for (int c0 = 0; c0 < S; c0 += 8) {
-      float v[8];
+    for (int c0 = 0; c0 < S; c0 += SPV_FUSED_MAX) {
+      float v[SPV_FUSED_MAX];
 #pragma unroll
-      for (int k = 0; k < 8; k++) {
+      for (int k = 0; k < SPV_FUSED_MAX; k++) {
         const uint32_t off = c0 + k < S ? (((uint32_t)(c0 + k) * (uint32_t)M + (uint32_t)m) * (uint32_t)N +
                                            (uint32_t)row) * 4u
                                         : OOB;
         v[k] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(pr, off, 0, SC1));
       }
 #pragma unroll
-      for (int k = 0; k < 8; k++)
+      for (int k = 0; k < SPV_FUSED_MAX; k++)
         if (c0 + k < S) sum = (c0 + k == 0) ? v[k] : sum + v[k];
     }
     const float o = sum * sc;
@@ -492,10 +499,7 @@ hipError_t launch_sp24_gemv(const uint32_t *meta, const float *scale, const void
     if (xt_bf16) run(reinterpret_cast<const uint16_t *>(x), yp);
     else run(reinterpret_cast<const float *>(x), yp);
   };
-  // up to 12 chunks the last chunk of each row block adds them; with more,
-  // its serial device-coherent reads cost more than a separate launch
-  // (4096 x 11008, 29 chunks: 12.9 against 10.8 us)
-  const bool fused = S <= 12;
+  const bool fused = S <= SPV_FUSED_MAX;
   if (!fused) counters = nullptr;
   if (yt_bf16) runx(reinterpret_cast<uint16_t *>(y));
   else runx(reinterpret_cast<float *>(y));
