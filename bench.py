@@ -31,7 +31,8 @@ default, one-launch and two-launch executions), the same decode step and
 decode FFN at B = 4 and 16 (default run), the B=1 GEMV at growing weight sizes (up to
 the stacked LLaMA-70B gate/up, 117 MB), prefill GEMM (X[2048,4096] x
 W[N,4096], N in {4096, 11008}), 2:4 sparse GEMM and the MoE expert layer, as
-TFLOP/s and fraction of the dense bf16 MFMA peak.
+TFLOP/s and fraction of the dense bf16 MFMA peak; the 2:4 decode GEMV (one
+token through the same 2:4 weights, metadata rotated over cold copies).
 """
 from __future__ import annotations
 
@@ -453,6 +454,39 @@ def _time_kernel(torch, stream, fn, iters, warm=3, stats=None):
     return ev[0].elapsed_time(ev[iters]) * 1e-3 / iters
 
 
+def _time_graph(torch, stream, fns, reps, stats=None):
+    """Average seconds per launch of a short kernel: the launches `fns`
+    captured back to back in one HIP graph (eager launches from Python would
+    time the host), replayed `reps` times between HIP events; with `stats`
+    also the median, p10 and p90 of the per-launch time over the replays."""
+    def seq():
+        for fn in fns:
+            fn()
+    with torch.cuda.stream(stream):
+        seq()
+    torch.cuda.synchronize()
+    gr = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(gr, stream=stream):
+        seq()
+    with torch.cuda.stream(stream):
+        gr.replay()
+    torch.cuda.synchronize()
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(reps + 1)]
+    with torch.cuda.stream(stream):
+        ev[0].record(stream)
+        for r in range(reps):
+            gr.replay()
+            ev[r + 1].record(stream)
+    torch.cuda.synchronize()
+    n = len(fns)
+    if stats is not None:
+        samples = np.array([ev[r].elapsed_time(ev[r + 1]) * 1e3 / n for r in range(reps)])
+        stats.update({"median_us": round(float(np.median(samples)), 2),
+                      "p10_us": round(float(np.percentile(samples, 10)), 2),
+                      "p90_us": round(float(np.percentile(samples, 90)), 2), "launches": reps * n})
+    return ev[0].elapsed_time(ev[reps]) * 1e-3 / (reps * n)
+
+
 def run_extra(torch, frx, synth, ctx, stream, dev, only=None, iters=200):
     res = {}
     M, K = 2048, 4096
@@ -492,7 +526,21 @@ def run_extra(torch, frx, synth, ctx, stream, dev, only=None, iters=200):
                 "us": round(dt * 1e6, 2), "tflops_dense_equiv": round(tf, 1),
                 "frac_bf16_peak": round(tf / BF16_PEAK_TFLOPS, 4), **st}
             log(f"bench: 2:4 prepared N={N}: {dt * 1e6:.1f} us (prepare {dtp * 1e6:.1f} us)")
-            del meta, prep
+            # one token through the 5-bit layout (the table GEMV), rotating over
+            # enough copies of the metadata that every launch reads it from HBM
+            mb = meta.numel() * 4
+            ncp = (320 << 20) // mb + 1
+            metas = [meta] + [meta.clone() for _ in range(ncp - 1)]
+            x1 = X[:1]
+            y1 = torch.empty((1, N), dtype=torch.bfloat16, device=dev)
+            st = {}
+            dt = _time_graph(torch, stream, [lambda c=c: ctx.sparse24_ternary_linear(metas[c], s, x1, y1)
+                                             for c in range(ncp)], max(3, iters // ncp + 1), stats=st)
+            res[f"sparse24_decode_gemv_1x{K}x{N}"] = {
+                "us": round(dt * 1e6, 2), "metadata_gb_s": round(mb / dt / 1e9, 1), "metadata_bytes": mb,
+                "copies": ncp, **st}
+            log(f"bench: 2:4 decode GEMV N={N}, one token: {dt * 1e6:.2f} us")
+            del meta, prep, metas
         del w, Y
     if only is None:
         res["gemm_ceilings"] = gemm_ceilings(torch, stream, dev, X)
