@@ -32,7 +32,8 @@ decode FFN at B = 4 and 16 (default run), the B=1 GEMV at growing weight sizes (
 the stacked LLaMA-70B gate/up, 117 MB), prefill GEMM (X[2048,4096] x
 W[N,4096], N in {4096, 11008}), 2:4 sparse GEMM and the MoE expert layer, as
 TFLOP/s and fraction of the dense bf16 MFMA peak; the 2:4 decode GEMV (one
-token through the same 2:4 weights, metadata rotated over cold copies).
+token through the same 2:4 weights, metadata rotated over cold copies) and
+the MoE layer at one token (weights rotated over cold expert sets).
 """
 from __future__ import annotations
 
@@ -570,6 +571,29 @@ def run_extra(torch, frx, synth, ctx, stream, dev, only=None, iters=200):
     res["moe_512tok_h2048_i5632_e16_top2"] = {"us": round(dt * 1e6, 2), "tflops": round(tf, 1),
                                               "frac_bf16_peak": round(tf / BF16_PEAK_TFLOPS, 4), **st}
     log(f"bench: MoE: {dt * 1e6:.1f} us, {tf:.1f} TFLOP/s")
+    # one token (the decode path: routing, a GEMV per routed row, combine),
+    # graph replays over NS sets of the 16 experts so that the two routed
+    # experts' weights (17 MB a call) come from HBM, not the 256 MB Infinity
+    # Cache
+    NS = 24
+    del wg, wu, wd
+    allg = torch.empty((NS * E,) + tuple(pg.shape), dtype=pg.dtype, device=dev)
+    allu = torch.empty_like(allg)
+    alld = torch.empty((NS * E,) + tuple(pd.shape), dtype=pd.dtype, device=dev)
+    allg.copy_(pg.expand_as(allg))
+    allu.copy_(pg.expand_as(allu))
+    alld.copy_(pd.expand_as(alld))
+    x1 = xm[:1]
+    y1 = torch.empty((1, Hm), dtype=torch.bfloat16, device=dev)
+    fns = [lambda c=c: ctx.moe_ternary_ffn(x1, rm, [allg[c * E + e] for e in range(E)], [sg] * E,
+                                           [allu[c * E + e] for e in range(E)], [sg] * E,
+                                           [alld[c * E + e] for e in range(E)], [sd] * E, y1, top_k=k)
+           for c in range(NS)]
+    st = {}
+    dt = _time_graph(torch, stream, fns, 10, stats=st)
+    res["moe_1tok_h2048_i5632_e16_top2"] = {"us": round(dt * 1e6, 2), "weight_sets": NS, **st}
+    log(f"bench: MoE one token: {dt * 1e6:.2f} us")
+    del allg, allu, alld
     return res
 
 
