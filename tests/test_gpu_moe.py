@@ -93,6 +93,40 @@ def test_moe_decode_rows_parity(ctx, T, H, I, E, k, act, xt):
     assert_bf16_within_1ulp(yb.view(torch.int16).cpu().numpy().view(np.uint16), ref)
 
 
+@pytest.mark.parametrize("T", [1, 40])
+def test_moe_unaligned_tokens_and_router(ctx, T):
+    """x and the router one bf16 element into larger buffers (element-aligned,
+    not 16-byte aligned): the router then runs without its LDS DMA of the
+    router rows, and the experts without the pipelined engines or the decode
+    GEMVs. Routing is bit-exact against the oracle and the aligned call, the
+    output within 1e-3."""
+    H, I, E, k = 256, 192, 8, 2
+    name = f"moe/unaligned/{T}"
+    xf, xb, rf, rb, ex = make_moe(name, T, H, I, E)
+    y0, idx0, w0 = run_gpu(ctx, xf, xb, rf, rb, ex, E, k, frx.ACT_SILU)
+    xbuf = torch.zeros(T * H + 8, dtype=torch.bfloat16, device="cuda:0")
+    rbuf = torch.zeros(E * H + 8, dtype=torch.bfloat16, device="cuda:0")
+    xbuf[1:1 + T * H] = dev_bf16(xb).reshape(-1)
+    rbuf[1:1 + E * H] = dev_bf16(rb).reshape(-1)
+    x, r = xbuf[1:1 + T * H].view(T, H), rbuf[1:1 + E * H].view(E, H)
+    assert x.data_ptr() % 16 != 0 and r.data_ptr() % 16 != 0
+    dw = {key: (dev_u32(v[0]), dev_f32(v[1])) for key, v in ex.items()}
+    g = lambda m, i: [dw[(m, e)][i] for e in range(E)]  # noqa: E731
+    y = torch.empty((T, H), dtype=torch.float32, device="cuda:0")
+    idx = torch.zeros((T, k), dtype=torch.int32, device="cuda:0")
+    w = torch.zeros((T, k), dtype=torch.float32, device="cuda:0")
+    ctx.moe_ternary_ffn(x, r, g("gate", 0), g("gate", 1), g("up", 0), g("up", 1), g("down", 0), g("down", 1),
+                        y, top_k=k, act=frx.ACT_SILU, topk_idx=idx, topk_w=w)
+    torch.cuda.synchronize()
+    ref, ridx, rw = run_oracle(xf, rf, ex, E, k, frx.ACT_SILU)
+    np.testing.assert_array_equal(idx.cpu().numpy().astype(np.uint32), ridx)
+    np.testing.assert_array_equal(idx.cpu().numpy().astype(np.uint32), idx0)
+    np.testing.assert_array_equal(w.cpu().numpy(), w0)
+    np.testing.assert_allclose(w.cpu().numpy(), rw, rtol=0, atol=1e-6)
+    assert_close_f32(host(y), ref)
+    assert_close_f32(host(y0), ref)
+
+
 def test_moe_f32_inputs(ctx):
     xf, xb, rf, rb, ex = make_moe("moe/f32", 33, 128, 192, 5)
     xf = synth.normal(99, 33 * 128).reshape(33, 128)
