@@ -328,7 +328,9 @@ static hipError_t launch_gemm2sp_parts(const uint32_t *meta, const void *x, int 
 // 4; twice the sum, the 2 dec(c) scale of the other kernels). A code then
 // costs one LDS read and one add per token; the lanes of a wave read the same
 // group's 32 entries at a time, one bank each. The chunks' sums go to
-// part[chunk][M][N], added in chunk order by gemm_splitk_reduce.
+// part[chunk][M][N] and are added in chunk order: by the last chunk of each
+// row block to arrive (up to SPV_FUSED_MAX chunks), else by
+// gemm_splitk_reduce in a second launch.
 template <int MT>
 __host__ __device__ constexpr int spv_words() { return 16; }  // LDS <= 54 KB at 4 tokens
 // Most chunks that the last-arriving workgroup adds itself, all loads in
