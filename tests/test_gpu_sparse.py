@@ -63,6 +63,32 @@ def test_sparse_parity_random(ctx, M, K, N, xt, yt):
         assert_bf16_within_1ulp(y.view(torch.int16).cpu().numpy().view(np.uint16), ref)
 
 
+@pytest.mark.parametrize("M,K,N,xt", [(1, 100, 12, "bf16"), (2, 388, 260, "bf16"), (1, 4100, 1028, "bf16"),
+                                      (2, 6004, 516, "bf16"), (1, 388, 260, "f32"), (3, 4100, 8196, "f32"),
+                                      (4, 8188, 4100, "f32")])
+@pytest.mark.parametrize("yt", ["f32", "bf16"])
+def test_sparse_decode_gemv_ragged(ctx, M, K, N, xt, yt):
+    """The one-token table GEMV (1-2 bf16 tokens; 3-4 f32 tokens over >= 32 M
+    codes) on ragged shapes: rows whose word count is not a multiple of 4 (a
+    row's last 16-byte metadata load runs into the next row, whose words are
+    cleared), a last chunk shorter than 16 words, a last row block shorter
+    than 256 rows, and chunk counts on both sides of the fused reduction's
+    limit (6004 columns: 16 chunks, added by the separate launch)."""
+    name = f"sp24/gemv/{M}x{K}x{N}"
+    t = synth.sparse24_uniform(name, "w", N, K)
+    meta = frx.pack_sparse24_gpu(t)
+    s = synth.row_scales(name, "s", N, samples=256)
+    xf, xb = synth.activations(name, "x", M, K)
+    if xt == "f32":
+        xf = synth.normal(11, M * K).reshape(M, K)
+    ref = oracle.sparse24_gpu_matmul(meta, s, xf, M, K, N)
+    y = _run(ctx, meta, s, xf, xb, xt, yt)
+    if yt == "f32":
+        assert_close_f32(host(y), ref)
+    else:
+        assert_bf16_within_1ulp(y.view(torch.int16).cpu().numpy().view(np.uint16), ref)
+
+
 @pytest.mark.parametrize("M,K,N", [(2048, 4096, 4096), (2048, 4096, 11008), (16, 4096, 11008), (64, 11008, 512)])
 def test_sparse_bit_exact_on_dyadic(ctx, M, K, N):
     """Whole output, bit for bit (dyadic x, power-of-two scales: every
