@@ -339,7 +339,7 @@ __host__ __device__ constexpr int spv_words() { return 16; }  // LDS <= 54 KB at
 // 29; a limit of 32 also slowed the shapes of 11 chunks, 9.3 -> 9.5 us).
 constexpr int SPV_FUSED_MAX = 12;
 
-template <typename XT, int MT, typename YT>
+template <typename XT, int MT, typename YT, bool XMAP>
 __global__ __launch_bounds__(256) void sp24_gemv_kernel(const uint32_t *__restrict__ meta, const XT *__restrict__ x,
                                                         float *__restrict__ part, unsigned *__restrict__ counters,
                                                         const float *__restrict__ scale, YT *__restrict__ Y, int M,
@@ -349,7 +349,17 @@ __global__ __launch_bounds__(256) void sp24_gemv_kernel(const uint32_t *__restri
   __shared__ float xs[MT][4 * G];
   __shared__ float tab[MT][G * 32];
   __shared__ uint32_t mw[256][W + 1];  // the block's rows' words (padded: conflict-free row reads)
-  const int wpr = ((K >> 2) + 5) / 6, chunk = blockIdx.y;
+  // XMAP: a one-dimensional grid, workgroup i dispatched to XCD i % 8, and
+  // every chunk of a row block on the XCD of that block (rb % 8), so the
+  // 128-byte lines that neighbouring chunks of a row share are fetched into
+  // one L2 (with the chunks of a block spread over the XCDs, 11008 x 4096
+  // fetched 3x its metadata bytes, 1.07x so); slots past the row blocks exit
+  // at once. Otherwise grid (row blocks, chunks).
+  const int nrb = (N + 255) >> 8, slot = (int)(blockIdx.x >> 3);
+  const int rb = XMAP ? (slot / S) * 8 + (int)(blockIdx.x & 7) : (int)blockIdx.x;
+  const int chunk = XMAP ? slot % S : (int)blockIdx.y;
+  if (XMAP && rb >= nrb) return;  // whole workgroup
+  const int wpr = ((K >> 2) + 5) / 6;
   const int w0 = chunk * W, nw = min(W, wpr - w0);
   const int c0 = 24 * w0;  // first column of the chunk
   // the chunk's activations first, then its metadata: vector loads complete
@@ -372,7 +382,7 @@ __global__ __launch_bounds__(256) void sp24_gemv_kernel(const uint32_t *__restri
   // t is words 4 (t % 4) .. + 3 of row 64 i + t / 4, 64 contiguous bytes per
   // row and 16 rows per wave instruction; words past the row's end belong to
   // the next row and are cleared, past the matrix the descriptor reads zeros
-  const int r0 = blockIdx.x * 256, lq = threadIdx.x & 3, lr = threadIdx.x >> 2;
+  const int r0 = rb * 256, lq = threadIdx.x & 3, lr = threadIdx.x >> 2;
   const __amdgpu_buffer_rsrc_t mr = buffer_rsrc(meta, (uint32_t)N * (uint32_t)wpr * 4u);
   u32x4 wl[4];
 #pragma unroll
@@ -434,9 +444,9 @@ __global__ __launch_bounds__(256) void sp24_gemv_kernel(const uint32_t *__restri
   wait_vmcnt<0>();
   __syncthreads();
   if (threadIdx.x == 0) {
-    const unsigned old = __hip_atomic_fetch_add(counters + blockIdx.x, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const unsigned old = __hip_atomic_fetch_add(counters + rb, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     last = old == (unsigned)S - 1u;
-    if (last) __hip_atomic_store(counters + blockIdx.x, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (last) __hip_atomic_store(counters + rb, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
   __syncthreads();
   if (!last || row >= N) return;
@@ -483,19 +493,32 @@ bool sp24_gemv_plan(int M, int K, int N, int xt_bf16, int *S) {
 hipError_t launch_sp24_gemv(const uint32_t *meta, const float *scale, const void *x, int xt_bf16, void *y,
                             int yt_bf16, int M, int K, int N, int S, float *part, unsigned *counters,
                             hipStream_t stream) {
-  const dim3 g((N + 255) / 256, S);
+  // the XCD-grouped order for 1-2 tokens where the plain order spreads a row
+  // block's chunks (with nrb % 8 == 0 it already keeps them on one XCD); at
+  // 3-4 tokens (about 66 KB of LDS, two workgroups per CU) grouping 43 row
+  // blocks put 66 workgroups on the 64 slots of some XCDs (11008 x 4096, 4
+  // f32 tokens: 20.5 -> 28.2 us)
+  const int nrb = (N + 255) / 256;
+  const bool xmap = M <= 2 && nrb % 8 != 0;
+  const dim3 g = xmap ? dim3(8 * S * ((nrb + 7) / 8)) : dim3(nrb, S);
   auto run = [&](auto xp, auto yp) {
     using XT = std::remove_const_t<std::remove_pointer_t<decltype(xp)>>;
     using YT = std::remove_pointer_t<decltype(yp)>;
-    if (M == 1)
-      hipLaunchKernelGGL((sp24_gemv_kernel<XT, 1, YT>), g, dim3(256), 0, stream, meta, xp, part, counters, scale, yp,
-                         M, N, K, S);
+    if (M == 1 && xmap)
+      hipLaunchKernelGGL((sp24_gemv_kernel<XT, 1, YT, true>), g, dim3(256), 0, stream, meta, xp, part, counters, scale,
+                         yp, M, N, K, S);
+    else if (M == 1)
+      hipLaunchKernelGGL((sp24_gemv_kernel<XT, 1, YT, false>), g, dim3(256), 0, stream, meta, xp, part, counters,
+                         scale, yp, M, N, K, S);
+    else if (M == 2 && xmap)
+      hipLaunchKernelGGL((sp24_gemv_kernel<XT, 2, YT, true>), g, dim3(256), 0, stream, meta, xp, part, counters, scale,
+                         yp, M, N, K, S);
     else if (M == 2)
-      hipLaunchKernelGGL((sp24_gemv_kernel<XT, 2, YT>), g, dim3(256), 0, stream, meta, xp, part, counters, scale, yp,
-                         M, N, K, S);
+      hipLaunchKernelGGL((sp24_gemv_kernel<XT, 2, YT, false>), g, dim3(256), 0, stream, meta, xp, part, counters,
+                         scale, yp, M, N, K, S);
     else
-      hipLaunchKernelGGL((sp24_gemv_kernel<XT, 4, YT>), g, dim3(256), 0, stream, meta, xp, part, counters, scale, yp,
-                         M, N, K, S);
+      hipLaunchKernelGGL((sp24_gemv_kernel<XT, 4, YT, false>), g, dim3(256), 0, stream, meta, xp, part, counters,
+                         scale, yp, M, N, K, S);
   };
   auto runx = [&](auto yp) {
     if (xt_bf16) run(reinterpret_cast<const uint16_t *>(x), yp);
