@@ -822,6 +822,12 @@ frx_status frx_moe_ternary_ffn(
     return st;
   frx::MoeWorkspace ws;
   frx::moe_workspace_carve(ctx->moe_ws, (int)T, (int)H, (int)I, (int)E, (int)top_k, &ws);
+  // a few routed rows (the decode path): its down launch also combines,
+  // through the context's arrival counters
+  if ((size_t)T * top_k <= (size_t)frx::MOE_DEC_MAXA) {
+    if ((st = ensure_sk_counters(ctx)) != FRX_OK) return st;
+    ws.cnt = ctx->sk_cnt;
+  }
   const void *router_eh = router;
   if (ctx->moe_routing == FRX_MOE_CPU_MOE_LAYER) {
     // CpuMoELayer reads its router as [H][E]; the kernels read [E][H]

@@ -245,6 +245,9 @@ hipError_t launch_fill(float *p, float v, size_t n, hipStream_t stream);
 hipError_t launch_router_transpose(const void *src, int rt_bf16, void *dst, int H, int E, hipStream_t stream);
 
 // MoE pipeline (frx_moe.hip).
+// Most routed rows (tokens x top_k) of the MoE decode path.
+constexpr int MOE_DEC_MAXA = 4;
+
 struct MoeWorkspace {
   uint32_t *idx;       // [T*k] selected experts (sorted order per token)
   float *wts;          // [T*k] routing weights
@@ -266,6 +269,9 @@ struct MoeWorkspace {
   float *dout_lo;      // [T*k][H] second partial (engine-2 path: the second
                        // K part)
   uint16_t *x2;        // [T][2H] f32 x as bf16 hi | lo rows (engine-2 path)
+  unsigned *cnt = nullptr;  // decode path: (column block, token) arrival
+                            // counters, zero between launches; null: the
+                            // combine runs as a launch of its own
 };
 // Largest LoRA rank of the MoE adapters.
 constexpr int MOE_LORA_MAXR = 64;

@@ -1199,7 +1199,6 @@ __global__ __launch_bounds__(256) void moe_down3_kernel(
 // the B operand of lane group g is the activation at the same columns (every
 // B column holds the same activation, so any output column is the result).
 // fp32 activations are multiplied as bf16 hi and lo planes (two MFMAs).
-constexpr int MOE_DEC_MAXA = 4;
 constexpr int MOE_DEC_ROWS = 64;  // weight rows of each matrix per workgroup
 
 // The activation slice [0, n) of one row into LDS as bf16 hi (and, for f32,
@@ -1380,9 +1379,18 @@ __global__ __launch_bounds__(512) void moe_dec_gateup_kernel(const GateUpArgs ar
 // K part part (columns [part ks, part ks + ks)), waves 0-3 its first half and
 // 4-7 its second (added through LDS), h as bf16 hi and lo planes; part 0 ->
 // dout, part 1 -> dout_lo (the combine adds them).
+// cnt != nullptr: the combine runs here too. Each workgroup stores its 64
+// columns device-coherent and counts itself in for (column block, token);
+// the last of the token's 2 top_k workgroups adds the routes as the combine
+// kernel does (acc from 0, k = 0, 1, ..., d = part 0 + part 1, d * w rounded
+// before the add, CpuMoELayer's skip of |w| < 1e-8) and writes y, then
+// resets the counter for the next launch.
 __global__ __launch_bounds__(512) void moe_dec_down_kernel(const DownArgs args, const float *__restrict__ h, int H,
                                                            int I, int ks, const uint32_t *__restrict__ idx,
-                                                           float *__restrict__ dout, float *__restrict__ dout_lo) {
+                                                           float *__restrict__ dout, float *__restrict__ dout_lo,
+                                                           unsigned *__restrict__ cnt, const float *__restrict__ wts,
+                                                           int top_k, int skip_small, void *__restrict__ y,
+                                                           int y_bf16) {
   extern __shared__ __align__(16) uint16_t dsm[];
   const int kp = dec_pad2(ks, MOE_DEC_DN_CH);
   uint16_t *hh = dsm, *hl = dsm + kp;
@@ -1403,15 +1411,55 @@ __global__ __launch_bounds__(512) void moe_dec_down_kernel(const DownArgs args, 
   dec_gemv<true, 1, MOE_DEC_DN_CH>(wrow, kw, hh + ko, hl + ko, acc, stage);
   if (kh) red[wl * 64 + lane] = acc[0];
   __syncthreads();
+  constexpr int SC1 = 16;  // cache policy: performed at the point of coherence of all XCDs
+  constexpr uint32_t OOB = 0x80000000u;
   if (!kh && (lane & 15) == 0) {
     const f32x4 v = acc[0] + red[wl * 64 + lane];
-    float *out = (part == 0 ? dout : dout_lo) + (size_t)a * H;
+    const __amdgpu_buffer_rsrc_t orr = buffer_rsrc((part == 0 ? dout : dout_lo) + (size_t)a * H, (uint32_t)H * 4u);
 #pragma unroll
     for (int j = 0; j < 4; j++) {
       const int n = n0 + wl * 16 + 4 * (lane >> 4) + j;
-      if (n < H) out[n] = v[j] * (0.5f * args.sd[e][n]);
+      const float o = n < H ? v[j] * (0.5f * args.sd[e][n]) : 0.f;
+      __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(o), orr, n < H ? (uint32_t)n * 4u : OOB, 0, SC1);
     }
   }
+  if (!cnt) return;  // a separate launch combines
+  __shared__ int last;
+  const int t = a / top_k;
+  wait_vmcnt<0>();
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    unsigned *c = cnt + blockIdx.x * MOE_DEC_MAXA + t;
+    const unsigned old = __hip_atomic_fetch_add(c, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    last = old == 2u * (unsigned)top_k - 1u;
+    if (last) __hip_atomic_store(c, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  __syncthreads();
+  if (!last || threadIdx.x >= MOE_DEC_ROWS) return;
+  const int n = n0 + (int)threadIdx.x;
+  if (n >= H) return;
+  const __amdgpu_buffer_rsrc_t d0r = buffer_rsrc(dout, (uint32_t)(gridDim.z * H) * 4u);
+  const __amdgpu_buffer_rsrc_t d1r = buffer_rsrc(dout_lo, (uint32_t)(gridDim.z * H) * 4u);
+  float d0[MOE_DEC_MAXA], d1[MOE_DEC_MAXA];
+#pragma unroll
+  for (int k = 0; k < MOE_DEC_MAXA; k++) {
+    const uint32_t off = k < top_k ? ((uint32_t)(t * top_k + k) * (uint32_t)H + (uint32_t)n) * 4u : OOB;
+    d0[k] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(d0r, off, 0, SC1));
+    d1[k] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(d1r, off, 0, SC1));
+  }
+  float accy = 0.0f;
+#pragma unroll
+  for (int k = 0; k < MOE_DEC_MAXA; k++) {
+#pragma clang fp contract(off)
+    if (k >= top_k) break;
+    const float w = wts[t * top_k + k];
+    if (skip_small && fabsf(w) < 1e-8f) continue;  // src/model/cpu_moe.rs:172
+    const float d = d0[k] + d1[k];
+    const float prod = d * w;
+    accy = accy + prod;
+  }
+  if (y_bf16) reinterpret_cast<uint16_t *>(y)[(size_t)t * H + n] = (uint16_t)bf16_rne(accy);
+  else reinterpret_cast<float *>(y)[(size_t)t * H + n] = accy;
 }
 
 // ---- 5. combine ---------------------------------------------------------------
@@ -1581,9 +1629,12 @@ hipError_t launch_moe(const void *x, int xt_bf16, const void *router,
       hipLaunchKernelGGL((moe_dec_gateup_kernel<float>), dim3((I + MOE_DEC_ROWS - 1) / MOE_DEC_ROWS, A), dim3(512),
                          gl, stream, ga, (const float *)x, H, I, top_k, ws.idx, (float *)ws.h_hi, ws.inv, act);
     if ((err = hipGetLastError()) != hipSuccess) return err;
+    // with arrival counters the down launch also combines (one launch fewer)
     hipLaunchKernelGGL(moe_dec_down_kernel, dim3((H + MOE_DEC_ROWS - 1) / MOE_DEC_ROWS, 2, A), dim3(512), dl, stream,
-                       da, (const float *)ws.h_hi, H, I, ks, ws.idx, ws.dout, ws.dout_lo);
+                       da, (const float *)ws.h_hi, H, I, ks, ws.idx, ws.dout, ws.dout_lo, ws.cnt, ws.wts, top_k,
+                       routing, y, yt_bf16);
     if ((err = hipGetLastError()) != hipSuccess) return err;
+    if (ws.cnt) return hipSuccess;
     if (yt_bf16)
       hipLaunchKernelGGL((moe_combine_kernel<uint16_t>), dim3(T), dim3(256), 0, stream, ws.dout, ws.dout_lo, ws.wts,
                          ws.inv, H, top_k, (uint16_t *)y, routing);
